@@ -1,0 +1,467 @@
+/*
+ * prime_oracle.c -- CPU oracle for the PRIME moment-attention hot paths.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP kernels are
+ * compared against.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product library never links or calls it.
+ *
+ * Every routine restates, in float64 and plain loops, one algorithm of the
+ * reference PyTorch package (src/prime_moment_attention/ in the reference tree);
+ * each function names the file:line range it follows.  Tensors are dense
+ * row-major arrays:
+ *     q, k, v, y      [BH][L][D]        (BH = batch*heads flattened)
+ *     S0, K1, K2      [BH][D]
+ *     S1, S2          [BH][D][D]        index [key i][value j]
+ *     K0              [BH]
+ *     lam             [BH]              per-(b,h) decay (the reference has one
+ *                                       scalar per module; heads are independent,
+ *                                       so a per-head value is the scalar
+ *                                       formula applied head by head)
+ *
+ * Pinning (which independent check holds each routine down) is documented in
+ * tests/test_oracle.py next to the checks themselves.
+ */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define IDX2(a, b, nb) ((size_t)(a) * (size_t)(nb) + (size_t)(b))
+
+/* ------------------------------------------------------------------------- */
+/* Recurrent decode step, applied token by token.                             */
+/* attention.py:119-143 (update S*,K* with decay, then read out with the new  */
+/* state; den clamped with max(den, eps)).                                    */
+/* ------------------------------------------------------------------------- */
+void oracle_recurrent(int BH, int L, int D, const double *q, const double *k,
+                      const double *v, const double *lam, double eps,
+                      double *S0, double *S1, double *S2, double *K0,
+                      double *K1, double *K2, double *y)
+{
+    for (int bh = 0; bh < BH; ++bh) {
+        double *s0 = S0 + (size_t)bh * D, *s1 = S1 + (size_t)bh * D * D;
+        double *s2 = S2 + (size_t)bh * D * D, *k0 = K0 + bh;
+        double *k1 = K1 + (size_t)bh * D, *k2 = K2 + (size_t)bh * D;
+        const double l = lam[bh];
+        for (int t = 0; t < L; ++t) {
+            const double *qt = q + ((size_t)bh * L + t) * D;
+            const double *kt = k + ((size_t)bh * L + t) * D;
+            const double *vt = v + ((size_t)bh * L + t) * D;
+            double *yt = y + ((size_t)bh * L + t) * D;
+            /* attention.py:126-132 */
+            for (int j = 0; j < D; ++j) s0[j] = l * s0[j] + vt[j];
+            for (int i = 0; i < D; ++i)
+                for (int j = 0; j < D; ++j) {
+                    s1[IDX2(i, j, D)] = l * s1[IDX2(i, j, D)] + kt[i] * vt[j];
+                    s2[IDX2(i, j, D)] = l * s2[IDX2(i, j, D)] + kt[i] * kt[i] * vt[j];
+                }
+            *k0 = l * (*k0) + 1.0;
+            for (int i = 0; i < D; ++i) {
+                k1[i] = l * k1[i] + kt[i];
+                k2[i] = l * k2[i] + kt[i] * kt[i];
+            }
+            /* attention.py:135-143 */
+            double den = *k0;
+            for (int i = 0; i < D; ++i) den += qt[i] * k1[i] + 0.5 * qt[i] * qt[i] * k2[i];
+            if (den < eps) den = eps;
+            for (int j = 0; j < D; ++j) {
+                double num = s0[j];
+                for (int i = 0; i < D; ++i)
+                    num += qt[i] * s1[IDX2(i, j, D)] + 0.5 * qt[i] * qt[i] * s2[IDX2(i, j, D)];
+                yt[j] = num / den;
+            }
+        }
+    }
+}
+
+/* score weight 1 + q.k + 0.5 (q*q).(k*k)  (attention.py:172-174, chunked_ssd.py:90-92) */
+static double taylor_score(int D, const double *qi, const double *kj)
+{
+    double d1 = 0.0, d2 = 0.0;
+    for (int f = 0; f < D; ++f) {
+        d1 += qi[f] * kj[f];
+        d2 += qi[f] * qi[f] * kj[f] * kj[f];
+    }
+    return 1.0 + d1 + 0.5 * d2;
+}
+
+/* readout of a state (num and den) for one query, without decay factor */
+static void state_readout(int D, const double *qt, const double *s0, const double *s1,
+                          const double *s2, double k0, const double *k1,
+                          const double *k2, double *num, double *den)
+{
+    double d = k0;
+    for (int i = 0; i < D; ++i) d += qt[i] * k1[i] + 0.5 * qt[i] * qt[i] * k2[i];
+    *den = d;
+    for (int j = 0; j < D; ++j) {
+        double n = s0[j];
+        for (int i = 0; i < D; ++i)
+            n += qt[i] * s1[IDX2(i, j, D)] + 0.5 * qt[i] * qt[i] * s2[IDX2(i, j, D)];
+        num[j] = n;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Chunked SSD core.  chunked_ssd.py:48-184.                                  */
+/* Zero-pad L to a multiple of C (:65-77); per chunk: intra Taylor block with */
+/* lambda^(i-j) mask (:79-94), carry readout lambda^(i+1)*(state readout)     */
+/* (:139-153), y = num / max(den, eps) (:155-157); chunk deltas with weights  */
+/* lambda^(C-1-i), zero on padding (:96-111); state carried chunk to chunk,   */
+/* S^(c) = lambda^C S^(c-1) + dS^(c-1) (the closed form of :113-137); terminal */
+/* state with the lambda^(-pad) correction (:162-182).                         */
+/* has_state == 0 starts from zeros (state arrays are outputs only).          */
+/* ------------------------------------------------------------------------- */
+void oracle_chunked(int BH, int L, int D, int C, const double *q, const double *k,
+                    const double *v, const double *lam, double eps, int has_state,
+                    double *S0, double *S1, double *S2, double *K0, double *K1,
+                    double *K2, double *y)
+{
+    const int pad = (C - (L % C)) % C;
+    const int Lp = L + pad, NC = Lp / C;
+    double *num = (double *)malloc(sizeof(double) * D);
+    double *cn = (double *)malloc(sizeof(double) * D);
+    double *dS1 = (double *)malloc(sizeof(double) * D * D);
+    double *dS2 = (double *)malloc(sizeof(double) * D * D);
+    double *dS0 = (double *)malloc(sizeof(double) * D);
+    double *dK1 = (double *)malloc(sizeof(double) * D);
+    double *dK2 = (double *)malloc(sizeof(double) * D);
+    double *zero = (double *)calloc(D, sizeof(double));
+    for (int bh = 0; bh < BH; ++bh) {
+        double *s0 = S0 + (size_t)bh * D, *s1 = S1 + (size_t)bh * D * D;
+        double *s2 = S2 + (size_t)bh * D * D, *k0 = K0 + bh;
+        double *k1 = K1 + (size_t)bh * D, *k2 = K2 + (size_t)bh * D;
+        if (!has_state) {
+            memset(s0, 0, sizeof(double) * D);
+            memset(s1, 0, sizeof(double) * D * D);
+            memset(s2, 0, sizeof(double) * D * D);
+            *k0 = 0.0;
+            memset(k1, 0, sizeof(double) * D);
+            memset(k2, 0, sizeof(double) * D);
+        }
+        const double l = lam[bh];
+        const double lC = pow(l, C);
+        const double *qb = q + (size_t)bh * L * D;
+        const double *kb = k + (size_t)bh * L * D;
+        const double *vb = v + (size_t)bh * L * D;
+        double *yb = y + (size_t)bh * L * D;
+        for (int c = 0; c < NC; ++c) {
+            /* readout: intra block + carry of the state entering chunk c */
+            for (int i = 0; i < C; ++i) {
+                const int t = c * C + i;
+                if (t >= L) break; /* padded rows are sliced off (:159-160) */
+                const double *qi = qb + (size_t)t * D;
+                double den = 0.0;
+                for (int f = 0; f < D; ++f) num[f] = 0.0;
+                for (int j = 0; j <= i; ++j) {
+                    const int tj = c * C + j;
+                    const double *kj = (tj < L) ? kb + (size_t)tj * D : zero;
+                    const double *vj = (tj < L) ? vb + (size_t)tj * D : zero;
+                    const double a = pow(l, i - j) * taylor_score(D, qi, kj);
+                    den += a;
+                    for (int f = 0; f < D; ++f) num[f] += a * vj[f];
+                }
+                double cn_den;
+                state_readout(D, qi, s0, s1, s2, *k0, k1, k2, cn, &cn_den);
+                const double din = pow(l, i + 1);
+                den += din * cn_den;
+                if (den < eps) den = eps;
+                for (int f = 0; f < D; ++f) yb[(size_t)t * D + f] = (num[f] + din * cn[f]) / den;
+            }
+            /* chunk deltas (weights lambda^(C-1-i), zero on pad) and carry */
+            memset(dS0, 0, sizeof(double) * D);
+            memset(dS1, 0, sizeof(double) * D * D);
+            memset(dS2, 0, sizeof(double) * D * D);
+            memset(dK1, 0, sizeof(double) * D);
+            memset(dK2, 0, sizeof(double) * D);
+            double dK0 = 0.0;
+            for (int j = 0; j < C; ++j) {
+                const int tj = c * C + j;
+                if (tj >= L) continue;
+                const double w = pow(l, C - 1 - j);
+                const double *kj = kb + (size_t)tj * D, *vj = vb + (size_t)tj * D;
+                dK0 += w;
+                for (int f = 0; f < D; ++f) {
+                    dS0[f] += w * vj[f];
+                    dK1[f] += w * kj[f];
+                    dK2[f] += w * kj[f] * kj[f];
+                }
+                for (int a = 0; a < D; ++a)
+                    for (int b = 0; b < D; ++b) {
+                        dS1[IDX2(a, b, D)] += w * kj[a] * vj[b];
+                        dS2[IDX2(a, b, D)] += w * kj[a] * kj[a] * vj[b];
+                    }
+            }
+            for (int f = 0; f < D; ++f) {
+                s0[f] = lC * s0[f] + dS0[f];
+                k1[f] = lC * k1[f] + dK1[f];
+                k2[f] = lC * k2[f] + dK2[f];
+            }
+            for (int a = 0; a < D * D; ++a) {
+                s1[a] = lC * s1[a] + dS1[a];
+                s2[a] = lC * s2[a] + dS2[a];
+            }
+            *k0 = lC * (*k0) + dK0;
+        }
+        if (pad > 0) { /* chunked_ssd.py:171-178 */
+            const double corr = pow(l, -pad);
+            for (int f = 0; f < D; ++f) { s0[f] *= corr; k1[f] *= corr; k2[f] *= corr; }
+            for (int a = 0; a < D * D; ++a) { s1[a] *= corr; s2[a] *= corr; }
+            *k0 *= corr;
+        }
+    }
+    free(num); free(cn); free(dS1); free(dS2); free(dS0); free(dK1); free(dK2); free(zero);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Dense prefill, attention.py:160-202 (the module's 1 < L <= chunk_threshold */
+/* branch).  Note the reference clamps the intra denominator first and, when  */
+/* an incoming state exists, clamps again after adding the carry (:177,185).  */
+/* Terminal state (:190-202) is always produced here.                         */
+/* ------------------------------------------------------------------------- */
+void oracle_dense(int BH, int L, int D, const double *q, const double *k,
+                  const double *v, const double *lam, double eps, int has_state,
+                  double *S0, double *S1, double *S2, double *K0, double *K1,
+                  double *K2, double *y)
+{
+    double *num = (double *)malloc(sizeof(double) * D);
+    double *cn = (double *)malloc(sizeof(double) * D);
+    for (int bh = 0; bh < BH; ++bh) {
+        double *s0 = S0 + (size_t)bh * D, *s1 = S1 + (size_t)bh * D * D;
+        double *s2 = S2 + (size_t)bh * D * D, *k0 = K0 + bh;
+        double *k1 = K1 + (size_t)bh * D, *k2 = K2 + (size_t)bh * D;
+        const double l = lam[bh];
+        const double *qb = q + (size_t)bh * L * D;
+        const double *kb = k + (size_t)bh * L * D;
+        const double *vb = v + (size_t)bh * L * D;
+        double *yb = y + (size_t)bh * L * D;
+        for (int i = 0; i < L; ++i) {
+            const double *qi = qb + (size_t)i * D;
+            double den = 0.0;
+            for (int f = 0; f < D; ++f) num[f] = 0.0;
+            for (int j = 0; j <= i; ++j) {
+                const double a = pow(l, i - j) * taylor_score(D, qi, kb + (size_t)j * D);
+                den += a;
+                for (int f = 0; f < D; ++f) num[f] += a * vb[(size_t)j * D + f];
+            }
+            if (den < eps) den = eps; /* :177 */
+            if (has_state) {          /* :180-185 */
+                double cd;
+                state_readout(D, qi, s0, s1, s2, *k0, k1, k2, cn, &cd);
+                const double din = pow(l, i + 1);
+                for (int f = 0; f < D; ++f) num[f] += din * cn[f];
+                den += din * cd;
+                if (den < eps) den = eps;
+            }
+            for (int f = 0; f < D; ++f) yb[(size_t)i * D + f] = num[f] / den;
+        }
+        /* terminal state :190-202 */
+        const double lL = pow(l, L);
+        if (!has_state) {
+            memset(s0, 0, sizeof(double) * D);
+            memset(s1, 0, sizeof(double) * D * D);
+            memset(s2, 0, sizeof(double) * D * D);
+            *k0 = 0.0;
+            memset(k1, 0, sizeof(double) * D);
+            memset(k2, 0, sizeof(double) * D);
+        }
+        for (int f = 0; f < D; ++f) { s0[f] *= lL; k1[f] *= lL; k2[f] *= lL; }
+        for (int a = 0; a < D * D; ++a) { s1[a] *= lL; s2[a] *= lL; }
+        *k0 *= lL;
+        for (int j = 0; j < L; ++j) {
+            const double w = pow(l, L - 1 - j);
+            const double *kj = kb + (size_t)j * D, *vj = vb + (size_t)j * D;
+            *k0 += w;
+            for (int f = 0; f < D; ++f) {
+                s0[f] += w * vj[f];
+                k1[f] += w * kj[f];
+                k2[f] += w * kj[f] * kj[f];
+            }
+            for (int a = 0; a < D; ++a)
+                for (int b = 0; b < D; ++b) {
+                    s1[IDX2(a, b, D)] += w * kj[a] * vj[b];
+                    s2[IDX2(a, b, D)] += w * kj[a] * kj[a] * vj[b];
+                }
+        }
+    }
+    free(num);
+    free(cn);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Delta-PRIME feature maps, chunked_delta_prime.py:73-87:                    */
+/*   phi = [k/max(|k|,e), (1/sqrt2) k^2/max(|k^2|,e)],  psi = [q, (1/sqrt2) q^2] */
+/* q is the already-scaled query (:120).  psi, phi are [BH][L][2D].            */
+/* ------------------------------------------------------------------------- */
+void oracle_delta_features(int BH, int L, int D, const double *q, const double *k,
+                           double eps, double *psi, double *phi)
+{
+    const double r2 = 1.0 / sqrt(2.0);
+    for (size_t t = 0; t < (size_t)BH * L; ++t) {
+        const double *qt = q + t * D, *kt = k + t * D;
+        double *ps = psi + t * 2 * D, *ph = phi + t * 2 * D;
+        double n1 = 0.0, n2 = 0.0;
+        for (int f = 0; f < D; ++f) {
+            n1 += kt[f] * kt[f];
+            n2 += kt[f] * kt[f] * kt[f] * kt[f];
+        }
+        n1 = sqrt(n1);
+        n2 = sqrt(n2);
+        if (n1 < eps) n1 = eps;
+        if (n2 < eps) n2 = eps;
+        for (int f = 0; f < D; ++f) {
+            ph[f] = kt[f] / n1;
+            ph[D + f] = r2 * (kt[f] * kt[f]) / n2;
+            ps[f] = qt[f];
+            ps[D + f] = r2 * qt[f] * qt[f];
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Chunked gated delta-PRIME prefill, chunked_delta_prime.py:177-283.         */
+/*   psi, phi [BH][L][P] (P = 2D), v [BH][L][D], beta, alpha [BH][L],         */
+/*   S [BH][D][P] in/out (has_state == 0 starts from zeros).                  */
+/* Per chunk: cum = cumsum(log clamp(alpha,1e-5,1)) (:199-200),               */
+/* Lambda_ij = exp(cum_i - cum_j) for i >= j (:203-206), T = I + strict-tril( */
+/* Lambda*G*beta_j) (:209-218), u = v - (phi*e^cum) S^T (:238-242), solve     */
+/* T E = u by forward substitution (:245), y = tril(psi phi^T * Lambda)(beta  */
+/* E) + (psi*e^cum) S^T (:248-255), S <- e^cum_end S + (beta E)^T (phi *      */
+/* e^(cum_end-cum)) (:259-264), then the Lyapunov clamp S <- S min(1, B/(|S|_F */
+/* + 1e-6)) when bound > 0 (:266-270).  Padded steps use alpha = decay_pad    */
+/* (:183) and zero psi/phi/v/beta.                                            */
+/* ------------------------------------------------------------------------- */
+void oracle_delta_chunked(int BH, int L, int D, int C, const double *psi,
+                          const double *phi, const double *v, const double *beta,
+                          const double *alpha, double decay_pad, double bound,
+                          int has_state, double *S, double *y)
+{
+    const int P = 2 * D;
+    const int pad = (C - (L % C)) % C;
+    const int NC = (L + pad) / C;
+    double *cum = (double *)malloc(sizeof(double) * C);
+    double *u = (double *)malloc(sizeof(double) * C * D);
+    double *E = (double *)malloc(sizeof(double) * C * D);
+    double *Sn = (double *)malloc(sizeof(double) * D * P);
+    double *zp = (double *)calloc(P, sizeof(double));
+    double *zd = (double *)calloc(D, sizeof(double));
+    for (int bh = 0; bh < BH; ++bh) {
+        double *Sb = S + (size_t)bh * D * P;
+        if (!has_state) memset(Sb, 0, sizeof(double) * D * P);
+        for (int c = 0; c < NC; ++c) {
+            const double *ps[256], *ph[256], *vv[256];
+            double bt[256], al[256];
+            for (int i = 0; i < C; ++i) {
+                const int t = c * C + i;
+                const size_t o = (size_t)bh * L + t;
+                if (t < L) {
+                    ps[i] = psi + o * P; ph[i] = phi + o * P; vv[i] = v + o * D;
+                    bt[i] = beta[o]; al[i] = alpha[o];
+                } else {
+                    ps[i] = zp; ph[i] = zp; vv[i] = zd; bt[i] = 0.0; al[i] = decay_pad;
+                }
+                double a = al[i];
+                if (a < 1e-5) a = 1e-5;
+                if (a > 1.0) a = 1.0;
+                cum[i] = log(a) + (i ? cum[i - 1] : 0.0);
+            }
+            /* u = v - (phi * e^cum) S^T */
+            for (int i = 0; i < C; ++i) {
+                const double ec = exp(cum[i]);
+                for (int d = 0; d < D; ++d) {
+                    double acc = 0.0;
+                    for (int e = 0; e < P; ++e) acc += ph[i][e] * ec * Sb[IDX2(d, e, P)];
+                    u[IDX2(i, d, D)] = vv[i][d] - acc;
+                }
+            }
+            /* forward substitution: E_i = u_i - sum_{j<i} T_ij E_j */
+            for (int i = 0; i < C; ++i) {
+                for (int d = 0; d < D; ++d) E[IDX2(i, d, D)] = u[IDX2(i, d, D)];
+                for (int j = 0; j < i; ++j) {
+                    double g = 0.0;
+                    for (int e = 0; e < P; ++e) g += ph[i][e] * ph[j][e];
+                    const double tij = exp(cum[i] - cum[j]) * g * bt[j];
+                    for (int d = 0; d < D; ++d) E[IDX2(i, d, D)] -= tij * E[IDX2(j, d, D)];
+                }
+            }
+            /* outputs */
+            for (int i = 0; i < C; ++i) {
+                const int t = c * C + i;
+                if (t >= L) break;
+                const double ec = exp(cum[i]);
+                double *yt = y + ((size_t)bh * L + t) * D;
+                for (int d = 0; d < D; ++d) {
+                    double acc = 0.0;
+                    for (int e = 0; e < P; ++e) acc += ps[i][e] * ec * Sb[IDX2(d, e, P)];
+                    yt[d] = acc;
+                }
+                for (int j = 0; j <= i; ++j) {
+                    double g = 0.0;
+                    for (int e = 0; e < P; ++e) g += ps[i][e] * ph[j][e];
+                    const double a = g * exp(cum[i] - cum[j]) * bt[j];
+                    for (int d = 0; d < D; ++d) yt[d] += a * E[IDX2(j, d, D)];
+                }
+            }
+            /* state update */
+            const double cend = cum[C - 1];
+            const double cdec = exp(cend);
+            for (int d = 0; d < D; ++d)
+                for (int e = 0; e < P; ++e) {
+                    double acc = cdec * Sb[IDX2(d, e, P)];
+                    for (int j = 0; j < C; ++j)
+                        acc += bt[j] * E[IDX2(j, d, D)] * ph[j][e] * exp(cend - cum[j]);
+                    Sn[IDX2(d, e, P)] = acc;
+                }
+            if (bound > 0.0) {
+                double nrm = 0.0;
+                for (int a = 0; a < D * P; ++a) nrm += Sn[a] * Sn[a];
+                nrm = sqrt(nrm);
+                double sc = bound / (nrm + 1e-6);
+                if (sc > 1.0) sc = 1.0;
+                for (int a = 0; a < D * P; ++a) Sn[a] *= sc;
+            }
+            memcpy(Sb, Sn, sizeof(double) * D * P);
+        }
+    }
+    free(cum); free(u); free(E); free(Sn); free(zp); free(zd);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Per-token gated delta rule with decay before prediction (the closed form   */
+/* the chunked routine above equals when bound == 0, for every C):            */
+/*   S_t = a_t S_{t-1} + b_t (v_t - a_t S_{t-1} phi_t) phi_t^T,  y_t = S_t psi_t */
+/* with a_t = clamp(alpha_t, 1e-5, 1).  Independent of chunking; used only to */
+/* pin oracle_delta_chunked.                                                   */
+/* ------------------------------------------------------------------------- */
+void oracle_delta_tokenwise(int BH, int L, int D, const double *psi,
+                            const double *phi, const double *v, const double *beta,
+                            const double *alpha, int has_state, double *S, double *y)
+{
+    const int P = 2 * D;
+    double *pred = (double *)malloc(sizeof(double) * D);
+    for (int bh = 0; bh < BH; ++bh) {
+        double *Sb = S + (size_t)bh * D * P;
+        if (!has_state) memset(Sb, 0, sizeof(double) * D * P);
+        for (int t = 0; t < L; ++t) {
+            const size_t o = (size_t)bh * L + t;
+            const double *ph = phi + o * P, *ps = psi + o * P, *vt = v + o * D;
+            double a = alpha[o];
+            if (a < 1e-5) a = 1e-5;
+            if (a > 1.0) a = 1.0;
+            for (int d = 0; d < D; ++d) {
+                double acc = 0.0;
+                for (int e = 0; e < P; ++e) acc += Sb[IDX2(d, e, P)] * ph[e];
+                pred[d] = a * acc;
+            }
+            for (int d = 0; d < D; ++d) {
+                const double err = beta[o] * (vt[d] - pred[d]);
+                for (int e = 0; e < P; ++e) Sb[IDX2(d, e, P)] = a * Sb[IDX2(d, e, P)] + err * ph[e];
+            }
+            double *yt = y + o * D;
+            for (int d = 0; d < D; ++d) {
+                double acc = 0.0;
+                for (int e = 0; e < P; ++e) acc += Sb[IDX2(d, e, P)] * ps[e];
+                yt[d] = acc;
+            }
+        }
+    }
+    free(pred);
+}
