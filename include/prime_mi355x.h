@@ -1,0 +1,120 @@
+/*
+ * prime_mi355x.h -- C ABI of the MI355X (gfx950) PRIME moment-attention library.
+ *
+ * All tensors are DEVICE pointers on the current HIP device; every call is
+ * asynchronous on the given stream (a hipStream_t passed as void*; NULL is the
+ * default stream) and performs no host synchronisation and no allocation.
+ * Every entry point returns 0 on success or a negative PRIME_ERR_* code; the
+ * message for the last failure on the calling thread is prime_last_error().
+ *
+ * Shapes follow the reference PyTorch package (src/prime_moment_attention):
+ *   q, k, v, y   [B, H, L, D]   any element strides for B, H, L; D contiguous
+ *   state        6 separate fp32 buffers, contiguous, in the reference order
+ *                (attention.py:108-117, cache.py:15-56):
+ *                  S0 [B,H,D]  S1 [B,H,D,D]  S2 [B,H,D,D]  (S* indexed [key][value])
+ *                  K0 [B,H,1]  K1 [B,H,D]    K2 [B,H,D]
+ *   decay        fp32 [H] device array (the reference's scalar `decay`, widened
+ *                to one value per head; pass H copies of the scalar for the
+ *                reference behaviour)
+ * q is taken PRE-SCALED by 1/sqrt(D), as at the reference's core boundary
+ * (chunked_ssd.py:58-61, attention.py:101).  D must be 64.
+ */
+#ifndef PRIME_MI355X_H
+#define PRIME_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PRIME_ABI_VERSION 1
+
+/* element types */
+#define PRIME_F32  0
+#define PRIME_BF16 1
+#define PRIME_F16  2
+
+/* error codes */
+#define PRIME_OK                   0
+#define PRIME_ERR_INVALID_ARG     -1  /* null pointer, bad size, inconsistent shape */
+#define PRIME_ERR_UNSUPPORTED_DIM -2  /* head dim other than 64 */
+#define PRIME_ERR_UNSUPPORTED_DTYPE -3
+#define PRIME_ERR_MISALIGNED      -4  /* pointer/stride breaks 16-byte row alignment */
+#define PRIME_ERR_ALIAS           -5  /* output overlaps an input it may not alias */
+#define PRIME_ERR_HIP             -6  /* HIP launch / runtime error */
+
+/* flags for prime_chunked_prefill */
+#define PRIME_FLAG_DENSE_CLAMP 1u /* reproduce the dense branch's double clamp:
+                                     den = max(max(den_call, eps) + carry_init, eps)
+                                     (attention.py:177,185) instead of the
+                                     recurrence's max(den, eps) */
+
+/* A strided [B, H, L, D] view (decode calls ignore stride_l). */
+typedef struct prime_tensor {
+    void   *data;
+    int32_t dtype;      /* PRIME_F32 / PRIME_BF16 / PRIME_F16 */
+    int32_t reserved;
+    int64_t stride_b;   /* strides in ELEMENTS */
+    int64_t stride_h;
+    int64_t stride_l;
+} prime_tensor_t;
+
+/* The 6-tuple moment state; each pointer is a contiguous fp32 buffer. */
+typedef struct prime_state {
+    float *s0, *s1, *s2, *k0, *k1, *k2;
+} prime_state_t;
+
+/* ABI version (PRIME_ABI_VERSION) and thread-local last error message. */
+int prime_abi_version(void);
+const char *prime_last_error(void);
+
+/*
+ * One recurrent decode step for B x H independent (sequence, head) tiles.
+ * Replaces the L == 1 branch of PrimeMomentAttention.forward
+ * (attention.py:119-143): decay-update S0..K2 with the new token, then read out
+ * y = (S0 + S1^T q + 1/2 S2^T q^2) / max(K0 + q.K1 + 1/2 q^2.K2, eps) with the
+ * updated state.
+ *   q, k, v : [B, H(q) / H_kv(k,v), D]; k/v head = h / (H / H_kv) (GQA,
+ *             attention.py:92-94)
+ *   state_in: NULL for a zero state (attention.py:111-117)
+ *   state_out may equal state_in (in place); otherwise they must not overlap.
+ *   y       : [B, H, D], F32 or BF16 or F16
+ */
+int prime_decode_step(const prime_tensor_t *q, const prime_tensor_t *k,
+                      const prime_tensor_t *v, int B, int H, int H_kv, int D,
+                      const float *decay, float eps, const prime_state_t *state_in,
+                      const prime_state_t *state_out, const prime_tensor_t *y,
+                      void *stream);
+
+/*
+ * Chunked prefill of L tokens for B x H sequences.  Replaces
+ * chunked_prime_ssd_core (chunked_ssd.py:48-184) and, with
+ * PRIME_FLAG_DENSE_CLAMP, the dense branch of PrimeMomentAttention.forward
+ * (attention.py:160-202).  The result does not depend on `chunk` (the reference
+ * algorithm is exact for any chunk size); the kernel tiles 64 tokens.
+ *   state_in : NULL for zeros; state_out: NULL when no final state is wanted;
+ *              state_out may equal state_in.
+ *   y        : [B, H, L, D]
+ *   workspace: optional device scratch of workspace_bytes (16-byte aligned).
+ *              With at least prime_chunked_prefill_workspace_size() bytes the
+ *              sequences are split into segments that run in parallel (a
+ *              carried-state scan between them); with less (or NULL) each
+ *              sequence runs as one segment.  Results agree either way.
+ */
+int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k,
+                          const prime_tensor_t *v, int B, int H, int H_kv, int L, int D,
+                          int chunk, const float *decay, float eps, unsigned flags,
+                          const prime_state_t *state_in, const prime_tensor_t *y,
+                          const prime_state_t *state_out, void *workspace,
+                          size_t workspace_bytes, void *stream);
+
+/* Workspace bytes prime_chunked_prefill uses for this shape (0 = none needed). */
+size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PRIME_MI355X_H */

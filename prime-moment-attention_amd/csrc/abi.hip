@@ -1,0 +1,185 @@
+// C-ABI entry points: argument validation, error reporting and dispatch.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "prime_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int elem_size(int dt) { return dt == PRIME_F32 ? 4 : 2; }
+bool valid_dtype(int dt) { return dt == PRIME_F32 || dt == PRIME_BF16 || dt == PRIME_F16; }
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// every row start of a strided view is 16-byte aligned
+bool rows_aligned(const prime_tensor_t *t, bool use_l) {
+    const int64_t es = elem_size(t->dtype);
+    if (!aligned16(t->data)) return false;
+    if ((t->stride_b * es) % 16 || (t->stride_h * es) % 16) return false;
+    if (use_l && (t->stride_l * es) % 16) return false;
+    return true;
+}
+
+bool overlap(const void *a, size_t na, const void *b, size_t nb) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return x < y + nb && y < x + na;
+}
+
+// state_out must be exactly state_in (in place) or disjoint from it.
+int check_state_alias(const prime_state_t *in, const prime_state_t *out, size_t BH, int D,
+                      bool *inplace) {
+    *inplace = false;
+    if (!in || !out) return PRIME_OK;
+    const float *pi[6] = {in->s0, in->s1, in->s2, in->k0, in->k1, in->k2};
+    const float *po[6] = {out->s0, out->s1, out->s2, out->k0, out->k1, out->k2};
+    const size_t n[6] = {BH * D, BH * D * D, BH * D * D, BH, BH * D, BH * D};
+    bool all_same = true, any_same = false;
+    for (int i = 0; i < 6; ++i) {
+        all_same &= pi[i] == po[i];
+        any_same |= pi[i] == po[i];
+    }
+    if (all_same) {
+        *inplace = true;
+        return PRIME_OK;
+    }
+    for (int i = 0; i < 6; ++i)
+        for (int j = 0; j < 6; ++j)
+            if (overlap(pi[i], n[i] * 4, po[j], n[j] * 4))
+                return fail(PRIME_ERR_ALIAS, "state_out buffer %d overlaps state_in buffer %d "
+                            "(only a fully in-place state is allowed)", j, i);
+    (void)any_same;
+    return PRIME_OK;
+}
+
+int check_state(const prime_state_t *s, const char *name) {
+    if (!s) return PRIME_OK;
+    const float *p[6] = {s->s0, s->s1, s->s2, s->k0, s->k1, s->k2};
+    for (int i = 0; i < 6; ++i) {
+        if (!p[i]) return fail(PRIME_ERR_INVALID_ARG, "%s: buffer %d is null", name, i);
+        if ((reinterpret_cast<uintptr_t>(p[i]) & 3u) != 0)
+            return fail(PRIME_ERR_MISALIGNED, "%s: buffer %d is not 4-byte aligned", name, i);
+    }
+    if (!aligned16(s->s1) || !aligned16(s->s2))
+        return fail(PRIME_ERR_MISALIGNED, "%s: S1/S2 must be 16-byte aligned", name);
+    return PRIME_OK;
+}
+
+int check_hip(hipError_t e, const char *what) {
+    if (e != hipSuccess) return fail(PRIME_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return PRIME_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int prime_abi_version(void) { return PRIME_ABI_VERSION; }
+
+const char *prime_last_error(void) { return g_err; }
+
+int prime_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                      int B, int H, int H_kv, int D, const float *decay, float eps,
+                      const prime_state_t *state_in, const prime_state_t *state_out,
+                      const prime_tensor_t *y, void *stream) {
+    g_err[0] = 0;
+    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !decay || !state_out)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_decode_step: null argument");
+    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d", B, H, H_kv);
+    if (!valid_dtype(q->dtype) || !valid_dtype(k->dtype) || !valid_dtype(v->dtype) || !valid_dtype(y->dtype))
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dtype");
+    int rc;
+    if ((rc = check_state(state_in, "state_in")) || (rc = check_state(state_out, "state_out"))) return rc;
+    bool inplace;
+    if ((rc = check_state_alias(state_in, state_out, static_cast<size_t>(B) * H, D, &inplace))) return rc;
+
+    prime::DecodeArgs a{};
+    a.q = q->data; a.k = k->data; a.v = v->data;
+    a.q_sb = q->stride_b; a.q_sh = q->stride_h;
+    a.k_sb = k->stride_b; a.k_sh = k->stride_h;
+    a.v_sb = v->stride_b; a.v_sh = v->stride_h;
+    a.dt_q = q->dtype; a.dt_k = k->dtype; a.dt_v = v->dtype;
+    a.B = B; a.H = H; a.group = H / H_kv;
+    a.decay = decay; a.eps = eps;
+    if (state_in) {
+        a.s0i = state_in->s0; a.s1i = state_in->s1; a.s2i = state_in->s2;
+        a.k0i = state_in->k0; a.k1i = state_in->k1; a.k2i = state_in->k2;
+    }
+    a.s0o = state_out->s0; a.s1o = state_out->s1; a.s2o = state_out->s2;
+    a.k0o = state_out->k0; a.k1o = state_out->k1; a.k2o = state_out->k2;
+    a.y = y->data; a.dt_y = y->dtype; a.y_sb = y->stride_b; a.y_sh = y->stride_h;
+    return check_hip(prime::launch_decode_step(a, static_cast<hipStream_t>(stream)), "decode launch");
+}
+
+int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                          int B, int H, int H_kv, int L, int D, int chunk, const float *decay,
+                          float eps, unsigned flags, const prime_state_t *state_in,
+                          const prime_tensor_t *y, const prime_state_t *state_out, void *workspace,
+                          size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !decay)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_chunked_prefill: null argument");
+    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0 || chunk <= 0)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d chunk=%d", B, H, H_kv, L, chunk);
+    if (flags & ~PRIME_FLAG_DENSE_CLAMP) return fail(PRIME_ERR_INVALID_ARG, "unknown flags 0x%x", flags);
+    if (q->dtype != k->dtype || q->dtype != v->dtype || (q->dtype != PRIME_BF16 && q->dtype != PRIME_F32))
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "q/k/v must share dtype BF16 or F32");
+    if (!valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported y dtype");
+    if (!rows_aligned(q, true) || !rows_aligned(k, true) || !rows_aligned(v, true) || !rows_aligned(y, true))
+        return fail(PRIME_ERR_MISALIGNED, "q/k/v/y rows must start on 16-byte boundaries");
+    int rc;
+    if ((rc = check_state(state_in, "state_in")) || (rc = check_state(state_out, "state_out"))) return rc;
+    bool inplace;
+    if ((rc = check_state_alias(state_in, state_out, static_cast<size_t>(B) * H, D, &inplace))) return rc;
+
+    prime::PrefillArgs a{};
+    a.q = q->data; a.k = k->data; a.v = v->data;
+    a.q_sb = q->stride_b; a.q_sh = q->stride_h; a.q_sl = q->stride_l;
+    a.k_sb = k->stride_b; a.k_sh = k->stride_h; a.k_sl = k->stride_l;
+    a.v_sb = v->stride_b; a.v_sh = v->stride_h; a.v_sl = v->stride_l;
+    a.dt_in = q->dtype;
+    a.B = B; a.H = H; a.group = H / H_kv; a.L = L;
+    a.decay = decay; a.eps = eps;
+    a.dense_clamp = (flags & PRIME_FLAG_DENSE_CLAMP) ? 1 : 0;
+    if (state_in) {
+        a.s0i = state_in->s0; a.s1i = state_in->s1; a.s2i = state_in->s2;
+        a.k0i = state_in->k0; a.k1i = state_in->k1; a.k2i = state_in->k2;
+    }
+    if (state_out) {
+        a.s0o = state_out->s0; a.s1o = state_out->s1; a.s2o = state_out->s2;
+        a.k0o = state_out->k0; a.k1o = state_out->k1; a.k2o = state_out->k2;
+    }
+    a.y = y->data; a.dt_y = y->dtype;
+    a.y_sb = y->stride_b; a.y_sh = y->stride_h; a.y_sl = y->stride_l;
+    if (workspace && !aligned16(workspace))
+        return fail(PRIME_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+    const int S = B * H;
+    prime::plan_segments(S, L, a.dense_clamp != 0, workspace ? workspace_bytes : 0, &a.G, &a.cps);
+    a.ws = a.G > 1 ? static_cast<float *>(workspace) : nullptr;
+    // With one segment per sequence and few sequences, split the value columns
+    // over two workgroups.  Both slices read the K state, so an in-place state
+    // forbids it.
+    a.nsplit = (a.G == 1 && S <= 160 && !inplace) ? 2 : 1;
+    return check_hip(prime::launch_prefill(a, static_cast<hipStream_t>(stream)), "prefill launch");
+}
+
+size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags) {
+    if (B <= 0 || H <= 0 || L <= 0) return 0;
+    int G, cps;
+    prime::plan_segments(B * H, L, (flags & PRIME_FLAG_DENSE_CLAMP) != 0, static_cast<size_t>(-1), &G, &cps);
+    return G > 1 ? static_cast<size_t>(B) * H * G * prime::kWsStride * sizeof(float) : 0;
+}
+
+}  // extern "C"

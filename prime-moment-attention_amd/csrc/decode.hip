@@ -1,0 +1,134 @@
+// Fused recurrent decode step for PRIME moment attention (gfx950).
+//
+// Semantics: attention.py:119-143 of the reference -- per (sequence, head) tile
+//   S0 = l S0 + v ; S1 = l S1 + k v^T ; S2 = l S2 + (k*k) v^T
+//   K0 = l K0 + 1 ; K1 = l K1 + k     ; K2 = l K2 + k*k
+//   y  = (S0 + S1^T q + 1/2 S2^T q^2) / max(K0 + q.K1 + 1/2 q^2.K2, eps)
+// read out with the UPDATED state.
+//
+// Design: the step is HBM-bound (67.6 KB of state traffic per tile against
+// ~33 kflop).  One wavefront owns one tile.  Lane l owns value columns
+// 4*(l&15)..+3 and key rows {4r + (l>>4)}, r = 0..15, so each wave-wide
+// 128-bit load/store instruction touches four consecutive 256-byte rows: one
+// contiguous 1 KB segment.  All 32 loads of S1/S2 are issued before any math
+// (registers hold the whole 32 KB tile across the wave), the update and readout
+// are fused per row, and the 64-term key contraction ends with two cross-lane
+// butterflies.  The denominator is a wavefront reduction.  state_in may alias
+// state_out: every element is read and written by the same lane.
+
+#include "prime_kernels.h"
+
+namespace prime {
+
+
+constexpr int kDecodeWaves = 4;
+
+__global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const DecodeArgs a) {
+    __shared__ float sh[kDecodeWaves][4][kD];  // per wave: q, k, v, updated S0
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int BH = a.B * a.H;
+    const int tile = blockIdx.x * kDecodeWaves + wave;
+    const bool active = tile < BH;
+    const int t = active ? tile : 0;
+    const int b = t / a.H, h = t - (t / a.H) * a.H, hk = h / a.group;
+    const bool has_in = a.s1i != nullptr;
+
+    float qv = 0.f, kv = 0.f, vv = 0.f, lam = 0.f;
+    if (active) {
+        qv = load_elem(a.q, b * a.q_sb + h * a.q_sh + lane, a.dt_q);
+        kv = load_elem(a.k, b * a.k_sb + hk * a.k_sh + lane, a.dt_k);
+        vv = load_elem(a.v, b * a.v_sb + hk * a.v_sh + lane, a.dt_v);
+        lam = a.decay[h];
+    }
+
+    const int rg = lane >> 4;  // row group: rows 4r + rg
+    const int cg = lane & 15;  // column group: columns 4cg..4cg+3
+    const size_t tb = static_cast<size_t>(t) * (kD * kD);
+    const size_t tv = static_cast<size_t>(t) * kD;
+
+    f32x4 r1[16], r2[16];
+    float s0v = 0.f, k1v = 0.f, k2v = 0.f, k0v = 0.f;
+    if (active && has_in) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const size_t o = tb + (4 * r + rg) * kD + 4 * cg;
+            r1[r] = *reinterpret_cast<const f32x4 *>(a.s1i + o);
+            r2[r] = *reinterpret_cast<const f32x4 *>(a.s2i + o);
+        }
+        s0v = a.s0i[tv + lane];
+        k1v = a.k1i[tv + lane];
+        k2v = a.k2i[tv + lane];
+        k0v = a.k0i[t];
+    } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            r1[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+            r2[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+
+    // small moments (lane l owns element l)
+    const float s0n = lam * s0v + vv;
+    const float k1n = lam * k1v + kv;
+    const float k2n = lam * k2v + kv * kv;
+    const float k0n = lam * k0v + 1.0f;
+    sh[wave][0][lane] = qv;
+    sh[wave][1][lane] = kv;
+    sh[wave][2][lane] = vv;
+    sh[wave][3][lane] = s0n;
+    __syncthreads();
+
+    const f32x4 v4 = *reinterpret_cast<const f32x4 *>(&sh[wave][2][4 * cg]);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int row = 4 * r + rg;
+        const float kr = sh[wave][1][row];
+        const float qr = sh[wave][0][row];
+        const float kr2 = kr * kr;
+        const float qh = 0.5f * qr * qr;
+        f32x4 n1, n2;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            n1[c] = lam * r1[r][c] + kr * v4[c];
+            n2[c] = lam * r2[r][c] + kr2 * v4[c];
+            acc[c] += qr * n1[c] + qh * n2[c];
+        }
+        if (active) {
+            const size_t o = tb + row * kD + 4 * cg;
+            *reinterpret_cast<f32x4 *>(a.s1o + o) = n1;
+            *reinterpret_cast<f32x4 *>(a.s2o + o) = n2;
+        }
+    }
+    // sum the four row groups (lanes cg, cg+16, cg+32, cg+48)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        acc[c] += __shfl_xor(acc[c], 16, kWave);
+        acc[c] += __shfl_xor(acc[c], 32, kWave);
+    }
+    const float den = k0n + wave_sum(qv * k1n + 0.5f * qv * qv * k2n);
+    const float inv = 1.0f / fmaxf(den, a.eps);
+
+    if (active) {
+        a.s0o[tv + lane] = s0n;
+        a.k1o[tv + lane] = k1n;
+        a.k2o[tv + lane] = k2n;
+        if (lane == 0) a.k0o[t] = k0n;
+        if (rg == 0) {
+            const f32x4 s04 = *reinterpret_cast<const f32x4 *>(&sh[wave][3][4 * cg]);
+            const int64_t yo = b * a.y_sb + h * a.y_sh + 4 * cg;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) store_elem(a.y, yo + c, a.dt_y, (s04[c] + acc[c]) * inv);
+        }
+    }
+}
+
+hipError_t launch_decode_step(const DecodeArgs &a, hipStream_t stream) {
+    const int BH = a.B * a.H;
+    const int blocks = (BH + kDecodeWaves - 1) / kDecodeWaves;
+    hipLaunchKernelGGL(decode_step_kernel, dim3(blocks), dim3(kDecodeWaves * kWave), 0, stream, a);
+    return hipGetLastError();
+}
+
+}  // namespace prime

@@ -1,0 +1,53 @@
+// Kernel argument blocks and launchers shared by the kernels and the C-ABI layer.
+#pragma once
+
+#include "prime_common.h"
+
+namespace prime {
+
+struct DecodeArgs {
+    const void *q, *k, *v;
+    int64_t q_sb, q_sh, k_sb, k_sh, v_sb, v_sh;
+    int dt_q, dt_k, dt_v;
+    int B, H, group;
+    const float *decay;
+    float eps;
+    const float *s0i, *s1i, *s2i, *k0i, *k1i, *k2i;  // all null => zero state
+    float *s0o, *s1o, *s2o, *k0o, *k1o, *k2o;
+    void *y;
+    int dt_y;
+    int64_t y_sb, y_sh;
+};
+
+struct PrefillArgs {
+    const void *q, *k, *v;
+    int64_t q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;
+    int dt_in;  // PRIME_BF16 or PRIME_F32 (all three inputs)
+    int B, H, group, L;
+    const float *decay;
+    float eps;
+    int dense_clamp;
+    const float *s0i, *s1i, *s2i, *k0i, *k1i, *k2i;  // null => zero state
+    float *s0o, *s1o, *s2o, *k0o, *k1o, *k2o;        // null => no final state
+    void *y;
+    int dt_y;
+    int64_t y_sb, y_sh, y_sl;
+    int nsplit;  // value-column slices per sequence (64 / NV)
+    // segment-parallel scan (G > 1): each sequence is cut into G segments of
+    // `cps` chunks; ws holds one packed fp32 state slot per (sequence, segment)
+    int G, cps;
+    int nseg_launch;  // segments covered by the current launch (G or G - 1)
+    float *ws;
+};
+
+// packed fp32 state slot in the workspace: S1 | S2 | S0 | K1 | K2 | K0
+constexpr int kWsS1 = 0, kWsS2 = 4096, kWsS0 = 8192, kWsK1 = 8256, kWsK2 = 8320, kWsK0 = 8384;
+constexpr int kWsStride = 8448;  // floats per slot (33,792 bytes)
+constexpr int kWsElems = 8385;   // used floats per slot
+
+hipError_t launch_decode_step(const DecodeArgs &a, hipStream_t stream);
+hipError_t launch_prefill(PrefillArgs a, hipStream_t stream);
+// segments per sequence for the launch plan, given the workspace the caller has
+void plan_segments(int S, int L, bool dense_clamp, size_t ws_bytes, int *G, int *cps);
+
+}  // namespace prime

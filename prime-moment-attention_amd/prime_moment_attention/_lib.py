@@ -1,0 +1,233 @@
+"""ctypes binding of libprime_mi355x.so (the C ABI in include/prime_mi355x.h).
+
+This is the only route from Python to the compute: there is no CPU or eager
+fallback.  If the library is missing, or a tensor is not on a HIP device, the
+calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libprime_mi355x.so")
+
+PRIME_F32, PRIME_BF16, PRIME_F16 = 0, 1, 2
+PRIME_FLAG_DENSE_CLAMP = 1
+ABI_VERSION = 1
+
+_DTYPES = {torch.float32: PRIME_F32, torch.bfloat16: PRIME_BF16, torch.float16: PRIME_F16}
+
+# every symbol include/prime_mi355x.h declares
+EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_chunked_prefill",
+           "prime_chunked_prefill_workspace_size")
+
+
+class PrimeTensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+                ("stride_b", ctypes.c_int64), ("stride_h", ctypes.c_int64), ("stride_l", ctypes.c_int64)]
+
+
+class PrimeState(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("s0", "s1", "s2", "k0", "k1", "k2")]
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library (no GPU needed to load it)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"PRIME HIP library not built: {LIB_PATH} is missing "
+                           "(run __graft_entry__.build() or make -C prime-moment-attention_amd)")
+    L = ctypes.CDLL(LIB_PATH)
+    L.prime_abi_version.restype = ctypes.c_int
+    L.prime_last_error.restype = ctypes.c_char_p
+    P = ctypes.POINTER
+    L.prime_decode_step.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 4 + [
+        ctypes.c_void_p, ctypes.c_float, P(PrimeState), P(PrimeState), P(PrimeTensor), ctypes.c_void_p]
+    L.prime_decode_step.restype = ctypes.c_int
+    L.prime_chunked_prefill.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 6 + [
+        ctypes.c_void_p, ctypes.c_float, ctypes.c_uint, P(PrimeState), P(PrimeTensor),
+        P(PrimeState), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    L.prime_chunked_prefill.restype = ctypes.c_int
+    L.prime_chunked_prefill_workspace_size.argtypes = [ctypes.c_int] * 3 + [ctypes.c_uint]
+    L.prime_chunked_prefill_workspace_size.restype = ctypes.c_size_t
+    v = L.prime_abi_version()
+    if v != ABI_VERSION:
+        raise RuntimeError(f"libprime_mi355x ABI {v} != expected {ABI_VERSION}")
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return load().prime_last_error().decode(errors="replace")
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc}): {last_error()}")
+
+
+def _dev_check(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError("PRIME kernels need tensors on a HIP device (no CPU fallback)")
+
+
+def _shape(t: torch.Tensor, shape, name: str) -> None:
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+
+
+def _check_decay(decay: torch.Tensor, H: int) -> None:
+    if decay.dtype != torch.float32 or decay.numel() != H or not decay.is_contiguous():
+        raise ValueError(f"decay must be a contiguous fp32 tensor of {H} values")
+
+
+def _check_state(state, B: int, H: int, D: int, name: str) -> None:
+    if state is None:
+        return
+    shapes = [(B, H, D), (B, H, D, D), (B, H, D, D), (B, H, 1), (B, H, D), (B, H, D)]
+    if len(state) != 6:
+        raise ValueError(f"{name} must be a 6-tuple")
+    for t, sh in zip(state, shapes):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != B * H * _prod(sh[2:]):
+            raise ValueError(f"{name}: component of shape {tuple(t.shape)} / {t.dtype} is not a "
+                             f"contiguous fp32 {sh}")
+        _dev_check(t)
+
+
+def tensor_desc(x: torch.Tensor, has_l: bool) -> PrimeTensor:
+    """Descriptor of a [B, H, L, D] (has_l) or [B, H, D] view; D must be contiguous."""
+    if x.dtype not in _DTYPES:
+        raise RuntimeError(f"unsupported dtype {x.dtype}")
+    if x.stride(-1) != 1:
+        raise RuntimeError("innermost (head) dimension must be contiguous")
+    sb, sh = x.stride(0), x.stride(1)
+    sl = x.stride(2) if has_l else 0
+    return PrimeTensor(x.data_ptr(), _DTYPES[x.dtype], 0, sb, sh, sl)
+
+
+def state_desc(state: Optional[Sequence[torch.Tensor]]) -> Optional[PrimeState]:
+    if state is None:
+        return None
+    return PrimeState(*[t.data_ptr() for t in state])
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def decode_step(q, k, v, decay: torch.Tensor, eps: float, state_in, state_out, y) -> None:
+    """One fused decode step (prime_decode_step).  q [B,H,D], k/v [B,Hkv,D],
+    decay fp32 [H] on device, states: 6-tuples of contiguous fp32 tensors."""
+    _dev_check(q, k, v, y, decay)
+    B, H, D = q.shape
+    Hkv = k.shape[1]
+    _shape(k, (B, Hkv, D), "k")
+    _shape(v, (B, Hkv, D), "v")
+    _shape(y, (B, H, D), "y")
+    _check_decay(decay, H)
+    _check_state(state_in, B, H, D, "state_in")
+    _check_state(state_out, B, H, D, "state_out")
+    L = load()
+    qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), tensor_desc(y, False)
+    si, so = state_desc(state_in), state_desc(state_out)
+    rc = L.prime_decode_step(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), B, H, k.shape[1], D,
+                             decay.data_ptr(), float(eps), ctypes.byref(si) if si else None,
+                             ctypes.byref(so), ctypes.byref(yd), _stream(q.device))
+    _check(rc, "prime_decode_step")
+
+
+def workspace_size(B: int, H: int, L: int, flags: int = 0) -> int:
+    return int(load().prime_chunked_prefill_workspace_size(B, H, L, flags))
+
+
+def chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, state_in, y,
+                    state_out, flags: int = 0, workspace: Optional[torch.Tensor] = None) -> None:
+    """Chunked prefill (prime_chunked_prefill).  q [B,H,L,D], k/v [B,Hkv,L,D].
+    workspace: None allocates the recommended scratch from torch's caching
+    allocator; pass an empty tensor to run one segment per sequence."""
+    _dev_check(q, k, v, y, decay)
+    B, H, Lq, D = q.shape
+    Hkv = k.shape[1]
+    _shape(k, (B, Hkv, Lq, D), "k")
+    _shape(v, (B, Hkv, Lq, D), "v")
+    _shape(y, (B, H, Lq, D), "y")
+    _check_decay(decay, H)
+    _check_state(state_in, B, H, D, "state_in")
+    _check_state(state_out, B, H, D, "state_out")
+    L = load()
+    if workspace is None:
+        nbytes = workspace_size(B, H, Lq, flags)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+    elif workspace.numel() == 0:
+        workspace = None
+    else:
+        _dev_check(workspace)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    qd, kd, vd, yd = tensor_desc(q, True), tensor_desc(k, True), tensor_desc(v, True), tensor_desc(y, True)
+    si, so = state_desc(state_in), state_desc(state_out)
+    rc = L.prime_chunked_prefill(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), B, H, k.shape[1],
+                                 Lq, D, int(chunk), decay.data_ptr(), float(eps), int(flags),
+                                 ctypes.byref(si) if si else None, ctypes.byref(yd),
+                                 ctypes.byref(so) if so else None, ws_ptr, ws_bytes, _stream(q.device))
+    _check(rc, "prime_chunked_prefill")
+
+
+_decay_cache = {}
+
+
+def decay_tensor(decay, H: int, device: torch.device) -> torch.Tensor:
+    """fp32 [H] device tensor for a scalar decay or a per-head tensor."""
+    if torch.is_tensor(decay):
+        d = decay.detach().to(device=device, dtype=torch.float32).reshape(-1)
+        if d.numel() == 1:
+            d = d.expand(H)
+        if d.numel() != H:
+            raise ValueError(f"decay has {d.numel()} values for {H} heads")
+        return d.contiguous()
+    key = (float(decay), H, str(device))
+    t = _decay_cache.get(key)
+    if t is None:
+        t = torch.full((H,), float(decay), dtype=torch.float32, device=device)
+        _decay_cache[key] = t
+    return t
+
+
+def new_state(B: int, H: int, D: int, device, zero: bool = False) -> Tuple[torch.Tensor, ...]:
+    f = torch.zeros if zero else torch.empty
+    kw = dict(device=device, dtype=torch.float32)
+    return (f(B, H, D, **kw), f(B, H, D, D, **kw), f(B, H, D, D, **kw),
+            f(B, H, 1, **kw), f(B, H, D, **kw), f(B, H, D, **kw))
+
+
+def as_state(state, B: int, H: int, D: int, device) -> Tuple[torch.Tensor, ...]:
+    """Validate a reference-layout 6-tuple; return contiguous fp32 tensors."""
+    if len(state) != 6:
+        raise ValueError("state must be the 6-tuple (S0, S1, S2, K0, K1, K2)")
+    shapes = [(B, H, D), (B, H, D, D), (B, H, D, D), (B, H, 1), (B, H, D), (B, H, D)]
+    out = []
+    for t, s in zip(state, shapes):
+        if t.numel() != _prod(s):
+            raise ValueError(f"state component has shape {tuple(t.shape)}, expected {s}")
+        t = t.to(device=device, dtype=torch.float32)
+        out.append(t.reshape(s).contiguous())
+    return tuple(out)
+
+
+def _prod(s):
+    p = 1
+    for x in s:
+        p *= x
+    return p

@@ -1,0 +1,118 @@
+"""PrimeMomentAttention: drop-in for the reference's attention.py.
+
+Same constructor, same ``forward(hidden_states, state=None, return_state=False)
+-> (out, next_state)`` and the same 6-tuple fp32 state (S0, S1, S2, K0, K1, K2)
+(attention.py:42-210).  Projections, the optional LayerNorm QK-norm and o_proj
+are ordinary torch layers; everything between them -- the moment recurrence in
+all three regimes the reference dispatches on L (attention.py:120, 146, 161) --
+is one HIP kernel launch through the C ABI:
+
+  L == 1                     prime_decode_step (attention.py:119-143)
+  L >  chunk_threshold       prime_chunked_prefill (attention.py:145-158)
+  1 < L <= chunk_threshold   prime_chunked_prefill with PRIME_FLAG_DENSE_CLAMP,
+                             which reproduces the dense branch's clamp of the
+                             intra denominator before the incoming-state carry
+                             is added (attention.py:177, 185)
+
+The state is functional by default, as in the reference (a new 6-tuple is
+returned, the incoming one is untouched).  ``inplace_state=True`` updates the
+incoming tensors instead, with the same HBM traffic.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .chunked_ssd import prime_prefill
+
+
+class PrimeMomentAttention(nn.Module):
+    def __init__(
+        self,
+        hidden_size: int,
+        num_heads: int,
+        head_dim: int,
+        num_kv_heads: Optional[int] = None,
+        decay=0.9995,
+        use_qk_norm: bool = False,
+        eps: float = 1.0,
+        chunk_size: int = 64,
+        chunk_threshold: int = 512,
+        inplace_state: bool = False,
+    ):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.num_kv_heads = num_kv_heads or num_heads
+        self.num_kv_groups = num_heads // self.num_kv_heads
+        self.decay = decay
+        self.scaling = 1.0 / math.sqrt(head_dim)
+        self.eps = eps
+        self.use_qk_norm = use_qk_norm
+        self.chunk_size = chunk_size
+        self.chunk_threshold = chunk_threshold
+        self.inplace_state = inplace_state
+
+        self.q_proj = nn.Linear(hidden_size, num_heads * head_dim, bias=False)
+        self.k_proj = nn.Linear(hidden_size, self.num_kv_heads * head_dim, bias=False)
+        self.v_proj = nn.Linear(hidden_size, self.num_kv_heads * head_dim, bias=False)
+        self.o_proj = nn.Linear(num_heads * head_dim, hidden_size, bias=False)
+        if self.use_qk_norm:
+            self.q_norm = nn.LayerNorm(head_dim)
+            self.k_norm = nn.LayerNorm(head_dim)
+
+    def project(self, hidden_states: torch.Tensor):
+        """q (scaled), k, v as [B, H(kv), L, D] views (attention.py:83-101)."""
+        B, L, _ = hidden_states.shape
+        q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
+        k = self.k_proj(hidden_states).view(B, L, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        v = self.v_proj(hidden_states).view(B, L, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        if self.use_qk_norm:
+            q = self.q_norm(q)
+            k = self.k_norm(k)
+        q = q * self.scaling
+        return q, k, v
+
+    def forward(
+        self,
+        hidden_states: torch.Tensor,
+        state: Optional[Tuple[torch.Tensor, ...]] = None,
+        return_state: bool = False,
+    ):
+        B, L, _ = hidden_states.shape
+        orig_dtype = hidden_states.dtype
+        H, D = self.num_heads, self.head_dim
+        dev = hidden_states.device
+        q, k, v = self.project(hidden_states)
+        y_dtype = orig_dtype if orig_dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
+
+        if L == 1:
+            dec = _lib.decay_tensor(self.decay, H, dev)
+            st_in = _lib.as_state(state, B, H, D, dev) if state is not None else None
+            if self.inplace_state and st_in is not None and all(a is b for a, b in zip(st_in, state)):
+                st_out = st_in
+            else:
+                st_out = _lib.new_state(B, H, D, dev)
+            y = torch.empty(B, H, D, device=dev, dtype=y_dtype)
+            _lib.decode_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], dec, self.eps, st_in, st_out, y)
+            y = y.unsqueeze(2)
+            next_state = st_out
+        else:
+            dense = L <= self.chunk_threshold
+            st_out = None
+            if return_state and self.inplace_state and state is not None:
+                st_in = _lib.as_state(state, B, H, D, dev)
+                if all(a is b for a, b in zip(st_in, state)):
+                    st_out = st_in
+            y, next_state = prime_prefill(q, k, v, state=state, decay=self.decay, eps=self.eps,
+                                          chunk_size=self.chunk_size, return_state=return_state,
+                                          out_dtype=y_dtype, dense_clamp=dense, state_out=st_out)
+
+        y = y.to(orig_dtype).transpose(1, 2).reshape(B, L, H * D)
+        output = self.o_proj(y)
+        return output, (next_state if return_state else None)

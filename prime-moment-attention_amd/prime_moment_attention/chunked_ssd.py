@@ -1,0 +1,111 @@
+"""Chunked PRIME prefill: drop-in for the reference's chunked_ssd.py.
+
+``chunked_prime_ssd_core`` keeps the reference signature and contract
+(chunked_ssd.py:48-61): q, k, v are projected, normalised [B, H, L, D] tensors
+with q already scaled by 1/sqrt(D); it returns (y fp32 [B, H, L, D], state or
+None).  All of it runs in one HIP kernel launch (prime_chunked_prefill); see
+csrc/prefill.hip for the algorithm.
+
+Differences from the reference, by design:
+  * ``decay`` may also be an [H] tensor (one decay per head).
+  * q/k/v may be bf16 (read as-is) or fp32; k/v may carry fewer heads (GQA:
+    head h uses k/v head h // (H // H_kv), like attention.py:92-94).
+  * an incoming ``state`` is carried as the recurrence defines it.  The
+    reference core raises a shape error for a 6-tuple state (its 3-D state
+    components broadcast against a 5-D decay table, chunked_ssd.py:129-137).
+  * the result does not depend on ``chunk_size`` beyond rounding (the chunked
+    form is exact for every chunk size); the kernel tiles 64 tokens.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+
+def _prep(x: torch.Tensor) -> torch.Tensor:
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.float()
+    if x.stride(-1) != 1 or x.data_ptr() % 16 or any((s * x.element_size()) % 16 for s in x.stride()[:-1]):
+        x = x.contiguous()
+    return x
+
+
+def prime_prefill(q, k, v, state=None, decay=0.9995, eps=1.0, chunk_size=64, return_state=False,
+                  out_dtype=torch.float32, dense_clamp=False, state_out=None):
+    """Core launcher shared by the modules.  Returns (y, next_state | None)."""
+    B, H, L, D = q.shape
+    q, k, v = _prep(q), _prep(k), _prep(v)
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        k, v = k.to(q.dtype), v.to(q.dtype)
+    dev = q.device
+    dec = _lib.decay_tensor(decay, H, dev)
+    st_in = _lib.as_state(state, B, H, D, dev) if state is not None else None
+    y = torch.empty(B, H, L, D, device=dev, dtype=out_dtype)
+    st_out = None
+    if return_state:
+        st_out = state_out if state_out is not None else _lib.new_state(B, H, D, dev)
+    _lib.chunked_prefill(q, k, v, dec, eps, chunk_size, st_in, y, st_out,
+                         _lib.PRIME_FLAG_DENSE_CLAMP if dense_clamp else 0)
+    return y, st_out
+
+
+def chunked_prime_ssd_core(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    state: Optional[Tuple[torch.Tensor, ...]] = None,
+    decay: float = 0.9995,
+    eps: float = 1.0,
+    chunk_size: int = 64,
+    return_state: bool = False,
+) -> Tuple[torch.Tensor, Optional[Tuple[torch.Tensor, ...]]]:
+    """Drop-in for chunked_ssd.py:48-184 (same arguments, same outputs)."""
+    if chunk_size <= 0:
+        raise ValueError("chunk_size must be positive")
+    return prime_prefill(q, k, v, state=state, decay=decay, eps=eps, chunk_size=chunk_size,
+                         return_state=return_state, out_dtype=torch.float32)
+
+
+class ChunkedPrimeSSD(nn.Module):
+    """Module twin that always runs the chunked core (chunked_ssd.py:187-251)."""
+
+    def __init__(self, hidden_size: int, num_heads: int, head_dim: int, chunk_size: int = 64,
+                 decay: float = 0.9995, eps: float = 1.0, use_qk_norm: bool = True):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.chunk_size = chunk_size
+        self.decay = decay
+        self.eps = eps
+        self.scaling = 1.0 / math.sqrt(head_dim)
+        self.use_qk_norm = use_qk_norm
+        self.q_proj = nn.Linear(hidden_size, num_heads * head_dim, bias=False)
+        self.k_proj = nn.Linear(hidden_size, num_heads * head_dim, bias=False)
+        self.v_proj = nn.Linear(hidden_size, num_heads * head_dim, bias=False)
+        self.o_proj = nn.Linear(num_heads * head_dim, hidden_size, bias=False)
+        if self.use_qk_norm:
+            self.q_norm = nn.LayerNorm(head_dim)
+            self.k_norm = nn.LayerNorm(head_dim)
+
+    def forward(self, hidden_states: torch.Tensor, state=None, return_state: bool = False):
+        B, L, _ = hidden_states.shape
+        dtype = hidden_states.dtype
+        q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
+        k = self.k_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
+        v = self.v_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
+        if self.use_qk_norm:
+            q = self.q_norm(q)
+            k = self.k_norm(k)
+        q = q * self.scaling
+        y, next_state = prime_prefill(q, k, v, state=state, decay=self.decay, eps=self.eps,
+                                      chunk_size=self.chunk_size, return_state=return_state,
+                                      out_dtype=dtype if dtype in (torch.float32, torch.bfloat16,
+                                                                   torch.float16) else torch.float32)
+        y = y.to(dtype).transpose(1, 2).reshape(B, L, self.num_heads * self.head_dim)
+        return self.o_proj(y), next_state

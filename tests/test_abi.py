@@ -1,0 +1,86 @@
+"""CPU checks of the C-ABI library: it loads without a GPU, exports every
+symbol include/prime_mi355x.h declares, and rejects bad arguments before any
+device work (error codes + prime_last_error)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from prime_moment_attention import _lib
+
+HDR = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                   "prime_mi355x.h")
+
+
+def _declared():
+    src = open(HDR).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char \*)\s*(prime_\w+)\s*\(", src, re.M)))
+
+
+def test_header_declares_exports():
+    assert _declared() == sorted(_lib.EXPORTS)
+
+
+def test_library_loads_and_exports_every_symbol():
+    L = _lib.load()
+    for name in _declared():
+        assert hasattr(L, name), name
+    assert L.prime_abi_version() == _lib.ABI_VERSION
+
+
+def test_null_arguments_rejected_without_device_work():
+    L = _lib.load()
+    st = _lib.PrimeState()
+    rc = L.prime_decode_step(None, None, None, 1, 1, 1, 64, None, 1.0, None, ctypes.byref(st), None, None)
+    assert rc == -1
+    assert "null" in _lib.last_error()
+    rc = L.prime_chunked_prefill(None, None, None, 1, 1, 1, 8, 64, 64, None, 1.0, 0, None, None, None, None, 0, None)
+    assert rc == -1
+
+
+def test_bad_dims_and_dtypes_rejected():
+    L = _lib.load()
+    t = _lib.PrimeTensor(16, _lib.PRIME_BF16, 0, 0, 0, 0)  # never dereferenced: validation fails first
+    st = _lib.PrimeState(16, 16, 16, 16, 16, 16)
+    b = ctypes.byref
+    rc = L.prime_decode_step(b(t), b(t), b(t), 1, 1, 1, 32, 16, 1.0, None, b(st), b(t), None)
+    assert rc == -2 and "head dim" in _lib.last_error()
+    rc = L.prime_decode_step(b(t), b(t), b(t), 1, 3, 2, 64, 16, 1.0, None, b(st), b(t), None)
+    assert rc == -1  # H not a multiple of H_kv
+    t16 = _lib.PrimeTensor(16, _lib.PRIME_F16, 0, 0, 0, 0)
+    rc = L.prime_chunked_prefill(b(t16), b(t16), b(t16), 1, 1, 1, 8, 64, 64, 16, 1.0, 0, None, b(t), None, None, 0, None)
+    assert rc == -3
+    rc = L.prime_chunked_prefill(b(t), b(t), b(t), 1, 1, 1, 8, 64, 64, 16, 1.0, 8, None, b(t), None, None, 0, None)
+    assert rc == -1 and "flags" in _lib.last_error()
+    tm = _lib.PrimeTensor(18, _lib.PRIME_BF16, 0, 0, 0, 0)  # misaligned rows
+    rc = L.prime_chunked_prefill(b(tm), b(tm), b(tm), 1, 1, 1, 8, 64, 64, 16, 1.0, 0, None, b(tm), None, None, 0, None)
+    assert rc == -4
+
+
+def test_partial_state_overlap_rejected():
+    L = _lib.load()
+    t = _lib.PrimeTensor(16, _lib.PRIME_BF16, 0, 0, 0, 0)
+    b = ctypes.byref
+    base = 1 << 20
+    sin = _lib.PrimeState(*[base + i * 65536 for i in range(6)])
+    sout = _lib.PrimeState(*[base + (i + 6) * 65536 for i in range(5)] + [base + 5 * 65536])
+    rc = L.prime_decode_step(b(t), b(t), b(t), 1, 1, 1, 64, 16, 1.0, b(sin), b(sout), b(t), None)
+    assert rc == -5 and "overlaps" in _lib.last_error()
+
+
+def test_host_wrappers_refuse_cpu_tensors():
+    import torch
+    x = torch.zeros(1, 1, 64)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        _lib.decode_step(x, x, x, torch.ones(1), 1.0, None, _lib.new_state(1, 1, 64, "cpu"), x)
+
+
+def test_workspace_plan():
+    """Few long sequences are cut into segments (a workspace is requested);
+    many sequences or the dense branch run one segment each (none needed)."""
+    assert _lib.workspace_size(8, 12, 8192) > 0
+    assert _lib.workspace_size(8, 12, 8192) % 16 == 0
+    assert _lib.workspace_size(1, 1000, 8192) == 0
+    assert _lib.workspace_size(8, 12, 8192, _lib.PRIME_FLAG_DENSE_CLAMP) == 0
+    assert _lib.workspace_size(1, 1, 64) == 0
