@@ -168,10 +168,7 @@ int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, cons
     const int S = B * H;
     prime::plan_segments(S, L, a.dense_clamp != 0, workspace ? workspace_bytes : 0, &a.G, &a.cps);
     a.ws = a.G > 1 ? static_cast<float *>(workspace) : nullptr;
-    // With one segment per sequence and few sequences, split the value columns
-    // over two workgroups.  Both slices read the K state, so an in-place state
-    // forbids it.
-    a.nsplit = (a.G == 1 && S <= 160 && !inplace) ? 2 : 1;
+    (void)inplace;  // in place is safe: each workgroup reads its own state before writing it
     return check_hip(prime::launch_prefill(a, static_cast<hipStream_t>(stream)), "prefill launch");
 }
 

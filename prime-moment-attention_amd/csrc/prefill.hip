@@ -2,35 +2,40 @@
 //
 // Semantics: chunked_prime_ssd_core (chunked_ssd.py:48-184) of the reference,
 // and with PRIME_FLAG_DENSE_CLAMP the module's dense branch
-// (attention.py:160-202).  For each (b,h) the tokens are processed in 64-token
-// chunks.  With features Fq_i = [q_i, q_i*q_i/2], Fk_j = [k_j, k_j*k_j]
-// (128 wide) and the state packed as Sst = [S1; S2] (128 x D), Kst = [K1; K2]:
-//   A_ij   = l^(i-j) [i>=j] (1 + Fq_i . Fk_j)                      (intra block)
-//   num_i  = sum_j A_ij v_j + l^(i+1) (S0 + Fq_i Sst)
-//   den_i  = sum_j A_ij     + l^(i+1) (K0 + Fq_i . Kst)
-//   y_i    = num_i / max(den_i, eps)
-//   Sst   <- l^n Sst + sum_j l^(n-1-j) Fk_j^T v_j   (n = valid tokens in chunk)
+// (attention.py:160-202).  Per (b,h), tokens are processed in 64-token chunks.
+// With query/key features Fq_i = [q_i, q_i*q_i], Fk_j = [k_j, k_j*k_j/2]
+// (128 wide) and the state kept as M = [S1; S2/2] (128 x 64) plus the K state
+// [K1; K2/2]:
+//   A_ij  = l^(i-j) [i>=j] (1 + Fq_i . Fk_j)                        (intra block)
+//   num_i = sum_j A_ij v_j + l^(i+1) (S0 + Fq_i M)
+//   den_i = sum_j A_ij     + l^(i+1) (K0 + Fq_i . [K1; K2/2])
+//   y_i   = num_i / max(den_i, eps)
+//   M    <- l^n M + sum_j Fk_j^T (w_j v_j),  w_j = l^(n-1-j)  (n valid tokens)
 // The reference's O(Nc^2) inter-chunk matrix (chunked_ssd.py:113-126) is the
-// closed form of this carried scan; padding is handled exactly by decaying with
-// the number of valid tokens, which equals the reference's l^(-pad) correction
+// closed form of this carried scan; padding is exact because decays use the
+// number of valid tokens, which equals the reference's l^(-pad) correction
 // (chunked_ssd.py:171-178).
 //
-// Mapping: one workgroup (4 wavefronts) per (sequence, value-column slice of
-// NV columns).  The state slice lives in MFMA accumulators across all chunks
-// (fp32); a bf16 copy in LDS feeds the readout.  Wave w owns query rows
-// [16w, 16w+16) for the score block, the intra product and the readout, and
-// feature rows [32w, 32w+32) of the state.  The score block is computed
-// transposed (S^T = Fk Fq^T) so its accumulator layout is directly the A
-// operand of the A.V product (the token index is permuted consistently in the
-// V operand), without an LDS round trip.  q/k/v tiles for chunk c+1 are loaded
-// into registers while chunk c computes.  Workgroups that share a sequence are
-// placed on the same XCD (blockIdx % 8) so their q/k reads share its L2.
+// Layout and mapping.  One workgroup per (sequence, segment) with two roles:
+//   readout waves 0..3 own query rows [16w, 16w+16): score block S^T = Fk Fq^T,
+//     y^T = V^T A^T + M^T Fq^T (computed transposed so each lane holds its own
+//     query row and four consecutive value columns), y stores;
+//   update waves 4..7 own feature rows [32u, 32u+32) of M in fp32 MFMA
+//     accumulators and add each chunk's Fk^T (w v).
+// q/k/v tiles stay row-major in LDS (16-byte stores).  Operands contracted over
+// the token index are read with ds_read_b64_tr_b16: in a 16-lane group, lane s
+// addresses X[r0 + s/4][c0 + 4(s%4)] and lane i receives X[r0 + e][c0 + i],
+// e = 0..3, i.e. four consecutive tokens of one column.  A 16-column block
+// whose first column is 1 (w in the update) rides along every product and
+// yields the intra denominator, the K state and its readout on MFMA.
+// Per chunk: barrier; readout and update compute (readout waves prefetch the
+// next chunk from HBM); barrier; the update role publishes the bf16 state copy
+// while both roles write the next chunk's tiles.
 //
-// Precision: bf16 inputs are exact in the MFMA operands; derived operands
-// (squares, decay-scaled features, the score block, the state copy) are rounded
-// to bf16 once.  fp32 inputs (F32IN) keep fp32 tiles in LDS and split every
-// operand x into bf16 hi + lo, accumulating hi*hi + hi*lo + lo*hi (three MFMAs
-// per product, ~2^-16 relative), with a hi/lo copy of the state.
+// Precision: bf16 inputs enter the MFMA exactly; derived operands (squares,
+// the score block, the state copy, w v) are rounded to bf16 once.  fp32 inputs
+// (F32IN) keep every LDS array as a bf16 hi plane plus a lo residual plane and
+// accumulate hi*hi + hi*lo + lo*hi (three MFMAs per product, ~2^-16 relative).
 
 #include "prime_kernels.h"
 
@@ -38,14 +43,24 @@ namespace prime {
 
 constexpr int kC = 64;          // tokens per chunk
 constexpr int kF = 2 * kD;      // feature width
-constexpr int kPF = kF + 8;     // LDS pitch for the 128-wide transposed state
+constexpr int kPW = kF + 8;     // pitch of 128-wide rows read 16 bytes per lane (68 dwords)
+// Pitch of rows read with ds_read_b64_tr_b16.  A 16-lane group reads 4
+// consecutive rows x 32 contiguous bytes and the next group the next 4 rows: a
+// pitch of 72 dwords (8 mod 32 and mod 64) puts 8 consecutive rows' windows on
+// disjoint banks.  The fp32 path (two planes per array) uses the tighter 68 /
+// 44-dword pitches to fit in LDS.
+constexpr int kPT = kF + 16;
 
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 r) { return __builtin_bit_cast(bf16x8, r); }
 
+// two floats -> packed bf16 pair (one v_cvt_pk_bf16_f32, round to nearest even)
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 __device__ __forceinline__ void unpack8(u32x4 r, float (&f)[8]) {
@@ -74,21 +89,6 @@ struct Opnd {
 };
 
 template <bool S>
-__device__ __forceinline__ Opnd<S> split8(const float (&f)[8]) {
-    Opnd<S> o;
-    const u32x4 hr = pack8(f);
-    o.h = as_bf16x8(hr);
-    if constexpr (S) {
-        float hf[8], r[8];
-        unpack8(hr, hf);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] = f[i] - hf[i];
-        o.l = as_bf16x8(pack8(r));
-    }
-    return o;
-}
-
-template <bool S>
 __device__ __forceinline__ f32x4 mma(const Opnd<S> &a, const Opnd<S> &b, f32x4 c) {
     c = mfma(a.h, b.h, c);
     if constexpr (S) {
@@ -98,46 +98,51 @@ __device__ __forceinline__ f32x4 mma(const Opnd<S> &a, const Opnd<S> &b, f32x4 c
     return c;
 }
 
-// 8 consecutive LDS elements as fp32
-__device__ __forceinline__ void lds8(const uint16_t *p, float (&f)[8]) {
-    unpack8(*reinterpret_cast<const u32x4 *>(p), f);
-}
-__device__ __forceinline__ void lds8(const float *p, float (&f)[8]) {
-    const f32x4 a = reinterpret_cast<const f32x4 *>(p)[0], b = reinterpret_cast<const f32x4 *>(p)[1];
+// 8 floats -> bf16 hi (and lo residual) packed
+template <bool S>
+__device__ __forceinline__ void split_pack(const float (&f)[8], u32x4 &hi, u32x4 &lo) {
+    hi = pack8(f);
+    if constexpr (S) {
+        float hf[8], r[8];
+        unpack8(hi, hf);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f[i] = a[i];
-        f[4 + i] = b[i];
-    }
-}
-__device__ __forceinline__ float ldsf(const uint16_t *p) { return bf16_bits_to_f32(*p); }
-__device__ __forceinline__ float ldsf(const float *p) { return *p; }
-
-// identity features: a bf16 row is already an operand
-template <bool S, typename T>
-__device__ __forceinline__ Opnd<S> raw_op(const T *p) {
-    if constexpr (!S) {
-        Opnd<S> o;
-        o.h = as_bf16x8(*reinterpret_cast<const u32x4 *>(p));
-        return o;
-    } else {
-        float f[8];
-        lds8(p, f);
-        return split8<S>(f);
+        for (int i = 0; i < 8; ++i) r[i] = f[i] - hf[i];
+        lo = pack8(r);
     }
 }
 
-// s*x or s*x*x features
-template <bool S, typename T>
-__device__ __forceinline__ Opnd<S> xform_op(const T *p, bool square, float s) {
-    float f[8];
-    lds8(p, f);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = square ? s * f[i] * f[i] : s * f[i];
-    return split8<S>(f);
+// 16-byte LDS read
+__device__ __forceinline__ u32x4 lds128(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
+
+// ds_read_b64_tr_b16 (see the header comment for the lane mapping)
+__device__ __forceinline__ uint2 lds_tr(const uint16_t *p) {
+    typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(const_cast<uint16_t *>(p)));
+    return __builtin_bit_cast(uint2, v);
 }
 
-// Registers holding one 8-element row segment of the next chunk.
+// operand of 8 consecutive tokens (two transposed 4-token reads) of one column
+template <bool S>
+__device__ __forceinline__ Opnd<S> tr_op(const uint16_t *p0, const uint16_t *p1, size_t plane) {
+    Opnd<S> o;
+    const uint2 a = lds_tr(p0), b = lds_tr(p1);
+    o.h = as_bf16x8(u32x4{a.x, a.y, b.x, b.y});
+    if constexpr (S) {
+        const uint2 c = lds_tr(p0 + plane), d = lds_tr(p1 + plane);
+        o.l = as_bf16x8(u32x4{c.x, c.y, d.x, d.y});
+    }
+    return o;
+}
+
+template <bool S>
+__device__ __forceinline__ Opnd<S> row_op(const uint16_t *p, size_t plane) {
+    Opnd<S> o;
+    o.h = as_bf16x8(lds128(p));
+    if constexpr (S) o.l = as_bf16x8(lds128(p + plane));
+    return o;
+}
+
+// one 8-element row segment of a q/k/v tile, kept packed until it is stored
 template <bool F32IN>
 struct Seg8;
 template <>
@@ -149,119 +154,226 @@ struct Seg8<true> {
     f32x4 a, b;
 };
 
+// Branch-free: the caller passes an in-bounds offset (rows past L clamped to
+// row L-1) and the value is replaced by zero when !valid.  (A conditional load
+// here lets the optimiser merge the stores into a pointer select and keep the
+// prefetch registers in scratch memory.)
 template <bool F32IN>
 __device__ __forceinline__ Seg8<F32IN> load_seg(const void *base, int64_t off, bool valid) {
     Seg8<F32IN> s;
     if constexpr (!F32IN) {
-        s.r = u32x4{0u, 0u, 0u, 0u};
-        if (valid) s.r = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(base) + off);
+        const u32x4 x = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(base) + off);
+        const uint32_t m = valid ? 0xFFFFFFFFu : 0u;
+        s.r = u32x4{x[0] & m, x[1] & m, x[2] & m, x[3] & m};
     } else {
-        s.a = f32x4{0.f, 0.f, 0.f, 0.f};
-        s.b = s.a;
-        if (valid) {
-            const f32x4 *p = reinterpret_cast<const f32x4 *>(static_cast<const float *>(base) + off);
-            s.a = p[0];
-            s.b = p[1];
-        }
+        const f32x4 *p = reinterpret_cast<const f32x4 *>(static_cast<const float *>(base) + off);
+        const f32x4 a = p[0], b = p[1];
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        s.a = valid ? a : z;
+        s.b = valid ? b : z;
     }
     return s;
 }
 
-// row-major store of a segment (8 elements at p)
-__device__ __forceinline__ void store_row(uint16_t *p, const Seg8<false> &s) {
-    *reinterpret_cast<u32x4 *>(p) = s.r;
+__device__ __forceinline__ void seg_f32(const Seg8<false> &s, float (&f)[8]) { unpack8(s.r, f); }
+__device__ __forceinline__ void seg_f32(const Seg8<true> &s, float (&f)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[i] = s.a[i];
+        f[4 + i] = s.b[i];
+    }
 }
-__device__ __forceinline__ void store_row(float *p, const Seg8<true> &s) {
-    reinterpret_cast<f32x4 *>(p)[0] = s.a;
-    reinterpret_cast<f32x4 *>(p)[1] = s.b;
+
+// store 8 fp32 as bf16 (hi plane, lo plane when S) at p
+template <bool S>
+__device__ __forceinline__ void put8(uint16_t *p, size_t plane, const float (&f)[8]) {
+    u32x4 hi, lo;
+    split_pack<S>(f, hi, lo);
+    *reinterpret_cast<u32x4 *>(p) = hi;
+    if constexpr (S) *reinterpret_cast<u32x4 *>(p + plane) = lo;
 }
-// element e of a segment in storage format
-__device__ __forceinline__ uint16_t seg_elem(const Seg8<false> &s, int e) {
-    return static_cast<uint16_t>((e & 1) ? (s.r[e >> 1] >> 16) : (s.r[e >> 1] & 0xFFFFu));
+
+template <bool S>
+__device__ __forceinline__ void put1(uint16_t *p, size_t plane, float x) {
+    const uint16_t hb = f32_to_bf16_bits(x);
+    *p = hb;
+    if constexpr (S) p[plane] = f32_to_bf16_bits(x - bf16_bits_to_f32(hb));
 }
-__device__ __forceinline__ float seg_elem(const Seg8<true> &s, int e) { return e < 4 ? s.a[e] : s.b[e - 4]; }
+
+// Registers holding the next chunk's tiles (kept packed until stored).  Each
+// role's 256 threads read rows rt/8 and rt/8 + 32, 16-byte segment rt%8, so a
+// wave's load covers 8 whole 128-byte rows.  Both roles fill the same four
+// slots -- readout: q -> r0,r1 and k -> r2,r3; update: v -> r0,r1 and k
+// (state-only launch) or zero -> r2,r3 -- so that no role branch leaves a slot
+// unwritten (which makes the optimiser keep the slots in scratch memory behind
+// a pointer select).
+template <bool F32IN>
+struct TileRegs {
+    Seg8<F32IN> r0, r1, r2, r3;
+};
+
+template <bool F32IN, bool STATE_ONLY>
+__device__ __forceinline__ void load_tiles_fn(const PrefillArgs &a, TileRegs<F32IN> &R, int c, int rt, bool is_u,
+                                              int64_t qb, int64_t kb, int64_t vb) {
+    const int col = 8 * (rt & 7);
+    const int ta = c * kC + (rt >> 3), tb = ta + 32;
+    const bool oka = ta < a.L, okb = tb < a.L;
+    const int sa = oka ? ta : a.L - 1, sb = okb ? tb : a.L - 1;  // in-bounds rows for the masked loads
+    const void *x = is_u ? a.v : a.q;
+    const int64_t xb = is_u ? vb : qb, xl = is_u ? a.v_sl : a.q_sl;
+    R.r0 = load_seg<F32IN>(x, xb + sa * xl + col, oka);
+    R.r1 = load_seg<F32IN>(x, xb + sb * xl + col, okb);
+    // update waves of the fused kernel need no k: they re-read their v rows (L1
+    // hits) and mask them to zero
+    const bool want_k = !is_u || STATE_ONLY;
+    const void *kx = want_k ? a.k : x;
+    const int64_t kbb = want_k ? kb : xb, kl = want_k ? a.k_sl : xl;
+    R.r2 = load_seg<F32IN>(kx, kbb + sa * kl + col, oka && want_k);
+    R.r3 = load_seg<F32IN>(kx, kbb + sb * kl + col, okb && want_k);
+}
+
+// One 8-column segment of one token row: q -> [q | q*q], k -> [k | k*k/2],
+// v -> v and w v (plus w itself in column 64 from the segment-0 thread).
+template <bool F32IN, bool STATE_ONLY>
+__device__ __forceinline__ void store_seg_fn(const Seg8<F32IN> &x01, const Seg8<F32IN> &k, int row, int col,
+                                             bool is_u, float w, uint16_t *sQf, size_t plQ, uint16_t *sKf,
+                                             size_t plK, int kPK, uint16_t *sV, size_t plV, uint16_t *sVw,
+                                             size_t plVw, int kPV) {
+    constexpr bool S = F32IN;
+    float x[8], y2[8];
+    if (!is_u || STATE_ONLY) {
+        if (!is_u) {
+            seg_f32(x01, x);
+            put8<S>(sQf + row * kPW + col, plQ, x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y2[e] = x[e] * x[e];
+            put8<S>(sQf + row * kPW + kD + col, plQ, y2);
+        }
+        seg_f32(k, x);
+        put8<S>(sKf + row * kPK + col, plK, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y2[e] = 0.5f * x[e] * x[e];
+        put8<S>(sKf + row * kPK + kD + col, plK, y2);
+    }
+    if (is_u) {
+        seg_f32(x01, x);
+        if constexpr (!STATE_ONLY) put8<S>(sV + row * kPV + col, plV, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y2[e] = w * x[e];
+        put8<S>(sVw + row * kPV + col, plVw, y2);
+        if (col == 0) put1<S>(sVw + row * kPV + kD, plVw, w);
+    }
+}
+
+template <bool F32IN, bool STATE_ONLY>
+__device__ __forceinline__ void store_tiles_fn(const TileRegs<F32IN> &R, int rt, bool is_u, const float *sPw,
+                                               int nvalid, uint16_t *sQf, size_t plQ, uint16_t *sKf, size_t plK,
+                                               int kPK, uint16_t *sV, size_t plV, uint16_t *sVw, size_t plVw,
+                                               int kPV) {
+    const int col = 8 * (rt & 7);
+    const int ra = rt >> 3, rb = ra + 32;
+    const float wa = ra < nvalid ? sPw[nvalid - 1 - ra] : 0.f;
+    const float wb = rb < nvalid ? sPw[nvalid - 1 - rb] : 0.f;
+    store_seg_fn<F32IN, STATE_ONLY>(R.r0, R.r2, ra, col, is_u, wa, sQf, plQ, sKf, plK, kPK, sV, plV, sVw, plVw, kPV);
+    store_seg_fn<F32IN, STATE_ONLY>(R.r1, R.r3, rb, col, is_u, wb, sQf, plQ, sKf, plK, kPK, sV, plV, sVw, plVw, kPV);
+}
 
 // Segment plan.  Without a workspace (or for the dense branch, whose clamp
-// needs the incoming state separate from the tokens of this call) every
-// sequence is one segment.  Otherwise sequences are cut into segments of whole
-// chunks so that about kTargetUnits workgroups run, each segment >= kMinCps
-// chunks long.
-constexpr int kTargetUnits = 768;
+// needs the incoming state apart from the tokens of this call) every sequence
+// is one segment.  Otherwise choose the number of segments G minimising a
+// simple cost in chunk-steps: the fused kernel runs one workgroup per CU, in
+// ceil(S*G / CUs) rounds of cps chunks each; the state-only pass (about half
+// the cost per chunk, several workgroups per CU) and the scan add the rest,
+// and every workspace slot costs ~4 x 33.8 KB of HBM traffic (~0.03 chunk-steps).
 constexpr int kMinCps = 4;
+
+static int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
 
 void plan_segments(int S, int L, bool dense_clamp, size_t ws_bytes, int *G, int *cps) {
     const int NC = (L + kC - 1) / kC;
-    int g = 1;
-    if (!dense_clamp && S < kTargetUnits) {
-        g = (kTargetUnits + S - 1) / S;
-        const int gmax = NC / kMinCps;
-        if (g > gmax) g = gmax;
-        if (g < 1) g = 1;
+    int best_g = 1, best_c = NC;
+    if (!dense_clamp && NC >= 2 * kMinCps) {
+        const int cu = device_cus();
+        const int gmax = NC / kMinCps < 64 ? NC / kMinCps : 64;
+        double best = 1e300;
+        for (int g0 = 1; g0 <= gmax; ++g0) {
+            const int c = (NC + g0 - 1) / g0;
+            const int g = (NC + c - 1) / c;  // no empty segments
+            if (g > 1 && static_cast<size_t>(S) * g * kWsStride * sizeof(float) > ws_bytes) continue;
+            const double rounds = static_cast<double>((static_cast<int64_t>(S) * g + cu - 1) / cu);
+            double cost = rounds * c;
+            if (g > 1)
+                cost += 0.5 * static_cast<double>((static_cast<int64_t>(S) * (g - 1) + 4 * cu - 1) / (4 * cu)) * c +
+                        1.0 + 0.03 * S * g;
+            if (cost < best - 1e-9) {
+                best = cost;
+                best_g = g;
+                best_c = c;
+            }
+        }
     }
-    int c = (NC + g - 1) / g;
-    g = (NC + c - 1) / c;  // no empty segments
-    while (g > 1 && static_cast<size_t>(S) * g * kWsStride * sizeof(float) > ws_bytes) {
-        c = c * 2;
-        g = (NC + c - 1) / c;
-    }
-    if (g <= 1) {
-        g = 1;
-        c = NC;
-    }
-    *G = g;
-    *cps = c;
+    *G = best_g;
+    *cps = best_c;
 }
 
-// One workgroup = (sequence, segment[, value slice]).  STATE_ONLY: only the
-// segment's state contribution from a zero state (no q, no output) -> ws slot.
-template <int NV, bool F32IN, bool STATE_ONLY>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a) {
-    using T = typename std::conditional<F32IN, float, uint16_t>::type;  // tile storage
-    constexpr bool S = F32IN;                    // split operands
-    constexpr int NP = S ? 2 : 1;                // state planes (hi, lo)
-    constexpr int kP = F32IN ? kD + 4 : kD + 8;  // tile row pitch (elements; 16-byte multiple)
-    constexpr int NB = NV / 16;                  // 16-wide value blocks per workgroup
-    constexpr int NVL = NV / 32;                 // v segments per thread
-    constexpr int QR = STATE_ONLY ? 1 : kC;      // q / bf16-state buffers unused when STATE_ONLY
-    constexpr int SR = STATE_ONLY ? 1 : NV;
+// One workgroup = (sequence, segment); see the header comment.  STATE_ONLY
+// launches the update role alone (4 waves, which also write the k tile) from
+// a zero state and stores the segment's contribution in its workspace slot.
+template <bool F32IN, bool STATE_ONLY>
+__global__ __launch_bounds__(512, 1) void prefill_kernel(const PrefillArgs a) {
+    constexpr bool S = F32IN;        // split operands
+    constexpr int NP = S ? 2 : 1;    // LDS planes (hi, lo)
+    constexpr int NB = kD / 16;      // value blocks
+    constexpr int NBX = NB + 1;      // + the ones / K block
+    constexpr int QR = STATE_ONLY ? 1 : kC;
+    constexpr int SR = STATE_ONLY ? 1 : kD + 1;  // state copy rows: 64 value columns + K
+    constexpr int kPK = F32IN ? kPW : kPT;       // sKf pitch (16-byte rows and transposed reads)
+    constexpr int kPV = F32IN ? kD + 24 : kPT;   // v pitch: 64 values + the 16-wide ones block
 
-    __shared__ __attribute__((aligned(16))) T sQ[QR][kP];               // q rows (pre-scaled)
-    __shared__ __attribute__((aligned(16))) T sK[QR][kP];               // k rows
-    __shared__ __attribute__((aligned(16))) T sKt[kD][kP];              // k transposed [f][j]
-    __shared__ __attribute__((aligned(16))) T sVt[NV][kP];              // v transposed [n][j]
-    __shared__ __attribute__((aligned(16))) uint16_t sSt[NP][SR][kPF];  // bf16 state [n][f]
-    __shared__ __attribute__((aligned(16))) float sW[kC];               // token weights of the chunk
-    __shared__ float sPw[kC + 2];                                       // l^n, n = 0..65
-    __shared__ float sPs[kC + 2];                                       // sum_{m<n} l^m
-    __shared__ __attribute__((aligned(16))) float sKc[kF], sKi[kF];     // K state (call / init part)
-    __shared__ float sS0[NV], sK0[2];
+    __shared__ __attribute__((aligned(16))) uint16_t sQf[NP][QR][kPW];   // [q | q*q]
+    __shared__ __attribute__((aligned(16))) uint16_t sKf[NP][kC][kPK];   // [k | k*k/2]
+    __shared__ __attribute__((aligned(16))) uint16_t sV[NP][QR][kPV];    // [v | 1 0..0]
+    __shared__ __attribute__((aligned(16))) uint16_t sVw[NP][kC][kPV];   // [w v | w 0..0]
+    __shared__ __attribute__((aligned(16))) uint16_t sSt[NP][SR][kPW];   // bf16 [S1; S2/2 | K]^T
+    __shared__ float sPw[kC + 2];                                         // l^n, n = 0..65
+    __shared__ float sPs[kC + 2];                                         // sum_{m<n} l^m
+    __shared__ __attribute__((aligned(16))) float sS0[kD];
+    __shared__ float sKi[kF];                                             // incoming [K1; K2/2] (dense)
+    __shared__ float sK0[2];                                              // K0 of the call / incoming
+    constexpr size_t plQ = static_cast<size_t>(QR) * kPW, plK = static_cast<size_t>(kC) * kPK;
+    constexpr size_t plV = static_cast<size_t>(QR) * kPV, plVw = static_cast<size_t>(kC) * kPV;
+    constexpr size_t plS = static_cast<size_t>(SR) * kPW;
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
+    const bool is_u = STATE_ONLY || wave >= 4;
+    const int u = STATE_ONLY ? wave : wave - 4;  // update-wave index
+    const int utid = 64 * u + lane;              // thread index within the update role
+    const int tr_r = c16 >> 2, tr_c = 4 * (c16 & 3);  // ds_read_tr address offsets of this lane
 
-    // ---- workgroup -> (sequence, segment, value slice); with two slices the
-    // pair shares an XCD (blockIdx % 8) so its q/k reads share that L2
     const int Sq = a.B * a.H;
-    int unit, split;
-    if (a.nsplit == 1) {
-        unit = blockIdx.x;
-        split = 0;
-    } else {
-        split = (blockIdx.x >> 3) & 1;
-        unit = ((blockIdx.x >> 4) << 3) + (blockIdx.x & 7);
-    }
+    const int unit = blockIdx.x;
     if (unit >= Sq * a.nseg_launch) return;  // whole workgroup leaves before any barrier
     const int seq = unit / a.nseg_launch, seg = unit - seq * a.nseg_launch;
     const int b = seq / a.H, h = seq - b * a.H, hk = h / a.group;
-    const int n0 = split * NV;
     const float lam = a.decay[h];
     const int NC = (a.L + kC - 1) / kC;
     const int c_begin = seg * a.cps;
     const int c_end = min(c_begin + a.cps, NC);
     const bool from_ws = !STATE_ONLY && a.G > 1;
     const bool has_in = !STATE_ONLY && !from_ws && a.s1i != nullptr;
-    const bool last_seg = seg == a.G - 1;
+    const bool dense = !STATE_ONLY && a.dense_clamp;
     float *wslot = a.ws ? a.ws + (static_cast<size_t>(seq) * a.G + seg) * kWsStride : nullptr;
 
     if (tid < kC + 2) {
@@ -271,73 +383,83 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a) {
         for (int m = 0; m < tid; ++m, pm *= ld) ps += pm;
         sPs[tid] = static_cast<float>(ps);
     }
-    if (tid < kC) sW[tid] = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(kC - 1 - tid)));
+    __syncthreads();  // the power tables are read by the first store_tiles below
 
-    // ---- initial state
+    // ---- initial state (update role): M = [S1; S2/2], K block = [K1; K2/2]
     const size_t so1 = static_cast<size_t>(seq) * kD * kD;
     const size_t so0 = static_cast<size_t>(seq) * kD;
-    f32x4 st[2][NB];  // feature blocks 2*wave+fi, value blocks nb
+    f32x4 st[2][NBX];  // feature blocks 2u+fi (rows 4g+r), value blocks nb (column c16)
+    if (is_u) {
 #pragma unroll
-    for (int fi = 0; fi < 2; ++fi)
+        for (int fi = 0; fi < 2; ++fi)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
+            for (int nb = 0; nb < NBX; ++nb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int f = 16 * (2 * wave + fi) + 4 * g + r;
-                const int n = n0 + 16 * nb + c16;
-                const int fr = f & (kD - 1);
-                float x = 0.f;
-                if (from_ws) x = wslot[(f < kD ? kWsS1 : kWsS2) + fr * kD + n];
-                else if (has_in) x = (f < kD ? a.s1i : a.s2i)[so1 + fr * kD + n];
-                st[fi][nb][r] = x;
+                for (int r = 0; r < 4; ++r) {
+                    const int f = 16 * (2 * u + fi) + 4 * g + r, fr = f & (kD - 1);
+                    const int n = 16 * nb + c16;
+                    float x = 0.f;
+                    if (n < kD) {
+                        if (from_ws) x = wslot[(f < kD ? kWsS1 : kWsS2) + fr * kD + n];
+                        else if (has_in) x = (f < kD ? a.s1i : a.s2i)[so1 + fr * kD + n];
+                    } else if (n == kD && !dense) {  // dense: K of the call only, incoming in sKi
+                        if (from_ws) x = wslot[(f < kD ? kWsK1 : kWsK2) + fr];
+                        else if (has_in) x = (f < kD ? a.k1i : a.k2i)[so0 + fr];
+                    }
+                    st[fi][nb][r] = f < kD ? x : 0.5f * x;
+                }
+        if (utid < kD) {
+            sS0[utid] = from_ws ? wslot[kWsS0 + utid] : (has_in ? a.s0i[so0 + utid] : 0.f);
+        } else if (utid < kD + kF) {
+            const int f = utid - kD, fr = f & (kD - 1);
+            float x = 0.f;
+            if (dense && has_in) x = (f < kD ? a.k1i : a.k2i)[so0 + fr];
+            sKi[f] = f < kD ? x : 0.5f * x;
+        } else if (utid == kD + kF) {
+            const float x = from_ws ? wslot[kWsK0] : (has_in ? a.k0i[seq] : 0.f);
+            sK0[0] = dense ? 0.f : x;
+            sK0[1] = dense ? x : 0.f;
+        }
+        // constant columns 64..79 of v (1, 0, ...) and 65..79 of w v (column 64,
+        // w, is written with every chunk's tile, racing nothing here)
+        for (int idx = utid; idx < kC * 16; idx += 256) {
+            const int row = idx >> 4, col = kD + (idx & 15);
+            for (int p = 0; p < NP; ++p) {
+                if constexpr (!STATE_ONLY) sV[p][row][col] = (col == kD && p == 0) ? 0x3F80u : 0u;
+                if (col != kD) sVw[p][row][col] = 0u;
             }
-    if (tid < kF) {
-        const int fr = tid & (kD - 1);
-        float x = 0.f;
-        if (from_ws) x = wslot[(tid < kD ? kWsK1 : kWsK2) + fr];
-        else if (has_in) x = (tid < kD ? a.k1i : a.k2i)[so0 + fr];
-        sKc[tid] = a.dense_clamp ? 0.f : x;
-        sKi[tid] = a.dense_clamp ? x : 0.f;
-    } else if (tid < kF + NV) {
-        const int n = n0 + tid - kF;
-        sS0[tid - kF] = from_ws ? wslot[kWsS0 + n] : (has_in ? a.s0i[so0 + n] : 0.f);
-    } else if (tid == kF + NV) {
-        const float x = from_ws ? wslot[kWsK0] : (has_in ? a.k0i[seq] : 0.f);
-        sK0[0] = a.dense_clamp ? 0.f : x;
-        sK0[1] = a.dense_clamp ? x : 0.f;
+        }
     }
-    // bf16 (hi[, lo]) copy of the state for the readout
+    // bf16 (hi[, lo]) copy of the state for the readout (rows 0..64)
     auto write_state_copy = [&]() {
         if constexpr (!STATE_ONLY) {
 #pragma unroll
-            for (int fi = 0; fi < 2; ++fi)
+            for (int fi = 0; fi < 2; ++fi) {
+                const int f = 16 * (2 * u + fi) + 4 * g;
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    const int f = 16 * (2 * wave + fi) + 4 * g;
+                for (int nb = 0; nb < NBX; ++nb) {
                     const int n = 16 * nb + c16;
-                    uint2 w2;
-                    w2.x = pack2(st[fi][nb][0], st[fi][nb][1]);
-                    w2.y = pack2(st[fi][nb][2], st[fi][nb][3]);
-                    *reinterpret_cast<uint2 *>(&sSt[0][n][f]) = w2;
+                    if (n > kD) continue;  // columns 65..79 of the ones block are zero
+                    const f32x4 x = st[fi][nb];
+                    const uint32_t h0 = pack2(x[0], x[1]), h1 = pack2(x[2], x[3]);
+                    *reinterpret_cast<uint2 *>(&sSt[0][n][f]) = uint2{h0, h1};
                     if constexpr (S) {
                         float lo[4];
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            lo[r] = st[fi][nb][r] - bf16_bits_to_f32(f32_to_bf16_bits(st[fi][nb][r]));
-                        w2.x = pack2(lo[0], lo[1]);
-                        w2.y = pack2(lo[2], lo[3]);
-                        *reinterpret_cast<uint2 *>(&sSt[NP - 1][n][f]) = w2;
+                        for (int r = 0; r < 4; ++r) lo[r] = x[r] - bf16_bits_to_f32(f32_to_bf16_bits(x[r]));
+                        *reinterpret_cast<uint2 *>(&sSt[NP - 1][n][f]) = uint2{pack2(lo[0], lo[1]), pack2(lo[2], lo[3])};
                     }
                 }
+            }
         }
     };
-    write_state_copy();
+    if (is_u) write_state_copy();
 
-    // ---- per-lane constants of the chunk layout (full chunks)
-    const int iw = 16 * wave + c16;  // query row of this lane in the score/readout operands
-    float mask[4][4];                // l^(i-j) [i >= j] for S^T[j = 16jb + 4g + r][i = iw]
-    float prow[4];                   // l^(i+1) for accumulator rows i = 16 wave + 4g + r
-    if constexpr (!STATE_ONLY) {
+    // ---- readout-role constants (query row of the lane: iw)
+    const int iw = 16 * wave + c16;
+    float mask[4][4];  // l^(i-j) [i >= j] for S^T[j = 16jb + 4g + r][i = iw]
+    float pin = 0.f;   // l^(iw+1)
+    if (!is_u) {
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
@@ -345,279 +467,234 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a) {
                 const int d = iw - (16 * jb + 4 * g + r);
                 mask[jb][r] = (jb <= wave && d >= 0) ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(d))) : 0.f;
             }
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            prow[r] = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(16 * wave + 4 * g + r + 1)));
+        pin = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(iw + 1)));
     }
-    const float pin = STATE_ONLY ? 0.f : static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(iw + 1)));
 
-    // ---- tile loads.  q: row = tid/8 (+32), segment = tid%8 (row-major, coalesced).
-    // k, v: token = lane and the 8-wide segments spread over the waves, so each
-    // transposed LDS write of a wave covers 64 consecutive tokens of one row.
+    // ---- tiles: readout waves load q, k; update waves load v (and k when STATE_ONLY).
     const int64_t qb = b * a.q_sb + h * a.q_sh, kb = b * a.k_sb + hk * a.k_sh, vb = b * a.v_sb + hk * a.v_sh;
-    Seg8<F32IN> Rq[2], Rk[2], Rv[NVL];
-    auto load_tiles = [&](int c) {
-        if constexpr (!STATE_ONLY) {
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                const int row = (tid >> 3) + 32 * p, sgm = tid & 7;
-                const int t = c * kC + row;
-                Rq[p] = load_seg<F32IN>(a.q, qb + t * a.q_sl + 8 * sgm, t < a.L);
-            }
-        }
-        const int t = c * kC + lane;
-        const bool ok = t < a.L;
-#pragma unroll
-        for (int p = 0; p < 2; ++p) Rk[p] = load_seg<F32IN>(a.k, kb + t * a.k_sl + 8 * (2 * wave + p), ok);
-#pragma unroll
-        for (int p = 0; p < NVL; ++p)
-            Rv[p] = load_seg<F32IN>(a.v, vb + t * a.v_sl + n0 + 8 * (NVL * wave + p), ok);
-    };
-    auto store_tiles = [&]() {
-        if constexpr (!STATE_ONLY) {
-#pragma unroll
-            for (int p = 0; p < 2; ++p) {
-                const int row = (tid >> 3) + 32 * p, sgm = tid & 7;
-                store_row(&sQ[row][8 * sgm], Rq[p]);
-            }
-        }
-#pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const int sgm = 2 * wave + p;
-            if constexpr (!STATE_ONLY) store_row(&sK[lane][8 * sgm], Rk[p]);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sKt[8 * sgm + e][lane] = seg_elem(Rk[p], e);
-        }
-#pragma unroll
-        for (int p = 0; p < NVL; ++p) {
-            const int sgm = NVL * wave + p;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sVt[8 * sgm + e][lane] = seg_elem(Rv[p], e);
-        }
-    };
+    const int rt = tid & 255;  // thread index within the role
+    TileRegs<F32IN> R;
+#define PRIME_LOAD_TILES(c) load_tiles_fn<F32IN, STATE_ONLY>(a, R, (c), rt, is_u, qb, kb, vb)
+#define PRIME_STORE_TILES(c)                                                                                       \
+    store_tiles_fn<F32IN, STATE_ONLY>(R, rt, is_u, sPw, min(kC, a.L - (c) * kC), &sQf[0][0][0], plQ, &sKf[0][0][0], \
+                                      plK, kPK, &sV[0][0][0], plV, &sVw[0][0][0], plVw, kPV)
 
-    load_tiles(c_begin);
+    PRIME_LOAD_TILES(c_begin);
+    PRIME_STORE_TILES(c_begin);
+    __syncthreads();
 
     for (int c = c_begin; c < c_end; ++c) {
         const int nvalid = min(kC, a.L - c * kC);
-        store_tiles();
-        if (nvalid < kC && tid < kC) sW[tid] = tid < nvalid ? sPw[nvalid - 1 - tid] : 0.f;
-        __syncthreads();  // A: tiles of chunk c and state^(c) visible
-        if (c + 1 < c_end) load_tiles(c + 1);
+        if (c + 1 < c_end) PRIME_LOAD_TILES(c + 1);
 
-        if constexpr (!STATE_ONLY) {
-            // ---- query features of row iw: B operand of the score block and A
-            // operand of the readout (k index f = 32 ks + 8g + t in both)
-            Opnd<S> fq[4];
+        float ds0 = 0.f;  // update role: sum_j w_j v[j][16u + c16] over this lane's tokens
+        if (!is_u) {
+            if constexpr (!STATE_ONLY) {
+                // ---- query features of row iw (B operand of S^T and of the readout)
+                Opnd<S> fq[4];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const T *qr = &sQ[iw][(ks & 1) * 32 + 8 * g];
-                fq[ks] = ks >= 2 ? xform_op<S>(qr, true, 0.5f) : raw_op<S>(qr);
-            }
-            // ---- transposed score block S^T[j][i] for j-blocks jb <= wave
-            f32x4 sT[4];
+                for (int ks = 0; ks < 4; ++ks) fq[ks] = row_op<S>(&sQf[0][iw][32 * ks + 8 * g], plQ);
+                // ---- transposed score block S^T[j][i] for j-blocks jb <= wave
+                f32x4 sT[4];
 #pragma unroll
-            for (int jb = 0; jb < 4; ++jb) sT[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int jb = 0; jb < 4; ++jb) {
+                    sT[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if (jb > wave) continue;
+                    Opnd<S> ak[4];
 #pragma unroll
-            for (int jb = 0; jb < 4; ++jb) {
-                if (jb > wave) continue;
+                    for (int ks = 0; ks < 4; ++ks) ak[ks] = row_op<S>(&sKf[0][16 * jb + c16][32 * ks + 8 * g], plK);
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const T *kr = &sK[16 * jb + c16][(ks & 1) * 32 + 8 * g];
-                    const Opnd<S> ak = ks >= 2 ? xform_op<S>(kr, true, 1.0f) : raw_op<S>(kr);
-                    sT[jb] = mma<S>(ak, fq[ks], sT[jb]);
+                    for (int ks = 0; ks < 4; ++ks) sT[jb] = mma<S>(ak[ks], fq[ks], sT[jb]);
                 }
-            }
-            // ---- decay mask -> A and the intra denominator (lane: S^T[16jb+4g+r][iw])
-            uint32_t Ah[4][2], Al[4][2];
-            float denp = 0.f;
+                // ---- A = decay mask * (1 + S) as packed bf16 (hi[, lo])
+                uint32_t Ah[4][2], Al[4][2];
 #pragma unroll
-            for (int jb = 0; jb < 4; ++jb) {
-                float av[4], lo[4];
+                for (int jb = 0; jb < 4; ++jb) {
+                    float x[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float x = mask[jb][r] * (1.0f + sT[jb][r]);
-                    const float xh = bf16_bits_to_f32(f32_to_bf16_bits(x));
-                    av[r] = xh;
-                    lo[r] = S ? x - xh : 0.f;
-                    denp += S ? x : xh;  // unsplit: numerator and denominator use the same weight
-                }
-                Ah[jb][0] = pack2(av[0], av[1]);
-                Ah[jb][1] = pack2(av[2], av[3]);
-                Al[jb][0] = pack2(lo[0], lo[1]);
-                Al[jb][1] = pack2(lo[2], lo[3]);
-            }
-            // ---- acc_av = A.V (register t <-> j = 32kk + 16(t/4) + 4g + t%4)
-            f32x4 acc_av[NB], acc_ro[NB];
+                    for (int r = 0; r < 4; ++r) x[r] = mask[jb][r] * (1.0f + sT[jb][r]);
+                    Ah[jb][0] = pack2(x[0], x[1]);
+                    Ah[jb][1] = pack2(x[2], x[3]);
+                    if constexpr (S) {
+                        float lo[4];
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                acc_av[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-                acc_ro[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                if (2 * kk > wave) continue;
-                Opnd<S> aop;
-                aop.h = as_bf16x8(u32x4{Ah[2 * kk][0], Ah[2 * kk][1], Ah[2 * kk + 1][0], Ah[2 * kk + 1][1]});
-                if constexpr (S) aop.l = as_bf16x8(u32x4{Al[2 * kk][0], Al[2 * kk][1], Al[2 * kk + 1][0], Al[2 * kk + 1][1]});
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    const T *vr = &sVt[16 * nb + c16][32 * kk + 4 * g];
-                    Opnd<S> bop;
-                    if constexpr (!S) {
-                        const uint2 lo = *reinterpret_cast<const uint2 *>(vr);
-                        const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16);
-                        bop.h = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
-                    } else {
-                        const f32x4 lo = *reinterpret_cast<const f32x4 *>(vr);
-                        const f32x4 hi = *reinterpret_cast<const f32x4 *>(vr + 16);
-                        const float f[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                        bop = split8<S>(f);
+                        for (int r = 0; r < 4; ++r) lo[r] = x[r] - bf16_bits_to_f32(f32_to_bf16_bits(x[r]));
+                        Al[jb][0] = pack2(lo[0], lo[1]);
+                        Al[jb][1] = pack2(lo[2], lo[3]);
                     }
-                    acc_av[nb] = mma<S>(aop, bop, acc_av[nb]);
                 }
-            }
-            // ---- acc_ro = Fq . Sst  (readout of the state entering the chunk)
+                // ---- y^T = V^T A^T: accumulator row = value column 16nb + 4g + r,
+                // column = query row iw; register t of A^T <-> token 32kk + 16(t/4) + 4g + t%4
+                f32x4 acc_av[NBX], acc_ro[NBX];
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
+                for (int nb = 0; nb < NBX; ++nb) {
+                    acc_av[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    acc_ro[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    Opnd<S> sop;
-                    sop.h = as_bf16x8(*reinterpret_cast<const u32x4 *>(&sSt[0][16 * nb + c16][32 * ks + 8 * g]));
+                for (int kk = 0; kk < 2; ++kk) {
+                    if (2 * kk > wave) continue;
+                    const bool second = 2 * kk + 1 <= wave;  // second j-block unmasked
+                    Opnd<S> aop;
+                    aop.h = as_bf16x8(u32x4{Ah[2 * kk][0], Ah[2 * kk][1], second ? Ah[2 * kk + 1][0] : 0u,
+                                            second ? Ah[2 * kk + 1][1] : 0u});
                     if constexpr (S)
-                        sop.l = as_bf16x8(*reinterpret_cast<const u32x4 *>(&sSt[NP - 1][16 * nb + c16][32 * ks + 8 * g]));
-                    acc_ro[nb] = mma<S>(fq[ks], sop, acc_ro[nb]);
+                        aop.l = as_bf16x8(u32x4{Al[2 * kk][0], Al[2 * kk][1], second ? Al[2 * kk + 1][0] : 0u,
+                                                second ? Al[2 * kk + 1][1] : 0u});
+                    Opnd<S> vop[NBX];
+#pragma unroll
+                    for (int nb = 0; nb < NBX; ++nb) {
+                        const uint16_t *p0 = &sV[0][32 * kk + 4 * g + tr_r][16 * nb + tr_c];
+                        vop[nb] = tr_op<S>(p0, p0 + 16 * kPV, plV);
+                    }
+#pragma unroll
+                    for (int nb = 0; nb < NBX; ++nb) acc_av[nb] = mma<S>(vop[nb], aop, acc_av[nb]);
                 }
-            // ---- denominator of row iw: intra + l^(i+1) (K0 + Fq . Kst), call and init parts
-            float kc = 0.f, ki = 0.f;
+                // ---- y^T += [S1; S2/2 | K]^T Fq^T  (the state entering the chunk)
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const int f = 32 * ks + 8 * g;
-                float qf[8];
-                unpack8(__builtin_bit_cast(u32x4, fq[ks].h), qf);
-                if constexpr (S) {
-                    float ql[8];
-                    unpack8(__builtin_bit_cast(u32x4, fq[ks].l), ql);
+                for (int kh = 0; kh < 2; ++kh) {
+                    Opnd<S> sop[2][NBX];
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) qf[t] += ql[t];
+                    for (int kq = 0; kq < 2; ++kq)
+#pragma unroll
+                        for (int nb = 0; nb < NBX; ++nb) {
+                            const int n = nb == NB ? kD : 16 * nb + c16;  // ones block: only row 64 (K)
+                            sop[kq][nb] = row_op<S>(&sSt[0][n][32 * (2 * kh + kq) + 8 * g], plS);
+                            if (nb == NB && c16 != 0) {
+                                sop[kq][nb].h = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
+                                if constexpr (S) sop[kq][nb].l = sop[kq][nb].h;
+                            }
+                        }
+#pragma unroll
+                    for (int kq = 0; kq < 2; ++kq)
+#pragma unroll
+                        for (int nb = 0; nb < NBX; ++nb) acc_ro[nb] = mma<S>(sop[kq][nb], fq[2 * kh + kq], acc_ro[nb]);
                 }
-                const f32x4 c0 = *reinterpret_cast<const f32x4 *>(&sKc[f]);
-                const f32x4 c1 = *reinterpret_cast<const f32x4 *>(&sKc[f + 4]);
-                const f32x4 i0 = *reinterpret_cast<const f32x4 *>(&sKi[f]);
-                const f32x4 i1 = *reinterpret_cast<const f32x4 *>(&sKi[f + 4]);
+                // ---- denominator of row iw: column 64 of both products (lane g = 0, r = 0)
+                float den_call = acc_av[NB][0] + pin * (sK0[0] + acc_ro[NB][0]);
+                den_call = __shfl(den_call, c16, kWave);
+                float den;
+                if (dense) {
+                    // incoming K state, decayed to this chunk, read out on the VALU
+                    float ki = 0.f;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    kc += qf[t] * c0[t] + qf[4 + t] * c1[t];
-                    ki += qf[t] * i0[t] + qf[4 + t] * i1[t];
+                    for (int ks = 0; ks < 4; ++ks) {
+                        float qf[8];
+                        unpack8(__builtin_bit_cast(u32x4, fq[ks].h), qf);
+                        if constexpr (S) {
+                            float ql[8];
+                            unpack8(__builtin_bit_cast(u32x4, fq[ks].l), ql);
+#pragma unroll
+                            for (int t = 0; t < 8; ++t) qf[t] += ql[t];
+                        }
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) ki += qf[t] * sKi[32 * ks + 8 * g + t];
+                    }
+                    ki += __shfl_xor(ki, 16, kWave);
+                    ki += __shfl_xor(ki, 32, kWave);
+                    const float den_init = pin * (sK0[1] + ki * static_cast<float>(pow(static_cast<double>(lam), 64.0 * c)));
+                    den = fmaxf(fmaxf(den_call, a.eps) + den_init, a.eps);
+                } else {
+                    den = fmaxf(den_call, a.eps);
                 }
-            }
-            denp += __shfl_xor(denp, 16, kWave);
-            denp += __shfl_xor(denp, 32, kWave);
-            kc += __shfl_xor(kc, 16, kWave);
-            kc += __shfl_xor(kc, 32, kWave);
-            ki += __shfl_xor(ki, 16, kWave);
-            ki += __shfl_xor(ki, 32, kWave);
-            const float den_call = denp + pin * (sK0[0] + kc);
-            const float den_init = pin * (sK0[1] + ki);
-            const float den = a.dense_clamp ? fmaxf(fmaxf(den_call, a.eps) + den_init, a.eps)
-                                            : fmaxf(den_call + den_init, a.eps);
-            // ---- y rows 16w + 4g + r straight from the accumulators
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 16 * wave + 4 * g + r;
-                const float inv = 1.0f / __shfl(den, 4 * g + r, kWave);
-                const int t = c * kC + row;
+                const float inv = 1.0f / den;
+                // ---- y[iw][16nb + 4g .. +4] straight from the accumulators
+                const int t = c * kC + iw;
                 if (t < a.L) {
-                    const int64_t yo = b * a.y_sb + h * a.y_sh + t * a.y_sl + n0 + c16;
+                    const int64_t yo = b * a.y_sb + h * a.y_sh + t * a.y_sl + 4 * g;
 #pragma unroll
                     for (int nb = 0; nb < NB; ++nb) {
-                        const float yv = (acc_av[nb][r] + prow[r] * (sS0[16 * nb + c16] + acc_ro[nb][r])) * inv;
-                        store_elem(a.y, yo + 16 * nb, a.dt_y, yv);
+                        const f32x4 s0 = *reinterpret_cast<const f32x4 *>(&sS0[16 * nb + 4 * g]);
+                        f32x4 yv;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) yv[r] = (acc_av[nb][r] + pin * (s0[r] + acc_ro[nb][r])) * inv;
+                        const int64_t o = yo + 16 * nb;
+                        if (a.dt_y == PRIME_BF16) {
+                            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + o) =
+                                uint2{pack2(yv[0], yv[1]), pack2(yv[2], yv[3])};
+                        } else if (a.dt_y == PRIME_F32) {
+                            *reinterpret_cast<f32x4 *>(static_cast<float *>(a.y) + o) = yv;
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) store_elem(a.y, o + r, a.dt_y, yv[r]);
+                        }
                     }
                 }
             }
-            __syncthreads();  // B: readout of state^(c) finished everywhere
+        } else {
+            // ---- state update: st = l^n st + [k; k*k/2]^T [w v | w]
+            const float ln = sPw[nvalid];
+#pragma unroll
+            for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+                for (int nb = 0; nb < NBX; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) st[fi][nb][r] *= ln;
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                // register t of both operands <-> token 32ks + 16(t/4) + 4g + t%4, so
+                // the lane groups of one transposed read cover consecutive rows
+                const int j0 = 32 * ks + 4 * g + tr_r;
+                Opnd<S> ak[2], vop[NBX];
+#pragma unroll
+                for (int fi = 0; fi < 2; ++fi) {
+                    const uint16_t *p0 = &sKf[0][j0][16 * (2 * u + fi) + tr_c];
+                    ak[fi] = tr_op<S>(p0, p0 + 16 * kPK, plK);
+                }
+#pragma unroll
+                for (int nb = 0; nb < NBX; ++nb) {
+                    const uint16_t *p0 = &sVw[0][j0][16 * nb + tr_c];
+                    vop[nb] = tr_op<S>(p0, p0 + 16 * kPV, plVw);
+                }
+                {  // S0 contribution of value block u: the w v operand summed over its
+                   // tokens (selected with compile-time indices: a runtime index into
+                   // a register array would send it to scratch memory)
+                    u32x4 sh = __builtin_bit_cast(u32x4, vop[0].h), sl = {0u, 0u, 0u, 0u};
+                    if constexpr (S) sl = __builtin_bit_cast(u32x4, vop[0].l);
+#pragma unroll
+                    for (int nb = 1; nb < NB; ++nb)
+                        if (u == nb) {
+                            sh = __builtin_bit_cast(u32x4, vop[nb].h);
+                            if constexpr (S) sl = __builtin_bit_cast(u32x4, vop[nb].l);
+                        }
+                    float vf[8];
+                    unpack8(sh, vf);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ds0 += vf[e];
+                    if constexpr (S) {
+                        unpack8(sl, vf);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) ds0 += vf[e];
+                    }
+                }
+#pragma unroll
+                for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+                    for (int nb = 0; nb < NBX; ++nb) st[fi][nb] = mma<S>(ak[fi], vop[nb], st[fi][nb]);
+            }
+            ds0 += __shfl_xor(ds0, 16, kWave);
+            ds0 += __shfl_xor(ds0, 32, kWave);
         }
+        __syncthreads();  // B: every read of chunk c's tiles, the state copy and S0/K0 done
 
-        // ---- state update with this chunk (exact for a partial last chunk)
-        const float ln = sPw[nvalid];
-#pragma unroll
-        for (int fi = 0; fi < 2; ++fi)
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) st[fi][nb][r] *= ln;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int j0 = 32 * ks + 8 * g;
-            const f32x4 w0 = *reinterpret_cast<const f32x4 *>(&sW[j0]);
-            const f32x4 w1 = *reinterpret_cast<const f32x4 *>(&sW[j0 + 4]);
-            Opnd<S> vop[NB];
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) vop[nb] = raw_op<S>(&sVt[16 * nb + c16][j0]);
-#pragma unroll
-            for (int fi = 0; fi < 2; ++fi) {
-                const int f = 16 * (2 * wave + fi) + c16;  // A-operand row (feature)
-                const bool sq = f >= kD;
-                float kf[8];
-                lds8(&sKt[f & (kD - 1)][j0], kf);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const float w = t < 4 ? w0[t] : w1[t - 4];
-                    kf[t] = sq ? w * kf[t] * kf[t] : w * kf[t];
-                }
-                const Opnd<S> ak = split8<S>(kf);
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) st[fi][nb] = mma<S>(ak, vop[nb], st[fi][nb]);
-            }
-        }
-        write_state_copy();
-        // ---- small moments (fp32 VALU): lanes split the token range, butterflies combine
-        {
-            const int f = 32 * wave + (lane & 31), fr = f & (kD - 1);
-            const int jh = 32 * (lane >> 5);
-            float s = 0.f;
-#pragma unroll
-            for (int jj = 0; jj < 32; jj += 8) {
-                float kf[8];
-                lds8(&sKt[fr][jh + jj], kf);
-                const f32x4 w0 = *reinterpret_cast<const f32x4 *>(&sW[jh + jj]);
-                const f32x4 w1 = *reinterpret_cast<const f32x4 *>(&sW[jh + jj + 4]);
-#pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    const float w = t < 4 ? w0[t] : w1[t - 4];
-                    s += w * (f < kD ? kf[t] : kf[t] * kf[t]);
-                }
-            }
-            s += __shfl_xor(s, 32, kWave);
-            constexpr int NPW = NV / 4, NPART = 64 / NPW, JL = kC / NPART;
-            const int n = NPW * wave + lane % NPW, jp = (lane / NPW) * JL;
-            float s0 = 0.f;
-#pragma unroll
-            for (int jj = 0; jj < JL; jj += 8) {
-                float vf[8];
-                lds8(&sVt[n][jp + jj], vf);
-                const f32x4 w0 = *reinterpret_cast<const f32x4 *>(&sW[jp + jj]);
-                const f32x4 w1 = *reinterpret_cast<const f32x4 *>(&sW[jp + jj + 4]);
-#pragma unroll
-                for (int t = 0; t < 4; ++t) s0 += w0[t] * vf[t] + w1[t] * vf[4 + t];
-            }
-#pragma unroll
-            for (int o = NPW; o < kWave; o <<= 1) s0 += __shfl_xor(s0, o, kWave);
-            if (lane < 32) {
-                sKc[f] = ln * sKc[f] + s;
-                sKi[f] = ln * sKi[f];
-            }
-            if (lane < NPW) sS0[n] = ln * sS0[n] + s0;
-            if (tid == 0) {
+        if (is_u) {
+            const float ln = sPw[nvalid];
+            write_state_copy();
+            if (g == 0) sS0[16 * u + c16] = ln * sS0[16 * u + c16] + ds0;
+            if (utid == 0) {
                 sK0[0] = ln * sK0[0] + sPs[nvalid];
                 sK0[1] = ln * sK0[1];
             }
         }
-        __syncthreads();  // C: tiles free for the next chunk, small state visible
+        if (c + 1 < c_end) PRIME_STORE_TILES(c + 1);
+        __syncthreads();  // A: chunk c+1 tiles, state copy and S0/K0 visible
     }
 
+#undef PRIME_LOAD_TILES
+#undef PRIME_STORE_TILES
+
     // ---- segment / final state (decays used the valid counts: no pad correction)
+    if (!is_u) return;
     float *o_s1, *o_s2, *o_s0, *o_k1, *o_k2, *o_k0;
     size_t off1, off0, offk0;
     if (STATE_ONLY) {
@@ -625,25 +702,30 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(const PrefillArgs a) {
         o_k1 = wslot + kWsK1; o_k2 = wslot + kWsK2; o_k0 = wslot + kWsK0;
         off1 = 0; off0 = 0; offk0 = 0;
     } else {
-        if (!last_seg || a.s1o == nullptr) return;
+        if (seg != a.G - 1 || a.s1o == nullptr) return;
         o_s1 = a.s1o; o_s2 = a.s2o; o_s0 = a.s0o; o_k1 = a.k1o; o_k2 = a.k2o; o_k0 = a.k0o;
         off1 = so1; off0 = so0; offk0 = seq;
     }
+    // dense clamp: the incoming K state decays separately (l^L over the call)
+    const float linit = dense ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(a.L))) : 0.f;
 #pragma unroll
     for (int fi = 0; fi < 2; ++fi)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
+        for (int r = 0; r < 4; ++r) {
+            const int f = 16 * (2 * u + fi) + 4 * g + r;
+            const int fr = f & (kD - 1);
+            const float sc = f < kD ? 1.0f : 2.0f;  // rows 64.. hold S2/2 and K2/2
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int f = 16 * (2 * wave + fi) + 4 * g + r;
-                const int n = n0 + 16 * nb + c16;
-                (f < kD ? o_s1 : o_s2)[off1 + (f & (kD - 1)) * kD + n] = st[fi][nb][r];
+            for (int nb = 0; nb < NB; ++nb)
+                (f < kD ? o_s1 : o_s2)[off1 + fr * kD + 16 * nb + c16] = sc * st[fi][nb][r];
+            if (c16 == 0) {
+                float kv = st[fi][NB][r];
+                if (dense) kv += linit * sKi[f];
+                (f < kD ? o_k1 : o_k2)[off0 + fr] = sc * kv;
             }
-    if (tid < NV) o_s0[off0 + n0 + tid] = sS0[tid];
-    if (split == 0) {
-        if (tid < kF) (tid < kD ? o_k1 : o_k2)[off0 + (tid & (kD - 1))] = sKc[tid] + sKi[tid];
-        if (tid == kF) o_k0[offk0] = sK0[0] + sK0[1];
-    }
+        }
+    if (utid < kD) o_s0[off0 + utid] = sS0[utid];
+    if (utid == kD) o_k0[offk0] = sK0[0] + sK0[1];
 }
 
 // Scan over segments, elementwise: slot s <- state entering segment s.
@@ -680,21 +762,14 @@ static void launch_variant(PrefillArgs a, hipStream_t stream) {
     const int Sq = a.B * a.H;
     if (a.G > 1) {
         // A: state contribution of every segment but the last, from zero
-        a.nsplit = 1;
         a.nseg_launch = a.G - 1;
-        hipLaunchKernelGGL((prefill_kernel<64, F32IN, true>), dim3(Sq * (a.G - 1)), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((prefill_kernel<F32IN, true>), dim3(Sq * (a.G - 1)), dim3(256), 0, stream, a);
         // B: exclusive scan over segments (incoming state first)
         const int64_t n = static_cast<int64_t>(Sq) * kWsElems;
         hipLaunchKernelGGL(segment_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, a);
     }
     a.nseg_launch = a.G;
-    if (a.nsplit == 2) {
-        const int U8 = (Sq * a.G + 7) / 8 * 8;
-        hipLaunchKernelGGL((prefill_kernel<32, F32IN, false>), dim3(U8 * 2), dim3(256), 0, stream, a);
-    } else {
-        a.nsplit = 1;
-        hipLaunchKernelGGL((prefill_kernel<64, F32IN, false>), dim3(Sq * a.G), dim3(256), 0, stream, a);
-    }
+    hipLaunchKernelGGL((prefill_kernel<F32IN, false>), dim3(Sq * a.G), dim3(512), 0, stream, a);
 }
 
 hipError_t launch_prefill(PrefillArgs a, hipStream_t stream) {

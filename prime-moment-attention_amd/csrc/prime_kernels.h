@@ -32,7 +32,6 @@ struct PrefillArgs {
     void *y;
     int dt_y;
     int64_t y_sb, y_sh, y_sl;
-    int nsplit;  // value-column slices per sequence (64 / NV)
     // segment-parallel scan (G > 1): each sequence is cut into G segments of
     // `cps` chunks; ws holds one packed fp32 state slot per (sequence, segment)
     int G, cps;
