@@ -1,0 +1,389 @@
+#!/usr/bin/env python3
+"""Benchmark of the PRIME moment-attention hot paths on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps K2] [--no-cpu]
+
+One "step" is one chunked prefill (prime_chunked_prefill) of the chunked-prefill
+workload: B=8 sequences x H=12 heads x L=8192 tokens, D=64, chunk 64, bf16
+q/k/v (N(0,1), L2-normalised per head, q scaled by 1/8), per-head lambda
+~ U[0.99, 0.9999], zero initial state, bf16 y and fp32 final state.
+`value` = prefill tokens/s = B*L / (seconds per step), inputs resident in HBM.
+
+The same JSON line carries
+  roofline      the dominant kernel of the step (the fused chunk loop), its
+                average launch duration from HIP events recorded by the library
+                around each launch inside the timed region, against HBM peak;
+  decode        the fused decode step at B=512 sequences x 12 layers x 12 heads
+                (one launch per layer, states pre-filled by 1024 tokens) and at
+                B=256, tok/s and its own roofline;
+  cpu_baseline  the reference's C99 engine (built from its sources into
+                oracle/_ref by oracle/Makefile) timed single-threaded on a
+                bounded sample of the same workload, plus the PyTorch-CPU and
+                C/OpenMP restatements under cpu_baselines.
+The CPU legs are the only use of oracle/ here, and only as timing baselines.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "prime-moment-attention_amd")]
+
+PEAK_HBM = 8.0e12          # bytes/s, MI355X HBM3E
+PEAK_BF16 = 2.5e15         # flop/s, dense bf16 MFMA
+D = 64
+STATE_BYTES = (2 * D * D + 3 * D + 1) * 4          # 33,540 B per (sequence, head)
+PREFILL_BYTES_PER_TOKEN_HEAD = 3 * 2 * D + 2 * D   # bf16 q, k, v in + bf16 y out
+PREFILL_FLOP_PER_TOKEN_HEAD = 6 * 64 * D + 8 * D * D  # intra 6CD + dS 4D^2 + carry readout 4D^2
+DECODE_BYTES_PER_TILE = 2 * STATE_BYTES + 3 * 2 * D + 2 * D  # state r+w, bf16 q,k,v, bf16 y
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100, help="timed prefill steps")
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--decode-steps", type=int, default=1000, help="timed decode steps (12 layers each)")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode legs")
+    ap.add_argument("--cpu-budget", type=float, default=8.0, help="seconds per CPU leg (approximate)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 1 GiB device copy 3 times (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
+    return ap.parse_args()
+
+
+# ----------------------------------------------------------------- inputs
+def qkv(shape, gen, device, dtype):
+    """q, k, v ~ N(0,1); q and k L2-normalised over D, rounded to dtype, q / 8."""
+    import torch
+    out = []
+    for i in range(3):
+        x = torch.randn(*shape, generator=gen, device=device, dtype=torch.float32)
+        if i < 2:
+            x = x / x.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+        x = x.to(dtype)
+        if i == 0:
+            x = x / 8
+        out.append(x)
+    return out
+
+
+def timed(fn, steps, warmup):
+    """W untimed calls, then K calls bracketed by synchronisation; ms per call
+    from events on the current stream (the stream the library launches on)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps
+
+
+def kernel_ms(lib, kid):
+    ms, n = lib.timer_read(kid)
+    return (ms / n if n else None), n
+
+
+def load_traffic():
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by the same counter's reading for a
+    copy kernel of known size); None if that summary is absent."""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return {}
+
+
+# ----------------------------------------------------------------- prefill
+def bench_prefill(args, lib, torch, dev):
+    B, H, L, C = 8, 12, 8192, 64
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    q, k, v = qkv((B, H, L, D), gen, dev, torch.bfloat16)
+    lam = torch.empty(H, device=dev).uniform_(0.99, 0.9999, generator=gen)
+    y = torch.empty(B, H, L, D, device=dev, dtype=torch.bfloat16)
+    st = lib.new_state(B, H, D, dev)
+    step = lib.bind_chunked_prefill(q, k, v, lam, 1.0, C, None, y, st)
+    ws = step.buffers[7]
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    # timed region: only the dominant kernel is bracketed by events
+    lib.timer_reset()
+    lib.timer_enable(lib.KERNEL_PREFILL_CHUNKS)
+    ms = timed(step, args.steps, 0)
+    lib.timer_enable()
+    main_ms, main_n = kernel_ms(lib, lib.KERNEL_PREFILL_CHUNKS)
+    # breakdown pass (not the timed region): every kernel of the call bracketed
+    ids = (lib.KERNEL_PREFILL_CHUNKS, lib.KERNEL_PREFILL_SEGMENTS, lib.KERNEL_SEGMENT_SCAN)
+    lib.timer_reset()
+    lib.timer_enable(*ids)
+    ms_all = timed(step, args.steps, 0)
+    lib.timer_enable()
+    kern = {lib.KERNEL_NAMES[kid]: kernel_ms(lib, kid) for kid in ids}
+    lib.timer_reset()
+    ok = bool(torch.isfinite(y).all().item())
+    tokens = B * L
+    algo_bytes = B * H * L * PREFILL_BYTES_PER_TOKEN_HEAD + B * H * STATE_BYTES
+    flops = B * H * L * PREFILL_FLOP_PER_TOKEN_HEAD
+    return dict(B=B, H=H, L=L, C=C, ms=ms, tokens=tokens, bytes=algo_bytes, flops=flops, finite=ok,
+                kernels={n: {"avg_us": None if t is None else t * 1e3, "launches": c} for n, (t, c) in kern.items()},
+                ms_all_bracketed=ms_all, main_ms=main_ms, main_n=main_n, ws_bytes=0 if ws is None else ws.numel())
+
+
+# ----------------------------------------------------------------- decode
+def bench_decode(args, lib, torch, dev, B, layers=12, H=12, pool=16, prefill_tokens=1024):
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 1000 + B)
+    lams = [torch.empty(H, device=dev).uniform_(0.99, 0.9999, generator=gen) for _ in range(layers)]
+    states = [lib.new_state(B, H, D, dev) for _ in range(layers)]
+    # states pre-filled by the library's own prefill of 1024 random tokens
+    chunkB = max(1, min(B, 128))
+    for l in range(layers):
+        for b0 in range(0, B, chunkB):
+            nb = min(chunkB, B - b0)
+            q, k, v = qkv((nb, H, prefill_tokens, D), gen, dev, torch.bfloat16)
+            yp = torch.empty_like(q)
+            part = tuple(t[b0:b0 + nb] for t in states[l])
+            lib.chunked_prefill(q, k, v, lams[l], 1.0, 64, None, yp, part)
+        del q, k, v, yp
+    torch.cuda.synchronize()
+    toks = [[qkv((B, H, D), gen, dev, torch.bfloat16) for _ in range(pool)] for _ in range(layers)]
+    ys = [torch.empty(B, H, D, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    calls = [[lib.bind_decode_step(*toks[l][p], lams[l], 1.0, states[l], states[l], ys[l])
+              for l in range(layers)] for p in range(pool)]
+    it = [0]
+
+    def step():
+        for c in calls[it[0] % pool]:
+            c()
+        it[0] += 1
+    steps = args.decode_steps
+    # a step is `layers` back-to-back launches of the decode kernel and nothing
+    # else, so the events around the timed region give the launch duration
+    # (ms per step / layers, gaps between launches included) without events
+    # between the launches
+    ms = timed(step, steps, args.warmup)
+    kms, n = ms / layers, steps * layers
+    ok = all(bool(torch.isfinite(y).all().item()) for y in ys)
+    per_launch = B * H * DECODE_BYTES_PER_TILE
+    achieved = per_launch / (kms * 1e-3)
+    return {
+        "workload": f"decode step B={B} x {layers} layers x {H} heads, D=64, bf16 q/k/v, fp32 state in place, "
+                    f"bf16 y; states pre-filled by {prefill_tokens} tokens; one launch per layer",
+        "tok_s": B / (ms * 1e-3), "ms_per_step": ms, "steps": steps, "finite": ok,
+        "state_bytes": layers * B * H * STATE_BYTES,
+        "roofline": {"kernel": "decode_step_kernel", "bound": "hbm", "achieved": achieved / 1e9,
+                     "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": achieved / PEAK_HBM,
+                     "bytes_per_launch": per_launch, "avg_launch_us": kms * 1e3, "launches": n,
+                     "traffic": None},
+    }
+
+
+# ----------------------------------------------------------------- CPU legs
+def cpu_cores():
+    n = len(os.sched_getaffinity(0))
+    try:
+        n = min(n, int(os.environ.get("OMP_NUM_THREADS", n)))
+    except ValueError:
+        pass
+    return max(1, n)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_inputs(nseq, H, L, seed):
+    import numpy as np
+    from oracle import oracle as O
+    q, k, v = O.make_inputs((nseq, H, L, D), seed=seed, bf16=True)
+    return q, k, v, np.random.default_rng(seed).uniform(0.99, 0.9999, H).astype(np.float32)
+
+
+def cpu_prefill_legs(args):
+    """Timed CPU baselines on bounded samples of the prefill workload; each
+    leg grows its sample (whole sequences of L=8192 tokens x 12 heads) until
+    about --cpu-budget seconds, capped at the workload's 8 sequences."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    from oracle import torch_cpu as T
+    H, L, maxseq = 12, 8192, 8
+    n = cpu_cores()
+    q, k, v, lam = cpu_inputs(maxseq, H, L, args.seed)
+    legs = []
+
+    def grow(run_one, kind, cores, label):
+        t0 = time.perf_counter()
+        run_one(0)
+        t1 = time.perf_counter() - t0
+        done, total = 1, t1
+        while done < maxseq and total + t1 < args.cpu_budget:
+            t0 = time.perf_counter()
+            run_one(done)
+            total += time.perf_counter() - t0
+            done += 1
+        legs.append({"value": done * L / total, "unit": "tok/s", "cores": cores, "kind": kind,
+                     "sample": f"{done} of 8 sequences x 12 heads x L=8192 of the prefill workload "
+                               f"({done * L} tokens, {total:.2f} s)", "impl": label})
+
+    if O.ref_available():
+        def ref_one(i):
+            e = O.RefEngine(H, D, 0.9995, 1.0)
+            # the engine scales q by 1/sqrt(D) itself and walks tokens [L, H, D]
+            e.prefill(np.ascontiguousarray((q[i] * 8).transpose(1, 0, 2)),
+                      np.ascontiguousarray(k[i].transpose(1, 0, 2)),
+                      np.ascontiguousarray(v[i].transpose(1, 0, 2)))
+        grow(ref_one, "reference", 1, "reference C99 engine (c/prime_moment.c, additive mode, single "
+             "decay 0.9995), built from the reference sources, 1 thread")
+
+    def port_one(i):
+        st = tuple(np.zeros(s, np.float32) for s in ((H, D), (H, D, D), (H, D, D), (H,), (H, D), (H, D)))
+        y = np.empty((H, L, D), np.float32)
+        O.baseline_prefill(np.ascontiguousarray(q[i]), np.ascontiguousarray(k[i]), np.ascontiguousarray(v[i]),
+                           lam, 1.0, st, y, H, n)
+    grow(port_one, "port", n, f"C restatement of c/prime_moment.c:276-312 with PyTorch semantics, "
+         f"OpenMP over (sequence, head), {n} threads")
+
+    torch.set_num_threads(n)
+
+    def torch_one(i):
+        t = lambda x: torch.from_numpy(np.ascontiguousarray(x[i:i + 1]))
+        T.chunked_core(t(q), t(k), t(v), torch.from_numpy(lam), chunk=64, carry="dense")
+    grow(torch_one, "port", n, f"PyTorch-CPU fp32 restatement of chunked_ssd.py:48-184 with the "
+         f"reference's O(Nc^2) carry, torch threads {n}")
+    return legs
+
+
+def cpu_decode_leg(args):
+    """Reference C99 engine, one decode step per (sequence, layer) of the B=512
+    x 12-layer x 12-head workload, 1 thread, on a bounded number of sequences."""
+    import numpy as np
+    from oracle import oracle as O
+    if not O.ref_available():
+        return None
+    H, layers = 12, 12
+    engines = [O.RefEngine(H, D, 0.9995, 1.0) for _ in range(layers)]
+    rng = np.random.default_rng(args.seed)
+    toks = rng.standard_normal((64, 3, H, D)).astype(np.float32)
+    seqs, t_total, steps = 0, 0.0, 0
+    t0 = time.perf_counter()
+    while t_total < min(args.cpu_budget, 4.0):
+        for e in engines:
+            x = toks[steps % 64]
+            e.step(x[0], x[1], x[2])
+        steps += 1
+        t_total = time.perf_counter() - t0
+    # every (sequence, layer) pair costs the same: tokens/s over 512 sequences
+    per_seq_step = t_total / steps
+    return {"value": 1.0 / per_seq_step, "unit": "tok/s", "cores": 1, "kind": "reference",
+            "sample": f"{steps} decode steps of one sequence through 12 layers x 12 heads "
+                      f"({t_total:.2f} s); a 512-sequence step costs 512x this"}
+
+
+# ----------------------------------------------------------------- main
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py runs on ONE GPU only: the PRIME hot paths here are single-GPU kernels "
+              "(sharding over (sequence, head) is a design note, not a built path). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+    from prime_moment_attention import _lib as lib
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    lib.load()
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, device=dev)   # 1 GiB of fp32
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    pf = bench_prefill(args, lib, torch, dev)
+    t_step = pf["ms"] * 1e-3
+    main_s = pf["main_ms"] * 1e-3
+    achieved = pf["bytes"] / main_s
+    traffic = load_traffic().get("prefill_chunks")  # measured for this kernel at this workload
+    rec = {
+        "metric": "prefill tok/s + decode tok/s (B=256) PRIME-125M, 1 MI355X; % MFMA/HBM roofline",
+        "value": pf["tokens"] / t_step,
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": pf["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, L2-normalised q/k, bf16)",
+        "config": {"workload": "chunked prefill, BASELINE config 2: B=8 x H=12 x L=8192, D=64, chunk 64, "
+                               "bf16 q/k/v, per-head lambda U[0.99,0.9999], zero initial state, bf16 y, "
+                               "fp32 final state",
+                   "B": pf["B"], "H": pf["H"], "L": pf["L"], "D": D, "chunk": pf["C"],
+                   "state_dtype": "fp32", "accumulate": "fp32", "workspace_bytes": pf["ws_bytes"],
+                   "seed": args.seed},
+        "roofline": {"kernel": "prefill_kernel<bf16,fused> (fused chunk loop)", "bound": "hbm",
+                     "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM,
+                     "traffic": None if traffic is None else traffic.get("bytes_per_launch"),
+                     "bytes_per_launch": pf["bytes"], "avg_launch_us": pf["main_ms"] * 1e3},
+        "prefill": {"whole_call_GBps": pf["bytes"] / t_step / 1e9,
+                    "whole_call_hbm_frac": pf["bytes"] / t_step / PEAK_HBM,
+                    "tflops": pf["flops"] / t_step / 1e12, "mfma_frac": pf["flops"] / t_step / PEAK_BF16,
+                    "kernels": pf["kernels"], "ms_per_step_all_kernels_bracketed": pf["ms_all_bracketed"],
+                    "finite": pf["finite"]},
+        "gpu": f"{torch.cuda.get_device_name(dev)} ({torch.cuda.get_device_properties(dev).gcnArchName}, "
+               f"{torch.cuda.get_device_properties(dev).multi_processor_count} CUs)",
+    }
+    if not args.no_decode:
+        d512 = bench_decode(args, lib, torch, dev, B=512)
+        d256 = bench_decode(args, lib, torch, dev, B=256)
+        for d, key in ((d512, "decode_b512"), (d256, "decode_b256")):
+            t = load_traffic().get(key)
+            if t is not None:
+                d["roofline"]["traffic"] = t.get("bytes_per_launch")
+        rec["decode"] = {"B=256": d256, "B=512": d512}
+    if not args.no_cpu:
+        try:
+            legs = cpu_prefill_legs(args)
+            ref = [x for x in legs if x["kind"] == "reference"]
+            rec["cpu_baseline"] = ref[0] if ref else legs[0]
+            rec["cpu_baselines"] = legs
+            rec["cpu_model"] = cpu_model()
+            if not args.no_decode:
+                rec["decode"]["cpu_baseline"] = cpu_decode_leg(args)
+        except Exception as exc:  # the GPU figures stand without the CPU legs
+            rec["cpu_baseline"] = None
+            rec["cpu_baseline_error"] = f"{type(exc).__name__}: {exc}"
+    print(json.dumps(rec), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

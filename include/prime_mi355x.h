@@ -113,6 +113,26 @@ int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k,
 /* Workspace bytes prime_chunked_prefill uses for this shape (0 = none needed). */
 size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags);
 
+/*
+ * Launch timer.  No counterpart in the reference: it serves benchmark harnesses
+ * that need the device time of ONE kernel of a multi-kernel call.
+ * prime_timer_enable(mask) (process-wide; bit (1 << PRIME_KERNEL_*) selects a
+ * kernel, 0 disables) brackets every launch of the selected kernels by a pair
+ * of HIP events on the call's stream.  prime_timer_read waits for the recorded
+ * events and returns the summed device time and launch count of one kernel
+ * since the last reset.  Event objects are created while enabled (never on the
+ * default, disabled path) and kept for reuse.
+ */
+#define PRIME_KERNEL_PREFILL_CHUNKS   0 /* fused chunk loop: y and final state */
+#define PRIME_KERNEL_PREFILL_SEGMENTS 1 /* per-segment state contributions */
+#define PRIME_KERNEL_SEGMENT_SCAN     2 /* exclusive scan over segments */
+#define PRIME_KERNEL_DECODE           3 /* fused decode step */
+#define PRIME_KERNEL_COUNT            4
+
+int prime_timer_enable(unsigned mask);
+int prime_timer_reset(void);
+int prime_timer_read(int kernel, double *total_ms, int64_t *launches);
+
 #ifdef __cplusplus
 }
 #endif

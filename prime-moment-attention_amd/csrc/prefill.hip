@@ -763,13 +763,19 @@ static void launch_variant(PrefillArgs a, hipStream_t stream) {
     if (a.G > 1) {
         // A: state contribution of every segment but the last, from zero
         a.nseg_launch = a.G - 1;
+        timer_begin(PRIME_KERNEL_PREFILL_SEGMENTS, stream);
         hipLaunchKernelGGL((prefill_kernel<F32IN, true>), dim3(Sq * (a.G - 1)), dim3(256), 0, stream, a);
+        timer_end(PRIME_KERNEL_PREFILL_SEGMENTS, stream);
         // B: exclusive scan over segments (incoming state first)
         const int64_t n = static_cast<int64_t>(Sq) * kWsElems;
+        timer_begin(PRIME_KERNEL_SEGMENT_SCAN, stream);
         hipLaunchKernelGGL(segment_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, a);
+        timer_end(PRIME_KERNEL_SEGMENT_SCAN, stream);
     }
     a.nseg_launch = a.G;
+    timer_begin(PRIME_KERNEL_PREFILL_CHUNKS, stream);
     hipLaunchKernelGGL((prefill_kernel<F32IN, false>), dim3(Sq * a.G), dim3(512), 0, stream, a);
+    timer_end(PRIME_KERNEL_PREFILL_CHUNKS, stream);
 }
 
 hipError_t launch_prefill(PrefillArgs a, hipStream_t stream) {

@@ -49,4 +49,8 @@ hipError_t launch_prefill(PrefillArgs a, hipStream_t stream);
 // segments per sequence for the launch plan, given the workspace the caller has
 void plan_segments(int S, int L, bool dense_clamp, size_t ws_bytes, int *G, int *cps);
 
+// Launch timer hooks (the C-ABI prime_timer_* calls); no-ops while disabled.
+void timer_begin(int kernel, hipStream_t stream);
+void timer_end(int kernel, hipStream_t stream);
+
 }  // namespace prime

@@ -23,7 +23,14 @@ _DTYPES = {torch.float32: PRIME_F32, torch.bfloat16: PRIME_BF16, torch.float16: 
 
 # every symbol include/prime_mi355x.h declares
 EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_chunked_prefill",
-           "prime_chunked_prefill_workspace_size")
+           "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
+           "prime_timer_read")
+
+# kernel identifiers of the launch timer
+KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
+KERNEL_NAMES = {KERNEL_PREFILL_CHUNKS: "prefill_kernel<bf16,fused>", KERNEL_PREFILL_SEGMENTS:
+                "prefill_kernel<bf16,state_only>", KERNEL_SEGMENT_SCAN: "segment_scan_kernel",
+                KERNEL_DECODE: "decode_step_kernel"}
 
 
 class PrimeTensor(ctypes.Structure):
@@ -59,6 +66,8 @@ def load() -> ctypes.CDLL:
     L.prime_chunked_prefill.restype = ctypes.c_int
     L.prime_chunked_prefill_workspace_size.argtypes = [ctypes.c_int] * 3 + [ctypes.c_uint]
     L.prime_chunked_prefill_workspace_size.restype = ctypes.c_size_t
+    L.prime_timer_enable.argtypes = [ctypes.c_uint]
+    L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     v = L.prime_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"libprime_mi355x ABI {v} != expected {ABI_VERSION}")
@@ -127,9 +136,29 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
-def decode_step(q, k, v, decay: torch.Tensor, eps: float, state_in, state_out, y) -> None:
-    """One fused decode step (prime_decode_step).  q [B,H,D], k/v [B,Hkv,D],
-    decay fp32 [H] on device, states: 6-tuples of contiguous fp32 tensors."""
+def bind_decode_step(q, k, v, decay: torch.Tensor, eps: float, state_in, state_out, y):
+    """Validate once and return a no-argument callable that launches
+    prime_decode_step on these exact buffers (on the device's current stream
+    at call time).  For tight loops whose buffers are fixed (generation, benchmarks):
+    the call skips the Python-side checks and descriptor building."""
+    _decode_checks(q, k, v, decay, state_in, state_out, y)
+    L = load()
+    B, H, D = q.shape
+    refs = (tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), state_desc(state_in),
+            state_desc(state_out), tensor_desc(y, False))
+    args = (ctypes.byref(refs[0]), ctypes.byref(refs[1]), ctypes.byref(refs[2]), B, H, k.shape[1], D,
+            ctypes.c_void_p(decay.data_ptr()), ctypes.c_float(eps),
+            ctypes.byref(refs[3]) if refs[3] else None, ctypes.byref(refs[4]), ctypes.byref(refs[5]))
+    fn, dev = L.prime_decode_step, q.device
+    keep = (q, k, v, decay, state_in, state_out, y, refs)
+
+    def launch():
+        _check(fn(*args, torch.cuda.current_stream(dev).cuda_stream), "prime_decode_step")
+    launch.buffers = keep
+    return launch
+
+
+def _decode_checks(q, k, v, decay, state_in, state_out, y):
     _dev_check(q, k, v, y, decay)
     B, H, D = q.shape
     Hkv = k.shape[1]
@@ -139,6 +168,13 @@ def decode_step(q, k, v, decay: torch.Tensor, eps: float, state_in, state_out, y
     _check_decay(decay, H)
     _check_state(state_in, B, H, D, "state_in")
     _check_state(state_out, B, H, D, "state_out")
+
+
+def decode_step(q, k, v, decay: torch.Tensor, eps: float, state_in, state_out, y) -> None:
+    """One fused decode step (prime_decode_step).  q [B,H,D], k/v [B,Hkv,D],
+    decay fp32 [H] on device, states: 6-tuples of contiguous fp32 tensors."""
+    _decode_checks(q, k, v, decay, state_in, state_out, y)
+    B, H, D = q.shape
     L = load()
     qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), tensor_desc(y, False)
     si, so = state_desc(state_in), state_desc(state_out)
@@ -152,11 +188,7 @@ def workspace_size(B: int, H: int, L: int, flags: int = 0) -> int:
     return int(load().prime_chunked_prefill_workspace_size(B, H, L, flags))
 
 
-def chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, state_in, y,
-                    state_out, flags: int = 0, workspace: Optional[torch.Tensor] = None) -> None:
-    """Chunked prefill (prime_chunked_prefill).  q [B,H,L,D], k/v [B,Hkv,L,D].
-    workspace: None allocates the recommended scratch from torch's caching
-    allocator; pass an empty tensor to run one segment per sequence."""
+def _prefill_args(q, k, v, decay, eps, chunk, state_in, y, state_out, flags, workspace):
     _dev_check(q, k, v, y, decay)
     B, H, Lq, D = q.shape
     Hkv = k.shape[1]
@@ -166,7 +198,6 @@ def chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, state_
     _check_decay(decay, H)
     _check_state(state_in, B, H, D, "state_in")
     _check_state(state_out, B, H, D, "state_out")
-    L = load()
     if workspace is None:
         nbytes = workspace_size(B, H, Lq, flags)
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
@@ -176,13 +207,57 @@ def chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, state_
         _dev_check(workspace)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    qd, kd, vd, yd = tensor_desc(q, True), tensor_desc(k, True), tensor_desc(v, True), tensor_desc(y, True)
-    si, so = state_desc(state_in), state_desc(state_out)
-    rc = L.prime_chunked_prefill(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), B, H, k.shape[1],
-                                 Lq, D, int(chunk), decay.data_ptr(), float(eps), int(flags),
-                                 ctypes.byref(si) if si else None, ctypes.byref(yd),
-                                 ctypes.byref(so) if so else None, ws_ptr, ws_bytes, _stream(q.device))
-    _check(rc, "prime_chunked_prefill")
+    refs = (tensor_desc(q, True), tensor_desc(k, True), tensor_desc(v, True), state_desc(state_in),
+            tensor_desc(y, True), state_desc(state_out))
+    args = (ctypes.byref(refs[0]), ctypes.byref(refs[1]), ctypes.byref(refs[2]), B, H, Hkv, Lq, D,
+            int(chunk), ctypes.c_void_p(decay.data_ptr()), ctypes.c_float(eps), int(flags),
+            ctypes.byref(refs[3]) if refs[3] else None, ctypes.byref(refs[4]),
+            ctypes.byref(refs[5]) if refs[5] else None, ws_ptr, ws_bytes)
+    return args, (q, k, v, decay, state_in, y, state_out, workspace, refs)
+
+
+def chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, state_in, y,
+                    state_out, flags: int = 0, workspace: Optional[torch.Tensor] = None) -> None:
+    """Chunked prefill (prime_chunked_prefill).  q [B,H,L,D], k/v [B,Hkv,L,D].
+    workspace: None allocates the recommended scratch from torch's caching
+    allocator; pass an empty tensor to run one segment per sequence."""
+    args, keep = _prefill_args(q, k, v, decay, eps, chunk, state_in, y, state_out, flags, workspace)
+    _check(load().prime_chunked_prefill(*args, _stream(q.device)), "prime_chunked_prefill")
+    del keep
+
+
+def bind_chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, state_in, y,
+                         state_out, flags: int = 0, workspace: Optional[torch.Tensor] = None):
+    """Validate once and return a no-argument callable that launches
+    prime_chunked_prefill on these exact buffers (current stream at call time);
+    the workspace, if allocated here, is held by the callable."""
+    args, keep = _prefill_args(q, k, v, decay, eps, chunk, state_in, y, state_out, flags, workspace)
+    fn, dev = load().prime_chunked_prefill, q.device
+
+    def launch():
+        _check(fn(*args, torch.cuda.current_stream(dev).cuda_stream), "prime_chunked_prefill")
+    launch.buffers = keep
+    return launch
+
+
+def timer_enable(*kernels: int) -> None:
+    """Bracket every launch of the given kernels (KERNEL_*) with HIP events;
+    no arguments disables the timer (prime_timer_enable)."""
+    mask = 0
+    for kid in kernels:
+        mask |= 1 << kid
+    load().prime_timer_enable(mask)
+
+
+def timer_reset() -> None:
+    _check(load().prime_timer_reset(), "prime_timer_reset")
+
+
+def timer_read(kernel: int) -> Tuple[float, int]:
+    """(summed device ms, launches) of one kernel since the last reset."""
+    ms, n = ctypes.c_double(), ctypes.c_int64()
+    _check(load().prime_timer_read(kernel, ctypes.byref(ms), ctypes.byref(n)), "prime_timer_read")
+    return ms.value, n.value
 
 
 _decay_cache = {}

@@ -84,3 +84,16 @@ def test_workspace_plan():
     assert _lib.workspace_size(1, 1000, 8192) == 0
     assert _lib.workspace_size(8, 12, 8192, _lib.PRIME_FLAG_DENSE_CLAMP) == 0
     assert _lib.workspace_size(1, 1, 64) == 0
+
+
+def test_timer_reads_without_launches():
+    """The launch timer: an unknown kernel id is rejected; with nothing
+    recorded every kernel reads zero launches (no device work involved)."""
+    L = _lib.load()
+    ms, n = ctypes.c_double(), ctypes.c_int64()
+    assert L.prime_timer_read(7, ctypes.byref(ms), ctypes.byref(n)) == -1
+    assert L.prime_timer_read(0, None, None) == -1
+    _lib.timer_enable()
+    _lib.timer_reset()
+    for kid in _lib.KERNEL_NAMES:
+        assert _lib.timer_read(kid) == (0.0, 0)

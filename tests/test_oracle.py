@@ -146,6 +146,34 @@ def test_chunked_state_carry_invariant():
     _states_close(s2, s_all, 1e-10)
 
 
+@pytest.mark.parametrize("carry", ["dense", "scan"])
+@pytest.mark.parametrize("L,with_state", [(200, False), (129, True), (64, True)])
+def test_torch_cpu_restatement_matches_oracle(carry, L, with_state):
+    """The fp32 PyTorch CPU baseline (oracle/torch_cpu.py) agrees with the fp64
+    oracle to fp32 accuracy, for both inter-chunk carries, per-head lambda, a
+    ragged last chunk and an incoming state; its decode step agrees with the
+    recurrence."""
+    import torch
+    from oracle import torch_cpu as T
+    B, H, D = 2, 3, 16
+    q, k, v = _rand(B * H, L, D, 31)
+    lam = np.array([0.97, 0.995, 0.9999])
+    st = _rand_state(B * H, D, 32) if with_state else None
+    yo, so = O.chunked(q, k, v, np.tile(lam, B), chunk=64, state=st)
+    t = lambda x: torch.tensor(x, dtype=torch.float32).reshape(B, H, *x.shape[1:])
+    tst = None
+    if st is not None:
+        tst = tuple(torch.tensor(x, dtype=torch.float32).reshape(B, H, *x.shape[1:]) for x in st)
+    y, s = T.chunked_core(t(q), t(k), t(v), torch.tensor(lam), chunk=64, state=tst, carry=carry)
+    _close(y.double().numpy().reshape(B * H, L, D), yo, 1e-5)
+    _states_close([x.double().numpy() for x in s], so, 1e-5)
+    # one decode step from the final state equals the recurrence on L + 1 tokens
+    q1, k1, v1 = _rand(B * H, 1, D, 33)
+    yr, _ = O.recurrent(q1, k1, v1, np.tile(lam, B), state=so)
+    yd, _ = T.decode_step(t(q1[:, 0]), t(k1[:, 0]), t(v1[:, 0]), torch.tensor(lam), 1.0, s)
+    _close(yd.double().numpy().reshape(B * H, D), yr[:, 0], 1e-5)
+
+
 def test_chunked_eps_clamp_active():
     """Early tokens with den < eps: the chunked form must clamp exactly like the
     recurrence (unnormalised inputs give s = q.k far from 0)."""
