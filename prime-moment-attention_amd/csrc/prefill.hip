@@ -28,9 +28,10 @@
 // e = 0..3, i.e. four consecutive tokens of one column.  A 16-column block
 // whose first column is 1 (w in the update) rides along every product and
 // yields the intra denominator, the K state and its readout on MFMA.
-// Per chunk: barrier; readout and update compute (readout waves prefetch the
-// next chunk from HBM); barrier; the update role publishes the bf16 state copy
-// while both roles write the next chunk's tiles.
+// Per chunk: barrier; both roles issue the next chunk's HBM loads (readout: q
+// and k, update: v; 8 whole 128-byte rows per wave load), then compute;
+// barrier; the update role publishes the bf16 state copy while both roles
+// write the next chunk's tiles to LDS.
 //
 // Precision: bf16 inputs enter the MFMA exactly; derived operands (squares,
 // the score block, the state copy, w v) are rounded to bf16 once.  fp32 inputs
