@@ -38,110 +38,9 @@
 // (F32IN) keep every LDS array as a bf16 hi plane plus a lo residual plane and
 // accumulate hi*hi + hi*lo + lo*hi (three MFMAs per product, ~2^-16 relative).
 
-#include "prime_kernels.h"
+#include "prefill_common.h"
 
 namespace prime {
-
-constexpr int kC = 64;          // tokens per chunk
-constexpr int kF = 2 * kD;      // feature width
-constexpr int kPW = kF + 8;     // pitch of 128-wide rows read 16 bytes per lane (68 dwords)
-// Pitch of rows read with ds_read_b64_tr_b16.  A 16-lane group reads 4
-// consecutive rows x 32 contiguous bytes and the next group the next 4 rows: a
-// pitch of 72 dwords (8 mod 32 and mod 64) puts 8 consecutive rows' windows on
-// disjoint banks.  The fp32 path (two planes per array) uses the tighter 68 /
-// 44-dword pitches to fit in LDS.
-constexpr int kPT = kF + 16;
-
-typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
-typedef __attribute__((__vector_size__(4 * sizeof(short)))) short i16x4;
-typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
-
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 r) { return __builtin_bit_cast(bf16x8, r); }
-
-// two floats -> packed bf16 pair (one v_cvt_pk_bf16_f32, round to nearest even)
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
-}
-
-__device__ __forceinline__ void unpack8(u32x4 r, float (&f)[8]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f[2 * i] = __uint_as_float(r[i] << 16);
-        f[2 * i + 1] = __uint_as_float(r[i] & 0xFFFF0000u);
-    }
-}
-
-__device__ __forceinline__ u32x4 pack8(const float (&f)[8]) {
-    u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = pack2(f[2 * i], f[2 * i + 1]);
-    return r;
-}
-
-__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// An MFMA operand: hi part, plus the lo residual when split (S).
-template <bool S>
-struct Opnd {
-    bf16x8 h, l;
-};
-
-template <bool S>
-__device__ __forceinline__ f32x4 mma(const Opnd<S> &a, const Opnd<S> &b, f32x4 c) {
-    c = mfma(a.h, b.h, c);
-    if constexpr (S) {
-        c = mfma(a.h, b.l, c);
-        c = mfma(a.l, b.h, c);
-    }
-    return c;
-}
-
-// 8 floats -> bf16 hi (and lo residual) packed
-template <bool S>
-__device__ __forceinline__ void split_pack(const float (&f)[8], u32x4 &hi, u32x4 &lo) {
-    hi = pack8(f);
-    if constexpr (S) {
-        float hf[8], r[8];
-        unpack8(hi, hf);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] = f[i] - hf[i];
-        lo = pack8(r);
-    }
-}
-
-// 16-byte LDS read
-__device__ __forceinline__ u32x4 lds128(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
-
-// ds_read_b64_tr_b16 (see the header comment for the lane mapping)
-__device__ __forceinline__ uint2 lds_tr(const uint16_t *p) {
-    typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(const_cast<uint16_t *>(p)));
-    return __builtin_bit_cast(uint2, v);
-}
-
-// operand of 8 consecutive tokens (two transposed 4-token reads) of one column
-template <bool S>
-__device__ __forceinline__ Opnd<S> tr_op(const uint16_t *p0, const uint16_t *p1, size_t plane) {
-    Opnd<S> o;
-    const uint2 a = lds_tr(p0), b = lds_tr(p1);
-    o.h = as_bf16x8(u32x4{a.x, a.y, b.x, b.y});
-    if constexpr (S) {
-        const uint2 c = lds_tr(p0 + plane), d = lds_tr(p1 + plane);
-        o.l = as_bf16x8(u32x4{c.x, c.y, d.x, d.y});
-    }
-    return o;
-}
-
-template <bool S>
-__device__ __forceinline__ Opnd<S> row_op(const uint16_t *p, size_t plane) {
-    Opnd<S> o;
-    o.h = as_bf16x8(lds128(p));
-    if constexpr (S) o.l = as_bf16x8(lds128(p + plane));
-    return o;
-}
 
 // one 8-element row segment of a q/k/v tile, kept packed until it is stored
 template <bool F32IN>
@@ -155,23 +54,21 @@ struct Seg8<true> {
     f32x4 a, b;
 };
 
-// Branch-free: the caller passes an in-bounds offset (rows past L clamped to
-// row L-1) and the value is replaced by zero when !valid.  (A conditional load
-// here lets the optimiser merge the stores into a pointer select and keep the
-// prefetch registers in scratch memory.)
+// Unconditional load of an in-bounds row (rows past L are clamped to row L-1
+// by the caller).  Rows that are not part of the chunk are zeroed when the
+// tile is stored to LDS, not here: a select on the loaded value right after
+// the load would make the wave wait for the load before its chunk's compute,
+// and a conditional load lets the optimiser merge the stores into a pointer
+// select and keep the prefetch registers in scratch memory.
 template <bool F32IN>
-__device__ __forceinline__ Seg8<F32IN> load_seg(const void *base, int64_t off, bool valid) {
+__device__ __forceinline__ Seg8<F32IN> load_seg(const void *base, int64_t off) {
     Seg8<F32IN> s;
     if constexpr (!F32IN) {
-        const u32x4 x = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(base) + off);
-        const uint32_t m = valid ? 0xFFFFFFFFu : 0u;
-        s.r = u32x4{x[0] & m, x[1] & m, x[2] & m, x[3] & m};
+        s.r = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(base) + off);
     } else {
         const f32x4 *p = reinterpret_cast<const f32x4 *>(static_cast<const float *>(base) + off);
-        const f32x4 a = p[0], b = p[1];
-        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        s.a = valid ? a : z;
-        s.b = valid ? b : z;
+        s.a = p[0];
+        s.b = p[1];
     }
     return s;
 }
@@ -218,46 +115,53 @@ __device__ __forceinline__ void load_tiles_fn(const PrefillArgs &a, TileRegs<F32
                                               int64_t qb, int64_t kb, int64_t vb) {
     const int col = 8 * (rt & 7);
     const int ta = c * kC + (rt >> 3), tb = ta + 32;
-    const bool oka = ta < a.L, okb = tb < a.L;
-    const int sa = oka ? ta : a.L - 1, sb = okb ? tb : a.L - 1;  // in-bounds rows for the masked loads
+    const int sa = min(ta, a.L - 1), sb = min(tb, a.L - 1);  // in-bounds rows
     const void *x = is_u ? a.v : a.q;
     const int64_t xb = is_u ? vb : qb, xl = is_u ? a.v_sl : a.q_sl;
-    R.r0 = load_seg<F32IN>(x, xb + sa * xl + col, oka);
-    R.r1 = load_seg<F32IN>(x, xb + sb * xl + col, okb);
+    R.r0 = load_seg<F32IN>(x, xb + sa * xl + col);
+    R.r1 = load_seg<F32IN>(x, xb + sb * xl + col);
     // update waves of the fused kernel need no k: they re-read their v rows (L1
-    // hits) and mask them to zero
+    // hits) into the k slots, which they never store
     const bool want_k = !is_u || STATE_ONLY;
     const void *kx = want_k ? a.k : x;
     const int64_t kbb = want_k ? kb : xb, kl = want_k ? a.k_sl : xl;
-    R.r2 = load_seg<F32IN>(kx, kbb + sa * kl + col, oka && want_k);
-    R.r3 = load_seg<F32IN>(kx, kbb + sb * kl + col, okb && want_k);
+    R.r2 = load_seg<F32IN>(kx, kbb + sa * kl + col);
+    R.r3 = load_seg<F32IN>(kx, kbb + sb * kl + col);
 }
 
 // One 8-column segment of one token row: q -> [q | q*q], k -> [k | k*k/2],
 // v -> v and w v (plus w itself in column 64 from the segment-0 thread).
+template <bool F32IN>
+__device__ __forceinline__ void seg_f32_masked(const Seg8<F32IN> &s, bool valid, float (&f)[8]) {
+    seg_f32(s, f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = valid ? f[e] : 0.f;
+}
+
+// Rows past the chunk's valid tokens (valid == false) are stored as zeros.
 template <bool F32IN, bool STATE_ONLY>
 __device__ __forceinline__ void store_seg_fn(const Seg8<F32IN> &x01, const Seg8<F32IN> &k, int row, int col,
-                                             bool is_u, float w, uint16_t *sQf, size_t plQ, uint16_t *sKf,
-                                             size_t plK, int kPK, uint16_t *sV, size_t plV, uint16_t *sVw,
-                                             size_t plVw, int kPV) {
+                                             bool valid, bool is_u, float w, uint16_t *sQf, size_t plQ,
+                                             uint16_t *sKf, size_t plK, int kPK, uint16_t *sV, size_t plV,
+                                             uint16_t *sVw, size_t plVw, int kPV) {
     constexpr bool S = F32IN;
     float x[8], y2[8];
     if (!is_u || STATE_ONLY) {
         if (!is_u) {
-            seg_f32(x01, x);
+            seg_f32_masked(x01, valid, x);
             put8<S>(sQf + row * kPW + col, plQ, x);
 #pragma unroll
             for (int e = 0; e < 8; ++e) y2[e] = x[e] * x[e];
             put8<S>(sQf + row * kPW + kD + col, plQ, y2);
         }
-        seg_f32(k, x);
+        seg_f32_masked(k, valid, x);
         put8<S>(sKf + row * kPK + col, plK, x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) y2[e] = 0.5f * x[e] * x[e];
         put8<S>(sKf + row * kPK + kD + col, plK, y2);
     }
     if (is_u) {
-        seg_f32(x01, x);
+        seg_f32_masked(x01, valid, x);
         if constexpr (!STATE_ONLY) put8<S>(sV + row * kPV + col, plV, x);
 #pragma unroll
         for (int e = 0; e < 8; ++e) y2[e] = w * x[e];
@@ -275,8 +179,10 @@ __device__ __forceinline__ void store_tiles_fn(const TileRegs<F32IN> &R, int rt,
     const int ra = rt >> 3, rb = ra + 32;
     const float wa = ra < nvalid ? sPw[nvalid - 1 - ra] : 0.f;
     const float wb = rb < nvalid ? sPw[nvalid - 1 - rb] : 0.f;
-    store_seg_fn<F32IN, STATE_ONLY>(R.r0, R.r2, ra, col, is_u, wa, sQf, plQ, sKf, plK, kPK, sV, plV, sVw, plVw, kPV);
-    store_seg_fn<F32IN, STATE_ONLY>(R.r1, R.r3, rb, col, is_u, wb, sQf, plQ, sKf, plK, kPK, sV, plV, sVw, plVw, kPV);
+    store_seg_fn<F32IN, STATE_ONLY>(R.r0, R.r2, ra, col, ra < nvalid, is_u, wa, sQf, plQ, sKf, plK, kPK, sV, plV,
+                                    sVw, plVw, kPV);
+    store_seg_fn<F32IN, STATE_ONLY>(R.r1, R.r3, rb, col, rb < nvalid, is_u, wb, sQf, plQ, sKf, plK, kPK, sV, plV,
+                                    sVw, plVw, kPV);
 }
 
 // Segment plan.  Without a workspace (or for the dense branch, whose clamp
@@ -356,7 +262,10 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(const PrefillArgs a) {
     constexpr size_t plS = static_cast<size_t>(SR) * kPW;
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    // wave index in a scalar register: every role / wave test below is then a
+    // scalar branch, so no MFMA runs under a partial or empty EXEC mask
+    // (MFMAs write their whole destination regardless of EXEC)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
     const bool is_u = STATE_ONLY || wave >= 4;
     const int u = STATE_ONLY ? wave : wave - 4;  // update-wave index
@@ -486,7 +395,10 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(const PrefillArgs a) {
 
     for (int c = c_begin; c < c_end; ++c) {
         const int nvalid = min(kC, a.L - c * kC);
-        if (c + 1 < c_end) PRIME_LOAD_TILES(c + 1);
+        // unconditional (past the last chunk the rows clamp to L-1 and the
+        // registers are never stored): no branch around the loads means no
+        // register copies, and no wait for the loads, at the join
+        PRIME_LOAD_TILES(c + 1);
 
         float ds0 = 0.f;  // update role: sum_j w_j v[j][16u + c16] over this lane's tokens
         if (!is_u) {
@@ -765,7 +677,8 @@ static void launch_variant(PrefillArgs a, hipStream_t stream) {
         // A: state contribution of every segment but the last, from zero
         a.nseg_launch = a.G - 1;
         timer_begin(PRIME_KERNEL_PREFILL_SEGMENTS, stream);
-        hipLaunchKernelGGL((prefill_kernel<F32IN, true>), dim3(Sq * (a.G - 1)), dim3(256), 0, stream, a);
+        if constexpr (F32IN) hipLaunchKernelGGL((prefill_kernel<true, true>), dim3(Sq * (a.G - 1)), dim3(256), 0, stream, a);
+        else launch_prefill_bf16(a, true, Sq * (a.G - 1), stream);
         timer_end(PRIME_KERNEL_PREFILL_SEGMENTS, stream);
         // B: exclusive scan over segments (incoming state first)
         const int64_t n = static_cast<int64_t>(Sq) * kWsElems;
@@ -775,7 +688,8 @@ static void launch_variant(PrefillArgs a, hipStream_t stream) {
     }
     a.nseg_launch = a.G;
     timer_begin(PRIME_KERNEL_PREFILL_CHUNKS, stream);
-    hipLaunchKernelGGL((prefill_kernel<F32IN, false>), dim3(Sq * a.G), dim3(512), 0, stream, a);
+    if constexpr (F32IN) hipLaunchKernelGGL((prefill_kernel<true, false>), dim3(Sq * a.G), dim3(512), 0, stream, a);
+    else launch_prefill_bf16(a, false, Sq * a.G, stream);
     timer_end(PRIME_KERNEL_PREFILL_CHUNKS, stream);
 }
 

@@ -1,0 +1,464 @@
+// Chunked PRIME prefill for bf16 inputs on gfx950: double-buffered chunk
+// tiles and state copy, one workgroup barrier per chunk.
+//
+// Same algorithm and semantics as the generic kernel in prefill.hip (see its
+// header comment for the chunk equations and the operand layouts); this kernel
+// differs in its schedule:
+//   readout waves 0..3 only compute: score block, AV, state readout, y;
+//   update waves 4..7 own the state M = [S1; S2/2 | K] in MFMA accumulators and,
+//     in the step of chunk c, (a) add chunk c's contribution, (b) convert and
+//     store chunk c+1's tiles (loaded from HBM one chunk earlier) into the other
+//     tile buffer, (c) issue the HBM loads of chunk c+2 and (d) publish the bf16
+//     state copy entering chunk c+1 into the other state buffer.
+// Chunk c reads tile buffer c&1 and state buffer c&1 while chunk c+1's are
+// written, so one barrier per chunk orders every hazard.  S0 also accumulates
+// on MFMA: update wave u multiplies value block u of [w v] by an A operand whose
+// row 0 is all ones (other rows zero), which sums w_j v_j over the chunk's
+// tokens; K0 is a scalar recurrence with the exact fp32 power sums.
+//
+// The state-only launch (segment contributions from a zero state) runs the
+// update role alone: 4 waves, k and v tiles only, one tile buffer and two
+// barriers per chunk (a third of the LDS: three workgroups fit on a CU).
+
+#include "prefill_common.h"
+
+namespace prime {
+namespace {
+
+constexpr int kPV8 = kD + 16;  // sV / sVw pitch in bf16 (40 dwords, conflict-free transposed reads)
+constexpr int kSR = kD + 1;    // state copy rows: 64 value columns + the K column
+
+__device__ __forceinline__ u32x4 ld16(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
+
+__device__ __forceinline__ void st16(uint16_t *p, u32x4 x) { *reinterpret_cast<u32x4 *>(p) = x; }
+
+__device__ __forceinline__ u32x4 and4(u32x4 x, uint32_t m) { return u32x4{x[0] & m, x[1] & m, x[2] & m, x[3] & m}; }
+
+// s * x * x of 8 packed bf16, repacked (round to nearest even)
+__device__ __forceinline__ u32x4 sq8(u32x4 x, float s) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = __uint_as_float(x[i] << 16), hi = __uint_as_float(x[i] & 0xFFFF0000u);
+        r[i] = pack2(s * lo * lo, s * hi * hi);
+    }
+    return r;
+}
+
+// w * x of 8 packed bf16, repacked
+__device__ __forceinline__ u32x4 scale8(u32x4 x, float w) {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = pack2(w * __uint_as_float(x[i] << 16), w * __uint_as_float(x[i] & 0xFFFF0000u));
+    return r;
+}
+
+// The next chunk's rows ra and ra + 32, one 16-byte segment each, per update thread.
+struct Tiles {
+    u32x4 q0, q1, k0, k1, v0, v1;
+};
+
+// Unconditional loads; rows past L clamp to row L-1 (zeroed when stored).
+template <bool STATE_ONLY>
+__device__ __forceinline__ void load_tiles(Tiles &T, const PrefillArgs &a, const uint16_t *qp, const uint16_t *kp,
+                                           const uint16_t *vp, int c, int ra) {
+    const int64_t ta = min(c * kC + ra, a.L - 1), tb = min(c * kC + ra + 32, a.L - 1);
+    if constexpr (!STATE_ONLY) {
+        T.q0 = ld16(qp + ta * a.q_sl);
+        T.q1 = ld16(qp + tb * a.q_sl);
+    }
+    T.k0 = ld16(kp + ta * a.k_sl);
+    T.k1 = ld16(kp + tb * a.k_sl);
+    T.v0 = ld16(vp + ta * a.v_sl);
+    T.v1 = ld16(vp + tb * a.v_sl);
+}
+
+// One row segment into the tile buffers: [q | q*q], [k | k*k/2], [v], [w v | w].
+// Invalid rows (past the chunk's tokens) are stored as zeros.
+template <bool STATE_ONLY>
+__device__ __forceinline__ void store_row(u32x4 q, u32x4 k, u32x4 v, int row, int col, bool valid, float w,
+                                          uint16_t *sQf, uint16_t *sKf, uint16_t *sV, uint16_t *sVw) {
+    const uint32_t m = valid ? 0xFFFFFFFFu : 0u;
+    k = and4(k, m);
+    v = and4(v, m);
+    if constexpr (!STATE_ONLY) {
+        q = and4(q, m);
+        st16(sQf + row * kPW + col, q);
+        st16(sQf + row * kPW + kD + col, sq8(q, 1.0f));
+        st16(sV + row * kPV8 + col, v);
+    }
+    st16(sKf + row * kPW + col, k);
+    st16(sKf + row * kPW + kD + col, sq8(k, 0.5f));
+    st16(sVw + row * kPV8 + col, scale8(v, w));
+    if (col == 0) sVw[row * kPV8 + kD] = f32_to_bf16_bits(w);
+}
+
+}  // namespace
+
+template <bool STATE_ONLY>
+__global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel(const PrefillArgs a) {
+    constexpr int NB = kD / 16;    // value blocks
+    constexpr int NBX = NB + 1;    // + the ones / K block
+    constexpr int QB = STATE_ONLY ? 1 : 2;   // buffers of the readout-only arrays
+    constexpr int QR = STATE_ONLY ? 1 : kC;
+    constexpr int SR = STATE_ONLY ? 1 : kSR;
+    constexpr int KI = STATE_ONLY ? 1 : kF;
+    constexpr int XB = STATE_ONLY ? 1 : 2;   // tile buffers
+
+    __shared__ __attribute__((aligned(16))) uint16_t sQf[QB][QR][kPW];   // [q | q*q]
+    __shared__ __attribute__((aligned(16))) uint16_t sKf[XB][kC][kPW];   // [k | k*k/2]
+    __shared__ __attribute__((aligned(16))) uint16_t sV[QB][QR][kPV8];   // [v | 1 0..0]
+    __shared__ __attribute__((aligned(16))) uint16_t sVw[XB][kC][kPV8];  // [w v | w 0..0]
+    __shared__ __attribute__((aligned(16))) uint16_t sSt[QB][SR][kPW];   // bf16 [S1; S2/2 | K]^T entering the chunk
+    __shared__ __attribute__((aligned(16))) float sS0[QB][kD];           // S0 entering the chunk
+    __shared__ float sK0[QB];                                             // K0 entering the chunk
+    __shared__ float sPw[kC + 2];                                         // l^n, n = 0..65
+    __shared__ float sPs[kC + 2];                                         // sum_{m<n} l^m
+    __shared__ float sKi[KI];                                             // incoming [K1; K2/2] (dense)
+    __shared__ float sKi0;                                                // incoming K0 (dense)
+
+    const int tid = threadIdx.x;
+    // wave index in a scalar register: every role / wave test below is then a
+    // scalar branch, so no MFMA runs under a partial or empty EXEC mask
+    // (MFMAs write their whole destination regardless of EXEC)
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int g = lane >> 4, c16 = lane & 15;
+    const bool is_u = STATE_ONLY || wave >= 4;
+    const int u = STATE_ONLY ? wave : wave - 4;       // update-wave index
+    const int ut = tid & 255;                          // thread index within the update role
+    const int tr_r = c16 >> 2, tr_c = 4 * (c16 & 3);  // ds_read_tr address offsets of this lane
+
+    const int Sq = a.B * a.H;
+    const int unit = blockIdx.x;
+    if (unit >= Sq * a.nseg_launch) return;  // whole workgroup leaves before any barrier
+    const int seq = unit / a.nseg_launch, seg = unit - seq * a.nseg_launch;
+    const int b = seq / a.H, h = seq - b * a.H, hk = h / a.group;
+    const float lam = a.decay[h];
+    const int NC = (a.L + kC - 1) / kC;
+    const int c_begin = seg * a.cps;
+    const int c_end = min(c_begin + a.cps, NC);
+    const bool from_ws = !STATE_ONLY && a.G > 1;
+    const bool has_in = !STATE_ONLY && !from_ws && a.s1i != nullptr;
+    const bool dense = !STATE_ONLY && a.dense_clamp;
+    float *wslot = a.ws ? a.ws + (static_cast<size_t>(seq) * a.G + seg) * kWsStride : nullptr;
+
+    if (tid < kC + 2) {
+        const double ld = static_cast<double>(lam);
+        sPw[tid] = static_cast<float>(pow(ld, static_cast<double>(tid)));
+        double ps = 0.0, pm = 1.0;  // prefix sum of powers in fp64 (1 - l is tiny near l = 1)
+        for (int m = 0; m < tid; ++m, pm *= ld) ps += pm;
+        sPs[tid] = static_cast<float>(ps);
+    }
+    __syncthreads();  // the power tables are read by the first tile stores below
+
+    // ---- update role: state registers, tile pointers, first tiles
+    const size_t so1 = static_cast<size_t>(seq) * kD * kD;
+    const size_t so0 = static_cast<size_t>(seq) * kD;
+    f32x4 st[2][NBX];  // feature blocks 2u+fi (rows 4g+r), value blocks nb (column c16)
+    f32x4 s0t;         // row 0 (lanes 0..15, element 0) = S0[16u + c16]
+    float k0 = 0.f;    // K0 (same value in every lane and update wave)
+    Tiles T;
+    if constexpr (STATE_ONLY) T.q0 = T.q1 = u32x4{0u, 0u, 0u, 0u};
+    const int ra = ut >> 3, col = 8 * (ut & 7);
+    const uint16_t *qp = static_cast<const uint16_t *>(a.q) + (b * a.q_sb + h * a.q_sh + col);
+    const uint16_t *kp = static_cast<const uint16_t *>(a.k) + (b * a.k_sb + hk * a.k_sh + col);
+    const uint16_t *vp = static_cast<const uint16_t *>(a.v) + (b * a.v_sb + hk * a.v_sh + col);
+    auto store_tiles = [&](int c, int xb) {
+        const int nv = min(kC, a.L - c * kC);
+        const bool va = ra < nv, vb = ra + 32 < nv;
+        const float wa = va ? sPw[nv - 1 - ra] : 0.f, wb = vb ? sPw[nv - 1 - (ra + 32)] : 0.f;
+        uint16_t *pq = &sQf[STATE_ONLY ? 0 : xb][0][0], *pv = &sV[STATE_ONLY ? 0 : xb][0][0];
+        store_row<STATE_ONLY>(T.q0, T.k0, T.v0, ra, col, va, wa, pq, &sKf[xb][0][0], pv, &sVw[xb][0][0]);
+        store_row<STATE_ONLY>(T.q1, T.k1, T.v1, ra + 32, col, vb, wb, pq, &sKf[xb][0][0], pv, &sVw[xb][0][0]);
+    };
+    // bf16 copy of the state entering the next chunk, into state buffer xb
+    auto publish_state = [&](int xb) {
+        if constexpr (!STATE_ONLY) {
+#pragma unroll
+            for (int fi = 0; fi < 2; ++fi) {
+                const int f = 16 * (2 * u + fi) + 4 * g;
+#pragma unroll
+                for (int nb = 0; nb < NBX; ++nb) {
+                    const int n = 16 * nb + c16;
+                    if (n > kD) continue;  // columns 65..79 of the ones block are zero
+                    *reinterpret_cast<uint2 *>(&sSt[xb][n][f]) =
+                        uint2{pack2(st[fi][nb][0], st[fi][nb][1]), pack2(st[fi][nb][2], st[fi][nb][3])};
+                }
+            }
+            if (g == 0) sS0[xb][16 * u + c16] = s0t[0];
+            if (u == 0 && lane == 0) sK0[xb] = k0;
+        }
+    };
+    if (is_u) {
+        load_tiles<STATE_ONLY>(T, a, qp, kp, vp, c_begin, ra);
+#pragma unroll
+        for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+            for (int nb = 0; nb < NBX; ++nb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int f = 16 * (2 * u + fi) + 4 * g + r, fr = f & (kD - 1);
+                    const int n = 16 * nb + c16;
+                    float x = 0.f;
+                    if (n < kD) {
+                        if (from_ws) x = wslot[(f < kD ? kWsS1 : kWsS2) + fr * kD + n];
+                        else if (has_in) x = (f < kD ? a.s1i : a.s2i)[so1 + fr * kD + n];
+                    } else if (n == kD && !dense) {  // dense: K of the call only, incoming in sKi
+                        if (from_ws) x = wslot[(f < kD ? kWsK1 : kWsK2) + fr];
+                        else if (has_in) x = (f < kD ? a.k1i : a.k2i)[so0 + fr];
+                    }
+                    st[fi][nb][r] = f < kD ? x : 0.5f * x;
+                }
+        {
+            float x = 0.f;
+            if (g == 0) x = from_ws ? wslot[kWsS0 + 16 * u + c16] : (has_in ? a.s0i[so0 + 16 * u + c16] : 0.f);
+            s0t = f32x4{x, 0.f, 0.f, 0.f};
+        }
+        {
+            const float x = from_ws ? wslot[kWsK0] : (has_in ? a.k0i[seq] : 0.f);
+            k0 = dense ? 0.f : x;
+            if (!STATE_ONLY && ut == 0) sKi0 = dense ? x : 0.f;
+        }
+        if constexpr (!STATE_ONLY) {
+            if (ut < kF) {
+                const int fr = ut & (kD - 1);
+                float x = 0.f;
+                if (dense && has_in) x = (ut < kD ? a.k1i : a.k2i)[so0 + fr];
+                sKi[ut] = ut < kD ? x : 0.5f * x;
+            }
+        }
+        // constant columns: 64..79 of v (1, 0, ...) and 65..79 of w v (column 64
+        // holds w and is written with every chunk's tile)
+        for (int idx = ut; idx < XB * kC * 16; idx += 256) {
+            const int xb = idx / (kC * 16), row = (idx >> 4) & (kC - 1), cc = kD + (idx & 15);
+            if constexpr (!STATE_ONLY) sV[xb][row][cc] = cc == kD ? 0x3F80u : 0u;
+            if (cc != kD) sVw[xb][row][cc] = 0u;
+        }
+        publish_state(c_begin & 1);
+        store_tiles(c_begin, STATE_ONLY ? 0 : c_begin & 1);
+        load_tiles<STATE_ONLY>(T, a, qp, kp, vp, c_begin + 1, ra);
+    }
+
+    // ---- readout-role constants (query row of the lane: iw)
+    const int iw = 16 * wave + c16;
+    float mask[4][4];  // l^(i-j) [i >= j] for S^T[j = 16jb + 4g + r][i = iw]
+    float pin = 0.f;   // l^(iw+1)
+    if (!is_u) {
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int d = iw - (16 * jb + 4 * g + r);
+                mask[jb][r] = (jb <= wave && d >= 0) ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(d))) : 0.f;
+            }
+        pin = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(iw + 1)));
+    }
+    // row 0 of the ones operand: lanes of A-row 0 hold eight 1.0s
+    const bf16x8 ones = as_bf16x8(c16 == 0 ? u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}
+                                           : u32x4{0u, 0u, 0u, 0u});
+    __syncthreads();
+
+    for (int c = c_begin; c < c_end; ++c) {
+        const int p = STATE_ONLY ? 0 : c & 1, xq = STATE_ONLY ? 0 : p ^ 1;
+        const int nvalid = min(kC, a.L - c * kC);
+        if (!is_u) {
+            if constexpr (!STATE_ONLY) {
+                // ---- query features of row iw (B operand of S^T and of the readout)
+                Opnd<false> fq[4];
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) fq[ks] = row_op<false>(&sQf[p][iw][32 * ks + 8 * g], 0);
+                // ---- transposed score block S^T[j][i] for j-blocks jb <= wave
+                f32x4 sT[4];
+#pragma unroll
+                for (int jb = 0; jb < 4; ++jb) {
+                    sT[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if (jb > wave) continue;
+                    Opnd<false> ak[4];
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) ak[ks] = row_op<false>(&sKf[p][16 * jb + c16][32 * ks + 8 * g], 0);
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) sT[jb] = mma<false>(ak[ks], fq[ks], sT[jb]);
+                }
+                // ---- A = decay mask * (1 + S) as packed bf16
+                uint32_t Ah[4][2];
+#pragma unroll
+                for (int jb = 0; jb < 4; ++jb) {
+                    float x[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) x[r] = mask[jb][r] * (1.0f + sT[jb][r]);
+                    Ah[jb][0] = pack2(x[0], x[1]);
+                    Ah[jb][1] = pack2(x[2], x[3]);
+                }
+                // ---- y^T = V^T A^T: accumulator row = value column 16nb + 4g + r,
+                // column = query row iw; register t of A^T <-> token 32kk + 16(t/4) + 4g + t%4
+                f32x4 acc_av[NBX], acc_ro[NBX];
+#pragma unroll
+                for (int nb = 0; nb < NBX; ++nb) {
+                    acc_av[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    acc_ro[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    if (2 * kk > wave) continue;
+                    const bool second = 2 * kk + 1 <= wave;  // second j-block unmasked
+                    Opnd<false> aop;
+                    aop.h = as_bf16x8(u32x4{Ah[2 * kk][0], Ah[2 * kk][1], second ? Ah[2 * kk + 1][0] : 0u,
+                                            second ? Ah[2 * kk + 1][1] : 0u});
+                    Opnd<false> vop[NBX];
+#pragma unroll
+                    for (int nb = 0; nb < NBX; ++nb) {
+                        const uint16_t *p0 = &sV[p][32 * kk + 4 * g + tr_r][16 * nb + tr_c];
+                        vop[nb] = tr_op<false>(p0, p0 + 16 * kPV8, 0);
+                    }
+#pragma unroll
+                    for (int nb = 0; nb < NBX; ++nb) acc_av[nb] = mma<false>(vop[nb], aop, acc_av[nb]);
+                }
+                // ---- y^T += [S1; S2/2 | K]^T Fq^T  (the state entering the chunk)
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    Opnd<false> sop[NBX];
+#pragma unroll
+                    for (int nb = 0; nb < NBX; ++nb) {
+                        const int n = nb == NB ? kD : 16 * nb + c16;  // ones block: only row 64 (K)
+                        sop[nb] = row_op<false>(&sSt[p][n][32 * ks + 8 * g], 0);
+                        if (nb == NB && c16 != 0) sop[nb].h = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
+                    }
+#pragma unroll
+                    for (int nb = 0; nb < NBX; ++nb) acc_ro[nb] = mma<false>(sop[nb], fq[ks], acc_ro[nb]);
+                }
+                // ---- denominator of row iw: column 64 of both products (lane g = 0, r = 0)
+                float den_call = acc_av[NB][0] + pin * (sK0[p] + acc_ro[NB][0]);
+                den_call = __shfl(den_call, c16, kWave);
+                float den;
+                if (dense) {
+                    // incoming K state, decayed to this chunk, read out on the VALU
+                    float ki = 0.f;
+#pragma unroll
+                    for (int ks = 0; ks < 4; ++ks) {
+                        float qf[8];
+                        unpack8(__builtin_bit_cast(u32x4, fq[ks].h), qf);
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) ki += qf[t] * sKi[32 * ks + 8 * g + t];
+                    }
+                    ki += __shfl_xor(ki, 16, kWave);
+                    ki += __shfl_xor(ki, 32, kWave);
+                    const float dc = static_cast<float>(pow(static_cast<double>(lam), 64.0 * c));
+                    den = fmaxf(fmaxf(den_call, a.eps) + pin * dc * (sKi0 + ki), a.eps);
+                } else {
+                    den = fmaxf(den_call, a.eps);
+                }
+                const float inv = __builtin_amdgcn_rcpf(den);  // 1 ulp
+                // ---- y[iw][16nb + 4g .. +4] straight from the accumulators
+                const int t = c * kC + iw;
+                if (t < a.L) {
+                    const int64_t yo = b * a.y_sb + h * a.y_sh + t * a.y_sl + 4 * g;
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb) {
+                        const f32x4 s0 = *reinterpret_cast<const f32x4 *>(&sS0[p][16 * nb + 4 * g]);
+                        f32x4 yv;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) yv[r] = (acc_av[nb][r] + pin * (s0[r] + acc_ro[nb][r])) * inv;
+                        const int64_t o = yo + 16 * nb;
+                        if (a.dt_y == PRIME_BF16) {
+                            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + o) =
+                                uint2{pack2(yv[0], yv[1]), pack2(yv[2], yv[3])};
+                        } else if (a.dt_y == PRIME_F32) {
+                            *reinterpret_cast<f32x4 *>(static_cast<float *>(a.y) + o) = yv;
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) store_elem(a.y, o + r, a.dt_y, yv[r]);
+                        }
+                    }
+                }
+            }
+        } else {
+            // ---- state update: st = l^n st + [k; k*k/2]^T [w v | w];  S0 on the ones row
+            const float ln = sPw[nvalid];
+#pragma unroll
+            for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+                for (int nb = 0; nb < NBX; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) st[fi][nb][r] *= ln;
+            s0t[0] *= ln;
+            k0 = ln * k0 + sPs[nvalid];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                // register t of both operands <-> token 32ks + 16(t/4) + 4g + t%4
+                const int j0 = 32 * ks + 4 * g + tr_r;
+                Opnd<false> ak[2], vop[NBX];
+#pragma unroll
+                for (int fi = 0; fi < 2; ++fi) {
+                    const uint16_t *p0 = &sKf[p][j0][16 * (2 * u + fi) + tr_c];
+                    ak[fi] = tr_op<false>(p0, p0 + 16 * kPW, 0);
+                }
+#pragma unroll
+                for (int nb = 0; nb < NBX; ++nb) {
+                    const uint16_t *p0 = &sVw[p][j0][16 * nb + tr_c];
+                    vop[nb] = tr_op<false>(p0, p0 + 16 * kPV8, 0);
+                }
+#pragma unroll
+                for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+                    for (int nb = 0; nb < NBX; ++nb) st[fi][nb] = mma<false>(ak[fi], vop[nb], st[fi][nb]);
+                // value block u of [w v] on the ones row (a wave-uniform switch, so
+                // that the operand is selected without a register-indexed access)
+                switch (u) {
+                    case 0: s0t = mfma(ones, vop[0].h, s0t); break;
+                    case 1: s0t = mfma(ones, vop[1].h, s0t); break;
+                    case 2: s0t = mfma(ones, vop[2].h, s0t); break;
+                    default: s0t = mfma(ones, vop[3].h, s0t); break;
+                }
+            }
+            const bool more = c + 1 < c_end;
+            if constexpr (STATE_ONLY) __syncthreads();  // every wave has read the single tile buffer
+            if (more) store_tiles(c + 1, xq);
+            load_tiles<STATE_ONLY>(T, a, qp, kp, vp, c + 2, ra);
+            if (more) publish_state(xq);
+        }
+        __syncthreads();
+    }
+
+    // ---- segment / final state (decays used the valid counts: no pad correction)
+    if (!is_u) return;
+    float *o_s1, *o_s2, *o_s0, *o_k1, *o_k2, *o_k0;
+    size_t off1, off0, offk0;
+    if (STATE_ONLY) {
+        o_s1 = wslot + kWsS1; o_s2 = wslot + kWsS2; o_s0 = wslot + kWsS0;
+        o_k1 = wslot + kWsK1; o_k2 = wslot + kWsK2; o_k0 = wslot + kWsK0;
+        off1 = 0; off0 = 0; offk0 = 0;
+    } else {
+        if (seg != a.G - 1 || a.s1o == nullptr) return;
+        o_s1 = a.s1o; o_s2 = a.s2o; o_s0 = a.s0o; o_k1 = a.k1o; o_k2 = a.k2o; o_k0 = a.k0o;
+        off1 = so1; off0 = so0; offk0 = seq;
+    }
+    // dense clamp: the incoming K state decays separately (l^L over the call)
+    const float linit = dense ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(a.L))) : 0.f;
+#pragma unroll
+    for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int f = 16 * (2 * u + fi) + 4 * g + r;
+            const int fr = f & (kD - 1);
+            const float sc = f < kD ? 1.0f : 2.0f;  // rows 64.. hold S2/2 and K2/2
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                (f < kD ? o_s1 : o_s2)[off1 + fr * kD + 16 * nb + c16] = sc * st[fi][nb][r];
+            if (c16 == 0) {
+                float kv = st[fi][NB][r];
+                if constexpr (!STATE_ONLY) {
+                    if (dense) kv += linit * sKi[f];
+                }
+                (f < kD ? o_k1 : o_k2)[off0 + fr] = sc * kv;
+            }
+        }
+    if (g == 0) o_s0[off0 + 16 * u + c16] = s0t[0];
+    if (u == 0 && lane == 0) o_k0[offk0] = k0 + (STATE_ONLY ? 0.f : linit * sKi0);
+}
+
+void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream) {
+    if (state_only) hipLaunchKernelGGL(prefill_bf16_kernel<true>, dim3(grid), dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(prefill_bf16_kernel<false>, dim3(grid), dim3(512), 0, stream, a);
+}
+
+}  // namespace prime

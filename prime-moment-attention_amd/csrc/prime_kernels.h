@@ -49,6 +49,10 @@ hipError_t launch_prefill(PrefillArgs a, hipStream_t stream);
 // segments per sequence for the launch plan, given the workspace the caller has
 void plan_segments(int S, int L, bool dense_clamp, size_t ws_bytes, int *G, int *cps);
 
+// bf16-input prefill kernels (prefill_bf16.hip): the state-only segment pass
+// (256 threads) or the fused chunk loop (512 threads) over `grid` workgroups.
+void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream);
+
 // Launch timer hooks (the C-ABI prime_timer_* calls); no-ops while disabled.
 void timer_begin(int kernel, hipStream_t stream);
 void timer_end(int kernel, hipStream_t stream);
