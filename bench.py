@@ -16,6 +16,8 @@ The same JSON line carries
   decode        the fused decode step at B=512 sequences x 12 layers x 12 heads
                 (one launch per layer, states pre-filled by 1024 tokens) and at
                 B=256, tok/s and its own roofline;
+  model         the PRIME-125M-shaped LM end to end: prefill tok/s (B=32 x
+                2048) and greedy decode tok/s at B=32 and B=256 (HIP-graph step);
   cpu_baseline  the reference's C99 engine (built from its sources into
                 oracle/_ref by oracle/Makefile) timed single-threaded on a
                 bounded sample of the same workload, plus the PyTorch-CPU and
@@ -51,6 +53,7 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode legs")
+    ap.add_argument("--no-model", action="store_true", help="skip the PRIME-125M model leg")
     ap.add_argument("--cpu-budget", type=float, default=8.0, help="seconds per CPU leg (approximate)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device copy 3 times (the reference kernel for "
@@ -189,6 +192,56 @@ def bench_decode(args, lib, torch, dev, B, layers=12, H=12, pool=16, prefill_tok
                      "bytes_per_launch": per_launch, "avg_launch_us": kms * 1e3, "launches": n,
                      "traffic": None},
     }
+
+
+# ----------------------------------------------------------------- model
+def bench_model(args, torch, dev):
+    """PRIME-125M-shaped causal LM (12 layers, d_model 768, 12 x 64 heads,
+    GELU MLP 3072, tied 50304 vocab, bf16 weights, fp32 states, LayerNorm
+    QK-norm), random init.  Prefill B=32 x 2048 random ids (states + last-token
+    logits + argmax); then greedy decode with the HIP-graph step at B=32 and at
+    B=256 (prompt of 128 tokens: decode cost does not depend on position)."""
+    from prime_moment_attention import GreedyDecoder, PrimeForCausalLM, prime_125m_config
+    torch.manual_seed(args.seed)
+    model = PrimeForCausalLM(prime_125m_config("gelu")).to(device=dev, dtype=torch.bfloat16).eval()
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 7)
+    V = model.config.vocab_size
+    out = {"workload": "PRIME-125M-shaped LM: 12 layers, d_model 768, 12 heads x 64, GELU MLP 3072, "
+                       "vocab 50304 tied, bf16 weights, fp32 states, LayerNorm QK-norm, random init; "
+                       "prefill B=32 x 2048 random ids, greedy decode 256 steps (HIP graph step)",
+           "params": sum(p.numel() for p in model.parameters())}
+
+    def timed_once(fn):
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        r = fn()
+        e.record()
+        torch.cuda.synchronize()
+        return s.elapsed_time(e), r
+
+    B, L = 32, 2048
+    ids = torch.randint(0, V, (B, L), device=dev, generator=gen)
+    dec = GreedyDecoder(model, use_graph=True)
+    for _ in range(2):
+        dec.prefill(ids)
+    reps = 3
+    ms = sum(timed_once(lambda: dec.prefill(ids))[0] for _ in range(reps)) / reps
+    out["prefill"] = {"B": B, "L": L, "tok_s": B * L / (ms * 1e-3), "ms": ms}
+    for Bd, Lp in ((32, None), (256, 128)):
+        if Lp is not None:
+            dec = GreedyDecoder(model, use_graph=True)
+            dec.prefill(torch.randint(0, V, (Bd, Lp), device=dev, generator=gen))
+        for _ in range(4):
+            dec.step()  # first step captures the graph
+        steps = 256
+        ms, _ = timed_once(lambda: [dec.step() for _ in range(steps)])
+        out[f"decode_B{Bd}"] = {"B": Bd, "steps": steps, "tok_s": Bd * steps / (ms * 1e-3),
+                                "ms_per_step": ms / steps,
+                                "state_bytes": 12 * Bd * 12 * STATE_BYTES}
+    del model, dec
+    torch.cuda.empty_cache()
+    return out
 
 
 # ----------------------------------------------------------------- CPU legs
@@ -369,6 +422,8 @@ def main():
             if t is not None:
                 d["roofline"]["traffic"] = t.get("bytes_per_launch")
         rec["decode"] = {"B=256": d256, "B=512": d512}
+    if not args.no_model:
+        rec["model"] = bench_model(args, torch, dev)
     if not args.no_cpu:
         try:
             legs = cpu_prefill_legs(args)

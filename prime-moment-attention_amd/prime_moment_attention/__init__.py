@@ -2,12 +2,15 @@
 
 Drop-in host API mirroring the reference package ``prime_moment_attention``
 (PrimeMomentAttention, chunked_prime_ssd_core, ChunkedPrimeSSD,
-PrimeMomentCache) over the HIP library libprime_mi355x.so.
+PrimeMomentCache, PrimeConfig / PrimeForCausalLM) over the HIP library
+libprime_mi355x.so.
 """
 from .attention import PrimeMomentAttention
 from .cache import PrimeMomentCache
 from .chunked_ssd import ChunkedPrimeSSD, chunked_prime_ssd_core
+from .model import GreedyDecoder, PrimeConfig, PrimeForCausalLM, prime_125m_config
 
 __version__ = "0.1.0"
 
-__all__ = ["PrimeMomentAttention", "PrimeMomentCache", "ChunkedPrimeSSD", "chunked_prime_ssd_core"]
+__all__ = ["PrimeMomentAttention", "PrimeMomentCache", "ChunkedPrimeSSD", "chunked_prime_ssd_core",
+           "PrimeConfig", "PrimeForCausalLM", "GreedyDecoder", "prime_125m_config"]

@@ -30,6 +30,12 @@ from . import _lib
 from .chunked_ssd import prime_prefill
 
 
+def _same_storage(a, b) -> bool:
+    """True when the validated state views alias the caller's tensors (so an
+    in-place update reaches them)."""
+    return all(x.data_ptr() == y.data_ptr() for x, y in zip(a, b))
+
+
 class PrimeMomentAttention(nn.Module):
     def __init__(
         self,
@@ -94,7 +100,7 @@ class PrimeMomentAttention(nn.Module):
         if L == 1:
             dec = _lib.decay_tensor(self.decay, H, dev)
             st_in = _lib.as_state(state, B, H, D, dev) if state is not None else None
-            if self.inplace_state and st_in is not None and all(a is b for a, b in zip(st_in, state)):
+            if self.inplace_state and st_in is not None and _same_storage(st_in, state):
                 st_out = st_in
             else:
                 st_out = _lib.new_state(B, H, D, dev)
@@ -107,7 +113,7 @@ class PrimeMomentAttention(nn.Module):
             st_out = None
             if return_state and self.inplace_state and state is not None:
                 st_in = _lib.as_state(state, B, H, D, dev)
-                if all(a is b for a, b in zip(st_in, state)):
+                if _same_storage(st_in, state):
                     st_out = st_in
             y, next_state = prime_prefill(q, k, v, state=state, decay=self.decay, eps=self.eps,
                                           chunk_size=self.chunk_size, return_state=return_state,

@@ -1,0 +1,289 @@
+"""PrimeForCausalLM: drop-in for the reference's model.py, on the HIP kernels.
+
+Same configuration fields, module tree and parameter names as the reference
+(model.py:20-149), so its state dicts load unchanged; the forward contract
+``forward(input_ids, labels=None, states=None, return_states=False) -> dict``
+and ``generate`` follow model.py:163-242.  Every PRIME attention layer runs the
+library's decode step or chunked prefill (PrimeMomentAttention); projections,
+norms and the MLP are torch layers (library GEMMs).
+
+Additions for serving, none of which changes results:
+  * ``PrimeConfig.mlp_type = "gelu"`` selects an up/GELU/down MLP of width
+    ``intermediate_size`` (the PRIME-125M benchmark shape); the default
+    "swiglu" is the reference's PrimeMLP (model.py:59-68).
+  * ``forward(..., logits_to_keep=n)`` computes logits for the last n
+    positions only (generation needs one).
+  * ``GreedyDecoder`` runs greedy decoding with per-layer states updated in
+    place and the whole one-token step (embedding, 12 layers, final norm,
+    lm_head, argmax) captured in one HIP graph, replayed per token.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Any, Dict, List, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from .attention import PrimeMomentAttention
+
+
+@dataclass
+class PrimeConfig:
+    """model.py:20-44, plus ``mlp_type``."""
+    vocab_size: int = 32000
+    hidden_size: int = 512
+    num_layers: int = 6
+    num_heads: int = 8
+    head_dim: int = 64
+    num_kv_heads: Optional[int] = None
+    intermediate_size: Optional[int] = None
+    decay: float = 0.9995
+    use_qk_norm: bool = True
+    rms_norm_eps: float = 1e-6
+    eps: float = 1.0
+    tie_word_embeddings: bool = True
+    initializer_range: float = 0.02
+    use_selective: bool = False
+    min_tau: float = 2.0
+    max_tau: float = 2000.0
+    mlp_type: str = "swiglu"
+
+    def __post_init__(self):
+        if self.num_kv_heads is None:
+            self.num_kv_heads = self.num_heads
+        if self.intermediate_size is None:
+            self.intermediate_size = int(2 * (4 * self.hidden_size) / 3)
+        if self.mlp_type not in ("swiglu", "gelu"):
+            raise ValueError(f"mlp_type must be 'swiglu' or 'gelu', not {self.mlp_type!r}")
+
+
+def prime_125m_config(mlp_type: str = "gelu", vocab_size: int = 50304) -> PrimeConfig:
+    """The PRIME-125M benchmark shape: 12 layers, d_model 768, 12 x 64 heads,
+    MLP 3072 (GELU) or the reference's SwiGLU width, tied 50304-token vocab."""
+    return PrimeConfig(vocab_size=vocab_size, hidden_size=768, num_layers=12, num_heads=12, head_dim=64,
+                       intermediate_size=3072 if mlp_type == "gelu" else None, mlp_type=mlp_type)
+
+
+class RMSNorm(nn.Module):
+    """model.py:47-56."""
+
+    def __init__(self, dim: int, eps: float = 1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        variance = x.pow(2).mean(-1, keepdim=True)
+        return x * torch.rsqrt(variance + self.eps) * self.weight
+
+
+class PrimeMLP(nn.Module):
+    """SwiGLU feed-forward, model.py:59-68."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int):
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.up_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class PrimeGeluMLP(nn.Module):
+    """up -> GELU -> down feed-forward (the PRIME-125M benchmark's MLP)."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int):
+        super().__init__()
+        self.up_proj = nn.Linear(hidden_size, intermediate_size, bias=False)
+        self.down_proj = nn.Linear(intermediate_size, hidden_size, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(F.gelu(self.up_proj(x)))
+
+
+class PrimeBlock(nn.Module):
+    """Pre-norm block, model.py:71-118: x + Attn(RMSNorm x); x + MLP(RMSNorm x)."""
+
+    def __init__(self, config: PrimeConfig):
+        super().__init__()
+        if config.use_selective:
+            raise NotImplementedError("selective PRIME attention (selective.py) is not built in this library")
+        self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.self_attn = PrimeMomentAttention(
+            hidden_size=config.hidden_size, num_heads=config.num_heads, head_dim=config.head_dim,
+            num_kv_heads=config.num_kv_heads, decay=config.decay, use_qk_norm=config.use_qk_norm,
+            eps=config.eps)
+        self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        mlp = PrimeGeluMLP if config.mlp_type == "gelu" else PrimeMLP
+        self.mlp = mlp(config.hidden_size, config.intermediate_size)
+
+    def forward(self, hidden_states, state=None, return_state=False):
+        residual = hidden_states
+        h, next_state = self.self_attn(self.input_layernorm(hidden_states), state=state,
+                                       return_state=return_state)
+        hidden_states = residual + h
+        hidden_states = hidden_states + self.mlp(self.post_attention_layernorm(hidden_states))
+        return hidden_states, next_state
+
+
+class PrimeForCausalLM(nn.Module):
+    """model.py:121-242 on the HIP attention kernels."""
+
+    def __init__(self, config: PrimeConfig):
+        super().__init__()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList([PrimeBlock(config) for _ in range(config.num_layers)])
+        self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+        if config.tie_word_embeddings:
+            self.lm_head.weight = self.embed_tokens.weight
+        self.apply(self._init_weights)
+        # output projections re-drawn with std / sqrt(2 * layers) (model.py:141-147)
+        scale = config.initializer_range / math.sqrt(2 * config.num_layers)
+        for layer in self.layers:
+            layer.self_attn.o_proj.weight.data.normal_(mean=0.0, std=scale)
+            layer.mlp.down_proj.weight.data.normal_(mean=0.0, std=scale)
+
+    def _init_weights(self, module: nn.Module):
+        if isinstance(module, (nn.Linear, nn.Embedding)):
+            nn.init.normal_(module.weight, mean=0.0, std=self.config.initializer_range)
+            if getattr(module, "bias", None) is not None:
+                nn.init.zeros_(module.bias)
+
+    def get_input_embeddings(self) -> nn.Embedding:
+        return self.embed_tokens
+
+    def set_input_embeddings(self, value: nn.Embedding):
+        self.embed_tokens = value
+
+    def forward(self, input_ids: torch.Tensor, labels: Optional[torch.Tensor] = None,
+                states: Optional[List[Tuple[torch.Tensor, ...]]] = None, return_states: bool = False,
+                logits_to_keep: int = 0) -> Dict[str, Any]:
+        hidden_states = self.embed_tokens(input_ids)
+        next_states = [] if return_states else None
+        for i, layer in enumerate(self.layers):
+            hidden_states, ns = layer(hidden_states, state=states[i] if states is not None else None,
+                                      return_state=return_states)
+            if return_states:
+                next_states.append(ns)
+        if logits_to_keep:
+            hidden_states = hidden_states[:, -logits_to_keep:]
+        logits = self.lm_head(self.norm(hidden_states))
+        loss = None
+        if labels is not None:
+            shift_logits = logits[..., :-1, :].contiguous().to(torch.float32)
+            loss = F.cross_entropy(shift_logits.view(-1, self.config.vocab_size),
+                                   labels[..., 1:].contiguous().view(-1), ignore_index=-100)
+        return {"loss": loss, "logits": logits, "states": next_states}
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int = 50, temperature: float = 1.0,
+                 top_k: int = 50, eos_token_id: Optional[int] = None) -> torch.Tensor:
+        """model.py:202-242: prefill, then one recurrent step per token."""
+        self.eval()
+        out = self.forward(input_ids, return_states=True, logits_to_keep=1)
+        states = out["states"]
+        next_logits = out["logits"][:, -1, :]
+        generated = input_ids
+        for _ in range(max_new_tokens):
+            next_logits = torch.nan_to_num(next_logits, nan=0.0, posinf=50.0, neginf=-50.0)
+            if temperature > 0.0:
+                logits = next_logits / max(temperature, 1e-4)
+                if top_k > 0:
+                    v, _ = torch.topk(logits, min(top_k, logits.size(-1)))
+                    logits[logits < v[:, [-1]]] = -float("Inf")
+                probs = torch.nan_to_num(F.softmax(logits, dim=-1), nan=1.0 / self.config.vocab_size)
+                next_token = torch.multinomial(probs, num_samples=1)
+            else:
+                next_token = torch.argmax(next_logits, dim=-1, keepdim=True)
+            generated = torch.cat([generated, next_token], dim=-1)
+            if eos_token_id is not None and (next_token == eos_token_id).all():
+                break
+            step = self.forward(next_token, states=states, return_states=True)
+            states = step["states"]
+            next_logits = step["logits"][:, -1, :]
+        return generated
+
+
+class GreedyDecoder:
+    """Greedy decoding with in-place states and a HIP-graph-captured step.
+
+    ``prefill(input_ids)`` runs the prompt through the chunked kernels and
+    keeps one state 6-tuple per layer; ``step()`` appends one token per
+    sequence: embedding -> layers (decode kernel, state in place) -> norm ->
+    lm_head -> argmax, the same computation as ``generate`` at temperature 0
+    (model.py:230-231).  With ``use_graph`` the step is captured once after
+    the prefill and replayed; every buffer it touches is fixed.
+    """
+
+    def __init__(self, model: PrimeForCausalLM, use_graph: bool = True):
+        self.model = model.eval()
+        self.use_graph = use_graph
+        self.graph = None
+        self.states = None
+        for layer in model.layers:
+            layer.self_attn.inplace_state = True
+
+    @torch.no_grad()
+    def prefill(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """Run the prompt; returns the first generated token [B, 1]."""
+        m = self.model
+        out = m.forward(input_ids, return_states=True, logits_to_keep=1)
+        self.states = [tuple(s) for s in out["states"]]
+        self.token = torch.argmax(out["logits"][:, -1, :], dim=-1, keepdim=True)
+        self.graph = None
+        return self.token
+
+    @torch.no_grad()
+    def _step_eager(self) -> torch.Tensor:
+        m = self.model
+        h = m.embed_tokens(self.token)
+        for layer, st in zip(m.layers, self.states):
+            h, _ = layer(h, state=st, return_state=True)  # decode kernel updates st in place
+        logits = m.lm_head(m.norm(h))[:, -1, :]
+        return torch.argmax(logits, dim=-1, keepdim=True)
+
+    @torch.no_grad()
+    def step(self) -> torch.Tensor:
+        """One decode step for every sequence; returns the new tokens [B, 1]."""
+        if not self.use_graph:
+            self.token = self._step_eager()
+            return self.token
+        if self.graph is None:
+            self._capture()
+        self.graph.replay()
+        return self.token
+
+    def _capture(self):
+        # warm up on a side stream (allocator pools, cached decay tensors), on a
+        # copy of the states so that the real states advance only by replays
+        saved = [tuple(t.clone() for t in st) for st in self.states]
+        tok = self.token.clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self._step_eager()
+        torch.cuda.current_stream().wait_stream(s)
+        for st, sv in zip(self.states, saved):
+            for t, x in zip(st, sv):
+                t.copy_(x)
+        self.token.copy_(tok)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            nxt = self._step_eager()
+            self.token.copy_(nxt)
+        # capture does not execute: states and token are as after the prefill
+        self.graph = g
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int) -> torch.Tensor:
+        toks = [self.prefill(input_ids).clone()]
+        for _ in range(max_new_tokens - 1):
+            toks.append(self.step().clone())
+        return torch.cat([input_ids] + toks, dim=-1)

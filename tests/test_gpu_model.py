@@ -1,0 +1,118 @@
+"""GPU tests of the PRIME-125M-shaped causal LM host path (model.py:20-242 of the
+reference) on the HIP kernels: logits against an fp32 CPU composition of the
+same weights (textbook layers + the fp32 PyTorch-CPU restatement of the PRIME
+core from oracle/torch_cpu.py), prefill/decode continuity, and the HIP-graph
+greedy decoder against eager generation."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import torch_cpu as TC
+from prime_moment_attention import GreedyDecoder, PrimeConfig, PrimeForCausalLM
+
+from gpu_util import dev
+
+pytestmark = pytest.mark.gpu
+
+TOL_LOGITS = 3e-2  # max|d| / max|ref| for bf16 weights/activations vs the fp32 composition
+
+
+def _small(mlp="swiglu", layers=2, heads=2, decay=0.995):
+    return PrimeConfig(vocab_size=384, hidden_size=128, num_layers=layers, num_heads=heads, head_dim=64,
+                       decay=decay, mlp_type=mlp, intermediate_size=256 if mlp == "gelu" else None)
+
+
+def _model(cfg, seed=0):
+    torch.manual_seed(seed)
+    return PrimeForCausalLM(cfg).to(device=dev(), dtype=torch.bfloat16).eval()
+
+
+def _ref_forward(model, ids, L_threshold=512):
+    """fp32 CPU forward of the same weights: model.py:163-199 with the attention
+    of attention.py:83-210 (dense below the threshold = chunked without state)."""
+    cfg = model.config
+    W = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    x = W["embed_tokens.weight"][ids.cpu()]
+    B, L = ids.shape
+    H, D = cfg.num_heads, cfg.head_dim
+
+    def rms(x, w):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + cfg.rms_norm_eps) * w
+
+    for i in range(cfg.num_layers):
+        p = f"layers.{i}."
+        hN = rms(x, W[p + "input_layernorm.weight"])
+        q = (hN @ W[p + "self_attn.q_proj.weight"].T).view(B, L, H, D).transpose(1, 2)
+        k = (hN @ W[p + "self_attn.k_proj.weight"].T).view(B, L, H, D).transpose(1, 2)
+        v = (hN @ W[p + "self_attn.v_proj.weight"].T).view(B, L, H, D).transpose(1, 2)
+        if cfg.use_qk_norm:
+            q = F.layer_norm(q, (D,), W[p + "self_attn.q_norm.weight"], W[p + "self_attn.q_norm.bias"])
+            k = F.layer_norm(k, (D,), W[p + "self_attn.k_norm.weight"], W[p + "self_attn.k_norm.bias"])
+        q = q / 8.0
+        y, _ = TC.chunked_core(q.contiguous(), k.contiguous(), v.contiguous(), cfg.decay, eps=cfg.eps)
+        y = y.transpose(1, 2).reshape(B, L, H * D)
+        x = x + y @ W[p + "self_attn.o_proj.weight"].T
+        hN = rms(x, W[p + "post_attention_layernorm.weight"])
+        if cfg.mlp_type == "gelu":
+            m = F.gelu(hN @ W[p + "mlp.up_proj.weight"].T) @ W[p + "mlp.down_proj.weight"].T
+        else:
+            m = (F.silu(hN @ W[p + "mlp.gate_proj.weight"].T) * (hN @ W[p + "mlp.up_proj.weight"].T)) \
+                @ W[p + "mlp.down_proj.weight"].T
+        x = x + m
+    return rms(x, W["norm.weight"]) @ W["embed_tokens.weight"].T
+
+
+def _rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return ((a - b).abs().max() / b.abs().max()).item()
+
+
+@pytest.mark.parametrize("mlp,L", [("swiglu", 70), ("gelu", 600)])
+def test_model_logits_match_fp32_composition(mlp, L):
+    """Dense branch (L <= 512) and chunked branch (L > 512)."""
+    model = _model(_small(mlp))
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, model.config.vocab_size, (2, L), generator=g)
+    with torch.no_grad():
+        out = model(ids.to(dev()))["logits"]
+    ref = _ref_forward(model, ids)
+    assert torch.isfinite(out).all()
+    assert _rel(out, ref) < TOL_LOGITS, _rel(out, ref)
+
+
+def test_prefill_then_steps_equal_longer_prefill():
+    """States carried by the decode kernel continue the prefill exactly (up to
+    bf16 rounding): logits of step-decoded tokens == logits of one long prefill."""
+    model = _model(_small())
+    ids = torch.randint(0, 384, (2, 45), generator=torch.Generator().manual_seed(2)).to(dev())
+    with torch.no_grad():
+        full = model(ids)["logits"]
+        out = model(ids[:, :40], return_states=True)
+        states = out["states"]
+        for t in range(40, 45):
+            step = model(ids[:, t:t + 1], states=states, return_states=True)
+            states = step["states"]
+            assert _rel(step["logits"][:, -1], full[:, t]) < TOL_LOGITS
+
+
+def test_greedy_decoder_graph_equals_eager_generate():
+    """Greedy tokens: HIP-graph decoder == eager decoder == generate(temperature=0);
+    graph replays are interleaved with eager work and synchronisations, and the
+    states stay in place."""
+    model = _model(_small(layers=2, heads=2, decay=0.99))
+    ids = torch.randint(0, 384, (3, 30), generator=torch.Generator().manual_seed(3)).to(dev())
+    n = 12
+    ref = model.generate(ids, max_new_tokens=n, temperature=0.0)
+    eager = GreedyDecoder(model, use_graph=False).generate(ids, n)
+    dec = GreedyDecoder(model, use_graph=True)
+    toks = [dec.prefill(ids).clone()]
+    ptrs = [t.data_ptr() for st in dec.states for t in st]
+    for i in range(n - 1):
+        toks.append(dec.step().clone())
+        torch.cuda.synchronize()
+        _ = torch.randn(1000, device=dev()).sum().item()  # unrelated eager work between replays
+    graph = torch.cat([ids] + toks, dim=-1)
+    assert [t.data_ptr() for st in dec.states for t in st] == ptrs
+    assert torch.equal(eager, ref), (eager, ref)
+    assert torch.equal(graph, ref), (graph, ref)
