@@ -114,6 +114,57 @@ int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k,
 size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags);
 
 /*
+ * Chunked gated delta-rule PRIME prefill.  Replaces the L > 1 branch of
+ * ChunkedGatedDeltaPrimeAttention.forward (chunked_delta_prime.py:177-283):
+ * per 64-token chunk, u = v - (phi e^cum) S^T, the unit-triangular solve
+ * T E = u, y = tril(Psi Phi^T * Lambda) (beta E) + (psi e^cum) S^T,
+ * S <- e^cum_end S + (beta E)^T (phi e^(cum_end - cum)), then the Lyapunov
+ * clamp S <- S min(1, bound / (|S|_F + 1e-6)).
+ *   q, k, v   : [B, H(q) / H_kv, L, D] after the module's projections, QK-norm
+ *               and q * 1/sqrt(D) (:107-126); the kernels form psi = [q, q*q/sqrt2]
+ *               and phi = [k/max(|k|,feat_eps), (k*k)/max(|k*k|,feat_eps)/sqrt2]
+ *               (:73-87).  BF16 or F32 (all three alike).
+ *   beta      : fp32 [B, H, L] contiguous, 0.5 mean sigmoid(write) (:134)
+ *   alpha     : fp32 [B, H, L] contiguous, decay (1 - 0.5 mean sigmoid(erase)) (:137)
+ *   decay_pad : alpha of the zero tokens padding the last chunk (:189, the
+ *               module's decay; the final state keeps that padding's decay)
+ *   bound     : Lyapunov bound; <= 0 disables the clamp (:266-270)
+ *   chunk     : must be 64 (the clamp is applied per chunk, so the result
+ *               depends on the chunk size)
+ *   state_in  : fp32 [B, H, D, 2D] or NULL (zero); state_out likewise or NULL;
+ *               they may be the same buffer
+ *   y         : [B, H, L, D], F32 / BF16 / F16
+ *   workspace : at least prime_delta_prefill_workspace_size(B, H, L, 0) bytes
+ *               (16-byte aligned).  A smaller workspace (at least
+ *               prime_delta_prefill_workspace_size(B, H, 64, 0)) makes the call
+ *               process the sequence in more, shorter windows; results agree.
+ */
+int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k,
+                        const prime_tensor_t *v, const float *beta, const float *alpha,
+                        int B, int H, int H_kv, int L, int D, int chunk, float decay_pad,
+                        float feat_eps, float bound, const float *state_in,
+                        const prime_tensor_t *y, float *state_out, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/* Workspace bytes of prime_delta_prefill for this shape (flags: 0). */
+size_t prime_delta_prefill_workspace_size(int B, int H, int L, unsigned flags);
+
+/*
+ * One delta-rule PRIME decode step.  Replaces the L == 1 branch of
+ * ChunkedGatedDeltaPrimeAttention.forward (chunked_delta_prime.py:140-176),
+ * which predicts with the undecayed state: v_hat = S phi, S <- alpha S +
+ * beta (v - v_hat) phi^T, Lyapunov clamp, y = S psi.
+ *   q, k, v : [B, H(q) / H_kv, D] (stride_l ignored); beta, alpha: fp32 [B, H]
+ *   state_in: fp32 [B, H, D, 2D] or NULL; state_out may equal state_in
+ *   y       : [B, H, D]
+ */
+int prime_delta_decode_step(const prime_tensor_t *q, const prime_tensor_t *k,
+                            const prime_tensor_t *v, const float *beta, const float *alpha,
+                            int B, int H, int H_kv, int D, float feat_eps, float bound,
+                            const float *state_in, float *state_out, const prime_tensor_t *y,
+                            void *stream);
+
+/*
  * Launch timer.  No counterpart in the reference: it serves benchmark harnesses
  * that need the device time of ONE kernel of a multi-kernel call.
  * prime_timer_enable(mask) (process-wide; bit (1 << PRIME_KERNEL_*) selects a
@@ -127,7 +178,10 @@ size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags)
 #define PRIME_KERNEL_PREFILL_SEGMENTS 1 /* per-segment state contributions */
 #define PRIME_KERNEL_SEGMENT_SCAN     2 /* exclusive scan over segments */
 #define PRIME_KERNEL_DECODE           3 /* fused decode step */
-#define PRIME_KERNEL_COUNT            4
+#define PRIME_KERNEL_DELTA_PREP       4 /* delta rule: per-chunk solve and transfer matrices */
+#define PRIME_KERNEL_DELTA_SCAN       5 /* delta rule: sequential scan over chunks */
+#define PRIME_KERNEL_DELTA_STEP       6 /* delta rule: decode step */
+#define PRIME_KERNEL_COUNT            7
 
 int prime_timer_enable(unsigned mask);
 int prime_timer_reset(void);

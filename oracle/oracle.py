@@ -57,6 +57,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_delta_features.argtypes = [i, i, i, _dp, _dp, d, _dp, _dp]
         L.oracle_delta_chunked.argtypes = [i, i, i, i, _dp, _dp, _dp, _dp, _dp, d, d, i, _dp, _dp]
         L.oracle_delta_tokenwise.argtypes = [i, i, i, _dp, _dp, _dp, _dp, _dp, i, _dp, _dp]
+        L.oracle_delta_step.argtypes = [i, i, _dp, _dp, _dp, _dp, _dp, d, _dp, _dp]
         f = ctypes.c_float
         L.baseline_decode_step.argtypes = [i, i, i, _fp, _fp, _fp, _fp, f] + [_fp] * 7 + [i]
         L.baseline_prefill.argtypes = [i, i, i, i, _fp, _fp, _fp, _fp, f] + [_fp] * 7 + [i]
@@ -159,6 +160,18 @@ def delta_tokenwise(psi, phi, v, beta, alpha, state=None):
     y = np.zeros_like(v)
     lib().oracle_delta_tokenwise(BH, L, D, _p(psi), _p(phi), _p(v), _p(beta), _p(alpha),
                                  0 if state is None else 1, _p(S), _p(y))
+    return y, S
+
+
+def delta_step(psi, phi, v, beta, alpha, bound=25.0, state=None):
+    """Delta-PRIME L == 1 step (chunked_delta_prime.py:140-176): psi/phi [BH, 2D],
+    v [BH, D], beta/alpha [BH]; returns (y [BH, D], S [BH, D, 2D])."""
+    psi, phi, v = _c64(psi), _c64(phi), _c64(v)
+    beta, alpha = _c64(beta), _c64(alpha)
+    BH, D = v.shape
+    S = np.zeros((BH, D, 2 * D)) if state is None else _c64(state).reshape(BH, D, 2 * D).copy()
+    y = np.zeros_like(v)
+    lib().oracle_delta_step(BH, D, _p(psi), _p(phi), _p(v), _p(beta), _p(alpha), float(bound), _p(S), _p(y))
     return y, S
 
 

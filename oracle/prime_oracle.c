@@ -465,3 +465,44 @@ void oracle_delta_tokenwise(int BH, int L, int D, const double *psi,
     }
     free(pred);
 }
+
+/* ------------------------------------------------------------------------- */
+/* Delta-PRIME single-token step, the L == 1 branch of                        */
+/* ChunkedGatedDeltaPrimeAttention.forward (chunked_delta_prime.py:140-176):  */
+/* prediction with the state as it is (:155-157, no decay first), update      */
+/* S = alpha S + (beta err) phi^T (:159-161, alpha not clamped), Lyapunov     */
+/* clamp (:163-167), readout y = S psi (:170).  One token per (b, h).          */
+/* ------------------------------------------------------------------------- */
+void oracle_delta_step(int BH, int D, const double *psi, const double *phi,
+                       const double *v, const double *beta, const double *alpha,
+                       double bound, double *S, double *y)
+{
+    const int P = 2 * D;
+    for (int bh = 0; bh < BH; ++bh) {
+        double *Sb = S + (size_t)bh * D * P;
+        const double *ph = phi + (size_t)bh * P, *ps = psi + (size_t)bh * P;
+        const double *vt = v + (size_t)bh * D;
+        double nrm = 0.0;
+        for (int d = 0; d < D; ++d) {
+            double vh = 0.0;
+            for (int e = 0; e < P; ++e) vh += Sb[IDX2(d, e, P)] * ph[e];
+            const double err = beta[bh] * (vt[d] - vh);
+            for (int e = 0; e < P; ++e) {
+                const double x = alpha[bh] * Sb[IDX2(d, e, P)] + err * ph[e];
+                Sb[IDX2(d, e, P)] = x;
+                nrm += x * x;
+            }
+        }
+        double sc = 1.0;
+        if (bound > 0.0) {
+            sc = bound / (sqrt(nrm) + 1e-6);
+            if (sc > 1.0) sc = 1.0;
+        }
+        for (int a = 0; a < D * P; ++a) Sb[a] *= sc;
+        for (int d = 0; d < D; ++d) {
+            double acc = 0.0;
+            for (int e = 0; e < P; ++e) acc += Sb[IDX2(d, e, P)] * ps[e];
+            y[(size_t)bh * D + d] = acc;
+        }
+    }
+}

@@ -172,6 +172,96 @@ int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, cons
     return check_hip(prime::launch_prefill(a, static_cast<hipStream_t>(stream)), "prefill launch");
 }
 
+size_t prime_delta_prefill_workspace_size(int B, int H, int L, unsigned flags) {
+    (void)flags;
+    if (B <= 0 || H <= 0 || L <= 0) return 0;
+    const int NC = (L + prime::kDeltaChunk - 1) / prime::kDeltaChunk;
+    const int win = NC < prime::kDeltaDefaultWindow ? NC : prime::kDeltaDefaultWindow;
+    const size_t S = static_cast<size_t>(B) * H;
+    return S * prime::kDeltaStateBytes + S * static_cast<size_t>(win) * prime::kDeltaRecBytes;
+}
+
+int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                        const float *beta, const float *alpha, int B, int H, int H_kv, int L, int D,
+                        int chunk, float decay_pad, float feat_eps, float bound, const float *state_in,
+                        const prime_tensor_t *y, float *state_out, void *workspace, size_t workspace_bytes,
+                        void *stream) {
+    g_err[0] = 0;
+    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !beta || !alpha || !workspace)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_delta_prefill: null argument");
+    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d", B, H, H_kv, L);
+    if (chunk != prime::kDeltaChunk)
+        return fail(PRIME_ERR_INVALID_ARG, "chunk %d unsupported: the per-chunk clamp fixes chunk = 64", chunk);
+    if (q->dtype != k->dtype || q->dtype != v->dtype || (q->dtype != PRIME_BF16 && q->dtype != PRIME_F32))
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "q/k/v must share dtype BF16 or F32");
+    if (!valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported y dtype");
+    if (!rows_aligned(y, true))
+        return fail(PRIME_ERR_MISALIGNED, "y rows must start on 16-byte boundaries");
+    if (!aligned16(workspace)) return fail(PRIME_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+    if ((state_in && !aligned16(state_in)) || (state_out && !aligned16(state_out)))
+        return fail(PRIME_ERR_MISALIGNED, "state buffers must be 16-byte aligned");
+    const size_t S = static_cast<size_t>(B) * H;
+    const size_t sbytes = S * prime::kDeltaStateBytes;
+    if (state_in && state_out && state_in != state_out && overlap(state_in, sbytes, state_out, sbytes))
+        return fail(PRIME_ERR_ALIAS, "state_out overlaps state_in (only a fully in-place state is allowed)");
+    if (workspace_bytes < sbytes + S * prime::kDeltaRecBytes)
+        return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes is below the minimum %zu", workspace_bytes,
+                    sbytes + S * prime::kDeltaRecBytes);
+    const int NC = (L + prime::kDeltaChunk - 1) / prime::kDeltaChunk;
+    const size_t cap = (workspace_bytes - sbytes) / (S * prime::kDeltaRecBytes);
+    const int window = static_cast<int>(cap < static_cast<size_t>(NC) ? cap : static_cast<size_t>(NC));
+
+    prime::DeltaArgs a{};
+    a.q = q->data; a.k = k->data; a.v = v->data;
+    a.q_sb = q->stride_b; a.q_sh = q->stride_h; a.q_sl = q->stride_l;
+    a.k_sb = k->stride_b; a.k_sh = k->stride_h; a.k_sl = k->stride_l;
+    a.v_sb = v->stride_b; a.v_sh = v->stride_h; a.v_sl = v->stride_l;
+    a.dt_in = q->dtype;
+    a.B = B; a.H = H; a.group = H / H_kv; a.L = L;
+    a.beta = beta; a.alpha = alpha;
+    a.decay_pad = decay_pad; a.feat_eps = feat_eps; a.bound = bound;
+    a.state_in = state_in; a.state_out = state_out;
+    a.y = y->data; a.dt_y = y->dtype;
+    a.y_sb = y->stride_b; a.y_sh = y->stride_h; a.y_sl = y->stride_l;
+    a.ws_state = static_cast<float *>(workspace);
+    a.ws_rec = static_cast<uint8_t *>(workspace) + sbytes;
+    return check_hip(prime::launch_delta_prefill(a, NC, window, static_cast<hipStream_t>(stream)),
+                     "delta prefill launch");
+}
+
+int prime_delta_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                            const float *beta, const float *alpha, int B, int H, int H_kv, int D,
+                            float feat_eps, float bound, const float *state_in, float *state_out,
+                            const prime_tensor_t *y, void *stream) {
+    g_err[0] = 0;
+    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !beta || !alpha || !state_out)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_delta_decode_step: null argument");
+    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d", B, H, H_kv);
+    if (!valid_dtype(q->dtype) || !valid_dtype(k->dtype) || !valid_dtype(v->dtype) || !valid_dtype(y->dtype))
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dtype");
+    if ((state_in && !aligned16(state_in)) || !aligned16(state_out))
+        return fail(PRIME_ERR_MISALIGNED, "state buffers must be 16-byte aligned");
+    const size_t sbytes = static_cast<size_t>(B) * H * prime::kDeltaStateBytes;
+    if (state_in && state_in != state_out && overlap(state_in, sbytes, state_out, sbytes))
+        return fail(PRIME_ERR_ALIAS, "state_out overlaps state_in (only a fully in-place state is allowed)");
+    prime::DeltaStepArgs a{};
+    a.q = q->data; a.k = k->data; a.v = v->data;
+    a.q_sb = q->stride_b; a.q_sh = q->stride_h;
+    a.k_sb = k->stride_b; a.k_sh = k->stride_h;
+    a.v_sb = v->stride_b; a.v_sh = v->stride_h;
+    a.dt_q = q->dtype; a.dt_k = k->dtype; a.dt_v = v->dtype;
+    a.B = B; a.H = H; a.group = H / H_kv;
+    a.beta = beta; a.alpha = alpha;
+    a.feat_eps = feat_eps; a.bound = bound;
+    a.state_in = state_in; a.state_out = state_out;
+    a.y = y->data; a.dt_y = y->dtype; a.y_sb = y->stride_b; a.y_sh = y->stride_h;
+    return check_hip(prime::launch_delta_step(a, static_cast<hipStream_t>(stream)), "delta step launch");
+}
+
 size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags) {
     if (B <= 0 || H <= 0 || L <= 0) return 0;
     int G, cps;

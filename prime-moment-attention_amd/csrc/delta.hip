@@ -1,0 +1,538 @@
+// Chunked gated delta-rule PRIME (ChunkedGatedDeltaPrimeAttention,
+// chunked_delta_prime.py:25-283) on gfx950.
+//
+// Per (sequence, head) the state S is [D = 64 values][P = 128 features]; a
+// 64-token chunk with features psi_i, phi_i, values v_i, write rates beta_i
+// and cumulative log-decays cum_i does (chunked_delta_prime.py:199-270)
+//   E   = T^-1 (V - diag(e^cum) Phi S^T),   T = I + N,
+//         N_ij = [i>j] e^(cum_i - cum_j) (phi_i . phi_j) beta_j
+//   y   = A E + diag(e^cum) Psi S^T,  A_ij = [i>=j] e^(cum_i - cum_j) (psi_i . phi_j) beta_j
+//   S'  = e^cum_63 S + E^T diag(omega) Phi,  omega_j = beta_j e^(cum_63 - cum_j)
+//   S'' = S' min(1, bound / (|S'|_F + 1e-6))
+// Everything but S depends on the chunk alone, so the work splits into
+//   delta_prep_kernel (all chunks in parallel): the solve X = T^-1 [V | diag(e^cum) Phi]
+//     = [U | W], then the chunk's transfer record
+//       Y0 = A U,  Z = diag(e^cum) Psi - A W,  R0 = U^T diag(omega) Phi,
+//       M = W^T diag(omega) Phi,  e^cum_63
+//     so that  y = Y0 + Z S^T  and  S' = e^cum_63 S - S M + R0;
+//   delta_scan_kernel (one workgroup per (sequence, head), chunks in order):
+//     y^T = Y0^T + S Z^T and S'^T = e^cum_63 S^T - M^T S^T + R0^T on bf16 MFMA,
+//     the state S^T held in fp32 accumulators, then the clamp (one barrier).
+// The scan's MFMA operands of S come straight from its accumulators: lane l
+// holds S^T[16eb + 4g + r][d = 16w + l%16] (g = l/16), and the 8 k-slots of an
+// operand take rows 4g..4g+3 of two adjacent 16-row tiles, a fixed permutation
+// of the contraction index that the prep kernel applies to the other operand.
+// Records are written in exactly the lane order the scan reads them.
+//
+// The sequence is processed in windows of chunks (prep then scan per window),
+// so the workspace is bounded by the window, not by L.
+
+#include "prefill_common.h"
+
+namespace prime {
+namespace {
+
+constexpr int kP = 2 * kD;        // features
+constexpr int kP136 = kP + 8;     // 128-wide rows, 16-byte row reads
+constexpr int kP144 = kP + 16;    // 128-wide rows, transposed reads
+constexpr int kP72 = kD + 8;      // 64-wide rows, 16 / 8-byte row reads
+constexpr int kP80 = kD + 16;     // 64-wide rows, transposed reads
+constexpr int kRecMT = 0;         // -M^T A operands   [8 eb'][4 ks][64 lanes] x 16 B
+constexpr int kRecZB = 32768;     // Z^T B operands    [4 tb][4 ks][64 lanes] x 16 B
+constexpr int kRecR0 = 49152;     // R0^T acc tiles    [4 w][8 eb][64 lanes] x 8 B (bf16x4)
+constexpr int kRecY0 = 65536;     // Y0^T acc tiles    [4 w][4 tb][64 lanes] x 8 B
+constexpr int kRecSC = 73728;     // e^cum_63 (fp32)
+constexpr int kRecVec = static_cast<int>(kDeltaRecBytes / 16);  // 16-byte vectors per record
+constexpr int kPre = (kRecVec + 255) / 256;                      // per-thread prefetch vectors
+
+static_assert(kRecSC + 16 <= static_cast<int>(kDeltaRecBytes), "record layout");
+
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+
+__device__ __forceinline__ float ld_in(const void *p, int64_t i, int dt) { return load_elem(p, i, dt); }
+
+__device__ __forceinline__ uint2 pack4(f32x4 x) { return uint2{pack2(x[0], x[1]), pack2(x[2], x[3])}; }
+
+__device__ __forceinline__ f32x4 unpack4(uint2 u) {
+    return f32x4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xFFFF0000u), __uint_as_float(u.y << 16),
+                 __uint_as_float(u.y & 0xFFFF0000u)};
+}
+
+__device__ __forceinline__ bf16x8 pack8x(f32x4 a, f32x4 b) {
+    return as_bf16x8(u32x4{pack2(a[0], a[1]), pack2(a[2], a[3]), pack2(b[0], b[1]), pack2(b[2], b[3])});
+}
+
+// operand of 8 tokens (k-slots 0..3: rows r0..r0+3, 4..7: rows r0+16..r0+19) of
+// one column, read transposed from a row-major bf16 tile
+__device__ __forceinline__ bf16x8 tr8(const uint16_t *p0, int pitch) {
+    const uint2 a = lds_tr(p0), b = lds_tr(p0 + 16 * pitch);
+    return as_bf16x8(u32x4{a.x, a.y, b.x, b.y});
+}
+
+// 4 + 4 bf16 of one row at columns c and c + 16 (the same k-slot permutation)
+__device__ __forceinline__ bf16x8 row8p(const uint16_t *row, int c) {
+    const uint2 a = *reinterpret_cast<const uint2 *>(row + c), b = *reinterpret_cast<const uint2 *>(row + c + 16);
+    return as_bf16x8(u32x4{a.x, a.y, b.x, b.y});
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Per-chunk transfer records.  One workgroup (256 threads) per (seq, chunk).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t sPhi[kC][kP136];  // phi rows (bf16)
+    __shared__ __attribute__((aligned(16))) uint16_t sPsi[kC][kP136];  // psi rows
+    __shared__ __attribute__((aligned(16))) uint16_t sV[kC][kP72];     // v rows
+    __shared__ __attribute__((aligned(16))) float sN[kC][kC + 4];      // N (strictly lower), fp32
+    __shared__ __attribute__((aligned(16))) uint16_t sA[kC][kP72];     // A (lower), bf16
+    __shared__ __attribute__((aligned(16))) uint16_t sU[kC][kP80];     // U = T^-1 V
+    __shared__ __attribute__((aligned(16))) uint16_t sUw[kC][kP80];    // diag(omega) U
+    __shared__ __attribute__((aligned(16))) uint16_t sW[kC][kP144];    // W = T^-1 diag(e^cum) Phi
+    __shared__ __attribute__((aligned(16))) uint16_t sWw[kC][kP144];   // diag(omega) W
+    __shared__ float sCum[kC], sBeta[kC], sEc[kC], sOm[kC];  // cum, beta, e^cum, omega
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int tr_r = c16 >> 2, tr_c = 4 * (c16 & 3);
+    const int Sq = a.B * a.H;
+    const int unit = blockIdx.x;
+    if (unit >= Sq * a.nw) return;
+    const int seq = unit / a.nw, cw = unit - seq * a.nw;
+    const int c = a.c0 + cw;
+    const int b = seq / a.H, h = seq - b * a.H, hk = h / a.group;
+
+    // ---- features (chunked_delta_prime.py:73-87): thread = (token tid/4, 16 dims)
+    {
+        const int i = tid >> 2, d0 = 16 * (tid & 3);
+        const int t = c * kC + i;
+        const bool valid = t < a.L;
+        const int tc = valid ? t : a.L - 1;
+        const int64_t qo = b * a.q_sb + h * a.q_sh + tc * a.q_sl + d0;
+        const int64_t ko = b * a.k_sb + hk * a.k_sh + tc * a.k_sl + d0;
+        const int64_t vo = b * a.v_sb + hk * a.v_sh + tc * a.v_sl + d0;
+        float qv[16], kv[16], vv[16];
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            qv[e] = valid ? ld_in(a.q, qo + e, a.dt_in) : 0.f;
+            kv[e] = valid ? ld_in(a.k, ko + e, a.dt_in) : 0.f;
+            vv[e] = valid ? ld_in(a.v, vo + e, a.dt_in) : 0.f;
+            const float k2 = kv[e] * kv[e];
+            s1 += k2;
+            s2 += k2 * k2;
+        }
+        s1 += __shfl_xor(s1, 1, kWave);
+        s1 += __shfl_xor(s1, 2, kWave);
+        s2 += __shfl_xor(s2, 1, kWave);
+        s2 += __shfl_xor(s2, 2, kWave);
+        const float r1 = 1.0f / fmaxf(sqrtf(s1), a.feat_eps);
+        const float r2 = 0.70710678118654752f / fmaxf(sqrtf(s2), a.feat_eps);
+        float ph[16], ph2[16], ps2[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            ph[e] = kv[e] * r1;
+            ph2[e] = kv[e] * kv[e] * r2;
+            ps2[e] = 0.70710678118654752f * qv[e] * qv[e];
+        }
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int o = 8 * hf;
+            *reinterpret_cast<u32x4 *>(&sPhi[i][d0 + o]) = u32x4{pack2(ph[o], ph[o + 1]), pack2(ph[o + 2], ph[o + 3]),
+                                                                  pack2(ph[o + 4], ph[o + 5]), pack2(ph[o + 6], ph[o + 7])};
+            *reinterpret_cast<u32x4 *>(&sPhi[i][kD + d0 + o]) =
+                u32x4{pack2(ph2[o], ph2[o + 1]), pack2(ph2[o + 2], ph2[o + 3]), pack2(ph2[o + 4], ph2[o + 5]),
+                      pack2(ph2[o + 6], ph2[o + 7])};
+            *reinterpret_cast<u32x4 *>(&sPsi[i][d0 + o]) = u32x4{pack2(qv[o], qv[o + 1]), pack2(qv[o + 2], qv[o + 3]),
+                                                                  pack2(qv[o + 4], qv[o + 5]), pack2(qv[o + 6], qv[o + 7])};
+            *reinterpret_cast<u32x4 *>(&sPsi[i][kD + d0 + o]) =
+                u32x4{pack2(ps2[o], ps2[o + 1]), pack2(ps2[o + 2], ps2[o + 3]), pack2(ps2[o + 4], ps2[o + 5]),
+                      pack2(ps2[o + 6], ps2[o + 7])};
+            *reinterpret_cast<u32x4 *>(&sV[i][d0 + o]) = u32x4{pack2(vv[o], vv[o + 1]), pack2(vv[o + 2], vv[o + 3]),
+                                                                pack2(vv[o + 4], vv[o + 5]), pack2(vv[o + 6], vv[o + 7])};
+        }
+    }
+    // ---- cumulative log-decay (:199-201), padding tokens: beta 0, alpha decay_pad (:186-189)
+    if (wave == 0) {
+        const int t = c * kC + lane;
+        const bool valid = t < a.L;
+        const int64_t o = static_cast<int64_t>(seq) * a.L + t;
+        const float bt = valid ? a.beta[o] : 0.f;
+        const float al = valid ? a.alpha[o] : a.decay_pad;
+        float cum = logf(fminf(fmaxf(al, 1e-5f), 1.0f));
+#pragma unroll
+        for (int s = 1; s < 64; s <<= 1) {
+            const float x = __shfl_up(cum, s, kWave);
+            if (lane >= s) cum += x;
+        }
+        const float cend = __shfl(cum, 63, kWave);
+        sCum[lane] = cum;
+        sBeta[lane] = bt;
+        sEc[lane] = expf(cum);
+        sOm[lane] = bt * expf(cend - cum);
+    }
+    __syncthreads();
+
+    // ---- N and A (:203-218, :248-250): row block of wave w, column blocks jb <= w
+    {
+        const int w = wave;
+        bf16x8 fa[4], fs[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            fa[ks] = as_bf16x8(lds128(&sPhi[16 * w + c16][32 * ks + 8 * g]));
+            fs[ks] = as_bf16x8(lds128(&sPsi[16 * w + c16][32 * ks + 8 * g]));
+        }
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+            f32x4 gr = {0.f, 0.f, 0.f, 0.f}, ga = {0.f, 0.f, 0.f, 0.f};
+            if (jb <= w) {
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const bf16x8 fb = as_bf16x8(lds128(&sPhi[16 * jb + c16][32 * ks + 8 * g]));
+                    gr = mfma(fa[ks], fb, gr);
+                    ga = mfma(fs[ks], fb, ga);
+                }
+            }
+            const int j = 16 * jb + c16;
+            const float cj = sCum[j], bj = sBeta[j];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * w + 4 * g + r;
+                const float lam = i >= j ? expf(sCum[i] - cj) * bj : 0.f;
+                sN[i][j] = i > j ? lam * gr[r] : 0.f;
+                sA[i][j] = f32_to_bf16_bits(lam * ga[r]);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- solve T X = [V | diag(e^cum) Phi] (:242-245): thread = one of 192 columns,
+    // forward substitution in fp32 registers.  Row i of N is read as broadcast
+    // 16-byte LDS reads; its offset and the row's result pass through empty asm
+    // statements so that the compiler neither hoists all 504 reads to the top
+    // nor sinks the rows' arithmetic to their last use (either spills).
+    if (tid < kD + kP) {
+        const int col = tid;
+        const float *nbase = &sN[0][0];
+        float x[kC];
+#pragma unroll
+        for (int i = 0; i < kC; ++i)
+            x[i] = col < kD ? bf16_bits_to_f32(sV[i][col]) : sEc[i] * bf16_bits_to_f32(sPhi[i][col - kD]);
+#pragma unroll
+        for (int i = 1; i < kC; ++i) {
+            int ro = i * (kC + 4);
+            asm volatile("" : "+v"(ro));
+            float acc = x[i];
+#pragma unroll
+            for (int j = 0; j < i; j += 4) {
+                const f32x4 n4 = *reinterpret_cast<const f32x4 *>(nbase + ro + j);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (j + e < i) acc -= n4[e] * x[j + e];
+            }
+            asm volatile("" : "+v"(acc));  // x[i] is final here (no sinking into later rows)
+            x[i] = acc;
+        }
+#pragma unroll
+        for (int i = 0; i < kC; ++i) {
+            const float om = sOm[i];
+            if (col < kD) {
+                sU[i][col] = f32_to_bf16_bits(x[i]);
+                sUw[i][col] = f32_to_bf16_bits(om * x[i]);
+            } else {
+                sW[i][col - kD] = f32_to_bf16_bits(x[i]);
+                sWw[i][col - kD] = f32_to_bf16_bits(om * x[i]);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- transfer record, in the scan's lane order
+    uint8_t *rec = a.ws_rec + (static_cast<size_t>(seq) * a.nw + cw) * kDeltaRecBytes;
+    const int w = wave;
+    // Y0^T tile (d-block w, token block tb) = U^T A^T
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            if (kt == 1 && tb < 2) continue;  // A is lower triangular
+            const bf16x8 ua = tr8(&sU[32 * kt + 4 * g + tr_r][16 * w + tr_c], kP80);
+            const bf16x8 ab = row8p(&sA[16 * tb + c16][0], 32 * kt + 4 * g);
+            acc = mfma(ua, ab, acc);
+        }
+        *reinterpret_cast<uint2 *>(rec + kRecY0 + ((w * 4 + tb) * 64 + lane) * 8) = pack4(acc);
+    }
+    // Z^T tiles (feature blocks 2w, 2w+1; token block tb) = diag(e^cum) Psi^T - W^T A^T
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        f32x4 zt[2];
+        const int i = 16 * tb + c16;
+        const float ec = sEc[i];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int eb = 2 * w + hf;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                if (kt == 1 && tb < 2) continue;
+                const bf16x8 wa = tr8(&sW[32 * kt + 4 * g + tr_r][16 * eb + tr_c], kP144);
+                const bf16x8 ab = row8p(&sA[i][0], 32 * kt + 4 * g);
+                acc = mfma(wa, ab, acc);
+            }
+            const f32x4 ps = unpack4(*reinterpret_cast<const uint2 *>(&sPsi[i][16 * eb + 4 * g]));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) zt[hf][r] = ec * ps[r] - acc[r];
+        }
+        *reinterpret_cast<bf16x8 *>(rec + kRecZB + ((tb * 4 + w) * 64 + lane) * 16) = pack8x(zt[0], zt[1]);
+    }
+    // R0^T tiles (feature blocks 2w, 2w+1; every d-block) = Phi^T diag(omega) U
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+        const int eb = 2 * w + hf;
+#pragma unroll
+        for (int dw = 0; dw < 4; ++dw) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const bf16x8 pa = tr8(&sPhi[32 * kt + 4 * g + tr_r][16 * eb + tr_c], kP136);
+                const bf16x8 ub = tr8(&sUw[32 * kt + 4 * g + tr_r][16 * dw + tr_c], kP80);
+                acc = mfma(pa, ub, acc);
+            }
+            *reinterpret_cast<uint2 *>(rec + kRecR0 + ((dw * 8 + eb) * 64 + lane) * 8) = pack4(acc);
+        }
+    }
+    // -M^T as the scan's A operands: M tiles (rows e in blocks 2w, 2w+1; columns e')
+    // = (diag(omega) W)^T Phi, packed two row blocks per k-step
+#pragma unroll
+    for (int ebp = 0; ebp < 8; ++ebp) {
+        f32x4 m[2];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int eb = 2 * w + hf;
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const bf16x8 wa = tr8(&sWw[32 * kt + 4 * g + tr_r][16 * eb + tr_c], kP144);
+                const bf16x8 pb = tr8(&sPhi[32 * kt + 4 * g + tr_r][16 * ebp + tr_c], kP136);
+                acc = mfma(wa, pb, acc);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) m[hf][r] = -acc[r];
+        }
+        *reinterpret_cast<bf16x8 *>(rec + kRecMT + ((ebp * 4 + w) * 64 + lane) * 16) = pack8x(m[0], m[1]);
+    }
+    if (tid == 0) *reinterpret_cast<float *>(rec + kRecSC) = sEc[kC - 1];
+}
+
+// ---------------------------------------------------------------------------
+// Sequential scan over a window's chunks.  One workgroup (4 waves) per
+// (sequence, head); wave w owns value columns d in [16w, 16w + 16).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256, 1) void delta_scan_kernel(const DeltaArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t sRec[2][kDeltaRecBytes];
+    __shared__ float sRed[2][4];
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int seq = blockIdx.x;
+    if (seq >= a.B * a.H) return;
+    const int b = seq / a.H, h = seq - b * a.H;
+    const int w = wave;
+    const size_t sofs = static_cast<size_t>(seq) * kD * kP;
+
+    // ---- state entering the window: S^T tiles st[eb][r] = S[d = 16w + c16][e = 16eb + 4g + r]
+    const float *src = a.first ? a.state_in : a.ws_state;
+    f32x4 st[8];
+#pragma unroll
+    for (int eb = 0; eb < 8; ++eb) {
+        if (src) st[eb] = *reinterpret_cast<const f32x4 *>(src + sofs + (16 * w + c16) * kP + 16 * eb + 4 * g);
+        else st[eb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    // ---- record staging: global -> registers one chunk ahead -> LDS
+    u32x4 pre[kPre];
+    // (unconditional loads; the tail index is clamped into the record and its
+    // duplicate never staged)
+    auto fetch = [&](int cw) {
+        const uint8_t *rec = a.ws_rec + (static_cast<size_t>(seq) * a.nw + cw) * kDeltaRecBytes;
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) {
+            const int v = min(tid + 256 * k, kRecVec - 1);
+            pre[k] = *reinterpret_cast<const u32x4 *>(rec + 16 * v);
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < kPre; ++k) {
+            const int v = tid + 256 * k;
+            if (k < kPre - 1 || v < kRecVec) *reinterpret_cast<u32x4 *>(&sRec[buf][16 * v]) = pre[k];
+        }
+    };
+    fetch(0);
+    stage(0);
+    if (a.nw > 1) fetch(1);
+    __syncthreads();
+
+    for (int cw = 0; cw < a.nw; ++cw) {
+        const int buf = cw & 1;
+        const uint8_t *R = sRec[buf];
+        const int c = a.c0 + cw;
+        // S operand packs (A of S Z^T, B of M^T S^T): k-slots = rows 4g..4g+3 of tiles 2ks, 2ks+1
+        bf16x8 sb[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) sb[ks] = pack8x(st[2 * ks], st[2 * ks + 1]);
+        // ---- y^T (d-block w, token block tb) = Y0^T + S Z^T
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            f32x4 acc = unpack4(*reinterpret_cast<const uint2 *>(R + kRecY0 + ((w * 4 + tb) * 64 + lane) * 8));
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                acc = mfma(sb[ks], *reinterpret_cast<const bf16x8 *>(R + kRecZB + ((tb * 4 + ks) * 64 + lane) * 16), acc);
+            const int t = c * kC + 16 * tb + c16;
+            if (t < a.L) {
+                const int64_t o = b * a.y_sb + h * a.y_sh + t * a.y_sl + 16 * w + 4 * g;
+                if (a.dt_y == PRIME_BF16) {
+                    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + o) = pack4(acc);
+                } else if (a.dt_y == PRIME_F32) {
+                    *reinterpret_cast<f32x4 *>(static_cast<float *>(a.y) + o) = acc;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) store_elem(a.y, o + r, a.dt_y, acc[r]);
+                }
+            }
+        }
+        // ---- S'^T = e^cum_63 S^T + R0^T - M^T S^T
+        const float e63 = *reinterpret_cast<const float *>(R + kRecSC);
+        float ss = 0.f;
+#pragma unroll
+        for (int eb = 0; eb < 8; ++eb) {
+            const f32x4 r0 = unpack4(*reinterpret_cast<const uint2 *>(R + kRecR0 + ((w * 8 + eb) * 64 + lane) * 8));
+            f32x4 n;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) n[r] = e63 * st[eb][r] + r0[r];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                n = mfma(*reinterpret_cast<const bf16x8 *>(R + kRecMT + ((eb * 4 + ks) * 64 + lane) * 16), sb[ks], n);
+            st[eb] = n;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ss += n[r] * n[r];
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) sRed[buf][w] = ss;
+        if (cw + 1 < a.nw) stage(buf ^ 1);
+        if (cw + 2 < a.nw) fetch(cw + 2);
+        __syncthreads();
+        // ---- Lyapunov clamp (:266-270)
+        if (a.bound > 0.f) {
+            const float nrm = sqrtf(sRed[buf][0] + sRed[buf][1] + sRed[buf][2] + sRed[buf][3]);
+            const float sc = fminf(1.0f, a.bound / (nrm + 1e-6f));
+#pragma unroll
+            for (int eb = 0; eb < 8; ++eb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) st[eb][r] *= sc;
+        }
+    }
+
+    // ---- state leaving the window
+    float *dst = a.last ? a.state_out : a.ws_state;
+    if (dst) {
+#pragma unroll
+        for (int eb = 0; eb < 8; ++eb)
+            *reinterpret_cast<f32x4 *>(dst + sofs + (16 * w + c16) * kP + 16 * eb + 4 * g) = st[eb];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode step (chunked_delta_prime.py:140-176).  One wave per (b, h); lane d
+// holds state row S[d][0..127].
+// ---------------------------------------------------------------------------
+constexpr int kStepWaves = 4;
+
+__global__ __launch_bounds__(kStepWaves * 64) void delta_step_kernel(const DeltaStepArgs a) {
+    __shared__ __attribute__((aligned(16))) float sPhi[kStepWaves][kP];
+    __shared__ __attribute__((aligned(16))) float sPsi[kStepWaves][kP];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t = blockIdx.x * kStepWaves + wave;
+    const bool active = t < a.B * a.H;
+    const int tt = active ? t : 0;
+    const int b = tt / a.H, h = tt - b * a.H, hk = h / a.group;
+    const float qv = load_elem(a.q, b * a.q_sb + h * a.q_sh + lane, a.dt_q);
+    const float kv = load_elem(a.k, b * a.k_sb + hk * a.k_sh + lane, a.dt_k);
+    const float vv = load_elem(a.v, b * a.v_sb + hk * a.v_sh + lane, a.dt_v);
+    const float k2 = kv * kv;
+    const float s1 = wave_sum(k2), s2 = wave_sum(k2 * k2);
+    sPhi[wave][lane] = kv / fmaxf(sqrtf(s1), a.feat_eps);
+    sPhi[wave][kD + lane] = 0.70710678118654752f * k2 / fmaxf(sqrtf(s2), a.feat_eps);
+    sPsi[wave][lane] = qv;
+    sPsi[wave][kD + lane] = 0.70710678118654752f * qv * qv;
+    __syncthreads();
+    const size_t so = static_cast<size_t>(tt) * kD * kP + static_cast<size_t>(lane) * kP;
+    f32x4 s[kP / 4];
+#pragma unroll
+    for (int i = 0; i < kP / 4; ++i)
+        s[i] = a.state_in ? *reinterpret_cast<const f32x4 *>(a.state_in + so + 4 * i) : f32x4{0.f, 0.f, 0.f, 0.f};
+    float vhat = 0.f;
+#pragma unroll
+    for (int i = 0; i < kP / 4; ++i) {
+        const f32x4 p = *reinterpret_cast<const f32x4 *>(&sPhi[wave][4 * i]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) vhat += s[i][r] * p[r];
+    }
+    const float bt = a.beta[tt], al = a.alpha[tt];
+    const float err = bt * (vv - vhat);
+    float ss = 0.f, yv = 0.f;
+#pragma unroll
+    for (int i = 0; i < kP / 4; ++i) {
+        const f32x4 p = *reinterpret_cast<const f32x4 *>(&sPhi[wave][4 * i]);
+        const f32x4 q = *reinterpret_cast<const f32x4 *>(&sPsi[wave][4 * i]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            s[i][r] = al * s[i][r] + err * p[r];
+            ss += s[i][r] * s[i][r];
+            yv += s[i][r] * q[r];
+        }
+    }
+    ss = wave_sum(ss);
+    const float sc = a.bound > 0.f ? fminf(1.0f, a.bound / (sqrtf(ss) + 1e-6f)) : 1.0f;
+    if (active) {
+#pragma unroll
+        for (int i = 0; i < kP / 4; ++i) {
+            f32x4 x = s[i];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[r] *= sc;
+            *reinterpret_cast<f32x4 *>(a.state_out + so + 4 * i) = x;
+        }
+        store_elem(a.y, b * a.y_sb + h * a.y_sh + lane, a.dt_y, sc * yv);
+    }
+}
+
+hipError_t launch_delta_prefill(DeltaArgs a, int NC, int window, hipStream_t stream) {
+    const int Sq = a.B * a.H;
+    for (int c0 = 0; c0 < NC; c0 += window) {
+        a.c0 = c0;
+        a.nw = NC - c0 < window ? NC - c0 : window;
+        a.first = c0 == 0;
+        a.last = c0 + a.nw >= NC;
+        timer_begin(PRIME_KERNEL_DELTA_PREP, stream);
+        hipLaunchKernelGGL(delta_prep_kernel, dim3(Sq * a.nw), dim3(256), 0, stream, a);
+        timer_end(PRIME_KERNEL_DELTA_PREP, stream);
+        timer_begin(PRIME_KERNEL_DELTA_SCAN, stream);
+        hipLaunchKernelGGL(delta_scan_kernel, dim3(Sq), dim3(256), 0, stream, a);
+        timer_end(PRIME_KERNEL_DELTA_SCAN, stream);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_delta_step(const DeltaStepArgs &a, hipStream_t stream) {
+    const int n = a.B * a.H;
+    timer_begin(PRIME_KERNEL_DELTA_STEP, stream);
+    hipLaunchKernelGGL(delta_step_kernel, dim3((n + kStepWaves - 1) / kStepWaves), dim3(kStepWaves * 64), 0, stream, a);
+    timer_end(PRIME_KERNEL_DELTA_STEP, stream);
+    return hipGetLastError();
+}
+
+}  // namespace prime

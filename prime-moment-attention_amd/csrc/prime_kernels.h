@@ -49,6 +49,49 @@ hipError_t launch_prefill(PrefillArgs a, hipStream_t stream);
 // segments per sequence for the launch plan, given the workspace the caller has
 void plan_segments(int S, int L, bool dense_clamp, size_t ws_bytes, int *G, int *cps);
 
+// Chunked gated delta-rule prefill (delta.hip).
+struct DeltaArgs {
+    const void *q, *k, *v;
+    int64_t q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;
+    int dt_in;  // PRIME_BF16 or PRIME_F32 (all three inputs)
+    int B, H, group, L;
+    const float *beta, *alpha;  // [B, H, L]
+    float decay_pad, feat_eps, bound;
+    const float *state_in;      // [B, H, D, 2D] or null
+    float *state_out;           // [B, H, D, 2D] or null
+    void *y;
+    int dt_y;
+    int64_t y_sb, y_sh, y_sl;
+    float *ws_state;            // [B*H][D*2D]: state between windows
+    uint8_t *ws_rec;            // [B*H][window][record]
+    int c0, nw;                 // window: chunks c0 .. c0 + nw - 1
+    int first, last;            // window is the first / last of the call
+};
+
+// One delta-rule decode step (delta.hip).
+struct DeltaStepArgs {
+    const void *q, *k, *v;
+    int64_t q_sb, q_sh, k_sb, k_sh, v_sb, v_sh;
+    int dt_q, dt_k, dt_v;
+    int B, H, group;
+    const float *beta, *alpha;  // [B, H]
+    float feat_eps, bound;
+    const float *state_in;      // [B, H, D, 2D] or null
+    float *state_out;
+    void *y;
+    int dt_y;
+    int64_t y_sb, y_sh;
+};
+
+constexpr int kDeltaChunk = 64;
+constexpr size_t kDeltaStateBytes = static_cast<size_t>(kD) * 2 * kD * sizeof(float);  // one (b,h) state
+constexpr size_t kDeltaRecBytes = 73984;         // per-chunk transfer record (multiple of 256)
+constexpr int kDeltaDefaultWindow = 128;         // chunks per window with the recommended workspace
+
+// Launch the delta prefill over every window (prep + scan per window).
+hipError_t launch_delta_prefill(DeltaArgs a, int NC, int window, hipStream_t stream);
+hipError_t launch_delta_step(const DeltaStepArgs &a, hipStream_t stream);
+
 // bf16-input prefill kernels (prefill_bf16.hip): the state-only segment pass
 // (256 threads) or the fused chunk loop (512 threads) over `grid` workgroups.
 void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream);

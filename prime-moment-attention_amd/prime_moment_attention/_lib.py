@@ -24,13 +24,16 @@ _DTYPES = {torch.float32: PRIME_F32, torch.bfloat16: PRIME_BF16, torch.float16: 
 # every symbol include/prime_mi355x.h declares
 EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_chunked_prefill",
            "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
-           "prime_timer_read")
+           "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
+           "prime_delta_decode_step")
 
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
+KERNEL_DELTA_PREP, KERNEL_DELTA_SCAN, KERNEL_DELTA_STEP = 4, 5, 6
 KERNEL_NAMES = {KERNEL_PREFILL_CHUNKS: "prefill_kernel<bf16,fused>", KERNEL_PREFILL_SEGMENTS:
                 "prefill_kernel<bf16,state_only>", KERNEL_SEGMENT_SCAN: "segment_scan_kernel",
-                KERNEL_DECODE: "decode_step_kernel"}
+                KERNEL_DECODE: "decode_step_kernel", KERNEL_DELTA_PREP: "delta_prep_kernel",
+                KERNEL_DELTA_SCAN: "delta_scan_kernel", KERNEL_DELTA_STEP: "delta_step_kernel"}
 
 
 class PrimeTensor(ctypes.Structure):
@@ -67,6 +70,15 @@ def load() -> ctypes.CDLL:
     L.prime_chunked_prefill_workspace_size.argtypes = [ctypes.c_int] * 3 + [ctypes.c_uint]
     L.prime_chunked_prefill_workspace_size.restype = ctypes.c_size_t
     L.prime_timer_enable.argtypes = [ctypes.c_uint]
+    fp = ctypes.c_void_p
+    L.prime_delta_prefill.argtypes = [P(PrimeTensor)] * 3 + [fp, fp] + [ctypes.c_int] * 6 + [
+        ctypes.c_float] * 3 + [fp, P(PrimeTensor), fp, fp, ctypes.c_size_t, fp]
+    L.prime_delta_prefill.restype = ctypes.c_int
+    L.prime_delta_prefill_workspace_size.argtypes = [ctypes.c_int] * 3 + [ctypes.c_uint]
+    L.prime_delta_prefill_workspace_size.restype = ctypes.c_size_t
+    L.prime_delta_decode_step.argtypes = [P(PrimeTensor)] * 3 + [fp, fp] + [ctypes.c_int] * 4 + [
+        ctypes.c_float] * 2 + [fp, fp, P(PrimeTensor), fp]
+    L.prime_delta_decode_step.restype = ctypes.c_int
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     v = L.prime_abi_version()
     if v != ABI_VERSION:
@@ -238,6 +250,77 @@ def bind_chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, s
         _check(fn(*args, torch.cuda.current_stream(dev).cuda_stream), "prime_chunked_prefill")
     launch.buffers = keep
     return launch
+
+
+# ---------------------------------------------------------------- delta rule
+def _check_delta_state(S, B, H, D, name):
+    if S is None:
+        return
+    if S.dtype != torch.float32 or not S.is_contiguous() or S.numel() != B * H * D * 2 * D:
+        raise ValueError(f"{name} must be a contiguous fp32 [B, H, D, 2D] tensor")
+    _dev_check(S)
+
+
+def _gate(t, B, H, L, name):
+    if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != B * H * L:
+        raise ValueError(f"{name} must be a contiguous fp32 tensor of {B * H * L} values ([B, H, L])")
+    _dev_check(t)
+
+
+def delta_workspace_size(B: int, H: int, L: int) -> int:
+    return int(load().prime_delta_prefill_workspace_size(B, H, L, 0))
+
+
+def delta_prefill(q, k, v, beta, alpha, decay_pad: float, feat_eps: float, bound: float, state_in, y,
+                  state_out, workspace: Optional[torch.Tensor] = None) -> None:
+    """Chunked delta-rule prefill (prime_delta_prefill).  q [B,H,L,D], k/v
+    [B,Hkv,L,D] (bf16 or fp32 alike), beta/alpha fp32 [B,H,L], states fp32
+    [B,H,D,2D] or None, y [B,H,L,D].  workspace None allocates the recommended
+    size from torch's caching allocator."""
+    _dev_check(q, k, v, y)
+    B, H, Lq, D = q.shape
+    Hkv = k.shape[1]
+    _shape(k, (B, Hkv, Lq, D), "k")
+    _shape(v, (B, Hkv, Lq, D), "v")
+    _shape(y, (B, H, Lq, D), "y")
+    _gate(beta, B, H, Lq, "beta")
+    _gate(alpha, B, H, Lq, "alpha")
+    _check_delta_state(state_in, B, H, D, "state_in")
+    _check_delta_state(state_out, B, H, D, "state_out")
+    if workspace is None:
+        workspace = torch.empty(delta_workspace_size(B, H, Lq), dtype=torch.uint8, device=q.device)
+    _dev_check(workspace)
+    qd, kd, vd, yd = tensor_desc(q, True), tensor_desc(k, True), tensor_desc(v, True), tensor_desc(y, True)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    rc = load().prime_delta_prefill(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ptr(beta), ptr(alpha),
+                                    B, H, Hkv, Lq, D, 64, float(decay_pad), float(feat_eps), float(bound),
+                                    ptr(state_in), ctypes.byref(yd), ptr(state_out), ptr(workspace),
+                                    workspace.numel(), _stream(q.device))
+    _check(rc, "prime_delta_prefill")
+
+
+def delta_decode_step(q, k, v, beta, alpha, feat_eps: float, bound: float, state_in, state_out, y) -> None:
+    """One delta-rule decode step (prime_delta_decode_step).  q [B,H,D], k/v
+    [B,Hkv,D], beta/alpha fp32 [B,H], states fp32 [B,H,D,2D] (state_in None:
+    zero), y [B,H,D]."""
+    _dev_check(q, k, v, y)
+    B, H, D = q.shape
+    Hkv = k.shape[1]
+    _shape(k, (B, Hkv, D), "k")
+    _shape(v, (B, Hkv, D), "v")
+    _shape(y, (B, H, D), "y")
+    _gate(beta, B, H, 1, "beta")
+    _gate(alpha, B, H, 1, "alpha")
+    _check_delta_state(state_in, B, H, D, "state_in")
+    _check_delta_state(state_out, B, H, D, "state_out")
+    if state_out is None:
+        raise ValueError("state_out is required")
+    qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), tensor_desc(y, False)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    rc = load().prime_delta_decode_step(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ptr(beta), ptr(alpha),
+                                        B, H, Hkv, D, float(feat_eps), float(bound), ptr(state_in), ptr(state_out),
+                                        ctypes.byref(yd), _stream(q.device))
+    _check(rc, "prime_delta_decode_step")
 
 
 def timer_enable(*kernels: int) -> None:

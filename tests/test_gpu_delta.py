@@ -1,0 +1,143 @@
+"""GPU parity of the delta-rule PRIME kernels (prime_delta_prefill,
+prime_delta_decode_step) against the oracle restatement of
+chunked_delta_prime.py:73-283 (oracle/prime_oracle.c: oracle_delta_features,
+oracle_delta_chunked, oracle_delta_step)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from prime_moment_attention import _lib
+
+from gpu_util import TOL_BF16, assert_close, dev, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+D = 64
+FEAT_EPS = 1e-5
+
+
+def _inputs(B, H, L, seed, Hkv=None, bf16=True, beta_scale=0.5):
+    Hkv = Hkv or H
+    q, _, _ = O.make_inputs((B, H, L, D), seed=seed, bf16=bf16)
+    _, k, v = O.make_inputs((B, Hkv, L, D), seed=seed + 1, bf16=bf16)
+    rng = np.random.default_rng(seed)
+    beta = (beta_scale / (1 + np.exp(-rng.standard_normal((B, H, L))))).astype(np.float32)
+    alpha = rng.uniform(0.95, 0.999, (B, H, L)).astype(np.float32)
+    return q, k, v, beta, alpha
+
+
+def _oracle(q, k, v, beta, alpha, decay_pad, bound, state=None):
+    B, H, L, _ = q.shape
+    grp = H // k.shape[1]
+    ke, ve = np.repeat(k, grp, axis=1), np.repeat(v, grp, axis=1)
+    BH = B * H
+    psi, phi = O.delta_features(q.reshape(BH, L, D), ke.reshape(BH, L, D), eps=FEAT_EPS)
+    return O.delta_chunked(psi, phi, ve.reshape(BH, L, D), beta.reshape(BH, L), alpha.reshape(BH, L),
+                           decay_pad, bound=bound, chunk=64, state=state)
+
+
+def _run(q, k, v, beta, alpha, decay_pad, bound, state=None, dt=torch.bfloat16, workspace=None, inplace=False):
+    B, H, L, _ = q.shape
+    y = torch.empty(B, H, L, D, device=dev())
+    s_in = None if state is None else to_dev(state.reshape(B, H, D, 2 * D))
+    s_out = s_in if (inplace and s_in is not None) else torch.empty(B, H, D, 2 * D, device=dev())
+    _lib.delta_prefill(to_dev(q, dt), to_dev(k, dt), to_dev(v, dt), to_dev(beta), to_dev(alpha), decay_pad,
+                       FEAT_EPS, bound, s_in, y, s_out, workspace=workspace)
+    torch.cuda.synchronize()
+    return to_np(y).reshape(B * H, L, D), to_np(s_out).reshape(B * H, D, 2 * D)
+
+
+@pytest.mark.parametrize("L", [1, 13, 64, 200, 700])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_delta_prefill_matches_oracle(L, with_state):
+    B, H = 2, 3
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=50 + L)
+    st = np.random.default_rng(51).standard_normal((B * H, D, 2 * D)) * 0.05 if with_state else None
+    yo, so = _oracle(q, k, v, beta, alpha, 0.995, 25.0, st)
+    y, s = _run(q, k, v, beta, alpha, 0.995, 25.0, st)
+    assert_close(y, yo, TOL_BF16, "y")
+    assert_close(s, so, TOL_BF16, "S")
+
+
+def test_delta_prefill_clamp_active_and_gqa():
+    """A small Lyapunov bound clamps every chunk; k/v shared by head pairs."""
+    B, H, L = 1, 4, 300
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=60, Hkv=2, beta_scale=1.0)
+    yo, so = _oracle(q, k, v, beta, alpha, 0.99, 0.5)
+    nrm = np.sqrt((so ** 2).sum(axis=(1, 2)))
+    assert np.all(nrm <= 0.5 + 1e-6) and np.all(nrm > 0.49)  # the clamp is active in the oracle
+    y, s = _run(q, k, v, beta, alpha, 0.99, 0.5)
+    assert_close(y, yo, TOL_BF16, "y")
+    assert_close(s, so, TOL_BF16, "S")
+
+
+def test_delta_prefill_without_clamp_equals_tokenwise():
+    """bound <= 0: the chunked form is the per-token gated delta rule with the
+    decay applied before the prediction (decay^pad on the final state)."""
+    B, H, L = 1, 2, 150
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=61)
+    y, s = _run(q, k, v, beta, alpha, 0.99, 0.0)
+    BH = B * H
+    psi, phi = O.delta_features(q.reshape(BH, L, D), k.reshape(BH, L, D), eps=FEAT_EPS)
+    yt, stk = O.delta_tokenwise(psi, phi, v.reshape(BH, L, D), beta.reshape(BH, L), alpha.reshape(BH, L))
+    pad = (64 - L % 64) % 64
+    assert_close(y, yt, TOL_BF16, "y")
+    assert_close(s, stk * 0.99 ** pad, TOL_BF16, "S")
+
+
+@pytest.mark.parametrize("with_state", [False, True])
+def test_delta_prefill_windows_agree(with_state):
+    """A workspace for one chunk per window (state carried between windows
+    through the workspace, in place) gives the same result as one window."""
+    B, H, L = 1, 2, 64 * 5 + 17
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=62)
+    st = np.random.default_rng(63).standard_normal((B * H, D, 2 * D)) * 0.05 if with_state else None
+    y1, s1 = _run(q, k, v, beta, alpha, 0.995, 25.0, st)
+    small = torch.empty(_lib.delta_workspace_size(B, H, 64), dtype=torch.uint8, device=dev())
+    y2, s2 = _run(q, k, v, beta, alpha, 0.995, 25.0, st, workspace=small, inplace=True)
+    assert_close(y2, y1, 1e-5, "y")
+    assert_close(s2, s1, 1e-5, "S")
+
+
+def test_delta_prefill_f32_inputs():
+    B, H, L = 1, 2, 130
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=64, bf16=False)
+    yo, so = _oracle(q, k, v, beta, alpha, 0.995, 25.0)
+    y, s = _run(q, k, v, beta, alpha, 0.995, 25.0, dt=torch.float32)
+    assert_close(y, yo, TOL_BF16, "y")  # bf16 MFMA inside: the bf16 tolerance applies
+    assert_close(s, so, TOL_BF16, "S")
+
+
+def test_delta_prefill_long_sequence_subset():
+    """4096 tokens (64 chunks, two windows of the default size would need more):
+    the scan stays within tolerance over many chunks and the state stays bounded."""
+    B, H, L = 1, 2, 4096
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=65, beta_scale=1.0)
+    yo, so = _oracle(q, k, v, beta, alpha, 0.995, 25.0)
+    y, s = _run(q, k, v, beta, alpha, 0.995, 25.0)
+    assert np.isfinite(y).all() and np.isfinite(s).all()
+    assert_close(y, yo, TOL_BF16, "y")
+    assert_close(s, so, TOL_BF16, "S")
+
+
+@pytest.mark.parametrize("bound", [25.0, 0.3])
+def test_delta_decode_step_matches_oracle(bound):
+    B, H = 3, 4
+    q, _, _ = O.make_inputs((B, H, D), seed=70)
+    _, k, v = O.make_inputs((B, H, D), seed=71)
+    rng = np.random.default_rng(72)
+    beta = rng.uniform(0.1, 0.5, (B, H)).astype(np.float32)
+    alpha = rng.uniform(0.9, 0.999, (B, H)).astype(np.float32)
+    st = rng.standard_normal((B * H, D, 2 * D)) * 0.05
+    BH = B * H
+    psi, phi = O.delta_features(q.reshape(BH, 1, D), k.reshape(BH, 1, D), eps=FEAT_EPS)
+    yo, so = O.delta_step(psi[:, 0], phi[:, 0], v.reshape(BH, D), beta.reshape(BH), alpha.reshape(BH),
+                          bound=bound, state=st)
+    s = to_dev(st.reshape(B, H, D, 2 * D))
+    y = torch.empty(B, H, D, device=dev())
+    _lib.delta_decode_step(to_dev(q, torch.bfloat16), to_dev(k, torch.bfloat16), to_dev(v, torch.bfloat16),
+                           to_dev(beta), to_dev(alpha), FEAT_EPS, bound, s, s, y)  # in place
+    torch.cuda.synchronize()
+    assert_close(to_np(y).reshape(BH, D), yo, 1e-4, "y")
+    assert_close(to_np(s).reshape(BH, D, 2 * D), so, 1e-4, "S")

@@ -319,3 +319,37 @@ def test_oracle_plant_check():
     y_bad, _ = O.recurrent(q, k, v, 0.95, state=stT)
     yc, _ = O.closed_form(q, k, v, 0.95, state=st)
     assert O.rel_err(y_bad, yc) > 1e-4
+
+
+# ---------------------------------------------------------------- delta step (L == 1 branch)
+def test_delta_step_known_answers():
+    """chunked_delta_prime.py:140-176: zero state gives S = beta v phi^T and
+    y = beta (phi . psi) v; a perfectly predicted value (v = S phi) or phi = 0
+    leaves alpha S; with alpha = 1 the step equals the decay-before-predict
+    per-token rule; the clamp bounds |S|_F."""
+    rng = np.random.default_rng(40)
+    BH, D = 3, 8
+    q, k = rng.standard_normal((2, BH, 1, D))
+    psi, phi = O.delta_features(q, k)
+    psi, phi = psi[:, 0], phi[:, 0]
+    v = rng.standard_normal((BH, D))
+    beta = rng.uniform(0.1, 0.5, BH)
+    alpha = rng.uniform(0.9, 0.99, BH)
+    y, S = O.delta_step(psi, phi, v, beta, alpha, bound=0.0)
+    _close(S, beta[:, None, None] * v[:, :, None] * phi[:, None, :])
+    _close(y, (beta * np.einsum("be,be->b", phi, psi))[:, None] * v)
+    S0 = rng.standard_normal((BH, D, 2 * D)) * 0.1
+    vp = np.einsum("bde,be->bd", S0, phi)
+    _, S1 = O.delta_step(psi, phi, vp, beta, alpha, bound=0.0, state=S0)
+    _close(S1, alpha[:, None, None] * S0)
+    _, S2 = O.delta_step(psi, np.zeros_like(phi), v, beta, alpha, bound=0.0, state=S0)
+    _close(S2, alpha[:, None, None] * S0)
+    one = np.ones(BH)
+    yt, St = O.delta_tokenwise(psi[:, None], phi[:, None], v[:, None], beta[:, None], one[:, None], state=S0)
+    ys, Ss = O.delta_step(psi, phi, v, beta, one, bound=0.0, state=S0)
+    _close(ys, yt[:, 0])
+    _close(Ss, St)
+    yb, Sb = O.delta_step(psi, phi, 50 * v, beta, alpha, bound=2.0, state=S0)
+    nrm = np.sqrt((Sb ** 2).sum(axis=(1, 2)))
+    assert np.all(np.abs(nrm - 2.0) < 1e-5), nrm
+    _close(yb, np.einsum("bde,be->bd", Sb, psi))
