@@ -16,6 +16,9 @@ The same JSON line carries
   decode        the fused decode step at B=512 sequences x 12 layers x 12 heads
                 (one launch per layer, states pre-filled by 1024 tokens) and at
                 B=256, tok/s and its own roofline;
+  delta         the chunked delta-rule prefill at config 5 (B=1, H=12,
+                L=131072): tok/s, per-kernel time, sustained tok/s per 16384
+                tokens and the memory in use (flat state);
   model         the PRIME-125M-shaped LM end to end: prefill tok/s (B=32 x
                 2048) and greedy decode tok/s at B=32 and B=256 (HIP-graph step);
   cpu_baseline  the reference's C99 engine (built from its sources into
@@ -54,6 +57,7 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode legs")
     ap.add_argument("--no-model", action="store_true", help="skip the PRIME-125M model leg")
+    ap.add_argument("--no-delta", action="store_true", help="skip the delta-rule (config 5) leg")
     ap.add_argument("--cpu-budget", type=float, default=8.0, help="seconds per CPU leg (approximate)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device copy 3 times (the reference kernel for "
@@ -244,6 +248,58 @@ def bench_model(args, torch, dev):
     return out
 
 
+# ----------------------------------------------------------------- delta rule
+def bench_delta(args, lib, torch, dev):
+    """Chunked gated delta-rule prefill: B=1, H=12, D=64,
+    L=131072, chunk 64, bf16 q/k/v (N(0,1), QK-normed, q / 8), beta ~
+    sigmoid(N(0,1)), alpha = per-head lambda ~ U[0.99, 0.9999], Lyapunov bound
+    25.  Whole-sequence tok/s, then the sequence again in 16384-token pieces
+    carrying the state, each piece timed, with the device memory in use after
+    each piece (flat state memory, sustained throughput)."""
+    B, H, L = 1, 12, 131072
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 5)
+    q, k, v = qkv((B, H, L, D), gen, dev, torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(B, H, L, device=dev, generator=gen)).contiguous()
+    lam = torch.empty(H, device=dev).uniform_(0.99, 0.9999, generator=gen)
+    alpha = lam.view(1, H, 1).expand(B, H, L).contiguous()
+    y = torch.empty(B, H, L, D, device=dev, dtype=torch.bfloat16)
+    st = torch.empty(B, H, D, 2 * D, device=dev)
+    ws = torch.empty(lib.delta_workspace_size(B, H, L), dtype=torch.uint8, device=dev)
+    run = lambda: lib.delta_prefill(q, k, v, beta, alpha, 0.9995, 1e-5, 25.0, None, y, st, workspace=ws)
+    run()
+    torch.cuda.synchronize()
+    lib.timer_reset()
+    lib.timer_enable(lib.KERNEL_DELTA_PREP, lib.KERNEL_DELTA_SCAN)
+    reps = 3
+    ms = timed(run, reps, 0)
+    lib.timer_enable()
+    kern = {lib.KERNEL_NAMES[kid]: kernel_ms(lib, kid) for kid in (lib.KERNEL_DELTA_PREP, lib.KERNEL_DELTA_SCAN)}
+    lib.timer_reset()
+    ok = bool(torch.isfinite(y).all().item())
+    nrm = float(st.norm(dim=(2, 3)).max().item())
+    # pieces of 16384 tokens, state carried in place
+    P = 16384
+    pieces = []
+    sp = torch.zeros(B, H, D, 2 * D, device=dev)
+    ws_p = torch.empty(lib.delta_workspace_size(B, H, P), dtype=torch.uint8, device=dev)
+    for i in range(L // P):
+        sl = slice(i * P, (i + 1) * P)
+        piece = lambda: lib.delta_prefill(q[:, :, sl], k[:, :, sl], v[:, :, sl], beta[:, :, sl].contiguous(),
+                                          alpha[:, :, sl].contiguous(), 0.9995, 1e-5, 25.0, sp, y[:, :, sl], sp,
+                                          workspace=ws_p)
+        t = timed(piece, 1, 0)
+        pieces.append({"tokens_end": (i + 1) * P, "tok_s": P / (t * 1e-3),
+                       "mem_allocated_MB": torch.cuda.memory_allocated(dev) / 1e6})
+    flops = B * H * L * (11 * 64 * D + 12 * D * D)
+    return {"workload": "chunked delta-rule prefill, BASELINE config 5: B=1 x H=12 x L=131072, D=64, chunk 64, "
+                        "bf16 q/k/v, beta ~ sigmoid(N(0,1)), alpha = per-head lambda U[0.99,0.9999], bound 25",
+            "tok_s": B * L / (ms * 1e-3), "ms": ms, "finite": ok, "state_norm_max": nrm,
+            "state_bytes": B * H * D * 2 * D * 4, "workspace_bytes": ws.numel(),
+            "tflops_algorithmic": flops / (ms * 1e-3) / 1e12,
+            "kernels": {n: {"avg_us": None if t is None else t * 1e3, "launches": c} for n, (t, c) in kern.items()},
+            "pieces_16384": pieces}
+
+
 # ----------------------------------------------------------------- CPU legs
 def cpu_cores():
     n = len(os.sched_getaffinity(0))
@@ -422,6 +478,8 @@ def main():
             if t is not None:
                 d["roofline"]["traffic"] = t.get("bytes_per_launch")
         rec["decode"] = {"B=256": d256, "B=512": d512}
+    if not args.no_delta:
+        rec["delta"] = bench_delta(args, lib, torch, dev)
     if not args.no_model:
         rec["model"] = bench_model(args, torch, dev)
     if not args.no_cpu:

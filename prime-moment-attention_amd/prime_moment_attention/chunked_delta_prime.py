@@ -1,0 +1,110 @@
+"""ChunkedGatedDeltaPrimeAttention: drop-in for the reference's chunked_delta_prime.py.
+
+Same constructor, parameters and ``forward(hidden_states, state=None,
+return_state=False) -> (out, next_state)`` as chunked_delta_prime.py:25-283,
+with the state an fp32 [B, H, D, 2D] tensor.  Projections, the erase/write
+gates, the LayerNorm QK-norm and o_proj are torch layers; the recurrence runs
+in the HIP kernels through the C ABI:
+
+  L == 1   prime_delta_decode_step  (the reference's step branch, :140-176,
+           which predicts with the undecayed state)
+  L >  1   prime_delta_prefill      (the chunked branch, :177-283)
+
+The per-token scalars the kernels take are the reference's: beta =
+0.5 mean(sigmoid(write)) and alpha = decay (1 - 0.5 mean(sigmoid(erase)))
+(:133-137).  The chunked branch clamps once per 64-token chunk, so its result
+depends on the chunk size; only ``chunk_size = 64`` (the reference default) is
+supported.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+
+class ChunkedGatedDeltaPrimeAttention(nn.Module):
+    def __init__(self, hidden_size: int, num_heads: int, head_dim: int, num_kv_heads: Optional[int] = None,
+                 chunk_size: int = 64, decay: float = 0.9995, use_qk_norm: bool = True,
+                 lyapunov_bound: float = 25.0, eps: float = 1e-5):
+        super().__init__()
+        if chunk_size != 64:
+            raise ValueError("chunk_size must be 64 (the Lyapunov clamp is applied per 64-token chunk)")
+        self.hidden_size = hidden_size
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.num_kv_heads = num_kv_heads or num_heads
+        self.num_kv_groups = num_heads // self.num_kv_heads
+        self.chunk_size = chunk_size
+        self.decay = decay
+        self.scaling = 1.0 / math.sqrt(head_dim)
+        self.use_qk_norm = use_qk_norm
+        self.lyapunov_bound = lyapunov_bound
+        self.eps = eps
+        self.q_proj = nn.Linear(hidden_size, num_heads * head_dim, bias=False)
+        self.k_proj = nn.Linear(hidden_size, self.num_kv_heads * head_dim, bias=False)
+        self.v_proj = nn.Linear(hidden_size, self.num_kv_heads * head_dim, bias=False)
+        self.o_proj = nn.Linear(num_heads * head_dim, hidden_size, bias=False)
+        self.erase_proj = nn.Linear(hidden_size, num_heads * head_dim, bias=True)
+        self.write_proj = nn.Linear(hidden_size, num_heads * head_dim, bias=True)
+        if use_qk_norm:
+            self.q_norm = nn.LayerNorm(head_dim)
+            self.k_norm = nn.LayerNorm(head_dim)
+        self._init_weights()
+
+    def _init_weights(self):
+        # gate biases as chunked_delta_prime.py:67-71 (erase ~ 0.05, write ~ 0.25)
+        nn.init.constant_(self.erase_proj.bias, -2.5)
+        nn.init.constant_(self.write_proj.bias, -1.0)
+
+    def gates(self, hidden_states: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(beta, alpha) fp32 [B, H, L] (chunked_delta_prime.py:110-111, 133-137)."""
+        B, L, _ = hidden_states.shape
+        H, D = self.num_heads, self.head_dim
+        b = torch.sigmoid(self.erase_proj(hidden_states)).view(B, L, H, D).float().mean(-1)
+        w = torch.sigmoid(self.write_proj(hidden_states)).view(B, L, H, D).float().mean(-1)
+        beta = (w * 0.5).transpose(1, 2).contiguous()
+        alpha = (self.decay * (1.0 - b * 0.5)).transpose(1, 2).contiguous()
+        return beta, alpha
+
+    def project(self, hidden_states: torch.Tensor):
+        """q (scaled), k, v as [B, H(kv), L, D] (chunked_delta_prime.py:105-126)."""
+        B, L, _ = hidden_states.shape
+        q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
+        k = self.k_proj(hidden_states).view(B, L, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        v = self.v_proj(hidden_states).view(B, L, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        if self.use_qk_norm:
+            q = self.q_norm(q)
+            k = self.k_norm(k)
+        return q * self.scaling, k, v
+
+    def forward(self, hidden_states: torch.Tensor, state: Optional[torch.Tensor] = None,
+                return_state: bool = False) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        B, L, _ = hidden_states.shape
+        H, D = self.num_heads, self.head_dim
+        dtype, dev = hidden_states.dtype, hidden_states.device
+        q, k, v = self.project(hidden_states)
+        beta, alpha = self.gates(hidden_states)
+        if q.dtype not in (torch.bfloat16, torch.float32):
+            q, k, v = q.float(), k.float(), v.float()
+        y_dtype = dtype if dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
+        s_in = None
+        if state is not None:
+            s_in = state.to(device=dev, dtype=torch.float32).reshape(B, H, D, 2 * D).contiguous()
+        s_out = torch.empty(B, H, D, 2 * D, device=dev, dtype=torch.float32)
+        if L == 1:
+            y = torch.empty(B, H, D, device=dev, dtype=y_dtype)
+            _lib.delta_decode_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], beta, alpha, self.eps,
+                                   self.lyapunov_bound, s_in, s_out, y)
+            y = y.unsqueeze(2)
+        else:
+            q, k, v = (t if (t.stride(-1) == 1 and all((s * t.element_size()) % 16 == 0 for s in t.stride()[:-1]))
+                       else t.contiguous() for t in (q, k, v))
+            y = torch.empty(B, H, L, D, device=dev, dtype=y_dtype)
+            _lib.delta_prefill(q, k, v, beta, alpha, self.decay, self.eps, self.lyapunov_bound, s_in, y, s_out)
+        y = y.to(dtype).transpose(1, 2).reshape(B, L, H * D)
+        return self.o_proj(y), (s_out if return_state else None)

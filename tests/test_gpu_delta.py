@@ -141,3 +141,52 @@ def test_delta_decode_step_matches_oracle(bound):
     torch.cuda.synchronize()
     assert_close(to_np(y).reshape(BH, D), yo, 1e-4, "y")
     assert_close(to_np(s).reshape(BH, D, 2 * D), so, 1e-4, "S")
+
+
+def _module_ref(mod, x, state=None):
+    """fp64 CPU composition of the module (chunked_delta_prime.py:89-283):
+    torch layers for projections, gates and LayerNorm, the oracle for the core."""
+    import torch.nn.functional as F
+    W = {k: v.detach().double().cpu() for k, v in mod.state_dict().items()}
+    xd = x.detach().double().cpu()
+    B, L, _ = xd.shape
+    H, Dh = mod.num_heads, mod.head_dim
+    proj = lambda n: (xd @ W[n + ".weight"].T + (W[n + ".bias"] if n + ".bias" in W else 0))
+    q = proj("q_proj").view(B, L, H, Dh).transpose(1, 2)
+    k = proj("k_proj").view(B, L, H, Dh).transpose(1, 2)
+    v = proj("v_proj").view(B, L, H, Dh).transpose(1, 2)
+    bg = torch.sigmoid(proj("erase_proj")).view(B, L, H, Dh).transpose(1, 2)
+    wg = torch.sigmoid(proj("write_proj")).view(B, L, H, Dh).transpose(1, 2)
+    q = F.layer_norm(q, (Dh,), W["q_norm.weight"], W["q_norm.bias"]) / 8.0
+    k = F.layer_norm(k, (Dh,), W["k_norm.weight"], W["k_norm.bias"])
+    beta = (wg.mean(-1) * 0.5).numpy()
+    alpha = (mod.decay * (1.0 - bg.mean(-1) * 0.5)).numpy()
+    BH = B * H
+    psi, phi = O.delta_features(q.reshape(BH, L, Dh).numpy(), k.reshape(BH, L, Dh).numpy(), eps=mod.eps)
+    if L == 1:
+        y, S = O.delta_step(psi[:, 0], phi[:, 0], v.reshape(BH, Dh).numpy(), beta.reshape(BH), alpha.reshape(BH),
+                            bound=mod.lyapunov_bound, state=state)
+        y = y[:, None]
+    else:
+        y, S = O.delta_chunked(psi, phi, v.reshape(BH, L, Dh).numpy(), beta.reshape(BH, L), alpha.reshape(BH, L),
+                               mod.decay, bound=mod.lyapunov_bound, chunk=64, state=state)
+    y = torch.from_numpy(y).view(B, H, L, Dh).transpose(1, 2).reshape(B, L, H * Dh)
+    return (y @ W["o_proj.weight"].T).numpy(), S
+
+
+def test_delta_module_prefill_then_step_matches_composition():
+    """The module's chunked (L = 100) and step (L = 1) branches against the fp64
+    composition of the same weights, the step continuing the prefill state."""
+    from prime_moment_attention import ChunkedGatedDeltaPrimeAttention
+    torch.manual_seed(0)
+    mod = ChunkedGatedDeltaPrimeAttention(128, 2, 64, decay=0.99).to(dev())
+    x = torch.randn(2, 101, 128, device=dev())
+    with torch.no_grad():
+        out, st = mod(x[:, :100], return_state=True)
+        out1, st1 = mod(x[:, 100:], state=st, return_state=True)
+    ref, S = _module_ref(mod, x[:, :100])
+    assert_close(to_np(out), ref, TOL_BF16, "prefill out")
+    assert_close(to_np(st).reshape(S.shape), S, TOL_BF16, "prefill state")
+    ref1, S1 = _module_ref(mod, x[:, 100:], state=S)
+    assert_close(to_np(out1), ref1, TOL_BF16, "step out")
+    assert_close(to_np(st1).reshape(S1.shape), S1, TOL_BF16, "step state")
