@@ -210,8 +210,8 @@ int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const 
         return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes is below the minimum %zu", workspace_bytes,
                     sbytes + S * prime::kDeltaRecBytes);
     const int NC = (L + prime::kDeltaChunk - 1) / prime::kDeltaChunk;
-    const size_t cap = (workspace_bytes - sbytes) / (S * prime::kDeltaRecBytes);
-    const int window = static_cast<int>(cap < static_cast<size_t>(NC) ? cap : static_cast<size_t>(NC));
+    const size_t cap_sz = (workspace_bytes - sbytes) / (S * prime::kDeltaRecBytes);
+    const int cap = static_cast<int>(cap_sz < static_cast<size_t>(NC) ? cap_sz : static_cast<size_t>(NC) + 1);
 
     prime::DeltaArgs a{};
     a.q = q->data; a.k = k->data; a.v = v->data;
@@ -227,7 +227,7 @@ int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const 
     a.y_sb = y->stride_b; a.y_sh = y->stride_h; a.y_sl = y->stride_l;
     a.ws_state = static_cast<float *>(workspace);
     a.ws_rec = static_cast<uint8_t *>(workspace) + sbytes;
-    return check_hip(prime::launch_delta_prefill(a, NC, window, static_cast<hipStream_t>(stream)),
+    return check_hip(prime::launch_delta_prefill(a, NC, cap, static_cast<hipStream_t>(stream)),
                      "delta prefill launch");
 }
 

@@ -18,14 +18,16 @@
 //   delta_scan_kernel (one workgroup per (sequence, head), chunks in order):
 //     y^T = Y0^T + S Z^T and S'^T = e^cum_63 S^T - M^T S^T + R0^T on bf16 MFMA,
 //     the state S^T held in fp32 accumulators, then the clamp (one barrier).
-// The scan's MFMA operands of S come straight from its accumulators: lane l
-// holds S^T[16eb + 4g + r][d = 16w + l%16] (g = l/16), and the 8 k-slots of an
+// The scan's MFMA operands of S are its accumulators repacked: lane l holds
+// S^T[16eb + 4g + r][d = 16dw + l%16] (g = l/16), and the 8 k-slots of an
 // operand take rows 4g..4g+3 of two adjacent 16-row tiles, a fixed permutation
 // of the contraction index that the prep kernel applies to the other operand.
 // Records are written in exactly the lane order the scan reads them.
 //
 // The sequence is processed in windows of chunks (prep then scan per window),
 // so the workspace is bounded by the window, not by L.
+
+#include <mutex>
 
 #include "prefill_common.h"
 
@@ -39,11 +41,9 @@ constexpr int kP72 = kD + 8;      // 64-wide rows, 16 / 8-byte row reads
 constexpr int kP80 = kD + 16;     // 64-wide rows, transposed reads
 constexpr int kRecMT = 0;         // -M^T A operands   [8 eb'][4 ks][64 lanes] x 16 B
 constexpr int kRecZB = 32768;     // Z^T B operands    [4 tb][4 ks][64 lanes] x 16 B
-constexpr int kRecR0 = 49152;     // R0^T acc tiles    [4 w][8 eb][64 lanes] x 8 B (bf16x4)
-constexpr int kRecY0 = 65536;     // Y0^T acc tiles    [4 w][4 tb][64 lanes] x 8 B
+constexpr int kRecR0 = 49152;     // R0^T acc tiles    [8 eb][4 dw][64 lanes] x 8 B (bf16x4)
+constexpr int kRecY0 = 65536;     // Y0^T acc tiles    [4 tb][4 dw][64 lanes] x 8 B
 constexpr int kRecSC = 73728;     // e^cum_63 (fp32)
-constexpr int kRecVec = static_cast<int>(kDeltaRecBytes / 16);  // 16-byte vectors per record
-constexpr int kPre = (kRecVec + 255) / 256;                      // per-thread prefetch vectors
 
 static_assert(kRecSC + 16 <= static_cast<int>(kDeltaRecBytes), "record layout");
 
@@ -262,7 +262,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
             const bf16x8 ab = row8p(&sA[16 * tb + c16][0], 32 * kt + 4 * g);
             acc = mfma(ua, ab, acc);
         }
-        *reinterpret_cast<uint2 *>(rec + kRecY0 + ((w * 4 + tb) * 64 + lane) * 8) = pack4(acc);
+        *reinterpret_cast<uint2 *>(rec + kRecY0 + ((tb * 4 + w) * 64 + lane) * 8) = pack4(acc);
     }
     // Z^T tiles (feature blocks 2w, 2w+1; token block tb) = diag(e^cum) Psi^T - W^T A^T
 #pragma unroll
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
                 const bf16x8 ub = tr8(&sUw[32 * kt + 4 * g + tr_r][16 * dw + tr_c], kP80);
                 acc = mfma(pa, ub, acc);
             }
-            *reinterpret_cast<uint2 *>(rec + kRecR0 + ((dw * 8 + eb) * 64 + lane) * 8) = pack4(acc);
+            *reinterpret_cast<uint2 *>(rec + kRecR0 + ((eb * 4 + dw) * 64 + lane) * 8) = pack4(acc);
         }
     }
     // -M^T as the scan's A operands: M tiles (rows e in blocks 2w, 2w+1; columns e')
@@ -328,10 +328,122 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
 
 // ---------------------------------------------------------------------------
 // Sequential scan over a window's chunks.  One workgroup (4 waves) per
-// (sequence, head); wave w owns value columns d in [16w, 16w + 16).
+// (sequence, head).  Wave w owns the state rows of feature blocks 2w, 2w+1
+// (S^T tiles for every value block dw) and the y tiles of token block w; it
+// loads only its quarter of each chunk's record, into registers, one chunk
+// ahead.  The waves exchange the state as bf16 MFMA operand packs through LDS
+// (pack (dw, ks) = rows 4g..4g+3 of feature blocks 2ks and 2ks+1 at value
+// column 16dw + l%16, written by wave ks).  The Lyapunov scale of chunk c is
+// applied inside chunk c+1 (the packs hold the unscaled state), so one barrier
+// per chunk suffices:
+//   y_c      = Y0 + sc_c (S~_c Z^T)
+//   S~_{c+1} = sc_c (e^cum_63 S~_c - M^T S~_c) + R0,  sc_{c+1} from |S~_{c+1}|_F.
 // ---------------------------------------------------------------------------
+namespace {
+
+// one wave's quarter of a chunk record, in registers
+struct RecQ {
+    bf16x8 mt[2][4];  // -M^T A operands: feature block 2w + hf, k-step ks
+    bf16x8 zb[4];     // Z^T B operands: token block w, k-step ks
+    uint2 r0[2][4];   // R0^T tiles: feature block 2w + hf, value block dw
+    uint2 y0[4];      // Y0^T tiles: value block dw, token block w
+    float e63;
+};
+
+__device__ __forceinline__ void load_recq(RecQ &R, const uint8_t *rec, int w, int lane) {
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            R.mt[hf][ks] = *reinterpret_cast<const bf16x8 *>(rec + kRecMT + (((2 * w + hf) * 4 + ks) * 64 + lane) * 16);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        R.zb[ks] = *reinterpret_cast<const bf16x8 *>(rec + kRecZB + ((w * 4 + ks) * 64 + lane) * 16);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int dw = 0; dw < 4; ++dw)
+            R.r0[hf][dw] = *reinterpret_cast<const uint2 *>(rec + kRecR0 + (((2 * w + hf) * 4 + dw) * 64 + lane) * 8);
+#pragma unroll
+    for (int dw = 0; dw < 4; ++dw)
+        R.y0[dw] = *reinterpret_cast<const uint2 *>(rec + kRecY0 + ((w * 4 + dw) * 64 + lane) * 8);
+    R.e63 = *reinterpret_cast<const float *>(rec + kRecSC);
+}
+
+}  // namespace
+
+// One chunk of the scan (see above).  `cur` holds this chunk's record quarter;
+// `nxt` receives the next chunk's.  Called with the two register sets swapped
+// on alternate chunks, so that no copy (and no wait for the loads) is needed.
+__device__ __forceinline__ void scan_chunk(const DeltaArgs &a, int cw, int b, int h, int w, int lane, int g, int c16,
+                                           const uint8_t *rbase, f32x4 (&st)[2][4], float &sc, const RecQ &cur,
+                                           RecQ &nxt, bf16x8 (*sPk)[4][4][64], float (*sRed)[4]) {
+    const int buf = cw & 1;
+    const int c = a.c0 + cw;
+    // next chunk's quarter (clamped to the window: the duplicate is unused)
+    load_recq(nxt, rbase + static_cast<size_t>(min(cw + 1, a.nw - 1)) * kDeltaRecBytes, w, lane);
+    bf16x8 pk[4][4];
+#pragma unroll
+    for (int dw = 0; dw < 4; ++dw)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) pk[dw][ks] = sPk[buf][dw][ks][lane];
+    // ---- y^T (value block dw, token block w) = Y0^T + sc S~ Z^T
+    const int t = c * kC + 16 * w + c16;
+#pragma unroll
+    for (int dw = 0; dw < 4; ++dw) {
+        f32x4 p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) p = mfma(pk[dw][ks], cur.zb[ks], p);
+        const f32x4 y0 = unpack4(cur.y0[dw]);
+        f32x4 yv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yv[r] = y0[r] + sc * p[r];
+        if (t < a.L) {
+            const int64_t o = b * a.y_sb + h * a.y_sh + t * a.y_sl + 16 * dw + 4 * g;
+            if (a.dt_y == PRIME_BF16) {
+                *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + o) = pack4(yv);
+            } else if (a.dt_y == PRIME_F32) {
+                *reinterpret_cast<f32x4 *>(static_cast<float *>(a.y) + o) = yv;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) store_elem(a.y, o + r, a.dt_y, yv[r]);
+            }
+        }
+    }
+    // ---- S~'^T = sc (e^cum_63 S~^T - M^T S~^T) + R0^T on this wave's feature blocks
+    float ss = 0.f;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int dw = 0; dw < 4; ++dw) {
+            f32x4 x;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) x[r] = cur.e63 * st[hf][dw][r];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) x = mfma(cur.mt[hf][ks], pk[dw][ks], x);
+            const f32x4 r0 = unpack4(cur.r0[hf][dw]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                x[r] = sc * x[r] + r0[r];
+                ss += x[r] * x[r];
+            }
+            st[hf][dw] = x;
+        }
+#pragma unroll
+    for (int dw = 0; dw < 4; ++dw) sPk[buf ^ 1][dw][w][lane] = pack8x(st[0][dw], st[1][dw]);
+    ss = wave_sum(ss);
+    if (lane == 0) sRed[buf][w] = ss;
+    __syncthreads();
+    // ---- Lyapunov clamp (:266-270), kept as the pending scale of the state
+    sc = 1.0f;
+    if (a.bound > 0.f) {
+        const float nrm = sqrtf(sRed[buf][0] + sRed[buf][1] + sRed[buf][2] + sRed[buf][3]);
+        sc = fminf(1.0f, a.bound / (nrm + 1e-6f));
+    }
+}
+
 __global__ __launch_bounds__(256, 1) void delta_scan_kernel(const DeltaArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t sRec[2][kDeltaRecBytes];
+    __shared__ __attribute__((aligned(16))) bf16x8 sPk[2][4][4][64];  // [buf][dw][ks][lane]
     __shared__ float sRed[2][4];
 
     const int tid = threadIdx.x;
@@ -342,105 +454,43 @@ __global__ __launch_bounds__(256, 1) void delta_scan_kernel(const DeltaArgs a) {
     const int b = seq / a.H, h = seq - b * a.H;
     const int w = wave;
     const size_t sofs = static_cast<size_t>(seq) * kD * kP;
+    const uint8_t *rbase = a.ws_rec + static_cast<size_t>(seq) * a.nw * kDeltaRecBytes;
 
-    // ---- state entering the window: S^T tiles st[eb][r] = S[d = 16w + c16][e = 16eb + 4g + r]
+    // ---- state entering the window: st[hf][dw][r] = S[d = 16dw + c16][e = 16(2w + hf) + 4g + r]
     const float *src = a.first ? a.state_in : a.ws_state;
-    f32x4 st[8];
+    f32x4 st[2][4];
 #pragma unroll
-    for (int eb = 0; eb < 8; ++eb) {
-        if (src) st[eb] = *reinterpret_cast<const f32x4 *>(src + sofs + (16 * w + c16) * kP + 16 * eb + 4 * g);
-        else st[eb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    // ---- record staging: global -> registers one chunk ahead -> LDS
-    u32x4 pre[kPre];
-    // (unconditional loads; the tail index is clamped into the record and its
-    // duplicate never staged)
-    auto fetch = [&](int cw) {
-        const uint8_t *rec = a.ws_rec + (static_cast<size_t>(seq) * a.nw + cw) * kDeltaRecBytes;
+    for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-        for (int k = 0; k < kPre; ++k) {
-            const int v = min(tid + 256 * k, kRecVec - 1);
-            pre[k] = *reinterpret_cast<const u32x4 *>(rec + 16 * v);
-        }
-    };
-    auto stage = [&](int buf) {
+        for (int dw = 0; dw < 4; ++dw)
+            st[hf][dw] = src ? *reinterpret_cast<const f32x4 *>(src + sofs + (16 * dw + c16) * kP + 16 * (2 * w + hf) + 4 * g)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < kPre; ++k) {
-            const int v = tid + 256 * k;
-            if (k < kPre - 1 || v < kRecVec) *reinterpret_cast<u32x4 *>(&sRec[buf][16 * v]) = pre[k];
-        }
-    };
-    fetch(0);
-    stage(0);
-    if (a.nw > 1) fetch(1);
+    for (int dw = 0; dw < 4; ++dw) sPk[0][dw][w][lane] = pack8x(st[0][dw], st[1][dw]);
+    float sc = 1.0f;  // pending Lyapunov scale of the state in st / the packs
+    RecQ ra, rb;
+    load_recq(ra, rbase, w, lane);
     __syncthreads();
 
-    for (int cw = 0; cw < a.nw; ++cw) {
-        const int buf = cw & 1;
-        const uint8_t *R = sRec[buf];
-        const int c = a.c0 + cw;
-        // S operand packs (A of S Z^T, B of M^T S^T): k-slots = rows 4g..4g+3 of tiles 2ks, 2ks+1
-        bf16x8 sb[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) sb[ks] = pack8x(st[2 * ks], st[2 * ks + 1]);
-        // ---- y^T (d-block w, token block tb) = Y0^T + S Z^T
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-            f32x4 acc = unpack4(*reinterpret_cast<const uint2 *>(R + kRecY0 + ((w * 4 + tb) * 64 + lane) * 8));
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                acc = mfma(sb[ks], *reinterpret_cast<const bf16x8 *>(R + kRecZB + ((tb * 4 + ks) * 64 + lane) * 16), acc);
-            const int t = c * kC + 16 * tb + c16;
-            if (t < a.L) {
-                const int64_t o = b * a.y_sb + h * a.y_sh + t * a.y_sl + 16 * w + 4 * g;
-                if (a.dt_y == PRIME_BF16) {
-                    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + o) = pack4(acc);
-                } else if (a.dt_y == PRIME_F32) {
-                    *reinterpret_cast<f32x4 *>(static_cast<float *>(a.y) + o) = acc;
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) store_elem(a.y, o + r, a.dt_y, acc[r]);
-                }
-            }
-        }
-        // ---- S'^T = e^cum_63 S^T + R0^T - M^T S^T
-        const float e63 = *reinterpret_cast<const float *>(R + kRecSC);
-        float ss = 0.f;
-#pragma unroll
-        for (int eb = 0; eb < 8; ++eb) {
-            const f32x4 r0 = unpack4(*reinterpret_cast<const uint2 *>(R + kRecR0 + ((w * 8 + eb) * 64 + lane) * 8));
-            f32x4 n;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) n[r] = e63 * st[eb][r] + r0[r];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                n = mfma(*reinterpret_cast<const bf16x8 *>(R + kRecMT + ((eb * 4 + ks) * 64 + lane) * 16), sb[ks], n);
-            st[eb] = n;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ss += n[r] * n[r];
-        }
-        ss = wave_sum(ss);
-        if (lane == 0) sRed[buf][w] = ss;
-        if (cw + 1 < a.nw) stage(buf ^ 1);
-        if (cw + 2 < a.nw) fetch(cw + 2);
-        __syncthreads();
-        // ---- Lyapunov clamp (:266-270)
-        if (a.bound > 0.f) {
-            const float nrm = sqrtf(sRed[buf][0] + sRed[buf][1] + sRed[buf][2] + sRed[buf][3]);
-            const float sc = fminf(1.0f, a.bound / (nrm + 1e-6f));
-#pragma unroll
-            for (int eb = 0; eb < 8; ++eb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) st[eb][r] *= sc;
-        }
+    int cw = 0;
+    for (; cw + 1 < a.nw; cw += 2) {
+        scan_chunk(a, cw, b, h, w, lane, g, c16, rbase, st, sc, ra, rb, sPk, sRed);
+        scan_chunk(a, cw + 1, b, h, w, lane, g, c16, rbase, st, sc, rb, ra, sPk, sRed);
     }
+    if (cw < a.nw) scan_chunk(a, cw, b, h, w, lane, g, c16, rbase, st, sc, ra, rb, sPk, sRed);
 
-    // ---- state leaving the window
+    // ---- state leaving the window (the pending scale applied)
     float *dst = a.last ? a.state_out : a.ws_state;
     if (dst) {
 #pragma unroll
-        for (int eb = 0; eb < 8; ++eb)
-            *reinterpret_cast<f32x4 *>(dst + sofs + (16 * w + c16) * kP + 16 * eb + 4 * g) = st[eb];
+        for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+            for (int dw = 0; dw < 4; ++dw) {
+                f32x4 x = st[hf][dw];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) x[r] *= sc;
+                *reinterpret_cast<f32x4 *>(dst + sofs + (16 * dw + c16) * kP + 16 * (2 * w + hf) + 4 * g) = x;
+            }
     }
 }
 
@@ -508,23 +558,102 @@ __global__ __launch_bounds__(kStepWaves * 64) void delta_step_kernel(const Delta
     }
 }
 
-hipError_t launch_delta_prefill(DeltaArgs a, int NC, int window, hipStream_t stream) {
-    const int Sq = a.B * a.H;
-    for (int c0 = 0; c0 < NC; c0 += window) {
-        a.c0 = c0;
-        a.nw = NC - c0 < window ? NC - c0 : window;
-        a.first = c0 == 0;
-        a.last = c0 + a.nw >= NC;
-        timer_begin(PRIME_KERNEL_DELTA_PREP, stream);
-        hipLaunchKernelGGL(delta_prep_kernel, dim3(Sq * a.nw), dim3(256), 0, stream, a);
-        timer_end(PRIME_KERNEL_DELTA_PREP, stream);
-        timer_begin(PRIME_KERNEL_DELTA_SCAN, stream);
-        hipLaunchKernelGGL(delta_scan_kernel, dim3(Sq), dim3(256), 0, stream, a);
-        timer_end(PRIME_KERNEL_DELTA_SCAN, stream);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+namespace {
+
+// Per-device side stream and events for overlapping the prep of window w+1 with
+// the scan of window w (the scan occupies one CU per (sequence, head); the
+// prep fills the rest).  Created once per device, default priority, kept for
+// the life of the process.
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t start = nullptr, prep[2] = {nullptr, nullptr}, scan[2] = {nullptr, nullptr};
+    bool ok = false;
+};
+
+std::mutex g_side_mu;
+SideStream g_side[64];
+
+SideStream *side_stream() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lk(g_side_mu);
+    SideStream &x = g_side[dev];
+    if (!x.ok) {
+        const unsigned f = hipEventDisableTiming;
+        if (hipStreamCreateWithFlags(&x.s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+        if (hipEventCreateWithFlags(&x.start, f) != hipSuccess) return nullptr;
+        for (int i = 0; i < 2; ++i)
+            if (hipEventCreateWithFlags(&x.prep[i], f) != hipSuccess ||
+                hipEventCreateWithFlags(&x.scan[i], f) != hipSuccess)
+                return nullptr;
+        x.ok = true;
     }
-    return hipSuccess;
+    return &x;
+}
+
+void launch_prep(const DeltaArgs &a, hipStream_t s) {
+    timer_begin(PRIME_KERNEL_DELTA_PREP, s);
+    hipLaunchKernelGGL(delta_prep_kernel, dim3(a.B * a.H * a.nw), dim3(256), 0, s, a);
+    timer_end(PRIME_KERNEL_DELTA_PREP, s);
+}
+
+void launch_scan(const DeltaArgs &a, hipStream_t s) {
+    timer_begin(PRIME_KERNEL_DELTA_SCAN, s);
+    hipLaunchKernelGGL(delta_scan_kernel, dim3(a.B * a.H), dim3(256), 0, s, a);
+    timer_end(PRIME_KERNEL_DELTA_SCAN, s);
+}
+
+DeltaArgs window_args(DeltaArgs a, int c0, int window, int NC, uint8_t *rec) {
+    a.c0 = c0;
+    a.nw = NC - c0 < window ? NC - c0 : window;
+    a.first = c0 == 0;
+    a.last = c0 + a.nw >= NC;
+    a.ws_rec = rec;
+    return a;
+}
+
+}  // namespace
+
+// `cap` = chunks of record space per (sequence, head) in the workspace.  One
+// window when the sequence fits; otherwise two record halves alternate: the
+// prep of window w+1 (side stream) writes one half while the scan of window w
+// (caller's stream) reads the other.
+hipError_t launch_delta_prefill(DeltaArgs a, int NC, int cap, hipStream_t stream) {
+    uint8_t *rec0 = a.ws_rec;
+    if (NC <= cap || cap < 2) {
+        const int window = NC <= cap ? NC : cap;
+        for (int c0 = 0; c0 < NC; c0 += window) {
+            const DeltaArgs w = window_args(a, c0, window, NC, rec0);
+            launch_prep(w, stream);
+            launch_scan(w, stream);
+        }
+        return hipGetLastError();
+    }
+    SideStream *ss = side_stream();
+    if (!ss) return hipErrorOutOfMemory;
+    const int half = cap / 2;
+    const size_t half_bytes = static_cast<size_t>(a.B) * a.H * half * kDeltaRecBytes;
+    const int nwin = (NC + half - 1) / half;
+    hipError_t e;
+    if ((e = hipEventRecord(ss->start, stream)) != hipSuccess) return e;
+    if ((e = hipStreamWaitEvent(ss->s, ss->start, 0)) != hipSuccess) return e;
+    // prep of window 0
+    launch_prep(window_args(a, 0, half, NC, rec0), ss->s);
+    if ((e = hipEventRecord(ss->prep[0], ss->s)) != hipSuccess) return e;
+    for (int w = 0; w < nwin; ++w) {
+        const int hb = w & 1;
+        if ((e = hipStreamWaitEvent(stream, ss->prep[hb], 0)) != hipSuccess) return e;
+        launch_scan(window_args(a, w * half, half, NC, rec0 + hb * half_bytes), stream);
+        if ((e = hipEventRecord(ss->scan[hb], stream)) != hipSuccess) return e;
+        if (w + 1 < nwin) {
+            const int nb = hb ^ 1;
+            // the half about to be overwritten was read by the scan of window w-1
+            if (w >= 1 && (e = hipStreamWaitEvent(ss->s, ss->scan[nb], 0)) != hipSuccess) return e;
+            launch_prep(window_args(a, (w + 1) * half, half, NC, rec0 + nb * half_bytes), ss->s);
+            if ((e = hipEventRecord(ss->prep[nb], ss->s)) != hipSuccess) return e;
+        }
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_delta_step(const DeltaStepArgs &a, hipStream_t stream) {

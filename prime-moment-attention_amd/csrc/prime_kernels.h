@@ -86,10 +86,11 @@ struct DeltaStepArgs {
 constexpr int kDeltaChunk = 64;
 constexpr size_t kDeltaStateBytes = static_cast<size_t>(kD) * 2 * kD * sizeof(float);  // one (b,h) state
 constexpr size_t kDeltaRecBytes = 73984;         // per-chunk transfer record (multiple of 256)
-constexpr int kDeltaDefaultWindow = 128;         // chunks per window with the recommended workspace
+constexpr int kDeltaDefaultWindow = 128;         // record chunks of the recommended workspace
 
-// Launch the delta prefill over every window (prep + scan per window).
-hipError_t launch_delta_prefill(DeltaArgs a, int NC, int window, hipStream_t stream);
+// Launch the delta prefill over every window (prep + scan per window); cap =
+// chunks of record space per (sequence, head) in the workspace.
+hipError_t launch_delta_prefill(DeltaArgs a, int NC, int cap, hipStream_t stream);
 hipError_t launch_delta_step(const DeltaStepArgs &a, hipStream_t stream);
 
 // bf16-input prefill kernels (prefill_bf16.hip): the state-only segment pass

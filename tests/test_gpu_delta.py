@@ -87,14 +87,17 @@ def test_delta_prefill_without_clamp_equals_tokenwise():
 
 
 @pytest.mark.parametrize("with_state", [False, True])
-def test_delta_prefill_windows_agree(with_state):
-    """A workspace for one chunk per window (state carried between windows
-    through the workspace, in place) gives the same result as one window."""
+@pytest.mark.parametrize("ws_chunks", [1, 4])
+def test_delta_prefill_windows_agree(with_state, ws_chunks):
+    """Workspaces for one chunk (one-chunk windows in order) and for four
+    chunks (two-chunk windows whose prep runs on the side stream, overlapped
+    with the previous window's scan), the state carried between windows
+    through the workspace and updated in place, give the one-window result."""
     B, H, L = 1, 2, 64 * 5 + 17
     q, k, v, beta, alpha = _inputs(B, H, L, seed=62)
     st = np.random.default_rng(63).standard_normal((B * H, D, 2 * D)) * 0.05 if with_state else None
     y1, s1 = _run(q, k, v, beta, alpha, 0.995, 25.0, st)
-    small = torch.empty(_lib.delta_workspace_size(B, H, 64), dtype=torch.uint8, device=dev())
+    small = torch.empty(_lib.delta_workspace_size(B, H, 64 * ws_chunks), dtype=torch.uint8, device=dev())
     y2, s2 = _run(q, k, v, beta, alpha, 0.995, 25.0, st, workspace=small, inplace=True)
     assert_close(y2, y1, 1e-5, "y")
     assert_close(s2, s1, 1e-5, "S")
