@@ -89,6 +89,41 @@ int prime_decode_step(const prime_tensor_t *q, const prime_tensor_t *k,
                       void *stream);
 
 /*
+ * The module's QK prologue, applied inside the decode step
+ * (attention.py:96-101): q <- LayerNorm(q) * q_scale, k <- LayerNorm(k), each
+ * over the head dim with the affine weight and bias (dtype `dtype`, [D] each)
+ * and `eps`; the LayerNorm output is rounded to q's / k's dtype first, as the
+ * module's LayerNorm returns it.  q_weight NULL: no LayerNorm, only q_scale.
+ */
+typedef struct prime_qk_norm {
+    const void *q_weight, *q_bias, *k_weight, *k_bias;
+    int32_t dtype;   /* of the four vectors */
+    float eps;       /* LayerNorm eps (torch default 1e-5) */
+    float q_scale;   /* 1/sqrt(D) for the module; 1 when q is pre-scaled */
+} prime_qk_norm_t;
+
+/*
+ * prime_decode_step on the raw projections: q, k are the q_proj / k_proj
+ * outputs, normalised and scaled in the kernel by `norm` (see above).  Replaces
+ * attention.py:96-143 for L == 1.
+ */
+int prime_decode_step_qknorm(const prime_tensor_t *q, const prime_tensor_t *k,
+                             const prime_tensor_t *v, int B, int H, int H_kv, int D,
+                             const float *decay, float eps, const prime_qk_norm_t *norm,
+                             const prime_state_t *state_in, const prime_state_t *state_out,
+                             const prime_tensor_t *y, void *stream);
+
+/*
+ * Residual add + RMSNorm of the PRIME decoder blocks (model.py:47-56, 107-118):
+ * x <- x + delta (when delta is not NULL; the sum rounded to `dtype`, as the
+ * block's residual add stores it), then out <- x * rsqrt(mean(x^2) + eps) *
+ * weight.  x, delta, out: [rows, hidden] contiguous, weight [hidden]; one dtype
+ * (F32 / BF16 / F16); hidden a multiple of 4.  out may be x.
+ */
+int prime_add_rmsnorm(void *x, const void *delta, const void *weight, void *out, int rows,
+                      int hidden, int dtype, float eps, void *stream);
+
+/*
  * Chunked prefill of L tokens for B x H sequences.  Replaces
  * chunked_prime_ssd_core (chunked_ssd.py:48-184) and, with
  * PRIME_FLAG_DENSE_CLAMP, the dense branch of PrimeMomentAttention.forward

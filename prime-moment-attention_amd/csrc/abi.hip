@@ -87,10 +87,13 @@ int prime_abi_version(void) { return PRIME_ABI_VERSION; }
 
 const char *prime_last_error(void) { return g_err; }
 
-int prime_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
-                      int B, int H, int H_kv, int D, const float *decay, float eps,
-                      const prime_state_t *state_in, const prime_state_t *state_out,
-                      const prime_tensor_t *y, void *stream) {
+}  // extern "C"
+
+namespace {
+
+int decode_impl(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv,
+                int D, const float *decay, float eps, const prime_qk_norm_t *norm, const prime_state_t *state_in,
+                const prime_state_t *state_out, const prime_tensor_t *y, void *stream) {
     g_err[0] = 0;
     if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !decay || !state_out)
         return fail(PRIME_ERR_INVALID_ARG, "prime_decode_step: null argument");
@@ -105,6 +108,10 @@ int prime_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const pr
     if ((rc = check_state_alias(state_in, state_out, static_cast<size_t>(B) * H, D, &inplace))) return rc;
 
     prime::DecodeArgs a{};
+    if (norm) {
+        a.qn_w = norm->q_weight; a.qn_b = norm->q_bias; a.kn_w = norm->k_weight; a.kn_b = norm->k_bias;
+        a.dt_norm = norm->dtype; a.ln_eps = norm->eps;
+    }
     a.q = q->data; a.k = k->data; a.v = v->data;
     a.q_sb = q->stride_b; a.q_sh = q->stride_h;
     a.k_sb = k->stride_b; a.k_sh = k->stride_h;
@@ -119,7 +126,48 @@ int prime_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const pr
     a.s0o = state_out->s0; a.s1o = state_out->s1; a.s2o = state_out->s2;
     a.k0o = state_out->k0; a.k1o = state_out->k1; a.k2o = state_out->k2;
     a.y = y->data; a.dt_y = y->dtype; a.y_sb = y->stride_b; a.y_sh = y->stride_h;
+    a.q_scale = norm ? norm->q_scale : 1.0f;
     return check_hip(prime::launch_decode_step(a, static_cast<hipStream_t>(stream)), "decode launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int prime_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                      int B, int H, int H_kv, int D, const float *decay, float eps,
+                      const prime_state_t *state_in, const prime_state_t *state_out,
+                      const prime_tensor_t *y, void *stream) {
+    return decode_impl(q, k, v, B, H, H_kv, D, decay, eps, nullptr, state_in, state_out, y, stream);
+}
+
+int prime_decode_step_qknorm(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                             int B, int H, int H_kv, int D, const float *decay, float eps,
+                             const prime_qk_norm_t *norm, const prime_state_t *state_in,
+                             const prime_state_t *state_out, const prime_tensor_t *y, void *stream) {
+    g_err[0] = 0;
+    if (!norm) return fail(PRIME_ERR_INVALID_ARG, "prime_decode_step_qknorm: null norm");
+    if (norm->q_weight && (!norm->q_bias || !norm->k_weight || !norm->k_bias))
+        return fail(PRIME_ERR_INVALID_ARG, "prime_decode_step_qknorm: LayerNorm weight without bias");
+    if (!valid_dtype(norm->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported norm dtype");
+    return decode_impl(q, k, v, B, H, H_kv, D, decay, eps, norm, state_in, state_out, y, stream);
+}
+
+int prime_add_rmsnorm(void *x, const void *delta, const void *weight, void *out, int rows, int hidden,
+                      int dtype, float eps, void *stream) {
+    g_err[0] = 0;
+    if (!x || !weight || !out) return fail(PRIME_ERR_INVALID_ARG, "prime_add_rmsnorm: null argument");
+    if (rows <= 0 || hidden <= 0 || hidden % 4)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes rows=%d hidden=%d (hidden must be a multiple of 4)", rows,
+                    hidden);
+    if (!valid_dtype(dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dtype");
+    const size_t n = static_cast<size_t>(rows) * hidden * elem_size(dtype);
+    if (delta && overlap(delta, n, x, n)) return fail(PRIME_ERR_ALIAS, "delta overlaps x");
+    if (out != x && overlap(out, n, x, n)) return fail(PRIME_ERR_ALIAS, "out overlaps x without being x");
+    prime::RmsNormArgs a{};
+    a.x = x; a.delta = delta; a.weight = weight; a.out = out;
+    a.rows = rows; a.hidden = hidden; a.dt = dtype; a.eps = eps;
+    return check_hip(prime::launch_add_rmsnorm(a, static_cast<hipStream_t>(stream)), "add_rmsnorm launch");
 }
 
 int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,

@@ -41,6 +41,19 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
         vv = load_elem(a.v, b * a.v_sb + hk * a.v_sh + lane, a.dt_v);
         lam = a.decay[h];
     }
+    if (a.qn_w) {
+        // the module's QK LayerNorm (attention.py:96-98, biased variance),
+        // output rounded to the input dtype as the module's LayerNorm returns it
+        const float qm = wave_sum(qv) * (1.0f / kD), km = wave_sum(kv) * (1.0f / kD);
+        const float qd = qv - qm, kd = kv - km;
+        const float qr = rsqrtf(wave_sum(qd * qd) * (1.0f / kD) + a.ln_eps);
+        const float kr = rsqrtf(wave_sum(kd * kd) * (1.0f / kD) + a.ln_eps);
+        qv = qd * qr * load_elem(a.qn_w, lane, a.dt_norm) + load_elem(a.qn_b, lane, a.dt_norm);
+        kv = kd * kr * load_elem(a.kn_w, lane, a.dt_norm) + load_elem(a.kn_b, lane, a.dt_norm);
+        if (a.dt_q == PRIME_BF16) qv = bf16_bits_to_f32(f32_to_bf16_bits(qv));
+        if (a.dt_k == PRIME_BF16) kv = bf16_bits_to_f32(f32_to_bf16_bits(kv));
+    }
+    qv *= a.q_scale;  // 1/sqrt(D) (attention.py:101); exact for powers of two
 
     const int rg = lane >> 4;  // row group: rows 4r + rg
     const int cg = lane & 15;  // column group: columns 4cg..4cg+3

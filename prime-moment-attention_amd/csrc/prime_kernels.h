@@ -17,7 +17,23 @@ struct DecodeArgs {
     void *y;
     int dt_y;
     int64_t y_sb, y_sh;
+    // optional prologue: q <- LN(q) * q_scale, k <- LN(k) (LN over the head dim,
+    // affine; qn_w == nullptr: no LN), LN output rounded to dt_q / dt_k
+    const void *qn_w, *qn_b, *kn_w, *kn_b;
+    int dt_norm;
+    float ln_eps, q_scale;
 };
+
+// Residual add + RMSNorm rows (norm.hip).
+struct RmsNormArgs {
+    void *x;              // [rows, hidden], updated in place when delta is given
+    const void *delta;    // [rows, hidden] or null
+    const void *weight;   // [hidden]
+    void *out;            // [rows, hidden]
+    int rows, hidden, dt;
+    float eps;
+};
+hipError_t launch_add_rmsnorm(const RmsNormArgs &a, hipStream_t stream);
 
 struct PrefillArgs {
     const void *q, *k, *v;

@@ -25,7 +25,7 @@ _DTYPES = {torch.float32: PRIME_F32, torch.bfloat16: PRIME_BF16, torch.float16: 
 EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_chunked_prefill",
            "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
            "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
-           "prime_delta_decode_step")
+           "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm")
 
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
@@ -43,6 +43,12 @@ class PrimeTensor(ctypes.Structure):
 
 class PrimeState(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in ("s0", "s1", "s2", "k0", "k1", "k2")]
+
+
+class PrimeQkNorm(ctypes.Structure):
+    _fields_ = [("q_weight", ctypes.c_void_p), ("q_bias", ctypes.c_void_p), ("k_weight", ctypes.c_void_p),
+                ("k_bias", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("eps", ctypes.c_float),
+                ("q_scale", ctypes.c_float)]
 
 
 _lib = None
@@ -79,6 +85,11 @@ def load() -> ctypes.CDLL:
     L.prime_delta_decode_step.argtypes = [P(PrimeTensor)] * 3 + [fp, fp] + [ctypes.c_int] * 4 + [
         ctypes.c_float] * 2 + [fp, fp, P(PrimeTensor), fp]
     L.prime_delta_decode_step.restype = ctypes.c_int
+    L.prime_decode_step_qknorm.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 4 + [
+        ctypes.c_void_p, ctypes.c_float, P(PrimeQkNorm), P(PrimeState), P(PrimeState), P(PrimeTensor), ctypes.c_void_p]
+    L.prime_decode_step_qknorm.restype = ctypes.c_int
+    L.prime_add_rmsnorm.argtypes = [fp] * 4 + [ctypes.c_int] * 3 + [ctypes.c_float, fp]
+    L.prime_add_rmsnorm.restype = ctypes.c_int
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     v = L.prime_abi_version()
     if v != ABI_VERSION:
@@ -194,6 +205,56 @@ def decode_step(q, k, v, decay: torch.Tensor, eps: float, state_in, state_out, y
                              decay.data_ptr(), float(eps), ctypes.byref(si) if si else None,
                              ctypes.byref(so), ctypes.byref(yd), _stream(q.device))
     _check(rc, "prime_decode_step")
+
+
+def qk_norm(q_norm, k_norm, q_scale: float, dtype) -> PrimeQkNorm:
+    """prime_qk_norm_t for two nn.LayerNorm modules (or None: no LayerNorm) and
+    the q scale; the parameters must be on the device, in `dtype`."""
+    if q_norm is None:
+        return PrimeQkNorm(None, None, None, None, _DTYPES[dtype], 1e-5, float(q_scale))
+    ps = [q_norm.weight, q_norm.bias, k_norm.weight, k_norm.bias]
+    for t in ps:
+        if t is None or t.dtype != dtype or not t.is_contiguous():
+            raise ValueError(f"QK LayerNorm parameters must be contiguous {dtype} with bias")
+        _dev_check(t)
+    return PrimeQkNorm(*[t.data_ptr() for t in ps], _DTYPES[dtype], float(q_norm.eps), float(q_scale))
+
+
+def decode_step_qknorm(q, k, v, decay: torch.Tensor, eps: float, norm: PrimeQkNorm, state_in, state_out,
+                       y) -> None:
+    """prime_decode_step_qknorm: q, k the raw projections [B,H,D] / [B,Hkv,D];
+    the QK LayerNorm and q scale (``qk_norm(...)``) are applied in the kernel."""
+    _decode_checks(q, k, v, decay, state_in, state_out, y)
+    B, H, D = q.shape
+    L = load()
+    qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), tensor_desc(y, False)
+    si, so = state_desc(state_in), state_desc(state_out)
+    rc = L.prime_decode_step_qknorm(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), B, H, k.shape[1], D,
+                                    decay.data_ptr(), float(eps), ctypes.byref(norm),
+                                    ctypes.byref(si) if si else None, ctypes.byref(so), ctypes.byref(yd),
+                                    _stream(q.device))
+    _check(rc, "prime_decode_step_qknorm")
+
+
+def add_rmsnorm(x: torch.Tensor, delta: Optional[torch.Tensor], weight: torch.Tensor, out: torch.Tensor,
+                eps: float) -> None:
+    """prime_add_rmsnorm: x <- x + delta (if delta), out <- RMSNorm(x) * weight;
+    x, delta, out contiguous [..., hidden] of one dtype, weight [hidden]."""
+    _dev_check(x, weight, out, delta)
+    hidden = x.shape[-1]
+    for t in (x, out) + ((delta,) if delta is not None else ()):
+        if not t.is_contiguous() or t.dtype != x.dtype or t.shape != x.shape:
+            raise ValueError("x, delta and out must be contiguous tensors of one shape and dtype")
+    if weight.dtype != x.dtype or weight.numel() != hidden or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous [hidden] tensor of x's dtype")
+    if x.dtype not in _DTYPES:
+        raise RuntimeError(f"unsupported dtype {x.dtype}")
+    rows = x.numel() // hidden
+    rc = load().prime_add_rmsnorm(ctypes.c_void_p(x.data_ptr()),
+                                  ctypes.c_void_p(delta.data_ptr()) if delta is not None else None,
+                                  ctypes.c_void_p(weight.data_ptr()), ctypes.c_void_p(out.data_ptr()), rows,
+                                  hidden, _DTYPES[x.dtype], float(eps), _stream(x.device))
+    _check(rc, "prime_add_rmsnorm")
 
 
 def workspace_size(B: int, H: int, L: int, flags: int = 0) -> int:

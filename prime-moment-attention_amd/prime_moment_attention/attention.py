@@ -72,12 +72,16 @@ class PrimeMomentAttention(nn.Module):
             self.q_norm = nn.LayerNorm(head_dim)
             self.k_norm = nn.LayerNorm(head_dim)
 
-    def project(self, hidden_states: torch.Tensor):
-        """q (scaled), k, v as [B, H(kv), L, D] views (attention.py:83-101)."""
+    def project(self, hidden_states: torch.Tensor, normalize: bool = True):
+        """q (scaled), k, v as [B, H(kv), L, D] views (attention.py:83-101);
+        normalize=False returns the raw projections (QK-norm and scale left
+        to the decode kernel)."""
         B, L, _ = hidden_states.shape
         q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
         k = self.k_proj(hidden_states).view(B, L, self.num_kv_heads, self.head_dim).transpose(1, 2)
         v = self.v_proj(hidden_states).view(B, L, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        if not normalize:
+            return q, k, v
         if self.use_qk_norm:
             q = self.q_norm(q)
             k = self.k_norm(k)
@@ -94,10 +98,13 @@ class PrimeMomentAttention(nn.Module):
         orig_dtype = hidden_states.dtype
         H, D = self.num_heads, self.head_dim
         dev = hidden_states.device
-        q, k, v = self.project(hidden_states)
         y_dtype = orig_dtype if orig_dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
 
         if L == 1:
+            # the QK LayerNorm and the 1/sqrt(D) scale run inside the decode kernel
+            q, k, v = self.project(hidden_states, normalize=False)
+            norm = _lib.qk_norm(self.q_norm if self.use_qk_norm else None,
+                                self.k_norm if self.use_qk_norm else None, self.scaling, q.dtype)
             dec = _lib.decay_tensor(self.decay, H, dev)
             st_in = _lib.as_state(state, B, H, D, dev) if state is not None else None
             if self.inplace_state and st_in is not None and _same_storage(st_in, state):
@@ -105,10 +112,11 @@ class PrimeMomentAttention(nn.Module):
             else:
                 st_out = _lib.new_state(B, H, D, dev)
             y = torch.empty(B, H, D, device=dev, dtype=y_dtype)
-            _lib.decode_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], dec, self.eps, st_in, st_out, y)
+            _lib.decode_step_qknorm(q[:, :, 0], k[:, :, 0], v[:, :, 0], dec, self.eps, norm, st_in, st_out, y)
             y = y.unsqueeze(2)
             next_state = st_out
         else:
+            q, k, v = self.project(hidden_states)
             dense = L <= self.chunk_threshold
             st_out = None
             if return_state and self.inplace_state and state is not None:

@@ -15,7 +15,9 @@ Additions for serving, none of which changes results:
     positions only (generation needs one).
   * ``GreedyDecoder`` runs greedy decoding with per-layer states updated in
     place and the whole one-token step (embedding, 12 layers, final norm,
-    lm_head, argmax) captured in one HIP graph, replayed per token.
+    lm_head, argmax) captured in one HIP graph, replayed per token; in that
+    step each residual add is fused into the next RMSNorm and the QK-norm and
+    scale into the decode kernel (same values as the blocks' forward).
 """
 from __future__ import annotations
 
@@ -69,7 +71,8 @@ def prime_125m_config(mlp_type: str = "gelu", vocab_size: int = 50304) -> PrimeC
 
 
 class RMSNorm(nn.Module):
-    """model.py:47-56."""
+    """model.py:47-56, one HIP kernel (prime_add_rmsnorm): x * rsqrt(mean(x^2)
+    + eps) * weight, computed in fp32 and rounded once to x's dtype."""
 
     def __init__(self, dim: int, eps: float = 1e-6):
         super().__init__()
@@ -77,8 +80,11 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        variance = x.pow(2).mean(-1, keepdim=True)
-        return x * torch.rsqrt(variance + self.eps) * self.weight
+        xc = x.contiguous()
+        out = torch.empty_like(xc)
+        w = self.weight if self.weight.dtype == xc.dtype else self.weight.to(xc.dtype)
+        _lib.add_rmsnorm(xc, None, w, out, self.eps)
+        return out
 
 
 class PrimeMLP(nn.Module):
@@ -227,8 +233,15 @@ class GreedyDecoder:
         self.use_graph = use_graph
         self.graph = None
         self.states = None
+        self._decay, self._norm = {}, {}
+        dev = model.embed_tokens.weight.device
         for layer in model.layers:
-            layer.self_attn.inplace_state = True
+            at = layer.self_attn
+            at.inplace_state = True
+            self._decay[id(at)] = _lib.decay_tensor(at.decay, at.num_heads, dev)
+            self._norm[id(at)] = _lib.qk_norm(at.q_norm if at.use_qk_norm else None,
+                                              at.k_norm if at.use_qk_norm else None, at.scaling,
+                                              model.embed_tokens.weight.dtype)
 
     @torch.no_grad()
     def prefill(self, input_ids: torch.Tensor) -> torch.Tensor:
@@ -242,12 +255,31 @@ class GreedyDecoder:
 
     @torch.no_grad()
     def _step_eager(self) -> torch.Tensor:
+        """One token per sequence through the blocks, the residual adds fused
+        into the following RMSNorm (prime_add_rmsnorm: the same rounding as
+        the blocks' separate add), QK-norm and scale inside the decode kernel,
+        states updated in place.  The values equal PrimeBlock.forward's."""
         m = self.model
-        h = m.embed_tokens(self.token)
+        cfg = m.config
+        x = m.embed_tokens(self.token).reshape(-1, cfg.hidden_size)  # the residual stream, updated in place
+        B = x.shape[0]
+        pending = None
         for layer, st in zip(m.layers, self.states):
-            h, _ = layer(h, state=st, return_state=True)  # decode kernel updates st in place
-        logits = m.lm_head(m.norm(h))[:, -1, :]
-        return torch.argmax(logits, dim=-1, keepdim=True)
+            at = layer.self_attn
+            n1 = torch.empty_like(x)
+            _lib.add_rmsnorm(x, pending, layer.input_layernorm.weight, n1, layer.input_layernorm.eps)
+            q = at.q_proj(n1).view(B, at.num_heads, at.head_dim)
+            k = at.k_proj(n1).view(B, at.num_kv_heads, at.head_dim)
+            v = at.v_proj(n1).view(B, at.num_kv_heads, at.head_dim)
+            y = torch.empty(B, at.num_heads, at.head_dim, device=x.device, dtype=x.dtype)
+            _lib.decode_step_qknorm(q, k, v, self._decay[id(at)], at.eps, self._norm[id(at)], st, st, y)
+            a = at.o_proj(y.view(B, -1))
+            n2 = torch.empty_like(x)
+            _lib.add_rmsnorm(x, a, layer.post_attention_layernorm.weight, n2, layer.post_attention_layernorm.eps)
+            pending = layer.mlp(n2)
+        nf = torch.empty_like(x)
+        _lib.add_rmsnorm(x, pending, m.norm.weight, nf, m.norm.eps)
+        return torch.argmax(m.lm_head(nf), dim=-1, keepdim=True)
 
     @torch.no_grad()
     def step(self) -> torch.Tensor:

@@ -135,3 +135,58 @@ def test_decode_rejects_bad_arguments():
     with pytest.raises(RuntimeError, match="overlaps"):
         _lib.decode_step(x, x, x, dec, 1.0, st_in, st, x)
     del st_bad
+
+
+@pytest.mark.parametrize("qk_norm", [True, False])
+def test_decode_qknorm_prologue_matches_module_ops(qk_norm):
+    """prime_decode_step_qknorm on raw projections == LayerNorm + scale in torch
+    (attention.py:96-101) followed by prime_decode_step."""
+    import torch.nn as nn
+    B, H = 3, 4
+    torch.manual_seed(5)
+    qn, kn = nn.LayerNorm(D).to(dev()).bfloat16(), nn.LayerNorm(D).to(dev()).bfloat16()
+    with torch.no_grad():
+        for m in (qn, kn):
+            m.weight.uniform_(0.5, 1.5)
+            m.bias.uniform_(-0.2, 0.2)
+    q = torch.randn(B, H, D, device=dev()).bfloat16()
+    k = torch.randn(B, H, D, device=dev()).bfloat16()
+    v = torch.randn(B, H, D, device=dev()).bfloat16()
+    lam = to_dev(np.full(H, 0.99, np.float32))
+    st0 = state_to_dev(random_state(B * H, D, 17), B, H, D)
+    with torch.no_grad():
+        qr, kr = (qn(q), kn(k)) if qk_norm else (q, k)
+        qr = qr * 0.125
+    y_ref = torch.empty(B, H, D, device=dev())
+    s_ref = _lib.new_state(B, H, D, dev())
+    _lib.decode_step(qr, kr, v, lam, 1.0, st0, s_ref, y_ref)
+    y = torch.empty(B, H, D, device=dev())
+    s = _lib.new_state(B, H, D, dev())
+    norm = _lib.qk_norm(qn if qk_norm else None, kn if qk_norm else None, 0.125, torch.bfloat16)
+    _lib.decode_step_qknorm(q, k, v, lam, 1.0, norm, st0, s, y)
+    torch.cuda.synchronize()
+    assert_close(to_np(y), to_np(y_ref), 5e-3, "y")
+    assert_state_close(state_to_np(s, B * H, D), state_to_np(s_ref, B * H, D), 5e-3)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
+def test_add_rmsnorm_matches_torch(dtype, tol):
+    """prime_add_rmsnorm: x <- x + delta (rounded to dtype), out = RMSNorm(x) * w
+    (model.py:47-56) against the fp32 formula on the rounded sum."""
+    rows, hid = 37, 768
+    torch.manual_seed(6)
+    x = torch.randn(rows, hid, device=dev()).to(dtype)
+    d = torch.randn(rows, hid, device=dev()).to(dtype)
+    w = (torch.rand(hid, device=dev()) + 0.5).to(dtype)
+    xs = (x + d)  # torch's add in dtype: the rounded sum the kernel must store
+    ref = xs.float() * torch.rsqrt(xs.float().pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()
+    out = torch.empty_like(x)
+    xk = x.clone()
+    _lib.add_rmsnorm(xk, d, w, out, 1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(xk, xs)
+    assert_close(to_np(out), to_np(ref), tol, "out")
+    out2 = torch.empty_like(x)
+    _lib.add_rmsnorm(xs, None, w, out2, 1e-6)  # no delta: x untouched, same normalisation
+    torch.cuda.synchronize()
+    assert torch.equal(out2, out)
