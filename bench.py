@@ -457,7 +457,7 @@ def main():
                    "B": pf["B"], "H": pf["H"], "L": pf["L"], "D": D, "chunk": pf["C"],
                    "state_dtype": "fp32", "accumulate": "fp32", "workspace_bytes": pf["ws_bytes"],
                    "seed": args.seed},
-        "roofline": {"kernel": "prefill_kernel<bf16,fused> (fused chunk loop)", "bound": "hbm",
+        "roofline": {"kernel": "prefill_bf16_kernel<false> (fused chunk loop)", "bound": "hbm",
                      "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM,
                      "traffic": None if traffic is None else traffic.get("bytes_per_launch"),

@@ -118,7 +118,8 @@ int prime_decode_step_qknorm(const prime_tensor_t *q, const prime_tensor_t *k,
  * x <- x + delta (when delta is not NULL; the sum rounded to `dtype`, as the
  * block's residual add stores it), then out <- x * rsqrt(mean(x^2) + eps) *
  * weight.  x, delta, out: [rows, hidden] contiguous, weight [hidden]; one dtype
- * (F32 / BF16 / F16); hidden a multiple of 4.  out may be x.
+ * (F32 / BF16 / F16); hidden a multiple of 4 and at most 4096; every pointer
+ * aligned to 4 elements.  out may be x.
  */
 int prime_add_rmsnorm(void *x, const void *delta, const void *weight, void *out, int rows,
                       int hidden, int dtype, float eps, void *stream);

@@ -160,7 +160,13 @@ int prime_add_rmsnorm(void *x, const void *delta, const void *weight, void *out,
     if (rows <= 0 || hidden <= 0 || hidden % 4)
         return fail(PRIME_ERR_INVALID_ARG, "bad sizes rows=%d hidden=%d (hidden must be a multiple of 4)", rows,
                     hidden);
+    if (hidden > 4 * 64 * prime::kNormMaxGroups)
+        return fail(PRIME_ERR_INVALID_ARG, "hidden=%d above the supported %d", hidden, 4 * 64 * prime::kNormMaxGroups);
     if (!valid_dtype(dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dtype");
+    const uintptr_t al = 4 * elem_size(dtype) - 1;  // one 4-element group per load
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(delta) | reinterpret_cast<uintptr_t>(weight) |
+         reinterpret_cast<uintptr_t>(out)) & al)
+        return fail(PRIME_ERR_MISALIGNED, "x/delta/weight/out must be aligned to 4 elements");
     const size_t n = static_cast<size_t>(rows) * hidden * elem_size(dtype);
     if (delta && overlap(delta, n, x, n)) return fail(PRIME_ERR_ALIAS, "delta overlaps x");
     if (out != x && overlap(out, n, x, n)) return fail(PRIME_ERR_ALIAS, "out overlaps x without being x");

@@ -33,6 +33,7 @@ struct RmsNormArgs {
     int rows, hidden, dt;
     float eps;
 };
+constexpr int kNormMaxGroups = 16;  // 4-element groups per lane: hidden <= 4 * 64 * 16 = 4096
 hipError_t launch_add_rmsnorm(const RmsNormArgs &a, hipStream_t stream);
 
 struct PrefillArgs {

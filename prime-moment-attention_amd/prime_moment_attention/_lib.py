@@ -30,8 +30,8 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
 KERNEL_DELTA_PREP, KERNEL_DELTA_SCAN, KERNEL_DELTA_STEP = 4, 5, 6
-KERNEL_NAMES = {KERNEL_PREFILL_CHUNKS: "prefill_kernel<bf16,fused>", KERNEL_PREFILL_SEGMENTS:
-                "prefill_kernel<bf16,state_only>", KERNEL_SEGMENT_SCAN: "segment_scan_kernel",
+KERNEL_NAMES = {KERNEL_PREFILL_CHUNKS: "prefill_bf16_kernel<false>", KERNEL_PREFILL_SEGMENTS:
+                "prefill_bf16_kernel<true>", KERNEL_SEGMENT_SCAN: "segment_scan_kernel",
                 KERNEL_DECODE: "decode_step_kernel", KERNEL_DELTA_PREP: "delta_prep_kernel",
                 KERNEL_DELTA_SCAN: "delta_scan_kernel", KERNEL_DELTA_STEP: "delta_step_kernel"}
 
