@@ -201,6 +201,16 @@ int prime_delta_decode_step(const prime_tensor_t *q, const prime_tensor_t *k,
                             void *stream);
 
 /*
+ * Greedy token choice of the generate loop (model.py:230-231, argmax over the
+ * vocabulary at temperature 0): out[i] = the first index j of the largest
+ * logits[i, j], NaN counting as the largest value (torch.argmax's answer).
+ * logits: n rows of `vocab` elements (F32 / BF16 / F16), row i starting
+ * stride_n elements after row i-1 (stride_n >= vocab); out: int64 [n].
+ */
+int prime_argmax(const void *logits, int dtype, int n, int vocab, int64_t stride_n, int64_t *out,
+                 void *stream);
+
+/*
  * Launch timer.  No counterpart in the reference: it serves benchmark harnesses
  * that need the device time of ONE kernel of a multi-kernel call.
  * prime_timer_enable(mask) (process-wide; bit (1 << PRIME_KERNEL_*) selects a

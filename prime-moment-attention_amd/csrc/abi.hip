@@ -176,6 +176,23 @@ int prime_add_rmsnorm(void *x, const void *delta, const void *weight, void *out,
     return check_hip(prime::launch_add_rmsnorm(a, static_cast<hipStream_t>(stream)), "add_rmsnorm launch");
 }
 
+int prime_argmax(const void *logits, int dtype, int n, int vocab, int64_t stride_n, int64_t *out, void *stream) {
+    g_err[0] = 0;
+    if (!logits || !out) return fail(PRIME_ERR_INVALID_ARG, "prime_argmax: null argument");
+    if (n <= 0 || vocab <= 0 || stride_n < vocab)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes n=%d vocab=%d stride_n=%lld", n, vocab,
+                    static_cast<long long>(stride_n));
+    if (!valid_dtype(dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dtype");
+    if (reinterpret_cast<uintptr_t>(out) & 7) return fail(PRIME_ERR_MISALIGNED, "out must be 8-byte aligned");
+    const int64_t es = elem_size(dtype);
+    if (reinterpret_cast<uintptr_t>(logits) % es) return fail(PRIME_ERR_MISALIGNED, "logits misaligned");
+    prime::ArgmaxArgs a{};
+    a.logits = logits; a.out = out; a.stride_n = stride_n;
+    a.n = n; a.vocab = vocab; a.dt = dtype;
+    a.vector = aligned16(logits) && (stride_n * es) % 16 == 0;
+    return check_hip(prime::launch_argmax_rows(a, static_cast<hipStream_t>(stream)), "argmax launch");
+}
+
 int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
                           int B, int H, int H_kv, int L, int D, int chunk, const float *decay,
                           float eps, unsigned flags, const prime_state_t *state_in,

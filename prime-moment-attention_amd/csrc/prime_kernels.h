@@ -33,6 +33,15 @@ struct RmsNormArgs {
     int rows, hidden, dt;
     float eps;
 };
+struct ArgmaxArgs {
+    const void *logits;   // n rows of `vocab` logits, row i at logits + i * stride_n elements
+    int64_t *out;         // [n]
+    int64_t stride_n;
+    int n, vocab, dt;
+    int vector;           // rows 16-byte aligned: 16-byte loads, element-wise tail
+};
+hipError_t launch_argmax_rows(const ArgmaxArgs &a, hipStream_t stream);
+
 constexpr int kNormMaxGroups = 16;  // 4-element groups per lane: hidden <= 4 * 64 * 16 = 4096
 hipError_t launch_add_rmsnorm(const RmsNormArgs &a, hipStream_t stream);
 

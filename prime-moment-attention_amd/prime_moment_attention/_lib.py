@@ -25,7 +25,7 @@ _DTYPES = {torch.float32: PRIME_F32, torch.bfloat16: PRIME_BF16, torch.float16: 
 EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_chunked_prefill",
            "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
            "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
-           "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm")
+           "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_argmax")
 
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
@@ -90,6 +90,8 @@ def load() -> ctypes.CDLL:
     L.prime_decode_step_qknorm.restype = ctypes.c_int
     L.prime_add_rmsnorm.argtypes = [fp] * 4 + [ctypes.c_int] * 3 + [ctypes.c_float, fp]
     L.prime_add_rmsnorm.restype = ctypes.c_int
+    L.prime_argmax.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, fp, fp]
+    L.prime_argmax.restype = ctypes.c_int
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     v = L.prime_abi_version()
     if v != ABI_VERSION:
@@ -255,6 +257,23 @@ def add_rmsnorm(x: torch.Tensor, delta: Optional[torch.Tensor], weight: torch.Te
                                   ctypes.c_void_p(weight.data_ptr()), ctypes.c_void_p(out.data_ptr()), rows,
                                   hidden, _DTYPES[x.dtype], float(eps), _stream(x.device))
     _check(rc, "prime_add_rmsnorm")
+
+
+def argmax(logits: torch.Tensor, out: torch.Tensor) -> None:
+    """prime_argmax: out[i] = argmax_j logits[i, j] (first index of the
+    largest, NaN largest), logits [n, vocab] with a contiguous last dimension,
+    out int64 [n] (or [n, 1])."""
+    _dev_check(logits, out)
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be [n, vocab] with a contiguous vocab dimension")
+    if logits.dtype not in _DTYPES:
+        raise RuntimeError(f"unsupported dtype {logits.dtype}")
+    n, vocab = logits.shape
+    if out.dtype != torch.int64 or out.numel() != n or not out.is_contiguous():
+        raise ValueError("out must be a contiguous int64 tensor of n elements")
+    rc = load().prime_argmax(ctypes.c_void_p(logits.data_ptr()), _DTYPES[logits.dtype], n, vocab,
+                             logits.stride(0), ctypes.c_void_p(out.data_ptr()), _stream(logits.device))
+    _check(rc, "prime_argmax")
 
 
 def workspace_size(B: int, H: int, L: int, flags: int = 0) -> int:

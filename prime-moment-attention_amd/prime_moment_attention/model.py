@@ -233,7 +233,7 @@ class GreedyDecoder:
         self.use_graph = use_graph
         self.graph = None
         self.states = None
-        self._decay, self._norm = {}, {}
+        self._decay, self._norm, self._qkv = {}, {}, {}
         dev = model.embed_tokens.weight.device
         for layer in model.layers:
             at = layer.self_attn
@@ -249,7 +249,13 @@ class GreedyDecoder:
         m = self.model
         out = m.forward(input_ids, return_states=True, logits_to_keep=1)
         self.states = [tuple(s) for s in out["states"]]
-        self.token = torch.argmax(out["logits"][:, -1, :], dim=-1, keepdim=True)
+        self.token = torch.empty(input_ids.shape[0], 1, dtype=torch.int64, device=input_ids.device)
+        _lib.argmax(out["logits"][:, -1, :], self.token)
+        # q/k/v projection weights stacked into one [Hq*D + 2*Hkv*D, hidden]
+        # matrix per layer (one GEMM per step), taken from the module now
+        for layer in m.layers:
+            at = layer.self_attn
+            self._qkv[id(at)] = torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight], dim=0)
         self.graph = None
         return self.token
 
@@ -268,9 +274,11 @@ class GreedyDecoder:
             at = layer.self_attn
             n1 = torch.empty_like(x)
             _lib.add_rmsnorm(x, pending, layer.input_layernorm.weight, n1, layer.input_layernorm.eps)
-            q = at.q_proj(n1).view(B, at.num_heads, at.head_dim)
-            k = at.k_proj(n1).view(B, at.num_kv_heads, at.head_dim)
-            v = at.v_proj(n1).view(B, at.num_kv_heads, at.head_dim)
+            nq, nk = at.num_heads * at.head_dim, at.num_kv_heads * at.head_dim
+            qkv = F.linear(n1, self._qkv[id(at)])
+            q = qkv[:, :nq].view(B, at.num_heads, at.head_dim)
+            k = qkv[:, nq:nq + nk].view(B, at.num_kv_heads, at.head_dim)
+            v = qkv[:, nq + nk:].view(B, at.num_kv_heads, at.head_dim)
             y = torch.empty(B, at.num_heads, at.head_dim, device=x.device, dtype=x.dtype)
             _lib.decode_step_qknorm(q, k, v, self._decay[id(at)], at.eps, self._norm[id(at)], st, st, y)
             a = at.o_proj(y.view(B, -1))
@@ -279,14 +287,14 @@ class GreedyDecoder:
             pending = layer.mlp(n2)
         nf = torch.empty_like(x)
         _lib.add_rmsnorm(x, pending, m.norm.weight, nf, m.norm.eps)
-        return torch.argmax(m.lm_head(nf), dim=-1, keepdim=True)
+        _lib.argmax(m.lm_head(nf), self.token)  # the embedding above has consumed the old token
+        return self.token
 
     @torch.no_grad()
     def step(self) -> torch.Tensor:
         """One decode step for every sequence; returns the new tokens [B, 1]."""
         if not self.use_graph:
-            self.token = self._step_eager()
-            return self.token
+            return self._step_eager()
         if self.graph is None:
             self._capture()
         self.graph.replay()
@@ -308,8 +316,7 @@ class GreedyDecoder:
         self.token.copy_(tok)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            nxt = self._step_eager()
-            self.token.copy_(nxt)
+            self._step_eager()
         # capture does not execute: states and token are as after the prefill
         self.graph = g
 

@@ -116,3 +116,33 @@ def test_greedy_decoder_graph_equals_eager_generate():
     assert [t.data_ptr() for st in dec.states for t in st] == ptrs
     assert torch.equal(eager, ref), (eager, ref)
     assert torch.equal(graph, ref), (graph, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("n,vocab,pad", [(256, 50304, 0), (3, 1000, 0), (5, 50257, 0), (4, 37, 3), (1, 9000, 1)])
+def test_argmax_matches_torch(dtype, n, vocab, pad):
+    """prime_argmax == torch.argmax (first index of the largest), on padded
+    (strided, unaligned) rows and ragged vocabularies."""
+    from prime_moment_attention import _lib
+    g = torch.Generator(device=dev()).manual_seed(n + vocab)
+    full = torch.randn(n, vocab + pad, device=dev(), generator=g).to(dtype)
+    x = full[:, :vocab]
+    out = torch.empty(n, dtype=torch.int64, device=dev())
+    _lib.argmax(x, out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.argmax(x, dim=-1))
+
+
+def test_argmax_ties_nan_and_signed_zero():
+    from prime_moment_attention import _lib
+    x = torch.full((5, 3000), -1.0, device=dev(), dtype=torch.bfloat16)
+    x[0, 7] = x[0, 2500] = 3.0            # tie: first index
+    x[1, 11] = float("nan"); x[1, 12] = float("inf")  # NaN counts as largest
+    x[2, :] = 0.0; x[2, :1000] = -0.0     # -0 == +0: first index (0)
+    x[3, 2999] = float("inf")             # last element
+    x[4, :] = float("-inf")               # all -inf: index 0
+    out = torch.empty(5, dtype=torch.int64, device=dev())
+    _lib.argmax(x, out)
+    torch.cuda.synchronize()
+    assert out.tolist() == [7, 11, 0, 2999, 0]
+    assert torch.equal(out, torch.argmax(x, dim=-1))
