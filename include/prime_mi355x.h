@@ -201,6 +201,19 @@ int prime_delta_decode_step(const prime_tensor_t *q, const prime_tensor_t *k,
                             void *stream);
 
 /*
+ * The module's per-head QK-norm on projected rows (attention.py:96-101):
+ * out = LayerNorm(x) over D (biased variance, affine weight/bias [D] of
+ * param_dtype, epsilon ln_eps) rounded to x's dtype, then multiplied by
+ * `scale` and rounded again (pass 1/sqrt(D) for q, 1 for k).  weight = bias =
+ * NULL applies the scale only (a module without QK-norm).  x, out: strided
+ * [B, H, L, D] views of one dtype, D = 64; out may be x (the same view) but may
+ * not partly overlap it.  The chunked prefill's producer for q and k.
+ */
+int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int B, int H, int L, int D,
+                         const void *weight, const void *bias, int param_dtype, float ln_eps, float scale,
+                         void *stream);
+
+/*
  * Greedy token choice of the generate loop (model.py:230-231, argmax over the
  * vocabulary at temperature 0): out[i] = the first index j of the largest
  * logits[i, j], NaN counting as the largest value (torch.argmax's answer).

@@ -176,6 +176,37 @@ int prime_add_rmsnorm(void *x, const void *delta, const void *weight, void *out,
     return check_hip(prime::launch_add_rmsnorm(a, static_cast<hipStream_t>(stream)), "add_rmsnorm launch");
 }
 
+int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int B, int H, int L, int D,
+                         const void *weight, const void *bias, int param_dtype, float ln_eps, float scale,
+                         void *stream) {
+    g_err[0] = 0;
+    if (!x || !out || !x->data || !out->data) return fail(PRIME_ERR_INVALID_ARG, "prime_head_layernorm: null argument");
+    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (B <= 0 || H <= 0 || L <= 0) return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d L=%d", B, H, L);
+    if (!valid_dtype(x->dtype) || out->dtype != x->dtype)
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "x and out must share one supported dtype");
+    if ((weight == nullptr) != (bias == nullptr))
+        return fail(PRIME_ERR_INVALID_ARG, "LayerNorm weight and bias must both be given or both be null");
+    if (weight && !valid_dtype(param_dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported parameter dtype");
+    if (!rows_aligned(x, true) || !rows_aligned(out, true))
+        return fail(PRIME_ERR_MISALIGNED, "x/out rows must start on 16-byte boundaries");
+    const int64_t es = elem_size(x->dtype);
+    auto span = [&](const prime_tensor_t *t) {
+        return static_cast<size_t>(((B - 1) * t->stride_b + (H - 1) * t->stride_h + (L - 1) * t->stride_l + D) * es);
+    };
+    const bool same = out->data == x->data && out->stride_b == x->stride_b && out->stride_h == x->stride_h &&
+                      out->stride_l == x->stride_l;
+    if (!same && overlap(out->data, span(out), x->data, span(x)))
+        return fail(PRIME_ERR_ALIAS, "out overlaps x without being the same view");
+    prime::HeadNormArgs a{};
+    a.x = x->data; a.out = out->data; a.weight = weight; a.bias = bias;
+    a.x_sb = x->stride_b; a.x_sh = x->stride_h; a.x_sl = x->stride_l;
+    a.o_sb = out->stride_b; a.o_sh = out->stride_h; a.o_sl = out->stride_l;
+    a.B = B; a.H = H; a.L = L; a.dt = x->dtype; a.dt_norm = param_dtype;
+    a.ln_eps = ln_eps; a.scale = scale;
+    return check_hip(prime::launch_head_layernorm(a, static_cast<hipStream_t>(stream)), "head_layernorm launch");
+}
+
 int prime_argmax(const void *logits, int dtype, int n, int vocab, int64_t stride_n, int64_t *out, void *stream) {
     g_err[0] = 0;
     if (!logits || !out) return fail(PRIME_ERR_INVALID_ARG, "prime_argmax: null argument");

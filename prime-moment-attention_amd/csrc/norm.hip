@@ -97,6 +97,66 @@ __global__ __launch_bounds__(kNormWaves * kWave) void add_rmsnorm_kernel(const R
     }
 }
 
+// Per-head LayerNorm of the module's QK-norm (attention.py:96-101) over rows
+// of 64: out = round(round(LN(x)) * scale), biased variance, each rounding to
+// the tensor's dtype as the module's LayerNorm output and its scaled copy are
+// stored.  Without LayerNorm parameters only the scale is applied.  16 lanes
+// per row (4 elements each), 16 rows per 256-thread block; rows are visited
+// in (b, l, h) order so that a block walks consecutive memory for the
+// projection layout [B, L, H, D].
+template <int DT>
+__global__ __launch_bounds__(256) void head_layernorm_kernel(const HeadNormArgs a) {
+    typedef Group<DT> G;
+    typedef typename G::raw raw;
+    const int64_t rows = static_cast<int64_t>(a.B) * a.L * a.H;
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+    const int sub = threadIdx.x & 15;
+    const bool live = r < rows;
+    const int64_t rr = live ? r : 0;
+    const int h = static_cast<int>(rr % a.H);
+    const int64_t bl = rr / a.H;
+    const int l = static_cast<int>(bl % a.L), b = static_cast<int>(bl / a.L);
+    const raw *xp = reinterpret_cast<const raw *>(static_cast<const char *>(a.x) +
+                                                  (b * a.x_sb + h * a.x_sh + l * a.x_sl) * (DT == PRIME_F32 ? 4 : 2));
+    float v[4];
+    G::unpack(xp[sub], v);
+    if (a.weight) {
+        float s = v[0] + v[1] + v[2] + v[3];
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+        const float mean = s * (1.0f / kD);
+        float d[4], q = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { d[e] = v[e] - mean; q += d[e] * d[e]; }
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) q += __shfl_xor(q, o, kWave);
+        const float rs = rsqrtf(q * (1.0f / kD) + a.ln_eps);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = 4 * sub + e;
+            v[e] = G::round(d[e] * rs * load_elem(a.weight, c, a.dt_norm) + load_elem(a.bias, c, a.dt_norm));
+        }
+    }
+    if (a.scale != 1.0f) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = G::round(v[e] * a.scale);
+    }
+    if (live) {
+        raw *op = reinterpret_cast<raw *>(static_cast<char *>(a.out) +
+                                          (b * a.o_sb + h * a.o_sh + l * a.o_sl) * (DT == PRIME_F32 ? 4 : 2));
+        op[sub] = G::pack(v);
+    }
+}
+
+hipError_t launch_head_layernorm(const HeadNormArgs &a, hipStream_t stream) {
+    const int64_t rows = static_cast<int64_t>(a.B) * a.L * a.H;
+    const dim3 grid(static_cast<unsigned>((rows + 15) / 16)), block(256);
+    if (a.dt == PRIME_BF16) hipLaunchKernelGGL(head_layernorm_kernel<PRIME_BF16>, grid, block, 0, stream, a);
+    else if (a.dt == PRIME_F16) hipLaunchKernelGGL(head_layernorm_kernel<PRIME_F16>, grid, block, 0, stream, a);
+    else hipLaunchKernelGGL(head_layernorm_kernel<PRIME_F32>, grid, block, 0, stream, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_add_rmsnorm(const RmsNormArgs &a, hipStream_t stream) {
     const dim3 grid((a.rows + kNormWaves - 1) / kNormWaves), block(kNormWaves * kWave);
     if (a.dt == PRIME_BF16) hipLaunchKernelGGL(add_rmsnorm_kernel<PRIME_BF16>, grid, block, 0, stream, a);

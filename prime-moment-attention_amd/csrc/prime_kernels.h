@@ -42,6 +42,17 @@ struct ArgmaxArgs {
 };
 hipError_t launch_argmax_rows(const ArgmaxArgs &a, hipStream_t stream);
 
+// Per-head LayerNorm (+ scale) of projected q or k rows (norm.hip).
+struct HeadNormArgs {
+    const void *x;        // [B, H, L, 64] view, element strides below
+    void *out;            // same shape, own strides; may be x itself
+    const void *weight, *bias;  // [64] each, or null (no LayerNorm: scale only)
+    int64_t x_sb, x_sh, x_sl, o_sb, o_sh, o_sl;
+    int B, H, L, dt, dt_norm;
+    float ln_eps, scale;
+};
+hipError_t launch_head_layernorm(const HeadNormArgs &a, hipStream_t stream);
+
 constexpr int kNormMaxGroups = 16;  // 4-element groups per lane: hidden <= 4 * 64 * 16 = 4096
 hipError_t launch_add_rmsnorm(const RmsNormArgs &a, hipStream_t stream);
 

@@ -25,7 +25,8 @@ _DTYPES = {torch.float32: PRIME_F32, torch.bfloat16: PRIME_BF16, torch.float16: 
 EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_chunked_prefill",
            "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
            "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
-           "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_argmax")
+           "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_argmax",
+           "prime_head_layernorm")
 
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
@@ -92,6 +93,9 @@ def load() -> ctypes.CDLL:
     L.prime_add_rmsnorm.restype = ctypes.c_int
     L.prime_argmax.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, fp, fp]
     L.prime_argmax.restype = ctypes.c_int
+    L.prime_head_layernorm.argtypes = [P(PrimeTensor)] * 2 + [ctypes.c_int] * 4 + [fp, fp, ctypes.c_int,
+                                                                                 ctypes.c_float, ctypes.c_float, fp]
+    L.prime_head_layernorm.restype = ctypes.c_int
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     v = L.prime_abi_version()
     if v != ABI_VERSION:
@@ -257,6 +261,31 @@ def add_rmsnorm(x: torch.Tensor, delta: Optional[torch.Tensor], weight: torch.Te
                                   ctypes.c_void_p(weight.data_ptr()), ctypes.c_void_p(out.data_ptr()), rows,
                                   hidden, _DTYPES[x.dtype], float(eps), _stream(x.device))
     _check(rc, "prime_add_rmsnorm")
+
+
+def head_layernorm(x: torch.Tensor, out: torch.Tensor, norm: Optional[torch.nn.LayerNorm], scale: float) -> None:
+    """prime_head_layernorm: out = round(round(LayerNorm(x)) * scale) per
+    [B, H, L, 64] row (norm None: the scale only); out may be x."""
+    _dev_check(x, out)
+    if x.dim() != 4 or out.shape != x.shape or out.dtype != x.dtype:
+        raise ValueError("x and out must be [B, H, L, D] views of one shape and dtype")
+    B, H, L, D = x.shape
+    w = b = None
+    pdt = _DTYPES.get(x.dtype, 0)
+    eps = 1e-5
+    if norm is not None:
+        if norm.weight is None or norm.bias is None:
+            raise ValueError("the LayerNorm needs weight and bias")
+        w, b, eps = norm.weight, norm.bias, norm.eps
+        if w.dtype not in _DTYPES or b.dtype != w.dtype or not (w.is_contiguous() and b.is_contiguous()):
+            raise ValueError("LayerNorm parameters must be contiguous and of one supported dtype")
+        pdt = _DTYPES[w.dtype]
+    xd, od = tensor_desc(x, True), tensor_desc(out, True)
+    rc = load().prime_head_layernorm(ctypes.byref(xd), ctypes.byref(od), B, H, L, D,
+                                     ctypes.c_void_p(w.data_ptr()) if w is not None else None,
+                                     ctypes.c_void_p(b.data_ptr()) if b is not None else None, pdt,
+                                     float(eps), float(scale), _stream(x.device))
+    _check(rc, "prime_head_layernorm")
 
 
 def argmax(logits: torch.Tensor, out: torch.Tensor) -> None:

@@ -82,10 +82,12 @@ class PrimeMomentAttention(nn.Module):
         v = self.v_proj(hidden_states).view(B, L, self.num_kv_heads, self.head_dim).transpose(1, 2)
         if not normalize:
             return q, k, v
+        # QK-norm and the 1/sqrt(D) scale in place on the fresh projections
+        # (prime_head_layernorm, the module's rounding), read by the prefill
+        # kernel through the [B, L, H, D] strides
+        _lib.head_layernorm(q, q, self.q_norm if self.use_qk_norm else None, self.scaling)
         if self.use_qk_norm:
-            q = self.q_norm(q)
-            k = self.k_norm(k)
-        q = q * self.scaling
+            _lib.head_layernorm(k, k, self.k_norm, 1.0)
         return q, k, v
 
     def forward(
@@ -123,9 +125,12 @@ class PrimeMomentAttention(nn.Module):
                 st_in = _lib.as_state(state, B, H, D, dev)
                 if _same_storage(st_in, state):
                     st_out = st_in
+            # y written in the o_proj input layout [B, L, H, D] through strides
+            y_bl = torch.empty(B, L, H, D, device=dev, dtype=y_dtype)
             y, next_state = prime_prefill(q, k, v, state=state, decay=self.decay, eps=self.eps,
                                           chunk_size=self.chunk_size, return_state=return_state,
-                                          out_dtype=y_dtype, dense_clamp=dense, state_out=st_out)
+                                          out_dtype=y_dtype, dense_clamp=dense, state_out=st_out,
+                                          y=y_bl.transpose(1, 2))
 
         y = y.to(orig_dtype).transpose(1, 2).reshape(B, L, H * D)
         output = self.o_proj(y)

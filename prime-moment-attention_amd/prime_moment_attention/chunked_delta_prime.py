@@ -77,10 +77,11 @@ class ChunkedGatedDeltaPrimeAttention(nn.Module):
         q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
         k = self.k_proj(hidden_states).view(B, L, self.num_kv_heads, self.head_dim).transpose(1, 2)
         v = self.v_proj(hidden_states).view(B, L, self.num_kv_heads, self.head_dim).transpose(1, 2)
+        # QK-norm and scale in place on the fresh projections (prime_head_layernorm)
+        _lib.head_layernorm(q, q, self.q_norm if self.use_qk_norm else None, self.scaling)
         if self.use_qk_norm:
-            q = self.q_norm(q)
-            k = self.k_norm(k)
-        return q * self.scaling, k, v
+            _lib.head_layernorm(k, k, self.k_norm, 1.0)
+        return q, k, v
 
     def forward(self, hidden_states: torch.Tensor, state: Optional[torch.Tensor] = None,
                 return_state: bool = False) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:

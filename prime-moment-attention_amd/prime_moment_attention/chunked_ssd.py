@@ -36,8 +36,10 @@ def _prep(x: torch.Tensor) -> torch.Tensor:
 
 
 def prime_prefill(q, k, v, state=None, decay=0.9995, eps=1.0, chunk_size=64, return_state=False,
-                  out_dtype=torch.float32, dense_clamp=False, state_out=None):
-    """Core launcher shared by the modules.  Returns (y, next_state | None)."""
+                  out_dtype=torch.float32, dense_clamp=False, state_out=None, y=None):
+    """Core launcher shared by the modules.  Returns (y, next_state | None);
+    ``y`` may be a caller-provided [B, H, L, D] view (any strides with a
+    contiguous D and 16-byte aligned rows)."""
     B, H, L, D = q.shape
     q, k, v = _prep(q), _prep(k), _prep(v)
     if k.dtype != q.dtype or v.dtype != q.dtype:
@@ -45,7 +47,8 @@ def prime_prefill(q, k, v, state=None, decay=0.9995, eps=1.0, chunk_size=64, ret
     dev = q.device
     dec = _lib.decay_tensor(decay, H, dev)
     st_in = _lib.as_state(state, B, H, D, dev) if state is not None else None
-    y = torch.empty(B, H, L, D, device=dev, dtype=out_dtype)
+    if y is None:
+        y = torch.empty(B, H, L, D, device=dev, dtype=out_dtype)
     st_out = None
     if return_state:
         st_out = state_out if state_out is not None else _lib.new_state(B, H, D, dev)
@@ -99,13 +102,14 @@ class ChunkedPrimeSSD(nn.Module):
         q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
         k = self.k_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
         v = self.v_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
+        # QK-norm and scale in place on the projections (chunked_ssd.py:225-236)
+        _lib.head_layernorm(q, q, self.q_norm if self.use_qk_norm else None, self.scaling)
         if self.use_qk_norm:
-            q = self.q_norm(q)
-            k = self.k_norm(k)
-        q = q * self.scaling
+            _lib.head_layernorm(k, k, self.k_norm, 1.0)
+        y_dtype = dtype if dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
+        y_bl = torch.empty(B, L, self.num_heads, self.head_dim, device=q.device, dtype=y_dtype)
         y, next_state = prime_prefill(q, k, v, state=state, decay=self.decay, eps=self.eps,
                                       chunk_size=self.chunk_size, return_state=return_state,
-                                      out_dtype=dtype if dtype in (torch.float32, torch.bfloat16,
-                                                                   torch.float16) else torch.float32)
+                                      out_dtype=y_dtype, y=y_bl.transpose(1, 2))
         y = y.to(dtype).transpose(1, 2).reshape(B, L, self.num_heads * self.head_dim)
         return self.o_proj(y), next_state

@@ -146,3 +146,29 @@ def test_argmax_ties_nan_and_signed_zero():
     torch.cuda.synchronize()
     assert out.tolist() == [7, 11, 0, 2999, 0]
     assert torch.equal(out, torch.argmax(x, dim=-1))
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, 0), (torch.float32, 1e-5)])
+@pytest.mark.parametrize("with_ln", [True, False])
+def test_head_layernorm_matches_module_ops(dtype, tol, with_ln):
+    """prime_head_layernorm in place on the projection layout ([B, L, H, D]
+    storage seen as [B, H, L, D]) == nn.LayerNorm then * scale (attention.py:96-101);
+    bf16: equal up to one bf16 ulp (the kernel's rsqrt vs torch's)."""
+    from prime_moment_attention import _lib
+    B, L, H, D = 3, 37, 5, 64
+    torch.manual_seed(4)
+    ln = torch.nn.LayerNorm(D).to(dev()).to(dtype)
+    with torch.no_grad():
+        ln.weight.uniform_(0.5, 1.5)
+        ln.bias.uniform_(-0.3, 0.3)
+    raw = (torch.randn(B, L, H * D, device=dev()) * 3 + 0.5).to(dtype)
+    x = raw.view(B, L, H, D).transpose(1, 2)
+    with torch.no_grad():
+        ref = (ln(x) if with_ln else x) * 0.125
+    _lib.head_layernorm(x, x, ln if with_ln else None, 0.125)
+    torch.cuda.synchronize()
+    d = (x.float() - ref.float()).abs()
+    bound = ref.float().abs() * (2 ** -7) + 1e-6 if dtype == torch.bfloat16 else tol * (1 + ref.float().abs())
+    assert bool((d <= bound).all()), float(d.max())
+    if not with_ln:
+        assert torch.equal(x, ref)  # a power-of-two scale is exact
