@@ -183,6 +183,9 @@ int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int
     if (!x || !out || !x->data || !out->data) return fail(PRIME_ERR_INVALID_ARG, "prime_head_layernorm: null argument");
     if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
     if (B <= 0 || H <= 0 || L <= 0) return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d L=%d", B, H, L);
+    if (static_cast<int64_t>(B) * H * L >= (int64_t(1) << 31))
+        return fail(PRIME_ERR_INVALID_ARG, "B*H*L = %lld rows exceeds 2^31 - 1",
+                    static_cast<long long>(static_cast<int64_t>(B) * H * L));
     if (!valid_dtype(x->dtype) || out->dtype != x->dtype)
         return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "x and out must share one supported dtype");
     if ((weight == nullptr) != (bias == nullptr))

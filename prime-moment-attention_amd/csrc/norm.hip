@@ -100,57 +100,90 @@ __global__ __launch_bounds__(kNormWaves * kWave) void add_rmsnorm_kernel(const R
 // Per-head LayerNorm of the module's QK-norm (attention.py:96-101) over rows
 // of 64: out = round(round(LN(x)) * scale), biased variance, each rounding to
 // the tensor's dtype as the module's LayerNorm output and its scaled copy are
-// stored.  Without LayerNorm parameters only the scale is applied.  16 lanes
-// per row (4 elements each), 16 rows per 256-thread block; rows are visited
-// in (b, l, h) order so that a block walks consecutive memory for the
-// projection layout [B, L, H, D].
+// stored.  Without LayerNorm parameters only the scale is applied.
+// A row is 128 B (16-bit types: 8 lanes x 16 B) or 256 B (fp32: 16 lanes x
+// 16 B); a wave covers 8 or 4 rows per load and holds kHeadNormBatch such
+// loads in flight; rows are visited in (b, l, h) order, so a wave walks
+// consecutive memory for the projection layout [B, L, H, D].
+constexpr int kHeadNormBatch = 4;
+
 template <int DT>
 __global__ __launch_bounds__(256) void head_layernorm_kernel(const HeadNormArgs a) {
-    typedef Group<DT> G;
-    typedef typename G::raw raw;
-    const int64_t rows = static_cast<int64_t>(a.B) * a.L * a.H;
-    const int64_t r = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
-    const int sub = threadIdx.x & 15;
-    const bool live = r < rows;
-    const int64_t rr = live ? r : 0;
-    const int h = static_cast<int>(rr % a.H);
-    const int64_t bl = rr / a.H;
-    const int l = static_cast<int>(bl % a.L), b = static_cast<int>(bl / a.L);
-    const raw *xp = reinterpret_cast<const raw *>(static_cast<const char *>(a.x) +
-                                                  (b * a.x_sb + h * a.x_sh + l * a.x_sl) * (DT == PRIME_F32 ? 4 : 2));
-    float v[4];
-    G::unpack(xp[sub], v);
+    constexpr int es = DT == PRIME_F32 ? 4 : 2;
+    constexpr int VE = 16 / es;             // elements per lane
+    constexpr int LPR = kD / VE;            // lanes per row
+    constexpr int RPW = kWave / LPR;        // rows per wave per load
+    const uint32_t rows = static_cast<uint32_t>(a.B) * a.L * a.H;
+    const int lane = threadIdx.x & 63, sub = lane % LPR;
+    const uint32_t wave = blockIdx.x * 4u + (threadIdx.x >> 6);
+    float w[VE], bb[VE];
     if (a.weight) {
-        float s = v[0] + v[1] + v[2] + v[3];
 #pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
-        const float mean = s * (1.0f / kD);
-        float d[4], q = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { d[e] = v[e] - mean; q += d[e] * d[e]; }
-#pragma unroll
-        for (int o = 8; o >= 1; o >>= 1) q += __shfl_xor(q, o, kWave);
-        const float rs = rsqrtf(q * (1.0f / kD) + a.ln_eps);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int c = 4 * sub + e;
-            v[e] = G::round(d[e] * rs * load_elem(a.weight, c, a.dt_norm) + load_elem(a.bias, c, a.dt_norm));
+        for (int e = 0; e < VE; ++e) {
+            w[e] = load_elem(a.weight, VE * sub + e, a.dt_norm);
+            bb[e] = load_elem(a.bias, VE * sub + e, a.dt_norm);
         }
     }
-    if (a.scale != 1.0f) {
+    uint4 raw[kHeadNormBatch];
+    int64_t oo[kHeadNormBatch];
+    bool live[kHeadNormBatch];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = G::round(v[e] * a.scale);
+    for (int i = 0; i < kHeadNormBatch; ++i) {
+        const uint32_t r = (wave * kHeadNormBatch + i) * RPW + lane / LPR;
+        live[i] = r < rows;
+        const uint32_t rr = live[i] ? r : 0u;
+        const uint32_t h = rr % static_cast<uint32_t>(a.H), bl = rr / static_cast<uint32_t>(a.H);
+        const uint32_t l = bl % static_cast<uint32_t>(a.L), b = bl / static_cast<uint32_t>(a.L);
+        const int64_t xo = b * a.x_sb + h * a.x_sh + l * a.x_sl + VE * sub;
+        oo[i] = b * a.o_sb + h * a.o_sh + l * a.o_sl + VE * sub;
+        raw[i] = *reinterpret_cast<const uint4 *>(static_cast<const char *>(a.x) + xo * es);
     }
-    if (live) {
-        raw *op = reinterpret_cast<raw *>(static_cast<char *>(a.out) +
-                                          (b * a.o_sb + h * a.o_sh + l * a.o_sl) * (DT == PRIME_F32 ? 4 : 2));
-        op[sub] = G::pack(v);
+#pragma unroll
+    for (int i = 0; i < kHeadNormBatch; ++i) {
+        float v[VE];
+        const uint32_t wd[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+            if constexpr (DT == PRIME_F32) v[e] = __uint_as_float(wd[e]);
+            else v[e] = Group<DT>::to_f(e & 1 ? wd[e >> 1] >> 16 : wd[e >> 1] & 0xffffu);
+        }
+        if (a.weight) {
+            float s = 0.f;
+#pragma unroll
+            for (int e = 0; e < VE; ++e) s += v[e];
+#pragma unroll
+            for (int o = LPR / 2; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+            const float mean = s * (1.0f / kD);
+            float q = 0.f;
+#pragma unroll
+            for (int e = 0; e < VE; ++e) { v[e] -= mean; q += v[e] * v[e]; }
+#pragma unroll
+            for (int o = LPR / 2; o >= 1; o >>= 1) q += __shfl_xor(q, o, kWave);
+            const float rs = rsqrtf(q * (1.0f / kD) + a.ln_eps);
+#pragma unroll
+            for (int e = 0; e < VE; ++e) v[e] = Group<DT>::round(v[e] * rs * w[e] + bb[e]);
+        }
+        if (a.scale != 1.0f) {
+#pragma unroll
+            for (int e = 0; e < VE; ++e) v[e] = Group<DT>::round(v[e] * a.scale);
+        }
+        uint4 o;
+        if constexpr (DT == PRIME_F32) {
+            o = make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+        } else {
+            uint32_t p[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[e] = Group<DT>::to_b(v[2 * e]) | (Group<DT>::to_b(v[2 * e + 1]) << 16);
+            o = make_uint4(p[0], p[1], p[2], p[3]);
+        }
+        if (live[i]) *reinterpret_cast<uint4 *>(static_cast<char *>(a.out) + oo[i] * es) = o;
     }
 }
 
 hipError_t launch_head_layernorm(const HeadNormArgs &a, hipStream_t stream) {
-    const int64_t rows = static_cast<int64_t>(a.B) * a.L * a.H;
-    const dim3 grid(static_cast<unsigned>((rows + 15) / 16)), block(256);
+    const uint32_t rows = static_cast<uint32_t>(a.B) * a.L * a.H;
+    const uint32_t per_block = 4u * kHeadNormBatch * (a.dt == PRIME_F32 ? 4u : 8u);  // 4 waves
+    const dim3 grid((rows + per_block - 1) / per_block), block(256);
     if (a.dt == PRIME_BF16) hipLaunchKernelGGL(head_layernorm_kernel<PRIME_BF16>, grid, block, 0, stream, a);
     else if (a.dt == PRIME_F16) hipLaunchKernelGGL(head_layernorm_kernel<PRIME_F16>, grid, block, 0, stream, a);
     else hipLaunchKernelGGL(head_layernorm_kernel<PRIME_F32>, grid, block, 0, stream, a);

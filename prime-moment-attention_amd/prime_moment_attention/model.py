@@ -171,16 +171,31 @@ class PrimeForCausalLM(nn.Module):
     def forward(self, input_ids: torch.Tensor, labels: Optional[torch.Tensor] = None,
                 states: Optional[List[Tuple[torch.Tensor, ...]]] = None, return_states: bool = False,
                 logits_to_keep: int = 0) -> Dict[str, Any]:
-        hidden_states = self.embed_tokens(input_ids)
+        # The blocks' residual adds are folded into the following RMSNorm
+        # (prime_add_rmsnorm stores the rounded sum, as the separate add does):
+        # x is this call's own residual stream, updated in place; `pending` is
+        # the MLP output still to be added.
+        x = self.embed_tokens(input_ids)
+        hidden = x.shape[-1]
         next_states = [] if return_states else None
+        pending = None
         for i, layer in enumerate(self.layers):
-            hidden_states, ns = layer(hidden_states, state=states[i] if states is not None else None,
-                                      return_state=return_states)
+            at = layer.self_attn
+            n1 = torch.empty_like(x)
+            _lib.add_rmsnorm(x, pending, layer.input_layernorm.weight, n1, layer.input_layernorm.eps)
+            h, ns = at(n1, state=states[i] if states is not None else None, return_state=return_states)
+            n2 = torch.empty_like(x)
+            _lib.add_rmsnorm(x, h, layer.post_attention_layernorm.weight, n2, layer.post_attention_layernorm.eps)
+            pending = layer.mlp(n2)
             if return_states:
                 next_states.append(ns)
         if logits_to_keep:
-            hidden_states = hidden_states[:, -logits_to_keep:]
-        logits = self.lm_head(self.norm(hidden_states))
+            x = x[:, -logits_to_keep:].contiguous()
+            pending = pending[:, -logits_to_keep:].contiguous() if pending is not None else None
+        nf = torch.empty_like(x)
+        _lib.add_rmsnorm(x.view(-1, hidden), pending.view(-1, hidden) if pending is not None else None,
+                         self.norm.weight, nf.view(-1, hidden), self.norm.eps)
+        logits = self.lm_head(nf)
         loss = None
         if labels is not None:
             shift_logits = logits[..., :-1, :].contiguous().to(torch.float32)
