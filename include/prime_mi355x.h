@@ -227,8 +227,9 @@ int prime_argmax(const void *logits, int dtype, int n, int vocab, int64_t stride
  * Launch timer.  No counterpart in the reference: it serves benchmark harnesses
  * that need the device time of ONE kernel of a multi-kernel call.
  * prime_timer_enable(mask) (process-wide; bit (1 << PRIME_KERNEL_*) selects a
- * kernel, 0 disables) brackets every launch of the selected kernels by a pair
- * of HIP events on the call's stream.  prime_timer_read waits for the recorded
+ * kernel, 0 disables) times every launch of the selected kernels with a pair
+ * of HIP events that the dispatch itself stamps at its start and end
+ * (hipExtLaunchKernel; no extra packets on the stream).  prime_timer_read waits for the recorded
  * events and returns the summed device time and launch count of one kernel
  * since the last reset.  Event objects are created while enabled (never on the
  * default, disabled path) and kept for reuse.

@@ -140,10 +140,11 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
 hipError_t launch_decode_step(const DecodeArgs &a, hipStream_t stream) {
     const int BH = a.B * a.H;
     const int blocks = (BH + kDecodeWaves - 1) / kDecodeWaves;
-    timer_begin(PRIME_KERNEL_DECODE, stream);
-    hipLaunchKernelGGL(decode_step_kernel, dim3(blocks), dim3(kDecodeWaves * kWave), 0, stream, a);
+    const TimerEvents t = timer_events(PRIME_KERNEL_DECODE);
+    hipExtLaunchKernelGGL(decode_step_kernel, dim3(blocks), dim3(kDecodeWaves * kWave), 0, stream, t.start, t.stop, 0,
+                          a);
     const hipError_t e = hipGetLastError();
-    timer_end(PRIME_KERNEL_DECODE, stream);
+    if (e != hipSuccess) timer_drop(t);
     return e;
 }
 

@@ -592,15 +592,15 @@ SideStream *side_stream() {
 }
 
 void launch_prep(const DeltaArgs &a, hipStream_t s) {
-    timer_begin(PRIME_KERNEL_DELTA_PREP, s);
-    hipLaunchKernelGGL(delta_prep_kernel, dim3(a.B * a.H * a.nw), dim3(256), 0, s, a);
-    timer_end(PRIME_KERNEL_DELTA_PREP, s);
+    const TimerEvents t = timer_events(PRIME_KERNEL_DELTA_PREP);
+    hipExtLaunchKernelGGL(delta_prep_kernel, dim3(a.B * a.H * a.nw), dim3(256), 0, s, t.start, t.stop, 0, a);
+    if (hipPeekAtLastError() != hipSuccess) timer_drop(t);
 }
 
 void launch_scan(const DeltaArgs &a, hipStream_t s) {
-    timer_begin(PRIME_KERNEL_DELTA_SCAN, s);
-    hipLaunchKernelGGL(delta_scan_kernel, dim3(a.B * a.H), dim3(256), 0, s, a);
-    timer_end(PRIME_KERNEL_DELTA_SCAN, s);
+    const TimerEvents t = timer_events(PRIME_KERNEL_DELTA_SCAN);
+    hipExtLaunchKernelGGL(delta_scan_kernel, dim3(a.B * a.H), dim3(256), 0, s, t.start, t.stop, 0, a);
+    if (hipPeekAtLastError() != hipSuccess) timer_drop(t);
 }
 
 DeltaArgs window_args(DeltaArgs a, int c0, int window, int NC, uint8_t *rec) {
@@ -658,10 +658,12 @@ hipError_t launch_delta_prefill(DeltaArgs a, int NC, int cap, hipStream_t stream
 
 hipError_t launch_delta_step(const DeltaStepArgs &a, hipStream_t stream) {
     const int n = a.B * a.H;
-    timer_begin(PRIME_KERNEL_DELTA_STEP, stream);
-    hipLaunchKernelGGL(delta_step_kernel, dim3((n + kStepWaves - 1) / kStepWaves), dim3(kStepWaves * 64), 0, stream, a);
-    timer_end(PRIME_KERNEL_DELTA_STEP, stream);
-    return hipGetLastError();
+    const TimerEvents t = timer_events(PRIME_KERNEL_DELTA_STEP);
+    hipExtLaunchKernelGGL(delta_step_kernel, dim3((n + kStepWaves - 1) / kStepWaves), dim3(kStepWaves * 64), 0, stream,
+                          t.start, t.stop, 0, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) timer_drop(t);
+    return e;
 }
 
 }  // namespace prime

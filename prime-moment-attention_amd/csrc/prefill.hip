@@ -671,32 +671,37 @@ __global__ __launch_bounds__(256) void segment_scan_kernel(const PrefillArgs a) 
 }
 
 template <bool F32IN>
-static void launch_variant(PrefillArgs a, hipStream_t stream) {
+static hipError_t launch_variant(PrefillArgs a, hipStream_t stream) {
     const int Sq = a.B * a.H;
+    hipError_t e;
     if (a.G > 1) {
         // A: state contribution of every segment but the last, from zero
         a.nseg_launch = a.G - 1;
-        timer_begin(PRIME_KERNEL_PREFILL_SEGMENTS, stream);
-        if constexpr (F32IN) hipLaunchKernelGGL((prefill_kernel<true, true>), dim3(Sq * (a.G - 1)), dim3(256), 0, stream, a);
-        else launch_prefill_bf16(a, true, Sq * (a.G - 1), stream);
-        timer_end(PRIME_KERNEL_PREFILL_SEGMENTS, stream);
+        const TimerEvents ta = timer_events(PRIME_KERNEL_PREFILL_SEGMENTS);
+        if constexpr (F32IN)
+            hipExtLaunchKernelGGL((prefill_kernel<true, true>), dim3(Sq * (a.G - 1)), dim3(256), 0, stream, ta.start,
+                                  ta.stop, 0, a);
+        else launch_prefill_bf16(a, true, Sq * (a.G - 1), stream, ta);
+        if ((e = hipGetLastError()) != hipSuccess) return timer_drop(ta), e;
         // B: exclusive scan over segments (incoming state first)
         const int64_t n = static_cast<int64_t>(Sq) * kWsElems;
-        timer_begin(PRIME_KERNEL_SEGMENT_SCAN, stream);
-        hipLaunchKernelGGL(segment_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, a);
-        timer_end(PRIME_KERNEL_SEGMENT_SCAN, stream);
+        const TimerEvents tb = timer_events(PRIME_KERNEL_SEGMENT_SCAN);
+        hipExtLaunchKernelGGL(segment_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                              tb.start, tb.stop, 0, a);
+        if ((e = hipGetLastError()) != hipSuccess) return timer_drop(tb), e;
     }
     a.nseg_launch = a.G;
-    timer_begin(PRIME_KERNEL_PREFILL_CHUNKS, stream);
-    if constexpr (F32IN) hipLaunchKernelGGL((prefill_kernel<true, false>), dim3(Sq * a.G), dim3(512), 0, stream, a);
-    else launch_prefill_bf16(a, false, Sq * a.G, stream);
-    timer_end(PRIME_KERNEL_PREFILL_CHUNKS, stream);
+    const TimerEvents tc = timer_events(PRIME_KERNEL_PREFILL_CHUNKS);
+    if constexpr (F32IN)
+        hipExtLaunchKernelGGL((prefill_kernel<true, false>), dim3(Sq * a.G), dim3(512), 0, stream, tc.start, tc.stop, 0,
+                              a);
+    else launch_prefill_bf16(a, false, Sq * a.G, stream, tc);
+    if ((e = hipGetLastError()) != hipSuccess) timer_drop(tc);
+    return e;
 }
 
 hipError_t launch_prefill(PrefillArgs a, hipStream_t stream) {
-    if (a.dt_in == PRIME_F32) launch_variant<true>(a, stream);
-    else launch_variant<false>(a, stream);
-    return hipGetLastError();
+    return a.dt_in == PRIME_F32 ? launch_variant<true>(a, stream) : launch_variant<false>(a, stream);
 }
 
 }  // namespace prime

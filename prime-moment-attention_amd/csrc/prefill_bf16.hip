@@ -456,9 +456,11 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
     if (u == 0 && lane == 0) o_k0[offk0] = k0 + (STATE_ONLY ? 0.f : linit * sKi0);
 }
 
-void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream) {
-    if (state_only) hipLaunchKernelGGL(prefill_bf16_kernel<true>, dim3(grid), dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(prefill_bf16_kernel<false>, dim3(grid), dim3(512), 0, stream, a);
+void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream, TimerEvents t) {
+    if (state_only)
+        hipExtLaunchKernelGGL(prefill_bf16_kernel<true>, dim3(grid), dim3(256), 0, stream, t.start, t.stop, 0, a);
+    else
+        hipExtLaunchKernelGGL(prefill_bf16_kernel<false>, dim3(grid), dim3(512), 0, stream, t.start, t.stop, 0, a);
 }
 
 }  // namespace prime

@@ -1,6 +1,8 @@
 // Kernel argument blocks and launchers shared by the kernels and the C-ABI layer.
 #pragma once
 
+#include <hip/hip_ext.h>
+
 #include "prime_common.h"
 
 namespace prime {
@@ -130,12 +132,19 @@ constexpr int kDeltaDefaultWindow = 128;         // record chunks of the recomme
 hipError_t launch_delta_prefill(DeltaArgs a, int NC, int cap, hipStream_t stream);
 hipError_t launch_delta_step(const DeltaStepArgs &a, hipStream_t stream);
 
+// Launch timer (the C-ABI prime_timer_* calls).  timer_events(kernel) hands
+// out the event pair for one launch of `kernel` while that kernel is being
+// timed (both null otherwise); the launch passes them to hipExtLaunchKernelGGL,
+// which stamps them with the dispatch's own start and end times (no marker
+// packets between kernels).  timer_drop() withdraws a pair whose launch failed.
+struct TimerEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+TimerEvents timer_events(int kernel);
+void timer_drop(const TimerEvents &t);
+
 // bf16-input prefill kernels (prefill_bf16.hip): the state-only segment pass
 // (256 threads) or the fused chunk loop (512 threads) over `grid` workgroups.
-void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream);
-
-// Launch timer hooks (the C-ABI prime_timer_* calls); no-ops while disabled.
-void timer_begin(int kernel, hipStream_t stream);
-void timer_end(int kernel, hipStream_t stream);
+void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream, TimerEvents t);
 
 }  // namespace prime

@@ -1,5 +1,6 @@
-// Launch timer: HIP event pairs around kernel launches, for benchmark harnesses
-// that need one kernel's device time out of a multi-kernel call.
+// Launch timer: HIP event pairs stamped by the kernel dispatches themselves
+// (hipExtLaunchKernelGGL), for benchmark harnesses that need one kernel's
+// device time out of a multi-kernel call.
 #include <atomic>
 #include <mutex>
 #include <vector>
@@ -18,38 +19,36 @@ std::atomic<unsigned> g_mask{0};
 std::mutex g_mu;
 std::vector<Pair> g_pairs;   // recorded since the last reset, in launch order
 std::vector<Pair> g_spare;   // created events kept for reuse
-thread_local int t_open = -1;  // index into g_pairs of the pair begun by this thread
 
 }  // namespace
 
-void timer_begin(int kernel, hipStream_t stream) {
-    if (!(g_mask.load(std::memory_order_relaxed) & (1u << kernel))) return;
+TimerEvents timer_events(int kernel) {
+    TimerEvents t;
+    if (!(g_mask.load(std::memory_order_relaxed) & (1u << kernel))) return t;
     std::lock_guard<std::mutex> lk(g_mu);
     Pair p;
     if (!g_spare.empty()) {
         p = g_spare.back();
         g_spare.pop_back();
-    } else if (hipEventCreate(&p.start) != hipSuccess || hipEventCreate(&p.stop) != hipSuccess) {
-        t_open = -1;
-        return;
-    }
-    if (hipEventRecord(p.start, stream) != hipSuccess) {
-        g_spare.push_back(p);
-        t_open = -1;
-        return;
+    } else {
+        if (hipEventCreate(&p.start) != hipSuccess) return t;  // untimed launch
+        if (hipEventCreate(&p.stop) != hipSuccess) {
+            (void)hipEventDestroy(p.start);
+            return t;
+        }
     }
     p.kernel = kernel;
     g_pairs.push_back(p);
-    t_open = static_cast<int>(g_pairs.size()) - 1;
+    t.start = p.start;
+    t.stop = p.stop;
+    return t;
 }
 
-void timer_end(int kernel, hipStream_t stream) {
-    if (t_open < 0) return;
+void timer_drop(const TimerEvents &t) {
+    if (!t.start) return;
     std::lock_guard<std::mutex> lk(g_mu);
-    if (t_open < static_cast<int>(g_pairs.size()) && g_pairs[t_open].kernel == kernel &&
-        hipEventRecord(g_pairs[t_open].stop, stream) != hipSuccess)
-        g_pairs[t_open].kernel = -1;  // unusable pair: left out of every reading
-    t_open = -1;
+    for (auto &p : g_pairs)
+        if (p.start == t.start) p.kernel = -1;  // never recorded: left out of every reading
 }
 
 }  // namespace prime
@@ -64,7 +63,7 @@ int prime_timer_enable(unsigned mask) {
 int prime_timer_reset(void) {
     std::lock_guard<std::mutex> lk(prime::g_mu);
     for (auto &p : prime::g_pairs) {
-        if (hipEventSynchronize(p.stop) != hipSuccess) return PRIME_ERR_HIP;
+        if (p.kernel >= 0 && hipEventSynchronize(p.stop) != hipSuccess) return PRIME_ERR_HIP;
         p.kernel = -1;
         prime::g_spare.push_back(p);
     }
