@@ -214,6 +214,21 @@ int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int
                          void *stream);
 
 /*
+ * Linear layer of the decode step, y = epilogue(x w^T) (F.linear without bias;
+ * model.py:59-68, 101-118, 160 at one token per sequence): x [M, K], w [N, K],
+ * y [M, N], all BF16, row strides ldx, ldw, ldy in elements; fp32
+ * accumulation, one rounding to bf16.  Epilogues: PRIME_EPILOGUE_NONE, or
+ * PRIME_EPILOGUE_GELU = the exact GELU 0.5 t (1 + erf(t / sqrt 2)) of
+ * F.gelu.  Built for few rows (M up to a few hundred: decode batches), where
+ * library GEMMs are latency-bound.  K a multiple of 64; N a multiple of 4;
+ * x, w rows 16-byte aligned, y rows 8-byte aligned; y may not overlap x or w.
+ */
+#define PRIME_EPILOGUE_NONE 0
+#define PRIME_EPILOGUE_GELU 1
+int prime_linear(const void *x, const void *w, void *y, int M, int N, int K, int64_t ldx, int64_t ldw,
+                 int64_t ldy, int dtype, int epilogue, void *stream);
+
+/*
  * Greedy token choice of the generate loop (model.py:230-231, argmax over the
  * vocabulary at temperature 0): out[i] = the first index j of the largest
  * logits[i, j], NaN counting as the largest value (torch.argmax's answer).

@@ -210,6 +210,29 @@ int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int
     return check_hip(prime::launch_head_layernorm(a, static_cast<hipStream_t>(stream)), "head_layernorm launch");
 }
 
+int prime_linear(const void *x, const void *w, void *y, int M, int N, int K, int64_t ldx, int64_t ldw,
+                 int64_t ldy, int dtype, int epilogue, void *stream) {
+    g_err[0] = 0;
+    if (!x || !w || !y) return fail(PRIME_ERR_INVALID_ARG, "prime_linear: null argument");
+    if (M <= 0 || N <= 0 || K <= 0 || K % 64 || N % 4)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes M=%d N=%d K=%d (K a multiple of 64, N of 4)", M, N, K);
+    if (ldx < K || ldw < K || ldy < N) return fail(PRIME_ERR_INVALID_ARG, "row strides below the row lengths");
+    if (dtype != PRIME_BF16) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "prime_linear: BF16 only");
+    if (epilogue != PRIME_EPILOGUE_NONE && epilogue != PRIME_EPILOGUE_GELU)
+        return fail(PRIME_ERR_INVALID_ARG, "unknown epilogue %d", epilogue);
+    if (!aligned16(x) || !aligned16(w) || (ldx % 8) || (ldw % 8))
+        return fail(PRIME_ERR_MISALIGNED, "x and w rows must start on 16-byte boundaries");
+    if ((reinterpret_cast<uintptr_t>(y) & 7) || (ldy % 4))
+        return fail(PRIME_ERR_MISALIGNED, "y rows must start on 8-byte boundaries");
+    const size_t nx = static_cast<size_t>((M - 1) * ldx + K) * 2, nw = static_cast<size_t>((N - 1) * ldw + K) * 2,
+                 ny = static_cast<size_t>((M - 1) * ldy + N) * 2;
+    if (overlap(y, ny, x, nx) || overlap(y, ny, w, nw)) return fail(PRIME_ERR_ALIAS, "y overlaps x or w");
+    prime::LinearArgs a{};
+    a.x = x; a.w = w; a.y = y; a.ldx = ldx; a.ldw = ldw; a.ldy = ldy;
+    a.M = M; a.N = N; a.K = K; a.epilogue = epilogue;
+    return check_hip(prime::launch_linear(a, static_cast<hipStream_t>(stream)), "linear launch");
+}
+
 int prime_argmax(const void *logits, int dtype, int n, int vocab, int64_t stride_n, int64_t *out, void *stream) {
     g_err[0] = 0;
     if (!logits || !out) return fail(PRIME_ERR_INVALID_ARG, "prime_argmax: null argument");

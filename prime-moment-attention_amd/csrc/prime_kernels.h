@@ -55,6 +55,15 @@ struct HeadNormArgs {
 };
 hipError_t launch_head_layernorm(const HeadNormArgs &a, hipStream_t stream);
 
+// Skinny bf16 linear layer y = epilogue(x w^T) (gemm.hip).
+struct LinearArgs {
+    const void *x, *w;
+    void *y;
+    int64_t ldx, ldw, ldy;  // row strides in elements
+    int M, N, K, epilogue;
+};
+hipError_t launch_linear(const LinearArgs &a, hipStream_t stream);
+
 constexpr int kNormMaxGroups = 16;  // 4-element groups per lane: hidden <= 4 * 64 * 16 = 4096
 hipError_t launch_add_rmsnorm(const RmsNormArgs &a, hipStream_t stream);
 

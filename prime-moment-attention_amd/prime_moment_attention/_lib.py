@@ -26,7 +26,7 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
            "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
            "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_argmax",
-           "prime_head_layernorm")
+           "prime_head_layernorm", "prime_linear")
 
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
@@ -96,6 +96,8 @@ def load() -> ctypes.CDLL:
     L.prime_head_layernorm.argtypes = [P(PrimeTensor)] * 2 + [ctypes.c_int] * 4 + [fp, fp, ctypes.c_int,
                                                                                  ctypes.c_float, ctypes.c_float, fp]
     L.prime_head_layernorm.restype = ctypes.c_int
+    L.prime_linear.argtypes = [fp, fp, fp] + [ctypes.c_int] * 3 + [ctypes.c_int64] * 3 + [ctypes.c_int] * 2 + [fp]
+    L.prime_linear.restype = ctypes.c_int
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     v = L.prime_abi_version()
     if v != ABI_VERSION:
@@ -286,6 +288,30 @@ def head_layernorm(x: torch.Tensor, out: torch.Tensor, norm: Optional[torch.nn.L
                                      ctypes.c_void_p(b.data_ptr()) if b is not None else None, pdt,
                                      float(eps), float(scale), _stream(x.device))
     _check(rc, "prime_head_layernorm")
+
+
+EPILOGUE_NONE, EPILOGUE_GELU = 0, 1
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, epilogue: int = EPILOGUE_NONE) -> torch.Tensor:
+    """prime_linear: out = epilogue(x @ w.T) for bf16 x [M, K], w [N, K],
+    out [M, N] (rows with a contiguous last dimension); returns out."""
+    _dev_check(x, w, out)
+    if x.dim() != 2 or w.dim() != 2 or out.dim() != 2:
+        raise ValueError("x, w and out must be 2-D")
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K or out.shape != (M, N):
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, w {tuple(w.shape)}, out {tuple(out.shape)}")
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
+        raise RuntimeError("prime_linear takes bf16 tensors")
+    if x.stride(1) != 1 or w.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError("the last dimension must be contiguous")
+    rc = load().prime_linear(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(w.data_ptr()),
+                             ctypes.c_void_p(out.data_ptr()), M, N, K, x.stride(0), w.stride(0), out.stride(0),
+                             _DTYPES[torch.bfloat16], int(epilogue), _stream(x.device))
+    _check(rc, "prime_linear")
+    return out
 
 
 def argmax(logits: torch.Tensor, out: torch.Tensor) -> None:

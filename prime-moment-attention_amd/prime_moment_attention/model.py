@@ -232,6 +232,21 @@ class PrimeForCausalLM(nn.Module):
         return generated
 
 
+def _decode_linear(x: torch.Tensor, w: torch.Tensor, gelu: bool = False) -> torch.Tensor:
+    """x @ w.T (then the exact GELU) for the decode step's few rows: the skinny
+    HIP kernel (prime_linear) on the shapes where it beats the library GEMM
+    on MI355X (up to 64 rows, or K and N both at most 1024), the library GEMM
+    otherwise."""
+    M, K = x.shape
+    N = w.shape[0]
+    if (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and K % 64 == 0 and N % 4 == 0 and K <= 1024
+            and (M <= 64 or N <= 1024)):
+        return _lib.linear(x, w, torch.empty(M, N, device=x.device, dtype=x.dtype),
+                           _lib.EPILOGUE_GELU if gelu else _lib.EPILOGUE_NONE)
+    y = F.linear(x, w)
+    return F.gelu(y) if gelu else y
+
+
 class GreedyDecoder:
     """Greedy decoding with in-place states and a HIP-graph-captured step.
 
@@ -290,16 +305,19 @@ class GreedyDecoder:
             n1 = torch.empty_like(x)
             _lib.add_rmsnorm(x, pending, layer.input_layernorm.weight, n1, layer.input_layernorm.eps)
             nq, nk = at.num_heads * at.head_dim, at.num_kv_heads * at.head_dim
-            qkv = F.linear(n1, self._qkv[id(at)])
+            qkv = _decode_linear(n1, self._qkv[id(at)])
             q = qkv[:, :nq].view(B, at.num_heads, at.head_dim)
             k = qkv[:, nq:nq + nk].view(B, at.num_kv_heads, at.head_dim)
             v = qkv[:, nq + nk:].view(B, at.num_kv_heads, at.head_dim)
             y = torch.empty(B, at.num_heads, at.head_dim, device=x.device, dtype=x.dtype)
             _lib.decode_step_qknorm(q, k, v, self._decay[id(at)], at.eps, self._norm[id(at)], st, st, y)
-            a = at.o_proj(y.view(B, -1))
+            a = _decode_linear(y.view(B, -1), at.o_proj.weight)
             n2 = torch.empty_like(x)
             _lib.add_rmsnorm(x, a, layer.post_attention_layernorm.weight, n2, layer.post_attention_layernorm.eps)
-            pending = layer.mlp(n2)
+            if isinstance(layer.mlp, PrimeGeluMLP):
+                pending = F.linear(_decode_linear(n2, layer.mlp.up_proj.weight, gelu=True), layer.mlp.down_proj.weight)
+            else:
+                pending = layer.mlp(n2)
         nf = torch.empty_like(x)
         _lib.add_rmsnorm(x, pending, m.norm.weight, nf, m.norm.eps)
         _lib.argmax(m.lm_head(nf), self.token)  # the embedding above has consumed the old token

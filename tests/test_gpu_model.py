@@ -172,3 +172,33 @@ def test_head_layernorm_matches_module_ops(dtype, tol, with_ln):
     assert bool((d <= bound).all()), float(d.max())
     if not with_ln:
         assert torch.equal(x, ref)  # a power-of-two scale is exact
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 2304, 768), (256, 768, 3072), (3, 100, 64), (37, 3072, 768), (1, 8, 128),
+                                   (300, 3000, 64), (256, 3072, 768),
+                                   (300, 52, 192)])
+@pytest.mark.parametrize("gelu", [False, True])
+def test_linear_matches_torch(M, N, K, gelu):
+    """prime_linear (skinny bf16 GEMM, fp32 accumulation) == F.linear in fp32
+    then the exact GELU, rounded once to bf16; x a strided row view."""
+    from prime_moment_attention import _lib
+    g = torch.Generator(device=dev()).manual_seed(M * 7 + N + K)
+    xb = torch.randn(M, K + 64, device=dev(), generator=g).bfloat16()
+    x = xb[:, 32:32 + K]  # row stride K + 64, 64-byte offset
+    w = (torch.randn(N, K, device=dev(), generator=g) * K ** -0.5).bfloat16()
+    out = torch.full((M, N), float("nan"), device=dev(), dtype=torch.bfloat16)
+    _lib.linear(x, w, out, _lib.EPILOGUE_GELU if gelu else _lib.EPILOGUE_NONE)
+    torch.cuda.synchronize()
+    ref = x.float() @ w.float().T
+    if gelu:
+        ref = torch.nn.functional.gelu(ref)
+    d = (out.float() - ref).abs()
+    assert bool((d <= ref.abs() * 2 ** -7 + 1e-3 * ref.abs().max()).all()), float(d.max())
+
+
+def test_linear_rejects_bad_shapes():
+    from prime_moment_attention import _lib
+    x = torch.zeros(4, 100, device=dev(), dtype=torch.bfloat16)
+    w = torch.zeros(8, 100, device=dev(), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        _lib.linear(x, w, torch.empty(4, 8, device=dev(), dtype=torch.bfloat16))
