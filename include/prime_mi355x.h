@@ -229,6 +229,40 @@ int prime_linear(const void *x, const void *w, void *y, int M, int N, int K, int
                  int64_t ldy, int dtype, int epilogue, void *stream);
 
 /*
+ * Selective PRIME (PrimeSelectiveMomentAttention, selective.py:264-444): the
+ * same moment recurrence with a decay per token and per head,
+ *   l_t = exp(-Delta_t / tau_h)  (Delta_t = softplus(W_delta x_t + b), clamped),
+ * and the key scaled by an inverse temperature beta_h:
+ *   S0 = l S0 + v;  S1 = l S1 + beta k v^T;  S2 = l S2 + 1/2 beta^2 (k*k) v^T
+ *   K0 = l K0 + 1;  K1 = l K1 + beta k;      K2 = l K2 + 1/2 beta^2 k*k
+ *   y  = (S0 + S1^T q + S2^T (q*q)) / max(K0 + q.K1 + (q*q).K2, eps)
+ * Note the state convention: S2 and K2 include the 1/2 (selective.py:395-400),
+ * unlike the base form's.  q arrives pre-scaled by 1/sqrt(D) as for the base
+ * form (selective.py:362).
+ *
+ * prime_selective_prefill: L tokens of BF16 q/k/v [B, H(kv), L, 64] (strided
+ * as prime_chunked_prefill), log_decay fp32 [B, H, L] contiguous = log l_t
+ * (natural log, <= 0), k_scale fp32 [H] = beta_h; state_in may be NULL (zero);
+ * same y, state_out, workspace rules as prime_chunked_prefill (whose
+ * workspace size applies).  Replaces the parallel branch (selective.py:
+ * 414-440), which builds the full [L, L] decay matrix; the reference branch
+ * ignores an incoming state, a caller reproducing it passes NULL.
+ *
+ * prime_selective_decode_step: one token; decay_bh fp32 [B, H] = l_t per
+ * (sequence, head) (selective.py:386), k_scale [H]; norm (may be NULL) as for
+ * prime_decode_step_qknorm (the module's QK LayerNorm and q scale applied to
+ * raw projections).  Replaces selective.py:384-409.
+ */
+int prime_selective_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
+                            int H, int H_kv, int L, int D, const float *log_decay, const float *k_scale, float eps,
+                            const prime_state_t *state_in, const prime_tensor_t *y, const prime_state_t *state_out,
+                            void *workspace, size_t workspace_bytes, void *stream);
+int prime_selective_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
+                                int H, int H_kv, int D, const float *decay_bh, const float *k_scale, float eps,
+                                const prime_qk_norm_t *norm, const prime_state_t *state_in,
+                                const prime_state_t *state_out, const prime_tensor_t *y, void *stream);
+
+/*
  * Greedy token choice of the generate loop (model.py:230-231, argmax over the
  * vocabulary at temperature 0): out[i] = the first index j of the largest
  * logits[i, j], NaN counting as the largest value (torch.argmax's answer).

@@ -58,6 +58,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_delta_chunked.argtypes = [i, i, i, i, _dp, _dp, _dp, _dp, _dp, d, d, i, _dp, _dp]
         L.oracle_delta_tokenwise.argtypes = [i, i, i, _dp, _dp, _dp, _dp, _dp, i, _dp, _dp]
         L.oracle_delta_step.argtypes = [i, i, _dp, _dp, _dp, _dp, _dp, d, _dp, _dp]
+        L.oracle_selective_recurrent.argtypes = [i, i, i, _dp, _dp, _dp, _dp, _dp, d] + [_dp] * 7
+        L.oracle_selective_parallel.argtypes = [i, i, i, _dp, _dp, _dp, _dp, _dp, _dp, d] + [_dp] * 7
         f = ctypes.c_float
         L.baseline_decode_step.argtypes = [i, i, i, _fp, _fp, _fp, _fp, f] + [_fp] * 7 + [i]
         L.baseline_prefill.argtypes = [i, i, i, i, _fp, _fp, _fp, _fp, f] + [_fp] * 7 + [i]
@@ -125,6 +127,31 @@ def dense(q, k, v, lam, eps=1.0, state=None):
     y = np.zeros_like(q)
     lib().oracle_dense(BH, L, D, _p(q), _p(k), _p(v), _p(_lam(lam, BH)), eps, has,
                        *[_p(x) for x in s], _p(y))
+    return y, s
+
+
+def selective_recurrent(q, k, v, lam_t, beta, eps=1.0, state=None):
+    """Selective PRIME step branch token by token (selective.py:384-409):
+    lam_t [BH, L] per-token decays, beta [BH]; state in the selective
+    convention (S2, K2 carry the 1/2)."""
+    q, k, v = _c64(q), _c64(k), _c64(v)
+    BH, L, D = q.shape
+    s, _ = _state_copy(state, BH, D)
+    y = np.zeros_like(q)
+    lib().oracle_selective_recurrent(BH, L, D, _p(q), _p(k), _p(v), _p(_c64(lam_t).reshape(BH, L)),
+                                     _p(_lam(beta, BH)), eps, *[_p(x) for x in s], _p(y))
+    return y, s
+
+
+def selective_parallel(q, k, v, delta, tau, beta, eps=1.0):
+    """Selective PRIME parallel branch (selective.py:414-440): delta [BH, L]
+    (the softplus step sizes), tau and beta [BH]; no incoming state."""
+    q, k, v = _c64(q), _c64(k), _c64(v)
+    BH, L, D = q.shape
+    s = zero_state(BH, D)
+    y = np.zeros_like(q)
+    lib().oracle_selective_parallel(BH, L, D, _p(q), _p(k), _p(v), _p(_c64(delta).reshape(BH, L)),
+                                    _p(_lam(tau, BH)), _p(_lam(beta, BH)), eps, *[_p(x) for x in s], _p(y))
     return y, s
 
 

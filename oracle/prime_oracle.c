@@ -506,3 +506,117 @@ void oracle_delta_step(int BH, int D, const double *psi, const double *phi,
         }
     }
 }
+
+/* ------------------------------------------------------------------------- */
+/* Selective PRIME, step branch applied token by token (selective.py:384-409):*/
+/* per-token decay lam[bh][t], key weights beta (first order) and beta^2 / 2  */
+/* (second order) folded into the state, whose S2 / K2 therefore carry the    */
+/* 1/2; the readout weighs the second-order term by 1.                        */
+/* ------------------------------------------------------------------------- */
+void oracle_selective_recurrent(int BH, int L, int D, const double *q, const double *k,
+                                const double *v, const double *lam, const double *beta, double eps,
+                                double *S0, double *S1, double *S2, double *K0,
+                                double *K1, double *K2, double *y)
+{
+    for (int bh = 0; bh < BH; ++bh) {
+        double *s0 = S0 + (size_t)bh * D, *s1 = S1 + (size_t)bh * D * D;
+        double *s2 = S2 + (size_t)bh * D * D, *k0 = K0 + bh;
+        double *k1 = K1 + (size_t)bh * D, *k2 = K2 + (size_t)bh * D;
+        const double b1 = beta[bh], b2 = 0.5 * beta[bh] * beta[bh];
+        for (int t = 0; t < L; ++t) {
+            const double l = lam[(size_t)bh * L + t];
+            const double *qt = q + ((size_t)bh * L + t) * D;
+            const double *kt = k + ((size_t)bh * L + t) * D;
+            const double *vt = v + ((size_t)bh * L + t) * D;
+            double *yt = y + ((size_t)bh * L + t) * D;
+            /* selective.py:394-400 */
+            for (int j = 0; j < D; ++j) s0[j] = l * s0[j] + vt[j];
+            for (int i = 0; i < D; ++i)
+                for (int j = 0; j < D; ++j) {
+                    s1[IDX2(i, j, D)] = l * s1[IDX2(i, j, D)] + b1 * kt[i] * vt[j];
+                    s2[IDX2(i, j, D)] = l * s2[IDX2(i, j, D)] + b2 * kt[i] * kt[i] * vt[j];
+                }
+            *k0 = l * (*k0) + 1.0;
+            for (int i = 0; i < D; ++i) {
+                k1[i] = l * k1[i] + b1 * kt[i];
+                k2[i] = l * k2[i] + b2 * kt[i] * kt[i];
+            }
+            /* selective.py:402-408 */
+            double den = *k0;
+            for (int i = 0; i < D; ++i) den += qt[i] * k1[i] + qt[i] * qt[i] * k2[i];
+            if (den < eps) den = eps;
+            for (int j = 0; j < D; ++j) {
+                double num = s0[j];
+                for (int i = 0; i < D; ++i)
+                    num += qt[i] * s1[IDX2(i, j, D)] + qt[i] * qt[i] * s2[IDX2(i, j, D)];
+                yt[j] = num / den;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* Selective PRIME, parallel branch (selective.py:414-440): C = cumsum(Delta),*/
+/* weight(i <- j) = (1 + b q_i.k_j + b^2/2 (q_i*q_i).(k_j*k_j))               */
+/*                  * exp(-max(C_i - C_j, 0) / tau) [i >= j],                  */
+/* y_i = sum_j weight v_j / max(sum_j weight, eps); the returned state from    */
+/* decay_to_end = exp(-(C_L-1 - C_j) / tau).  No incoming state (the branch    */
+/* ignores it).                                                               */
+/* ------------------------------------------------------------------------- */
+void oracle_selective_parallel(int BH, int L, int D, const double *q, const double *k,
+                               const double *v, const double *delta, const double *tau,
+                               const double *beta, double eps,
+                               double *S0, double *S1, double *S2, double *K0,
+                               double *K1, double *K2, double *y)
+{
+    double *C = (double *)malloc(sizeof(double) * (size_t)L);
+    double *w = (double *)malloc(sizeof(double) * (size_t)L);
+    for (int bh = 0; bh < BH; ++bh) {
+        const double b1 = beta[bh], b2 = 0.5 * beta[bh] * beta[bh], ta = tau[bh];
+        double acc = 0.0;
+        for (int t = 0; t < L; ++t) { acc += delta[(size_t)bh * L + t]; C[t] = acc; }
+        for (int i = 0; i < L; ++i) {
+            const double *qi = q + ((size_t)bh * L + i) * D;
+            double den = 0.0;
+            for (int j = 0; j <= i; ++j) {
+                const double *kj = k + ((size_t)bh * L + j) * D;
+                double s1 = 0.0, s2 = 0.0;
+                for (int d = 0; d < D; ++d) { s1 += qi[d] * kj[d]; s2 += qi[d] * qi[d] * kj[d] * kj[d]; }
+                const double dd = C[i] - C[j] > 0.0 ? C[i] - C[j] : 0.0;
+                w[j] = (1.0 + b1 * s1 + b2 * s2) * exp(-dd / ta);
+                den += w[j];
+            }
+            if (den < eps) den = eps;
+            double *yi = y + ((size_t)bh * L + i) * D;
+            for (int d = 0; d < D; ++d) {
+                double num = 0.0;
+                for (int j = 0; j <= i; ++j) num += w[j] * v[((size_t)bh * L + j) * D + d];
+                yi[d] = num / den;
+            }
+        }
+        /* selective.py:428-438: the state after the last token */
+        double *s0 = S0 + (size_t)bh * D, *s1 = S1 + (size_t)bh * D * D;
+        double *s2 = S2 + (size_t)bh * D * D, *k1 = K1 + (size_t)bh * D, *k2 = K2 + (size_t)bh * D;
+        memset(s0, 0, sizeof(double) * D); memset(s1, 0, sizeof(double) * D * D);
+        memset(s2, 0, sizeof(double) * D * D); memset(k1, 0, sizeof(double) * D);
+        memset(k2, 0, sizeof(double) * D);
+        K0[bh] = 0.0;
+        for (int j = 0; j < L; ++j) {
+            const double dd = C[L - 1] - C[j] > 0.0 ? C[L - 1] - C[j] : 0.0;
+            const double e = exp(-dd / ta);
+            const double *kj = k + ((size_t)bh * L + j) * D, *vj = v + ((size_t)bh * L + j) * D;
+            K0[bh] += e;
+            for (int a = 0; a < D; ++a) {
+                s0[a] += e * vj[a];
+                k1[a] += b1 * e * kj[a];
+                k2[a] += b2 * e * kj[a] * kj[a];
+                for (int c = 0; c < D; ++c) {
+                    s1[IDX2(a, c, D)] += b1 * e * kj[a] * vj[c];
+                    s2[IDX2(a, c, D)] += b2 * e * kj[a] * kj[a] * vj[c];
+                }
+            }
+        }
+    }
+    free(C);
+    free(w);
+}

@@ -93,9 +93,12 @@ namespace {
 
 int decode_impl(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv,
                 int D, const float *decay, float eps, const prime_qk_norm_t *norm, const prime_state_t *state_in,
-                const prime_state_t *state_out, const prime_tensor_t *y, void *stream) {
+                const prime_state_t *state_out, const prime_tensor_t *y, void *stream,
+                const float *decay_bh = nullptr, const float *k_scale = nullptr) {
     g_err[0] = 0;
-    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !decay || !state_out)
+    const bool selective = decay_bh != nullptr;
+    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !(decay || decay_bh) || !state_out ||
+        (selective && !k_scale))
         return fail(PRIME_ERR_INVALID_ARG, "prime_decode_step: null argument");
     if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv)
@@ -127,6 +130,7 @@ int decode_impl(const prime_tensor_t *q, const prime_tensor_t *k, const prime_te
     a.k0o = state_out->k0; a.k1o = state_out->k1; a.k2o = state_out->k2;
     a.y = y->data; a.dt_y = y->dtype; a.y_sb = y->stride_b; a.y_sh = y->stride_h;
     a.q_scale = norm ? norm->q_scale : 1.0f;
+    a.decay_bh = decay_bh; a.k_scale = k_scale; a.selective = selective ? 1 : 0;
     return check_hip(prime::launch_decode_step(a, static_cast<hipStream_t>(stream)), "decode launch");
 }
 
@@ -250,14 +254,18 @@ int prime_argmax(const void *logits, int dtype, int n, int vocab, int64_t stride
     return check_hip(prime::launch_argmax_rows(a, static_cast<hipStream_t>(stream)), "argmax launch");
 }
 
-int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
-                          int B, int H, int H_kv, int L, int D, int chunk, const float *decay,
-                          float eps, unsigned flags, const prime_state_t *state_in,
-                          const prime_tensor_t *y, const prime_state_t *state_out, void *workspace,
-                          size_t workspace_bytes, void *stream) {
+static int prefill_impl(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B, int H,
+                        int H_kv, int L, int D, int chunk, const float *decay, float eps, unsigned flags,
+                        const prime_state_t *state_in, const prime_tensor_t *y, const prime_state_t *state_out,
+                        void *workspace, size_t workspace_bytes, void *stream, const float *log_decay,
+                        const float *k_scale) {
     g_err[0] = 0;
-    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !decay)
-        return fail(PRIME_ERR_INVALID_ARG, "prime_chunked_prefill: null argument");
+    const bool selective = log_decay != nullptr;
+    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !(decay || selective) ||
+        (selective && !k_scale))
+        return fail(PRIME_ERR_INVALID_ARG, "prefill: null argument");
+    if (selective && q->dtype != PRIME_BF16)
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "the selective prefill takes BF16 q/k/v");
     if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0 || chunk <= 0)
         return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d chunk=%d", B, H, H_kv, L, chunk);
@@ -281,6 +289,8 @@ int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, cons
     a.B = B; a.H = H; a.group = H / H_kv; a.L = L;
     a.decay = decay; a.eps = eps;
     a.dense_clamp = (flags & PRIME_FLAG_DENSE_CLAMP) ? 1 : 0;
+    if (selective && a.dense_clamp) return fail(PRIME_ERR_INVALID_ARG, "the selective form has no dense clamp");
+    a.log_decay = log_decay; a.k_scale = k_scale;
     if (state_in) {
         a.s0i = state_in->s0; a.s1i = state_in->s1; a.s2i = state_in->s2;
         a.k0i = state_in->k0; a.k1i = state_in->k1; a.k2i = state_in->k2;
@@ -298,6 +308,50 @@ int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, cons
     a.ws = a.G > 1 ? static_cast<float *>(workspace) : nullptr;
     (void)inplace;  // in place is safe: each workgroup reads its own state before writing it
     return check_hip(prime::launch_prefill(a, static_cast<hipStream_t>(stream)), "prefill launch");
+}
+
+int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                          int B, int H, int H_kv, int L, int D, int chunk, const float *decay,
+                          float eps, unsigned flags, const prime_state_t *state_in,
+                          const prime_tensor_t *y, const prime_state_t *state_out, void *workspace,
+                          size_t workspace_bytes, void *stream) {
+    if (!decay) {
+        g_err[0] = 0;
+        return fail(PRIME_ERR_INVALID_ARG, "prime_chunked_prefill: null decay");
+    }
+    return prefill_impl(q, k, v, B, H, H_kv, L, D, chunk, decay, eps, flags, state_in, y, state_out, workspace,
+                        workspace_bytes, stream, nullptr, nullptr);
+}
+
+int prime_selective_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
+                            int H, int H_kv, int L, int D, const float *log_decay, const float *k_scale, float eps,
+                            const prime_state_t *state_in, const prime_tensor_t *y, const prime_state_t *state_out,
+                            void *workspace, size_t workspace_bytes, void *stream) {
+    if (!log_decay || !k_scale) {
+        g_err[0] = 0;
+        return fail(PRIME_ERR_INVALID_ARG, "prime_selective_prefill: null log_decay or k_scale");
+    }
+    return prefill_impl(q, k, v, B, H, H_kv, L, D, 64, nullptr, eps, 0, state_in, y, state_out, workspace,
+                        workspace_bytes, stream, log_decay, k_scale);
+}
+
+int prime_selective_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
+                                int H, int H_kv, int D, const float *decay_bh, const float *k_scale, float eps,
+                                const prime_qk_norm_t *norm, const prime_state_t *state_in,
+                                const prime_state_t *state_out, const prime_tensor_t *y, void *stream) {
+    if (!decay_bh || !k_scale) {
+        g_err[0] = 0;
+        return fail(PRIME_ERR_INVALID_ARG, "prime_selective_decode_step: null decay or k_scale");
+    }
+    if (norm && norm->q_weight && (!norm->q_bias || !norm->k_weight || !norm->k_bias)) {
+        g_err[0] = 0;
+        return fail(PRIME_ERR_INVALID_ARG, "prime_selective_decode_step: LayerNorm weight without bias");
+    }
+    if (norm && !valid_dtype(norm->dtype)) {
+        g_err[0] = 0;
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported norm dtype");
+    }
+    return decode_impl(q, k, v, B, H, H_kv, D, nullptr, eps, norm, state_in, state_out, y, stream, decay_bh, k_scale);
 }
 
 size_t prime_delta_prefill_workspace_size(int B, int H, int L, unsigned flags) {

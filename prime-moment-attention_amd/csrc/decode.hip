@@ -39,7 +39,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
         qv = load_elem(a.q, b * a.q_sb + h * a.q_sh + lane, a.dt_q);
         kv = load_elem(a.k, b * a.k_sb + hk * a.k_sh + lane, a.dt_k);
         vv = load_elem(a.v, b * a.v_sb + hk * a.v_sh + lane, a.dt_v);
-        lam = a.decay[h];
+        lam = a.decay_bh ? a.decay_bh[b * a.H + h] : a.decay[h];
     }
     if (a.qn_w) {
         // the module's QK LayerNorm (attention.py:96-98, biased variance),
@@ -54,6 +54,10 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
         if (a.dt_k == PRIME_BF16) kv = bf16_bits_to_f32(f32_to_bf16_bits(kv));
     }
     qv *= a.q_scale;  // 1/sqrt(D) (attention.py:101); exact for powers of two
+    if (a.k_scale) kv *= a.k_scale[h];  // selective: beta k (selective.py:394-400)
+    // the 1/2 of the second-order term sits on the k side in the selective
+    // state convention (S2 = 1/2 beta^2 sum k^2 v), on the q side otherwise
+    const float h2k = a.selective ? 0.5f : 1.0f, h2q = a.selective ? 1.0f : 0.5f;
 
     const int rg = lane >> 4;  // row group: rows 4r + rg
     const int cg = lane & 15;  // column group: columns 4cg..4cg+3
@@ -84,7 +88,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
     // small moments (lane l owns element l)
     const float s0n = lam * s0v + vv;
     const float k1n = lam * k1v + kv;
-    const float k2n = lam * k2v + kv * kv;
+    const float k2n = lam * k2v + h2k * kv * kv;
     const float k0n = lam * k0v + 1.0f;
     sh[wave][0][lane] = qv;
     sh[wave][1][lane] = kv;
@@ -99,8 +103,8 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
         const int row = 4 * r + rg;
         const float kr = sh[wave][1][row];
         const float qr = sh[wave][0][row];
-        const float kr2 = kr * kr;
-        const float qh = 0.5f * qr * qr;
+        const float kr2 = h2k * kr * kr;
+        const float qh = h2q * qr * qr;
         f32x4 n1, n2;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -120,7 +124,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
         acc[c] += __shfl_xor(acc[c], 16, kWave);
         acc[c] += __shfl_xor(acc[c], 32, kWave);
     }
-    const float den = k0n + wave_sum(qv * k1n + 0.5f * qv * qv * k2n);
+    const float den = k0n + wave_sum(qv * k1n + h2q * qv * qv * k2n);
     const float inv = 1.0f / fmaxf(den, a.eps);
 
     if (active) {

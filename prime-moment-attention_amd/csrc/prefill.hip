@@ -650,7 +650,8 @@ __global__ __launch_bounds__(256) void segment_scan_kernel(const PrefillArgs a) 
     if (gid >= static_cast<int64_t>(Sq) * kWsElems) return;
     const int seq = static_cast<int>(gid / kWsElems), e = static_cast<int>(gid % kWsElems);
     const int h = seq % a.H;
-    const float lT = static_cast<float>(pow(static_cast<double>(a.decay[h]), static_cast<double>(a.cps) * kC));
+    const bool sel = a.log_decay != nullptr;
+    const float lT = sel ? 0.f : static_cast<float>(pow(static_cast<double>(a.decay[h]), static_cast<double>(a.cps) * kC));
     float carry = 0.f;
     if (a.s1i != nullptr) {
         const size_t so1 = static_cast<size_t>(seq) * kD * kD, so0 = static_cast<size_t>(seq) * kD;
@@ -665,7 +666,9 @@ __global__ __launch_bounds__(256) void segment_scan_kernel(const PrefillArgs a) 
     for (int s = 0; s + 1 < a.G; ++s) {
         const float d = slot[static_cast<size_t>(s) * kWsStride];
         slot[static_cast<size_t>(s) * kWsStride] = carry;
-        carry = lT * carry + d;
+        // selective: segment s's own decay, stored beside its slot's state
+        const float f = sel ? exp2f(slot[static_cast<size_t>(s) * kWsStride + kWsDecay - e]) : lT;
+        carry = f * carry + d;
     }
     slot[static_cast<size_t>(a.G - 1) * kWsStride] = carry;
 }

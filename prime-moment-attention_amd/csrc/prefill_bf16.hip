@@ -56,13 +56,15 @@ __device__ __forceinline__ u32x4 scale8(u32x4 x, float w) {
 // The next chunk's rows ra and ra + 32, one 16-byte segment each, per update thread.
 struct Tiles {
     u32x4 q0, q1, k0, k1, v0, v1;
+    float ld;  // selective: log2 decay of token `lane` of the chunk (0 past L)
 };
 
 // Unconditional loads; rows past L clamp to row L-1 (zeroed when stored).
-template <bool STATE_ONLY>
+template <bool STATE_ONLY, bool SEL>
 __device__ __forceinline__ void load_tiles(Tiles &T, const PrefillArgs &a, const uint16_t *qp, const uint16_t *kp,
-                                           const uint16_t *vp, int c, int ra) {
+                                           const uint16_t *vp, const float *ldp, int c, int ra, int lane) {
     const int64_t ta = min(c * kC + ra, a.L - 1), tb = min(c * kC + ra + 32, a.L - 1);
+    if constexpr (SEL) T.ld = ldp[min(c * kC + lane, a.L - 1)];  // scaled and masked when used
     if constexpr (!STATE_ONLY) {
         T.q0 = ld16(qp + ta * a.q_sl);
         T.q1 = ld16(qp + tb * a.q_sl);
@@ -75,8 +77,8 @@ __device__ __forceinline__ void load_tiles(Tiles &T, const PrefillArgs &a, const
 
 // One row segment into the tile buffers: [q | q*q], [k | k*k/2], [v], [w v | w].
 // Invalid rows (past the chunk's tokens) are stored as zeros.
-template <bool STATE_ONLY>
-__device__ __forceinline__ void store_row(u32x4 q, u32x4 k, u32x4 v, int row, int col, bool valid, float w,
+template <bool STATE_ONLY, bool SEL>
+__device__ __forceinline__ void store_row(u32x4 q, u32x4 k, u32x4 v, int row, int col, bool valid, float w, float ks,
                                           uint16_t *sQf, uint16_t *sKf, uint16_t *sV, uint16_t *sVw) {
     const uint32_t m = valid ? 0xFFFFFFFFu : 0u;
     k = and4(k, m);
@@ -87,15 +89,17 @@ __device__ __forceinline__ void store_row(u32x4 q, u32x4 k, u32x4 v, int row, in
         st16(sQf + row * kPW + kD + col, sq8(q, 1.0f));
         st16(sV + row * kPV8 + col, v);
     }
-    st16(sKf + row * kPW + col, k);
-    st16(sKf + row * kPW + kD + col, sq8(k, 0.5f));
+    // selective: k enters as beta k, its square feature as beta^2 k^2 / 2 (from the
+    // unrounded product), i.e. the module's beta and beta^2 / 2 weights
+    st16(sKf + row * kPW + col, SEL ? scale8(k, ks) : k);
+    st16(sKf + row * kPW + kD + col, sq8(k, SEL ? 0.5f * ks * ks : 0.5f));
     st16(sVw + row * kPV8 + col, scale8(v, w));
     if (col == 0) sVw[row * kPV8 + kD] = f32_to_bf16_bits(w);
 }
 
 }  // namespace
 
-template <bool STATE_ONLY>
+template <bool STATE_ONLY, bool SEL>
 __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel(const PrefillArgs a) {
     constexpr int NB = kD / 16;    // value blocks
     constexpr int NBX = NB + 1;    // + the ones / K block
@@ -116,6 +120,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
     __shared__ float sPs[kC + 2];                                         // sum_{m<n} l^m
     __shared__ float sKi[KI];                                             // incoming [K1; K2/2] (dense)
     __shared__ float sKi0;                                                // incoming K0 (dense)
+    __shared__ float sCum[SEL && !STATE_ONLY ? 2 : 1][kC];                // selective: log2 decay to token i
 
     const int tid = threadIdx.x;
     // wave index in a scalar register: every role / wave test below is then a
@@ -133,7 +138,10 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
     if (unit >= Sq * a.nseg_launch) return;  // whole workgroup leaves before any barrier
     const int seq = unit / a.nseg_launch, seg = unit - seq * a.nseg_launch;
     const int b = seq / a.H, h = seq - b * a.H, hk = h / a.group;
-    const float lam = a.decay[h];
+    const float lam = SEL ? 1.0f : a.decay[h];
+    const float kscale = SEL ? a.k_scale[h] : 1.0f;
+    // selective: per-token natural-log decays, read as log2 (exp2 on the VALU)
+    const float *ldp = SEL ? a.log_decay + static_cast<size_t>(b * a.H + h) * a.L : nullptr;
     const int NC = (a.L + kC - 1) / kC;
     const int c_begin = seg * a.cps;
     const int c_end = min(c_begin + a.cps, NC);
@@ -163,13 +171,43 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
     const uint16_t *qp = static_cast<const uint16_t *>(a.q) + (b * a.q_sb + h * a.q_sh + col);
     const uint16_t *kp = static_cast<const uint16_t *>(a.k) + (b * a.k_sb + hk * a.k_sh + col);
     const uint16_t *vp = static_cast<const uint16_t *>(a.v) + (b * a.v_sb + hk * a.v_sh + col);
+    // selective: log2 decay of the stored chunk (l^n) and its weight sum
+    // sum_j w_j (the K0 increment), for the update of that chunk; and the
+    // segment's total log2 decay (state-only pass)
+    float sel_ln = 1.f, sel_sw = 0.f, seg_ld = 0.f;
     auto store_tiles = [&](int c, int xb) {
         const int nv = min(kC, a.L - c * kC);
         const bool va = ra < nv, vb = ra + 32 < nv;
-        const float wa = va ? sPw[nv - 1 - ra] : 0.f, wb = vb ? sPw[nv - 1 - (ra + 32)] : 0.f;
+        float wa, wb;
+        if constexpr (SEL) {
+            // inclusive scan of the chunk's log2 decays over the lanes (lane = token)
+            float x = lane < nv ? T.ld * 1.4426950408889634f : 0.f;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const float y = __shfl_up(x, o, kWave);
+                if (lane >= o) x += y;
+            }
+            // every lane takes part in the shuffles (a lane outside a branch
+            // would not supply its value to the lanes reading it)
+            const float tot = __shfl(x, nv - 1, kWave);
+            const float xra = __shfl(x, ra, kWave), xrb = __shfl(x, ra + 32, kWave);
+            wa = va ? exp2f(tot - xra) : 0.f;
+            wb = vb ? exp2f(tot - xrb) : 0.f;
+            sel_ln = exp2f(tot);
+            sel_sw = wave_sum(lane < nv ? exp2f(tot - x) : 0.f);
+            seg_ld += tot;
+            if constexpr (!STATE_ONLY) {
+                if (u == 0) sCum[xb][lane] = x;
+            }
+        } else {
+            wa = va ? sPw[nv - 1 - ra] : 0.f;
+            wb = vb ? sPw[nv - 1 - (ra + 32)] : 0.f;
+        }
         uint16_t *pq = &sQf[STATE_ONLY ? 0 : xb][0][0], *pv = &sV[STATE_ONLY ? 0 : xb][0][0];
-        store_row<STATE_ONLY>(T.q0, T.k0, T.v0, ra, col, va, wa, pq, &sKf[xb][0][0], pv, &sVw[xb][0][0]);
-        store_row<STATE_ONLY>(T.q1, T.k1, T.v1, ra + 32, col, vb, wb, pq, &sKf[xb][0][0], pv, &sVw[xb][0][0]);
+        store_row<STATE_ONLY, SEL>(T.q0, T.k0, T.v0, ra, col, va, wa, kscale, pq, &sKf[xb][0][0], pv,
+                                   &sVw[xb][0][0]);
+        store_row<STATE_ONLY, SEL>(T.q1, T.k1, T.v1, ra + 32, col, vb, wb, kscale, pq, &sKf[xb][0][0], pv,
+                                   &sVw[xb][0][0]);
     };
     // bf16 copy of the state entering the next chunk, into state buffer xb
     auto publish_state = [&](int xb) {
@@ -190,7 +228,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
         }
     };
     if (is_u) {
-        load_tiles<STATE_ONLY>(T, a, qp, kp, vp, c_begin, ra);
+        load_tiles<STATE_ONLY, SEL>(T, a, qp, kp, vp, ldp, c_begin, ra, lane);
 #pragma unroll
         for (int fi = 0; fi < 2; ++fi)
 #pragma unroll
@@ -207,7 +245,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
                         if (from_ws) x = wslot[(f < kD ? kWsK1 : kWsK2) + fr];
                         else if (has_in) x = (f < kD ? a.k1i : a.k2i)[so0 + fr];
                     }
-                    st[fi][nb][r] = f < kD ? x : 0.5f * x;
+                    st[fi][nb][r] = (f < kD || SEL) ? x : 0.5f * x;  // selective states carry the 1/2
                 }
         {
             float x = 0.f;
@@ -236,14 +274,14 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
         }
         publish_state(c_begin & 1);
         store_tiles(c_begin, STATE_ONLY ? 0 : c_begin & 1);
-        load_tiles<STATE_ONLY>(T, a, qp, kp, vp, c_begin + 1, ra);
+        load_tiles<STATE_ONLY, SEL>(T, a, qp, kp, vp, ldp, c_begin + 1, ra, lane);
     }
 
     // ---- readout-role constants (query row of the lane: iw)
     const int iw = 16 * wave + c16;
     float mask[4][4];  // l^(i-j) [i >= j] for S^T[j = 16jb + 4g + r][i = iw]
     float pin = 0.f;   // l^(iw+1)
-    if (!is_u) {
+    if (!is_u && !SEL) {
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
@@ -263,6 +301,19 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
         const int nvalid = min(kC, a.L - c * kC);
         if (!is_u) {
             if constexpr (!STATE_ONLY) {
+                if constexpr (SEL) {
+                    // decays within the chunk: l(i <- j) = 2^(cum_i - cum_j), and from
+                    // the chunk start to row iw: 2^cum_iw
+                    const float ci = sCum[p][iw];
+                    pin = exp2f(ci);
+#pragma unroll
+                    for (int jb = 0; jb < 4; ++jb) {
+                        const f32x4 cj = *reinterpret_cast<const f32x4 *>(&sCum[p][16 * jb + 4 * g]);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            mask[jb][r] = (jb <= wave && 16 * jb + 4 * g + r <= iw) ? exp2f(ci - cj[r]) : 0.f;
+                    }
+                }
                 // ---- query features of row iw (B operand of S^T and of the readout)
                 Opnd<false> fq[4];
 #pragma unroll
@@ -373,7 +424,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
             }
         } else {
             // ---- state update: st = l^n st + [k; k*k/2]^T [w v | w];  S0 on the ones row
-            const float ln = sPw[nvalid];
+            const float ln = SEL ? sel_ln : sPw[nvalid];  // selective: set when chunk c was stored
 #pragma unroll
             for (int fi = 0; fi < 2; ++fi)
 #pragma unroll
@@ -381,7 +432,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
 #pragma unroll
                     for (int r = 0; r < 4; ++r) st[fi][nb][r] *= ln;
             s0t[0] *= ln;
-            k0 = ln * k0 + sPs[nvalid];
+            k0 = ln * k0 + (SEL ? sel_sw : sPs[nvalid]);
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 // register t of both operands <-> token 32ks + 16(t/4) + 4g + t%4
@@ -413,7 +464,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
             const bool more = c + 1 < c_end;
             if constexpr (STATE_ONLY) __syncthreads();  // every wave has read the single tile buffer
             if (more) store_tiles(c + 1, xq);
-            load_tiles<STATE_ONLY>(T, a, qp, kp, vp, c + 2, ra);
+            load_tiles<STATE_ONLY, SEL>(T, a, qp, kp, vp, ldp, c + 2, ra, lane);
             if (more) publish_state(xq);
         }
         __syncthreads();
@@ -440,7 +491,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
         for (int r = 0; r < 4; ++r) {
             const int f = 16 * (2 * u + fi) + 4 * g + r;
             const int fr = f & (kD - 1);
-            const float sc = f < kD ? 1.0f : 2.0f;  // rows 64.. hold S2/2 and K2/2
+            const float sc = (f < kD || SEL) ? 1.0f : 2.0f;  // rows 64.. hold S2/2 and K2/2
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
                 (f < kD ? o_s1 : o_s2)[off1 + fr * kD + 16 * nb + c16] = sc * st[fi][nb][r];
@@ -454,13 +505,21 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
         }
     if (g == 0) o_s0[off0 + 16 * u + c16] = s0t[0];
     if (u == 0 && lane == 0) o_k0[offk0] = k0 + (STATE_ONLY ? 0.f : linit * sKi0);
+    // selective: the segment's own log2 decay, for the scan over segments
+    if (SEL && STATE_ONLY && u == 0 && lane == 0) wslot[kWsDecay] = seg_ld;
 }
 
 void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream, TimerEvents t) {
-    if (state_only)
-        hipExtLaunchKernelGGL(prefill_bf16_kernel<true>, dim3(grid), dim3(256), 0, stream, t.start, t.stop, 0, a);
+    const bool sel = a.log_decay != nullptr;
+    const dim3 g(grid), blk(state_only ? 256 : 512);
+    if (state_only && sel)
+        hipExtLaunchKernelGGL(prefill_bf16_kernel<true, true>, g, blk, 0, stream, t.start, t.stop, 0, a);
+    else if (state_only)
+        hipExtLaunchKernelGGL(prefill_bf16_kernel<true, false>, g, blk, 0, stream, t.start, t.stop, 0, a);
+    else if (sel)
+        hipExtLaunchKernelGGL(prefill_bf16_kernel<false, true>, g, blk, 0, stream, t.start, t.stop, 0, a);
     else
-        hipExtLaunchKernelGGL(prefill_bf16_kernel<false>, dim3(grid), dim3(512), 0, stream, t.start, t.stop, 0, a);
+        hipExtLaunchKernelGGL(prefill_bf16_kernel<false, false>, g, blk, 0, stream, t.start, t.stop, 0, a);
 }
 
 }  // namespace prime

@@ -24,6 +24,11 @@ struct DecodeArgs {
     const void *qn_w, *qn_b, *kn_w, *kn_b;
     int dt_norm;
     float ln_eps, q_scale;
+    // selective form: decay per (sequence, head) [B, H] instead of per head,
+    // k scaled by k_scale[h] (beta), S2 / K2 carrying the 1/2 (selective != 0)
+    const float *decay_bh;
+    const float *k_scale;
+    int selective;
 };
 
 // Residual add + RMSNorm rows (norm.hip).
@@ -85,12 +90,18 @@ struct PrefillArgs {
     int G, cps;
     int nseg_launch;  // segments covered by the current launch (G or G - 1)
     float *ws;
+    // selective form (null for the base form): per-token natural-log decays
+    // [B, H, L] replace `decay`; k is scaled by k_scale[h] (beta) and the
+    // S2 / K2 state components carry the 1/2 of the module's convention
+    const float *log_decay;
+    const float *k_scale;
 };
 
 // packed fp32 state slot in the workspace: S1 | S2 | S0 | K1 | K2 | K0
 constexpr int kWsS1 = 0, kWsS2 = 4096, kWsS0 = 8192, kWsK1 = 8256, kWsK2 = 8320, kWsK0 = 8384;
 constexpr int kWsStride = 8448;  // floats per slot (33,792 bytes)
-constexpr int kWsElems = 8385;   // used floats per slot
+constexpr int kWsElems = 8385;   // state floats per slot
+constexpr int kWsDecay = 8385;   // selective: the segment's log2 decay (not part of the scanned state)
 
 hipError_t launch_decode_step(const DecodeArgs &a, hipStream_t stream);
 hipError_t launch_prefill(PrefillArgs a, hipStream_t stream);

@@ -26,7 +26,8 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
            "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
            "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_argmax",
-           "prime_head_layernorm", "prime_linear")
+           "prime_head_layernorm", "prime_linear", "prime_selective_prefill",
+           "prime_selective_decode_step")
 
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
@@ -98,6 +99,14 @@ def load() -> ctypes.CDLL:
     L.prime_head_layernorm.restype = ctypes.c_int
     L.prime_linear.argtypes = [fp, fp, fp] + [ctypes.c_int] * 3 + [ctypes.c_int64] * 3 + [ctypes.c_int] * 2 + [fp]
     L.prime_linear.restype = ctypes.c_int
+    L.prime_selective_prefill.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 5 + [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, P(PrimeState), P(PrimeTensor), P(PrimeState),
+        ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    L.prime_selective_prefill.restype = ctypes.c_int
+    L.prime_selective_decode_step.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 4 + [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, P(PrimeQkNorm), P(PrimeState), P(PrimeState),
+        P(PrimeTensor), ctypes.c_void_p]
+    L.prime_selective_decode_step.restype = ctypes.c_int
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     v = L.prime_abi_version()
     if v != ABI_VERSION:
@@ -371,6 +380,46 @@ def chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, state_
     args, keep = _prefill_args(q, k, v, decay, eps, chunk, state_in, y, state_out, flags, workspace)
     _check(load().prime_chunked_prefill(*args, _stream(q.device)), "prime_chunked_prefill")
     del keep
+
+
+def _sel_vec(t: torch.Tensor, n: int, name: str) -> None:
+    _dev_check(t)
+    if t.dtype != torch.float32 or t.numel() != n or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous fp32 tensor of {n} elements")
+
+
+def selective_prefill(q, k, v, log_decay: torch.Tensor, k_scale: torch.Tensor, eps: float, state_in, y,
+                      state_out, workspace: Optional[torch.Tensor] = None) -> None:
+    """Selective PRIME prefill (prime_selective_prefill): bf16 q [B,H,L,D],
+    k/v [B,Hkv,L,D]; log_decay fp32 [B,H,L] (log lambda_t, contiguous);
+    k_scale fp32 [H] (beta); states in the selective convention."""
+    B, H, Lq, D = q.shape
+    _sel_vec(log_decay, B * H * Lq, "log_decay")
+    _sel_vec(k_scale, H, "k_scale")
+    # the decay argument of the base form is not used: pass the k scale for the checks
+    args, keep = _prefill_args(q, k, v, k_scale, eps, 64, state_in, y, state_out, 0, workspace)
+    args = args[:8] + (ctypes.c_void_p(log_decay.data_ptr()), ctypes.c_void_p(k_scale.data_ptr()), args[10]) + args[12:]
+    _check(load().prime_selective_prefill(*args, _stream(q.device)), "prime_selective_prefill")
+    del keep
+
+
+def selective_decode_step(q, k, v, decay_bh: torch.Tensor, k_scale: torch.Tensor, eps: float,
+                          norm: Optional[PrimeQkNorm], state_in, state_out, y) -> None:
+    """Selective PRIME decode step (prime_selective_decode_step): decay_bh fp32
+    [B,H] (lambda_t per sequence and head), k_scale fp32 [H]; norm: the QK
+    LayerNorm and q scale for raw projections (``qk_norm(...)``) or None."""
+    B, H, D = q.shape
+    _sel_vec(decay_bh, B * H, "decay_bh")
+    _decode_checks(q, k, v, k_scale, state_in, state_out, y)
+    L = load()
+    qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), tensor_desc(y, False)
+    si, so = state_desc(state_in), state_desc(state_out)
+    rc = L.prime_selective_decode_step(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), B, H, k.shape[1], D,
+                                       decay_bh.data_ptr(), k_scale.data_ptr(), float(eps),
+                                       ctypes.byref(norm) if norm is not None else None,
+                                       ctypes.byref(si) if si else None, ctypes.byref(so), ctypes.byref(yd),
+                                       _stream(q.device))
+    _check(rc, "prime_selective_decode_step")
 
 
 def bind_chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, state_in, y,

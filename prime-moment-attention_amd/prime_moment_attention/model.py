@@ -31,6 +31,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .attention import PrimeMomentAttention
+from .selective import PrimeSelectiveMomentAttention
 
 
 @dataclass
@@ -117,13 +118,17 @@ class PrimeBlock(nn.Module):
 
     def __init__(self, config: PrimeConfig):
         super().__init__()
-        if config.use_selective:
-            raise NotImplementedError("selective PRIME attention (selective.py) is not built in this library")
         self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
-        self.self_attn = PrimeMomentAttention(
-            hidden_size=config.hidden_size, num_heads=config.num_heads, head_dim=config.head_dim,
-            num_kv_heads=config.num_kv_heads, decay=config.decay, use_qk_norm=config.use_qk_norm,
-            eps=config.eps)
+        if config.use_selective:
+            self.self_attn = PrimeSelectiveMomentAttention(
+                hidden_size=config.hidden_size, num_heads=config.num_heads, head_dim=config.head_dim,
+                num_kv_heads=config.num_kv_heads, decay=config.decay, use_qk_norm=config.use_qk_norm,
+                eps=config.eps, min_tau=config.min_tau, max_tau=config.max_tau)
+        else:
+            self.self_attn = PrimeMomentAttention(
+                hidden_size=config.hidden_size, num_heads=config.num_heads, head_dim=config.head_dim,
+                num_kv_heads=config.num_kv_heads, decay=config.decay, use_qk_norm=config.use_qk_norm,
+                eps=config.eps)
         self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
         mlp = PrimeGeluMLP if config.mlp_type == "gelu" else PrimeMLP
         self.mlp = mlp(config.hidden_size, config.intermediate_size)
@@ -155,6 +160,8 @@ class PrimeForCausalLM(nn.Module):
         for layer in self.layers:
             layer.self_attn.o_proj.weight.data.normal_(mean=0.0, std=scale)
             layer.mlp.down_proj.weight.data.normal_(mean=0.0, std=scale)
+            if hasattr(layer.self_attn, "init_selective_weights"):  # model.py:148-149
+                layer.self_attn.init_selective_weights()
 
     def _init_weights(self, module: nn.Module):
         if isinstance(module, (nn.Linear, nn.Embedding)):
@@ -263,12 +270,13 @@ class GreedyDecoder:
         self.use_graph = use_graph
         self.graph = None
         self.states = None
-        self._decay, self._norm, self._qkv = {}, {}, {}
+        self._decay, self._norm, self._qkv, self._sel = {}, {}, {}, {}
         dev = model.embed_tokens.weight.device
         for layer in model.layers:
             at = layer.self_attn
             at.inplace_state = True
-            self._decay[id(at)] = _lib.decay_tensor(at.decay, at.num_heads, dev)
+            if not isinstance(at, PrimeSelectiveMomentAttention):
+                self._decay[id(at)] = _lib.decay_tensor(at.decay, at.num_heads, dev)
             self._norm[id(at)] = _lib.qk_norm(at.q_norm if at.use_qk_norm else None,
                                               at.k_norm if at.use_qk_norm else None, at.scaling,
                                               model.embed_tokens.weight.dtype)
@@ -286,6 +294,9 @@ class GreedyDecoder:
         for layer in m.layers:
             at = layer.self_attn
             self._qkv[id(at)] = torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight], dim=0)
+            if isinstance(at, PrimeSelectiveMomentAttention):  # tau_h and beta_h as the module has them now
+                dev = at.log_tau.device
+                self._sel[id(at)] = (at.get_tau(dev).float().contiguous(), at.get_beta(dev).float().contiguous())
         self.graph = None
         return self.token
 
@@ -310,7 +321,13 @@ class GreedyDecoder:
             k = qkv[:, nq:nq + nk].view(B, at.num_kv_heads, at.head_dim)
             v = qkv[:, nq + nk:].view(B, at.num_kv_heads, at.head_dim)
             y = torch.empty(B, at.num_heads, at.head_dim, device=x.device, dtype=x.dtype)
-            _lib.decode_step_qknorm(q, k, v, self._decay[id(at)], at.eps, self._norm[id(at)], st, st, y)
+            if id(at) in self._sel:
+                # lambda_t = exp(-Delta_t / tau_h) as the module's step (selective.py:368, 385-386)
+                tau, beta = self._sel[id(at)]
+                lam = torch.exp(-at.step_size(n1).float() / tau.view(1, -1))
+                _lib.selective_decode_step(q, k, v, lam, beta, at.eps, self._norm[id(at)], st, st, y)
+            else:
+                _lib.decode_step_qknorm(q, k, v, self._decay[id(at)], at.eps, self._norm[id(at)], st, st, y)
             a = _decode_linear(y.view(B, -1), at.o_proj.weight)
             n2 = torch.empty_like(x)
             _lib.add_rmsnorm(x, a, layer.post_attention_layernorm.weight, n2, layer.post_attention_layernorm.eps)

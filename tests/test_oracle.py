@@ -14,6 +14,10 @@ Each oracle routine is checked against something it was not written from:
   delta_chunked  <- per-token delta rule and an unrolled transition-matrix
                     product (bound = 0, several C); golden fixtures from the
                     reference for the active Lyapunov clamp.
+  selective      <- the parallel branch (selective.py:414-440, a separate
+                    O(L^2) routine) against the step branch applied token by
+                    token; beta = 1 with a constant step reduces to the base
+                    recurrence with S2, K2 halved; one token gives y = v.
 A planted-mistake check (oracle_plant_check) shows the pins detect a wrong
 index/sign in a modified copy of the formula.
 """
@@ -353,3 +357,48 @@ def test_delta_step_known_answers():
     nrm = np.sqrt((Sb ** 2).sum(axis=(1, 2)))
     assert np.all(np.abs(nrm - 2.0) < 1e-5), nrm
     _close(yb, np.einsum("bde,be->bd", Sb, psi))
+
+
+def _sel_inputs(BH, L, D, seed):
+    q, k, v = _rand(BH, L, D, seed)
+    rng = np.random.default_rng(seed + 1)
+    delta = np.log1p(np.exp(rng.standard_normal((BH, L))))  # softplus
+    tau = rng.uniform(4.0, 300.0, BH)
+    beta = rng.uniform(0.5, 3.0, BH)
+    return q, k, v, delta, tau, beta
+
+
+@pytest.mark.parametrize("L", [1, 9, 70])
+def test_selective_parallel_equals_token_steps(L):
+    """The reference's two selective branches agree: the O(L^2) parallel form
+    with C = cumsum(Delta) and the per-token step with lam_t = exp(-Delta_t / tau)."""
+    BH, D = 3, 8
+    q, k, v, delta, tau, beta = _sel_inputs(BH, L, D, 90 + L)
+    yp, sp = O.selective_parallel(q, k, v, delta, tau, beta, eps=1e-5)
+    lam = np.exp(-delta / tau[:, None])
+    yr, sr = O.selective_recurrent(q, k, v, lam, beta, eps=1e-5)
+    np.testing.assert_allclose(yp, yr, rtol=1e-10, atol=1e-12)
+    for a, b in zip(sp, sr):
+        np.testing.assert_allclose(a, b, rtol=1e-10, atol=1e-12)
+
+
+def test_selective_reduces_to_base_recurrence():
+    """beta = 1 and one decay per head: the base recurrence, with the selective
+    state's S2 and K2 being half the base ones (the 1/2 moves into the state)."""
+    BH, L, D = 2, 40, 8
+    q, k, v = _rand(BH, L, D, 95)
+    lam = np.array([0.97, 0.999])
+    yb, sb = O.recurrent(q, k, v, lam, eps=0.5)
+    ys, ss = O.selective_recurrent(q, k, v, np.repeat(lam[:, None], L, 1), np.ones(BH), eps=0.5)
+    np.testing.assert_allclose(ys, yb, rtol=1e-12, atol=1e-13)
+    for i, (a, b) in enumerate(zip(ss, sb)):
+        np.testing.assert_allclose(a, b * (0.5 if i in (2, 5) else 1.0), rtol=1e-12, atol=1e-13)
+
+
+def test_selective_single_token_is_v():
+    BH, D = 4, 8
+    q, k, v, delta, tau, beta = _sel_inputs(BH, 1, D, 97)
+    y, s = O.selective_parallel(q, k, v, delta, tau, beta, eps=1e-5)
+    np.testing.assert_allclose(y, v, rtol=1e-12)
+    np.testing.assert_allclose(s[4], beta[:, None] * k[:, 0], rtol=1e-12)
+    np.testing.assert_allclose(s[5], 0.5 * beta[:, None] ** 2 * k[:, 0] ** 2, rtol=1e-12)
