@@ -19,6 +19,8 @@ The same JSON line carries
   decode        the fused decode step at B=512 sequences x 12 layers x 12 heads
                 (one launch per layer, states pre-filled by 1024 tokens) and at
                 B=256, tok/s and its own roofline;
+  selective     selective PRIME (per-token decays, beta-weighted keys): the
+                prefill at the config-2 shape and the decode step at B=256;
   delta         the chunked delta-rule prefill at config 5 (B=1, H=12,
                 L=131072): tok/s, per-kernel time, sustained tok/s per 16384
                 tokens and the memory in use (flat state);
@@ -61,6 +63,7 @@ def parse_args():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode legs")
     ap.add_argument("--no-model", action="store_true", help="skip the PRIME-125M model leg")
     ap.add_argument("--no-delta", action="store_true", help="skip the delta-rule (config 5) leg")
+    ap.add_argument("--no-selective", action="store_true", help="skip the selective PRIME leg")
     ap.add_argument("--cpu-budget", type=float, default=8.0, help="seconds per CPU leg (approximate)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device copy 3 times (the reference kernel for "
@@ -235,7 +238,7 @@ def bench_decode(args, lib, torch, dev, B, layers=12, H=12, pool=16, prefill_tok
 
 
 # ----------------------------------------------------------------- model
-def bench_model(args, torch, dev):
+def bench_model(args, torch, dev, selective=False):
     """PRIME-125M-shaped causal LM (12 layers, d_model 768, 12 x 64 heads,
     GELU MLP 3072, tied 50304 vocab, bf16 weights, fp32 states, LayerNorm
     QK-norm), random init.  Prefill B=32 x 2048 random ids (states + last-token
@@ -243,12 +246,19 @@ def bench_model(args, torch, dev):
     B=256 (prompt of 128 tokens: decode cost does not depend on position)."""
     from prime_moment_attention import GreedyDecoder, PrimeForCausalLM, prime_125m_config
     torch.manual_seed(args.seed)
-    model = PrimeForCausalLM(prime_125m_config("gelu")).to(device=dev, dtype=torch.bfloat16).eval()
+    model = PrimeForCausalLM(prime_125m_config("gelu", use_selective=selective)).to(device=dev,
+                                                                                  dtype=torch.bfloat16).eval()
     gen = torch.Generator(device=dev).manual_seed(args.seed + 7)
     V = model.config.vocab_size
+    if selective:  # off the identity initialisation: data-dependent step sizes, per-head beta
+        with torch.no_grad():
+            for layer in model.layers:
+                layer.self_attn.delta_proj.weight.normal_(0.0, 0.01, generator=gen)
+                layer.self_attn.log_beta.uniform_(-0.5, 0.5, generator=gen)
     out = {"workload": "PRIME-125M-shaped LM: 12 layers, d_model 768, 12 heads x 64, GELU MLP 3072, "
                        "vocab 50304 tied, bf16 weights, fp32 states, LayerNorm QK-norm, random init; "
-                       "prefill B=32 x 2048 random ids, greedy decode 256 steps (HIP graph step)",
+                       + ("selective attention (per-token decays, beta-weighted keys); " if selective else "")
+                       + "prefill B=32 x 2048 random ids, greedy decode 256 steps (HIP graph step)",
            "params": sum(p.numel() for p in model.parameters())}
 
     def timed_once(fn):
@@ -280,6 +290,89 @@ def bench_model(args, torch, dev):
                                 "ms_per_step": ms / steps,
                                 "state_bytes": 12 * Bd * 12 * STATE_BYTES}
     del model, dec
+    torch.cuda.empty_cache()
+    return out
+
+
+# ----------------------------------------------------------------- selective
+def bench_selective(args, lib, torch, dev):
+    """Selective PRIME (selective.py:264-444) at the chunked-prefill shape
+    (B=8, H=12, L=8192, bf16 q/k/v as config 2) with per-token decays
+    lambda_t = exp(-softplus(N(0,1)) / tau_h), tau_h ~ U[8, 2000], beta_h ~
+    U[0.5, 2]; then the decode step at B=256 x 12 layers (one launch per layer,
+    replayed from a HIP graph)."""
+    B, H, L = 8, 12, 8192
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 11)
+    q, k, v = qkv((B, H, L, D), gen, dev, torch.bfloat16)
+    tau = torch.empty(H, device=dev).uniform_(8.0, 2000.0, generator=gen)
+    beta = torch.empty(H, device=dev).uniform_(0.5, 2.0, generator=gen)
+    delta = torch.nn.functional.softplus(torch.randn(B, H, L, device=dev, generator=gen))
+    log_decay = (-delta / tau.view(1, H, 1)).contiguous()
+    y = torch.empty(B, H, L, D, device=dev, dtype=torch.bfloat16)
+    st = lib.new_state(B, H, D, dev)
+    ws = torch.empty(lib.workspace_size(B, H, L), dtype=torch.uint8, device=dev)
+    run = lambda: lib.selective_prefill(q, k, v, log_decay, beta, 1.0, None, y, st, workspace=ws)
+    ids = (lib.KERNEL_PREFILL_CHUNKS, lib.KERNEL_PREFILL_SEGMENTS, lib.KERNEL_SEGMENT_SCAN)
+    for _ in range(20):
+        run()
+    torch.cuda.synchronize()
+    lib.timer_reset()
+    lib.timer_enable(*ids)
+    steps = max(50, args.steps // 10)
+    ms = timed(run, steps, 0)
+    lib.timer_enable()
+    kern = {lib.KERNEL_NAMES[kid]: kernel_ms(lib, kid) for kid in ids}
+    lib.timer_reset()
+    main_ms = kern[lib.KERNEL_NAMES[lib.KERNEL_PREFILL_CHUNKS]][0]
+    # q, k, v, y bf16 and the fp32 log decay per token-head, plus the final state
+    algo = B * H * L * (PREFILL_BYTES_PER_TOKEN_HEAD + 4) + B * H * STATE_BYTES
+    out = {"workload": "selective PRIME prefill, B=8 x H=12 x L=8192, D=64, bf16 q/k/v, per-token decays, "
+                       "beta-weighted keys, zero initial state, bf16 y, fp32 final state",
+           "prefill": {"tok_s": B * L / (ms * 1e-3), "ms": ms, "finite": bool(torch.isfinite(y).all().item()),
+                       "kernels": {n: {"avg_us": None if t is None else t * 1e3, "launches": c}
+                                   for n, (t, c) in kern.items()},
+                       "roofline": {"kernel": "prefill_bf16_kernel<false, true>", "bound": "hbm",
+                                    "bytes_per_launch": algo, "avg_launch_us": main_ms * 1e3,
+                                    "achieved": algo / (main_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
+                                    "unit": "GB/s", "frac": algo / (main_ms * 1e-3) / PEAK_HBM}}}
+    del q, k, v, y, delta, log_decay, ws
+    # decode B=256 x 12 layers
+    Bd, layers = 256, 12
+    states = []
+    for _ in range(layers):
+        s_ = lib.new_state(Bd, H, D, dev, zero=True)
+        for t in s_:
+            t.normal_(generator=gen).mul_(0.1)
+        s_[3].abs_().add_(1.0)
+        states.append(s_)
+    toks = [qkv((Bd, H, D), gen, dev, torch.bfloat16) for _ in range(layers)]
+    lams = [torch.exp(-torch.nn.functional.softplus(torch.randn(Bd, H, device=dev, generator=gen)) / tau.view(1, H))
+            .contiguous() for _ in range(layers)]
+    ys = [torch.empty(Bd, H, D, device=dev, dtype=torch.bfloat16) for _ in range(layers)]
+    gates = [lib.selective_gate(Bd, H, decay_bh=lam) for lam in lams]
+
+    def step():
+        for l in range(layers):
+            lib.selective_decode_step(*toks[l], gates[l], beta, 1.0, None, states[l], states[l], ys[l])
+    s0 = torch.cuda.Stream()
+    s0.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s0):
+        step()
+    torch.cuda.current_stream().wait_stream(s0)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    dsteps = max(100, args.decode_steps // 4)
+    dms = timed(g.replay, dsteps, 10)
+    per_launch = Bd * H * (DECODE_BYTES_PER_TILE + 4)
+    out["decode_B256"] = {"tok_s": Bd / (dms * 1e-3), "ms_per_step": dms, "steps": dsteps,
+                          "finite": all(bool(torch.isfinite(t).all().item()) for t in ys),
+                          "roofline": {"kernel": "decode_step_kernel (selective)", "bound": "hbm",
+                                       "bytes_per_launch": per_launch, "avg_launch_us": dms / layers * 1e3,
+                                       "achieved": per_launch / (dms / layers * 1e-3) / 1e9,
+                                       "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                                       "frac": per_launch / (dms / layers * 1e-3) / PEAK_HBM}}
+    del g, states
     torch.cuda.empty_cache()
     return out
 
@@ -521,8 +614,12 @@ def main():
         rec["decode"] = {"B=256": d256, "B=512": d512}
     if not args.no_delta:
         rec["delta"] = bench_delta(args, lib, torch, dev)
+    if not args.no_selective:
+        rec["selective"] = bench_selective(args, lib, torch, dev)
     if not args.no_model:
         rec["model"] = bench_model(args, torch, dev)
+        if not args.no_selective:
+            rec["model_selective"] = bench_model(args, torch, dev, selective=True)
     if not args.no_cpu:
         try:
             legs = cpu_prefill_legs(args)

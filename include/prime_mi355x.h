@@ -248,18 +248,33 @@ int prime_linear(const void *x, const void *w, void *y, int M, int N, int K, int
  * 414-440), which builds the full [L, L] decay matrix; the reference branch
  * ignores an incoming state, a caller reproducing it passes NULL.
  *
- * prime_selective_decode_step: one token; decay_bh fp32 [B, H] = l_t per
- * (sequence, head) (selective.py:386), k_scale [H]; norm (may be NULL) as for
- * prime_decode_step_qknorm (the module's QK LayerNorm and q scale applied to
- * raw projections).  Replaces selective.py:384-409.
+ * prime_selective_decode_step: one token; the decays come from `gate`
+ * (below), k_scale [H]; norm (may be NULL) as for prime_decode_step_qknorm
+ * (the module's QK LayerNorm and q scale applied to raw projections).
+ * Replaces selective.py:384-409.
  */
+typedef struct prime_selective_gate {
+    /* either l_t per (sequence, head), fp32 [B, H] contiguous ... */
+    const float *decay;
+    /* ... or (decay == NULL) the step-size pre-activations delta_proj(x):
+       element (b, h) at step + b * step_sb + h, of step_dtype; the kernel
+       forms Delta = clamp(softplus(.), step_min, step_max) rounded to
+       step_dtype as the module's tensors are (selective.py:368), and
+       l = exp(-Delta / tau[h]) (selective.py:386) */
+    const void *step;
+    int32_t step_dtype;
+    int32_t reserved;
+    int64_t step_sb;
+    const float *tau;  /* [H] */
+    float step_min, step_max;
+} prime_selective_gate_t;
 int prime_selective_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
                             int H, int H_kv, int L, int D, const float *log_decay, const float *k_scale, float eps,
                             const prime_state_t *state_in, const prime_tensor_t *y, const prime_state_t *state_out,
                             void *workspace, size_t workspace_bytes, void *stream);
 int prime_selective_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
-                                int H, int H_kv, int D, const float *decay_bh, const float *k_scale, float eps,
-                                const prime_qk_norm_t *norm, const prime_state_t *state_in,
+                                int H, int H_kv, int D, const prime_selective_gate_t *gate, const float *k_scale,
+                                float eps, const prime_qk_norm_t *norm, const prime_state_t *state_in,
                                 const prime_state_t *state_out, const prime_tensor_t *y, void *stream);
 
 /*

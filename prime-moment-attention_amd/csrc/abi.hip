@@ -94,10 +94,10 @@ namespace {
 int decode_impl(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv,
                 int D, const float *decay, float eps, const prime_qk_norm_t *norm, const prime_state_t *state_in,
                 const prime_state_t *state_out, const prime_tensor_t *y, void *stream,
-                const float *decay_bh = nullptr, const float *k_scale = nullptr) {
+                const prime_selective_gate_t *gate = nullptr, const float *k_scale = nullptr) {
     g_err[0] = 0;
-    const bool selective = decay_bh != nullptr;
-    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !(decay || decay_bh) || !state_out ||
+    const bool selective = gate != nullptr;
+    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !(decay || selective) || !state_out ||
         (selective && !k_scale))
         return fail(PRIME_ERR_INVALID_ARG, "prime_decode_step: null argument");
     if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
@@ -130,7 +130,18 @@ int decode_impl(const prime_tensor_t *q, const prime_tensor_t *k, const prime_te
     a.k0o = state_out->k0; a.k1o = state_out->k1; a.k2o = state_out->k2;
     a.y = y->data; a.dt_y = y->dtype; a.y_sb = y->stride_b; a.y_sh = y->stride_h;
     a.q_scale = norm ? norm->q_scale : 1.0f;
-    a.decay_bh = decay_bh; a.k_scale = k_scale; a.selective = selective ? 1 : 0;
+    a.k_scale = k_scale; a.selective = selective ? 1 : 0;
+    if (gate) {
+        a.decay_bh = gate->decay;
+        if (!gate->decay) {
+            if (!gate->step || !gate->tau) return fail(PRIME_ERR_INVALID_ARG, "selective gate: null step or tau");
+            if (!valid_dtype(gate->step_dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported step dtype");
+            if (!(gate->step_min > 0.f) || !(gate->step_max >= gate->step_min))
+                return fail(PRIME_ERR_INVALID_ARG, "selective gate: bad step bounds");
+            a.step = gate->step; a.step_sb = gate->step_sb; a.dt_step = gate->step_dtype; a.tau = gate->tau;
+            a.step_min = gate->step_min; a.step_max = gate->step_max;
+        }
+    }
     return check_hip(prime::launch_decode_step(a, static_cast<hipStream_t>(stream)), "decode launch");
 }
 
@@ -336,12 +347,12 @@ int prime_selective_prefill(const prime_tensor_t *q, const prime_tensor_t *k, co
 }
 
 int prime_selective_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
-                                int H, int H_kv, int D, const float *decay_bh, const float *k_scale, float eps,
-                                const prime_qk_norm_t *norm, const prime_state_t *state_in,
+                                int H, int H_kv, int D, const prime_selective_gate_t *gate, const float *k_scale,
+                                float eps, const prime_qk_norm_t *norm, const prime_state_t *state_in,
                                 const prime_state_t *state_out, const prime_tensor_t *y, void *stream) {
-    if (!decay_bh || !k_scale) {
+    if (!gate || !k_scale) {
         g_err[0] = 0;
-        return fail(PRIME_ERR_INVALID_ARG, "prime_selective_decode_step: null decay or k_scale");
+        return fail(PRIME_ERR_INVALID_ARG, "prime_selective_decode_step: null gate or k_scale");
     }
     if (norm && norm->q_weight && (!norm->q_bias || !norm->k_weight || !norm->k_bias)) {
         g_err[0] = 0;
@@ -351,7 +362,7 @@ int prime_selective_decode_step(const prime_tensor_t *q, const prime_tensor_t *k
         g_err[0] = 0;
         return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported norm dtype");
     }
-    return decode_impl(q, k, v, B, H, H_kv, D, nullptr, eps, norm, state_in, state_out, y, stream, decay_bh, k_scale);
+    return decode_impl(q, k, v, B, H, H_kv, D, nullptr, eps, norm, state_in, state_out, y, stream, gate, k_scale);
 }
 
 size_t prime_delta_prefill_workspace_size(int B, int H, int L, unsigned flags) {

@@ -23,6 +23,13 @@ namespace prime {
 
 constexpr int kDecodeWaves = 4;
 
+// x rounded to dtype dt (to nearest even), returned as fp32
+__device__ __forceinline__ float round_to(float x, int dt) {
+    if (dt == PRIME_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
+    if (dt == PRIME_F16) return h16_bits_to_f32(f32_to_h16_bits(x));
+    return x;
+}
+
 __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const DecodeArgs a) {
     __shared__ float sh[kDecodeWaves][4][kD];  // per wave: q, k, v, updated S0
     const int wave = threadIdx.x >> 6;
@@ -39,7 +46,19 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
         qv = load_elem(a.q, b * a.q_sb + h * a.q_sh + lane, a.dt_q);
         kv = load_elem(a.k, b * a.k_sb + hk * a.k_sh + lane, a.dt_k);
         vv = load_elem(a.v, b * a.v_sb + hk * a.v_sh + lane, a.dt_v);
-        lam = a.decay_bh ? a.decay_bh[b * a.H + h] : a.decay[h];
+        if (a.decay_bh) {
+            lam = a.decay_bh[b * a.H + h];
+        } else if (a.step) {
+            // selective gate (selective.py:368, 386): Delta = clamp(softplus(s)),
+            // each stage rounded to the step dtype as the module's tensors are
+            const float s = load_elem(a.step, b * a.step_sb + h, a.dt_step);
+            float d = s > 20.f ? s : log1pf(expf(s));
+            d = round_to(d, a.dt_step);
+            d = round_to(fminf(fmaxf(d, a.step_min), a.step_max), a.dt_step);
+            lam = expf(-d / a.tau[h]);
+        } else {
+            lam = a.decay[h];
+        }
     }
     if (a.qn_w) {
         // the module's QK LayerNorm (attention.py:96-98, biased variance),

@@ -29,6 +29,12 @@ struct DecodeArgs {
     const float *decay_bh;
     const float *k_scale;
     int selective;
+    // selective, decay_bh == null: l = exp(-clamp(softplus(step)) / tau)
+    const void *step;
+    int64_t step_sb;
+    int dt_step;
+    const float *tau;
+    float step_min, step_max;
 };
 
 // Residual add + RMSNorm rows (norm.hip).

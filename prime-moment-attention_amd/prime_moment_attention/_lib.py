@@ -53,6 +53,12 @@ class PrimeQkNorm(ctypes.Structure):
                 ("q_scale", ctypes.c_float)]
 
 
+class PrimeSelectiveGate(ctypes.Structure):
+    _fields_ = [("decay", ctypes.c_void_p), ("step", ctypes.c_void_p), ("step_dtype", ctypes.c_int32),
+                ("reserved", ctypes.c_int32), ("step_sb", ctypes.c_int64), ("tau", ctypes.c_void_p),
+                ("step_min", ctypes.c_float), ("step_max", ctypes.c_float)]
+
+
 _lib = None
 
 
@@ -104,7 +110,7 @@ def load() -> ctypes.CDLL:
         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     L.prime_selective_prefill.restype = ctypes.c_int
     L.prime_selective_decode_step.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 4 + [
-        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, P(PrimeQkNorm), P(PrimeState), P(PrimeState),
+        P(PrimeSelectiveGate), ctypes.c_void_p, ctypes.c_float, P(PrimeQkNorm), P(PrimeState), P(PrimeState),
         P(PrimeTensor), ctypes.c_void_p]
     L.prime_selective_decode_step.restype = ctypes.c_int
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
@@ -403,19 +409,38 @@ def selective_prefill(q, k, v, log_decay: torch.Tensor, k_scale: torch.Tensor, e
     del keep
 
 
-def selective_decode_step(q, k, v, decay_bh: torch.Tensor, k_scale: torch.Tensor, eps: float,
+def selective_gate(B: int, H: int, decay_bh: Optional[torch.Tensor] = None, step: Optional[torch.Tensor] = None,
+                   tau: Optional[torch.Tensor] = None, step_min: float = 1e-4,
+                   step_max: float = 50.0) -> PrimeSelectiveGate:
+    """prime_selective_gate_t: lambda_t per (sequence, head) as decay_bh fp32
+    [B,H], or the step pre-activations `step` [B,H] (delta_proj(x), any row
+    stride, contiguous heads) with tau fp32 [H] (the kernel forms the decays)."""
+    if decay_bh is not None:
+        _sel_vec(decay_bh, B * H, "decay_bh")
+        return PrimeSelectiveGate(decay_bh.data_ptr(), None, 0, 0, 0, None, 0.0, 0.0)
+    if step is None or tau is None:
+        raise ValueError("give decay_bh, or step and tau")
+    _dev_check(step)
+    _sel_vec(tau, H, "tau")
+    if step.dim() != 2 or step.shape != (B, H) or step.stride(1) != 1 or step.dtype not in _DTYPES:
+        raise ValueError("step must be [B, H] with contiguous heads")
+    return PrimeSelectiveGate(None, step.data_ptr(), _DTYPES[step.dtype], 0, step.stride(0), tau.data_ptr(),
+                              float(step_min), float(step_max))
+
+
+def selective_decode_step(q, k, v, gate: PrimeSelectiveGate, k_scale: torch.Tensor, eps: float,
                           norm: Optional[PrimeQkNorm], state_in, state_out, y) -> None:
-    """Selective PRIME decode step (prime_selective_decode_step): decay_bh fp32
-    [B,H] (lambda_t per sequence and head), k_scale fp32 [H]; norm: the QK
-    LayerNorm and q scale for raw projections (``qk_norm(...)``) or None."""
+    """Selective PRIME decode step (prime_selective_decode_step): the decays
+    from ``selective_gate(...)``, k_scale fp32 [H]; norm: the QK LayerNorm
+    and q scale for raw projections (``qk_norm(...)``) or None.  The tensors
+    the gate points to must stay alive until the call returns."""
     B, H, D = q.shape
-    _sel_vec(decay_bh, B * H, "decay_bh")
     _decode_checks(q, k, v, k_scale, state_in, state_out, y)
     L = load()
     qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), tensor_desc(y, False)
     si, so = state_desc(state_in), state_desc(state_out)
     rc = L.prime_selective_decode_step(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), B, H, k.shape[1], D,
-                                       decay_bh.data_ptr(), k_scale.data_ptr(), float(eps),
+                                       ctypes.byref(gate), k_scale.data_ptr(), float(eps),
                                        ctypes.byref(norm) if norm is not None else None,
                                        ctypes.byref(si) if si else None, ctypes.byref(so), ctypes.byref(yd),
                                        _stream(q.device))

@@ -64,11 +64,13 @@ class PrimeConfig:
             raise ValueError(f"mlp_type must be 'swiglu' or 'gelu', not {self.mlp_type!r}")
 
 
-def prime_125m_config(mlp_type: str = "gelu", vocab_size: int = 50304) -> PrimeConfig:
+def prime_125m_config(mlp_type: str = "gelu", vocab_size: int = 50304, use_selective: bool = False) -> PrimeConfig:
     """The PRIME-125M benchmark shape: 12 layers, d_model 768, 12 x 64 heads,
-    MLP 3072 (GELU) or the reference's SwiGLU width, tied 50304-token vocab."""
+    MLP 3072 (GELU) or the reference's SwiGLU width, tied 50304-token vocab;
+    use_selective for the selective attention of the shipped PRIME-125M."""
     return PrimeConfig(vocab_size=vocab_size, hidden_size=768, num_layers=12, num_heads=12, head_dim=64,
-                       intermediate_size=3072 if mlp_type == "gelu" else None, mlp_type=mlp_type)
+                       intermediate_size=3072 if mlp_type == "gelu" else None, mlp_type=mlp_type,
+                       use_selective=use_selective)
 
 
 class RMSNorm(nn.Module):
@@ -322,10 +324,10 @@ class GreedyDecoder:
             v = qkv[:, nq + nk:].view(B, at.num_kv_heads, at.head_dim)
             y = torch.empty(B, at.num_heads, at.head_dim, device=x.device, dtype=x.dtype)
             if id(at) in self._sel:
-                # lambda_t = exp(-Delta_t / tau_h) as the module's step (selective.py:368, 385-386)
+                # lambda_t = exp(-Delta_t / tau_h) formed in the kernel (selective.py:368, 385-386)
                 tau, beta = self._sel[id(at)]
-                lam = torch.exp(-at.step_size(n1).float() / tau.view(1, -1))
-                _lib.selective_decode_step(q, k, v, lam, beta, at.eps, self._norm[id(at)], st, st, y)
+                gate = _lib.selective_gate(B, at.num_heads, step=at.delta_proj(n1), tau=tau)
+                _lib.selective_decode_step(q, k, v, gate, beta, at.eps, self._norm[id(at)], st, st, y)
             else:
                 _lib.decode_step_qknorm(q, k, v, self._decay[id(at)], at.eps, self._norm[id(at)], st, st, y)
             a = _decode_linear(y.view(B, -1), at.o_proj.weight)

@@ -92,11 +92,12 @@ class PrimeSelectiveMomentAttention(nn.Module):
         v = self.v_proj(hidden_states).view(B, L, self.num_kv_heads, D).transpose(1, 2)
         tau = self.get_tau(dev).float().contiguous()
         beta = self.get_beta(dev).float().contiguous()
-        delta = self.step_size(hidden_states)  # [B, L, H]
         if L == 1:
             norm = _lib.qk_norm(self.q_norm if self.use_qk_norm else None,
                                 self.k_norm if self.use_qk_norm else None, self.scaling, q.dtype)
-            lam = torch.exp(-delta[:, 0, :].float() / tau.view(1, H)).contiguous()  # selective.py:386
+            # the kernel forms Delta and lambda from the pre-activations (selective.py:368, 386)
+            pre = self.delta_proj(hidden_states)[:, 0, :]
+            gate = _lib.selective_gate(B, H, step=pre, tau=tau)
             st_in = _lib.as_state(state, B, H, D, dev) if state is not None else None
             if self.inplace_state and st_in is not None and all(
                     a.data_ptr() == b.data_ptr() for a, b in zip(st_in, state)):
@@ -104,7 +105,7 @@ class PrimeSelectiveMomentAttention(nn.Module):
             else:
                 st_out = _lib.new_state(B, H, D, dev)
             y = torch.empty(B, H, D, device=dev, dtype=y_dtype)
-            _lib.selective_decode_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], lam, beta, self.eps, norm, st_in,
+            _lib.selective_decode_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], gate, beta, self.eps, norm, st_in,
                                        st_out, y)
             y = y.unsqueeze(2)
             next_state = st_out
@@ -115,6 +116,7 @@ class PrimeSelectiveMomentAttention(nn.Module):
             if self.use_qk_norm:
                 _lib.head_layernorm(k, k, self.k_norm, 1.0)
             # per-token log decays -(Delta / tau), [B, H, L]
+            delta = self.step_size(hidden_states)  # [B, L, H]
             log_decay = (-delta.float() / tau.view(1, 1, H)).transpose(1, 2).contiguous()
             y_bl = torch.empty(B, L, H, D, device=dev, dtype=y_dtype)
             next_state = _lib.new_state(B, H, D, dev) if return_state else None

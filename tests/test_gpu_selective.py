@@ -131,7 +131,8 @@ def test_selective_decode_step_matches_oracle(qk_norm):
                      ld[:, :, None], beta, 1.0, st)
     s = state_to_dev(st, B, H, D)
     y = torch.empty(B, H, D, device=dev())
-    _lib.selective_decode_step(q_in, k_in, to_dev(v, torch.bfloat16), to_dev(np.exp(ld).astype(np.float32)),
+    lam = to_dev(np.exp(ld).astype(np.float32))
+    _lib.selective_decode_step(q_in, k_in, to_dev(v, torch.bfloat16), _lib.selective_gate(B, H, decay_bh=lam),
                                to_dev(beta), 1.0, norm, s, s, y)
     torch.cuda.synchronize()
     # fp32 arithmetic; with the LayerNorm prologue the normed rows may differ
@@ -228,3 +229,28 @@ def test_selective_model_steps_continue_prefill_and_greedy_decoder():
     graph = GreedyDecoder(model, use_graph=True).generate(ids[:, :30], n)
     assert torch.equal(eager, ref), (eager, ref)
     assert torch.equal(graph, ref), (graph, ref)
+
+
+def test_selective_gate_from_step_preactivations():
+    """The in-kernel gate (softplus, clamp and rounding in bf16, then
+    exp(-Delta / tau)) gives the decays the module's torch ops give
+    (selective.py:368, 386): the steps agree with the explicit-decay call."""
+    B, H = 5, 4
+    q, k, v, _, beta = _inputs(B, H, 1, seed=60)
+    q, k, v = (to_dev(x[:, :, 0], torch.bfloat16) for x in (q, k, v))
+    g = torch.Generator(device=dev()).manual_seed(61)
+    pre = (torch.randn(B, H + 3, device=dev(), generator=g) * 4).bfloat16()[:, :H]  # row stride H + 3
+    pre[0, 0], pre[0, 1], pre[1, 0] = -30.0, 60.0, 25.0  # clamp low, clamp high, softplus identity branch
+    tau = torch.tensor([3.0, 50.0, 700.0, 1999.0], device=dev())
+    lam = torch.exp(-torch.nn.functional.softplus(pre).clamp(min=1e-4, max=50.0).float() / tau.view(1, H))
+    st = state_to_dev(_rand_state(B * H, 62), B, H, D)
+    outs = []
+    for gate in (_lib.selective_gate(B, H, decay_bh=lam.contiguous()), _lib.selective_gate(B, H, step=pre, tau=tau)):
+        s_out = _lib.new_state(B, H, D, dev())
+        y = torch.empty(B, H, D, device=dev())
+        _lib.selective_decode_step(q, k, v, gate, to_dev(beta), 1.0, None, st, s_out, y)
+        outs.append((y, s_out))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0])
+    for a, b in zip(outs[0][1], outs[1][1]):
+        assert torch.equal(a, b)
