@@ -21,6 +21,9 @@ The same JSON line carries
                 B=256, tok/s and its own roofline;
   selective     selective PRIME (per-token decays, beta-weighted keys): the
                 prefill at the config-2 shape and the decode step at B=256;
+  hybrid        the hybrid window-PRIME pieces: eviction accumulator and
+                fp32-input prefill at the config-2 shape, per-token update and
+                readout at B=256;
   delta         the chunked delta-rule prefill at config 5 (B=1, H=12,
                 L=131072): tok/s, per-kernel time, sustained tok/s per 16384
                 tokens and the memory in use (flat state);
@@ -64,6 +67,7 @@ def parse_args():
     ap.add_argument("--no-model", action="store_true", help="skip the PRIME-125M model leg")
     ap.add_argument("--no-delta", action="store_true", help="skip the delta-rule (config 5) leg")
     ap.add_argument("--no-selective", action="store_true", help="skip the selective PRIME leg")
+    ap.add_argument("--no-hybrid", action="store_true", help="skip the hybrid window-PRIME leg")
     ap.add_argument("--cpu-budget", type=float, default=8.0, help="seconds per CPU leg (approximate)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device copy 3 times (the reference kernel for "
@@ -378,6 +382,101 @@ def bench_selective(args, lib, torch, dev):
 
 
 # ----------------------------------------------------------------- delta rule
+def bench_hybrid(args, lib, torch, dev):
+    """The hybrid window-PRIME pieces (prime_cpp_kernel.cpp:6-117 replaced by
+    prime_chunked_prefill at eps 1e-3, prime_accumulate, prime_decode_update,
+    prime_decode_readout): the eviction accumulator over B=8 x H=12 x L=8192
+    bf16 k/v, the fp32-input prefill (the reference's hybrid casts q/k/v to
+    fp32, hybrid.py:109-114) at the same shape, and the per-token update and
+    readout at B=256 x 12 layers (HIP-graph replays)."""
+    B, H, L = 8, 12, 8192
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 13)
+    q, k, v = qkv((B, H, L, D), gen, dev, torch.bfloat16)
+    lam = torch.empty(H, device=dev).uniform_(0.99, 0.9999, generator=gen)
+    st = lib.new_state(B, H, D, dev)
+    ws = torch.empty(lib.accumulate_workspace_size(B, H, L), dtype=torch.uint8, device=dev)
+    out = {}
+
+    def leg(run, ids, main_id, algo, steps, tokens, workload, kernel, names=None):
+        names = names or lib.KERNEL_NAMES
+        for _ in range(10):
+            run()
+        torch.cuda.synchronize()
+        lib.timer_reset()
+        lib.timer_enable(*ids)
+        ms = timed(run, steps, 0)
+        lib.timer_enable()
+        kern = {names[kid]: kernel_ms(lib, kid) for kid in ids}
+        lib.timer_reset()
+        main_ms = kern[names[main_id]][0]
+        return {"workload": workload, "tok_s": tokens / (ms * 1e-3), "ms": ms,
+                "kernels": {n: {"avg_us": None if t is None else t * 1e3, "launches": c} for n, (t, c) in kern.items()},
+                "roofline": {"kernel": kernel, "bound": "hbm", "bytes_per_launch": algo,
+                             "avg_launch_us": main_ms * 1e3, "achieved": algo / (main_ms * 1e-3) / 1e9,
+                             "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": algo / (main_ms * 1e-3) / PEAK_HBM}}
+
+    steps = max(50, args.steps // 10)
+    # bf16 k, v in; fp32 final state out
+    out["accumulate"] = leg(lambda: lib.accumulate(k, v, lam, None, st, workspace=ws),
+                            (lib.KERNEL_PREFILL_SEGMENTS, lib.KERNEL_SEGMENT_SCAN), lib.KERNEL_PREFILL_SEGMENTS,
+                            B * H * L * 4 * D + B * H * STATE_BYTES, steps, B * L,
+                            "prime_accumulate, B=8 x H=12 x L=8192 bf16 k/v, zero initial state",
+                            "prefill_bf16_kernel<true> (state-only)")
+    del q, k, v
+    q32, k32, v32 = qkv((B, H, L, D), gen, dev, torch.float32)
+    y32 = torch.empty(B, H, L, D, device=dev)
+    ws2 = torch.empty(lib.workspace_size(B, H, L), dtype=torch.uint8, device=dev)
+    ids = (lib.KERNEL_PREFILL_CHUNKS, lib.KERNEL_PREFILL_SEGMENTS, lib.KERNEL_SEGMENT_SCAN)
+    out["prefill_f32"] = leg(lambda: lib.chunked_prefill(q32, k32, v32, lam, 1e-3, 64, None, y32, st, workspace=ws2),
+                             ids, lib.KERNEL_PREFILL_CHUNKS, B * H * L * 16 * D + B * H * STATE_BYTES,
+                             max(20, steps // 2), B * L,
+                             "prime_chunked_prefill with fp32 q/k/v/y and eps 1e-3 (prime_prefill_cpp), "
+                             "B=8 x H=12 x L=8192", "prefill_kernel<true, false> (fp32 inputs)",
+                             {lib.KERNEL_PREFILL_CHUNKS: "prefill_kernel<true, false>",
+                              lib.KERNEL_PREFILL_SEGMENTS: "prefill_kernel<true, true>",
+                              lib.KERNEL_SEGMENT_SCAN: "segment_scan_kernel"})
+    del q32, k32, v32, y32, ws, ws2
+    # per-token update and readout, B=256 x 12 layers
+    Bd, layers = 256, 12
+    states = []
+    for _ in range(layers):
+        s_ = lib.new_state(Bd, H, D, dev, zero=True)
+        for t in s_:
+            t.normal_(generator=gen).mul_(0.1)
+        s_[3].abs_().add_(1.0)
+        states.append(s_)
+    toks = [qkv((Bd, H, D), gen, dev, torch.float32) for _ in range(layers)]
+    ys = [torch.empty(Bd, H, D, device=dev) for _ in range(layers)]
+    for name, fn, per_tile in (
+            ("update_B256", lambda l: lib.decode_update(toks[l][1], toks[l][2], lam, states[l], states[l]),
+             2 * STATE_BYTES + 2 * 4 * D),
+            ("readout_B256", lambda l: lib.decode_readout(toks[l][0], 1e-3, states[l], ys[l]),
+             STATE_BYTES + 2 * 4 * D)):
+        def step():
+            for l in range(layers):
+                fn(l)
+        s0 = torch.cuda.Stream()
+        s0.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s0):
+            step()
+        torch.cuda.current_stream().wait_stream(s0)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        dsteps = max(100, args.decode_steps // 4)
+        dms = timed(g.replay, dsteps, 10)
+        per_launch = Bd * H * per_tile
+        out[name] = {"tok_s": Bd / (dms * 1e-3), "ms_per_step": dms, "steps": dsteps, "layers": layers,
+                     "roofline": {"kernel": "decode_step_kernel (" + name.split("_")[0] + " only)", "bound": "hbm",
+                                  "bytes_per_launch": per_launch, "avg_launch_us": dms / layers * 1e3,
+                                  "achieved": per_launch / (dms / layers * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
+                                  "unit": "GB/s", "frac": per_launch / (dms / layers * 1e-3) / PEAK_HBM}}
+        del g
+    del states
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_delta(args, lib, torch, dev):
     """Chunked gated delta-rule prefill: B=1, H=12, D=64,
     L=131072, chunk 64, bf16 q/k/v (N(0,1), QK-normed, q / 8), beta ~
@@ -616,6 +715,8 @@ def main():
         rec["delta"] = bench_delta(args, lib, torch, dev)
     if not args.no_selective:
         rec["selective"] = bench_selective(args, lib, torch, dev)
+    if not args.no_hybrid:
+        rec["hybrid"] = bench_hybrid(args, lib, torch, dev)
     if not args.no_model:
         rec["model"] = bench_model(args, torch, dev)
         if not args.no_selective:

@@ -288,6 +288,45 @@ int prime_argmax(const void *logits, int dtype, int n, int vocab, int64_t stride
                  void *stream);
 
 /*
+ * Hybrid window-PRIME pieces (hybrid.py:98-170 calls them through the JIT
+ * extension of prime_cpp_kernel.cpp).  The reference's prime_prefill_cpp
+ * (prime_cpp_kernel.cpp:6-46) is prime_chunked_prefill with eps = 1e-3 and a
+ * zero initial state.
+ *
+ * prime_accumulate replaces prime_accumulate_evicted_cpp
+ * (prime_cpp_kernel.cpp:48-83): the moment state of L tokens of k/v
+ * ([B, H_kv, L, D], BF16 or F32, 16-byte rows), no queries and no readout.
+ * state_in = NULL starts from zeros (the reference always does); otherwise
+ * the tokens are appended to state_in, and state_out may equal state_in.
+ * workspace (16-byte aligned) must hold at least B*H*kSlot bytes with
+ * kSlot = 33,792 (one per sequence); prime_accumulate_workspace_size() bytes
+ * let the sequences split into segments that run in parallel.
+ */
+int prime_accumulate(const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv, int L, int D,
+                     const float *decay, const prime_state_t *state_in, const prime_state_t *state_out,
+                     void *workspace, size_t workspace_bytes, void *stream);
+size_t prime_accumulate_workspace_size(int B, int H, int L);
+
+/*
+ * prime_decode_readout replaces prime_query_step_cpp (prime_cpp_kernel.cpp:85-100):
+ * y = (S0 + S1^T q + 1/2 S2^T q^2) / max(K0 + q.K1 + 1/2 q^2.K2, eps) against
+ * `state` as it is (the reference's eps is 1e-3); the state is not written.
+ * q, y: [B, H, D] views (stride_l unused).
+ */
+int prime_decode_readout(const prime_tensor_t *q, int B, int H, int D, float eps, const prime_state_t *state,
+                         const prime_tensor_t *y, void *stream);
+
+/*
+ * prime_decode_update replaces prime_step_evict_update_cpp
+ * (prime_cpp_kernel.cpp:102-117): one token of k/v ([B, H_kv, D]) appended
+ * to the state, no readout.  The reference updates in place: pass
+ * state_out == state_in.  state_in = NULL starts from zeros.
+ */
+int prime_decode_update(const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv, int D,
+                        const float *decay, const prime_state_t *state_in, const prime_state_t *state_out,
+                        void *stream);
+
+/*
  * Launch timer.  No counterpart in the reference: it serves benchmark harnesses
  * that need the device time of ONE kernel of a multi-kernel call.
  * prime_timer_enable(mask) (process-wide; bit (1 << PRIME_KERNEL_*) selects a

@@ -334,6 +334,102 @@ int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, cons
                         workspace_bytes, stream, nullptr, nullptr);
 }
 
+int prime_accumulate(const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv, int L, int D,
+                     const float *decay, const prime_state_t *state_in, const prime_state_t *state_out,
+                     void *workspace, size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    if (!k || !v || !k->data || !v->data || !decay || !state_out || !workspace)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_accumulate: null argument");
+    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d", B, H, H_kv, L);
+    if (k->dtype != v->dtype || (k->dtype != PRIME_BF16 && k->dtype != PRIME_F32))
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "k/v must share dtype BF16 or F32");
+    if (!rows_aligned(k, true) || !rows_aligned(v, true))
+        return fail(PRIME_ERR_MISALIGNED, "k/v rows must start on 16-byte boundaries");
+    if (!aligned16(workspace)) return fail(PRIME_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+    int rc;
+    if ((rc = check_state(state_in, "state_in")) || (rc = check_state(state_out, "state_out"))) return rc;
+    bool inplace;
+    if ((rc = check_state_alias(state_in, state_out, static_cast<size_t>(B) * H, D, &inplace))) return rc;
+    const int S = B * H;
+    const size_t slot = static_cast<size_t>(S) * prime::kWsStride * sizeof(float);
+    if (workspace_bytes < slot)
+        return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes is below the minimum %zu", workspace_bytes, slot);
+    prime::PrefillArgs a{};
+    // q is not read by the state-only kernels; it points at v for safety
+    a.q = v->data; a.k = k->data; a.v = v->data;
+    a.q_sb = v->stride_b; a.q_sh = v->stride_h; a.q_sl = v->stride_l;
+    a.k_sb = k->stride_b; a.k_sh = k->stride_h; a.k_sl = k->stride_l;
+    a.v_sb = v->stride_b; a.v_sh = v->stride_h; a.v_sl = v->stride_l;
+    a.dt_in = k->dtype;
+    a.B = B; a.H = H; a.group = H / H_kv; a.L = L;
+    a.decay = decay; a.eps = 1.0f;
+    if (state_in) {
+        a.s0i = state_in->s0; a.s1i = state_in->s1; a.s2i = state_in->s2;
+        a.k0i = state_in->k0; a.k1i = state_in->k1; a.k2i = state_in->k2;
+    }
+    a.s0o = state_out->s0; a.s1o = state_out->s1; a.s2o = state_out->s2;
+    a.k0o = state_out->k0; a.k1o = state_out->k1; a.k2o = state_out->k2;
+    // G = 1 (one slot per sequence, cps = all chunks) when the workspace holds no more
+    prime::plan_segments(S, L, false, workspace_bytes, &a.G, &a.cps);
+    a.ws = static_cast<float *>(workspace);
+    a.accumulate = 1;
+    (void)inplace;  // the scan reads state_in and the slots before it writes state_out, element by element
+    return check_hip(prime::launch_prefill(a, static_cast<hipStream_t>(stream)), "accumulate launch");
+}
+
+int prime_decode_readout(const prime_tensor_t *q, int B, int H, int D, float eps, const prime_state_t *state,
+                         const prime_tensor_t *y, void *stream) {
+    g_err[0] = 0;
+    if (!q || !q->data || !y || !y->data || !state)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_decode_readout: null argument");
+    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (B <= 0 || H <= 0) return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d", B, H);
+    if (!valid_dtype(q->dtype) || !valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dtype");
+    int rc;
+    if ((rc = check_state(state, "state"))) return rc;
+    prime::DecodeArgs a{};
+    a.q = q->data; a.q_sb = q->stride_b; a.q_sh = q->stride_h; a.dt_q = q->dtype;
+    a.k = q->data; a.v = q->data; a.dt_k = a.dt_v = q->dtype;  // not read
+    a.B = B; a.H = H; a.group = 1; a.eps = eps; a.q_scale = 1.0f;
+    a.s0i = state->s0; a.s1i = state->s1; a.s2i = state->s2; a.k0i = state->k0; a.k1i = state->k1; a.k2i = state->k2;
+    a.s0o = state->s0; a.s1o = state->s1; a.s2o = state->s2; a.k0o = state->k0; a.k1o = state->k1; a.k2o = state->k2;
+    a.y = y->data; a.dt_y = y->dtype; a.y_sb = y->stride_b; a.y_sh = y->stride_h;
+    a.no_update = 1;
+    return check_hip(prime::launch_decode_step(a, static_cast<hipStream_t>(stream)), "readout launch");
+}
+
+int prime_decode_update(const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv, int D,
+                        const float *decay, const prime_state_t *state_in, const prime_state_t *state_out,
+                        void *stream) {
+    g_err[0] = 0;
+    if (!k || !v || !k->data || !v->data || !decay || !state_out)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_decode_update: null argument");
+    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d", B, H, H_kv);
+    if (!valid_dtype(k->dtype) || !valid_dtype(v->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dtype");
+    int rc;
+    if ((rc = check_state(state_in, "state_in")) || (rc = check_state(state_out, "state_out"))) return rc;
+    bool inplace;
+    if ((rc = check_state_alias(state_in, state_out, static_cast<size_t>(B) * H, D, &inplace))) return rc;
+    prime::DecodeArgs a{};
+    a.k = k->data; a.v = v->data; a.q = k->data;  // q not read
+    a.k_sb = k->stride_b; a.k_sh = k->stride_h; a.v_sb = v->stride_b; a.v_sh = v->stride_h;
+    a.dt_k = k->dtype; a.dt_v = v->dtype; a.dt_q = k->dtype;
+    a.B = B; a.H = H; a.group = H / H_kv; a.decay = decay; a.eps = 1.0f; a.q_scale = 1.0f;
+    if (state_in) {
+        a.s0i = state_in->s0; a.s1i = state_in->s1; a.s2i = state_in->s2;
+        a.k0i = state_in->k0; a.k1i = state_in->k1; a.k2i = state_in->k2;
+    }
+    a.s0o = state_out->s0; a.s1o = state_out->s1; a.s2o = state_out->s2;
+    a.k0o = state_out->k0; a.k1o = state_out->k1; a.k2o = state_out->k2;
+    a.y = state_out->s0; a.dt_y = PRIME_F32;  // not written
+    a.no_readout = 1;
+    return check_hip(prime::launch_decode_step(a, static_cast<hipStream_t>(stream)), "update launch");
+}
+
 int prime_selective_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
                             int H, int H_kv, int L, int D, const float *log_decay, const float *k_scale, float eps,
                             const prime_state_t *state_in, const prime_tensor_t *y, const prime_state_t *state_out,
@@ -453,6 +549,13 @@ int prime_delta_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, co
     a.state_in = state_in; a.state_out = state_out;
     a.y = y->data; a.dt_y = y->dtype; a.y_sb = y->stride_b; a.y_sh = y->stride_h;
     return check_hip(prime::launch_delta_step(a, static_cast<hipStream_t>(stream)), "delta step launch");
+}
+
+size_t prime_accumulate_workspace_size(int B, int H, int L) {
+    if (B <= 0 || H <= 0 || L <= 0) return 0;
+    int G, cps;
+    prime::plan_segments(B * H, L, false, static_cast<size_t>(-1), &G, &cps);
+    return static_cast<size_t>(B) * H * (G > 1 ? G : 1) * prime::kWsStride * sizeof(float);
 }
 
 size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags) {

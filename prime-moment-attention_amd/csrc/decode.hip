@@ -43,9 +43,11 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
 
     float qv = 0.f, kv = 0.f, vv = 0.f, lam = 0.f;
     if (active) {
-        qv = load_elem(a.q, b * a.q_sb + h * a.q_sh + lane, a.dt_q);
-        kv = load_elem(a.k, b * a.k_sb + hk * a.k_sh + lane, a.dt_k);
-        vv = load_elem(a.v, b * a.v_sb + hk * a.v_sh + lane, a.dt_v);
+        if (!a.no_readout) qv = load_elem(a.q, b * a.q_sb + h * a.q_sh + lane, a.dt_q);
+        if (!a.no_update) {
+            kv = load_elem(a.k, b * a.k_sb + hk * a.k_sh + lane, a.dt_k);
+            vv = load_elem(a.v, b * a.v_sb + hk * a.v_sh + lane, a.dt_v);
+        }
         if (a.decay_bh) {
             lam = a.decay_bh[b * a.H + h];
         } else if (a.step) {
@@ -56,8 +58,10 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
             d = round_to(d, a.dt_step);
             d = round_to(fminf(fmaxf(d, a.step_min), a.step_max), a.dt_step);
             lam = expf(-d / a.tau[h]);
-        } else {
+        } else if (!a.no_update) {
             lam = a.decay[h];
+        } else {
+            lam = 1.0f;  // readout only: the state as it is (k = v = 0 above)
         }
     }
     if (a.qn_w) {
@@ -108,7 +112,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
     const float s0n = lam * s0v + vv;
     const float k1n = lam * k1v + kv;
     const float k2n = lam * k2v + h2k * kv * kv;
-    const float k0n = lam * k0v + 1.0f;
+    const float k0n = lam * k0v + (a.no_update ? 0.0f : 1.0f);
     sh[wave][0][lane] = qv;
     sh[wave][1][lane] = kv;
     sh[wave][2][lane] = vv;
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
             n2[c] = lam * r2[r][c] + kr2 * v4[c];
             acc[c] += qr * n1[c] + qh * n2[c];
         }
-        if (active) {
+        if (active && !a.no_update) {
             const size_t o = tb + row * kD + 4 * cg;
             *reinterpret_cast<f32x4 *>(a.s1o + o) = n1;
             *reinterpret_cast<f32x4 *>(a.s2o + o) = n2;
@@ -147,11 +151,13 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
     const float inv = 1.0f / fmaxf(den, a.eps);
 
     if (active) {
-        a.s0o[tv + lane] = s0n;
-        a.k1o[tv + lane] = k1n;
-        a.k2o[tv + lane] = k2n;
-        if (lane == 0) a.k0o[t] = k0n;
-        if (rg == 0) {
+        if (!a.no_update) {
+            a.s0o[tv + lane] = s0n;
+            a.k1o[tv + lane] = k1n;
+            a.k2o[tv + lane] = k2n;
+            if (lane == 0) a.k0o[t] = k0n;
+        }
+        if (rg == 0 && !a.no_readout) {
             const f32x4 s04 = *reinterpret_cast<const f32x4 *>(&sh[wave][3][4 * cg]);
             const int64_t yo = b * a.y_sb + h * a.y_sh + 4 * cg;
 #pragma unroll

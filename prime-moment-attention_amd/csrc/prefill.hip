@@ -663,20 +663,54 @@ __global__ __launch_bounds__(256) void segment_scan_kernel(const PrefillArgs a) 
         else carry = a.k0i[seq];
     }
     float *slot = a.ws + static_cast<size_t>(seq) * a.G * kWsStride + e;
-    for (int s = 0; s + 1 < a.G; ++s) {
+    // accumulate: all G segments (the last one may be short), the total out;
+    // otherwise: exclusive prefixes for the chunk loop, in place
+    const int ns = a.accumulate ? a.G : a.G - 1;
+    const float lLast = (a.accumulate && !sel)
+        ? static_cast<float>(pow(static_cast<double>(a.decay[h]),
+                                 static_cast<double>(a.L - (a.G - 1) * a.cps * kC)))
+        : 0.f;
+    for (int s = 0; s < ns; ++s) {
         const float d = slot[static_cast<size_t>(s) * kWsStride];
-        slot[static_cast<size_t>(s) * kWsStride] = carry;
+        if (!a.accumulate) slot[static_cast<size_t>(s) * kWsStride] = carry;
         // selective: segment s's own decay, stored beside its slot's state
-        const float f = sel ? exp2f(slot[static_cast<size_t>(s) * kWsStride + kWsDecay - e]) : lT;
+        const float f = sel ? exp2f(slot[static_cast<size_t>(s) * kWsStride + kWsDecay - e])
+                            : (s == a.G - 1 ? lLast : lT);
         carry = f * carry + d;
     }
-    slot[static_cast<size_t>(a.G - 1) * kWsStride] = carry;
+    if (!a.accumulate) {
+        slot[static_cast<size_t>(a.G - 1) * kWsStride] = carry;
+        return;
+    }
+    const size_t so1 = static_cast<size_t>(seq) * kD * kD, so0 = static_cast<size_t>(seq) * kD;
+    if (e < kWsS2) a.s1o[so1 + e] = carry;
+    else if (e < kWsS0) a.s2o[so1 + e - kWsS2] = carry;
+    else if (e < kWsK1) a.s0o[so0 + e - kWsS0] = carry;
+    else if (e < kWsK2) a.k1o[so0 + e - kWsK1] = carry;
+    else if (e < kWsK0) a.k2o[so0 + e - kWsK2] = carry;
+    else a.k0o[seq] = carry;
 }
 
 template <bool F32IN>
 static hipError_t launch_variant(PrefillArgs a, hipStream_t stream) {
     const int Sq = a.B * a.H;
     hipError_t e;
+    if (a.accumulate) {
+        // every segment's contribution, then the inclusive scan into the state
+        a.nseg_launch = a.G;
+        const TimerEvents ta = timer_events(PRIME_KERNEL_PREFILL_SEGMENTS);
+        if constexpr (F32IN)
+            hipExtLaunchKernelGGL((prefill_kernel<true, true>), dim3(Sq * a.G), dim3(256), 0, stream, ta.start,
+                                  ta.stop, 0, a);
+        else launch_prefill_bf16(a, true, Sq * a.G, stream, ta);
+        if ((e = hipGetLastError()) != hipSuccess) return timer_drop(ta), e;
+        const int64_t n = static_cast<int64_t>(Sq) * kWsElems;
+        const TimerEvents tb = timer_events(PRIME_KERNEL_SEGMENT_SCAN);
+        hipExtLaunchKernelGGL(segment_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                              tb.start, tb.stop, 0, a);
+        if ((e = hipGetLastError()) != hipSuccess) timer_drop(tb);
+        return e;
+    }
     if (a.G > 1) {
         // A: state contribution of every segment but the last, from zero
         a.nseg_launch = a.G - 1;

@@ -35,6 +35,9 @@ struct DecodeArgs {
     int dt_step;
     const float *tau;
     float step_min, step_max;
+    // hybrid-window pieces: no_update = read out the incoming state only
+    // (k, v unused, no state written); no_readout = update only (q, y unused)
+    int no_update, no_readout;
 };
 
 // Residual add + RMSNorm rows (norm.hip).
@@ -101,6 +104,9 @@ struct PrefillArgs {
     // S2 / K2 state components carry the 1/2 of the module's convention
     const float *log_decay;
     const float *k_scale;
+    // accumulate only (no q, no y): every segment's contribution from zero,
+    // then an inclusive scan that writes the final state
+    int accumulate;
 };
 
 // packed fp32 state slot in the workspace: S1 | S2 | S0 | K1 | K2 | K0

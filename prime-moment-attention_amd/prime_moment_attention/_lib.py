@@ -27,7 +27,8 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
            "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_argmax",
            "prime_head_layernorm", "prime_linear", "prime_selective_prefill",
-           "prime_selective_decode_step")
+           "prime_selective_decode_step", "prime_accumulate", "prime_accumulate_workspace_size",
+           "prime_decode_readout", "prime_decode_update")
 
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
@@ -113,6 +114,17 @@ def load() -> ctypes.CDLL:
         P(PrimeSelectiveGate), ctypes.c_void_p, ctypes.c_float, P(PrimeQkNorm), P(PrimeState), P(PrimeState),
         P(PrimeTensor), ctypes.c_void_p]
     L.prime_selective_decode_step.restype = ctypes.c_int
+    L.prime_accumulate.argtypes = [P(PrimeTensor)] * 2 + [ctypes.c_int] * 5 + [
+        fp, P(PrimeState), P(PrimeState), fp, ctypes.c_size_t, fp]
+    L.prime_accumulate.restype = ctypes.c_int
+    L.prime_accumulate_workspace_size.argtypes = [ctypes.c_int] * 3
+    L.prime_accumulate_workspace_size.restype = ctypes.c_size_t
+    L.prime_decode_readout.argtypes = [P(PrimeTensor)] + [ctypes.c_int] * 3 + [
+        ctypes.c_float, P(PrimeState), P(PrimeTensor), fp]
+    L.prime_decode_readout.restype = ctypes.c_int
+    L.prime_decode_update.argtypes = [P(PrimeTensor)] * 2 + [ctypes.c_int] * 4 + [
+        fp, P(PrimeState), P(PrimeState), fp]
+    L.prime_decode_update.restype = ctypes.c_int
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     v = L.prime_abi_version()
     if v != ABI_VERSION:
@@ -445,6 +457,61 @@ def selective_decode_step(q, k, v, gate: PrimeSelectiveGate, k_scale: torch.Tens
                                        ctypes.byref(si) if si else None, ctypes.byref(so), ctypes.byref(yd),
                                        _stream(q.device))
     _check(rc, "prime_selective_decode_step")
+
+
+def accumulate_workspace_size(B: int, H: int, L: int) -> int:
+    return int(load().prime_accumulate_workspace_size(B, H, L))
+
+
+def accumulate(k, v, decay: torch.Tensor, state_in, state_out, H: Optional[int] = None,
+               workspace: Optional[torch.Tensor] = None) -> None:
+    """State of the tokens of k/v [B,Hkv,L,D] (prime_accumulate), appended to
+    state_in (None: zeros) and written to state_out (may be state_in).  H
+    query heads (default Hkv; a multiple of Hkv)."""
+    _dev_check(k, v, decay)
+    B, Hkv, Lk, D = k.shape
+    H = Hkv if H is None else H
+    _shape(v, (B, Hkv, Lk, D), "v")
+    _check_decay(decay, H)
+    _check_state(state_in, B, H, D, "state_in")
+    _check_state(state_out, B, H, D, "state_out")
+    if workspace is None:
+        workspace = torch.empty(max(accumulate_workspace_size(B, H, Lk), 1), dtype=torch.uint8, device=k.device)
+    _dev_check(workspace)
+    kd, vd = tensor_desc(k, True), tensor_desc(v, True)
+    si, so = state_desc(state_in), state_desc(state_out)
+    rc = load().prime_accumulate(ctypes.byref(kd), ctypes.byref(vd), B, H, Hkv, Lk, D, decay.data_ptr(),
+                                 ctypes.byref(si) if si else None, ctypes.byref(so), workspace.data_ptr(),
+                                 workspace.numel() * workspace.element_size(), _stream(k.device))
+    _check(rc, "prime_accumulate")
+
+
+def decode_readout(q, eps: float, state, y) -> None:
+    """y = the moment readout of q [B,H,D] against `state` (prime_decode_readout)."""
+    _dev_check(q, y)
+    B, H, D = q.shape
+    _shape(y, (B, H, D), "y")
+    _check_state(state, B, H, D, "state")
+    qd, yd, sd = tensor_desc(q, False), tensor_desc(y, False), state_desc(state)
+    rc = load().prime_decode_readout(ctypes.byref(qd), B, H, D, float(eps), ctypes.byref(sd), ctypes.byref(yd),
+                                     _stream(q.device))
+    _check(rc, "prime_decode_readout")
+
+
+def decode_update(k, v, decay: torch.Tensor, state_in, state_out, H: Optional[int] = None) -> None:
+    """Append one token of k/v [B,Hkv,D] to the state (prime_decode_update)."""
+    _dev_check(k, v, decay)
+    B, Hkv, D = k.shape
+    H = Hkv if H is None else H
+    _shape(v, (B, Hkv, D), "v")
+    _check_decay(decay, H)
+    _check_state(state_in, B, H, D, "state_in")
+    _check_state(state_out, B, H, D, "state_out")
+    kd, vd = tensor_desc(k, False), tensor_desc(v, False)
+    si, so = state_desc(state_in), state_desc(state_out)
+    rc = load().prime_decode_update(ctypes.byref(kd), ctypes.byref(vd), B, H, Hkv, D, decay.data_ptr(),
+                                    ctypes.byref(si) if si else None, ctypes.byref(so), _stream(k.device))
+    _check(rc, "prime_decode_update")
 
 
 def bind_chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, state_in, y,
