@@ -60,6 +60,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_delta_step.argtypes = [i, i, _dp, _dp, _dp, _dp, _dp, d, _dp, _dp]
         L.oracle_selective_recurrent.argtypes = [i, i, i, _dp, _dp, _dp, _dp, _dp, d] + [_dp] * 7
         L.oracle_selective_parallel.argtypes = [i, i, i, _dp, _dp, _dp, _dp, _dp, _dp, d] + [_dp] * 7
+        L.oracle_recurrent_vjp.argtypes = [i, i, i, _dp, _dp, _dp, _dp, d] + [_dp] * 6 + [_dp] + [_dp] * 6 + [
+            _dp] * 3 + [_dp] * 6
         f = ctypes.c_float
         L.baseline_decode_step.argtypes = [i, i, i, _fp, _fp, _fp, _fp, f] + [_fp] * 7 + [i]
         L.baseline_prefill.argtypes = [i, i, i, i, _fp, _fp, _fp, _fp, f] + [_fp] * 7 + [i]
@@ -153,6 +155,25 @@ def selective_parallel(q, k, v, delta, tau, beta, eps=1.0):
     lib().oracle_selective_parallel(BH, L, D, _p(q), _p(k), _p(v), _p(_c64(delta).reshape(BH, L)),
                                     _p(_lam(tau, BH)), _p(_lam(beta, BH)), eps, *[_p(x) for x in s], _p(y))
     return y, s
+
+
+def recurrent_vjp(q, k, v, lam, dy, eps=1.0, state=None, dstate=None):
+    """Reverse mode of the recurrence (attention.py:119-143): returns
+    (dq, dk, dv, dstate_in) for the output adjoint dy [BH,L,D] and the final
+    state's adjoint dstate (None = 0); dstate_in is the adjoint of `state`
+    (zero state when None)."""
+    q, k, v, dy = _c64(q), _c64(k), _c64(v), _c64(dy)
+    BH, L, D = q.shape
+    si = None if state is None else _state_copy(state, BH, D)[0]
+    so = None if dstate is None else _state_copy(dstate, BH, D)[0]
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(q), np.zeros_like(q)
+    ds = zero_state(BH, D)
+    null = [None] * 6
+    lib().oracle_recurrent_vjp(BH, L, D, _p(q), _p(k), _p(v), _p(_lam(lam, BH)), eps,
+                               *([_p(x) for x in si] if si else null), _p(dy),
+                               *([_p(x) for x in so] if so else null), _p(dq), _p(dk), _p(dv),
+                               *[_p(x) for x in ds])
+    return dq, dk, dv, ds
 
 
 def delta_features(q, k, eps=1e-5):

@@ -620,3 +620,140 @@ void oracle_selective_parallel(int BH, int L, int D, const double *q, const doub
     free(C);
     free(w);
 }
+
+/* ------------------------------------------------------------------------- */
+/* Reverse mode (vector-Jacobian product) of the recurrence.                  */
+/* The reference trains through its prefill with torch autograd               */
+/* (tests/test_attention.py:50-62, attention.py:77-210); this is the same     */
+/* derivative written by hand on the token recurrence of attention.py:119-143,*/
+/* in the reference's state coordinates:                                      */
+/*   after token t: num_j = s0_j + sum_i q_i s1_ij + 1/2 q_i^2 s2_ij,         */
+/*   den = max(k0 + q.k1 + 1/2 q^2.k2, eps), y = num / den;                   */
+/*   torch's clamp passes the gradient where den_raw >= eps.                  */
+/* Inputs: dy [BH,L,D], dstate_out (adjoint of the final state, NULL = 0).    */
+/* Outputs: dq, dk, dv [BH,L,D] and dstate_in (adjoint of state_in).          */
+/* The forward states of one sequence are kept in a buffer of L states.       */
+/* ------------------------------------------------------------------------- */
+void oracle_recurrent_vjp(int BH, int L, int D, const double *q, const double *k,
+                          const double *v, const double *lam, double eps,
+                          const double *S0i, const double *S1i, const double *S2i,
+                          const double *K0i, const double *K1i, const double *K2i,
+                          const double *dy, const double *dS0o, const double *dS1o,
+                          const double *dS2o, const double *dK0o, const double *dK1o,
+                          const double *dK2o, double *dq, double *dk, double *dv,
+                          double *dS0, double *dS1, double *dS2, double *dK0, double *dK1,
+                          double *dK2)
+{
+    const size_t DD = (size_t)D * D, NS = 2 * DD + 3 * (size_t)D + 1;
+    double *hist = (double *)malloc(sizeof(double) * NS * (size_t)(L > 0 ? L : 1));
+    double *cur = (double *)malloc(sizeof(double) * NS);
+    double *dnum = (double *)malloc(sizeof(double) * D);
+    for (int bh = 0; bh < BH; ++bh) {
+        /* state layout in a buffer: s0 | s1 | s2 | k0 | k1 | k2 */
+        double *s0 = cur, *s1 = cur + D, *s2 = s1 + DD, *k0 = s2 + DD, *k1 = k0 + 1, *k2 = k1 + D;
+        if (S0i) {
+            memcpy(s0, S0i + (size_t)bh * D, sizeof(double) * D);
+            memcpy(s1, S1i + (size_t)bh * DD, sizeof(double) * DD);
+            memcpy(s2, S2i + (size_t)bh * DD, sizeof(double) * DD);
+            *k0 = K0i[bh];
+            memcpy(k1, K1i + (size_t)bh * D, sizeof(double) * D);
+            memcpy(k2, K2i + (size_t)bh * D, sizeof(double) * D);
+        } else {
+            memset(cur, 0, sizeof(double) * NS);
+        }
+        const double l = lam[bh];
+        for (int t = 0; t < L; ++t) {  /* forward: the state after each token */
+            const double *kt = k + ((size_t)bh * L + t) * D, *vt = v + ((size_t)bh * L + t) * D;
+            for (int j = 0; j < D; ++j) s0[j] = l * s0[j] + vt[j];
+            for (int i = 0; i < D; ++i)
+                for (int j = 0; j < D; ++j) {
+                    s1[IDX2(i, j, D)] = l * s1[IDX2(i, j, D)] + kt[i] * vt[j];
+                    s2[IDX2(i, j, D)] = l * s2[IDX2(i, j, D)] + kt[i] * kt[i] * vt[j];
+                }
+            *k0 = l * (*k0) + 1.0;
+            for (int i = 0; i < D; ++i) {
+                k1[i] = l * k1[i] + kt[i];
+                k2[i] = l * k2[i] + kt[i] * kt[i];
+            }
+            memcpy(hist + (size_t)t * NS, cur, sizeof(double) * NS);
+        }
+        /* adjoint of the state after the current token, same layout */
+        double *a0 = dS0 + (size_t)bh * D, *a1 = dS1 + (size_t)bh * DD, *a2 = dS2 + (size_t)bh * DD;
+        double *ak0 = dK0 + bh, *ak1 = dK1 + (size_t)bh * D, *ak2 = dK2 + (size_t)bh * D;
+        if (dS0o) {
+            memcpy(a0, dS0o + (size_t)bh * D, sizeof(double) * D);
+            memcpy(a1, dS1o + (size_t)bh * DD, sizeof(double) * DD);
+            memcpy(a2, dS2o + (size_t)bh * DD, sizeof(double) * DD);
+            *ak0 = dK0o[bh];
+            memcpy(ak1, dK1o + (size_t)bh * D, sizeof(double) * D);
+            memcpy(ak2, dK2o + (size_t)bh * D, sizeof(double) * D);
+        } else {
+            memset(a0, 0, sizeof(double) * D); memset(a1, 0, sizeof(double) * DD);
+            memset(a2, 0, sizeof(double) * DD); *ak0 = 0.0;
+            memset(ak1, 0, sizeof(double) * D); memset(ak2, 0, sizeof(double) * D);
+        }
+        for (int t = L - 1; t >= 0; --t) {
+            const double *h = hist + (size_t)t * NS;
+            const double *h0 = h, *h1 = h + D, *h2 = h1 + DD, *hk0 = h2 + DD, *hk1 = hk0 + 1, *hk2 = hk1 + D;
+            const double *qt = q + ((size_t)bh * L + t) * D, *kt = k + ((size_t)bh * L + t) * D;
+            const double *vt = v + ((size_t)bh * L + t) * D, *gy = dy + ((size_t)bh * L + t) * D;
+            double *gq = dq + ((size_t)bh * L + t) * D, *gk = dk + ((size_t)bh * L + t) * D;
+            double *gv = dv + ((size_t)bh * L + t) * D;
+            /* readout of token t */
+            double raw = *hk0;
+            for (int i = 0; i < D; ++i) raw += qt[i] * hk1[i] + 0.5 * qt[i] * qt[i] * hk2[i];
+            const double den = raw < eps ? eps : raw;
+            double dot = 0.0;
+            for (int j = 0; j < D; ++j) {
+                double num = h0[j];
+                for (int i = 0; i < D; ++i) num += qt[i] * h1[IDX2(i, j, D)] + 0.5 * qt[i] * qt[i] * h2[IDX2(i, j, D)];
+                dot += gy[j] * num / den;
+                dnum[j] = gy[j] / den;
+            }
+            const double dden = raw >= eps ? -dot / den : 0.0;
+            for (int i = 0; i < D; ++i) {
+                double g = dden * (hk1[i] + qt[i] * hk2[i]);
+                for (int j = 0; j < D; ++j) g += dnum[j] * (h1[IDX2(i, j, D)] + qt[i] * h2[IDX2(i, j, D)]);
+                gq[i] = g;
+            }
+            for (int j = 0; j < D; ++j) a0[j] += dnum[j];
+            for (int i = 0; i < D; ++i)
+                for (int j = 0; j < D; ++j) {
+                    a1[IDX2(i, j, D)] += qt[i] * dnum[j];
+                    a2[IDX2(i, j, D)] += 0.5 * qt[i] * qt[i] * dnum[j];
+                }
+            *ak0 += dden;
+            for (int i = 0; i < D; ++i) {
+                ak1[i] += qt[i] * dden;
+                ak2[i] += 0.5 * qt[i] * qt[i] * dden;
+            }
+            /* update of token t: state = l * state_before + f(k_t, v_t) */
+            for (int j = 0; j < D; ++j) {
+                double g = a0[j];
+                for (int i = 0; i < D; ++i) g += a1[IDX2(i, j, D)] * kt[i] + a2[IDX2(i, j, D)] * kt[i] * kt[i];
+                gv[j] = g;
+            }
+            for (int i = 0; i < D; ++i) {
+                double g1 = 0.0, g2 = 0.0;
+                for (int j = 0; j < D; ++j) {
+                    g1 += a1[IDX2(i, j, D)] * vt[j];
+                    g2 += a2[IDX2(i, j, D)] * vt[j];
+                }
+                gk[i] = g1 + 2.0 * kt[i] * g2 + ak1[i] + 2.0 * kt[i] * ak2[i];
+            }
+            for (int j = 0; j < D; ++j) a0[j] *= l;
+            for (size_t x = 0; x < DD; ++x) {
+                a1[x] *= l;
+                a2[x] *= l;
+            }
+            *ak0 *= l;
+            for (int i = 0; i < D; ++i) {
+                ak1[i] *= l;
+                ak2[i] *= l;
+            }
+        }
+    }
+    free(hist);
+    free(cur);
+    free(dnum);
+}

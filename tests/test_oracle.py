@@ -402,3 +402,113 @@ def test_selective_single_token_is_v():
     np.testing.assert_allclose(y, v, rtol=1e-12)
     np.testing.assert_allclose(s[4], beta[:, None] * k[:, 0], rtol=1e-12)
     np.testing.assert_allclose(s[5], 0.5 * beta[:, None] ** 2 * k[:, 0] ** 2, rtol=1e-12)
+
+
+# ---------------------------------------------------------------- reverse mode
+def _vjp_case(BH, L, seed, with_state, normalize=True, eps=1.0, D=64):
+    q, k, v = O.make_inputs((BH, L, D), seed=seed, bf16=False, normalize=normalize)
+    rng = np.random.default_rng(seed + 1)
+    lam = rng.uniform(0.9, 0.999, BH)
+    st = _random_state(BH, D, seed + 2) if with_state else None
+    dy = rng.standard_normal((BH, L, D))
+    ds = tuple(rng.standard_normal(x.shape) for x in O.zero_state(BH, D))
+    return q, k, v, lam, st, dy, ds
+
+
+def _random_state(BH, D, seed):
+    q, k, v = O.make_inputs((BH, 16, D), seed=seed, bf16=False)
+    return O.recurrent(q, k, v, 0.95)[1]
+
+
+def _objective(q, k, v, lam, st, dy, ds, eps):
+    y, so = O.recurrent(q, k, v, lam, eps=eps, state=st)
+    return float((y * dy).sum() + sum((a * b).sum() for a, b in zip(so, ds)))
+
+
+@pytest.mark.parametrize("with_state", [False, True])
+@pytest.mark.parametrize("normalize,eps", [(True, 1.0), (False, 1e-3)])
+def test_recurrent_vjp_matches_finite_differences(with_state, normalize, eps):
+    """Directional derivatives of <dy, y> + <dstate, state_out> by central
+    differences of the forward recurrence, against the hand-written reverse
+    mode, along random directions of q, k, v and the incoming state."""
+    BH, L = 2, 6
+    q, k, v, lam, st, dy, ds = _vjp_case(BH, L, 300, with_state, normalize, eps)
+    dq, dk, dv, dst = O.recurrent_vjp(q, k, v, lam, dy, eps=eps, state=st, dstate=ds)
+    rng = np.random.default_rng(301)
+    h = 1e-6
+    for _ in range(4):
+        tq, tk, tv = (rng.standard_normal(q.shape) for _ in range(3))
+        ts = tuple(rng.standard_normal(x.shape) for x in O.zero_state(BH, 64)) if with_state else None
+        move = lambda s: (q + s * tq, k + s * tk, v + s * tv,
+                          None if st is None else tuple(a + s * b for a, b in zip(st, ts)))
+        fp = _objective(*move(h)[:3], lam, move(h)[3], dy, ds, eps)
+        fm = _objective(*move(-h)[:3], lam, move(-h)[3], dy, ds, eps)
+        fd = (fp - fm) / (2 * h)
+        an = float((dq * tq).sum() + (dk * tk).sum() + (dv * tv).sum())
+        if with_state:
+            an += float(sum((a * b).sum() for a, b in zip(dst, ts)))
+        assert abs(fd - an) <= 1e-6 * max(1.0, abs(an)), (fd, an)
+
+
+def test_recurrent_vjp_clamped_tokens_pass_no_denominator_gradient():
+    """A token whose denominator is below eps: its output is num / eps, so dq
+    of that token only carries the numerator term (element-wise check by
+    central differences on every q element of that token)."""
+    BH, L, eps = 1, 4, 1e-3
+    q, k, v = O.make_inputs((BH, L, 64), seed=310, bf16=False, normalize=False)
+    # token 3 queries against -K1: its denominator is negative (clamped)
+    _, so = O.recurrent(q[:, :3], k[:, :3], v[:, :3], 0.99)
+    K1, K2 = so[4], so[5]
+    kk = k[:, 3]
+    K1n = 0.99 * K1 + kk
+    K2n = 0.99 * K2 + kk * kk
+    a = (K1n * K1n).sum(-1) / (K1n * K1n * K2n).sum(-1)
+    q, k, v = (x.astype(np.float64) for x in (q, k, v))  # perturbations below float32 resolution
+    q[:, 3] = -a[:, None] * K1n
+    y, st = O.recurrent(q, k, v, 0.99, eps=eps)
+    assert (st[3] + (q[:, 3] * st[4]).sum(-1) + 0.5 * (q[:, 3] ** 2 * st[5]).sum(-1) < eps).all()
+    dy = np.random.default_rng(311).standard_normal(y.shape)
+    dq = O.recurrent_vjp(q, k, v, 0.99, dy, eps=eps)[0]
+    h = 1e-6
+    for i in range(64):
+        qp, qm = q.copy(), q.copy()
+        qp[0, 3, i] += h
+        qm[0, 3, i] -= h
+        fd = (((O.recurrent(qp, k, v, 0.99, eps=eps)[0] - O.recurrent(qm, k, v, 0.99, eps=eps)[0]) * dy).sum()
+              / (2 * h))
+        assert abs(fd - dq[0, 3, i]) <= 1e-6 * max(1.0, abs(fd))
+
+
+@pytest.mark.parametrize("with_state", [False, True])
+def test_recurrent_vjp_matches_torch_autograd_of_dense_branch(with_state):
+    """torch's float64 autograd through the dense branch's formula
+    (attention.py:160-202; one clamp, as its L == 1 and chunked forms,
+    chunked_ssd.py:156) gives the same dq, dk, dv and state adjoints."""
+    import torch
+    BH, L, D, eps = 3, 9, 64, 1.0
+    q, k, v, lam, st, dy, _ = _vjp_case(BH, L, 320, with_state)
+    dq, dk, dv, dst = O.recurrent_vjp(q, k, v, lam, dy, eps=eps, state=st)
+    T = lambda x: torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    tq, tk, tv = T(q), T(k), T(v)
+    ts = [T(x) for x in st] if with_state else None
+    lam_t = torch.tensor(lam, dtype=torch.float64).view(BH, 1, 1)
+    idx = torch.arange(L, dtype=torch.float64)
+    diff = idx.view(L, 1) - idx.view(1, L)
+    dm = torch.where(diff >= 0, lam_t ** diff.clamp(min=0), torch.zeros(()))
+    A = dm * (1.0 + tq @ tk.transpose(1, 2) + 0.5 * (tq * tq) @ (tk * tk).transpose(1, 2))
+    num = A @ tv
+    den = A.sum(-1, keepdim=True)
+    if with_state:
+        S0, S1, S2, K0, K1, K2 = ts
+        into = lam_t ** (idx + 1).view(1, L, 1)
+        num = num + into * (S0.unsqueeze(1) + tq @ S1 + 0.5 * (tq * tq) @ S2)
+        den = den + into * (K0.view(BH, 1, 1) + (tq * K1.unsqueeze(1)).sum(-1, keepdim=True)
+                            + 0.5 * (tq * tq * K2.unsqueeze(1)).sum(-1, keepdim=True))
+    y = num / den.clamp(min=eps)
+    (y * torch.tensor(dy)).sum().backward()
+    for got, ref in ((dq, tq.grad), (dk, tk.grad), (dv, tv.grad)):
+        assert np.abs(got - ref.numpy()).max() <= 1e-10 * max(1.0, np.abs(ref.numpy()).max())
+    if with_state:
+        for got, ref in zip(dst, ts):
+            r = ref.grad.numpy().reshape(got.shape)
+            assert np.abs(got - r).max() <= 1e-10 * max(1.0, np.abs(r).max())
