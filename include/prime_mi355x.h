@@ -308,6 +308,32 @@ int prime_accumulate(const prime_tensor_t *k, const prime_tensor_t *v, int B, in
 size_t prime_accumulate_workspace_size(int B, int H, int L);
 
 /*
+ * Backward of prime_chunked_prefill: the reverse-mode derivative the reference
+ * obtains from torch autograd when it trains through its prefill
+ * (tests/test_attention.py:50-62 through attention.py:77-210 and
+ * chunked_ssd.py:48-184).  For output adjoints dy [B, H, L, D] (and
+ * dstate_out, the adjoint of the final state; NULL = 0) it writes
+ *   dq, dk, dv   [B, H, L, D] (one dtype and one set of strides for the three)
+ *   dstate_in    the adjoint of state_in (NULL: not written)
+ * with the clamp's gradient passing where den >= eps, as torch's clamp.
+ * q (pre-scaled), k, v, decay, eps and state_in are the forward's arguments.
+ * k/v must have one head per query head (H_kv == H: the reference module
+ * expands grouped k/v before the recurrence, attention.py:92-94).  With
+ * PRIME_FLAG_DENSE_CLAMP an incoming state is rejected; without one the two
+ * clamps are the same.  MFMA operands are bf16 (fp32 accumulation) for bf16
+ * and fp32 inputs alike.  workspace: at least
+ * prime_chunked_prefill_backward_workspace_size() bytes, 4-byte aligned.
+ */
+int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                                   int B, int H, int H_kv, int L, int D, const float *decay, float eps,
+                                   unsigned flags, const prime_state_t *state_in, const prime_tensor_t *dy,
+                                   const prime_state_t *dstate_out, const prime_tensor_t *dq,
+                                   const prime_tensor_t *dk, const prime_tensor_t *dv,
+                                   const prime_state_t *dstate_in, void *workspace, size_t workspace_bytes,
+                                   void *stream);
+size_t prime_chunked_prefill_backward_workspace_size(int B, int H, int L);
+
+/*
  * prime_decode_readout replaces prime_query_step_cpp (prime_cpp_kernel.cpp:85-100):
  * y = (S0 + S1^T q + 1/2 S2^T q^2) / max(K0 + q.K1 + 1/2 q^2.K2, eps) against
  * `state` as it is (the reference's eps is 1e-3); the state is not written.
@@ -344,7 +370,9 @@ int prime_decode_update(const prime_tensor_t *k, const prime_tensor_t *v, int B,
 #define PRIME_KERNEL_DELTA_PREP       4 /* delta rule: per-chunk solve and transfer matrices */
 #define PRIME_KERNEL_DELTA_SCAN       5 /* delta rule: sequential scan over chunks */
 #define PRIME_KERNEL_DELTA_STEP       6 /* delta rule: decode step */
-#define PRIME_KERNEL_COUNT            7
+#define PRIME_KERNEL_BWD_DQ           7 /* prefill backward: dq pass (chunks in order) */
+#define PRIME_KERNEL_BWD_DKV          8 /* prefill backward: dk, dv pass (chunks in reverse) */
+#define PRIME_KERNEL_COUNT            9
 
 int prime_timer_enable(unsigned mask);
 int prime_timer_reset(void);

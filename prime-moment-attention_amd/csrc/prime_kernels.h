@@ -115,6 +115,26 @@ constexpr int kWsStride = 8448;  // floats per slot (33,792 bytes)
 constexpr int kWsElems = 8385;   // state floats per slot
 constexpr int kWsDecay = 8385;   // selective: the segment's log2 decay (not part of the scanned state)
 
+// Backward of the chunked prefill (prefill_bwd.hip): the adjoints of q, k,
+// v and of the incoming state for output adjoints dy (and of the final state).
+struct BwdArgs {
+    const void *q, *k, *v, *dy;
+    int64_t q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl, dy_sb, dy_sh, dy_sl;
+    int dt_in, dt_dy;  // q/k/v: PRIME_BF16 or PRIME_F32; dy: any
+    int B, H, L;
+    const float *decay;
+    float eps;
+    const float *s0i, *s1i, *s2i, *k0i, *k1i, *k2i;         // incoming state (null => zero)
+    const float *ds0o, *ds1o, *ds2o, *dk0o, *dk1o, *dk2o;   // adjoint of the final state (null => 0)
+    void *dq, *dk, *dv;
+    int dt_g;
+    int64_t g_sb, g_sh, g_sl;                               // strides of dq, dk, dv
+    float *ds0i, *ds1i, *ds2i, *dk0i, *dk1i, *dk2i;         // adjoint of the incoming state (null => none)
+    float *inv_den, *g_den;                                 // [B*H, L] fp32, written by the dq pass
+};
+
+hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream);
+
 hipError_t launch_decode_step(const DecodeArgs &a, hipStream_t stream);
 hipError_t launch_prefill(PrefillArgs a, hipStream_t stream);
 // segments per sequence for the launch plan, given the workspace the caller has

@@ -28,15 +28,18 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_argmax",
            "prime_head_layernorm", "prime_linear", "prime_selective_prefill",
            "prime_selective_decode_step", "prime_accumulate", "prime_accumulate_workspace_size",
-           "prime_decode_readout", "prime_decode_update")
+           "prime_decode_readout", "prime_decode_update", "prime_chunked_prefill_backward",
+           "prime_chunked_prefill_backward_workspace_size")
 
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
 KERNEL_DELTA_PREP, KERNEL_DELTA_SCAN, KERNEL_DELTA_STEP = 4, 5, 6
+KERNEL_BWD_DQ, KERNEL_BWD_DKV = 7, 8
 KERNEL_NAMES = {KERNEL_PREFILL_CHUNKS: "prefill_bf16_kernel<false>", KERNEL_PREFILL_SEGMENTS:
                 "prefill_bf16_kernel<true>", KERNEL_SEGMENT_SCAN: "segment_scan_kernel",
                 KERNEL_DECODE: "decode_step_kernel", KERNEL_DELTA_PREP: "delta_prep_kernel",
-                KERNEL_DELTA_SCAN: "delta_scan_kernel", KERNEL_DELTA_STEP: "delta_step_kernel"}
+                KERNEL_DELTA_SCAN: "delta_scan_kernel", KERNEL_DELTA_STEP: "delta_step_kernel",
+                KERNEL_BWD_DQ: "prefill_bwd_dq_kernel", KERNEL_BWD_DKV: "prefill_bwd_dkv_kernel"}
 
 
 class PrimeTensor(ctypes.Structure):
@@ -125,6 +128,12 @@ def load() -> ctypes.CDLL:
     L.prime_decode_update.argtypes = [P(PrimeTensor)] * 2 + [ctypes.c_int] * 4 + [
         fp, P(PrimeState), P(PrimeState), fp]
     L.prime_decode_update.restype = ctypes.c_int
+    L.prime_chunked_prefill_backward.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 5 + [
+        fp, ctypes.c_float, ctypes.c_uint, P(PrimeState), P(PrimeTensor), P(PrimeState)] + [
+        P(PrimeTensor)] * 3 + [P(PrimeState), fp, ctypes.c_size_t, fp]
+    L.prime_chunked_prefill_backward.restype = ctypes.c_int
+    L.prime_chunked_prefill_backward_workspace_size.argtypes = [ctypes.c_int] * 3
+    L.prime_chunked_prefill_backward_workspace_size.restype = ctypes.c_size_t
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     v = L.prime_abi_version()
     if v != ABI_VERSION:
@@ -457,6 +466,36 @@ def selective_decode_step(q, k, v, gate: PrimeSelectiveGate, k_scale: torch.Tens
                                        ctypes.byref(si) if si else None, ctypes.byref(so), ctypes.byref(yd),
                                        _stream(q.device))
     _check(rc, "prime_selective_decode_step")
+
+
+def backward_workspace_size(B: int, H: int, L: int) -> int:
+    return int(load().prime_chunked_prefill_backward_workspace_size(B, H, L))
+
+
+def chunked_prefill_backward(q, k, v, decay: torch.Tensor, eps: float, state_in, dy, dstate_out, dq, dk, dv,
+                             dstate_in, flags: int = 0, workspace: Optional[torch.Tensor] = None) -> None:
+    """Backward of the chunked prefill (prime_chunked_prefill_backward).
+    q, k, v [B,H,L,D] (bf16 or fp32, k/v with H heads), dy [B,H,L,D];
+    dstate_out / state_in / dstate_in: 6-tuples or None; dq, dk, dv share a
+    dtype and strides."""
+    _dev_check(q, k, v, dy, dq, dk, dv, decay)
+    B, H, Lq, D = q.shape
+    for t, n in ((k, "k"), (v, "v"), (dy, "dy"), (dq, "dq"), (dk, "dk"), (dv, "dv")):
+        _shape(t, (B, H, Lq, D), n)
+    _check_decay(decay, H)
+    _check_state(state_in, B, H, D, "state_in")
+    _check_state(dstate_out, B, H, D, "dstate_out")
+    _check_state(dstate_in, B, H, D, "dstate_in")
+    if workspace is None:
+        workspace = torch.empty(max(backward_workspace_size(B, H, Lq), 4), dtype=torch.uint8, device=q.device)
+    descs = [tensor_desc(t, True) for t in (q, k, v, dy, dq, dk, dv)]
+    si, so, sd = state_desc(state_in), state_desc(dstate_out), state_desc(dstate_in)
+    r = lambda x: ctypes.byref(x) if x is not None else None
+    rc = load().prime_chunked_prefill_backward(
+        r(descs[0]), r(descs[1]), r(descs[2]), B, H, H, Lq, D, decay.data_ptr(), float(eps), int(flags), r(si),
+        r(descs[3]), r(so), r(descs[4]), r(descs[5]), r(descs[6]), r(sd), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _stream(q.device))
+    _check(rc, "prime_chunked_prefill_backward")
 
 
 def accumulate_workspace_size(B: int, H: int, L: int) -> int:

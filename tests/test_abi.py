@@ -91,7 +91,7 @@ def test_timer_reads_without_launches():
     recorded every kernel reads zero launches (no device work involved)."""
     L = _lib.load()
     ms, n = ctypes.c_double(), ctypes.c_int64()
-    assert L.prime_timer_read(7, ctypes.byref(ms), ctypes.byref(n)) == -1
+    assert L.prime_timer_read(len(_lib.KERNEL_NAMES), ctypes.byref(ms), ctypes.byref(n)) == -1
     assert L.prime_timer_read(0, None, None) == -1
     _lib.timer_enable()
     _lib.timer_reset()
