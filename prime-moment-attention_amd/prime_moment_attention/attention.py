@@ -27,7 +27,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .chunked_ssd import prime_prefill
+from .chunked_ssd import needs_grad, prime_prefill
 
 
 def _same_storage(a, b) -> bool:
@@ -101,6 +101,22 @@ class PrimeMomentAttention(nn.Module):
         H, D = self.num_heads, self.head_dim
         dev = hidden_states.device
         y_dtype = orig_dtype if orig_dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
+
+        if torch.is_grad_enabled() and (hidden_states.requires_grad or any(p.requires_grad for p in self.parameters())):
+            # training: QK-norm and scale as torch ops, the recurrence through the
+            # differentiable prefill (for L == 1 its chunked form is the step,
+            # attention.py:119-143; for L <= chunk_threshold without a state the
+            # dense branch's clamps are one clamp)
+            q, k, v = self.project(hidden_states, normalize=False)
+            if self.use_qk_norm:
+                q, k = self.q_norm(q), self.k_norm(k)
+            q = q * self.scaling
+            dense = 1 < L <= self.chunk_threshold
+            y, next_state = prime_prefill(q, k, v, state=state, decay=self.decay, eps=self.eps,
+                                          chunk_size=self.chunk_size, return_state=return_state,
+                                          dense_clamp=dense)
+            y = y.to(orig_dtype).transpose(1, 2).reshape(B, L, H * D)
+            return self.o_proj(y), (next_state if return_state else None)
 
         if L == 1:
             # the QK LayerNorm and the 1/sqrt(D) scale run inside the decode kernel

@@ -25,6 +25,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
+from .chunked_ssd import no_backward
 
 
 class ChunkedGatedDeltaPrimeAttention(nn.Module):
@@ -107,5 +108,6 @@ class ChunkedGatedDeltaPrimeAttention(nn.Module):
                        else t.contiguous() for t in (q, k, v))
             y = torch.empty(B, H, L, D, device=dev, dtype=y_dtype)
             _lib.delta_prefill(q, k, v, beta, alpha, self.decay, self.eps, self.lyapunov_bound, s_in, y, s_out)
+        y = no_backward("the delta-rule PRIME recurrence", y, q, k, v, beta, alpha, s_in)
         y = y.to(dtype).transpose(1, 2).reshape(B, L, H * D)
         return self.o_proj(y), (s_out if return_state else None)

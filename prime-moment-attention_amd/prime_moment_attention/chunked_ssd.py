@@ -35,11 +35,83 @@ def _prep(x: torch.Tensor) -> torch.Tensor:
     return x
 
 
+def needs_grad(*xs) -> bool:
+    """True when autograd records: grad mode on and some input requires grad."""
+    return torch.is_grad_enabled() and any(torch.is_tensor(x) and x.requires_grad for x in xs)
+
+
+class _NoBackward(torch.autograd.Function):
+    """Ties a HIP result to the inputs it was computed from, so that a
+    backward through it fails loudly instead of leaving their gradients
+    silently empty."""
+
+    @staticmethod
+    def forward(ctx, what, y, *inputs):
+        ctx.what = what
+        return y.view_as(y)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError(f"{ctx.what} has no backward in this library (the base chunked prefill does); "
+                                  "run it under torch.no_grad()")
+
+
+def no_backward(what: str, y: torch.Tensor, *inputs) -> torch.Tensor:
+    """y, marked as not differentiable with respect to `inputs` (a backward raises)."""
+    if needs_grad(*inputs):
+        return _NoBackward.apply(what, y, *[x for x in inputs if torch.is_tensor(x)])
+    return y
+
+
+class _PrefillFn(torch.autograd.Function):
+    """prime_chunked_prefill with its backward (prime_chunked_prefill_backward):
+    the derivative torch autograd takes through the reference's prefill
+    (attention.py:77-210, chunked_ssd.py:48-184) when it trains."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, dec, eps, flags, return_state, out_dtype, *state):
+        B, H, L, D = q.shape
+        st_in = tuple(state) if state else None
+        y = torch.empty(B, H, L, D, device=q.device, dtype=out_dtype)
+        st_out = _lib.new_state(B, H, D, q.device) if return_state else None
+        _lib.chunked_prefill(q, k, v, dec, eps, 64, st_in, y, st_out, flags)
+        ctx.save_for_backward(q, k, v, dec, *(st_in or ()))
+        ctx.eps, ctx.flags, ctx.has_state = eps, flags, st_in is not None
+        ctx.set_materialize_grads(False)
+        return (y, *st_out) if return_state else y
+
+    @staticmethod
+    def backward(ctx, dy, *dstate):
+        q, k, v, dec, *st = ctx.saved_tensors
+        B, H, L, D = q.shape
+        Hkv = k.shape[1]
+        grp = H // Hkv
+        if grp > 1:  # the kernel takes one k/v head per query head (attention.py:92-94 expands them too)
+            k, v = k.repeat_interleave(grp, dim=1), v.repeat_interleave(grp, dim=1)
+        dev = q.device
+        dy = torch.zeros(B, H, L, D, device=dev, dtype=torch.float32) if dy is None else _prep(dy)
+        dso = None
+        if any(t is not None for t in dstate):
+            zs = _lib.new_state(B, H, D, dev, zero=True)
+            dso = tuple(z if t is None else t.to(torch.float32).reshape(z.shape).contiguous()
+                        for z, t in zip(zs, dstate))
+        dq, dk, dv = (torch.empty(B, H, L, D, device=dev, dtype=q.dtype) for _ in range(3))
+        dsi = _lib.new_state(B, H, D, dev) if ctx.has_state else None
+        _lib.chunked_prefill_backward(q, k, v, dec, ctx.eps, tuple(st) if st else None, dy, dso, dq, dk, dv, dsi,
+                                      flags=ctx.flags)
+        if grp > 1:
+            dk, dv = dk.view(B, Hkv, grp, L, D).sum(2), dv.view(B, Hkv, grp, L, D).sum(2)
+        return (dq, dk, dv, None, None, None, None, None, *(dsi or ()))
+
+
 def prime_prefill(q, k, v, state=None, decay=0.9995, eps=1.0, chunk_size=64, return_state=False,
                   out_dtype=torch.float32, dense_clamp=False, state_out=None, y=None):
     """Core launcher shared by the modules.  Returns (y, next_state | None);
     ``y`` may be a caller-provided [B, H, L, D] view (any strides with a
-    contiguous D and 16-byte aligned rows)."""
+    contiguous D and 16-byte aligned rows).  When autograd records (an input
+    requires grad), the call is differentiable -- in q, k, v and the incoming
+    state -- through the HIP backward; ``y`` and ``state_out`` are then not
+    used (fresh outputs are returned)."""
     B, H, L, D = q.shape
     q, k, v = _prep(q), _prep(k), _prep(v)
     if k.dtype != q.dtype or v.dtype != q.dtype:
@@ -47,6 +119,15 @@ def prime_prefill(q, k, v, state=None, decay=0.9995, eps=1.0, chunk_size=64, ret
     dev = q.device
     dec = _lib.decay_tensor(decay, H, dev)
     st_in = _lib.as_state(state, B, H, D, dev) if state is not None else None
+    if needs_grad(q, k, v, *(st_in or ())):
+        if dense_clamp and st_in is not None:
+            raise NotImplementedError("the dense branch's double clamp with an incoming state has no backward "
+                                      "here; call under torch.no_grad() or without a state")
+        flags = _lib.PRIME_FLAG_DENSE_CLAMP if dense_clamp else 0
+        outs = _PrefillFn.apply(q, k, v, dec, float(eps), flags, bool(return_state), out_dtype, *(st_in or ()))
+        if return_state:
+            return outs[0], tuple(outs[1:])
+        return outs, None
     if y is None:
         y = torch.empty(B, H, L, D, device=dev, dtype=out_dtype)
     st_out = None
@@ -102,6 +183,15 @@ class ChunkedPrimeSSD(nn.Module):
         q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
         k = self.k_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
         v = self.v_proj(hidden_states).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
+        if needs_grad(q, k, v):
+            # training: QK-norm and scale as torch ops (chunked_ssd.py:225-236), the core differentiable
+            if self.use_qk_norm:
+                q, k = self.q_norm(q), self.k_norm(k)
+            q = q * self.scaling
+            y, next_state = prime_prefill(q, k, v, state=state, decay=self.decay, eps=self.eps,
+                                          chunk_size=self.chunk_size, return_state=return_state)
+            y = y.to(dtype).transpose(1, 2).reshape(B, L, self.num_heads * self.head_dim)
+            return self.o_proj(y), next_state
         # QK-norm and scale in place on the projections (chunked_ssd.py:225-236)
         _lib.head_layernorm(q, q, self.q_norm if self.use_qk_norm else None, self.scaling)
         if self.use_qk_norm:

@@ -83,6 +83,9 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad):
+            # training: the reference's ops (model.py:54-56), differentiable
+            return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps) * self.weight
         xc = x.contiguous()
         out = torch.empty_like(xc)
         w = self.weight if self.weight.dtype == xc.dtype else self.weight.to(xc.dtype)
@@ -180,6 +183,8 @@ class PrimeForCausalLM(nn.Module):
     def forward(self, input_ids: torch.Tensor, labels: Optional[torch.Tensor] = None,
                 states: Optional[List[Tuple[torch.Tensor, ...]]] = None, return_states: bool = False,
                 logits_to_keep: int = 0) -> Dict[str, Any]:
+        if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
+            return self._forward_graph(input_ids, labels, states, return_states, logits_to_keep)
         # The blocks' residual adds are folded into the following RMSNorm
         # (prime_add_rmsnorm stores the rounded sum, as the separate add does):
         # x is this call's own residual stream, updated in place; `pending` is
@@ -205,6 +210,26 @@ class PrimeForCausalLM(nn.Module):
         _lib.add_rmsnorm(x.view(-1, hidden), pending.view(-1, hidden) if pending is not None else None,
                          self.norm.weight, nf.view(-1, hidden), self.norm.eps)
         logits = self.lm_head(nf)
+        loss = None
+        if labels is not None:
+            shift_logits = logits[..., :-1, :].contiguous().to(torch.float32)
+            loss = F.cross_entropy(shift_logits.view(-1, self.config.vocab_size),
+                                   labels[..., 1:].contiguous().view(-1), ignore_index=-100)
+        return {"loss": loss, "logits": logits, "states": next_states}
+
+    def _forward_graph(self, input_ids, labels, states, return_states, logits_to_keep):
+        """The reference's composition (model.py:175-200) for autograd: each
+        block's residual adds and RMSNorms as torch ops, the attention through
+        the differentiable prefill."""
+        x = self.embed_tokens(input_ids)
+        next_states = [] if return_states else None
+        for i, layer in enumerate(self.layers):
+            x, ns = layer(x, state=states[i] if states is not None else None, return_state=return_states)
+            if return_states:
+                next_states.append(ns)
+        if logits_to_keep:
+            x = x[:, -logits_to_keep:]
+        logits = self.lm_head(self.norm(x))
         loss = None
         if labels is not None:
             shift_logits = logits[..., :-1, :].contiguous().to(torch.float32)

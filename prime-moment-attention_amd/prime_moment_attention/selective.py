@@ -30,6 +30,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
+from .chunked_ssd import no_backward
 
 
 class PrimeSelectiveMomentAttention(nn.Module):
@@ -122,5 +123,7 @@ class PrimeSelectiveMomentAttention(nn.Module):
             next_state = _lib.new_state(B, H, D, dev) if return_state else None
             _lib.selective_prefill(q, k, v, log_decay, beta, self.eps, None, y_bl.transpose(1, 2), next_state)
             y = y_bl.transpose(1, 2)
+        y = no_backward("selective PRIME", y, q, k, v, tau, beta, hidden_states,
+                        *(state if state is not None else ()))
         y = y.to(orig_dtype).transpose(1, 2).reshape(B, L, H * D)
         return self.o_proj(y), (next_state if return_state else None)

@@ -117,3 +117,136 @@ def test_backward_rejects_bad_arguments():
                                       workspace=torch.empty(64, dtype=torch.uint8, device=dev()))
     with pytest.raises(RuntimeError, match="share dtype"):
         _lib.chunked_prefill_backward(x, x, x, lam, 1.0, None, x, None, g[0], g[1], g[2].bfloat16(), None)
+
+
+# ---------------------------------------------------------------- autograd
+def test_core_autograd_matches_oracle_vjp():
+    """chunked_prime_ssd_core under autograd (q, k, v and the incoming state
+    requiring grad, the final state used in the loss) against the oracle."""
+    from prime_moment_attention import chunked_prime_ssd_core
+    B, H, L = 2, 2, 300
+    BH = B * H
+    q, k, v = O.make_inputs((B, H, L, D), seed=450, bf16=False)
+    rng = np.random.default_rng(451)
+    lam = rng.uniform(0.99, 0.9999, H).astype(np.float32)
+    st0 = random_state(BH, D, 452)
+    dy = rng.standard_normal((B, H, L, D))
+    ds = tuple(0.1 * rng.standard_normal(x.shape) for x in O.zero_state(BH, D))
+    ref = O.recurrent_vjp(q.reshape(BH, L, D), k.reshape(BH, L, D), v.reshape(BH, L, D),
+                          np.tile(lam.astype(np.float64), B), dy.reshape(BH, L, D), state=st0, dstate=ds)
+    tq, tk, tv = (to_dev(x).requires_grad_(True) for x in (q, k, v))
+    ts = [t.requires_grad_(True) for t in state_to_dev(st0, B, H, D)]
+    y, st = chunked_prime_ssd_core(tq, tk, tv, state=tuple(ts), decay=to_dev(lam), return_state=True)
+    loss = (y * to_dev(dy)).sum() + sum((a * to_dev(b).reshape(a.shape)).sum() for a, b in zip(st, ds))
+    loss.backward()
+    torch.cuda.synchronize()
+    for name, t, r in (("dq", tq, ref[0]), ("dk", tk, ref[1]), ("dv", tv, ref[2])):
+        assert_close(to_np(t.grad).reshape(BH, L, D), r, TOL_BF16, name)
+    assert_state_close(tuple(to_np(t.grad) for t in ts), ref[3], TOL_BF16, "dstate_in")
+
+
+def _module_reference(mod, x, L):
+    """float64 CPU composition of PrimeMomentAttention.forward (attention.py:77-210,
+    no state: the dense and chunked branches compute the same recurrence)."""
+    m = {n: p.detach().double().cpu().requires_grad_(True) for n, p in mod.named_parameters()}
+    xd = x.detach().double().cpu().requires_grad_(True)
+    B = x.shape[0]
+    H, Hk = mod.num_heads, mod.num_kv_heads
+    q = (xd @ m["q_proj.weight"].t()).view(B, L, H, D).transpose(1, 2)
+    k = (xd @ m["k_proj.weight"].t()).view(B, L, Hk, D).transpose(1, 2)
+    v = (xd @ m["v_proj.weight"].t()).view(B, L, Hk, D).transpose(1, 2)
+    if H != Hk:
+        k, v = k.repeat_interleave(H // Hk, 1), v.repeat_interleave(H // Hk, 1)
+    if mod.use_qk_norm:
+        q = torch.nn.functional.layer_norm(q, (D,), m["q_norm.weight"], m["q_norm.bias"], 1e-5)
+        k = torch.nn.functional.layer_norm(k, (D,), m["k_norm.weight"], m["k_norm.bias"], 1e-5)
+    q = q / 8.0
+    idx = torch.arange(L, dtype=torch.float64)
+    diff = idx.view(L, 1) - idx.view(1, L)
+    dm = torch.where(diff >= 0, mod.decay ** diff.clamp(min=0), torch.zeros(()))
+    A = dm * (1.0 + q @ k.transpose(-1, -2) + 0.5 * (q * q) @ (k * k).transpose(-1, -2))
+    y = (A @ v) / A.sum(-1, keepdim=True).clamp(min=mod.eps)
+    out = y.transpose(1, 2).reshape(B, L, H * D) @ m["o_proj.weight"].t()
+    return out, xd, m
+
+
+@pytest.mark.parametrize("L,Hkv", [(200, 2), (600, 2), (130, 1)])
+def test_module_gradients_match_float64_composition(L, Hkv):
+    """PrimeMomentAttention trained through (out.sum()-style loss, as
+    tests/test_attention.py:50-62): x and every weight gradient against the
+    float64 composition of the reference formula."""
+    from prime_moment_attention import PrimeMomentAttention
+    torch.manual_seed(460)
+    mod = PrimeMomentAttention(hidden_size=128, num_heads=2, head_dim=D, num_kv_heads=Hkv, decay=0.999,
+                               use_qk_norm=True).to(dev())
+    with torch.no_grad():
+        for ln in (mod.q_norm, mod.k_norm):
+            ln.weight.uniform_(0.5, 1.5)
+            ln.bias.uniform_(-0.2, 0.2)
+    x = torch.randn(2, L, 128, device=dev()).requires_grad_(True)
+    out, _ = mod(x)
+    g = torch.randn_like(out)
+    (out * g).sum().backward()
+    ref_out, xd, m = _module_reference(mod, x, L)
+    (ref_out * g.double().cpu()).sum().backward()
+    torch.cuda.synchronize()
+    assert_close(to_np(out), ref_out.detach().numpy(), TOL_BF16, "out")
+    assert_close(to_np(x.grad), xd.grad.numpy(), TOL_BF16, "x.grad")
+    for n, p in mod.named_parameters():
+        assert p.grad is not None and torch.isfinite(p.grad).all(), n
+        assert_close(to_np(p.grad), m[n].grad.numpy(), TOL_BF16, n + ".grad")
+
+
+def test_module_state_gradient_flows_through_steps():
+    """A prefill followed by two L == 1 steps with the state carried, all
+    under autograd: gradients reach x of every call and equal those of one
+    prefill over the concatenated input."""
+    from prime_moment_attention import PrimeMomentAttention
+    torch.manual_seed(470)
+    mod = PrimeMomentAttention(hidden_size=128, num_heads=2, head_dim=D, decay=0.995, use_qk_norm=True,
+                               chunk_threshold=16).to(dev())
+    x = torch.randn(1, 40, 128, device=dev())
+    x1, x2, x3 = (t.clone().requires_grad_(True) for t in (x[:, :38], x[:, 38:39], x[:, 39:]))
+    o1, s = mod(x1, return_state=True)
+    o2, s = mod(x2, state=s, return_state=True)
+    o3, _ = mod(x3, state=s)
+    g = torch.randn(1, 40, 128, device=dev())
+    (torch.cat([o1, o2, o3], 1) * g).sum().backward()
+    xa = x.clone().requires_grad_(True)
+    oa, _ = mod(xa)
+    (oa * g).sum().backward()
+    torch.cuda.synchronize()
+    assert_close(to_np(torch.cat([x1.grad, x2.grad, x3.grad], 1)), to_np(xa.grad), TOL_BF16, "x.grad")
+
+
+def test_model_trains():
+    """PrimeForCausalLM (tests/test_model.py:32-43 of the reference): the loss
+    backward gives finite gradients to the embedding, attention and MLP
+    weights, and a few AdamW steps lower the loss on a fixed batch."""
+    from prime_moment_attention import PrimeConfig, PrimeForCausalLM
+    torch.manual_seed(480)
+    cfg = PrimeConfig(vocab_size=100, hidden_size=128, num_layers=2, num_heads=2, head_dim=D, decay=0.999,
+                      use_qk_norm=True)
+    model = PrimeForCausalLM(cfg).to(dev())
+    ids = torch.randint(0, 100, (4, 96), device=dev())
+    opt = torch.optim.AdamW(model.parameters(), lr=3e-3)
+    losses = []
+    for _ in range(8):
+        opt.zero_grad()
+        loss = model(ids, labels=ids)["loss"]
+        loss.backward()
+        losses.append(float(loss.detach()))
+        for n in ("embed_tokens.weight", "layers.0.self_attn.q_proj.weight", "layers.0.mlp.gate_proj.weight"):
+            gr = dict(model.named_parameters())[n].grad
+            assert gr is not None and torch.isfinite(gr).all(), n
+        opt.step()
+    assert losses[-1] < losses[0] - 0.1, losses
+
+
+def test_selective_and_delta_backward_raise():
+    from prime_moment_attention import ChunkedGatedDeltaPrimeAttention, PrimeSelectiveMomentAttention
+    for mod in (PrimeSelectiveMomentAttention(128, 2, D), ChunkedGatedDeltaPrimeAttention(128, 2, D)):
+        mod = mod.to(dev())
+        out, _ = mod(torch.randn(1, 70, 128, device=dev()))
+        with pytest.raises(NotImplementedError, match="no backward"):
+            out.sum().backward()
