@@ -24,6 +24,8 @@ The same JSON line carries
   hybrid        the hybrid window-PRIME pieces: eviction accumulator and
                 fp32-input prefill at the config-2 shape, per-token update and
                 readout at B=256;
+  backward      the prefill backward (dq and dk/dv passes) at the config-2
+                shape and at a training shape, with its roofline;
   delta         the chunked delta-rule prefill at config 5 (B=1, H=12,
                 L=131072): tok/s, per-kernel time, sustained tok/s per 16384
                 tokens and the memory in use (flat state);
@@ -68,6 +70,7 @@ def parse_args():
     ap.add_argument("--no-delta", action="store_true", help="skip the delta-rule (config 5) leg")
     ap.add_argument("--no-selective", action="store_true", help="skip the selective PRIME leg")
     ap.add_argument("--no-hybrid", action="store_true", help="skip the hybrid window-PRIME leg")
+    ap.add_argument("--no-backward", action="store_true", help="skip the prefill-backward leg")
     ap.add_argument("--cpu-budget", type=float, default=8.0, help="seconds per CPU leg (approximate)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device copy 3 times (the reference kernel for "
@@ -477,6 +480,53 @@ def bench_hybrid(args, lib, torch, dev):
     return out
 
 
+BWD_FLOP_PER_TOKEN_HEAD = 2 * 2 * 64 * 64 * 768 // 64  # two passes, 7 GEMM blocks each: 196,608 flop
+
+
+def bench_backward(args, lib, torch, dev):
+    """Backward of the chunked prefill (prime_chunked_prefill_backward): dq pass
+    + dk/dv pass, bf16 q/k/v/dy, fp32 gradients, zero initial state, at the
+    config-2 shape (B=8 x H=12 x L=8192) and at a training shape (B=32 x
+    H=12 x L=2048).  Algorithmic bytes per token-head: q, k, v, dy read by both
+    passes (2 x 512 B), dq, dk, dv written (3 x 256 B fp32), 16 B of per-token
+    denominators; flop per token-head: 196,608 (MFMA blocks of both passes)."""
+    out = {}
+    for (B, H, L) in ((8, 12, 8192), (32, 12, 2048)):
+        gen = torch.Generator(device=dev).manual_seed(args.seed + 17 + B)
+        q, k, v = qkv((B, H, L, D), gen, dev, torch.bfloat16)
+        dy = torch.randn(B, H, L, D, device=dev, generator=gen).to(torch.bfloat16)
+        lam = torch.empty(H, device=dev).uniform_(0.99, 0.9999, generator=gen)
+        g = [torch.empty(B, H, L, D, device=dev) for _ in range(3)]
+        ws = torch.empty(lib.backward_workspace_size(B, H, L), dtype=torch.uint8, device=dev)
+        run = lambda: lib.chunked_prefill_backward(q, k, v, lam, 1.0, None, dy, None, *g, None, workspace=ws)
+        ids = (lib.KERNEL_BWD_DQ, lib.KERNEL_BWD_DKV)
+        for _ in range(5):
+            run()
+        torch.cuda.synchronize()
+        lib.timer_reset()
+        lib.timer_enable(*ids)
+        steps = max(10, args.steps // 50)
+        ms = timed(run, steps, 0)
+        lib.timer_enable()
+        kern = {lib.KERNEL_NAMES[kid]: kernel_ms(lib, kid) for kid in ids}
+        lib.timer_reset()
+        th = B * H * L
+        byts = th * (2 * 512 + 3 * 256 + 16)
+        flops = th * BWD_FLOP_PER_TOKEN_HEAD
+        kt = sum(t for t, _ in kern.values())
+        out[f"B{B}_H{H}_L{L}"] = {
+            "tok_s": B * L / (ms * 1e-3), "ms": ms,
+            "finite": all(bool(torch.isfinite(t).all().item()) for t in g),
+            "kernels": {n: {"avg_us": None if t is None else t * 1e3, "launches": c} for n, (t, c) in kern.items()},
+            "roofline": {"bound": "hbm", "bytes_per_call": byts, "flop_per_call": flops,
+                         "kernels_us": kt * 1e3, "achieved_GBps": byts / (kt * 1e-3) / 1e9,
+                         "hbm_frac": byts / (kt * 1e-3) / PEAK_HBM,
+                         "tflops": flops / (kt * 1e-3) / 1e12, "mfma_frac": flops / (kt * 1e-3) / PEAK_BF16}}
+        del q, k, v, dy, g, ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def bench_delta(args, lib, torch, dev):
     """Chunked gated delta-rule prefill: B=1, H=12, D=64,
     L=131072, chunk 64, bf16 q/k/v (N(0,1), QK-normed, q / 8), beta ~
@@ -717,6 +767,8 @@ def main():
         rec["selective"] = bench_selective(args, lib, torch, dev)
     if not args.no_hybrid:
         rec["hybrid"] = bench_hybrid(args, lib, torch, dev)
+    if not args.no_backward:
+        rec["backward"] = bench_backward(args, lib, torch, dev)
     if not args.no_model:
         rec["model"] = bench_model(args, torch, dev)
         if not args.no_selective:

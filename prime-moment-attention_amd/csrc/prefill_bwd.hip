@@ -46,14 +46,15 @@
 namespace prime {
 namespace {
 
-constexpr int kPV = kD + 16;   // pitch of 80-wide rows ([v | 1 | 0..], [g | gden | 0..])
-constexpr int kPY = kD + 8;    // pitch of the dy tile
+constexpr int kPV = kD + 16;   // pitch of 80-wide rows ([v | 0..], [g | gden | 0..])
 constexpr int kSR = kD + 1;    // rows of a transposed state copy: 64 value columns + the K column
 
 __device__ __forceinline__ void st16(uint16_t *p, u32x4 x) { *reinterpret_cast<u32x4 *>(p) = x; }
 
-// 8 consecutive elements of a row of dtype dt, as fp32
-__device__ __forceinline__ void load8(const void *base, int64_t off, int dt, float (&f)[8]) {
+// 8 consecutive elements of a row of dtype dt, as packed bf16 (round to nearest even)
+__device__ __forceinline__ u32x4 load_packed(const void *base, int64_t off, int dt) {
+    if (dt == PRIME_BF16) return *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(base) + off);
+    float f[8];
     if (dt == PRIME_F32) {
         const f32x4 a = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(base) + off);
         const f32x4 b = *reinterpret_cast<const f32x4 *>(static_cast<const float *>(base) + off + 4);
@@ -64,16 +65,25 @@ __device__ __forceinline__ void load8(const void *base, int64_t off, int dt, flo
         }
     } else {
         const u32x4 r = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(base) + off);
-        if (dt == PRIME_BF16) {
-            unpack8(r, f);
-        } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                f[2 * i] = h16_bits_to_f32(static_cast<uint16_t>(r[i] & 0xFFFFu));
-                f[2 * i + 1] = h16_bits_to_f32(static_cast<uint16_t>(r[i] >> 16));
-            }
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = h16_bits_to_f32(static_cast<uint16_t>(r[i] & 0xFFFFu));
+            f[2 * i + 1] = h16_bits_to_f32(static_cast<uint16_t>(r[i] >> 16));
         }
     }
+    return pack8(f);
+}
+
+__device__ __forceinline__ u32x4 and4(u32x4 x, uint32_t m) { return u32x4{x[0] & m, x[1] & m, x[2] & m, x[3] & m}; }
+
+// s * x * x of 8 packed bf16, repacked
+__device__ __forceinline__ u32x4 sq8(u32x4 x, float s) {
+    float f[8];
+    unpack8(x, f);
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = pack2(s * f[2 * i] * f[2 * i], s * f[2 * i + 1] * f[2 * i + 1]);
+    return r;
 }
 
 // 8 floats times s, packed to bf16
@@ -81,14 +91,6 @@ __device__ __forceinline__ u32x4 pack8s(const float (&f)[8], float s) {
     u32x4 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[i] = pack2(s * f[2 * i], s * f[2 * i + 1]);
-    return r;
-}
-
-// 8 floats squared times s, packed to bf16
-__device__ __forceinline__ u32x4 pack8sq(const float (&f)[8], float s) {
-    u32x4 r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = pack2(s * f[2 * i] * f[2 * i], s * f[2 * i + 1] * f[2 * i + 1]);
     return r;
 }
 
@@ -110,9 +112,42 @@ __device__ __forceinline__ bf16x8 perm_row_op(const uint16_t *row, int ks, int g
     return as_bf16x8(r);
 }
 
+// an operand's 8 bf16 values times per-slot weights, repacked
+__device__ __forceinline__ bf16x8 scale_op(bf16x8 x, const float (&wt)[8]) {
+    const u32x4 r = __builtin_bit_cast(u32x4, x);
+    float f[8];
+    unpack8(r, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] *= wt[i];
+    return as_bf16x8(pack8(f));
+}
+
+// v[r][fb] to base[o[r] + 16 fb + c16] for the rows with ok[r], in dtype dt
+// (one wave-uniform dtype branch around all 16 stores)
+__device__ __forceinline__ void store_rows4(void *base, int dt, const int64_t (&o)[4], const bool (&ok)[4], int c16,
+                                            const float (&v)[4][4]) {
+    if (dt == PRIME_F32) {
+        float *p = static_cast<float *>(base) + c16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (ok[r])
+#pragma unroll
+                for (int fb = 0; fb < 4; ++fb) p[o[r] + 16 * fb] = v[r][fb];
+    } else {
+        uint16_t *p = static_cast<uint16_t *>(base) + c16;
+        const bool bf = dt == PRIME_BF16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (ok[r])
+#pragma unroll
+                for (int fb = 0; fb < 4; ++fb)
+                    p[o[r] + 16 * fb] = bf ? f32_to_bf16_bits(v[r][fb]) : f32_to_h16_bits(v[r][fb]);
+    }
+}
+
 // One chunk's inputs for one thread: rows ra and ra + 32, columns col..col+7.
 struct Rows {
-    float q[2][8], k[2][8], v[2][8], dy[2][8];
+    u32x4 q[2], k[2], v[2], dy[2];  // packed bf16
     float inv[2], gden[2];
 };
 
@@ -121,12 +156,12 @@ __device__ __forceinline__ void load_rows(Rows &R, const BwdArgs &a, int b, int 
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         const int64_t t = min(c * kC + ra + 32 * s, a.L - 1);  // clamped; rows past L are zeroed when stored
-        if (want_q) load8(a.q, b * a.q_sb + h * a.q_sh + t * a.q_sl + col, a.dt_in, R.q[s]);
+        if (want_q) R.q[s] = load_packed(a.q, b * a.q_sb + h * a.q_sh + t * a.q_sl + col, a.dt_in);
         if (want_kv) {
-            load8(a.k, b * a.k_sb + h * a.k_sh + t * a.k_sl + col, a.dt_in, R.k[s]);
-            load8(a.v, b * a.v_sb + h * a.v_sh + t * a.v_sl + col, a.dt_in, R.v[s]);
+            R.k[s] = load_packed(a.k, b * a.k_sb + h * a.k_sh + t * a.k_sl + col, a.dt_in);
+            R.v[s] = load_packed(a.v, b * a.v_sb + h * a.v_sh + t * a.v_sl + col, a.dt_in);
         }
-        load8(a.dy, b * a.dy_sb + h * a.dy_sh + t * a.dy_sl + col, a.dt_dy, R.dy[s]);
+        R.dy[s] = load_packed(a.dy, b * a.dy_sb + h * a.dy_sh + t * a.dy_sl + col, a.dt_dy);
         if (want_g) {
             const size_t o = static_cast<size_t>(b * a.H + h) * a.L + t;
             R.inv[s] = a.inv_den[o];
@@ -135,24 +170,20 @@ __device__ __forceinline__ void load_rows(Rows &R, const BwdArgs &a, int b, int 
     }
 }
 
-__device__ __forceinline__ void zero8(float (&f)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = 0.f;
-}
 
 }  // namespace
 
 // ---------------------------------------------------------------- dq pass
-__global__ __launch_bounds__(256, 1) void prefill_bwd_dq_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t sQf[kC][kPW];   // [q | q*q]
     __shared__ __attribute__((aligned(16))) uint16_t sKf[kC][kPW];   // [k | k*k/2]
-    __shared__ __attribute__((aligned(16))) uint16_t sV[kC][kPV];    // [v | 1 | 0..]
-    __shared__ __attribute__((aligned(16))) uint16_t sVw[kC][kPV];   // [w v | 0..]
-    __shared__ __attribute__((aligned(16))) uint16_t sY[kC][kPY];    // dy
-    __shared__ __attribute__((aligned(16))) uint16_t sG[kC][kPV];    // G value part (dy / d)
+    __shared__ __attribute__((aligned(16))) uint16_t sV[kC][kPV];    // [v | 0..]
+    __shared__ __attribute__((aligned(16))) uint16_t sG[kC][kPV];    // dy, overwritten by the value part of G (dy / d)
     __shared__ __attribute__((aligned(16))) uint16_t sSt[kD][kPW];   // bf16 value columns of M^T entering the chunk
     // fp32: the K column of M (the denominator's moments) entering the chunk, S0, K0
     __shared__ float sKv[kF], sS0[kD], sK0[1], sGd[kC], sPg[kC], sPw[kC + 2], sPs[kC + 2];
+    __shared__ float sRedK[4][kF], sRedS[8][kD];  // partial sums of the K and S0 updates
+    __shared__ __attribute__((aligned(16))) float sWt[kC];  // the chunk's state-update weights l^(n-1-j)
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -180,8 +211,7 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dq_kernel(const BwdArgs a)
     // constant columns of the 80-wide tiles
     for (int idx = tid; idx < kC * 16; idx += 256) {
         const int row = idx >> 4, cc = kD + (idx & 15);
-        sV[row][cc] = cc == kD ? 0x3F80u : 0u;
-        sVw[row][cc] = 0u;
+        sV[row][cc] = 0u;
         sG[row][cc] = 0u;
     }
 
@@ -231,20 +261,14 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dq_kernel(const BwdArgs a)
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const int row = ra + 32 * s;
-            if (row >= nv) {
-                zero8(R.q[s]);
-                zero8(R.k[s]);
-                zero8(R.v[s]);
-                zero8(R.dy[s]);
-            }
-            const float wr = row < nv ? sPw[nv - 1 - row] : 0.f;
-            st16(&sQf[row][col], pack8s(R.q[s], 1.f));
-            st16(&sQf[row][kD + col], pack8sq(R.q[s], 1.f));
-            st16(&sKf[row][col], pack8s(R.k[s], 1.f));
-            st16(&sKf[row][kD + col], pack8sq(R.k[s], 0.5f));
-            st16(&sV[row][col], pack8s(R.v[s], 1.f));
-            st16(&sVw[row][col], pack8s(R.v[s], wr));
-            st16(&sY[row][col], pack8s(R.dy[s], 1.f));
+            const uint32_t m = row < nv ? 0xFFFFFFFFu : 0u;
+            const u32x4 q = and4(R.q[s], m), k = and4(R.k[s], m);
+            st16(&sQf[row][col], q);
+            st16(&sQf[row][kD + col], sq8(q, 1.f));
+            st16(&sKf[row][col], k);
+            st16(&sKf[row][kD + col], sq8(k, 0.5f));
+            st16(&sV[row][col], and4(R.v[s], m));
+            st16(&sG[row][col], and4(R.dy[s], m));
         }
     };
 
@@ -257,6 +281,7 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dq_kernel(const BwdArgs a)
     for (int c = 0; c < NC; ++c) {
         const int nvalid = min(kC, a.L - c * kC);
         __syncthreads();  // tiles of chunk c and M_c in LDS
+        if (tid < kC) sWt[tid] = tid < nvalid ? sPw[nvalid - 1 - tid] : 0.f;  // read after the next barrier
         // ---- scores S^T[j][iw] (blocks jb <= w), masked: A = l^(i-j) (1 + phi_q . phi_k)
         f32x4 sT[4];
 #pragma unroll
@@ -325,7 +350,7 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dq_kernel(const BwdArgs a)
             float part = 0.f, gn[4];
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb) {
-                const float dyv = bf16_bits_to_f32(sY[i][16 * nb + c16]);
+                const float dyv = bf16_bits_to_f32(sG[i][16 * nb + c16]);  // read, then overwritten by this lane
                 part += dyv * (acc[nb][r] * inv);
                 gn[nb] = valid ? dyv * inv : 0.f;
             }
@@ -391,19 +416,23 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dq_kernel(const BwdArgs a)
             for (int r = 0; r < 4; ++r) dphi[fb][r] += sPg[16 * w + 4 * g + r] * kf;
         }
         // ---- dq = dphi[q] + 2 q dphi[q*q]
+        {
+            int64_t o[4];
+            bool ok[4];
+            float dv[4][4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = 16 * w + 4 * g + r;
-            if (i >= nvalid) continue;
-            const int64_t o = b * a.g_sb + h * a.g_sh + static_cast<int64_t>(c * kC + i) * a.g_sl;
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * w + 4 * g + r;
+                ok[r] = i < nvalid;
+                o[r] = b * a.g_sb + h * a.g_sh + static_cast<int64_t>(c * kC + i) * a.g_sl;
 #pragma unroll
-            for (int fb = 0; fb < 4; ++fb) {
-                const int cc = 16 * fb + c16;
-                const float qv = bf16_bits_to_f32(sQf[i][cc]);
-                store_elem(a.dq, o + cc, a.dt_g, dphi[fb][r] + 2.0f * qv * dphi[fb + 4][r]);
+                for (int fb = 0; fb < 4; ++fb)
+                    dv[r][fb] = dphi[fb][r] + 2.0f * bf16_bits_to_f32(sQf[i][16 * fb + c16]) * dphi[fb + 4][r];
             }
+            store_rows4(a.dq, a.dt_g, o, ok, c16, dv);
         }
-        // ---- M <- l^n M + phi_k^T (w v), S0 and K0 likewise, K = [K1; K2/2] in fp32
+        // ---- M <- l^n M + (w phi_k)^T v with w_j = l^(n-1-j) on the A operand's
+        // token slots; S0 and K = [K1; K2/2] (fp32) as partial sums over all threads
         const float ln = sPw[nvalid];
 #pragma unroll
         for (int fi = 0; fi < 2; ++fi)
@@ -413,38 +442,70 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dq_kernel(const BwdArgs a)
                 for (int r = 0; r < 4; ++r) st[fi][nb][r] *= ln;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
+            float wt[8];
+            {
+                const f32x4 w0 = *reinterpret_cast<const f32x4 *>(&sWt[32 * ks + 4 * g]);
+                const f32x4 w1 = *reinterpret_cast<const f32x4 *>(&sWt[32 * ks + 16 + 4 * g]);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    wt[t] = w0[t];
+                    wt[4 + t] = w1[t];
+                }
+            }
             bf16x8 ak[2];
 #pragma unroll
             for (int fi = 0; fi < 2; ++fi) {
                 const uint16_t *p0 = &sKf[32 * ks + 4 * g + tr_r][16 * (2 * w + fi) + tr_c];
-                ak[fi] = tr_op<false>(p0, p0 + 16 * kPW, 0).h;
+                ak[fi] = scale_op(tr_op<false>(p0, p0 + 16 * kPW, 0).h, wt);
             }
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb) {
-                const uint16_t *p0 = &sVw[32 * ks + 4 * g + tr_r][16 * nb + tr_c];
+                const uint16_t *p0 = &sV[32 * ks + 4 * g + tr_r][16 * nb + tr_c];
                 const bf16x8 vb = tr_op<false>(p0, p0 + 16 * kPV, 0).h;
 #pragma unroll
                 for (int fi = 0; fi < 2; ++fi) st[fi][nb] = mfma(ak[fi], vb, st[fi][nb]);
             }
         }
-        if (tid < kF) {
-            // K[f] <- l^n K[f] + sum_j l^(n-1-j) phi_k(j)[f], phi_k from the bf16 k
-            float s = 0.f;
-            for (int j = 0; j < nvalid; ++j) {
-                const float x = bf16_bits_to_f32(sKf[j][tid & (kD - 1)]);
-                s += sPw[nvalid - 1 - j] * (tid < kD ? x : 0.5f * x * x);
+        {
+            // K[f]: sum_j w_j phi_k(j)[f] (phi_k from the bf16 k): feature pairs x token quarters
+            const int f0 = 2 * (tid & 63), j0 = 16 * (tid >> 6);
+            const bool sq = f0 >= kD;
+            float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+            for (int j = j0; j < j0 + 16; ++j) {
+                const uint32_t u = *reinterpret_cast<const uint32_t *>(&sKf[j][f0 & (kD - 1)]);
+                float x0 = __uint_as_float(u << 16), x1 = __uint_as_float(u & 0xFFFF0000u);
+                if (sq) {
+                    x0 = 0.5f * x0 * x0;
+                    x1 = 0.5f * x1 * x1;
+                }
+                const float wj = sWt[j];
+                s0 += wj * x0;
+                s1 += wj * x1;
             }
-            kv = ln * kv + s;
+            *reinterpret_cast<f32x2 *>(&sRedK[tid >> 6][f0]) = f32x2{s0, s1};
+            // S0[n]: sum_j w_j v_j[n]: column pairs x eighths of the tokens
+            const int n0 = 2 * (tid & 31), i0 = 8 * (tid >> 5);
+            float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+            for (int j = i0; j < i0 + 8; ++j) {
+                const uint32_t u = *reinterpret_cast<const uint32_t *>(&sV[j][n0]);
+                const float wj = sWt[j];
+                v0 += wj * __uint_as_float(u << 16);
+                v1 += wj * __uint_as_float(u & 0xFFFF0000u);
+            }
+            *reinterpret_cast<f32x2 *>(&sRedS[tid >> 5][n0]) = f32x2{v0, v1};
         }
-        if (tid < kD) {
-            float s = 0.f;
-            for (int j = 0; j < kC; ++j) s += bf16_bits_to_f32(sVw[j][tid]);
-            sS0[tid] = ln * sS0[tid] + s;
-        } else if (tid == kD) {
-            sK0[0] = ln * sK0[0] + sPs[nvalid];
-        }
-        __syncthreads();  // every read of chunk c's tiles and of M_c is done
+        __syncthreads();  // every read of chunk c's tiles and of M_c is done; partial sums in LDS
         if (c + 1 < NC) {
+            if (tid < kF) kv = ln * kv + ((sRedK[0][tid] + sRedK[1][tid]) + (sRedK[2][tid] + sRedK[3][tid]));
+            if (tid < kD) {
+                float t8 = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) t8 += sRedS[e][tid];
+                sS0[tid] = ln * sS0[tid] + t8;
+            }
+            if (tid == kF) sK0[0] = ln * sK0[0] + sPs[nvalid];
             publish();
             store_rows(c + 1);
             if (c + 2 < NC) load_rows(R, a, b, h, c + 2, ra, col, true, true, false);
@@ -453,14 +514,14 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dq_kernel(const BwdArgs a)
 }
 
 // ---------------------------------------------------------------- dk, dv pass
-__global__ __launch_bounds__(256, 1) void prefill_bwd_dkv_kernel(const BwdArgs a) {
+__global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t sQf[kC][kPW];   // [q | q*q]
     __shared__ __attribute__((aligned(16))) uint16_t sKf[kC][kPW];   // [k | k*k/2]
     __shared__ __attribute__((aligned(16))) uint16_t sV[kC][kPV];    // [v | 0..]
     __shared__ __attribute__((aligned(16))) uint16_t sG[kC][kPV];    // [dy / d | gden | 0..]
-    __shared__ __attribute__((aligned(16))) uint16_t sGw[kC][kPV];   // l^(t+1) [dy / d | gden | 0..]
     __shared__ __attribute__((aligned(16))) uint16_t sW[kSR][kPW];   // bf16 W^T at the chunk end
     __shared__ float sW1[kSR], sGd[kC], sPw[kC + 2];
+    __shared__ float sRed[8][kD], sRedG[1];  // partial sums of the W1 update
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -478,7 +539,6 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dkv_kernel(const BwdArgs a
         const int row = idx >> 4, cc = kD + (idx & 15);
         sV[row][cc] = 0u;
         sG[row][cc] = 0u;
-        sGw[row][cc] = 0u;
     }
 
     // this lane's key row jw of the transposed blocks; rows 16w + 4g + r of the outputs
@@ -530,28 +590,21 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dkv_kernel(const BwdArgs a
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const int row = ra + 32 * s;
-            float gn[8];
             const bool ok = row < nv;
+            const uint32_t m = ok ? 0xFFFFFFFFu : 0u;
             const float inv = ok ? R.inv[s] : 0.f, gd = ok ? R.gden[s] : 0.f;
-            if (!ok) {
-                zero8(R.q[s]);
-                zero8(R.k[s]);
-                zero8(R.v[s]);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) gn[e] = R.dy[s][e] * inv;
-            const float om = sPw[row + 1];  // l^(t - c0 + 1)
-            st16(&sQf[row][col], pack8s(R.q[s], 1.f));
-            st16(&sQf[row][kD + col], pack8sq(R.q[s], 1.f));
-            st16(&sKf[row][col], pack8s(R.k[s], 1.f));
-            st16(&sKf[row][kD + col], pack8sq(R.k[s], 0.5f));
-            st16(&sV[row][col], pack8s(R.v[s], 1.f));
-            st16(&sG[row][col], pack8s(gn, 1.f));
-            st16(&sGw[row][col], pack8s(gn, om));
+            float gn[8];
+            unpack8(R.dy[s], gn);
+            const u32x4 q = and4(R.q[s], m), k = and4(R.k[s], m);
+            st16(&sQf[row][col], q);
+            st16(&sQf[row][kD + col], sq8(q, 1.f));
+            st16(&sKf[row][col], k);
+            st16(&sKf[row][kD + col], sq8(k, 0.5f));
+            st16(&sV[row][col], and4(R.v[s], m));
+            st16(&sG[row][col], pack8s(gn, inv));
             if (col == 0) {
                 sGd[row] = gd;
                 sG[row][kD] = f32_to_bf16_bits(gd);
-                sGw[row][kD] = f32_to_bf16_bits(om * gd);
             }
         }
     };
@@ -616,16 +669,21 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dkv_kernel(const BwdArgs a
             for (int nb = 0; nb < 4; ++nb)
                 dvv[nb] = mfma(A, as_bf16x8(lds128(&sW[16 * nb + c16][32 * ks + 8 * g])), dvv[nb]);
         }
+        int64_t orow[4];
+        bool okr[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int j = 16 * w + 4 * g + r;
-            if (j >= nvalid) continue;
-            const int64_t o = b * a.g_sb + h * a.g_sh + static_cast<int64_t>(c * kC + j) * a.g_sl;
+            okr[r] = j < nvalid;
+            orow[r] = b * a.g_sb + h * a.g_sh + static_cast<int64_t>(c * kC + j) * a.g_sl;
+        }
+        {
+            float dv[4][4];
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb) {
-                const int n = 16 * nb + c16;
-                store_elem(a.dv, o + n, a.dt_g, dvv[nb][r] + tjr[r] * sW1[n]);
-            }
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) dv[r][nb] = dvv[nb][r] + tjr[r] * sW1[16 * nb + c16];
+            store_rows4(a.dv, a.dt_g, orow, okr, c16, dv);
         }
         // ---- dphi_k rows 16w + 4g + r: P^T phi_q + tail (W V')
         f32x4 dphi[8];
@@ -657,19 +715,18 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dkv_kernel(const BwdArgs a
             for (int r = 0; r < 4; ++r) dphi[fb][r] += tjr[r] * wk;
         }
         // ---- dk = dphi[k] + k dphi[k*k/2]
+        {
+            float dv[4][4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int j = 16 * w + 4 * g + r;
-            if (j >= nvalid) continue;
-            const int64_t o = b * a.g_sb + h * a.g_sh + static_cast<int64_t>(c * kC + j) * a.g_sl;
+            for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int fb = 0; fb < 4; ++fb) {
-                const int cc = 16 * fb + c16;
-                const float kv = bf16_bits_to_f32(sKf[j][cc]);
-                store_elem(a.dk, o + cc, a.dt_g, dphi[fb][r] + kv * dphi[fb + 4][r]);
-            }
+                for (int fb = 0; fb < 4; ++fb)
+                    dv[r][fb] = dphi[fb][r] +
+                                bf16_bits_to_f32(sKf[16 * w + 4 * g + r][16 * fb + c16]) * dphi[fb + 4][r];
+            store_rows4(a.dk, a.dt_g, orow, okr, c16, dv);
         }
-        // ---- W <- l^n W + phi_q^T (l^(t+1) G);  W1 likewise
+        // ---- W <- l^n W + (om phi_q)^T G with om_t = l^(t-c0+1) on the A operand's
+        // token slots; W1 likewise from partial sums over all threads
         const float ln = sPw[nvalid];
 #pragma unroll
         for (int fi = 0; fi < 2; ++fi)
@@ -679,26 +736,49 @@ __global__ __launch_bounds__(256, 1) void prefill_bwd_dkv_kernel(const BwdArgs a
                 for (int r = 0; r < 4; ++r) st[fi][nb][r] *= ln;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
+            float om[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) om[t] = sPw[32 * ks + 16 * (t >> 2) + 4 * g + (t & 3) + 1];
             bf16x8 aq[2];
 #pragma unroll
             for (int fi = 0; fi < 2; ++fi) {
                 const uint16_t *p0 = &sQf[32 * ks + 4 * g + tr_r][16 * (2 * w + fi) + tr_c];
-                aq[fi] = tr_op<false>(p0, p0 + 16 * kPW, 0).h;
+                aq[fi] = scale_op(tr_op<false>(p0, p0 + 16 * kPW, 0).h, om);
             }
 #pragma unroll
             for (int nb = 0; nb < 5; ++nb) {
-                const uint16_t *p0 = &sGw[32 * ks + 4 * g + tr_r][16 * nb + tr_c];
+                const uint16_t *p0 = &sG[32 * ks + 4 * g + tr_r][16 * nb + tr_c];
                 const bf16x8 gb = tr_op<false>(p0, p0 + 16 * kPV, 0).h;
 #pragma unroll
                 for (int fi = 0; fi < 2; ++fi) st[fi][nb] = mfma(aq[fi], gb, st[fi][nb]);
             }
         }
-        if (tid <= kD) {
-            float s = 0.f;
-            for (int i = 0; i < kC; ++i) s += bf16_bits_to_f32(sGw[i][tid]);
-            w1 = ln * w1 + s;
+        {
+            // W1[n] = sum_t om_t G_t[n]: column pairs x eighths of the tokens; the gden column on wave 0
+            const int n0 = 2 * (tid & 31), i0 = 8 * (tid >> 5);
+            float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+            for (int i = i0; i < i0 + 8; ++i) {
+                const uint32_t u = *reinterpret_cast<const uint32_t *>(&sG[i][n0]);
+                const float om = sPw[i + 1];
+                s0 += om * __uint_as_float(u << 16);
+                s1 += om * __uint_as_float(u & 0xFFFF0000u);
+            }
+            *reinterpret_cast<f32x2 *>(&sRed[tid >> 5][n0]) = f32x2{s0, s1};
+            if (w == 0) {
+                const float gs = wave_sum(sPw[lane + 1] * sGd[lane]);
+                if (lane == 0) sRedG[0] = gs;
+            }
         }
-        __syncthreads();  // every read of chunk c's tiles and of W is done
+        __syncthreads();  // every read of chunk c's tiles and of W is done; partial sums in LDS
+        if (tid < kD) {
+            float t8 = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) t8 += sRed[e][tid];
+            w1 = ln * w1 + t8;
+        } else if (tid == kD) {
+            w1 = ln * w1 + sRedG[0];
+        }
         if (c > 0) {
             publish();
             store_rows(c - 1);
