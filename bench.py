@@ -499,7 +499,8 @@ def bench_backward(args, lib, torch, dev):
         g = [torch.empty(B, H, L, D, device=dev) for _ in range(3)]
         ws = torch.empty(lib.backward_workspace_size(B, H, L), dtype=torch.uint8, device=dev)
         run = lambda: lib.chunked_prefill_backward(q, k, v, lam, 1.0, None, dy, None, *g, None, workspace=ws)
-        ids = (lib.KERNEL_BWD_DQ, lib.KERNEL_BWD_DKV)
+        ids = (lib.KERNEL_PREFILL_SEGMENTS, lib.KERNEL_SEGMENT_SCAN, lib.KERNEL_BWD_DQ, lib.KERNEL_BWD_DUAL,
+               lib.KERNEL_BWD_DUAL_SCAN, lib.KERNEL_BWD_DKV)
         for _ in range(5):
             run()
         torch.cuda.synchronize()
@@ -513,6 +514,7 @@ def bench_backward(args, lib, torch, dev):
         th = B * H * L
         byts = th * (2 * 512 + 3 * 256 + 16)
         flops = th * BWD_FLOP_PER_TOKEN_HEAD
+        kern = {n: v for n, v in kern.items() if v[1]}  # the segment kernels run only for few long sequences
         kt = sum(t for t, _ in kern.values())
         out[f"B{B}_H{H}_L{L}"] = {
             "tok_s": B * L / (ms * 1e-3), "ms": ms,

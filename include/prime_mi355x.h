@@ -321,8 +321,11 @@ size_t prime_accumulate_workspace_size(int B, int H, int L);
  * expands grouped k/v before the recurrence, attention.py:92-94).  With
  * PRIME_FLAG_DENSE_CLAMP an incoming state is rejected; without one the two
  * clamps are the same.  MFMA operands are bf16 (fp32 accumulation) for bf16
- * and fp32 inputs alike.  workspace: at least
- * prime_chunked_prefill_backward_workspace_size() bytes, 4-byte aligned.
+ * and fp32 inputs alike.  workspace (16-byte aligned): at least B*H*L*8 bytes
+ * (per-token denominators); with prime_chunked_prefill_backward_workspace_size()
+ * bytes, few long sequences are split into segments that run in parallel
+ * (segment-entry states by the forward's state-only pass, dual states by a
+ * reverse scan).  Results agree either way.
  */
 int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
                                    int B, int H, int H_kv, int L, int D, const float *decay, float eps,
@@ -372,7 +375,9 @@ int prime_decode_update(const prime_tensor_t *k, const prime_tensor_t *v, int B,
 #define PRIME_KERNEL_DELTA_STEP       6 /* delta rule: decode step */
 #define PRIME_KERNEL_BWD_DQ           7 /* prefill backward: dq pass (chunks in order) */
 #define PRIME_KERNEL_BWD_DKV          8 /* prefill backward: dk, dv pass (chunks in reverse) */
-#define PRIME_KERNEL_COUNT            9
+#define PRIME_KERNEL_BWD_DUAL         9 /* prefill backward: per-segment dual contributions */
+#define PRIME_KERNEL_BWD_DUAL_SCAN   10 /* prefill backward: reverse scan over segments */
+#define PRIME_KERNEL_COUNT           11
 
 int prime_timer_enable(unsigned mask);
 int prime_timer_reset(void);

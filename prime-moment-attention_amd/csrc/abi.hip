@@ -379,9 +379,19 @@ int prime_accumulate(const prime_tensor_t *k, const prime_tensor_t *v, int B, in
     return check_hip(prime::launch_prefill(a, static_cast<hipStream_t>(stream)), "accumulate launch");
 }
 
+namespace {
+// per-token denominators, rounded up to a slot boundary
+size_t bwd_token_bytes(int B, int H, int L) {
+    return (static_cast<size_t>(B) * H * L * 2 * sizeof(float) + 255) & ~static_cast<size_t>(255);
+}
+}  // namespace
+
 size_t prime_chunked_prefill_backward_workspace_size(int B, int H, int L) {
     if (B <= 0 || H <= 0 || L <= 0) return 0;
-    return static_cast<size_t>(B) * H * L * 2 * sizeof(float);
+    int G, cps;
+    prime::plan_backward_segments(B * H, L, &G, &cps);
+    const size_t slots = G > 1 ? static_cast<size_t>(B) * H * G * prime::kWsStride * sizeof(float) : 0;
+    return bwd_token_bytes(B, H, L) + slots;
 }
 
 int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
@@ -412,9 +422,9 @@ int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t
         return fail(PRIME_ERR_INVALID_ARG, "dq, dk and dv must share dtype and strides");
     if (!rows_aligned(q, true) || !rows_aligned(k, true) || !rows_aligned(v, true) || !rows_aligned(dy, true))
         return fail(PRIME_ERR_MISALIGNED, "q/k/v/dy rows must start on 16-byte boundaries");
-    const size_t need = prime_chunked_prefill_backward_workspace_size(B, H, L);
-    if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 3u))
-        return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes (4-byte aligned) is below the %zu needed",
+    const size_t need = bwd_token_bytes(B, H, L);
+    if (workspace_bytes < need || !aligned16(workspace))
+        return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes (16-byte aligned) is below the %zu needed",
                     workspace_bytes, need);
     int rc;
     if ((rc = check_state(state_in, "state_in")) || (rc = check_state(dstate_out, "dstate_out")) ||
@@ -444,6 +454,12 @@ int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t
     }
     a.inv_den = static_cast<float *>(workspace);
     a.g_den = a.inv_den + static_cast<size_t>(B) * H * L;
+    prime::plan_backward_segments(B * H, L, &a.G, &a.cps);
+    if (a.G > 1 && workspace_bytes < prime_chunked_prefill_backward_workspace_size(B, H, L)) {
+        a.G = 1;  // one segment per sequence in the workspace given
+        a.cps = (L + 63) / 64;
+    }
+    a.ws = a.G > 1 ? reinterpret_cast<float *>(static_cast<char *>(workspace) + need) : nullptr;
     return check_hip(prime::launch_prefill_backward(a, static_cast<hipStream_t>(stream)), "backward launch");
 }
 

@@ -194,7 +194,7 @@ __device__ __forceinline__ void store_tiles_fn(const TileRegs<F32IN> &R, int rt,
 // and every workspace slot costs ~4 x 33.8 KB of HBM traffic (~0.03 chunk-steps).
 constexpr int kMinCps = 4;
 
-static int device_cus() {
+int device_cus() {
     static int cached[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
@@ -726,6 +726,7 @@ static hipError_t launch_variant(PrefillArgs a, hipStream_t stream) {
         hipExtLaunchKernelGGL(segment_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
                               tb.start, tb.stop, 0, a);
         if ((e = hipGetLastError()) != hipSuccess) return timer_drop(tb), e;
+        if (a.states_only) return hipSuccess;
     }
     a.nseg_launch = a.G;
     const TimerEvents tc = timer_events(PRIME_KERNEL_PREFILL_CHUNKS);

@@ -189,12 +189,26 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
     const int tr_r = c16 >> 2, tr_c = 4 * (c16 & 3);
-    const int seq = blockIdx.x;
-    if (seq >= a.B * a.H) return;
+    const int unit = blockIdx.x;
+    if (unit >= a.B * a.H * a.G) return;
+    const int seq = unit / a.G, seg = unit - seq * a.G;
     const int b = seq / a.H, h = seq - b * a.H;
     const float lam = a.decay[h];
     const int NC = (a.L + kC - 1) / kC;
-    const size_t so1 = static_cast<size_t>(seq) * kD * kD, so0 = static_cast<size_t>(seq) * kD;
+    const int c_begin = seg * a.cps, c_end = min(c_begin + a.cps, NC);
+    // the state entering the first chunk: state_in, or the segment's slot (same components)
+    const float *S0p, *S1p, *S2p, *K0p, *K1p, *K2p;
+    if (a.G > 1) {
+        const float *slot = a.ws + static_cast<size_t>(unit) * kWsStride;
+        S1p = slot + kWsS1; S2p = slot + kWsS2; S0p = slot + kWsS0;
+        K1p = slot + kWsK1; K2p = slot + kWsK2; K0p = slot + kWsK0;
+    } else if (a.s1i) {
+        S1p = a.s1i + static_cast<size_t>(seq) * kD * kD; S2p = a.s2i + static_cast<size_t>(seq) * kD * kD;
+        S0p = a.s0i + static_cast<size_t>(seq) * kD; K1p = a.k1i + static_cast<size_t>(seq) * kD;
+        K2p = a.k2i + static_cast<size_t>(seq) * kD; K0p = a.k0i + seq;
+    } else {
+        S0p = S1p = S2p = K0p = K1p = K2p = nullptr;
+    }
 
     if (tid < kC + 2) {
         const double ld = static_cast<double>(lam);
@@ -203,11 +217,11 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
         for (int m = 0; m < tid; ++m, pm *= ld) ps += pm;
         sPs[tid] = static_cast<float>(ps);
     }
-    if (tid < kD) sS0[tid] = a.s0i ? a.s0i[so0 + tid] : 0.f;
-    if (tid == 0) sK0[0] = a.s0i ? a.k0i[seq] : 0.f;
+    if (tid < kD) sS0[tid] = S0p ? S0p[tid] : 0.f;
+    if (tid == 0) sK0[0] = K0p ? K0p[0] : 0.f;
     // the denominator's moments [K1; K2/2] in fp32, one feature per thread (tid < 128)
     float kv = 0.f;
-    if (tid < kF && a.s1i) kv = tid < kD ? a.k1i[so0 + tid] : 0.5f * a.k2i[so0 + tid - kD];
+    if (tid < kF && K1p) kv = tid < kD ? K1p[tid] : 0.5f * K2p[tid - kD];
     // constant columns of the 80-wide tiles
     for (int idx = tid; idx < kC * 16; idx += 256) {
         const int row = idx >> 4, cc = kD + (idx & 15);
@@ -241,7 +255,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int f = 16 * (2 * w + fi) + 4 * g + r, fr = f & (kD - 1), n = 16 * nb + c16;
-                const float x = a.s1i ? (f < kD ? a.s1i : a.s2i)[so1 + fr * kD + n] : 0.f;
+                const float x = S1p ? (f < kD ? S1p : S2p)[fr * kD + n] : 0.f;
                 st[fi][nb][r] = f < kD ? x : 0.5f * x;
             }
     auto publish = [&]() {
@@ -273,12 +287,12 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
     };
 
     __syncthreads();  // power tables
-    load_rows(R, a, b, h, 0, ra, col, true, true, false);
-    store_rows(0);
+    load_rows(R, a, b, h, c_begin, ra, col, true, true, false);
+    store_rows(c_begin);
     publish();
-    if (NC > 1) load_rows(R, a, b, h, 1, ra, col, true, true, false);
+    if (c_begin + 1 < c_end) load_rows(R, a, b, h, c_begin + 1, ra, col, true, true, false);
 
-    for (int c = 0; c < NC; ++c) {
+    for (int c = c_begin; c < c_end; ++c) {
         const int nvalid = min(kC, a.L - c * kC);
         __syncthreads();  // tiles of chunk c and M_c in LDS
         if (tid < kC) sWt[tid] = tid < nvalid ? sPw[nvalid - 1 - tid] : 0.f;  // read after the next barrier
@@ -497,7 +511,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             *reinterpret_cast<f32x2 *>(&sRedS[tid >> 5][n0]) = f32x2{v0, v1};
         }
         __syncthreads();  // every read of chunk c's tiles and of M_c is done; partial sums in LDS
-        if (c + 1 < NC) {
+        if (c + 1 < c_end) {
             if (tid < kF) kv = ln * kv + ((sRedK[0][tid] + sRedK[1][tid]) + (sRedK[2][tid] + sRedK[3][tid]));
             if (tid < kD) {
                 float t8 = 0.f;
@@ -508,12 +522,15 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             if (tid == kF) sK0[0] = ln * sK0[0] + sPs[nvalid];
             publish();
             store_rows(c + 1);
-            if (c + 2 < NC) load_rows(R, a, b, h, c + 2, ra, col, true, true, false);
+            if (c + 2 < c_end) load_rows(R, a, b, h, c + 2, ra, col, true, true, false);
         }
     }
 }
 
 // ---------------------------------------------------------------- dk, dv pass
+// DUAL: the dual-state pass of a segment only -- from zero, no dk / dv, the
+// segment's contribution sum_t l^(t-s0+1) phi_q(t) G_t^T written to its slot.
+template <bool DUAL>
 __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t sQf[kC][kPW];   // [q | q*q]
     __shared__ __attribute__((aligned(16))) uint16_t sKf[kC][kPW];   // [k | k*k/2]
@@ -527,12 +544,15 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
     const int tr_r = c16 >> 2, tr_c = 4 * (c16 & 3);
-    const int seq = blockIdx.x;
-    if (seq >= a.B * a.H) return;
+    const int unit = blockIdx.x;
+    if (unit >= a.B * a.H * a.G) return;
+    const int seq = unit / a.G, seg = unit - seq * a.G;
     const int b = seq / a.H, h = seq - b * a.H;
     const float lam = a.decay[h];
     const int NC = (a.L + kC - 1) / kC;
+    const int c_begin = seg * a.cps, c_end = min(c_begin + a.cps, NC);
     const size_t so1 = static_cast<size_t>(seq) * kD * kD, so0 = static_cast<size_t>(seq) * kD;
+    float *slot = a.G > 1 ? a.ws + static_cast<size_t>(unit) * kWsStride : nullptr;
 
     if (tid < kC + 2) sPw[tid] = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(tid)));
     for (int idx = tid; idx < kC * 16; idx += 256) {
@@ -562,14 +582,22 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
             for (int r = 0; r < 4; ++r) {
                 const int f = 16 * (2 * w + fi) + 4 * g + r, fr = f & (kD - 1), n = 16 * nb + c16;
                 float x = 0.f;
-                if (a.ds1o) {
+                if (DUAL) {
+                } else if (slot) {  // W at the segment end, in this kernel's convention
+                    if (n < kD) x = slot[(f < kD ? kWsS1 : kWsS2) + fr * kD + n];
+                    else if (n == kD) x = slot[(f < kD ? kWsK1 : kWsK2) + fr];
+                } else if (a.ds1o) {
                     if (n < kD) x = (f < kD ? a.ds1o : a.ds2o)[so1 + fr * kD + n];
                     else if (n == kD) x = (f < kD ? a.dk1o : a.dk2o)[so0 + fr];
+                    if (f >= kD) x *= 2.0f;  // rows 64.. of M hold S2/2 and K2/2
                 }
-                st[fi][nb][r] = f < kD ? x : 2.0f * x;  // rows 64.. of M hold S2/2 and K2/2
+                st[fi][nb][r] = x;
             }
     float w1 = 0.f;  // constant row of W, column tid (tid <= 64)
-    if (a.ds1o && tid <= kD) w1 = tid < kD ? a.ds0o[so0 + tid] : a.dk0o[seq];
+    if (!DUAL && tid <= kD) {
+        if (slot) w1 = slot[tid < kD ? kWsS0 + tid : kWsK0];
+        else if (a.ds1o) w1 = tid < kD ? a.ds0o[so0 + tid] : a.dk0o[seq];
+    }
     auto publish = [&]() {
 #pragma unroll
         for (int fi = 0; fi < 2; ++fi)
@@ -595,12 +623,15 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
             const float inv = ok ? R.inv[s] : 0.f, gd = ok ? R.gden[s] : 0.f;
             float gn[8];
             unpack8(R.dy[s], gn);
-            const u32x4 q = and4(R.q[s], m), k = and4(R.k[s], m);
+            const u32x4 q = and4(R.q[s], m);
             st16(&sQf[row][col], q);
             st16(&sQf[row][kD + col], sq8(q, 1.f));
-            st16(&sKf[row][col], k);
-            st16(&sKf[row][kD + col], sq8(k, 0.5f));
-            st16(&sV[row][col], and4(R.v[s], m));
+            if constexpr (!DUAL) {
+                const u32x4 k = and4(R.k[s], m);
+                st16(&sKf[row][col], k);
+                st16(&sKf[row][kD + col], sq8(k, 0.5f));
+                st16(&sV[row][col], and4(R.v[s], m));
+            }
             st16(&sG[row][col], pack8s(gn, inv));
             if (col == 0) {
                 sGd[row] = gd;
@@ -610,14 +641,15 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
     };
 
     __syncthreads();  // power table
-    load_rows(R, a, b, h, NC - 1, ra, col, true, true, true);
-    store_rows(NC - 1);
+    load_rows(R, a, b, h, c_end - 1, ra, col, true, !DUAL, true);
+    store_rows(c_end - 1);
     publish();
-    if (NC > 1) load_rows(R, a, b, h, NC - 2, ra, col, true, true, true);
+    if (c_end - 2 >= c_begin) load_rows(R, a, b, h, c_end - 2, ra, col, true, !DUAL, true);
 
-    for (int c = NC - 1; c >= 0; --c) {
+    for (int c = c_end - 1; c >= c_begin; --c) {
         const int nvalid = min(kC, a.L - c * kC);
         __syncthreads();  // tiles of chunk c and W at its end in LDS
+        if constexpr (!DUAL) {
         // ---- A[i][jw] = mask (1 + phi_q(i) . phi_k(jw)) and P[i][jw] = mask (g_i . v_jw + gden_i), i blocks ib >= w
         f32x4 sc[4], pp[4];
 #pragma unroll
@@ -725,6 +757,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
                                 bf16_bits_to_f32(sKf[16 * w + 4 * g + r][16 * fb + c16]) * dphi[fb + 4][r];
             store_rows4(a.dk, a.dt_g, orow, okr, c16, dv);
         }
+        }  // !DUAL
         // ---- W <- l^n W + (om phi_q)^T G with om_t = l^(t-c0+1) on the A operand's
         // token slots; W1 likewise from partial sums over all threads
         const float ln = sPw[nvalid];
@@ -779,14 +812,30 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
         } else if (tid == kD) {
             w1 = ln * w1 + sRedG[0];
         }
-        if (c > 0) {
+        if (c > c_begin) {
             publish();
             store_rows(c - 1);
-            if (c > 1) load_rows(R, a, b, h, c - 2, ra, col, true, true, true);
+            if (c - 2 >= c_begin) load_rows(R, a, b, h, c - 2, ra, col, true, !DUAL, true);
         }
     }
-    // ---- the incoming state's adjoint: W after chunk 0 (S2, K2 rows halved back)
-    if (a.ds1i) {
+    if constexpr (DUAL) {
+        // the segment's contribution, in this kernel's convention
+#pragma unroll
+        for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+            for (int nb = 0; nb < 5; ++nb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int f = 16 * (2 * w + fi) + 4 * g + r, fr = f & (kD - 1), n = 16 * nb + c16;
+                    if (n < kD) slot[(f < kD ? kWsS1 : kWsS2) + fr * kD + n] = st[fi][nb][r];
+                    else if (n == kD) slot[(f < kD ? kWsK1 : kWsK2) + fr] = st[fi][nb][r];
+                }
+        if (tid <= kD) slot[tid < kD ? kWsS0 + tid : kWsK0] = w1;
+        return;
+    }
+    // ---- the incoming state's adjoint: W after chunk 0 (S2, K2 rows halved back);
+    // with segments the dual scan writes it
+    if (a.ds1i && a.G == 1) {
 #pragma unroll
         for (int fi = 0; fi < 2; ++fi)
 #pragma unroll
@@ -803,16 +852,92 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
     }
 }
 
+// Reverse scan over segments, elementwise (one thread per (sequence, state
+// element)): slot s holds segment s's contribution C_s on entry and the dual
+// state at its end on exit: W_end(G-1) = dM_out, W_end(s-1) = l^len(s) W_end(s)
+// + C_s; W_end(-1) is the incoming state's adjoint.
+__global__ __launch_bounds__(256) void bwd_dual_scan_kernel(const BwdArgs a) {
+    const int S = a.B * a.H;
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid >= static_cast<int64_t>(S) * kWsElems) return;
+    const int seq = static_cast<int>(gid / kWsElems), e = static_cast<int>(gid % kWsElems);
+    const int h = seq % a.H;
+    const double ld = static_cast<double>(a.decay[h]);
+    const float lT = static_cast<float>(pow(ld, static_cast<double>(a.cps) * kC));
+    const float lLast = static_cast<float>(pow(ld, static_cast<double>(a.L - (a.G - 1) * a.cps * kC)));
+    const size_t so1 = static_cast<size_t>(seq) * kD * kD, so0 = static_cast<size_t>(seq) * kD;
+    // the element's place in the reference state, and the factor of this kernel's convention
+    const float *src = nullptr;
+    float *dst = nullptr;
+    size_t off = 0;
+    float fac = 1.0f;
+    if (e < kWsS2) { src = a.ds1o; dst = a.ds1i; off = so1 + e; }
+    else if (e < kWsS0) { src = a.ds2o; dst = a.ds2i; off = so1 + e - kWsS2; fac = 2.0f; }
+    else if (e < kWsK1) { src = a.ds0o; dst = a.ds0i; off = so0 + e - kWsS0; }
+    else if (e < kWsK2) { src = a.dk1o; dst = a.dk1i; off = so0 + e - kWsK1; }
+    else if (e < kWsK0) { src = a.dk2o; dst = a.dk2i; off = so0 + e - kWsK2; fac = 2.0f; }
+    else { src = a.dk0o; dst = a.dk0i; off = seq; }
+    float carry = a.ds1o ? fac * src[off] : 0.f;
+    float *slot = a.ws + static_cast<size_t>(seq) * a.G * kWsStride + e;
+    for (int s = a.G - 1; s >= 0; --s) {
+        const float cs = slot[static_cast<size_t>(s) * kWsStride];
+        slot[static_cast<size_t>(s) * kWsStride] = carry;
+        carry = (s == a.G - 1 ? lLast : lT) * carry + cs;
+    }
+    if (a.ds1i) dst[off] = carry / fac;
+}
+
+void plan_backward_segments(int S, int L, int *G, int *cps) {
+    const int NC = (L + kC - 1) / kC;
+    int g = 1;
+    const int cu = device_cus();
+    if (S > 0 && S < 2 * cu) g = min(min(2 * cu / S, NC / 8), 64);
+    if (g < 2) {
+        *G = 1;
+        *cps = NC;
+        return;
+    }
+    const int c = (NC + g - 1) / g;
+    *cps = c;
+    *G = (NC + c - 1) / c;  // no empty segments
+}
+
 hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream) {
     const int S = a.B * a.H;
+    hipError_t e;
+    if (a.G > 1) {
+        // the state entering every segment, by the forward's state-only pass and scan
+        PrefillArgs f{};
+        f.q = a.q; f.k = a.k; f.v = a.v;
+        f.q_sb = a.q_sb; f.q_sh = a.q_sh; f.q_sl = a.q_sl;
+        f.k_sb = a.k_sb; f.k_sh = a.k_sh; f.k_sl = a.k_sl;
+        f.v_sb = a.v_sb; f.v_sh = a.v_sh; f.v_sl = a.v_sl;
+        f.dt_in = a.dt_in; f.B = a.B; f.H = a.H; f.group = 1; f.L = a.L;
+        f.decay = a.decay; f.eps = a.eps;
+        f.s0i = a.s0i; f.s1i = a.s1i; f.s2i = a.s2i; f.k0i = a.k0i; f.k1i = a.k1i; f.k2i = a.k2i;
+        f.G = a.G; f.cps = a.cps; f.ws = a.ws; f.states_only = 1;
+        if ((e = launch_prefill(f, stream)) != hipSuccess) return e;
+    }
+    const int units = S * a.G;
     const TimerEvents t1 = timer_events(PRIME_KERNEL_BWD_DQ);
-    hipExtLaunchKernelGGL(prefill_bwd_dq_kernel, dim3(S), dim3(256), 0, stream, t1.start, t1.stop, 0, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return timer_drop(t1), e;
+    hipExtLaunchKernelGGL(prefill_bwd_dq_kernel, dim3(units), dim3(256), 0, stream, t1.start, t1.stop, 0, a);
+    if ((e = hipGetLastError()) != hipSuccess) return timer_drop(t1), e;
+    if (a.G > 1) {
+        // each segment's dual contribution, then the reverse scan (slots now hold dual states)
+        const TimerEvents td = timer_events(PRIME_KERNEL_BWD_DUAL);
+        hipExtLaunchKernelGGL(prefill_bwd_dkv_kernel<true>, dim3(units), dim3(256), 0, stream, td.start, td.stop, 0,
+                              a);
+        if ((e = hipGetLastError()) != hipSuccess) return timer_drop(td), e;
+        const int64_t n = static_cast<int64_t>(S) * kWsElems;
+        const TimerEvents ts = timer_events(PRIME_KERNEL_BWD_DUAL_SCAN);
+        hipExtLaunchKernelGGL(bwd_dual_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
+                              stream, ts.start, ts.stop, 0, a);
+        if ((e = hipGetLastError()) != hipSuccess) return timer_drop(ts), e;
+    }
     const TimerEvents t2 = timer_events(PRIME_KERNEL_BWD_DKV);
-    hipExtLaunchKernelGGL(prefill_bwd_dkv_kernel, dim3(S), dim3(256), 0, stream, t2.start, t2.stop, 0, a);
-    e = hipGetLastError();
-    if (e != hipSuccess) timer_drop(t2);
+    hipExtLaunchKernelGGL(prefill_bwd_dkv_kernel<false>, dim3(units), dim3(256), 0, stream, t2.start, t2.stop, 0,
+                          a);
+    if ((e = hipGetLastError()) != hipSuccess) timer_drop(t2);
     return e;
 }
 

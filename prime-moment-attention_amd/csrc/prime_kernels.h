@@ -107,6 +107,9 @@ struct PrefillArgs {
     // accumulate only (no q, no y): every segment's contribution from zero,
     // then an inclusive scan that writes the final state
     int accumulate;
+    // segment-entry states only (G > 1): the state-only pass and the
+    // exclusive scan, leaving the state entering segment s in slot s
+    int states_only;
 };
 
 // packed fp32 state slot in the workspace: S1 | S2 | S0 | K1 | K2 | K0
@@ -118,6 +121,10 @@ constexpr int kWsDecay = 8385;   // selective: the segment's log2 decay (not par
 // Backward of the chunked prefill (prefill_bwd.hip): the adjoints of q, k,
 // v and of the incoming state for output adjoints dy (and of the final state).
 struct BwdArgs {
+    // segments per sequence (G > 1: slot s of `ws` holds the state entering
+    // segment s for the dq pass, then the dual state at its end for the dk/dv pass)
+    int G, cps;
+    float *ws;
     const void *q, *k, *v, *dy;
     int64_t q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl, dy_sb, dy_sh, dy_sl;
     int dt_in, dt_dy;  // q/k/v: PRIME_BF16 or PRIME_F32; dy: any
@@ -134,6 +141,10 @@ struct BwdArgs {
 };
 
 hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream);
+// segments per sequence for the backward: enough (sequence, segment) units to
+// fill two workgroups per CU, at least 8 chunks per segment
+void plan_backward_segments(int S, int L, int *G, int *cps);
+int device_cus();  // compute units of the current device (cached)
 
 hipError_t launch_decode_step(const DecodeArgs &a, hipStream_t stream);
 hipError_t launch_prefill(PrefillArgs a, hipStream_t stream);

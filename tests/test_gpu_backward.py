@@ -253,3 +253,40 @@ def test_selective_and_delta_backward_raise():
         out, _ = mod(torch.randn(1, 70, 128, device=dev()))
         with pytest.raises(NotImplementedError, match="no backward"):
             out.sum().backward()
+
+
+@pytest.mark.parametrize("with_state", [False, True])
+def test_backward_segmented_equals_one_segment(with_state):
+    """Few long sequences: the segment-parallel plan (forward state-only pass
+    and scan for the segment-entry states, per-segment dual contributions and
+    a reverse scan) against one segment per sequence (minimum workspace) and
+    the oracle, with a ragged last chunk, an incoming state and a final-state
+    adjoint."""
+    B, H, L = 1, 2, 64 * 37 + 5
+    BH = B * H
+    q, k, v = O.make_inputs((B, H, L, D), seed=490, bf16=True)
+    rng = np.random.default_rng(491)
+    lam = np.array([0.995, 0.9995], np.float32)
+    dy = O.bf16_round(rng.standard_normal((B, H, L, D)).astype(np.float32))
+    st0 = random_state(BH, D, 492) if with_state else None
+    ds = tuple(0.1 * rng.standard_normal(x.shape) for x in O.zero_state(BH, D))
+    full = _lib.backward_workspace_size(B, H, L)
+    small = (BH * L * 8 + 255) // 256 * 256  # per-token denominators only
+    assert full > small, "this shape should split into segments"
+    outs = []
+    for nbytes in (full, small):
+        g = [torch.empty(B, H, L, D, device=dev()) for _ in range(3)]
+        dsi = _lib.new_state(B, H, D, dev()) if with_state else None
+        _lib.chunked_prefill_backward(to_dev(q, torch.bfloat16), to_dev(k, torch.bfloat16), to_dev(v, torch.bfloat16),
+                                      to_dev(lam), 1.0, state_to_dev(st0, B, H, D) if with_state else None,
+                                      to_dev(dy, torch.bfloat16), state_to_dev(ds, B, H, D), *g, dsi,
+                                      workspace=torch.empty(nbytes, dtype=torch.uint8, device=dev()))
+        torch.cuda.synchronize()
+        outs.append(([to_np(t).reshape(BH, L, D) for t in g], state_to_np(dsi, BH, D) if with_state else None))
+    for x, y, n in zip(outs[0][0], outs[1][0], ("dq", "dk", "dv")):
+        assert_close(x, y, 5e-3, n + " segmented vs one segment")
+    if with_state:
+        assert_state_close(outs[0][1], outs[1][1], 5e-3, "dstate_in")
+    ref = O.recurrent_vjp(q.reshape(BH, L, D), k.reshape(BH, L, D), v.reshape(BH, L, D),
+                          np.tile(lam.astype(np.float64), B), dy.reshape(BH, L, D), state=st0, dstate=ds)
+    _check(ref, outs[0][0], outs[0][1])
