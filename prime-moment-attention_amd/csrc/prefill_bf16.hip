@@ -60,19 +60,22 @@ struct Tiles {
 };
 
 // Unconditional loads; rows past L clamp to row L-1 (zeroed when stored).
-template <bool STATE_ONLY, bool SEL>
+// ONE_ROW: the thread owns row ra only (512 update threads).
+template <bool STATE_ONLY, bool SEL, bool ONE_ROW = false>
 __device__ __forceinline__ void load_tiles(Tiles &T, const PrefillArgs &a, const uint16_t *qp, const uint16_t *kp,
                                            const uint16_t *vp, const float *ldp, int c, int ra, int lane) {
     const int64_t ta = min(c * kC + ra, a.L - 1), tb = min(c * kC + ra + 32, a.L - 1);
     if constexpr (SEL) T.ld = ldp[min(c * kC + lane, a.L - 1)];  // scaled and masked when used
     if constexpr (!STATE_ONLY) {
         T.q0 = ld16(qp + ta * a.q_sl);
-        T.q1 = ld16(qp + tb * a.q_sl);
+        if constexpr (!ONE_ROW) T.q1 = ld16(qp + tb * a.q_sl);
     }
     T.k0 = ld16(kp + ta * a.k_sl);
-    T.k1 = ld16(kp + tb * a.k_sl);
     T.v0 = ld16(vp + ta * a.v_sl);
-    T.v1 = ld16(vp + tb * a.v_sl);
+    if constexpr (!ONE_ROW) {
+        T.k1 = ld16(kp + tb * a.k_sl);
+        T.v1 = ld16(vp + tb * a.v_sl);
+    }
 }
 
 // One row segment into the tile buffers: [q | q*q], [k | k*k/2], [v], [w v | w].
@@ -99,10 +102,18 @@ __device__ __forceinline__ void store_row(u32x4 q, u32x4 k, u32x4 v, int row, in
 
 }  // namespace
 
-template <bool STATE_ONLY, bool SEL>
-__global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel(const PrefillArgs a) {
+// Wave layouts of the fused pass: UW8 = 8 update waves (one feature block each,
+// one tile row per thread) instead of 4; RH = 8 readout waves (query block x
+// half of the value columns) instead of 4.
+template <bool STATE_ONLY, bool SEL, bool UW8 = false, bool RH = false>
+__global__ __launch_bounds__(STATE_ONLY ? 256 : 64 * ((RH ? 8 : 4) + (UW8 ? 8 : 4)), 1) void prefill_bf16_kernel(
+    const PrefillArgs a) {
     constexpr int NB = kD / 16;    // value blocks
     constexpr int NBX = NB + 1;    // + the ones / K block
+    constexpr int NRW = STATE_ONLY ? 0 : (RH ? 8 : 4);  // readout waves
+    constexpr int NUW = UW8 ? 8 : 4;                     // update waves
+    constexpr int FI = UW8 ? 1 : 2;                      // feature blocks per update wave
+    constexpr int NVB = RH ? 3 : NBX;                    // value blocks per readout wave (incl. the K block)
     constexpr int QB = STATE_ONLY ? 1 : 2;   // buffers of the readout-only arrays
     constexpr int QR = STATE_ONLY ? 1 : kC;
     constexpr int SR = STATE_ONLY ? 1 : kSR;
@@ -118,6 +129,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
     __shared__ float sK0[QB];                                             // K0 entering the chunk
     __shared__ float sPw[kC + 2];                                         // l^n, n = 0..65
     __shared__ float sPs[kC + 2];                                         // sum_{m<n} l^m
+    __shared__ float sPm[RH ? 2 * kC : 1];                                // RH: [63 + d] = l^d (d >= 0), 0 (d < 0)
     __shared__ float sKi[KI];                                             // incoming [K1; K2/2] (dense)
     __shared__ float sKi0;                                                // incoming K0 (dense)
     __shared__ float sCum[SEL && !STATE_ONLY ? 2 : 1][kC];                // selective: log2 decay to token i
@@ -128,9 +140,9 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
     // (MFMAs write their whole destination regardless of EXEC)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
-    const bool is_u = STATE_ONLY || wave >= 4;
-    const int u = STATE_ONLY ? wave : wave - 4;       // update-wave index
-    const int ut = tid & 255;                          // thread index within the update role
+    const bool is_u = STATE_ONLY || wave >= NRW;
+    const int u = wave - NRW;                          // update-wave index
+    const int ut = tid - 64 * NRW;                     // thread index within the update role
     const int tr_r = c16 >> 2, tr_c = 4 * (c16 & 3);  // ds_read_tr address offsets of this lane
 
     const int Sq = a.B * a.H;
@@ -157,13 +169,18 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
         for (int m = 0; m < tid; ++m, pm *= ld) ps += pm;
         sPs[tid] = static_cast<float>(ps);
     }
+    if constexpr (RH) {
+        if (tid < 2 * kC)
+            sPm[tid] = tid >= kC - 1 ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(tid - (kC - 1))))
+                                     : 0.f;
+    }
     __syncthreads();  // the power tables are read by the first tile stores below
 
     // ---- update role: state registers, tile pointers, first tiles
     const size_t so1 = static_cast<size_t>(seq) * kD * kD;
     const size_t so0 = static_cast<size_t>(seq) * kD;
-    f32x4 st[2][NBX];  // feature blocks 2u+fi (rows 4g+r), value blocks nb (column c16)
-    f32x4 s0t;         // row 0 (lanes 0..15, element 0) = S0[16u + c16]
+    f32x4 st[FI][NBX];  // feature blocks FI u + fi (rows 4g+r), value blocks nb (column c16)
+    f32x4 s0t;          // row 0 (lanes 0..15, element 0) = S0[16u + c16] (update waves u < 4)
     float k0 = 0.f;    // K0 (same value in every lane and update wave)
     Tiles T;
     if constexpr (STATE_ONLY) T.q0 = T.q1 = u32x4{0u, 0u, 0u, 0u};
@@ -206,15 +223,16 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
         uint16_t *pq = &sQf[STATE_ONLY ? 0 : xb][0][0], *pv = &sV[STATE_ONLY ? 0 : xb][0][0];
         store_row<STATE_ONLY, SEL>(T.q0, T.k0, T.v0, ra, col, va, wa, kscale, pq, &sKf[xb][0][0], pv,
                                    &sVw[xb][0][0]);
-        store_row<STATE_ONLY, SEL>(T.q1, T.k1, T.v1, ra + 32, col, vb, wb, kscale, pq, &sKf[xb][0][0], pv,
-                                   &sVw[xb][0][0]);
+        if constexpr (!UW8)
+            store_row<STATE_ONLY, SEL>(T.q1, T.k1, T.v1, ra + 32, col, vb, wb, kscale, pq, &sKf[xb][0][0], pv,
+                                       &sVw[xb][0][0]);
     };
     // bf16 copy of the state entering the next chunk, into state buffer xb
     auto publish_state = [&](int xb) {
         if constexpr (!STATE_ONLY) {
 #pragma unroll
-            for (int fi = 0; fi < 2; ++fi) {
-                const int f = 16 * (2 * u + fi) + 4 * g;
+            for (int fi = 0; fi < FI; ++fi) {
+                const int f = 16 * (FI * u + fi) + 4 * g;
 #pragma unroll
                 for (int nb = 0; nb < NBX; ++nb) {
                     const int n = 16 * nb + c16;
@@ -223,19 +241,19 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
                         uint2{pack2(st[fi][nb][0], st[fi][nb][1]), pack2(st[fi][nb][2], st[fi][nb][3])};
                 }
             }
-            if (g == 0) sS0[xb][16 * u + c16] = s0t[0];
+            if (g == 0 && u < 4) sS0[xb][16 * u + c16] = s0t[0];
             if (u == 0 && lane == 0) sK0[xb] = k0;
         }
     };
     if (is_u) {
-        load_tiles<STATE_ONLY, SEL>(T, a, qp, kp, vp, ldp, c_begin, ra, lane);
+        load_tiles<STATE_ONLY, SEL, UW8>(T, a, qp, kp, vp, ldp, c_begin, ra, lane);
 #pragma unroll
-        for (int fi = 0; fi < 2; ++fi)
+        for (int fi = 0; fi < FI; ++fi)
 #pragma unroll
             for (int nb = 0; nb < NBX; ++nb)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int f = 16 * (2 * u + fi) + 4 * g + r, fr = f & (kD - 1);
+                    const int f = 16 * (FI * u + fi) + 4 * g + r, fr = f & (kD - 1);
                     const int n = 16 * nb + c16;
                     float x = 0.f;
                     if (n < kD) {
@@ -249,7 +267,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
                 }
         {
             float x = 0.f;
-            if (g == 0) x = from_ws ? wslot[kWsS0 + 16 * u + c16] : (has_in ? a.s0i[so0 + 16 * u + c16] : 0.f);
+            if (g == 0 && u < 4) x = from_ws ? wslot[kWsS0 + 16 * u + c16] : (has_in ? a.s0i[so0 + 16 * u + c16] : 0.f);
             s0t = f32x4{x, 0.f, 0.f, 0.f};
         }
         {
@@ -267,39 +285,48 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
         }
         // constant columns: 64..79 of v (1, 0, ...) and 65..79 of w v (column 64
         // holds w and is written with every chunk's tile)
-        for (int idx = ut; idx < XB * kC * 16; idx += 256) {
+        for (int idx = ut; idx < XB * kC * 16; idx += 64 * NUW) {
             const int xb = idx / (kC * 16), row = (idx >> 4) & (kC - 1), cc = kD + (idx & 15);
             if constexpr (!STATE_ONLY) sV[xb][row][cc] = cc == kD ? 0x3F80u : 0u;
             if (cc != kD) sVw[xb][row][cc] = 0u;
         }
         publish_state(c_begin & 1);
         store_tiles(c_begin, STATE_ONLY ? 0 : c_begin & 1);
-        load_tiles<STATE_ONLY, SEL>(T, a, qp, kp, vp, ldp, c_begin + 1, ra, lane);
+        load_tiles<STATE_ONLY, SEL, UW8>(T, a, qp, kp, vp, ldp, c_begin + 1, ra, lane);
     }
 
-    // ---- readout-role constants (query row of the lane: iw)
-    const int iw = 16 * wave + c16;
-    float mask[4][4];  // l^(i-j) [i >= j] for S^T[j = 16jb + 4g + r][i = iw]
-    float pin = 0.f;   // l^(iw+1)
-    if (!is_u && !SEL) {
-#pragma unroll
-        for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int d = iw - (16 * jb + 4 * g + r);
-                mask[jb][r] = (jb <= wave && d >= 0) ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(d))) : 0.f;
-            }
-        pin = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(iw + 1)));
-    }
-    // row 0 of the ones operand: lanes of A-row 0 hold eight 1.0s
-    const bf16x8 ones = as_bf16x8(c16 == 0 ? u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}
-                                           : u32x4{0u, 0u, 0u, 0u});
     __syncthreads();
 
-    for (int c = c_begin; c < c_end; ++c) {
-        const int p = STATE_ONLY ? 0 : c & 1, xq = STATE_ONLY ? 0 : p ^ 1;
-        const int nvalid = min(kC, a.L - c * kC);
-        if (!is_u) {
+    // each role runs its own copy of the chunk loop (the same barriers, one per
+    // chunk), so that only its own loop-carried registers are live in it
+    if (!is_u) {
+        // ---- readout-role constants (query row of the lane: iw)
+        // query block rb of this readout wave (RH: the two halves of a block sit on
+        // different SIMDs) and, for RH, its half hh of the value columns
+        const int rb = RH ? (wave < 4 ? wave : ((wave + 2) & 3)) : wave;
+        const int hh = RH ? (wave >> 2) : 0;
+        auto vblk = [&](int i) { return RH ? (i < 2 ? 2 * hh + i : NB) : i; };
+        const int iw = 16 * rb + c16;
+        float mask[4][4];  // l^(i-j) [i >= j] for S^T[j = 16jb + 4g + r][i = iw]
+        float pin = 0.f;   // l^(iw+1)
+        if (!is_u && !SEL) {
+            if constexpr (!RH) {
+    #pragma unroll
+                for (int jb = 0; jb < 4; ++jb)
+    #pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int d = iw - (16 * jb + 4 * g + r);
+                        mask[jb][r] = (jb <= rb && d >= 0) ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(d))) : 0.f;
+                    }
+            }
+            pin = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(iw + 1)));
+        }
+        // dense: l^(64 c) of the chunk, advanced by one chunk decay per step
+        float dcr = dense ? static_cast<float>(pow(static_cast<double>(lam), 64.0 * c_begin)) : 0.f;
+        for (int c = c_begin; c < c_end; ++c) {
+            const int p = STATE_ONLY ? 0 : c & 1;
+            const int nvalid = min(kC, a.L - c * kC);
+            (void)nvalid;
             if constexpr (!STATE_ONLY) {
                 if constexpr (SEL) {
                     // decays within the chunk: l(i <- j) = 2^(cum_i - cum_j), and from
@@ -311,24 +338,45 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
                         const f32x4 cj = *reinterpret_cast<const f32x4 *>(&sCum[p][16 * jb + 4 * g]);
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            mask[jb][r] = (jb <= wave && 16 * jb + 4 * g + r <= iw) ? exp2f(ci - cj[r]) : 0.f;
+                            mask[jb][r] = (jb <= rb && 16 * jb + 4 * g + r <= iw) ? exp2f(ci - cj[r]) : 0.f;
                     }
                 }
-                // ---- query features of row iw (B operand of S^T and of the readout)
-                Opnd<false> fq[4];
+                // ---- y^T = [S1; S2/2 | K]^T Fq^T first (the state entering the chunk);
+                // the query features of row iw are read per k-step where used, and the
+                // phases are kept apart so that few operands are live at once
+                f32x4 acc_av[NVB], acc_ro[NVB];
+#pragma unroll
+                for (int i = 0; i < NVB; ++i) {
+                    acc_av[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    acc_ro[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+                Opnd<false> fq[4];  // query features of row iw, read once per chunk
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) fq[ks] = row_op<false>(&sQf[p][iw][32 * ks + 8 * g], 0);
-                // ---- transposed score block S^T[j][i] for j-blocks jb <= wave
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const Opnd<false> &fqk = fq[ks];
+                    Opnd<false> sop[NVB];
+#pragma unroll
+                    for (int i = 0; i < NVB; ++i) {
+                        const int nb = vblk(i);
+                        const int n = nb == NB ? kD : 16 * nb + c16;  // ones block: only row 64 (K)
+                        sop[i] = row_op<false>(&sSt[p][n][32 * ks + 8 * g], 0);
+                        if (nb == NB && c16 != 0) sop[i].h = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
+                    }
+#pragma unroll
+                    for (int i = 0; i < NVB; ++i) acc_ro[i] = mma<false>(sop[i], fqk, acc_ro[i]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                // ---- transposed score block S^T[j][i] for j-blocks jb <= rb
                 f32x4 sT[4];
 #pragma unroll
                 for (int jb = 0; jb < 4; ++jb) {
                     sT[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    if (jb > wave) continue;
-                    Opnd<false> ak[4];
+                    if (jb > rb) continue;
 #pragma unroll
-                    for (int ks = 0; ks < 4; ++ks) ak[ks] = row_op<false>(&sKf[p][16 * jb + c16][32 * ks + 8 * g], 0);
-#pragma unroll
-                    for (int ks = 0; ks < 4; ++ks) sT[jb] = mma<false>(ak[ks], fq[ks], sT[jb]);
+                    for (int ks = 0; ks < 4; ++ks)
+                        sT[jb] = mma<false>(row_op<false>(&sKf[p][16 * jb + c16][32 * ks + 8 * g], 0), fq[ks], sT[jb]);
                 }
                 // ---- A = decay mask * (1 + S) as packed bf16
                 uint32_t Ah[4][2];
@@ -336,49 +384,38 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
                 for (int jb = 0; jb < 4; ++jb) {
                     float x[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) x[r] = mask[jb][r] * (1.0f + sT[jb][r]);
+                    for (int r = 0; r < 4; ++r) {
+                        // RH: the decay mask from the power table (registers are short)
+                        const int d = iw - (16 * jb + 4 * g + r);
+                        // RH: one base address, immediate offsets: index 63 + iw - j
+                        const float mk = RH ? (&sPm[RH ? iw - 4 * g + 12 : 0])[51 - 16 * jb - r] : mask[jb][r];
+                        (void)d;
+                        x[r] = mk * (1.0f + sT[jb][r]);
+                    }
                     Ah[jb][0] = pack2(x[0], x[1]);
                     Ah[jb][1] = pack2(x[2], x[3]);
                 }
-                // ---- y^T = V^T A^T: accumulator row = value column 16nb + 4g + r,
+                __builtin_amdgcn_sched_barrier(0);
+                // ---- y^T += V^T A^T: accumulator row = value column 16nb + 4g + r,
                 // column = query row iw; register t of A^T <-> token 32kk + 16(t/4) + 4g + t%4
-                f32x4 acc_av[NBX], acc_ro[NBX];
-#pragma unroll
-                for (int nb = 0; nb < NBX; ++nb) {
-                    acc_av[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    acc_ro[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-                }
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
-                    if (2 * kk > wave) continue;
-                    const bool second = 2 * kk + 1 <= wave;  // second j-block unmasked
+                    if (2 * kk > rb) continue;
+                    const bool second = 2 * kk + 1 <= rb;  // second j-block unmasked
                     Opnd<false> aop;
                     aop.h = as_bf16x8(u32x4{Ah[2 * kk][0], Ah[2 * kk][1], second ? Ah[2 * kk + 1][0] : 0u,
                                             second ? Ah[2 * kk + 1][1] : 0u});
-                    Opnd<false> vop[NBX];
+                    Opnd<false> vop[NVB];
 #pragma unroll
-                    for (int nb = 0; nb < NBX; ++nb) {
-                        const uint16_t *p0 = &sV[p][32 * kk + 4 * g + tr_r][16 * nb + tr_c];
-                        vop[nb] = tr_op<false>(p0, p0 + 16 * kPV8, 0);
+                    for (int i = 0; i < NVB; ++i) {
+                        const uint16_t *p0 = &sV[p][32 * kk + 4 * g + tr_r][16 * vblk(i) + tr_c];
+                        vop[i] = tr_op<false>(p0, p0 + 16 * kPV8, 0);
                     }
 #pragma unroll
-                    for (int nb = 0; nb < NBX; ++nb) acc_av[nb] = mma<false>(vop[nb], aop, acc_av[nb]);
-                }
-                // ---- y^T += [S1; S2/2 | K]^T Fq^T  (the state entering the chunk)
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    Opnd<false> sop[NBX];
-#pragma unroll
-                    for (int nb = 0; nb < NBX; ++nb) {
-                        const int n = nb == NB ? kD : 16 * nb + c16;  // ones block: only row 64 (K)
-                        sop[nb] = row_op<false>(&sSt[p][n][32 * ks + 8 * g], 0);
-                        if (nb == NB && c16 != 0) sop[nb].h = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
-                    }
-#pragma unroll
-                    for (int nb = 0; nb < NBX; ++nb) acc_ro[nb] = mma<false>(sop[nb], fq[ks], acc_ro[nb]);
+                    for (int i = 0; i < NVB; ++i) acc_av[i] = mma<false>(vop[i], aop, acc_av[i]);
                 }
                 // ---- denominator of row iw: column 64 of both products (lane g = 0, r = 0)
-                float den_call = acc_av[NB][0] + pin * (sK0[p] + acc_ro[NB][0]);
+                float den_call = acc_av[NVB - 1][0] + pin * (sK0[p] + acc_ro[NVB - 1][0]);
                 den_call = __shfl(den_call, c16, kWave);
                 float den;
                 if (dense) {
@@ -387,13 +424,14 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
 #pragma unroll
                     for (int ks = 0; ks < 4; ++ks) {
                         float qf[8];
-                        unpack8(__builtin_bit_cast(u32x4, fq[ks].h), qf);
+                        unpack8(lds128(&sQf[p][iw][32 * ks + 8 * g]), qf);
 #pragma unroll
                         for (int t = 0; t < 8; ++t) ki += qf[t] * sKi[32 * ks + 8 * g + t];
                     }
                     ki += __shfl_xor(ki, 16, kWave);
                     ki += __shfl_xor(ki, 32, kWave);
-                    const float dc = static_cast<float>(pow(static_cast<double>(lam), 64.0 * c));
+                    const float dc = dcr;
+                    dcr *= sPw[kC];
                     den = fmaxf(fmaxf(den_call, a.eps) + pin * dc * (sKi0 + ki), a.eps);
                 } else {
                     den = fmaxf(den_call, a.eps);
@@ -404,11 +442,12 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
                 if (t < a.L) {
                     const int64_t yo = b * a.y_sb + h * a.y_sh + t * a.y_sl + 4 * g;
 #pragma unroll
-                    for (int nb = 0; nb < NB; ++nb) {
+                    for (int i = 0; i < NVB - 1; ++i) {
+                        const int nb = vblk(i);
                         const f32x4 s0 = *reinterpret_cast<const f32x4 *>(&sS0[p][16 * nb + 4 * g]);
                         f32x4 yv;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) yv[r] = (acc_av[nb][r] + pin * (s0[r] + acc_ro[nb][r])) * inv;
+                        for (int r = 0; r < 4; ++r) yv[r] = (acc_av[i][r] + pin * (s0[r] + acc_ro[i][r])) * inv;
                         const int64_t o = yo + 16 * nb;
                         if (a.dt_y == PRIME_BF16) {
                             *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + o) =
@@ -422,11 +461,21 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
                     }
                 }
             }
-        } else {
+            __syncthreads();
+        }
+        return;
+    }
+    // row 0 of the ones operand: lanes of A-row 0 hold eight 1.0s
+    const bf16x8 ones = as_bf16x8(c16 == 0 ? u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u}
+                                           : u32x4{0u, 0u, 0u, 0u});
+    for (int c = c_begin; c < c_end; ++c) {
+        const int p = STATE_ONLY ? 0 : c & 1, xq = STATE_ONLY ? 0 : p ^ 1;
+        const int nvalid = min(kC, a.L - c * kC);
+        {
             // ---- state update: st = l^n st + [k; k*k/2]^T [w v | w];  S0 on the ones row
             const float ln = SEL ? sel_ln : sPw[nvalid];  // selective: set when chunk c was stored
 #pragma unroll
-            for (int fi = 0; fi < 2; ++fi)
+            for (int fi = 0; fi < FI; ++fi)
 #pragma unroll
                 for (int nb = 0; nb < NBX; ++nb)
 #pragma unroll
@@ -437,10 +486,10 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
             for (int ks = 0; ks < 2; ++ks) {
                 // register t of both operands <-> token 32ks + 16(t/4) + 4g + t%4
                 const int j0 = 32 * ks + 4 * g + tr_r;
-                Opnd<false> ak[2], vop[NBX];
+                Opnd<false> ak[FI], vop[NBX];
 #pragma unroll
-                for (int fi = 0; fi < 2; ++fi) {
-                    const uint16_t *p0 = &sKf[p][j0][16 * (2 * u + fi) + tr_c];
+                for (int fi = 0; fi < FI; ++fi) {
+                    const uint16_t *p0 = &sKf[p][j0][16 * (FI * u + fi) + tr_c];
                     ak[fi] = tr_op<false>(p0, p0 + 16 * kPW, 0);
                 }
 #pragma unroll
@@ -449,12 +498,12 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
                     vop[nb] = tr_op<false>(p0, p0 + 16 * kPV8, 0);
                 }
 #pragma unroll
-                for (int fi = 0; fi < 2; ++fi)
+                for (int fi = 0; fi < FI; ++fi)
 #pragma unroll
                     for (int nb = 0; nb < NBX; ++nb) st[fi][nb] = mma<false>(ak[fi], vop[nb], st[fi][nb]);
                 // value block u of [w v] on the ones row (a wave-uniform switch, so
                 // that the operand is selected without a register-indexed access)
-                switch (u) {
+                if (u < 4) switch (u) {
                     case 0: s0t = mfma(ones, vop[0].h, s0t); break;
                     case 1: s0t = mfma(ones, vop[1].h, s0t); break;
                     case 2: s0t = mfma(ones, vop[2].h, s0t); break;
@@ -464,14 +513,13 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
             const bool more = c + 1 < c_end;
             if constexpr (STATE_ONLY) __syncthreads();  // every wave has read the single tile buffer
             if (more) store_tiles(c + 1, xq);
-            load_tiles<STATE_ONLY, SEL>(T, a, qp, kp, vp, ldp, c + 2, ra, lane);
+            load_tiles<STATE_ONLY, SEL, UW8>(T, a, qp, kp, vp, ldp, c + 2, ra, lane);
             if (more) publish_state(xq);
         }
         __syncthreads();
     }
 
     // ---- segment / final state (decays used the valid counts: no pad correction)
-    if (!is_u) return;
     float *o_s1, *o_s2, *o_s0, *o_k1, *o_k2, *o_k0;
     size_t off1, off0, offk0;
     if (STATE_ONLY) {
@@ -486,10 +534,10 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
     // dense clamp: the incoming K state decays separately (l^L over the call)
     const float linit = dense ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(a.L))) : 0.f;
 #pragma unroll
-    for (int fi = 0; fi < 2; ++fi)
+    for (int fi = 0; fi < FI; ++fi)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int f = 16 * (2 * u + fi) + 4 * g + r;
+            const int f = 16 * (FI * u + fi) + 4 * g + r;
             const int fr = f & (kD - 1);
             const float sc = (f < kD || SEL) ? 1.0f : 2.0f;  // rows 64.. hold S2/2 and K2/2
 #pragma unroll
@@ -503,7 +551,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
                 (f < kD ? o_k1 : o_k2)[off0 + fr] = sc * kv;
             }
         }
-    if (g == 0) o_s0[off0 + 16 * u + c16] = s0t[0];
+    if (g == 0 && u < 4) o_s0[off0 + 16 * u + c16] = s0t[0];
     if (u == 0 && lane == 0) o_k0[offk0] = k0 + (STATE_ONLY ? 0.f : linit * sKi0);
     // selective: the segment's own log2 decay, for the scan over segments
     if (SEL && STATE_ONLY && u == 0 && lane == 0) wslot[kWsDecay] = seg_ld;
@@ -511,7 +559,7 @@ __global__ __launch_bounds__(STATE_ONLY ? 256 : 512, 1) void prefill_bf16_kernel
 
 void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream, TimerEvents t) {
     const bool sel = a.log_decay != nullptr;
-    const dim3 g(grid), blk(state_only ? 256 : 512);
+    const dim3 g(grid), blk(state_only ? 256 : (sel ? 512 : 1024));
     if (state_only && sel)
         hipExtLaunchKernelGGL(prefill_bf16_kernel<true, true>, g, blk, 0, stream, t.start, t.stop, 0, a);
     else if (state_only)
@@ -519,7 +567,7 @@ void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStr
     else if (sel)
         hipExtLaunchKernelGGL(prefill_bf16_kernel<false, true>, g, blk, 0, stream, t.start, t.stop, 0, a);
     else
-        hipExtLaunchKernelGGL(prefill_bf16_kernel<false, false>, g, blk, 0, stream, t.start, t.stop, 0, a);
+        hipExtLaunchKernelGGL((prefill_bf16_kernel<false, false, true, true>), g, blk, 0, stream, t.start, t.stop, 0, a);
 }
 
 }  // namespace prime
