@@ -35,8 +35,8 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
 KERNEL_DELTA_PREP, KERNEL_DELTA_SCAN, KERNEL_DELTA_STEP = 4, 5, 6
 KERNEL_BWD_DQ, KERNEL_BWD_DKV, KERNEL_BWD_DUAL, KERNEL_BWD_DUAL_SCAN = 7, 8, 9, 10
-KERNEL_NAMES = {KERNEL_PREFILL_CHUNKS: "prefill_bf16_kernel<false>", KERNEL_PREFILL_SEGMENTS:
-                "prefill_bf16_kernel<true>", KERNEL_SEGMENT_SCAN: "segment_scan_kernel",
+KERNEL_NAMES = {KERNEL_PREFILL_CHUNKS: "prefill_bf16_kernel (fused chunk loop)", KERNEL_PREFILL_SEGMENTS:
+                "prefill_bf16_kernel (segment states)", KERNEL_SEGMENT_SCAN: "segment_scan_kernel",
                 KERNEL_DECODE: "decode_step_kernel", KERNEL_DELTA_PREP: "delta_prep_kernel",
                 KERNEL_DELTA_SCAN: "delta_scan_kernel", KERNEL_DELTA_STEP: "delta_step_kernel",
                 KERNEL_BWD_DQ: "prefill_bwd_dq_kernel", KERNEL_BWD_DKV: "prefill_bwd_dkv_kernel<false>",
