@@ -670,13 +670,23 @@ __global__ __launch_bounds__(256) void segment_scan_kernel(const PrefillArgs a) 
         ? static_cast<float>(pow(static_cast<double>(a.decay[h]),
                                  static_cast<double>(a.L - (a.G - 1) * a.cps * kC)))
         : 0.f;
-    for (int s = 0; s < ns; ++s) {
-        const float d = slot[static_cast<size_t>(s) * kWsStride];
-        if (!a.accumulate) slot[static_cast<size_t>(s) * kWsStride] = carry;
-        // selective: segment s's own decay, stored beside its slot's state
-        const float f = sel ? exp2f(slot[static_cast<size_t>(s) * kWsStride + kWsDecay - e])
-                            : (s == a.G - 1 ? lLast : lT);
-        carry = f * carry + d;
+    // eight slots' loads in flight at a time, then their dependent updates
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+        float d[8], f[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int s = s0 + t < ns ? s0 + t : ns - 1;  // clamped (unused past ns)
+            d[t] = slot[static_cast<size_t>(s) * kWsStride];
+            // selective: segment s's own decay, stored beside its slot's state
+            f[t] = sel ? exp2f(slot[static_cast<size_t>(s) * kWsStride + kWsDecay - e])
+                       : (s == a.G - 1 ? lLast : lT);
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            if (s0 + t >= ns) break;
+            if (!a.accumulate) slot[static_cast<size_t>(s0 + t) * kWsStride] = carry;
+            carry = f[t] * carry + d[t];
+        }
     }
     if (!a.accumulate) {
         slot[static_cast<size_t>(a.G - 1) * kWsStride] = carry;
