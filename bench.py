@@ -174,26 +174,27 @@ def bench_prefill(args, lib, torch, dev):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    # timed region: every kernel of the call is bracketed by HIP events on the
-    # call's stream (an event pair around the dominant kernel alone would open
-    # while the preceding scan kernel still runs and count part of it)
+    # timed region for `value`: the call alone, no instrumentation
+    ms = timed(step, args.steps, 0)
+    # the same steps again with every kernel of the call bracketed by HIP events
+    # on the call's stream, for the per-kernel durations (an event pair around
+    # the dominant kernel alone would open while the preceding scan kernel still
+    # runs and count part of it); the events add a few microseconds per call
     ids = (lib.KERNEL_PREFILL_CHUNKS, lib.KERNEL_PREFILL_SEGMENTS, lib.KERNEL_SEGMENT_SCAN)
     lib.timer_reset()
     lib.timer_enable(*ids)
-    ms = timed(step, args.steps, 0)
+    ms_events = timed(step, args.steps, 0)
     lib.timer_enable()
     kern = {lib.KERNEL_NAMES[kid]: kernel_ms(lib, kid) for kid in ids}
     main_ms, main_n = kernel_ms(lib, lib.KERNEL_PREFILL_CHUNKS)
     lib.timer_reset()
-    # the same steps without events, for the event overhead
-    ms_plain = timed(step, args.steps, 0)
     ok = bool(torch.isfinite(y).all().item())
     tokens = B * L
     algo_bytes = B * H * L * PREFILL_BYTES_PER_TOKEN_HEAD + B * H * STATE_BYTES
     flops = B * H * L * PREFILL_FLOP_PER_TOKEN_HEAD
     return dict(B=B, H=H, L=L, C=C, ms=ms, tokens=tokens, bytes=algo_bytes, flops=flops, finite=ok,
                 kernels={n: {"avg_us": None if t is None else t * 1e3, "launches": c} for n, (t, c) in kern.items()},
-                ms_plain=ms_plain, main_ms=main_ms, main_n=main_n, ws_bytes=0 if ws is None else ws.numel())
+                ms_events=ms_events, main_ms=main_ms, main_n=main_n, ws_bytes=0 if ws is None else ws.numel())
 
 
 # ----------------------------------------------------------------- decode
@@ -749,7 +750,7 @@ def main():
         "prefill": {"whole_call_GBps": pf["bytes"] / t_step / 1e9,
                     "whole_call_hbm_frac": pf["bytes"] / t_step / PEAK_HBM,
                     "tflops": pf["flops"] / t_step / 1e12, "mfma_frac": pf["flops"] / t_step / PEAK_BF16,
-                    "kernels": pf["kernels"], "ms_per_step_without_events": pf["ms_plain"],
+                    "kernels": pf["kernels"], "ms_per_step_with_events": pf["ms_events"],
                     "finite": pf["finite"]},
         "gpu": f"{torch.cuda.get_device_name(dev)} ({torch.cuda.get_device_properties(dev).gcnArchName}, "
                f"{torch.cuda.get_device_properties(dev).multi_processor_count} CUs)",
