@@ -23,7 +23,7 @@
 namespace prime {
 
 
-constexpr int kDecodeWaves = 4;
+constexpr int kDecodeWaves = 1;  // one wavefront per workgroup: the scheduler places waves one at a time
 
 // x rounded to dtype dt (to nearest even), returned as fp32
 __device__ __forceinline__ float round_to(float x, int dt) {
