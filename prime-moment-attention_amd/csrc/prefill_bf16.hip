@@ -26,7 +26,7 @@ namespace prime {
 namespace {
 
 constexpr int kPV8 = kD + 16;  // sV / sVw pitch in bf16 (40 dwords, conflict-free transposed reads)
-constexpr int kSR = kD + 1;    // state copy rows: 64 value columns + the K column
+constexpr int kSR = kD + 2;    // state copy rows: 64 value columns, the K column, a zero row
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
@@ -81,13 +81,16 @@ __device__ __forceinline__ void load_tiles(Tiles &T, const PrefillArgs &a, const
 // One row segment into the tile buffers: [q | q*q], [k | k*k/2], [v], [w v | w].
 // Invalid rows (past the chunk's tokens) are stored as zeros.
 template <bool STATE_ONLY, bool SEL>
-__device__ __forceinline__ void store_row(u32x4 q, u32x4 k, u32x4 v, int row, int col, bool valid, float w, float ks,
-                                          uint16_t *sQf, uint16_t *sKf, uint16_t *sV, uint16_t *sVw) {
-    const uint32_t m = valid ? 0xFFFFFFFFu : 0u;
-    k = and4(k, m);
-    v = and4(v, m);
+__device__ __forceinline__ void store_row(u32x4 q, u32x4 k, u32x4 v, int row, int col, bool ragged, bool valid,
+                                          float w, float ks, uint16_t *sQf, uint16_t *sKf, uint16_t *sV,
+                                          uint16_t *sVw) {
+    if (ragged) {  // wave-uniform: only a chunk with rows past the end masks them
+        const uint32_t m = valid ? 0xFFFFFFFFu : 0u;
+        k = and4(k, m);
+        v = and4(v, m);
+        if constexpr (!STATE_ONLY) q = and4(q, m);
+    }
     if constexpr (!STATE_ONLY) {
-        q = and4(q, m);
         st16(sQf + row * kPW + col, q);
         st16(sQf + row * kPW + kD + col, sq8(q, 1.0f));
         st16(sV + row * kPV8 + col, v);
@@ -221,10 +224,11 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
             wb = vb ? sPw[nv - 1 - (ra + 32)] : 0.f;
         }
         uint16_t *pq = &sQf[STATE_ONLY ? 0 : xb][0][0], *pv = &sV[STATE_ONLY ? 0 : xb][0][0];
-        store_row<STATE_ONLY, SEL>(T.q0, T.k0, T.v0, ra, col, va, wa, kscale, pq, &sKf[xb][0][0], pv,
+        const bool ragged = nv < kC;
+        store_row<STATE_ONLY, SEL>(T.q0, T.k0, T.v0, ra, col, ragged, va, wa, kscale, pq, &sKf[xb][0][0], pv,
                                    &sVw[xb][0][0]);
         if constexpr (!UW8)
-            store_row<STATE_ONLY, SEL>(T.q1, T.k1, T.v1, ra + 32, col, vb, wb, kscale, pq, &sKf[xb][0][0], pv,
+            store_row<STATE_ONLY, SEL>(T.q1, T.k1, T.v1, ra + 32, col, ragged, vb, wb, kscale, pq, &sKf[xb][0][0], pv,
                                        &sVw[xb][0][0]);
     };
     // bf16 copy of the state entering the next chunk, into state buffer xb
@@ -282,6 +286,11 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
                 if (dense && has_in) x = (ut < kD ? a.k1i : a.k2i)[so0 + fr];
                 sKi[ut] = ut < kD ? x : 0.5f * x;
             }
+        }
+        // the zero row of both state copies (read as the K block's other columns)
+        if constexpr (!STATE_ONLY) {
+            for (int idx = ut; idx < 2 * (kF / 2); idx += 64 * NUW)
+                reinterpret_cast<uint32_t *>(&sSt[idx / (kF / 2)][kD + 1][0])[idx % (kF / 2)] = 0u;
         }
         // constant columns: 64..79 of v (1, 0, ...) and 65..79 of w v (column 64
         // holds w and is written with every chunk's tile)
@@ -360,9 +369,9 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
 #pragma unroll
                     for (int i = 0; i < NVB; ++i) {
                         const int nb = vblk(i);
-                        const int n = nb == NB ? kD : 16 * nb + c16;  // ones block: only row 64 (K)
+                        // ones block: row 64 (K) in lane 0 of each row group, the zero row elsewhere
+                        const int n = nb == NB ? (c16 == 0 ? kD : kD + 1) : 16 * nb + c16;
                         sop[i] = row_op<false>(&sSt[p][n][32 * ks + 8 * g], 0);
-                        if (nb == NB && c16 != 0) sop[i].h = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
                     }
 #pragma unroll
                     for (int i = 0; i < NVB; ++i) acc_ro[i] = mma<false>(sop[i], fqk, acc_ro[i]);
@@ -390,7 +399,7 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
                         // RH: one base address, immediate offsets: index 63 + iw - j
                         const float mk = RH ? (&sPm[RH ? iw - 4 * g + 12 : 0])[51 - 16 * jb - r] : mask[jb][r];
                         (void)d;
-                        x[r] = mk * (1.0f + sT[jb][r]);
+                        x[r] = fmaf(mk, sT[jb][r], mk);  // mk (1 + s)
                     }
                     Ah[jb][0] = pack2(x[0], x[1]);
                     Ah[jb][1] = pack2(x[2], x[3]);
