@@ -350,9 +350,11 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
                             mask[jb][r] = (jb <= rb && 16 * jb + 4 * g + r <= iw) ? exp2f(ci - cj[r]) : 0.f;
                     }
                 }
-                // ---- y^T = [S1; S2/2 | K]^T Fq^T first (the state entering the chunk);
-                // the query features of row iw are read per k-step where used, and the
-                // phases are kept apart so that few operands are live at once
+                // ---- phases: score block, A, y^T += V^T A^T, then the state readout
+                // y^T += [S1; S2/2 | K]^T Fq^T last (its operand reads then miss the
+                // burst of LDS reads that follows the barrier); the query features of
+                // row iw are read once, and the phases are kept apart so that few
+                // operands are live at once
                 f32x4 acc_av[NVB], acc_ro[NVB];
 #pragma unroll
                 for (int i = 0; i < NVB; ++i) {
@@ -362,20 +364,6 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
                 Opnd<false> fq[4];  // query features of row iw, read once per chunk
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) fq[ks] = row_op<false>(&sQf[p][iw][32 * ks + 8 * g], 0);
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const Opnd<false> &fqk = fq[ks];
-                    Opnd<false> sop[NVB];
-#pragma unroll
-                    for (int i = 0; i < NVB; ++i) {
-                        const int nb = vblk(i);
-                        // ones block: row 64 (K) in lane 0 of each row group, the zero row elsewhere
-                        const int n = nb == NB ? (c16 == 0 ? kD : kD + 1) : 16 * nb + c16;
-                        sop[i] = row_op<false>(&sSt[p][n][32 * ks + 8 * g], 0);
-                    }
-#pragma unroll
-                    for (int i = 0; i < NVB; ++i) acc_ro[i] = mma<false>(sop[i], fqk, acc_ro[i]);
-                }
                 __builtin_amdgcn_sched_barrier(0);
                 // ---- transposed score block S^T[j][i] for j-blocks jb <= rb
                 f32x4 sT[4];
@@ -422,6 +410,21 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
                     }
 #pragma unroll
                     for (int i = 0; i < NVB; ++i) acc_av[i] = mma<false>(vop[i], aop, acc_av[i]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const Opnd<false> &fqk = fq[ks];
+                    Opnd<false> sop[NVB];
+#pragma unroll
+                    for (int i = 0; i < NVB; ++i) {
+                        const int nb = vblk(i);
+                        // ones block: row 64 (K) in lane 0 of each row group, the zero row elsewhere
+                        const int n = nb == NB ? (c16 == 0 ? kD : kD + 1) : 16 * nb + c16;
+                        sop[i] = row_op<false>(&sSt[p][n][32 * ks + 8 * g], 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < NVB; ++i) acc_ro[i] = mma<false>(sop[i], fqk, acc_ro[i]);
                 }
                 // ---- denominator of row iw: column 64 of both products (lane g = 0, r = 0)
                 float den_call = acc_av[NVB - 1][0] + pin * (sK0[p] + acc_ro[NVB - 1][0]);
