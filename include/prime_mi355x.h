@@ -146,6 +146,21 @@ int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k,
                           const prime_state_t *state_out, void *workspace,
                           size_t workspace_bytes, void *stream);
 
+/*
+ * prime_chunked_prefill on the raw projections: q, k are the q_proj / k_proj
+ * outputs, normalised and scaled as the kernels load them by `norm` (see
+ * prime_qk_norm_t), bit-identical to prime_head_layernorm on q (with q_scale)
+ * and k (scale 1) followed by prime_chunked_prefill.  Replaces
+ * attention.py:96-101 together with the prefill branches (:145-202).
+ * BF16 q/k/v only; workspace and the other arguments as above.
+ */
+int prime_chunked_prefill_qknorm(const prime_tensor_t *q, const prime_tensor_t *k,
+                                 const prime_tensor_t *v, int B, int H, int H_kv, int L, int D,
+                                 int chunk, const float *decay, float eps, unsigned flags,
+                                 const prime_qk_norm_t *norm, const prime_state_t *state_in,
+                                 const prime_tensor_t *y, const prime_state_t *state_out,
+                                 void *workspace, size_t workspace_bytes, void *stream);
+
 /* Workspace bytes prime_chunked_prefill uses for this shape (0 = none needed). */
 size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags);
 
@@ -272,6 +287,14 @@ int prime_selective_prefill(const prime_tensor_t *q, const prime_tensor_t *k, co
                             int H, int H_kv, int L, int D, const float *log_decay, const float *k_scale, float eps,
                             const prime_state_t *state_in, const prime_tensor_t *y, const prime_state_t *state_out,
                             void *workspace, size_t workspace_bytes, void *stream);
+/* prime_selective_prefill with the module's QK LayerNorm and scale applied
+ * on load by `norm` (selective.py:358-362), as prime_chunked_prefill_qknorm. */
+int prime_selective_prefill_qknorm(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                                   int B, int H, int H_kv, int L, int D, const float *log_decay,
+                                   const float *k_scale, float eps, const prime_qk_norm_t *norm,
+                                   const prime_state_t *state_in, const prime_tensor_t *y,
+                                   const prime_state_t *state_out, void *workspace, size_t workspace_bytes,
+                                   void *stream);
 int prime_selective_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
                                 int H, int H_kv, int D, const prime_selective_gate_t *gate, const float *k_scale,
                                 float eps, const prime_qk_norm_t *norm, const prime_state_t *state_in,

@@ -269,7 +269,7 @@ static int prefill_impl(const prime_tensor_t *q, const prime_tensor_t *k, const 
                         int H_kv, int L, int D, int chunk, const float *decay, float eps, unsigned flags,
                         const prime_state_t *state_in, const prime_tensor_t *y, const prime_state_t *state_out,
                         void *workspace, size_t workspace_bytes, void *stream, const float *log_decay,
-                        const float *k_scale) {
+                        const float *k_scale, const prime_qk_norm_t *norm = nullptr) {
     g_err[0] = 0;
     const bool selective = log_decay != nullptr;
     if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !(decay || selective) ||
@@ -302,6 +302,18 @@ static int prefill_impl(const prime_tensor_t *q, const prime_tensor_t *k, const 
     a.dense_clamp = (flags & PRIME_FLAG_DENSE_CLAMP) ? 1 : 0;
     if (selective && a.dense_clamp) return fail(PRIME_ERR_INVALID_ARG, "the selective form has no dense clamp");
     a.log_decay = log_decay; a.k_scale = k_scale;
+    if (norm) {
+        if (q->dtype != PRIME_BF16)
+            return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "the QK-norm prefill takes BF16 q/k/v");
+        if ((norm->q_weight == nullptr) != (norm->q_bias == nullptr) ||
+            (norm->k_weight == nullptr) != (norm->k_bias == nullptr))
+            return fail(PRIME_ERR_INVALID_ARG, "QK-norm: LayerNorm weight without bias or bias without weight");
+        if ((norm->q_weight || norm->k_weight) && !valid_dtype(norm->dtype))
+            return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported norm dtype");
+        a.qk_norm = 1;
+        a.qn_w = norm->q_weight; a.qn_b = norm->q_bias; a.kn_w = norm->k_weight; a.kn_b = norm->k_bias;
+        a.dt_norm = norm->dtype; a.ln_eps = norm->eps; a.q_scale = norm->q_scale;
+    }
     if (state_in) {
         a.s0i = state_in->s0; a.s1i = state_in->s1; a.s2i = state_in->s2;
         a.k0i = state_in->k0; a.k1i = state_in->k1; a.k2i = state_in->k2;
@@ -332,6 +344,19 @@ int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k, cons
     }
     return prefill_impl(q, k, v, B, H, H_kv, L, D, chunk, decay, eps, flags, state_in, y, state_out, workspace,
                         workspace_bytes, stream, nullptr, nullptr);
+}
+
+int prime_chunked_prefill_qknorm(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
+                                 int H, int H_kv, int L, int D, int chunk, const float *decay, float eps,
+                                 unsigned flags, const prime_qk_norm_t *norm, const prime_state_t *state_in,
+                                 const prime_tensor_t *y, const prime_state_t *state_out, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+    if (!decay || !norm) {
+        g_err[0] = 0;
+        return fail(PRIME_ERR_INVALID_ARG, "prime_chunked_prefill_qknorm: null decay or norm");
+    }
+    return prefill_impl(q, k, v, B, H, H_kv, L, D, chunk, decay, eps, flags, state_in, y, state_out, workspace,
+                        workspace_bytes, stream, nullptr, nullptr, norm);
 }
 
 int prime_accumulate(const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv, int L, int D,
@@ -524,6 +549,19 @@ int prime_selective_prefill(const prime_tensor_t *q, const prime_tensor_t *k, co
     }
     return prefill_impl(q, k, v, B, H, H_kv, L, D, 64, nullptr, eps, 0, state_in, y, state_out, workspace,
                         workspace_bytes, stream, log_decay, k_scale);
+}
+
+int prime_selective_prefill_qknorm(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,
+                                   int H, int H_kv, int L, int D, const float *log_decay, const float *k_scale,
+                                   float eps, const prime_qk_norm_t *norm, const prime_state_t *state_in,
+                                   const prime_tensor_t *y, const prime_state_t *state_out, void *workspace,
+                                   size_t workspace_bytes, void *stream) {
+    if (!log_decay || !k_scale || !norm) {
+        g_err[0] = 0;
+        return fail(PRIME_ERR_INVALID_ARG, "prime_selective_prefill_qknorm: null log_decay, k_scale or norm");
+    }
+    return prefill_impl(q, k, v, B, H, H_kv, L, D, 64, nullptr, eps, 0, state_in, y, state_out, workspace,
+                        workspace_bytes, stream, log_decay, k_scale, norm);
 }
 
 int prime_selective_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v, int B,

@@ -3,13 +3,16 @@
 //
 // Same algorithm and semantics as the generic kernel in prefill.hip (see its
 // header comment for the chunk equations and the operand layouts); this kernel
-// differs in its schedule:
-//   readout waves 0..3 only compute: score block, AV, state readout, y;
-//   update waves 4..7 own the state M = [S1; S2/2 | K] in MFMA accumulators and,
-//     in the step of chunk c, (a) add chunk c's contribution, (b) convert and
-//     store chunk c+1's tiles (loaded from HBM one chunk earlier) into the other
-//     tile buffer, (c) issue the HBM loads of chunk c+2 and (d) publish the bf16
-//     state copy entering chunk c+1 into the other state buffer.
+// differs in its schedule.  The fused pass runs 16 waves (the base form; the
+// selective form runs 4 + 4 with two feature blocks per update wave):
+//   readout waves 0..7 only compute, each for one query block and half of the
+//     value columns: score block, AV, state readout, y;
+//   update waves 8..15 own the state M = [S1; S2/2 | K] in MFMA accumulators,
+//     one feature block each, and, in the step of chunk c, (a) add chunk c's
+//     contribution, (b) convert and store chunk c+1's tiles (loaded from HBM one
+//     chunk earlier) into the other tile buffer, (c) issue the HBM loads of chunk
+//     c+2 and (d) publish the bf16 state copy entering chunk c+1 into the other
+//     state buffer.
 // Chunk c reads tile buffer c&1 and state buffer c&1 while chunk c+1's are
 // written, so one barrier per chunk orders every hazard.  S0 also accumulates
 // on MFMA: update wave u multiplies value block u of [w v] by an A operand whose
@@ -50,6 +53,70 @@ __device__ __forceinline__ u32x4 scale8(u32x4 x, float w) {
     u32x4 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[i] = pack2(w * __uint_as_float(x[i] << 16), w * __uint_as_float(x[i] & 0xFFFF0000u));
+    return r;
+}
+
+// x of lane (lane ^ M) for M = 4, 2, 1 (the partner in its group of 8 lanes),
+// by DPP moves on the VALU instead of a shuffle through the LDS unit:
+// M = 4 takes row_shl:4 in the first four lanes of each 8 and row_shr:4 in the
+// last four (bank masks), M = 2 and 1 are quad permutations.
+template <int M>
+__device__ __forceinline__ float xor8(float x) {
+    const int v = __float_as_int(x);
+    if constexpr (M == 4) {
+        int t = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0x5, false);  // row_shl:4, lanes 0-3 / 8-11
+        t = __builtin_amdgcn_update_dpp(t, v, 0x114, 0xF, 0xA, false);      // row_shr:4, lanes 4-7 / 12-15
+        return __int_as_float(t);
+    } else if constexpr (M == 2) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    } else {
+        static_assert(M == 1, "partners at 4, 2, 1");
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    }
+}
+
+// QK LayerNorm of one 64-element row held as 8 bf16 by each of 8 consecutive
+// lanes (this lane: columns col..col+7): the same arithmetic, summation order
+// and roundings as head_layernorm_kernel, so the result is bit-identical to
+// normalising the projections first.  affine false: no LayerNorm, the scale only.
+// Every lane of the wave takes part (the sums are lane shuffles).
+// (w, b: LDS rows of the parameters, read at columns col..col+7)
+__device__ __forceinline__ u32x4 norm_row8(u32x4 x, bool affine, const float *w, const float *b, int col, float eps,
+                                          float scale) {
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(x[i] << 16);
+        v[2 * i + 1] = __uint_as_float(x[i] & 0xFFFF0000u);
+    }
+    if (affine) {
+        float sm = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm += v[e];
+        sm += xor8<4>(sm);
+        sm += xor8<2>(sm);
+        sm += xor8<1>(sm);
+        const float mean = sm * (1.0f / kD);
+        float sq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            v[e] -= mean;
+            sq += v[e] * v[e];
+        }
+        sq += xor8<4>(sq);
+        sq += xor8<2>(sq);
+        sq += xor8<1>(sq);
+        const float rs = rsqrtf(sq * (1.0f / kD) + eps);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e] * rs * w[col + e] + b[col + e]));
+    }
+    if (scale != 1.0f) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e] * scale));
+    }
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = f32_to_bf16_bits(v[2 * i]) | (static_cast<uint32_t>(f32_to_bf16_bits(v[2 * i + 1])) << 16);
     return r;
 }
 
@@ -107,8 +174,8 @@ __device__ __forceinline__ void store_row(u32x4 q, u32x4 k, u32x4 v, int row, in
 
 // Wave layouts of the fused pass: UW8 = 8 update waves (one feature block each,
 // one tile row per thread) instead of 4; RH = 8 readout waves (query block x
-// half of the value columns) instead of 4.
-template <bool STATE_ONLY, bool SEL, bool UW8 = false, bool RH = false>
+// half of the value columns) instead of 4.  QKN: the QK LayerNorm on load.
+template <bool STATE_ONLY, bool SEL, bool UW8 = false, bool RH = false, bool QKN = false>
 __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 4)), 1) void prefill_bf16_kernel(
     const PrefillArgs a) {
     constexpr int NB = kD / 16;    // value blocks
@@ -136,6 +203,7 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
     __shared__ float sKi[KI];                                             // incoming [K1; K2/2] (dense)
     __shared__ float sKi0;                                                // incoming K0 (dense)
     __shared__ float sCum[SEL && !STATE_ONLY ? 2 : 1][kC];                // selective: log2 decay to token i
+    __shared__ float sLn[QKN ? 4 : 1][kD];                                // QKN: q weight, q bias, k weight, k bias
 
     const int tid = threadIdx.x;
     // wave index in a scalar register: every role / wave test below is then a
@@ -177,7 +245,14 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
             sPm[tid] = tid >= kC - 1 ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(tid - (kC - 1))))
                                      : 0.f;
     }
-    __syncthreads();  // the power tables are read by the first tile stores below
+    if constexpr (QKN) {
+        if (tid < 4 * kD) {
+            const int t = tid >> 6, e = tid & (kD - 1);
+            const void *src = t == 0 ? a.qn_w : t == 1 ? a.qn_b : t == 2 ? a.kn_w : a.kn_b;
+            sLn[t][e] = src ? load_elem(src, e, a.dt_norm) : 0.f;
+        }
+    }
+    __syncthreads();  // the power tables (and QKN's parameters) are read by the first tile stores below
 
     // ---- update role: state registers, tile pointers, first tiles
     const size_t so1 = static_cast<size_t>(seq) * kD * kD;
@@ -222,6 +297,17 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
         } else {
             wa = va ? sPw[nv - 1 - ra] : 0.f;
             wb = vb ? sPw[nv - 1 - (ra + 32)] : 0.f;
+        }
+        if constexpr (QKN) {
+            // the module's QK LayerNorm (and q's scale) on the raw projections
+            const bool qa = a.qn_w != nullptr, ka = a.kn_w != nullptr;
+            if constexpr (!STATE_ONLY) {
+                T.q0 = norm_row8(T.q0, qa, sLn[0], sLn[1], col, a.ln_eps, a.q_scale);
+                if constexpr (!UW8) T.q1 = norm_row8(T.q1, qa, sLn[0], sLn[1], col, a.ln_eps, a.q_scale);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // one row's temporaries at a time
+            T.k0 = norm_row8(T.k0, ka, sLn[2], sLn[3], col, a.ln_eps, 1.0f);
+            if constexpr (!UW8) T.k1 = norm_row8(T.k1, ka, sLn[2], sLn[3], col, a.ln_eps, 1.0f);
         }
         uint16_t *pq = &sQf[STATE_ONLY ? 0 : xb][0][0], *pv = &sV[STATE_ONLY ? 0 : xb][0][0];
         const bool ragged = nv < kC;
@@ -569,17 +655,23 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
     if (SEL && STATE_ONLY && u == 0 && lane == 0) wslot[kWsDecay] = seg_ld;
 }
 
-void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream, TimerEvents t) {
+template <bool QKN>
+static void launch_variant_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream, TimerEvents t) {
     const bool sel = a.log_decay != nullptr;
     const dim3 g(grid), blk(state_only ? 256 : (sel ? 512 : 1024));
     if (state_only && sel)
-        hipExtLaunchKernelGGL(prefill_bf16_kernel<true, true>, g, blk, 0, stream, t.start, t.stop, 0, a);
+        hipExtLaunchKernelGGL((prefill_bf16_kernel<true, true, false, false, QKN>), g, blk, 0, stream, t.start, t.stop, 0, a);
     else if (state_only)
-        hipExtLaunchKernelGGL(prefill_bf16_kernel<true, false>, g, blk, 0, stream, t.start, t.stop, 0, a);
+        hipExtLaunchKernelGGL((prefill_bf16_kernel<true, false, false, false, QKN>), g, blk, 0, stream, t.start, t.stop, 0, a);
     else if (sel)
-        hipExtLaunchKernelGGL(prefill_bf16_kernel<false, true>, g, blk, 0, stream, t.start, t.stop, 0, a);
+        hipExtLaunchKernelGGL((prefill_bf16_kernel<false, true, false, false, QKN>), g, blk, 0, stream, t.start, t.stop, 0, a);
     else
-        hipExtLaunchKernelGGL((prefill_bf16_kernel<false, false, true, true>), g, blk, 0, stream, t.start, t.stop, 0, a);
+        hipExtLaunchKernelGGL((prefill_bf16_kernel<false, false, true, true, QKN>), g, blk, 0, stream, t.start, t.stop, 0, a);
+}
+
+void launch_prefill_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream, TimerEvents t) {
+    if (a.qk_norm) launch_variant_bf16<true>(a, state_only, grid, stream, t);
+    else launch_variant_bf16<false>(a, state_only, grid, stream, t);
 }
 
 }  // namespace prime

@@ -110,6 +110,14 @@ struct PrefillArgs {
     // segment-entry states only (G > 1): the state-only pass and the
     // exclusive scan, leaving the state entering segment s in slot s
     int states_only;
+    // QK LayerNorm on load (bf16 inputs): each q and k row is normalised with
+    // the per-column weight and bias (the module's nn.LayerNorm, eps ln_eps) and
+    // rounded to bf16, and q is then scaled by q_scale and rounded again;
+    // qn_w null: q is only scaled; kn_w null: k is used as it is
+    int qk_norm;
+    const void *qn_w, *qn_b, *kn_w, *kn_b;
+    int dt_norm;
+    float ln_eps, q_scale;
 };
 
 // packed fp32 state slot in the workspace: S1 | S2 | S0 | K1 | K2 | K0

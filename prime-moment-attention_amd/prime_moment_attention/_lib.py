@@ -29,7 +29,8 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_head_layernorm", "prime_linear", "prime_selective_prefill",
            "prime_selective_decode_step", "prime_accumulate", "prime_accumulate_workspace_size",
            "prime_decode_readout", "prime_decode_update", "prime_chunked_prefill_backward",
-           "prime_chunked_prefill_backward_workspace_size")
+           "prime_chunked_prefill_backward_workspace_size", "prime_chunked_prefill_qknorm",
+           "prime_selective_prefill_qknorm")
 
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
@@ -114,6 +115,14 @@ def load() -> ctypes.CDLL:
         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, P(PrimeState), P(PrimeTensor), P(PrimeState),
         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     L.prime_selective_prefill.restype = ctypes.c_int
+    L.prime_chunked_prefill_qknorm.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 6 + [
+        ctypes.c_void_p, ctypes.c_float, ctypes.c_uint, P(PrimeQkNorm), P(PrimeState), P(PrimeTensor),
+        P(PrimeState), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    L.prime_chunked_prefill_qknorm.restype = ctypes.c_int
+    L.prime_selective_prefill_qknorm.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 5 + [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, P(PrimeQkNorm), P(PrimeState), P(PrimeTensor),
+        P(PrimeState), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    L.prime_selective_prefill_qknorm.restype = ctypes.c_int
     L.prime_selective_decode_step.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 4 + [
         P(PrimeSelectiveGate), ctypes.c_void_p, ctypes.c_float, P(PrimeQkNorm), P(PrimeState), P(PrimeState),
         P(PrimeTensor), ctypes.c_void_p]
@@ -265,6 +274,22 @@ def qk_norm(q_norm, k_norm, q_scale: float, dtype) -> PrimeQkNorm:
     return PrimeQkNorm(*[t.data_ptr() for t in ps], _DTYPES[dtype], float(q_norm.eps), float(q_scale))
 
 
+def qk_norm_on_load(q_norm, k_norm, q_scale: float, q: torch.Tensor) -> Optional[PrimeQkNorm]:
+    """The QK-norm for the bf16 prefill kernels to apply as they load q and k,
+    or None where q and k must be normalised first: projections other than
+    bf16, LayerNorm parameters of another dtype or device, or q and k
+    LayerNorms with different eps (the kernels take one)."""
+    if q.dtype != torch.bfloat16:
+        return None
+    if q_norm is not None:
+        ps = (q_norm.weight, q_norm.bias, k_norm.weight, k_norm.bias)
+        if any(t is None or t.dtype != q.dtype or not t.is_contiguous() or t.device != q.device for t in ps):
+            return None
+        if q_norm.eps != k_norm.eps:
+            return None
+    return qk_norm(q_norm, k_norm, q_scale, q.dtype)
+
+
 def decode_step_qknorm(q, k, v, decay: torch.Tensor, eps: float, norm: PrimeQkNorm, state_in, state_out,
                        y) -> None:
     """prime_decode_step_qknorm: q, k the raw projections [B,H,D] / [B,Hkv,D];
@@ -401,12 +426,20 @@ def _prefill_args(q, k, v, decay, eps, chunk, state_in, y, state_out, flags, wor
 
 
 def chunked_prefill(q, k, v, decay: torch.Tensor, eps: float, chunk: int, state_in, y,
-                    state_out, flags: int = 0, workspace: Optional[torch.Tensor] = None) -> None:
+                    state_out, flags: int = 0, workspace: Optional[torch.Tensor] = None,
+                    qk_norm: Optional[PrimeQkNorm] = None) -> None:
     """Chunked prefill (prime_chunked_prefill).  q [B,H,L,D], k/v [B,Hkv,L,D].
     workspace: None allocates the recommended scratch from torch's caching
-    allocator; pass an empty tensor to run one segment per sequence."""
+    allocator; pass an empty tensor to run one segment per sequence.
+    qk_norm (``qk_norm(...)``, bf16 only): q, k are the raw projections and the
+    module's QK LayerNorm and q scale are applied as the kernels load them
+    (prime_chunked_prefill_qknorm)."""
     args, keep = _prefill_args(q, k, v, decay, eps, chunk, state_in, y, state_out, flags, workspace)
-    _check(load().prime_chunked_prefill(*args, _stream(q.device)), "prime_chunked_prefill")
+    if qk_norm is None:
+        _check(load().prime_chunked_prefill(*args, _stream(q.device)), "prime_chunked_prefill")
+    else:
+        args = args[:12] + (ctypes.byref(qk_norm),) + args[12:]
+        _check(load().prime_chunked_prefill_qknorm(*args, _stream(q.device)), "prime_chunked_prefill_qknorm")
     del keep
 
 
@@ -417,17 +450,23 @@ def _sel_vec(t: torch.Tensor, n: int, name: str) -> None:
 
 
 def selective_prefill(q, k, v, log_decay: torch.Tensor, k_scale: torch.Tensor, eps: float, state_in, y,
-                      state_out, workspace: Optional[torch.Tensor] = None) -> None:
+                      state_out, workspace: Optional[torch.Tensor] = None,
+                      qk_norm: Optional[PrimeQkNorm] = None) -> None:
     """Selective PRIME prefill (prime_selective_prefill): bf16 q [B,H,L,D],
     k/v [B,Hkv,L,D]; log_decay fp32 [B,H,L] (log lambda_t, contiguous);
-    k_scale fp32 [H] (beta); states in the selective convention."""
+    k_scale fp32 [H] (beta); states in the selective convention.  qk_norm: as
+    for chunked_prefill (prime_selective_prefill_qknorm)."""
     B, H, Lq, D = q.shape
     _sel_vec(log_decay, B * H * Lq, "log_decay")
     _sel_vec(k_scale, H, "k_scale")
     # the decay argument of the base form is not used: pass the k scale for the checks
     args, keep = _prefill_args(q, k, v, k_scale, eps, 64, state_in, y, state_out, 0, workspace)
-    args = args[:8] + (ctypes.c_void_p(log_decay.data_ptr()), ctypes.c_void_p(k_scale.data_ptr()), args[10]) + args[12:]
-    _check(load().prime_selective_prefill(*args, _stream(q.device)), "prime_selective_prefill")
+    head = args[:8] + (ctypes.c_void_p(log_decay.data_ptr()), ctypes.c_void_p(k_scale.data_ptr()), args[10])
+    if qk_norm is None:
+        _check(load().prime_selective_prefill(*(head + args[12:]), _stream(q.device)), "prime_selective_prefill")
+    else:
+        _check(load().prime_selective_prefill_qknorm(*(head + (ctypes.byref(qk_norm),) + args[12:]),
+                                                      _stream(q.device)), "prime_selective_prefill_qknorm")
     del keep
 
 

@@ -82,13 +82,23 @@ class PrimeMomentAttention(nn.Module):
         v = self.v_proj(hidden_states).view(B, L, self.num_kv_heads, self.head_dim).transpose(1, 2)
         if not normalize:
             return q, k, v
-        # QK-norm and the 1/sqrt(D) scale in place on the fresh projections
-        # (prime_head_layernorm, the module's rounding), read by the prefill
-        # kernel through the [B, L, H, D] strides
+        self._normalize(q, k)
+        return q, k, v
+
+    def _normalize(self, q: torch.Tensor, k: torch.Tensor) -> None:
+        """QK-norm and the 1/sqrt(D) scale in place on the fresh projections
+        (prime_head_layernorm, the module's rounding), read by the prefill
+        kernel through the [B, L, H, D] strides."""
         _lib.head_layernorm(q, q, self.q_norm if self.use_qk_norm else None, self.scaling)
         if self.use_qk_norm:
             _lib.head_layernorm(k, k, self.k_norm, 1.0)
-        return q, k, v
+
+    def _load_norm(self, q: torch.Tensor):
+        """The QK-norm for the prefill kernels to apply as they load q and k
+        (bf16 projections with LayerNorm parameters of that dtype and one eps),
+        or None when q and k are to be normalised first."""
+        return _lib.qk_norm_on_load(self.q_norm if self.use_qk_norm else None,
+                                    self.k_norm if self.use_qk_norm else None, self.scaling, q)
 
     def forward(
         self,
@@ -134,7 +144,10 @@ class PrimeMomentAttention(nn.Module):
             y = y.unsqueeze(2)
             next_state = st_out
         else:
-            q, k, v = self.project(hidden_states)
+            q, k, v = self.project(hidden_states, normalize=False)
+            norm = self._load_norm(q)
+            if norm is None:
+                self._normalize(q, k)
             dense = L <= self.chunk_threshold
             st_out = None
             if return_state and self.inplace_state and state is not None:
@@ -146,7 +159,7 @@ class PrimeMomentAttention(nn.Module):
             y, next_state = prime_prefill(q, k, v, state=state, decay=self.decay, eps=self.eps,
                                           chunk_size=self.chunk_size, return_state=return_state,
                                           out_dtype=y_dtype, dense_clamp=dense, state_out=st_out,
-                                          y=y_bl.transpose(1, 2))
+                                          y=y_bl.transpose(1, 2), qk_norm=norm)
 
         y = y.to(orig_dtype).transpose(1, 2).reshape(B, L, H * D)
         output = self.o_proj(y)

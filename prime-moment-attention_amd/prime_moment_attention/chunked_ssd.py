@@ -105,13 +105,15 @@ class _PrefillFn(torch.autograd.Function):
 
 
 def prime_prefill(q, k, v, state=None, decay=0.9995, eps=1.0, chunk_size=64, return_state=False,
-                  out_dtype=torch.float32, dense_clamp=False, state_out=None, y=None):
+                  out_dtype=torch.float32, dense_clamp=False, state_out=None, y=None, qk_norm=None):
     """Core launcher shared by the modules.  Returns (y, next_state | None);
     ``y`` may be a caller-provided [B, H, L, D] view (any strides with a
     contiguous D and 16-byte aligned rows).  When autograd records (an input
     requires grad), the call is differentiable -- in q, k, v and the incoming
     state -- through the HIP backward; ``y`` and ``state_out`` are then not
-    used (fresh outputs are returned)."""
+    used (fresh outputs are returned).  ``qk_norm`` (``_lib.qk_norm(...)``,
+    bf16 only, no autograd): q and k are the raw projections and the module's
+    QK LayerNorm and q scale are applied by the kernels as they load them."""
     B, H, L, D = q.shape
     q, k, v = _prep(q), _prep(k), _prep(v)
     if k.dtype != q.dtype or v.dtype != q.dtype:
@@ -120,6 +122,8 @@ def prime_prefill(q, k, v, state=None, decay=0.9995, eps=1.0, chunk_size=64, ret
     dec = _lib.decay_tensor(decay, H, dev)
     st_in = _lib.as_state(state, B, H, D, dev) if state is not None else None
     if needs_grad(q, k, v, *(st_in or ())):
+        if qk_norm is not None:
+            raise NotImplementedError("the QK-norm on load has no backward; normalise q and k with torch ops")
         if dense_clamp and st_in is not None:
             raise NotImplementedError("the dense branch's double clamp with an incoming state has no backward "
                                       "here; call under torch.no_grad() or without a state")
@@ -134,7 +138,7 @@ def prime_prefill(q, k, v, state=None, decay=0.9995, eps=1.0, chunk_size=64, ret
     if return_state:
         st_out = state_out if state_out is not None else _lib.new_state(B, H, D, dev)
     _lib.chunked_prefill(q, k, v, dec, eps, chunk_size, st_in, y, st_out,
-                         _lib.PRIME_FLAG_DENSE_CLAMP if dense_clamp else 0)
+                         _lib.PRIME_FLAG_DENSE_CLAMP if dense_clamp else 0, qk_norm=qk_norm)
     return y, st_out
 
 

@@ -113,15 +113,21 @@ class PrimeSelectiveMomentAttention(nn.Module):
         else:
             if q.dtype != torch.bfloat16:
                 q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
-            _lib.head_layernorm(q, q, self.q_norm if self.use_qk_norm else None, self.scaling)
-            if self.use_qk_norm:
-                _lib.head_layernorm(k, k, self.k_norm, 1.0)
+            # the QK LayerNorm and scale as the kernels load q and k (or first,
+            # in place, where the parameters do not allow that)
+            norm = _lib.qk_norm_on_load(self.q_norm if self.use_qk_norm else None,
+                                        self.k_norm if self.use_qk_norm else None, self.scaling, q)
+            if norm is None:
+                _lib.head_layernorm(q, q, self.q_norm if self.use_qk_norm else None, self.scaling)
+                if self.use_qk_norm:
+                    _lib.head_layernorm(k, k, self.k_norm, 1.0)
             # per-token log decays -(Delta / tau), [B, H, L]
             delta = self.step_size(hidden_states)  # [B, L, H]
             log_decay = (-delta.float() / tau.view(1, 1, H)).transpose(1, 2).contiguous()
             y_bl = torch.empty(B, L, H, D, device=dev, dtype=y_dtype)
             next_state = _lib.new_state(B, H, D, dev) if return_state else None
-            _lib.selective_prefill(q, k, v, log_decay, beta, self.eps, None, y_bl.transpose(1, 2), next_state)
+            _lib.selective_prefill(q, k, v, log_decay, beta, self.eps, None, y_bl.transpose(1, 2), next_state,
+                                   qk_norm=norm)
             y = y_bl.transpose(1, 2)
         y = no_backward("selective PRIME", y, q, k, v, tau, beta, hidden_states,
                         *(state if state is not None else ()))
