@@ -56,25 +56,6 @@ __device__ __forceinline__ u32x4 scale8(u32x4 x, float w) {
     return r;
 }
 
-// x of lane (lane ^ M) for M = 4, 2, 1 (the partner in its group of 8 lanes),
-// by DPP moves on the VALU instead of a shuffle through the LDS unit:
-// M = 4 takes row_shl:4 in the first four lanes of each 8 and row_shr:4 in the
-// last four (bank masks), M = 2 and 1 are quad permutations.
-template <int M>
-__device__ __forceinline__ float xor8(float x) {
-    const int v = __float_as_int(x);
-    if constexpr (M == 4) {
-        int t = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0x5, false);  // row_shl:4, lanes 0-3 / 8-11
-        t = __builtin_amdgcn_update_dpp(t, v, 0x114, 0xF, 0xA, false);      // row_shr:4, lanes 4-7 / 12-15
-        return __int_as_float(t);
-    } else if constexpr (M == 2) {
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
-    } else {
-        static_assert(M == 1, "partners at 4, 2, 1");
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
-    }
-}
-
 // QK LayerNorm of one 64-element row held as 8 bf16 by each of 8 consecutive
 // lanes (this lane: columns col..col+7): the same arithmetic, summation order
 // and roundings as head_layernorm_kernel, so the result is bit-identical to
@@ -93,9 +74,9 @@ __device__ __forceinline__ u32x4 norm_row8(u32x4 x, bool affine, const float *w,
         float sm = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) sm += v[e];
-        sm += xor8<4>(sm);
-        sm += xor8<2>(sm);
-        sm += xor8<1>(sm);
+        sm += xor_lane<4>(sm);
+        sm += xor_lane<2>(sm);
+        sm += xor_lane<1>(sm);
         const float mean = sm * (1.0f / kD);
         float sq = 0.f;
 #pragma unroll
@@ -103,9 +84,9 @@ __device__ __forceinline__ u32x4 norm_row8(u32x4 x, bool affine, const float *w,
             v[e] -= mean;
             sq += v[e] * v[e];
         }
-        sq += xor8<4>(sq);
-        sq += xor8<2>(sq);
-        sq += xor8<1>(sq);
+        sq += xor_lane<4>(sq);
+        sq += xor_lane<2>(sq);
+        sq += xor_lane<1>(sq);
         const float rs = rsqrtf(sq * (1.0f / kD) + eps);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e] * rs * w[col + e] + b[col + e]));

@@ -344,9 +344,11 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
 #pragma unroll
             for (int r = 0; r < 4; ++r) dsum += sT[jb][r];
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float qv = bf16_bits_to_f32(sQf[iw][(32 * g + e) & (kD - 1)]);
-            dcar += (g < 2 ? qv : qv * qv) * sKv[32 * g + e];
+        for (int t = 0; t < 4; ++t) {  // features 32g + 8t + 0..7 of row iw, one 16-byte read
+            float qf[8];
+            unpack8(lds128(&sQf[iw][((32 * g) & (kD - 1)) + 8 * t]), qf);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dcar += (g < 2 ? qf[e] : qf[e] * qf[e]) * sKv[32 * g + 8 * t + e];
         }
         dsum += __shfl_xor(dsum, 16, kWave);
         dsum += __shfl_xor(dsum, 32, kWave);
@@ -368,10 +370,10 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
                 part += dyv * (acc[nb][r] * inv);
                 gn[nb] = valid ? dyv * inv : 0.f;
             }
-            part += __shfl_xor(part, 1, kWave);
-            part += __shfl_xor(part, 2, kWave);
-            part += __shfl_xor(part, 4, kWave);
-            part += __shfl_xor(part, 8, kWave);
+            part += xor_lane<1>(part);
+            part += xor_lane<2>(part);
+            part += xor_lane<4>(part);
+            part += xor_lane<8>(part);
             const float gden = (valid && den >= a.eps) ? -part * inv : 0.f;
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb) sG[i][16 * nb + c16] = f32_to_bf16_bits(gn[nb]);
@@ -439,9 +441,17 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
                 const int i = 16 * w + 4 * g + r;
                 ok[r] = i < nvalid;
                 o[r] = b * a.g_sb + h * a.g_sh + static_cast<int64_t>(c * kC + i) * a.g_sl;
+            }
 #pragma unroll
-                for (int fb = 0; fb < 4; ++fb)
-                    dv[r][fb] = dphi[fb][r] + 2.0f * bf16_bits_to_f32(sQf[i][16 * fb + c16]) * dphi[fb + 4][r];
+            for (int fb = 0; fb < 4; ++fb) {
+                // q of rows 16w + 4g + r at column 16fb + c16: one transposed read
+                const uint2 qt = lds_tr(&sQf[16 * w + 4 * g + tr_r][16 * fb + tr_c]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t qw = r < 2 ? qt.x : qt.y;
+                    const float qv = __uint_as_float((r & 1) ? qw & 0xFFFF0000u : qw << 16);
+                    dv[r][fb] = dphi[fb][r] + 2.0f * qv * dphi[fb + 4][r];
+                }
             }
             store_rows4(a.dq, a.dt_g, o, ok, c16, dv);
         }
