@@ -350,10 +350,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
 #pragma unroll
             for (int e = 0; e < 8; ++e) dcar += (g < 2 ? qf[e] : qf[e] * qf[e]) * sKv[32 * g + 8 * t + e];
         }
-        dsum += __shfl_xor(dsum, 16, kWave);
-        dsum += __shfl_xor(dsum, 32, kWave);
-        dcar += __shfl_xor(dcar, 16, kWave);
-        dcar += __shfl_xor(dcar, 32, kWave);
+        dsum = sum_lane32(sum_lane16(dsum));
+        dcar = sum_lane32(sum_lane16(dcar));
         const float den_iw = dsum + pinc * (dcar + sK0[0]);
         // ---- G of rows i = 16w + 4g + r
 #pragma unroll
@@ -760,11 +758,15 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
         {
             float dv[4][4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
+            for (int fb = 0; fb < 4; ++fb) {
+                // k of rows 16w + 4g + r at column 16fb + c16: one transposed read
+                const uint2 kt = lds_tr(&sKf[16 * w + 4 * g + tr_r][16 * fb + tr_c]);
 #pragma unroll
-                for (int fb = 0; fb < 4; ++fb)
-                    dv[r][fb] = dphi[fb][r] +
-                                bf16_bits_to_f32(sKf[16 * w + 4 * g + r][16 * fb + c16]) * dphi[fb + 4][r];
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t kw = r < 2 ? kt.x : kt.y;
+                    dv[r][fb] = dphi[fb][r] + __uint_as_float((r & 1) ? kw & 0xFFFF0000u : kw << 16) * dphi[fb + 4][r];
+                }
+            }
             store_rows4(a.dk, a.dt_g, orow, okr, c16, dv);
         }
         }  // !DUAL

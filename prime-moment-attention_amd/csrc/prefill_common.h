@@ -100,6 +100,18 @@ __device__ __forceinline__ float xor_lane(float x) {
     }
 }
 
+// x + x of lane (lane ^ 16), or (lane ^ 32), on the VALU: a v_permlane16_swap /
+// v_permlane32_swap of x with itself leaves, in every lane, its own x in one
+// result and its partner's in the other, so their sum is the pair's sum.
+__device__ __forceinline__ float sum_lane16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_lane32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // 16-byte LDS read
 __device__ __forceinline__ u32x4 lds128(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
