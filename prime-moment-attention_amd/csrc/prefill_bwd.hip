@@ -229,22 +229,6 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
         sG[row][cc] = 0u;
     }
 
-    // readout constants of this lane: row iw of the transposed blocks, rows
-    // 16w + 4g + r of the [num | den] accumulators
-    const int iw = 16 * w + c16;
-    float mask[4][4];
-#pragma unroll
-    for (int jb = 0; jb < 4; ++jb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int d = iw - (16 * jb + 4 * g + r);
-            mask[jb][r] = (jb <= w && d >= 0) ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(d))) : 0.f;
-        }
-    const float pinc = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(iw + 1)));
-    float pinr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-        pinr[r] = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(16 * w + 4 * g + r + 1)));
 
     // value columns of M (features 32w..32w+31 of this wave, value blocks 0..3) from state_in
     f32x4 st[2][4];
@@ -287,6 +271,22 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
     };
 
     __syncthreads();  // power tables
+    // readout constants of this lane: row iw of the transposed blocks, rows
+    // 16w + 4g + r of the [num | den] accumulators (powers from the table:
+    // sPw[n] is l^n rounded from fp64)
+    const int iw = 16 * w + c16;
+    float mask[4][4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int d = iw - (16 * jb + 4 * g + r);
+            mask[jb][r] = (jb <= w && d >= 0) ? sPw[max(d, 0)] : 0.f;
+        }
+    const float pinc = sPw[iw + 1];
+    float pinr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pinr[r] = sPw[16 * w + 4 * g + r + 1];
     load_rows(R, a, b, h, c_begin, ra, col, true, true, false);
     store_rows(c_begin);
     publish();
@@ -571,14 +571,6 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
 
     // this lane's key row jw of the transposed blocks; rows 16w + 4g + r of the outputs
     const int jw = 16 * w + c16;
-    float mask[4][4];  // l^(i-j) [i >= j] for i = 16ib + 4g + r, j = jw
-#pragma unroll
-    for (int ib = 0; ib < 4; ++ib)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int d = 16 * ib + 4 * g + r - jw;
-            mask[ib][r] = (ib >= w && d >= 0) ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(d))) : 0.f;
-        }
 
     // dual state W (features 32w..32w+31, value blocks 0..4) from the final state's adjoint
     f32x4 st[2][5];
@@ -649,6 +641,14 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
     };
 
     __syncthreads();  // power table
+    float mask[4][4];  // l^(i-j) [i >= j] for i = 16ib + 4g + r, j = jw (sPw[n]: l^n rounded from fp64)
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int d = 16 * ib + 4 * g + r - jw;
+            mask[ib][r] = (ib >= w && d >= 0) ? sPw[max(d, 0)] : 0.f;
+        }
     load_rows(R, a, b, h, c_end - 1, ra, col, true, !DUAL, true);
     store_rows(c_end - 1);
     publish();
