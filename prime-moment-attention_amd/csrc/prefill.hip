@@ -369,15 +369,15 @@ __global__ __launch_bounds__(512, 1) void prefill_kernel(const PrefillArgs a) {
     const int iw = 16 * wave + c16;
     float mask[4][4];  // l^(i-j) [i >= j] for S^T[j = 16jb + 4g + r][i = iw]
     float pin = 0.f;   // l^(iw+1)
-    if (!is_u) {
+    if (!is_u) {  // from the power table (sPw[n]: l^n rounded from fp64)
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int d = iw - (16 * jb + 4 * g + r);
-                mask[jb][r] = (jb <= wave && d >= 0) ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(d))) : 0.f;
+                mask[jb][r] = (jb <= wave && d >= 0) ? sPw[max(d, 0)] : 0.f;
             }
-        pin = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(iw + 1)));
+        pin = sPw[iw + 1];
     }
 
     // ---- tiles: readout waves load q, k; update waves load v (and k when STATE_ONLY).

@@ -392,10 +392,10 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
     #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int d = iw - (16 * jb + 4 * g + r);
-                        mask[jb][r] = (jb <= rb && d >= 0) ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(d))) : 0.f;
+                        mask[jb][r] = (jb <= rb && d >= 0) ? sPw[max(d, 0)] : 0.f;
                     }
             }
-            pin = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(iw + 1)));
+            pin = sPw[iw + 1];  // the power tables: sPw[n] is l^n rounded from fp64
         }
         // dense: l^(64 c) of the chunk, advanced by one chunk decay per step
         float dcr = dense ? static_cast<float>(pow(static_cast<double>(lam), 64.0 * c_begin)) : 0.f;
