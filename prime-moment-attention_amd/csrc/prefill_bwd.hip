@@ -182,8 +182,11 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
     __shared__ __attribute__((aligned(16))) uint16_t sSt[kD][kPW];   // bf16 value columns of M^T entering the chunk
     // fp32: the K column of M (the denominator's moments) entering the chunk, S0, K0
     __shared__ float sKv[kF], sS0[kD], sK0[1], sGd[kC], sPg[kC], sPw[kC + 2], sPs[kC + 2];
-    __shared__ float sRedK[4][kF], sRedS[8][kD];  // partial sums of the K and S0 updates
+    __shared__ float sRedK[kF], sRedS[kD];  // the chunk's K and S0 increments
     __shared__ __attribute__((aligned(16))) float sWt[kC];  // the chunk's state-update weights l^(n-1-j)
+    // the same weights split into three bf16 parts (hi, mid, lo: about fp32 precision
+    // in sum), row 3 zero: an MFMA operand whose columns (or rows) 0..2 are the parts
+    __shared__ __attribute__((aligned(16))) uint16_t sWp[4][kC];
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -228,6 +231,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
         sV[row][cc] = 0u;
         sG[row][cc] = 0u;
     }
+    if (tid < kC) sWp[3][tid] = 0u;
 
 
     // value columns of M (features 32w..32w+31 of this wave, value blocks 0..3) from state_in
@@ -295,7 +299,16 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
     for (int c = c_begin; c < c_end; ++c) {
         const int nvalid = min(kC, a.L - c * kC);
         __syncthreads();  // tiles of chunk c and M_c in LDS
-        if (tid < kC) sWt[tid] = tid < nvalid ? sPw[nvalid - 1 - tid] : 0.f;  // read after the next barrier
+        if (tid < kC) {  // read after the next barrier
+            const float wv = tid < nvalid ? sPw[nvalid - 1 - tid] : 0.f;
+            sWt[tid] = wv;
+            const uint16_t hi = f32_to_bf16_bits(wv);
+            const float r1 = wv - bf16_bits_to_f32(hi);
+            const uint16_t mid = f32_to_bf16_bits(r1);
+            sWp[0][tid] = hi;
+            sWp[1][tid] = mid;
+            sWp[2][tid] = f32_to_bf16_bits(r1 - bf16_bits_to_f32(mid));
+        }
         // ---- scores S^T[j][iw] (blocks jb <= w), masked: A = l^(i-j) (1 + phi_q . phi_k)
         f32x4 sT[4];
 #pragma unroll
@@ -462,6 +475,11 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) st[fi][nb][r] *= ln;
+        // K and S0 increments on MFMA, against the three parts of w (fp32-accurate
+        // sums: K decides the clamp): dk[fi] rows = features, columns 0..2 = parts;
+        // ds0 rows 0..2 = parts, columns = value block w
+        f32x4 dk[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        f32x4 ds0 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             float wt[8];
@@ -474,59 +492,47 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
                     wt[4 + t] = w1[t];
                 }
             }
+            // lane (g, c16): part min(c16, 3) of w at its eight token slots, the
+            // same slots as the transposed operands (token 32ks + 16(t/4) + 4g + t%4)
+            const int pr = min(c16, 3);
+            const uint2 p0 = *reinterpret_cast<const uint2 *>(&sWp[pr][32 * ks + 4 * g]);
+            const uint2 p1 = *reinterpret_cast<const uint2 *>(&sWp[pr][32 * ks + 16 + 4 * g]);
+            const bf16x8 wpart = as_bf16x8(u32x4{p0.x, p0.y, p1.x, p1.y});
             bf16x8 ak[2];
 #pragma unroll
             for (int fi = 0; fi < 2; ++fi) {
-                const uint16_t *p0 = &sKf[32 * ks + 4 * g + tr_r][16 * (2 * w + fi) + tr_c];
-                ak[fi] = scale_op(tr_op<false>(p0, p0 + 16 * kPW, 0).h, wt);
+                const uint16_t *pk = &sKf[32 * ks + 4 * g + tr_r][16 * (2 * w + fi) + tr_c];
+                const bf16x8 raw = tr_op<false>(pk, pk + 16 * kPW, 0).h;
+                dk[fi] = mfma(raw, wpart, dk[fi]);
+                ak[fi] = scale_op(raw, wt);
             }
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb) {
-                const uint16_t *p0 = &sV[32 * ks + 4 * g + tr_r][16 * nb + tr_c];
-                const bf16x8 vb = tr_op<false>(p0, p0 + 16 * kPV, 0).h;
+                const uint16_t *p0v = &sV[32 * ks + 4 * g + tr_r][16 * nb + tr_c];
+                const bf16x8 vb = tr_op<false>(p0v, p0v + 16 * kPV, 0).h;
 #pragma unroll
                 for (int fi = 0; fi < 2; ++fi) st[fi][nb] = mfma(ak[fi], vb, st[fi][nb]);
+                if (nb == w) ds0 = mfma(wpart, vb, ds0);  // wave-uniform
             }
         }
         {
-            // K[f]: sum_j w_j phi_k(j)[f] (phi_k from the bf16 k): feature pairs x token quarters
-            const int f0 = 2 * (tid & 63), j0 = 16 * (tid >> 6);
-            const bool sq = f0 >= kD;
-            float s0 = 0.f, s1 = 0.f;
+            // K increment of features 16(2w + fi) + 4g + r: the quad (columns 0..3) sum
 #pragma unroll
-            for (int j = j0; j < j0 + 16; ++j) {
-                const uint32_t u = *reinterpret_cast<const uint32_t *>(&sKf[j][f0 & (kD - 1)]);
-                float x0 = __uint_as_float(u << 16), x1 = __uint_as_float(u & 0xFFFF0000u);
-                if (sq) {
-                    x0 = 0.5f * x0 * x0;
-                    x1 = 0.5f * x1 * x1;
+            for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = dk[fi][r];
+                    x += xor_lane<1>(x);
+                    x += xor_lane<2>(x);
+                    if (c16 == 0) sRedK[16 * (2 * w + fi) + 4 * g + r] = x;
                 }
-                const float wj = sWt[j];
-                s0 += wj * x0;
-                s1 += wj * x1;
-            }
-            *reinterpret_cast<f32x2 *>(&sRedK[tid >> 6][f0]) = f32x2{s0, s1};
-            // S0[n]: sum_j w_j v_j[n]: column pairs x eighths of the tokens
-            const int n0 = 2 * (tid & 31), i0 = 8 * (tid >> 5);
-            float v0 = 0.f, v1 = 0.f;
-#pragma unroll
-            for (int j = i0; j < i0 + 8; ++j) {
-                const uint32_t u = *reinterpret_cast<const uint32_t *>(&sV[j][n0]);
-                const float wj = sWt[j];
-                v0 += wj * __uint_as_float(u << 16);
-                v1 += wj * __uint_as_float(u & 0xFFFF0000u);
-            }
-            *reinterpret_cast<f32x2 *>(&sRedS[tid >> 5][n0]) = f32x2{v0, v1};
+            // S0 increment of value column 16w + c16: rows 0..2 (lane group g = 0)
+            if (g == 0) sRedS[16 * w + c16] = (ds0[0] + ds0[1]) + ds0[2];
         }
         __syncthreads();  // every read of chunk c's tiles and of M_c is done; partial sums in LDS
         if (c + 1 < c_end) {
-            if (tid < kF) kv = ln * kv + ((sRedK[0][tid] + sRedK[1][tid]) + (sRedK[2][tid] + sRedK[3][tid]));
-            if (tid < kD) {
-                float t8 = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) t8 += sRedS[e][tid];
-                sS0[tid] = ln * sS0[tid] + t8;
-            }
+            if (tid < kF) kv = ln * kv + sRedK[tid];
+            if (tid < kD) sS0[tid] = ln * sS0[tid] + sRedS[tid];
             if (tid == kF) sK0[0] = ln * sK0[0] + sPs[nvalid];
             publish();
             store_rows(c + 1);
