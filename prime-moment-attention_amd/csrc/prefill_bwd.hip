@@ -552,7 +552,10 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
     __shared__ __attribute__((aligned(16))) uint16_t sG[kC][kPV];    // [dy / d | gden | 0..]
     __shared__ __attribute__((aligned(16))) uint16_t sW[kSR][kPW];   // bf16 W^T at the chunk end
     __shared__ float sW1[kSR], sGd[kC], sPw[kC + 2];
-    __shared__ float sRed[8][kD], sRedG[1];  // partial sums of the W1 update
+    __shared__ float sRed[kD], sRedG[1];  // the chunk's W1 increment (value columns, gden column)
+    // om_t = l^(t+1) split into three bf16 parts (hi, mid, lo), row 3 zero: the
+    // A operand of the W1 increment on MFMA
+    __shared__ __attribute__((aligned(16))) uint16_t sOmp[4][kC];
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -569,6 +572,16 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
     float *slot = a.G > 1 ? a.ws + static_cast<size_t>(unit) * kWsStride : nullptr;
 
     if (tid < kC + 2) sPw[tid] = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(tid)));
+    if (tid < kC) {
+        const float om = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(tid + 1)));
+        const uint16_t hi = f32_to_bf16_bits(om);
+        const float r1 = om - bf16_bits_to_f32(hi);
+        const uint16_t mid = f32_to_bf16_bits(r1);
+        sOmp[0][tid] = hi;
+        sOmp[1][tid] = mid;
+        sOmp[2][tid] = f32_to_bf16_bits(r1 - bf16_bits_to_f32(mid));
+        sOmp[3][tid] = 0u;
+    }
     for (int idx = tid; idx < kC * 16; idx += 256) {
         const int row = idx >> 4, cc = kD + (idx & 15);
         sV[row][cc] = 0u;
@@ -785,11 +798,17 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
             for (int nb = 0; nb < 5; ++nb)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) st[fi][nb][r] *= ln;
+        f32x4 dw1 = f32x4{0.f, 0.f, 0.f, 0.f};  // W1 increment of value block w: rows 0..2 = om parts
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             float om[8];
 #pragma unroll
             for (int t = 0; t < 8; ++t) om[t] = sPw[32 * ks + 16 * (t >> 2) + 4 * g + (t & 3) + 1];
+            // lane (g, c16): part min(c16, 3) of om at its eight token slots
+            const int pr = min(c16, 3);
+            const uint2 o0 = *reinterpret_cast<const uint2 *>(&sOmp[pr][32 * ks + 4 * g]);
+            const uint2 o1 = *reinterpret_cast<const uint2 *>(&sOmp[pr][32 * ks + 16 + 4 * g]);
+            const bf16x8 ompart = as_bf16x8(u32x4{o0.x, o0.y, o1.x, o1.y});
             bf16x8 aq[2];
 #pragma unroll
             for (int fi = 0; fi < 2; ++fi) {
@@ -802,20 +821,13 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
                 const bf16x8 gb = tr_op<false>(p0, p0 + 16 * kPV, 0).h;
 #pragma unroll
                 for (int fi = 0; fi < 2; ++fi) st[fi][nb] = mfma(aq[fi], gb, st[fi][nb]);
+                if (nb == w) dw1 = mfma(ompart, gb, dw1);  // wave-uniform
             }
         }
         {
-            // W1[n] = sum_t om_t G_t[n]: column pairs x eighths of the tokens; the gden column on wave 0
-            const int n0 = 2 * (tid & 31), i0 = 8 * (tid >> 5);
-            float s0 = 0.f, s1 = 0.f;
-#pragma unroll
-            for (int i = i0; i < i0 + 8; ++i) {
-                const uint32_t u = *reinterpret_cast<const uint32_t *>(&sG[i][n0]);
-                const float om = sPw[i + 1];
-                s0 += om * __uint_as_float(u << 16);
-                s1 += om * __uint_as_float(u & 0xFFFF0000u);
-            }
-            *reinterpret_cast<f32x2 *>(&sRed[tid >> 5][n0]) = f32x2{s0, s1};
+            // W1[n] = sum_t om_t G_t[n]: value column 16w + c16 from the three om parts
+            // (rows 0..2, lane group g = 0); the gden column (fp32) on wave 0
+            if (g == 0) sRed[16 * w + c16] = (dw1[0] + dw1[1]) + dw1[2];
             if (w == 0) {
                 const float gs = wave_sum(sPw[lane + 1] * sGd[lane]);
                 if (lane == 0) sRedG[0] = gs;
@@ -823,10 +835,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
         }
         __syncthreads();  // every read of chunk c's tiles and of W is done; partial sums in LDS
         if (tid < kD) {
-            float t8 = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) t8 += sRed[e][tid];
-            w1 = ln * w1 + t8;
+            w1 = ln * w1 + sRed[tid];
         } else if (tid == kD) {
             w1 = ln * w1 + sRedG[0];
         }
