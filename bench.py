@@ -339,7 +339,7 @@ def bench_selective(args, lib, torch, dev):
            "prefill": {"tok_s": B * L / (ms * 1e-3), "ms": ms, "finite": bool(torch.isfinite(y).all().item()),
                        "kernels": {n: {"avg_us": None if t is None else t * 1e3, "launches": c}
                                    for n, (t, c) in kern.items()},
-                       "roofline": {"kernel": "prefill_bf16_kernel<false, true, false, false>", "bound": "hbm",
+                       "roofline": {"kernel": "prefill_bf16_kernel<false, true, false, false, false>", "bound": "hbm",
                                     "bytes_per_launch": algo, "avg_launch_us": main_ms * 1e3,
                                     "achieved": algo / (main_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                                     "unit": "GB/s", "frac": algo / (main_ms * 1e-3) / PEAK_HBM}}}
@@ -425,7 +425,7 @@ def bench_hybrid(args, lib, torch, dev):
                             (lib.KERNEL_PREFILL_SEGMENTS, lib.KERNEL_SEGMENT_SCAN), lib.KERNEL_PREFILL_SEGMENTS,
                             B * H * L * 4 * D + B * H * STATE_BYTES, steps, B * L,
                             "prime_accumulate, B=8 x H=12 x L=8192 bf16 k/v, zero initial state",
-                            "prefill_bf16_kernel<true, false, false, false> (state-only)")
+                            "prefill_bf16_kernel<true, false, false, false, false> (state-only)")
     del q, k, v
     q32, k32, v32 = qkv((B, H, L, D), gen, dev, torch.float32)
     y32 = torch.empty(B, H, L, D, device=dev)
@@ -740,7 +740,7 @@ def main():
                    "B": pf["B"], "H": pf["H"], "L": pf["L"], "D": D, "chunk": pf["C"],
                    "state_dtype": "fp32", "accumulate": "fp32", "workspace_bytes": pf["ws_bytes"],
                    "seed": args.seed},
-        "roofline": {"kernel": "prefill_bf16_kernel<false, false, true, true> (fused chunk loop, 16 waves)", "bound": "hbm",
+        "roofline": {"kernel": "prefill_bf16_kernel<false, false, true, true, false> (fused chunk loop, 16 waves)", "bound": "hbm",
                      "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM,
                      "traffic": None if traffic is None else traffic.get("bytes_per_launch"),
