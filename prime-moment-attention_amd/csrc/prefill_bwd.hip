@@ -366,7 +366,11 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
         dsum = sum_lane32(sum_lane16(dsum));
         dcar = sum_lane32(sum_lane16(dcar));
         const float den_iw = dsum + pinc * (dcar + sK0[0]);
-        // ---- G of rows i = 16w + 4g + r
+        // ---- G of rows i = 16w + 4g + r; dy of those rows at column 16nb + c16
+        // from transposed reads (dyt[nb] element r: row 16w + 4g + r)
+        uint2 dyt[4];
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) dyt[nb] = lds_tr(&sG[16 * w + 4 * g + tr_r][16 * nb + tr_c]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int i = 16 * w + 4 * g + r;
@@ -377,7 +381,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             float part = 0.f, gn[4];
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb) {
-                const float dyv = bf16_bits_to_f32(sG[i][16 * nb + c16]);  // read, then overwritten by this lane
+                const uint32_t dw = r < 2 ? dyt[nb].x : dyt[nb].y;  // overwritten below by this lane
+                const float dyv = __uint_as_float((r & 1) ? dw & 0xFFFF0000u : dw << 16);
                 part += dyv * (acc[nb][r] * inv);
                 gn[nb] = valid ? dyv * inv : 0.f;
             }
@@ -552,6 +557,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
     __shared__ __attribute__((aligned(16))) uint16_t sG[kC][kPV];    // [dy / d | gden | 0..]
     __shared__ __attribute__((aligned(16))) uint16_t sW[kSR][kPW];   // bf16 W^T at the chunk end
     __shared__ float sW1[kSR], sGd[kC], sPw[kC + 2];
+    __shared__ __attribute__((aligned(16))) float sOm[kC];  // om_t = l^(t+1) (= sPw[t + 1]), 16-byte aligned
     __shared__ float sRed[kD], sRedG[1];  // the chunk's W1 increment (value columns, gden column)
     // om_t = l^(t+1) split into three bf16 parts (hi, mid, lo), row 3 zero: the
     // A operand of the W1 increment on MFMA
@@ -574,6 +580,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
     if (tid < kC + 2) sPw[tid] = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(tid)));
     if (tid < kC) {
         const float om = static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(tid + 1)));
+        sOm[tid] = om;
         const uint16_t hi = f32_to_bf16_bits(om);
         const float r1 = om - bf16_bits_to_f32(hi);
         const uint16_t mid = f32_to_bf16_bits(r1);
@@ -802,8 +809,15 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             float om[8];
+            {
+                const f32x4 o0 = *reinterpret_cast<const f32x4 *>(&sOm[32 * ks + 4 * g]);
+                const f32x4 o1 = *reinterpret_cast<const f32x4 *>(&sOm[32 * ks + 16 + 4 * g]);
 #pragma unroll
-            for (int t = 0; t < 8; ++t) om[t] = sPw[32 * ks + 16 * (t >> 2) + 4 * g + (t & 3) + 1];
+                for (int t = 0; t < 4; ++t) {
+                    om[t] = o0[t];
+                    om[4 + t] = o1[t];
+                }
+            }
             // lane (g, c16): part min(c16, 3) of om at its eight token slots
             const int pr = min(c16, 3);
             const uint2 o0 = *reinterpret_cast<const uint2 *>(&sOmp[pr][32 * ks + 4 * g]);
