@@ -183,10 +183,12 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
     // fp32: the K column of M (the denominator's moments) entering the chunk, S0, K0
     __shared__ float sKv[kF], sS0[kD], sK0[1], sGd[kC], sPg[kC], sPw[kC + 2], sPs[kC + 2];
     __shared__ float sRedK[kF], sRedS[kD];  // the chunk's K and S0 increments
-    __shared__ __attribute__((aligned(16))) float sWt[kC];  // the chunk's state-update weights l^(n-1-j)
-    // the same weights split into three bf16 parts (hi, mid, lo: about fp32 precision
-    // in sum), row 3 zero: an MFMA operand whose columns (or rows) 0..2 are the parts
-    __shared__ __attribute__((aligned(16))) uint16_t sWp[4][kC];
+    // the state-update weights l^(n-1-j) of a full chunk (0) and of the
+    // sequence's last chunk (1, n = its valid tokens), and the same weights split
+    // into three bf16 parts (hi, mid, lo: about fp32 precision in sum), row 3
+    // zero: an MFMA operand whose columns (or rows) 0..2 are the parts
+    __shared__ __attribute__((aligned(16))) float sWt[2][kC];
+    __shared__ __attribute__((aligned(16))) uint16_t sWp[2][4][kC];
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
         sV[row][cc] = 0u;
         sG[row][cc] = 0u;
     }
-    if (tid < kC) sWp[3][tid] = 0u;
+
 
 
     // value columns of M (features 32w..32w+31 of this wave, value blocks 0..3) from state_in
@@ -275,6 +277,19 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
     };
 
     __syncthreads();  // power tables
+    if (tid < 2 * kC) {  // the two weight tables (read after the chunk loop's first barrier)
+        const int t = tid & (kC - 1), which = tid >> 6;
+        const int nv = which ? a.L - (NC - 1) * kC : kC;
+        const float wv = t < nv ? sPw[nv - 1 - t] : 0.f;
+        sWt[which][t] = wv;
+        const uint16_t hi = f32_to_bf16_bits(wv);
+        const float r1 = wv - bf16_bits_to_f32(hi);
+        const uint16_t mid = f32_to_bf16_bits(r1);
+        sWp[which][0][t] = hi;
+        sWp[which][1][t] = mid;
+        sWp[which][2][t] = f32_to_bf16_bits(r1 - bf16_bits_to_f32(mid));
+        sWp[which][3][t] = 0u;
+    }
     // readout constants of this lane: row iw of the transposed blocks, rows
     // 16w + 4g + r of the [num | den] accumulators (powers from the table:
     // sPw[n] is l^n rounded from fp64)
@@ -299,16 +314,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
     for (int c = c_begin; c < c_end; ++c) {
         const int nvalid = min(kC, a.L - c * kC);
         __syncthreads();  // tiles of chunk c and M_c in LDS
-        if (tid < kC) {  // read after the next barrier
-            const float wv = tid < nvalid ? sPw[nvalid - 1 - tid] : 0.f;
-            sWt[tid] = wv;
-            const uint16_t hi = f32_to_bf16_bits(wv);
-            const float r1 = wv - bf16_bits_to_f32(hi);
-            const uint16_t mid = f32_to_bf16_bits(r1);
-            sWp[0][tid] = hi;
-            sWp[1][tid] = mid;
-            sWp[2][tid] = f32_to_bf16_bits(r1 - bf16_bits_to_f32(mid));
-        }
+        const int wsel = nvalid == kC ? 0 : 1;  // weights of a full chunk or of the last one
         // ---- scores S^T[j][iw] (blocks jb <= w), masked: A = l^(i-j) (1 + phi_q . phi_k)
         f32x4 sT[4];
 #pragma unroll
@@ -403,7 +409,11 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
                 }
             }
         }
-        __syncthreads();  // G of the chunk in LDS
+        // G of the chunk in LDS: each wave reads back only its own rows of sG, sGd
+        // and sPg below, so a wave-local ordering suffices
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // ---- P^T[j][iw] = mask * (v_j . g_iw + gden_iw)
         f32x4 pT[4];
         const float gdi = sGd[iw];
@@ -489,8 +499,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
         for (int ks = 0; ks < 2; ++ks) {
             float wt[8];
             {
-                const f32x4 w0 = *reinterpret_cast<const f32x4 *>(&sWt[32 * ks + 4 * g]);
-                const f32x4 w1 = *reinterpret_cast<const f32x4 *>(&sWt[32 * ks + 16 + 4 * g]);
+                const f32x4 w0 = *reinterpret_cast<const f32x4 *>(&sWt[wsel][32 * ks + 4 * g]);
+                const f32x4 w1 = *reinterpret_cast<const f32x4 *>(&sWt[wsel][32 * ks + 16 + 4 * g]);
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     wt[t] = w0[t];
@@ -500,8 +510,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             // lane (g, c16): part min(c16, 3) of w at its eight token slots, the
             // same slots as the transposed operands (token 32ks + 16(t/4) + 4g + t%4)
             const int pr = min(c16, 3);
-            const uint2 p0 = *reinterpret_cast<const uint2 *>(&sWp[pr][32 * ks + 4 * g]);
-            const uint2 p1 = *reinterpret_cast<const uint2 *>(&sWp[pr][32 * ks + 16 + 4 * g]);
+            const uint2 p0 = *reinterpret_cast<const uint2 *>(&sWp[wsel][pr][32 * ks + 4 * g]);
+            const uint2 p1 = *reinterpret_cast<const uint2 *>(&sWp[wsel][pr][32 * ks + 16 + 4 * g]);
             const bf16x8 wpart = as_bf16x8(u32x4{p0.x, p0.y, p1.x, p1.y});
             bf16x8 ak[2];
 #pragma unroll
