@@ -256,21 +256,20 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
         const bool va = ra < nv, vb = ra + 32 < nv;
         float wa, wb;
         if constexpr (SEL) {
-            // inclusive scan of the chunk's log2 decays over the lanes (lane = token)
-            float x = lane < nv ? T.ld * 1.4426950408889634f : 0.f;
-#pragma unroll
-            for (int o = 1; o < kWave; o <<= 1) {
-                const float y = __shfl_up(x, o, kWave);
-                if (lane >= o) x += y;
-            }
-            // every lane takes part in the shuffles (a lane outside a branch
-            // would not supply its value to the lanes reading it)
-            const float tot = __shfl(x, nv - 1, kWave);
-            const float xra = __shfl(x, ra, kWave), xrb = __shfl(x, ra + 32, kWave);
+            // inclusive scan of the chunk's log2 decays over the lanes (lane = token),
+            // on the VALU; every lane takes part (the cross-lane moves read all lanes)
+            const float x = wave_prefix_sum(lane < nv ? T.ld * 1.4426950408889634f : 0.f);
+            const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), nv - 1));
+            const float xra = __shfl(x, ra, kWave);
             wa = va ? exp2f(tot - xra) : 0.f;
-            wb = vb ? exp2f(tot - xrb) : 0.f;
+            if constexpr (!UW8) {
+                const float xrb = __shfl(x, ra + 32, kWave);
+                wb = vb ? exp2f(tot - xrb) : 0.f;
+            } else {
+                wb = 0.f;
+            }
             sel_ln = exp2f(tot);
-            sel_sw = wave_sum(lane < nv ? exp2f(tot - x) : 0.f);
+            sel_sw = wave_sum_valu(lane < nv ? exp2f(tot - x) : 0.f);
             seg_ld += tot;
             if constexpr (!STATE_ONLY) {
                 if (u == 0) sCum[xb][lane] = x;
@@ -452,7 +451,7 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
                         // RH: the decay mask from the power table (registers are short)
                         const int d = iw - (16 * jb + 4 * g + r);
                         // RH: one base address, immediate offsets: index 63 + iw - j
-                        const float mk = RH ? (&sPm[RH ? iw - 4 * g + 12 : 0])[51 - 16 * jb - r] : mask[jb][r];
+                        const float mk = (RH && !SEL) ? (&sPm[RH ? iw - 4 * g + 12 : 0])[51 - 16 * jb - r] : mask[jb][r];
                         (void)d;
                         x[r] = fmaf(mk, sT[jb][r], mk);  // mk (1 + s)
                     }
@@ -639,13 +638,13 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
 template <bool QKN>
 static void launch_variant_bf16(const PrefillArgs &a, bool state_only, int grid, hipStream_t stream, TimerEvents t) {
     const bool sel = a.log_decay != nullptr;
-    const dim3 g(grid), blk(state_only ? 256 : (sel ? 512 : 1024));
+    const dim3 g(grid), blk(state_only ? 256 : 1024);
     if (state_only && sel)
         hipExtLaunchKernelGGL((prefill_bf16_kernel<true, true, false, false, QKN>), g, blk, 0, stream, t.start, t.stop, 0, a);
     else if (state_only)
         hipExtLaunchKernelGGL((prefill_bf16_kernel<true, false, false, false, QKN>), g, blk, 0, stream, t.start, t.stop, 0, a);
     else if (sel)
-        hipExtLaunchKernelGGL((prefill_bf16_kernel<false, true, false, false, QKN>), g, blk, 0, stream, t.start, t.stop, 0, a);
+        hipExtLaunchKernelGGL((prefill_bf16_kernel<false, true, true, true, QKN>), g, blk, 0, stream, t.start, t.stop, 0, a);
     else
         hipExtLaunchKernelGGL((prefill_bf16_kernel<false, false, true, true, QKN>), g, blk, 0, stream, t.start, t.stop, 0, a);
 }

@@ -112,6 +112,29 @@ __device__ __forceinline__ float sum_lane32(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Inclusive prefix sum of x over the 64 lanes on the VALU (DPP): Hillis-Steele
+// within each row of 16 lanes (row_shr 1, 2, 4, 8, zero-filled), then the last
+// lane of rows 0 and 2 added to rows 1 and 3 (row_bcast:15) and lane 31 added
+// to rows 2 and 3 (row_bcast:31).
+__device__ __forceinline__ float wave_prefix_sum(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xF, 0xF, true));  // row_shr:1
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xF, 0xF, true));  // row_shr:2
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xF, 0xF, true));  // row_shr:4
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xF, 0xF, true));  // row_shr:8
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x142, 0xA, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x143, 0xC, 0xF, false));
+    return x;
+}
+
+// Sum of x over the 64 lanes, in every lane, on the VALU (DPP and permlane swaps).
+__device__ __forceinline__ float wave_sum_valu(float x) {
+    x += xor_lane<1>(x);
+    x += xor_lane<2>(x);
+    x += xor_lane<4>(x);
+    x += xor_lane<8>(x);
+    return sum_lane32(sum_lane16(x));
+}
+
 // 16-byte LDS read
 __device__ __forceinline__ u32x4 lds128(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
