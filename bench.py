@@ -339,7 +339,7 @@ def bench_selective(args, lib, torch, dev):
            "prefill": {"tok_s": B * L / (ms * 1e-3), "ms": ms, "finite": bool(torch.isfinite(y).all().item()),
                        "kernels": {n: {"avg_us": None if t is None else t * 1e3, "launches": c}
                                    for n, (t, c) in kern.items()},
-                       "roofline": {"kernel": "prefill_bf16_kernel<false, true, false, false, false>", "bound": "hbm",
+                       "roofline": {"kernel": "prefill_bf16_kernel<false, true, true, true, false>", "bound": "hbm",
                                     "bytes_per_launch": algo, "avg_launch_us": main_ms * 1e3,
                                     "achieved": algo / (main_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                                     "unit": "GB/s", "frac": algo / (main_ms * 1e-3) / PEAK_HBM}}}
