@@ -3,8 +3,8 @@
 //
 // Same algorithm and semantics as the generic kernel in prefill.hip (see its
 // header comment for the chunk equations and the operand layouts); this kernel
-// differs in its schedule.  The fused pass runs 16 waves (the base form; the
-// selective form runs 4 + 4 with two feature blocks per update wave):
+// differs in its schedule.  The fused pass runs 16 waves (base and selective
+// forms):
 //   readout waves 0..7 only compute, each for one query block and half of the
 //     value columns: score block, AV, state readout, y;
 //   update waves 8..15 own the state M = [S1; S2/2 | K] in MFMA accumulators,
