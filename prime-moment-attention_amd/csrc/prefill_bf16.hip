@@ -157,7 +157,7 @@ __device__ __forceinline__ void store_row(u32x4 q, u32x4 k, u32x4 v, int row, in
 // one tile row per thread) instead of 4; RH = 8 readout waves (query block x
 // half of the value columns) instead of 4.  QKN: the QK LayerNorm on load.
 template <bool STATE_ONLY, bool SEL, bool UW8 = false, bool RH = false, bool QKN = false>
-__global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 4)), 1) void prefill_bf16_kernel(
+__global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 4)), STATE_ONLY ? 3 : 1) void prefill_bf16_kernel(
     const PrefillArgs a) {
     constexpr int NB = kD / 16;    // value blocks
     constexpr int NBX = NB + 1;    // + the ones / K block
