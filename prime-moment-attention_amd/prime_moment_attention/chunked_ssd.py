@@ -115,6 +115,12 @@ def prime_prefill(q, k, v, state=None, decay=0.9995, eps=1.0, chunk_size=64, ret
     bf16 only, no autograd): q and k are the raw projections and the module's
     QK LayerNorm and q scale are applied by the kernels as they load them."""
     B, H, L, D = q.shape
+    if needs_grad(decay):
+        # a per-head decay tensor is this library's extension; the backward
+        # kernels give no derivative in it, so a learnable decay would train
+        # with a silently missing gradient
+        raise NotImplementedError("the prefill has no gradient with respect to decay; pass a decay that does not "
+                                  "require grad (e.g. decay.detach()) or run under torch.no_grad()")
     q, k, v = _prep(q), _prep(k), _prep(v)
     if k.dtype != q.dtype or v.dtype != q.dtype:
         k, v = k.to(q.dtype), v.to(q.dtype)

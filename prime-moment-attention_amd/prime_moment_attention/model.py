@@ -299,9 +299,11 @@ class GreedyDecoder:
         self.states = None
         self._decay, self._norm, self._qkv, self._sel = {}, {}, {}, {}
         dev = model.embed_tokens.weight.device
+        # the modules keep their functional state contract: the decoder's own
+        # prefill starts from no state and its step hands the decode kernel the
+        # same buffers as input and output, so no module flag is changed here
         for layer in model.layers:
             at = layer.self_attn
-            at.inplace_state = True
             if not isinstance(at, PrimeSelectiveMomentAttention):
                 self._decay[id(at)] = _lib.decay_tensor(at.decay, at.num_heads, dev)
             self._norm[id(at)] = _lib.qk_norm(at.q_norm if at.use_qk_norm else None,

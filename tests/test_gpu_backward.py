@@ -46,13 +46,15 @@ def _run(B, H, L, dtype, with_state, with_dstate, seed, normalize=True, eps=1.0,
     return ref, [to_np(t).reshape(BH, L, D) for t in g], (state_to_np(dsi, BH, D) if with_state else None)
 
 
-def _check(ref, got, dsi, tol=TOL_BF16):
-    # dq and dk vanish analytically for one token from a zero state (y = v):
-    # their error is then measured against the gradient scale of dv
-    floor = 0.1 * np.abs(ref[2]).max()
+def _check(ref, got, dsi, tol=TOL_BF16, one_token_from_zero=False):
+    """max|d| / max|ref| per gradient tensor.  For one token from a zero
+    state y = v * min(1, den / eps), so dq and dk are tiny or zero (exactly
+    zero where den >= eps); only in that case is their error measured
+    against the gradient scale of dv instead of their own."""
+    floor = 0.1 * np.abs(ref[2]).max() if one_token_from_zero else 0.0
     for name, r, x in zip(("dq", "dk", "dv"), ref[:3], got):
         assert np.isfinite(x).all(), name
-        e = np.abs(x - r).max() / max(np.abs(r).max(), floor)
+        e = np.abs(x - r).max() / max(np.abs(r).max(), floor, 1e-300)
         assert e < tol, f"{name}: rel err {e:.3e} >= {tol}"
     if dsi is not None:
         assert_state_close(dsi, ref[3], tol, "dstate_in")
@@ -62,7 +64,7 @@ def _check(ref, got, dsi, tol=TOL_BF16):
 @pytest.mark.parametrize("with_state", [False, True])
 def test_backward_bf16_matches_oracle(B, H, L, with_state):
     ref, got, dsi = _run(B, H, L, torch.bfloat16, with_state, with_state, seed=400 + L)
-    _check(ref, got, dsi)
+    _check(ref, got, dsi, one_token_from_zero=(L == 1 and not with_state))
 
 
 @pytest.mark.parametrize("B,H,L", [(2, 2, 77), (1, 3, 130)])

@@ -118,8 +118,32 @@ def test_greedy_decoder_graph_equals_eager_generate():
     assert torch.equal(graph, ref), (graph, ref)
 
 
+def test_greedy_decoder_leaves_module_states_functional():
+    """Building and running a GreedyDecoder changes no module setting: a later
+    model.forward with a saved state still returns new state tensors and leaves
+    the passed-in ones untouched (the reference's functional contract,
+    attention.py:126-132), so a saved prefix can be branched from."""
+    model = _model(_small())
+    ids = torch.randint(0, 384, (2, 20), generator=torch.Generator().manual_seed(8)).to(dev())
+    with torch.no_grad():
+        saved = model(ids, return_states=True)["states"]
+        dec = GreedyDecoder(model, use_graph=True)
+        dec.prefill(ids)
+        for _ in range(3):
+            dec.step()
+        snap = [tuple(t.clone() for t in st) for st in saved]
+        tok = ids[:, -1:]
+        a = model(tok, states=saved, return_states=True)
+        b = model(tok, states=saved, return_states=True)
+    torch.cuda.synchronize()
+    for st, sn, new in zip(saved, snap, a["states"]):
+        assert all(torch.equal(x, y) for x, y in zip(st, sn))
+        assert all(x.data_ptr() != y.data_ptr() for x, y in zip(st, new))
+    assert torch.equal(a["logits"], b["logits"])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
-@pytest.mark.parametrize("n,vocab,pad", [(256, 50304, 0), (3, 1000, 0), (5, 50257, 0), (4, 37, 3), (1, 9000, 1)])
+@pytest.mark.parametrize("n,vocab,pad",[(256, 50304, 0), (3, 1000, 0), (5, 50257, 0), (4, 37, 3), (1, 9000, 1)])
 def test_argmax_matches_torch(dtype, n, vocab, pad):
     """prime_argmax == torch.argmax (first index of the largest), on padded
     (strided, unaligned) rows and ragged vocabularies."""
