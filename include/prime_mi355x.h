@@ -331,6 +331,24 @@ int prime_accumulate(const prime_tensor_t *k, const prime_tensor_t *v, int B, in
 size_t prime_accumulate_workspace_size(int B, int H, int L);
 
 /*
+ * prime_accumulate without a workspace argument: it allocates nothing.  No
+ * counterpart in the reference; it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The segment slots live in a fixed device array of
+ * PRIME_NOALLOC_SCRATCH_BYTES inside the library (one per device, held until
+ * the process ends); the call needs one 33,792-byte slot per (sequence, head)
+ * and fails with PRIME_ERR_INVALID_ARG when B * H exceeds 992.  Within that
+ * array the segment plan is the one prime_accumulate picks for a workspace of
+ * the same size.  All calls on one device share the array: calls that overlap
+ * in time on one device (different streams or threads) race and must be
+ * ordered by the caller.  Other arguments and results as prime_accumulate.
+ */
+#define PRIME_NOALLOC_SCRATCH_BYTES (32u << 20)
+int prime_accumulate_noalloc(const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv, int L,
+                             int D, const float *decay, const prime_state_t *state_in,
+                             const prime_state_t *state_out, void *stream);
+
+/*
  * Backward of prime_chunked_prefill: the reverse-mode derivative the reference
  * obtains from torch autograd when it trains through its prefill
  * (tests/test_attention.py:50-62 through attention.py:77-210 and

@@ -2,6 +2,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "prime_kernels.h"
 
 namespace {
@@ -359,12 +361,17 @@ int prime_chunked_prefill_qknorm(const prime_tensor_t *q, const prime_tensor_t *
                         workspace_bytes, stream, nullptr, nullptr, norm);
 }
 
-int prime_accumulate(const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv, int L, int D,
-                     const float *decay, const prime_state_t *state_in, const prime_state_t *state_out,
-                     void *workspace, size_t workspace_bytes, void *stream) {
-    g_err[0] = 0;
-    if (!k || !v || !k->data || !v->data || !decay || !state_out || !workspace)
-        return fail(PRIME_ERR_INVALID_ARG, "prime_accumulate: null argument");
+}  // extern "C"
+
+namespace {
+
+// Validation shared by prime_accumulate and prime_accumulate_noalloc; the
+// workspace is checked separately (the no-allocation variant brings its own).
+int accumulate_checks(const char *who, const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv,
+                      int L, int D, const float *decay, const prime_state_t *state_in,
+                      const prime_state_t *state_out) {
+    if (!k || !v || !k->data || !v->data || !decay || !state_out)
+        return fail(PRIME_ERR_INVALID_ARG, "%s: null argument", who);
     if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0)
         return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d", B, H, H_kv, L);
@@ -372,15 +379,18 @@ int prime_accumulate(const prime_tensor_t *k, const prime_tensor_t *v, int B, in
         return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "k/v must share dtype BF16 or F32");
     if (!rows_aligned(k, true) || !rows_aligned(v, true))
         return fail(PRIME_ERR_MISALIGNED, "k/v rows must start on 16-byte boundaries");
-    if (!aligned16(workspace)) return fail(PRIME_ERR_MISALIGNED, "workspace must be 16-byte aligned");
     int rc;
     if ((rc = check_state(state_in, "state_in")) || (rc = check_state(state_out, "state_out"))) return rc;
     bool inplace;
-    if ((rc = check_state_alias(state_in, state_out, static_cast<size_t>(B) * H, D, &inplace))) return rc;
+    return check_state_alias(state_in, state_out, static_cast<size_t>(B) * H, D, &inplace);
+}
+
+// Launch of a validated accumulate call on a workspace of at least one slot
+// per sequence (the segment plan uses as much of workspace_bytes as it pays to).
+int accumulate_launch(const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv, int L,
+                      const float *decay, const prime_state_t *state_in, const prime_state_t *state_out,
+                      void *workspace, size_t workspace_bytes, void *stream) {
     const int S = B * H;
-    const size_t slot = static_cast<size_t>(S) * prime::kWsStride * sizeof(float);
-    if (workspace_bytes < slot)
-        return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes is below the minimum %zu", workspace_bytes, slot);
     prime::PrefillArgs a{};
     // q is not read by the state-only kernels; it points at v for safety
     a.q = v->data; a.k = k->data; a.v = v->data;
@@ -400,8 +410,82 @@ int prime_accumulate(const prime_tensor_t *k, const prime_tensor_t *v, int B, in
     prime::plan_segments(S, L, false, workspace_bytes, &a.G, &a.cps);
     a.ws = static_cast<float *>(workspace);
     a.accumulate = 1;
-    (void)inplace;  // the scan reads state_in and the slots before it writes state_out, element by element
+    // in place is safe: the scan reads state_in and the slots before it writes
+    // state_out, element by element
     return check_hip(prime::launch_prefill(a, static_cast<hipStream_t>(stream)), "accumulate launch");
+}
+
+}  // namespace
+
+// Scratch of prime_accumulate_noalloc: the segment slots live in this fixed
+// device array instead of a caller workspace.  Every slot a call reads is
+// written earlier in the same call (the state-only pass writes all 8,385
+// state floats of each of its slots before the scan reads them), so nothing
+// needs clearing between calls.  One copy per device, held until the process
+// ends; calls that overlap on one device share it and race.
+static __device__ __align__(256) float scratch[PRIME_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+// The array's device address, looked up once per device with that device
+// current (the host-side name `scratch` is only a stand-in for the symbol).
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[64] = {};
+
+int scratch_address(void **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(PRIME_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= 64) return fail(PRIME_ERR_HIP, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr)
+            return fail(PRIME_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return PRIME_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int prime_accumulate(const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv, int L, int D,
+                     const float *decay, const prime_state_t *state_in, const prime_state_t *state_out,
+                     void *workspace, size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    int rc;
+    if ((rc = accumulate_checks("prime_accumulate", k, v, B, H, H_kv, L, D, decay, state_in, state_out)))
+        return rc;
+    if (!workspace) return fail(PRIME_ERR_INVALID_ARG, "prime_accumulate: null workspace");
+    if (!aligned16(workspace)) return fail(PRIME_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+    const size_t slot = static_cast<size_t>(B) * H * prime::kWsStride * sizeof(float);
+    if (workspace_bytes < slot)
+        return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes is below the minimum %zu", workspace_bytes, slot);
+    return accumulate_launch(k, v, B, H, H_kv, L, decay, state_in, state_out, workspace, workspace_bytes, stream);
+}
+
+int prime_accumulate_noalloc(const prime_tensor_t *k, const prime_tensor_t *v, int B, int H, int H_kv, int L,
+                             int D, const float *decay, const prime_state_t *state_in,
+                             const prime_state_t *state_out, void *stream) {
+    g_err[0] = 0;
+    int rc;
+    if ((rc = accumulate_checks("prime_accumulate_noalloc", k, v, B, H, H_kv, L, D, decay, state_in, state_out)))
+        return rc;
+    const size_t slot = static_cast<size_t>(B) * H * prime::kWsStride * sizeof(float);
+    if (slot > PRIME_NOALLOC_SCRATCH_BYTES)
+        return fail(PRIME_ERR_INVALID_ARG,
+                    "prime_accumulate_noalloc: B*H = %d sequences need %zu bytes of scratch, above its fixed %zu "
+                    "(at most %zu sequences); use prime_accumulate with a workspace",
+                    B * H, slot, static_cast<size_t>(PRIME_NOALLOC_SCRATCH_BYTES),
+                    static_cast<size_t>(PRIME_NOALLOC_SCRATCH_BYTES) / (prime::kWsStride * sizeof(float)));
+    void *ws = nullptr;
+    if ((rc = scratch_address(&ws))) return rc;
+    return accumulate_launch(k, v, B, H, H_kv, L, decay, state_in, state_out, ws, PRIME_NOALLOC_SCRATCH_BYTES,
+                             stream);
 }
 
 namespace {

@@ -30,7 +30,10 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_selective_decode_step", "prime_accumulate", "prime_accumulate_workspace_size",
            "prime_decode_readout", "prime_decode_update", "prime_chunked_prefill_backward",
            "prime_chunked_prefill_backward_workspace_size", "prime_chunked_prefill_qknorm",
-           "prime_selective_prefill_qknorm")
+           "prime_selective_prefill_qknorm", "prime_accumulate_noalloc")
+
+# bytes of the fixed device scratch behind prime_accumulate_noalloc
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 # kernel identifiers of the launch timer
 KERNEL_PREFILL_CHUNKS, KERNEL_PREFILL_SEGMENTS, KERNEL_SEGMENT_SCAN, KERNEL_DECODE = 0, 1, 2, 3
@@ -130,6 +133,9 @@ def load() -> ctypes.CDLL:
     L.prime_accumulate.argtypes = [P(PrimeTensor)] * 2 + [ctypes.c_int] * 5 + [
         fp, P(PrimeState), P(PrimeState), fp, ctypes.c_size_t, fp]
     L.prime_accumulate.restype = ctypes.c_int
+    L.prime_accumulate_noalloc.argtypes = [P(PrimeTensor)] * 2 + [ctypes.c_int] * 5 + [
+        fp, P(PrimeState), P(PrimeState), fp]
+    L.prime_accumulate_noalloc.restype = ctypes.c_int
     L.prime_accumulate_workspace_size.argtypes = [ctypes.c_int] * 3
     L.prime_accumulate_workspace_size.restype = ctypes.c_size_t
     L.prime_decode_readout.argtypes = [P(PrimeTensor)] + [ctypes.c_int] * 3 + [
@@ -542,11 +548,7 @@ def accumulate_workspace_size(B: int, H: int, L: int) -> int:
     return int(load().prime_accumulate_workspace_size(B, H, L))
 
 
-def accumulate(k, v, decay: torch.Tensor, state_in, state_out, H: Optional[int] = None,
-               workspace: Optional[torch.Tensor] = None) -> None:
-    """State of the tokens of k/v [B,Hkv,L,D] (prime_accumulate), appended to
-    state_in (None: zeros) and written to state_out (may be state_in).  H
-    query heads (default Hkv; a multiple of Hkv)."""
+def _accumulate_checks(k, v, decay, state_in, state_out, H):
     _dev_check(k, v, decay)
     B, Hkv, Lk, D = k.shape
     H = Hkv if H is None else H
@@ -554,6 +556,15 @@ def accumulate(k, v, decay: torch.Tensor, state_in, state_out, H: Optional[int] 
     _check_decay(decay, H)
     _check_state(state_in, B, H, D, "state_in")
     _check_state(state_out, B, H, D, "state_out")
+    return B, H, Hkv, Lk, D
+
+
+def accumulate(k, v, decay: torch.Tensor, state_in, state_out, H: Optional[int] = None,
+               workspace: Optional[torch.Tensor] = None) -> None:
+    """State of the tokens of k/v [B,Hkv,L,D] (prime_accumulate), appended to
+    state_in (None: zeros) and written to state_out (may be state_in).  H
+    query heads (default Hkv; a multiple of Hkv)."""
+    B, H, Hkv, Lk, D = _accumulate_checks(k, v, decay, state_in, state_out, H)
     if workspace is None:
         workspace = torch.empty(max(accumulate_workspace_size(B, H, Lk), 1), dtype=torch.uint8, device=k.device)
     _dev_check(workspace)
@@ -563,6 +574,19 @@ def accumulate(k, v, decay: torch.Tensor, state_in, state_out, H: Optional[int] 
                                  ctypes.byref(si) if si else None, ctypes.byref(so), workspace.data_ptr(),
                                  workspace.numel() * workspace.element_size(), _stream(k.device))
     _check(rc, "prime_accumulate")
+
+
+def accumulate_noalloc(k, v, decay: torch.Tensor, state_in, state_out, H: Optional[int] = None) -> None:
+    """accumulate() through prime_accumulate_noalloc: no workspace, nothing
+    allocated (the segment slots live in the library's fixed device scratch
+    of NOALLOC_SCRATCH_BYTES; B * H at most 992).  Calls that overlap on one
+    device share that scratch."""
+    B, H, Hkv, Lk, D = _accumulate_checks(k, v, decay, state_in, state_out, H)
+    kd, vd = tensor_desc(k, True), tensor_desc(v, True)
+    si, so = state_desc(state_in), state_desc(state_out)
+    rc = load().prime_accumulate_noalloc(ctypes.byref(kd), ctypes.byref(vd), B, H, Hkv, Lk, D, decay.data_ptr(),
+                                         ctypes.byref(si) if si else None, ctypes.byref(so), _stream(k.device))
+    _check(rc, "prime_accumulate_noalloc")
 
 
 def decode_readout(q, eps: float, state, y) -> None:

@@ -97,3 +97,23 @@ def test_timer_reads_without_launches():
     _lib.timer_reset()
     for kid in _lib.KERNEL_NAMES:
         assert _lib.timer_read(kid) == (0.0, 0)
+
+
+def test_accumulate_noalloc_rejects_sizes_beyond_its_scratch():
+    """prime_accumulate_noalloc needs one 33,792-byte slot per (sequence,
+    head) in its fixed scratch: B * H = 993 is refused with a clear message
+    before any device work (992 is the largest that fits)."""
+    L = _lib.load()
+    src = open(HDR).read()
+    m = re.search(r"#define PRIME_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", src)
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
+    assert _lib.NOALLOC_SCRATCH_BYTES // 33792 == 992
+    t = _lib.PrimeTensor(16, _lib.PRIME_BF16, 0, 0, 0, 0)  # never dereferenced: validation fails first
+    st = _lib.PrimeState(16, 16, 16, 16, 16, 16)
+    b = ctypes.byref
+    rc = L.prime_accumulate_noalloc(b(t), b(t), 3, 331, 331, 64, 64, 16, None, b(st), None)
+    assert rc == -1
+    msg = _lib.last_error()
+    assert "993" in msg and "scratch" in msg and "prime_accumulate" in msg
+    rc = L.prime_accumulate_noalloc(None, b(t), 1, 1, 1, 64, 64, 16, None, b(st), None)
+    assert rc == -1 and "null" in _lib.last_error()
