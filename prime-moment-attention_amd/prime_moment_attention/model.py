@@ -7,17 +7,22 @@ and ``generate`` follow model.py:163-242.  Every PRIME attention layer runs the
 library's decode step or chunked prefill (PrimeMomentAttention); projections,
 norms and the MLP are torch layers (library GEMMs).
 
-Additions for serving, none of which changes results:
+Additions for serving:
   * ``PrimeConfig.mlp_type = "gelu"`` selects an up/GELU/down MLP of width
     ``intermediate_size`` (the PRIME-125M benchmark shape); the default
     "swiglu" is the reference's PrimeMLP (model.py:59-68).
   * ``forward(..., logits_to_keep=n)`` computes logits for the last n
     positions only (generation needs one).
-  * ``GreedyDecoder`` runs greedy decoding with per-layer states updated in
-    place and the whole one-token step (embedding, 12 layers, final norm,
-    lm_head, argmax) captured in one HIP graph, replayed per token; in that
-    step each residual add is fused into the next RMSNorm and the QK-norm and
-    scale into the decode kernel (same values as the blocks' forward).
+  * One token per sequence (the generate loop) runs a fused step: each
+    residual add folded into the next RMSNorm (same rounding as the separate
+    add), one stacked q/k/v GEMM, the QK-norm and scale inside the decode
+    kernel, and the skinny HIP GEMM (exact GELU applied to its fp32
+    accumulator) where it beats the library GEMM.  Its rounding differs from
+    the blocks' separate torch ops only in those GEMMs.
+  * ``GreedyDecoder`` runs that same step with per-layer states updated in
+    place, the whole step (embedding, 12 layers, final norm, lm_head, argmax)
+    captured in one HIP graph and replayed per token, so its tokens equal
+    ``generate``'s at temperature 0.
 """
 from __future__ import annotations
 
@@ -185,6 +190,17 @@ class PrimeForCausalLM(nn.Module):
                 logits_to_keep: int = 0) -> Dict[str, Any]:
         if torch.is_grad_enabled() and any(p.requires_grad for p in self.parameters()):
             return self._forward_graph(input_ids, labels, states, return_states, logits_to_keep)
+        if input_ids.shape[-1] == 1 and _fused_step_supported(self):
+            # one token per sequence (the generate loop, model.py:238): the fused
+            # step GreedyDecoder runs, with functional states
+            logits, ns = _fused_step(self, input_ids, states, _step_constants(self), inplace=False)
+            logits = logits.unsqueeze(1)
+            loss = None
+            if labels is not None:
+                shift_logits = logits[..., :-1, :].contiguous().to(torch.float32)
+                loss = F.cross_entropy(shift_logits.view(-1, self.config.vocab_size),
+                                       labels[..., 1:].contiguous().view(-1), ignore_index=-100)
+            return {"loss": loss, "logits": logits, "states": ns if return_states else None}
         # The blocks' residual adds are folded into the following RMSNorm
         # (prime_add_rmsnorm stores the rounded sum, as the separate add does):
         # x is this call's own residual stream, updated in place; `pending` is
@@ -281,34 +297,131 @@ def _decode_linear(x: torch.Tensor, w: torch.Tensor, gelu: bool = False) -> torc
     return F.gelu(y) if gelu else y
 
 
+class _LayerStep:
+    """Per-layer constants of the fused one-token step: the q/k/v projection
+    weights stacked into one [Hq*D + 2*Hkv*D, hidden] matrix (one GEMM), the
+    QK-norm descriptor, and the decay tensor (base attention) or (tau, beta)
+    (selective attention), all taken from the module as it is now."""
+
+    def __init__(self, layer: "PrimeBlock", dtype: torch.dtype, device: torch.device):
+        at = layer.self_attn
+        self.qkv = torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight], dim=0)
+        self.norm = _lib.qk_norm(at.q_norm if at.use_qk_norm else None, at.k_norm if at.use_qk_norm else None,
+                                 at.scaling, dtype)
+        if isinstance(at, PrimeSelectiveMomentAttention):
+            self.decay = None
+            self.sel = (at.get_tau(device).float().contiguous(), at.get_beta(device).float().contiguous())
+        else:
+            self.decay = _lib.decay_tensor(at.decay, at.num_heads, device)
+            self.sel = None
+
+
+def _step_constants(model: "PrimeForCausalLM") -> List[_LayerStep]:
+    w = model.embed_tokens.weight
+    return [_LayerStep(layer, w.dtype, w.device) for layer in model.layers]
+
+
+def _fused_step_supported(model: "PrimeForCausalLM") -> bool:
+    """The fused step takes the QK LayerNorm parameters in the activations'
+    dtype, on the model's device (the kernels read them directly)."""
+    w = model.embed_tokens.weight
+    if not w.is_cuda:
+        return False
+    for layer in model.layers:
+        at = layer.self_attn
+        if at.use_qk_norm:
+            for t in (at.q_norm.weight, at.q_norm.bias, at.k_norm.weight, at.k_norm.bias):
+                if t is None or t.dtype != w.dtype or t.device != w.device or not t.is_contiguous():
+                    return False
+    return True
+
+
+@torch.no_grad()
+def _fused_step(model: "PrimeForCausalLM", tokens: torch.Tensor, states, consts: List[_LayerStep],
+                inplace: bool):
+    """One token per sequence through the whole model (the blocks of
+    model.py:107-118, then the final norm and lm_head): embedding -> per layer
+    add_rmsnorm -> one stacked q/k/v GEMM -> the decode kernel with the QK-norm
+    and 1/sqrt(D) inside (attention.py:96-143, or selective.py:384-409) -> o_proj
+    -> add_rmsnorm -> MLP; each residual add is fused into the following RMSNorm
+    with the block's rounding.  Returns (logits [B, V], next states).
+
+    inplace: the kernels update `states` in place (every layer's state must be
+    given).  Otherwise the states are functional, as in the reference: new
+    6-tuples are returned and the given ones are not written (unless the
+    module was built with inplace_state and the given tensors are its own
+    layout)."""
+    cfg = model.config
+    x = model.embed_tokens(tokens).reshape(-1, cfg.hidden_size)  # the residual stream, updated in place
+    B = x.shape[0]
+    dev = x.device
+    pending = None
+    next_states = []
+    for i, (layer, c) in enumerate(zip(model.layers, consts)):
+        at = layer.self_attn
+        H, Hk, D = at.num_heads, at.num_kv_heads, at.head_dim
+        n1 = torch.empty_like(x)
+        _lib.add_rmsnorm(x, pending, layer.input_layernorm.weight, n1, layer.input_layernorm.eps)
+        qkv = _decode_linear(n1, c.qkv)
+        q = qkv[:, :H * D].view(B, H, D)
+        k = qkv[:, H * D:(H + Hk) * D].view(B, Hk, D)
+        v = qkv[:, (H + Hk) * D:].view(B, Hk, D)
+        st = states[i] if states is not None else None
+        if inplace:
+            st_in = st_out = st
+        else:
+            st_in = _lib.as_state(st, B, H, D, dev) if st is not None else None
+            if at.inplace_state and st_in is not None and all(a.data_ptr() == b.data_ptr()
+                                                              for a, b in zip(st_in, st)):
+                st_out = st_in
+            else:
+                st_out = _lib.new_state(B, H, D, dev)
+        y = torch.empty(B, H, D, device=dev, dtype=x.dtype)
+        if c.sel is not None:
+            # lambda_t = exp(-Delta_t / tau_h) formed in the kernel (selective.py:368, 385-386)
+            tau, beta = c.sel
+            gate = _lib.selective_gate(B, H, step=at.delta_proj(n1), tau=tau)
+            _lib.selective_decode_step(q, k, v, gate, beta, at.eps, c.norm, st_in, st_out, y)
+        else:
+            _lib.decode_step_qknorm(q, k, v, c.decay, at.eps, c.norm, st_in, st_out, y)
+        next_states.append(st_out)
+        a = _decode_linear(y.view(B, -1), at.o_proj.weight)
+        n2 = torch.empty_like(x)
+        _lib.add_rmsnorm(x, a, layer.post_attention_layernorm.weight, n2, layer.post_attention_layernorm.eps)
+        if isinstance(layer.mlp, PrimeGeluMLP):
+            pending = _decode_linear(_decode_linear(n2, layer.mlp.up_proj.weight, gelu=True),
+                                     layer.mlp.down_proj.weight)
+        else:
+            pending = layer.mlp(n2)
+    nf = torch.empty_like(x)
+    _lib.add_rmsnorm(x, pending, model.norm.weight, nf, model.norm.eps)
+    return model.lm_head(nf), next_states
+
+
 class GreedyDecoder:
     """Greedy decoding with in-place states and a HIP-graph-captured step.
 
     ``prefill(input_ids)`` runs the prompt through the chunked kernels and
     keeps one state 6-tuple per layer; ``step()`` appends one token per
-    sequence: embedding -> layers (decode kernel, state in place) -> norm ->
-    lm_head -> argmax, the same computation as ``generate`` at temperature 0
-    (model.py:230-231).  With ``use_graph`` the step is captured once after
+    sequence with the model's fused one-token step (the one
+    ``PrimeForCausalLM.forward`` runs for a single token, so the tokens equal
+    those of ``generate`` at temperature 0, model.py:230-231), states updated
+    in place, then argmax.  With ``use_graph`` the step is captured once after
     the prefill and replayed; every buffer it touches is fixed.
     """
 
     def __init__(self, model: PrimeForCausalLM, use_graph: bool = True):
+        # the modules keep their functional state contract: no module flag is
+        # changed here; the decoder's own prefill starts from no state and its
+        # step hands the kernels the same buffers as input and output
+        if not _fused_step_supported(model):
+            raise ValueError("GreedyDecoder needs the model on a HIP device with QK LayerNorm parameters in the "
+                             "activations' dtype")
         self.model = model.eval()
         self.use_graph = use_graph
         self.graph = None
         self.states = None
-        self._decay, self._norm, self._qkv, self._sel = {}, {}, {}, {}
-        dev = model.embed_tokens.weight.device
-        # the modules keep their functional state contract: the decoder's own
-        # prefill starts from no state and its step hands the decode kernel the
-        # same buffers as input and output, so no module flag is changed here
-        for layer in model.layers:
-            at = layer.self_attn
-            if not isinstance(at, PrimeSelectiveMomentAttention):
-                self._decay[id(at)] = _lib.decay_tensor(at.decay, at.num_heads, dev)
-            self._norm[id(at)] = _lib.qk_norm(at.q_norm if at.use_qk_norm else None,
-                                              at.k_norm if at.use_qk_norm else None, at.scaling,
-                                              model.embed_tokens.weight.dtype)
+        self.consts = None
 
     @torch.no_grad()
     def prefill(self, input_ids: torch.Tensor) -> torch.Tensor:
@@ -318,55 +431,15 @@ class GreedyDecoder:
         self.states = [tuple(s) for s in out["states"]]
         self.token = torch.empty(input_ids.shape[0], 1, dtype=torch.int64, device=input_ids.device)
         _lib.argmax(out["logits"][:, -1, :], self.token)
-        # q/k/v projection weights stacked into one [Hq*D + 2*Hkv*D, hidden]
-        # matrix per layer (one GEMM per step), taken from the module now
-        for layer in m.layers:
-            at = layer.self_attn
-            self._qkv[id(at)] = torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight], dim=0)
-            if isinstance(at, PrimeSelectiveMomentAttention):  # tau_h and beta_h as the module has them now
-                dev = at.log_tau.device
-                self._sel[id(at)] = (at.get_tau(dev).float().contiguous(), at.get_beta(dev).float().contiguous())
+        # the step's per-layer constants, taken from the modules now
+        self.consts = _step_constants(m)
         self.graph = None
         return self.token
 
     @torch.no_grad()
     def _step_eager(self) -> torch.Tensor:
-        """One token per sequence through the blocks, the residual adds fused
-        into the following RMSNorm (prime_add_rmsnorm: the same rounding as
-        the blocks' separate add), QK-norm and scale inside the decode kernel,
-        states updated in place.  The values equal PrimeBlock.forward's."""
-        m = self.model
-        cfg = m.config
-        x = m.embed_tokens(self.token).reshape(-1, cfg.hidden_size)  # the residual stream, updated in place
-        B = x.shape[0]
-        pending = None
-        for layer, st in zip(m.layers, self.states):
-            at = layer.self_attn
-            n1 = torch.empty_like(x)
-            _lib.add_rmsnorm(x, pending, layer.input_layernorm.weight, n1, layer.input_layernorm.eps)
-            nq, nk = at.num_heads * at.head_dim, at.num_kv_heads * at.head_dim
-            qkv = _decode_linear(n1, self._qkv[id(at)])
-            q = qkv[:, :nq].view(B, at.num_heads, at.head_dim)
-            k = qkv[:, nq:nq + nk].view(B, at.num_kv_heads, at.head_dim)
-            v = qkv[:, nq + nk:].view(B, at.num_kv_heads, at.head_dim)
-            y = torch.empty(B, at.num_heads, at.head_dim, device=x.device, dtype=x.dtype)
-            if id(at) in self._sel:
-                # lambda_t = exp(-Delta_t / tau_h) formed in the kernel (selective.py:368, 385-386)
-                tau, beta = self._sel[id(at)]
-                gate = _lib.selective_gate(B, at.num_heads, step=at.delta_proj(n1), tau=tau)
-                _lib.selective_decode_step(q, k, v, gate, beta, at.eps, self._norm[id(at)], st, st, y)
-            else:
-                _lib.decode_step_qknorm(q, k, v, self._decay[id(at)], at.eps, self._norm[id(at)], st, st, y)
-            a = _decode_linear(y.view(B, -1), at.o_proj.weight)
-            n2 = torch.empty_like(x)
-            _lib.add_rmsnorm(x, a, layer.post_attention_layernorm.weight, n2, layer.post_attention_layernorm.eps)
-            if isinstance(layer.mlp, PrimeGeluMLP):
-                pending = F.linear(_decode_linear(n2, layer.mlp.up_proj.weight, gelu=True), layer.mlp.down_proj.weight)
-            else:
-                pending = layer.mlp(n2)
-        nf = torch.empty_like(x)
-        _lib.add_rmsnorm(x, pending, m.norm.weight, nf, m.norm.eps)
-        _lib.argmax(m.lm_head(nf), self.token)  # the embedding above has consumed the old token
+        logits, _ = _fused_step(self.model, self.token, self.states, self.consts, inplace=True)
+        _lib.argmax(logits, self.token)  # the embedding above has consumed the old token
         return self.token
 
     @torch.no_grad()

@@ -49,7 +49,7 @@ class PrimeSelectiveMomentAttention(nn.Module):
         self.use_qk_norm = use_qk_norm
         self.min_tau = min_tau
         self.max_tau = max_tau
-        self.inplace_state = False  # set by GreedyDecoder: L == 1 updates the incoming state tensors
+        self.inplace_state = False  # True: L == 1 updates the incoming state tensors in place
         self.q_proj = nn.Linear(hidden_size, num_heads * head_dim, bias=False)
         self.k_proj = nn.Linear(hidden_size, self.num_kv_heads * head_dim, bias=False)
         self.v_proj = nn.Linear(hidden_size, self.num_kv_heads * head_dim, bias=False)

@@ -151,6 +151,31 @@ def test_chunked_state_carry_invariant():
 
 
 @pytest.mark.parametrize("carry", ["dense", "scan"])
+def test_config1_cpu_plumbing(carry):
+    """BASELINE config 1 on the CPU reference path: fp32, B=1, H=12, L=512,
+    D=64, q/k/v ~ N(0,1) with q/k L2-normalised, lambda 0.9995 per head.  The
+    recurrent readout O_t (attention.py:119-143) against the chunked form at
+    chunk 64 (chunked_ssd.py:48-184): the fp64 restatements agree to
+    rounding, and the fp32 PyTorch-CPU restatement (with the reference's
+    O(Nc^2) carry, or the O(Nc) scan) within the fp32 tolerance 1e-3."""
+    import torch
+    from oracle import torch_cpu as T
+    B, H, L, D = 1, 12, 512, 64
+    q, k, v = O.make_inputs((B, H, L, D), seed=1, bf16=False)
+    lam = np.full(H, 0.9995)
+    yr, sr = O.recurrent(q.reshape(H, L, D), k.reshape(H, L, D), v.reshape(H, L, D), lam)
+    yc, sc = O.chunked(q.reshape(H, L, D), k.reshape(H, L, D), v.reshape(H, L, D), lam, chunk=64)
+    _close(yc, yr, 1e-10)
+    _states_close(sc, sr, 1e-10)
+    y, st = T.chunked_core(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+                           torch.tensor(lam, dtype=torch.float32), chunk=64, carry=carry)
+    assert y.dtype == torch.float32
+    assert O.rel_err(y.double().numpy().reshape(H, L, D), yr) < 1e-3
+    for a, b in zip(st, sr):
+        assert O.rel_err(a.double().numpy().reshape(-1), np.asarray(b).reshape(-1)) < 1e-3
+
+
+@pytest.mark.parametrize("carry", ["dense", "scan"])
 @pytest.mark.parametrize("L,with_state", [(200, False), (129, True), (64, True)])
 def test_torch_cpu_restatement_matches_oracle(carry, L, with_state):
     """The fp32 PyTorch CPU baseline (oracle/torch_cpu.py) agrees with the fp64
