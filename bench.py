@@ -3,38 +3,36 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--decode-steps K2] [--no-cpu]
 
-One "step" is one chunked prefill (prime_chunked_prefill) of the chunked-prefill
-workload: B=8 sequences x H=12 heads x L=8192 tokens, D=64, chunk 64, bf16
-q/k/v (N(0,1), L2-normalised per head, q scaled by 1/8), per-head lambda
-~ U[0.99, 0.9999], zero initial state, bf16 y and fp32 final state.
-`value` = prefill tokens/s = B*L / (seconds per step), inputs resident in HBM.
-
-The same JSON line carries
-  roofline      the dominant kernel of the step (the fused chunk loop), its
-                average launch duration from HIP events recorded by the library
-                around each launch inside the timed region, against HBM peak
-                (and, as frac_of_measured, against hbm_measured);
-  hbm_measured  achievable HBM bandwidth on this GPU (device copy and an
-                in-place stream over 2.5 GB);
-  decode        the fused decode step at B=512 sequences x 12 layers x 12 heads
-                (one launch per layer, states pre-filled by 1024 tokens) and at
-                B=256, tok/s and its own roofline;
-  selective     selective PRIME (per-token decays, beta-weighted keys): the
-                prefill at the config-2 shape and the decode step at B=256;
-  hybrid        the hybrid window-PRIME pieces: eviction accumulator and
-                fp32-input prefill at the config-2 shape, per-token update and
-                readout at B=256;
-  backward      the prefill backward (dq and dk/dv passes) at the config-2
-                shape and at a training shape, with its roofline;
-  delta         the chunked delta-rule prefill at config 5 (B=1, H=12,
-                L=131072): tok/s, per-kernel time, sustained tok/s per 16384
-                tokens and the memory in use (flat state);
-  model         the PRIME-125M-shaped LM end to end: prefill tok/s (B=32 x
-                2048) and greedy decode tok/s at B=32 and B=256 (HIP-graph step);
-  cpu_baseline  the reference's C99 engine (built from its sources into
-                oracle/_ref by oracle/Makefile) timed single-threaded on a
-                bounded sample of the same workload, plus the PyTorch-CPU and
-                C/OpenMP restatements under cpu_baselines.
+The headline is BASELINE.json's metric, "prefill tok/s + decode tok/s (B=256)
+PRIME-125M": the PRIME-125M-shaped causal LM (12 layers, d_model 768, 12 x 64
+heads, GELU MLP 3072, tied vocab 50304, bf16 weights, fp32 states, LayerNorm
+QK-norm, random init).  One "step" is one prefill of B=32 x 2048 random token
+ids (all layers, the states, and the last position's logits and greedy token);
+W untimed steps, then K timed steps between synchronisations.
+  value         prefill tokens/s = 32 * 2048 / (seconds per step)
+  decode_tok_s  greedy decode tokens/s at B=256 (the metric's decode batch):
+                the HIP-graph one-token step (embedding, 12 layers, lm_head,
+                argmax), timed over --decode-steps steps after a 128-token
+                prompt; decode_B32 (config 4's batch) rides along
+  roofline      the prefill call against dense bf16 MFMA peak (algorithmic
+                flops per call / measured seconds per call); decode_roofline
+                the decode step against HBM peak (weights + state bytes per
+                step / measured seconds per step)
+  cpu_baseline  the fp32 PyTorch-CPU restatement of the same model
+                (oracle/torch_cpu.py CausalLMCPU, the reference's chunked core
+                with its O(Nc^2) carry) on the same weights: a bounded sample
+                of the prefill, and decode steps at B=256 under
+                decode_cpu_baseline
+Extra keys carry the kernel-level workloads of BASELINE.json (run first; they
+also bring the GPU clocks up before the headline):
+  kernels.prefill_config2  the chunked prefill alone (B=8, H=12, L=8192), its
+                fused chunk kernel's HBM roofline from HIP events inside the
+                timed region, and the kernel's rocprof-calibrated traffic
+  decode        the fused decode kernel at B=512 x 12 layers x 12 heads (and
+                B=256), states pre-filled by 1024 tokens, HBM roofline
+  delta, selective, hybrid, backward   the other built paths
+  hbm_measured  achievable HBM bandwidth on this GPU
+  gpu_clock     the graphics clock read before and after the headline
 The CPU legs are the only use of oracle/ here, and only as timing baselines.
 """
 from __future__ import annotations
@@ -60,9 +58,13 @@ DECODE_BYTES_PER_TILE = 2 * STATE_BYTES + 3 * 2 * D + 2 * D  # state r+w, bf16 q
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000, help="timed prefill steps")
-    ap.add_argument("--warmup", type=int, default=1000, help="untimed steps first (also brings the GPU clocks up)")
-    ap.add_argument("--decode-steps", type=int, default=1000, help="timed decode steps (12 layers each)")
+    ap.add_argument("--steps", type=int, default=30, help="timed PRIME-125M prefill steps (B=32 x 2048 each)")
+    ap.add_argument("--warmup", type=int, default=5, help="untimed prefill steps before them")
+    ap.add_argument("--decode-steps", type=int, default=256, help="timed greedy decode steps of the model")
+    ap.add_argument("--kernel-steps", type=int, default=200,
+                    help="timed calls of each kernel-level leg (chunked prefill, selective, hybrid, backward)")
+    ap.add_argument("--kernel-decode-steps", type=int, default=1000,
+                    help="timed steps of the decode-kernel leg (12 layers each)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode legs")
@@ -71,7 +73,7 @@ def parse_args():
     ap.add_argument("--no-selective", action="store_true", help="skip the selective PRIME leg")
     ap.add_argument("--no-hybrid", action="store_true", help="skip the hybrid window-PRIME leg")
     ap.add_argument("--no-backward", action="store_true", help="skip the prefill-backward leg")
-    ap.add_argument("--cpu-budget", type=float, default=8.0, help="seconds per CPU leg (approximate)")
+    ap.add_argument("--cpu-budget", type=float, default=6.0, help="seconds per CPU leg (approximate)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run a plain 1 GiB device copy 3 times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -171,11 +173,11 @@ def bench_prefill(args, lib, torch, dev):
     st = lib.new_state(B, H, D, dev)
     step = lib.bind_chunked_prefill(q, k, v, lam, 1.0, C, None, y, st)
     ws = step.buffers[7]
-    for _ in range(args.warmup):
+    for _ in range(50):
         step()
     torch.cuda.synchronize()
-    # timed region for `value`: the call alone, no instrumentation
-    ms = timed(step, args.steps, 0)
+    # the call alone, no instrumentation
+    ms = timed(step, args.kernel_steps, 0)
     # the same steps again with every kernel of the call bracketed by HIP events
     # on the call's stream, for the per-kernel durations (an event pair around
     # the dominant kernel alone would open while the preceding scan kernel still
@@ -183,7 +185,7 @@ def bench_prefill(args, lib, torch, dev):
     ids = (lib.KERNEL_PREFILL_CHUNKS, lib.KERNEL_PREFILL_SEGMENTS, lib.KERNEL_SEGMENT_SCAN)
     lib.timer_reset()
     lib.timer_enable(*ids)
-    ms_events = timed(step, args.steps, 0)
+    ms_events = timed(step, args.kernel_steps, 0)
     lib.timer_enable()
     kern = {lib.KERNEL_NAMES[kid]: kernel_ms(lib, kid) for kid in ids}
     main_ms, main_n = kernel_ms(lib, lib.KERNEL_PREFILL_CHUNKS)
@@ -223,12 +225,12 @@ def bench_decode(args, lib, torch, dev, B, layers=12, H=12, pool=16, prefill_tok
         for c in calls[it[0] % pool]:
             c()
         it[0] += 1
-    steps = args.decode_steps
+    steps = args.kernel_decode_steps
     # a step is `layers` back-to-back launches of the decode kernel and nothing
     # else, so the events around the timed region give the launch duration
     # (ms per step / layers, gaps between launches included) without events
     # between the launches
-    ms = timed(step, steps, args.warmup)
+    ms = timed(step, steps, 20)
     kms, n = ms / layers, steps * layers
     ok = all(bool(torch.isfinite(y).all().item()) for y in ys)
     per_launch = B * H * DECODE_BYTES_PER_TILE
@@ -246,60 +248,198 @@ def bench_decode(args, lib, torch, dev, B, layers=12, H=12, pool=16, prefill_tok
 
 
 # ----------------------------------------------------------------- model
-def bench_model(args, torch, dev, selective=False):
-    """PRIME-125M-shaped causal LM (12 layers, d_model 768, 12 x 64 heads,
-    GELU MLP 3072, tied 50304 vocab, bf16 weights, fp32 states, LayerNorm
-    QK-norm), random init.  Prefill B=32 x 2048 random ids (states + last-token
-    logits + argmax); then greedy decode with the HIP-graph step at B=32 and at
-    B=256 (prompt of 128 tokens: decode cost does not depend on position)."""
+MODEL_B, MODEL_L, DECODE_B, DECODE_PROMPT = 32, 2048, 256, 128
+
+
+def model_flop_per_token(cfg):
+    """Algorithmic flops per prefill token: 2 x (q, k, v, o: 4 d^2; up and
+    down: 2 d f) per layer, plus the chunked attention's 57,344 flop per
+    token-head.  The lm_head runs for the last position only: greedy decoding
+    needs no other logits."""
+    d, f, nl, H = cfg.hidden_size, cfg.intermediate_size, cfg.num_layers, cfg.num_heads
+    return 2 * nl * (4 * d * d + 2 * d * f) + nl * H * PREFILL_FLOP_PER_TOKEN_HEAD
+
+
+def model_decode_bytes_per_step(cfg, B):
+    """Algorithmic HBM bytes of one greedy step: every bf16 weight read once
+    (the 12 layers' projections and MLP, and the tied 50304 x 768 lm_head),
+    and every fp32 state read and written once."""
+    d, f, nl, H, V = cfg.hidden_size, cfg.intermediate_size, cfg.num_layers, cfg.num_heads, cfg.vocab_size
+    weights = 2 * (nl * (4 * d * d + 2 * d * f) + V * d)
+    return weights + 2 * nl * B * H * STATE_BYTES
+
+
+def bench_model(args, lib, torch, dev):
+    """The headline: PRIME-125M-shaped causal LM (12 layers, d_model 768,
+    12 x 64 heads, GELU MLP 3072, tied 50304 vocab, bf16 weights, fp32 states,
+    LayerNorm QK-norm), random init.  One step = the prefill of B=32 x 2048
+    random ids: the 12 layers with their final states, the last position's
+    logits and its greedy token (model.forward + argmax).  Then greedy decode
+    with the HIP-graph step at B=256 (a 128-token prompt; the step's cost does
+    not depend on the position) and at B=32 after the 2048-token prefill."""
     from prime_moment_attention import GreedyDecoder, PrimeForCausalLM, prime_125m_config
+    cfg = prime_125m_config("gelu")
     torch.manual_seed(args.seed)
-    model = PrimeForCausalLM(prime_125m_config("gelu", use_selective=selective)).to(device=dev,
-                                                                                  dtype=torch.bfloat16).eval()
+    model = PrimeForCausalLM(cfg).to(device=dev, dtype=torch.bfloat16).eval()
     gen = torch.Generator(device=dev).manual_seed(args.seed + 7)
-    V = model.config.vocab_size
-    if selective:  # off the identity initialisation: data-dependent step sizes, per-head beta
+    V = cfg.vocab_size
+    ids = torch.randint(0, V, (MODEL_B, MODEL_L), device=dev, generator=gen)
+    tok = torch.empty(MODEL_B, 1, dtype=torch.int64, device=dev)
+
+    def prefill():
         with torch.no_grad():
-            for layer in model.layers:
-                layer.self_attn.delta_proj.weight.normal_(0.0, 0.01, generator=gen)
-                layer.self_attn.log_beta.uniform_(-0.5, 0.5, generator=gen)
-    out = {"workload": "PRIME-125M-shaped LM: 12 layers, d_model 768, 12 heads x 64, GELU MLP 3072, "
-                       "vocab 50304 tied, bf16 weights, fp32 states, LayerNorm QK-norm, random init; "
-                       + ("selective attention (per-token decays, beta-weighted keys); " if selective else "")
-                       + "prefill B=32 x 2048 random ids, greedy decode 256 steps (HIP graph step)",
-           "params": sum(p.numel() for p in model.parameters())}
+            out = model(ids, return_states=True, logits_to_keep=1)
+            lib.argmax(out["logits"][:, -1, :], tok)
+        return out
 
-    def timed_once(fn):
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        r = fn()
-        e.record()
-        torch.cuda.synchronize()
-        return s.elapsed_time(e), r
+    clock_before = read_gpu_clock()
+    for _ in range(args.warmup):
+        prefill()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        prefill()
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / args.steps
+    clock_after = read_gpu_clock()
+    # the attention kernels of the same steps, stamped by their dispatches
+    ids_k = (lib.KERNEL_PREFILL_CHUNKS, lib.KERNEL_PREFILL_SEGMENTS, lib.KERNEL_SEGMENT_SCAN)
+    lib.timer_reset()
+    lib.timer_enable(*ids_k)
+    nk = min(args.steps, 10)
+    for _ in range(nk):
+        prefill()
+    torch.cuda.synchronize()
+    lib.timer_enable()
+    kern = {lib.KERNEL_NAMES[kid]: kernel_ms(lib, kid) for kid in ids_k}
+    lib.timer_reset()
+    attn_us = {n: {"avg_us": None if t is None else t * 1e3, "launches_per_step": c / nk}
+               for n, (t, c) in kern.items() if c}
+    fused_ms = kern[lib.KERNEL_NAMES[lib.KERNEL_PREFILL_CHUNKS]][0]
+    attn_per_layer_us = sum(v["avg_us"] * v["launches_per_step"] for v in attn_us.values()) / cfg.num_layers
+    th = MODEL_B * cfg.num_heads * MODEL_L
+    attn_bytes = th * PREFILL_BYTES_PER_TOKEN_HEAD + MODEL_B * cfg.num_heads * STATE_BYTES
+    tokens = MODEL_B * MODEL_L
+    flops = tokens * model_flop_per_token(cfg)
+    out = {"prefill": {"B": MODEL_B, "L": MODEL_L, "ms": ms, "tok_s": tokens / (ms * 1e-3),
+                       "flop_per_token": model_flop_per_token(cfg), "flop_per_step": flops,
+                       "attention_kernels": attn_us, "attention_us_per_layer": attn_per_layer_us,
+                       "attention_roofline": {
+                           "kernel": "prefill_bf16_kernel (fused chunk loop, QK-norm on load) per layer",
+                           "bound": "hbm", "bytes_per_launch": attn_bytes, "avg_launch_us": fused_ms * 1e3,
+                           "achieved": attn_bytes / (fused_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                           "frac": attn_bytes / (fused_ms * 1e-3) / PEAK_HBM}},
+           "params": sum(p.numel() for p in model.parameters()),
+           "gpu_clock": {"before_prefill": clock_before, "after_prefill": clock_after}}
+    out["roofline"] = {"kernel": "PRIME-125M prefill step, all kernels (library GEMMs of the projections and MLP, "
+                                 "the fused PRIME prefill, norms, GELU)", "bound": "mfma",
+                       "achieved": flops / (ms * 1e-3) / 1e12, "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                       "frac": flops / (ms * 1e-3) / PEAK_BF16, "traffic": None,
+                       "flop_per_step": flops, "avg_step_ms": ms}
 
-    B, L = 32, 2048
-    ids = torch.randint(0, V, (B, L), device=dev, generator=gen)
-    dec = GreedyDecoder(model, use_graph=True)
-    for _ in range(2):
-        dec.prefill(ids)
-    reps = 3
-    ms = sum(timed_once(lambda: dec.prefill(ids))[0] for _ in range(reps)) / reps
-    out["prefill"] = {"B": B, "L": L, "tok_s": B * L / (ms * 1e-3), "ms": ms}
-    for Bd, Lp in ((32, None), (256, 128)):
-        if Lp is not None:
-            dec = GreedyDecoder(model, use_graph=True)
-            dec.prefill(torch.randint(0, V, (Bd, Lp), device=dev, generator=gen))
+    def decode_leg(Bd, prompt):
+        dec = GreedyDecoder(model, use_graph=True)
+        dec.prefill(prompt)
         for _ in range(4):
-            dec.step()  # first step captures the graph
-        steps = 256
-        ms, _ = timed_once(lambda: [dec.step() for _ in range(steps)])
-        out[f"decode_B{Bd}"] = {"B": Bd, "steps": steps, "tok_s": Bd * steps / (ms * 1e-3),
-                                "ms_per_step": ms / steps,
-                                "state_bytes": 12 * Bd * 12 * STATE_BYTES}
-    del model, dec
+            dec.step()  # the first step captures the graph
+        torch.cuda.synchronize()
+        s_, e_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_.record()
+        for _ in range(args.decode_steps):
+            dec.step()
+        e_.record()
+        torch.cuda.synchronize()
+        dms = s_.elapsed_time(e_) / args.decode_steps
+        byts = model_decode_bytes_per_step(cfg, Bd)
+        res = {"B": Bd, "prompt_tokens": prompt.shape[1], "steps": args.decode_steps, "ms_per_step": dms,
+               "tok_s": Bd / (dms * 1e-3),
+               "roofline": {"kernel": f"greedy decode step at B={Bd}, all kernels (HIP graph)", "bound": "hbm",
+                            "achieved": byts / (dms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                            "frac": byts / (dms * 1e-3) / PEAK_HBM, "traffic": None, "bytes_per_step": byts,
+                            "avg_step_ms": dms},
+               "states": dec.states}
+        del dec
+        return res
+
+    d256 = decode_leg(DECODE_B, torch.randint(0, V, (DECODE_B, DECODE_PROMPT), device=dev, generator=gen))
+    d32 = decode_leg(MODEL_B, ids)
+    out["decode_B256"] = {k: v for k, v in d256.items() if k != "states"}
+    out["decode_B32"] = {k: v for k, v in d32.items() if k != "states"}
+    out["_model"], out["_ids"] = model, ids
+    out["_decode_states_B256"] = d256["states"]
     torch.cuda.empty_cache()
     return out
+
+
+def bench_model_selective(args, torch, dev):
+    """The same model with the selective attention of the shipped PRIME-125M
+    (per-token decays, beta-weighted keys; off the identity initialisation):
+    prefill B=32 x 2048 and greedy decode at B=256."""
+    from prime_moment_attention import GreedyDecoder, PrimeForCausalLM, prime_125m_config
+    torch.manual_seed(args.seed)
+    model = PrimeForCausalLM(prime_125m_config("gelu", use_selective=True)).to(
+        device=dev, dtype=torch.bfloat16).eval()
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 7)
+    with torch.no_grad():
+        for layer in model.layers:
+            layer.self_attn.delta_proj.weight.normal_(0.0, 0.01, generator=gen)
+            layer.self_attn.log_beta.uniform_(-0.5, 0.5, generator=gen)
+    V = model.config.vocab_size
+    ids = torch.randint(0, V, (MODEL_B, MODEL_L), device=dev, generator=gen)
+    run = lambda: model(ids, return_states=True, logits_to_keep=1)
+    with torch.no_grad():
+        ms = timed(run, 5, 2)
+    dec = GreedyDecoder(model, use_graph=True)
+    dec.prefill(torch.randint(0, V, (DECODE_B, DECODE_PROMPT), device=dev, generator=gen))
+    dms = timed(dec.step, max(64, args.decode_steps // 2), 4)
+    del model, dec
+    torch.cuda.empty_cache()
+    return {"workload": "PRIME-125M shape with selective attention (per-token decays, beta-weighted keys): "
+                        "prefill B=32 x 2048, greedy decode B=256",
+            "prefill": {"ms": ms, "tok_s": MODEL_B * MODEL_L / (ms * 1e-3)},
+            "decode_B256": {"ms_per_step": dms, "tok_s": DECODE_B / (dms * 1e-3)}}
+
+
+def read_gpu_clock():
+    """The graphics clock(s) of the visible GPU in MHz, from amd-smi (or
+    rocm-smi); an error string when neither answers."""
+    import subprocess
+    for cmd in (["amd-smi", "metric", "--clock", "--json"], ["rocm-smi", "--showclocks", "--json"]):
+        try:
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=20)
+        except (OSError, subprocess.TimeoutExpired) as exc:
+            err = f"{cmd[0]}: {exc}"
+            continue
+        try:
+            data = json.loads(r.stdout[r.stdout.find("[") if r.stdout.lstrip().startswith("[") else
+                                      r.stdout.find("{"):])
+        except ValueError:
+            err = f"{cmd[0]}: unparsed output {r.stdout[:120]!r}"
+            continue
+        found = {}
+
+        def walk(x, path):
+            if isinstance(x, dict):
+                for k, v in x.items():
+                    walk(v, path + (str(k),))
+            elif isinstance(x, list):
+                for i, v in enumerate(x):
+                    walk(v, path + (str(i),))
+            else:
+                p = "/".join(path).lower()
+                if ("gfx" in p or "sclk" in p) and ("clk" in p or "value" in p or "clock" in p):
+                    found["/".join(path)] = x
+        walk(data, ())
+        cur = {k.split("/")[-3]: v for k, v in found.items() if k.endswith("/clk/value")}
+        mx = [v for k, v in found.items() if k.endswith("/max_clk/value")]
+        if cur:
+            return {"tool": cmd[0], "gfx_mhz": cur, "max_mhz": mx[0] if mx else None}
+        if found:
+            return {"tool": cmd[0], "raw": dict(list(found.items())[:8])}
+        err = f"{cmd[0]}: no graphics clock in its output"
+    return {"error": err}
 
 
 # ----------------------------------------------------------------- selective
@@ -326,7 +466,7 @@ def bench_selective(args, lib, torch, dev):
     torch.cuda.synchronize()
     lib.timer_reset()
     lib.timer_enable(*ids)
-    steps = max(50, args.steps // 10)
+    steps = max(50, args.kernel_steps // 4)
     ms = timed(run, steps, 0)
     lib.timer_enable()
     kern = {lib.KERNEL_NAMES[kid]: kernel_ms(lib, kid) for kid in ids}
@@ -370,7 +510,7 @@ def bench_selective(args, lib, torch, dev):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         step()
-    dsteps = max(100, args.decode_steps // 4)
+    dsteps = max(100, args.kernel_decode_steps // 4)
     dms = timed(g.replay, dsteps, 10)
     per_launch = Bd * H * (DECODE_BYTES_PER_TILE + 4)
     out["decode_B256"] = {"tok_s": Bd / (dms * 1e-3), "ms_per_step": dms, "steps": dsteps,
@@ -419,7 +559,7 @@ def bench_hybrid(args, lib, torch, dev):
                              "avg_launch_us": main_ms * 1e3, "achieved": algo / (main_ms * 1e-3) / 1e9,
                              "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": algo / (main_ms * 1e-3) / PEAK_HBM}}
 
-    steps = max(50, args.steps // 10)
+    steps = max(50, args.kernel_steps // 4)
     # bf16 k, v in; fp32 final state out
     out["accumulate"] = leg(lambda: lib.accumulate(k, v, lam, None, st, workspace=ws),
                             (lib.KERNEL_PREFILL_SEGMENTS, lib.KERNEL_SEGMENT_SCAN), lib.KERNEL_PREFILL_SEGMENTS,
@@ -467,7 +607,7 @@ def bench_hybrid(args, lib, torch, dev):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             step()
-        dsteps = max(100, args.decode_steps // 4)
+        dsteps = max(100, args.kernel_decode_steps // 4)
         dms = timed(g.replay, dsteps, 10)
         per_launch = Bd * H * per_tile
         out[name] = {"tok_s": Bd / (dms * 1e-3), "ms_per_step": dms, "steps": dsteps, "layers": layers,
@@ -507,7 +647,7 @@ def bench_backward(args, lib, torch, dev):
         torch.cuda.synchronize()
         lib.timer_reset()
         lib.timer_enable(*ids)
-        steps = max(10, args.steps // 50)
+        steps = max(10, args.kernel_steps // 20)
         ms = timed(run, steps, 0)
         lib.timer_enable()
         kern = {lib.KERNEL_NAMES[kid]: kernel_ms(lib, kid) for kid in ids}
@@ -664,6 +804,51 @@ def cpu_prefill_legs(args):
     return legs
 
 
+def cpu_model_legs(args, model, ids, decode_states):
+    """The fp32 PyTorch-CPU restatement of the same model (oracle/torch_cpu.py
+    CausalLMCPU: the reference's layers and its chunked core with the O(Nc^2)
+    carry) on the same weights, all host cores.  Prefill: whole sequences of
+    the B=32 x 2048 workload, grown until about --cpu-budget seconds.  Decode:
+    greedy steps at B=256 from the GPU's states after the 128-token prompt
+    (a step's cost does not depend on the position), up to 8 steps or the
+    budget."""
+    import torch
+    from oracle.torch_cpu import CausalLMCPU
+    n = cpu_cores()
+    torch.set_num_threads(n)
+    cfg = model.config
+    c = CausalLMCPU(model.state_dict(), cfg.num_layers, cfg.num_heads, cfg.head_dim, cfg.decay, eps=cfg.eps,
+                    rms_eps=cfg.rms_norm_eps, qk_norm=cfg.use_qk_norm)
+    ids_c = ids.cpu()
+    impl = (f"fp32 PyTorch-CPU restatement of the reference model (model.py:47-200, attention through "
+            f"chunked_ssd.py:48-184 with its O(Nc^2) carry, step attention.py:119-143), same weights, "
+            f"torch threads {n}")
+    done, total = 0, 0.0
+    while done < ids_c.shape[0] and (done == 0 or total * (done + 1) / done < args.cpu_budget):
+        t0 = time.perf_counter()
+        c.prefill(ids_c[done:done + 1])
+        total += time.perf_counter() - t0
+        done += 1
+    L = ids_c.shape[1]
+    pre = {"value": done * L / total, "unit": "tok/s", "cores": n, "kind": "port",
+           "sample": f"prefill of {done} of {ids_c.shape[0]} sequences x {L} tokens of the workload, one sequence "
+                     f"per call ({done * L} tokens, {total:.2f} s)", "impl": impl}
+    states = [tuple(t.detach().float().cpu() for t in st) for st in decode_states]
+    Bd = states[0][0].shape[0]
+    tok = torch.randint(0, cfg.vocab_size, (Bd,), generator=torch.Generator().manual_seed(args.seed))
+    steps, total = 0, 0.0
+    while steps < 8 and (steps == 0 or total * (steps + 1) / steps < args.cpu_budget):
+        t0 = time.perf_counter()
+        logits, states = c.step(tok, states)
+        tok = logits.argmax(-1)
+        total += time.perf_counter() - t0
+        steps += 1
+    dec = {"value": Bd * steps / total, "unit": "tok/s", "cores": n, "kind": "port",
+           "sample": f"{steps} greedy decode steps at B={Bd} from the GPU's states after a 128-token prompt "
+                     f"({total:.2f} s)", "impl": impl}
+    return pre, dec
+
+
 def cpu_decode_leg(args):
     """Reference C99 engine, one decode step per (sequence, layer) of the B=512
     x 12-layer x 12-head workload, 1 thread, on a bounded number of sequences."""
@@ -714,47 +899,28 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    # kernel-level legs first: they also bring the GPU clocks up before the headline
     hbm = bench_hbm(torch, dev)
     ach = hbm["achievable_GBps"] * 1e9
     pf = bench_prefill(args, lib, torch, dev)
-    t_step = pf["ms"] * 1e-3
     main_s = pf["main_ms"] * 1e-3
-    achieved = pf["bytes"] / main_s
     traffic = load_traffic().get("prefill_chunks")  # measured for this kernel at this workload
-    rec = {
-        "metric": "prefill tok/s + decode tok/s (B=256) PRIME-125M, 1 MI355X; % MFMA/HBM roofline",
-        "value": pf["tokens"] / t_step,
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": pf["ms"],
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) q/k/v, L2-normalised q/k, bf16)",
-        "config": {"workload": "chunked prefill, BASELINE config 2: B=8 x H=12 x L=8192, D=64, chunk 64, "
-                               "bf16 q/k/v, per-head lambda U[0.99,0.9999], zero initial state, bf16 y, "
-                               "fp32 final state",
-                   "B": pf["B"], "H": pf["H"], "L": pf["L"], "D": D, "chunk": pf["C"],
-                   "state_dtype": "fp32", "accumulate": "fp32", "workspace_bytes": pf["ws_bytes"],
-                   "seed": args.seed},
-        "roofline": {"kernel": "prefill_bf16_kernel<false, false, true, true, false> (fused chunk loop, 16 waves)", "bound": "hbm",
-                     "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM,
+    kernels = {"prefill_config2": {
+        "workload": "chunked prefill alone, BASELINE config 2: B=8 x H=12 x L=8192, D=64, chunk 64, bf16 q/k/v, "
+                    "per-head lambda U[0.99,0.9999], zero initial state, bf16 y, fp32 final state",
+        "tok_s": pf["tokens"] / (pf["ms"] * 1e-3), "ms_per_call": pf["ms"], "calls": args.kernel_steps,
+        "workspace_bytes": pf["ws_bytes"], "finite": pf["finite"],
+        "roofline": {"kernel": "prefill_bf16_kernel<false, false, true, true, false> (fused chunk loop, 16 waves)",
+                     "bound": "hbm", "achieved": pf["bytes"] / main_s / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                     "frac": pf["bytes"] / main_s / PEAK_HBM,
                      "traffic": None if traffic is None else traffic.get("bytes_per_launch"),
                      "bytes_per_launch": pf["bytes"], "avg_launch_us": pf["main_ms"] * 1e3,
-                     "frac_of_measured": achieved / ach},
-        "hbm_measured": hbm,
-        "prefill": {"whole_call_GBps": pf["bytes"] / t_step / 1e9,
-                    "whole_call_hbm_frac": pf["bytes"] / t_step / PEAK_HBM,
-                    "tflops": pf["flops"] / t_step / 1e12, "mfma_frac": pf["flops"] / t_step / PEAK_BF16,
-                    "kernels": pf["kernels"], "ms_per_step_with_events": pf["ms_events"],
-                    "finite": pf["finite"]},
-        "gpu": f"{torch.cuda.get_device_name(dev)} ({torch.cuda.get_device_properties(dev).gcnArchName}, "
-               f"{torch.cuda.get_device_properties(dev).multi_processor_count} CUs)",
-    }
+                     "frac_of_measured": pf["bytes"] / main_s / ach},
+        "whole_call_GBps": pf["bytes"] / (pf["ms"] * 1e-3) / 1e9,
+        "whole_call_hbm_frac": pf["bytes"] / (pf["ms"] * 1e-3) / PEAK_HBM,
+        "mfma_frac": pf["flops"] / (pf["ms"] * 1e-3) / PEAK_BF16,
+        "kernels": pf["kernels"], "ms_per_call_with_events": pf["ms_events"]}}
+    extra = {}
     if not args.no_decode:
         d512 = bench_decode(args, lib, torch, dev, B=512)
         d256 = bench_decode(args, lib, torch, dev, B=256)
@@ -763,31 +929,72 @@ def main():
             if t is not None:
                 d["roofline"]["traffic"] = t.get("bytes_per_launch")
             d["roofline"]["frac_of_measured"] = d["roofline"]["achieved"] * 1e9 / ach
-        rec["decode"] = {"B=256": d256, "B=512": d512}
+        extra["decode"] = {"B=512": d512, "B=256": d256}
     if not args.no_delta:
-        rec["delta"] = bench_delta(args, lib, torch, dev)
+        extra["delta"] = bench_delta(args, lib, torch, dev)
     if not args.no_selective:
-        rec["selective"] = bench_selective(args, lib, torch, dev)
+        extra["selective"] = bench_selective(args, lib, torch, dev)
     if not args.no_hybrid:
-        rec["hybrid"] = bench_hybrid(args, lib, torch, dev)
+        extra["hybrid"] = bench_hybrid(args, lib, torch, dev)
     if not args.no_backward:
-        rec["backward"] = bench_backward(args, lib, torch, dev)
-    if not args.no_model:
-        rec["model"] = bench_model(args, torch, dev)
-        if not args.no_selective:
-            rec["model_selective"] = bench_model(args, torch, dev, selective=True)
+        extra["backward"] = bench_backward(args, lib, torch, dev)
+
+    # the headline: PRIME-125M prefill (value) and greedy decode at B=256
+    m = bench_model(args, lib, torch, dev)
+    model, ids, dstates = m.pop("_model"), m.pop("_ids"), m.pop("_decode_states_B256")
+    roof = m.pop("roofline")
+    d256m = m["decode_B256"]
+    rec = {
+        "metric": "prefill tok/s + decode tok/s (B=256) PRIME-125M, 1 MI355X; % MFMA/HBM roofline",
+        "value": m["prefill"]["tok_s"],
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": m["prefill"]["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform random token ids, random-init weights N(0, 0.02), seeded)",
+        "config": {"workload": "PRIME-125M-shaped causal LM (12 layers, d_model 768, 12 heads x 64, GELU MLP 3072, "
+                               "vocab 50304 tied, bf16 weights, fp32 states, LayerNorm QK-norm): value = prefill "
+                               "tok/s of B=32 x 2048 (a step = one prefill: states and the last position's logits "
+                               "and greedy token); decode_tok_s = greedy decode tok/s at B=256 (HIP-graph step)",
+                   "prefill_batch": MODEL_B, "prefill_len": MODEL_L, "decode_batch": DECODE_B,
+                   "decode_prompt": DECODE_PROMPT, "decode_steps": args.decode_steps, "seed": args.seed},
+        "decode_tok_s": d256m["tok_s"],
+        "decode_ms_per_step": d256m["ms_per_step"],
+        "roofline": roof,
+        "decode_roofline": d256m["roofline"],
+        "model": m,
+        "kernels": kernels,
+        **extra,
+        "hbm_measured": hbm,
+        "gpu": f"{torch.cuda.get_device_name(dev)} ({torch.cuda.get_device_properties(dev).gcnArchName}, "
+               f"{torch.cuda.get_device_properties(dev).multi_processor_count} CUs)",
+        "gpu_clock": m.pop("gpu_clock"),
+    }
+    if not args.no_selective:
+        rec["model_selective"] = bench_model_selective(args, torch, dev)
     if not args.no_cpu:
         try:
-            legs = cpu_prefill_legs(args)
-            ref = [x for x in legs if x["kind"] == "reference"]
-            rec["cpu_baseline"] = ref[0] if ref else legs[0]
-            rec["cpu_baselines"] = legs
+            pre, dec = cpu_model_legs(args, model, ids, dstates)
+            rec["cpu_baseline"] = pre
+            rec["decode_cpu_baseline"] = dec
             rec["cpu_model"] = cpu_model()
-            if not args.no_decode:
-                rec["decode"]["cpu_baseline"] = cpu_decode_leg(args)
         except Exception as exc:  # the GPU figures stand without the CPU legs
             rec["cpu_baseline"] = None
             rec["cpu_baseline_error"] = f"{type(exc).__name__}: {exc}"
+        try:
+            legs = cpu_prefill_legs(args)
+            ref = [x for x in legs if x["kind"] == "reference"]
+            kernels["prefill_config2"]["cpu_baseline"] = ref[0] if ref else legs[0]
+            kernels["prefill_config2"]["cpu_baselines"] = legs
+            if not args.no_decode:
+                rec["decode"]["cpu_baseline"] = cpu_decode_leg(args)
+        except Exception as exc:
+            kernels["prefill_config2"]["cpu_baseline_error"] = f"{type(exc).__name__}: {exc}"
     print(json.dumps(rec), flush=True)
     return 0
 
