@@ -189,6 +189,14 @@ size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags)
  *               (16-byte aligned).  A smaller workspace (at least
  *               prime_delta_prefill_workspace_size(B, H, 64, 0)) makes the call
  *               process the sequence in more, shorter windows; results agree.
+ * When the workspace holds fewer chunks than the sequence, the per-chunk
+ * solve of the next window runs on a side stream while the current window is
+ * scanned on `stream`.  The library keeps one side stream and its events per
+ * (device, caller stream), created on the first such call outside graph
+ * capture and held for the life of the process; a call holds them for its
+ * whole enqueue sequence, so calls on different streams or threads are
+ * independent.  Under capture, or past 64 caller streams, the windows run on
+ * `stream` alone (same results).
  */
 int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k,
                         const prime_tensor_t *v, const float *beta, const float *alpha,

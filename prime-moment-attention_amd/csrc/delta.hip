@@ -327,170 +327,203 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Sequential scan over a window's chunks.  One workgroup (4 waves) per
-// (sequence, head).  Wave w owns the state rows of feature blocks 2w, 2w+1
-// (S^T tiles for every value block dw) and the y tiles of token block w; it
-// loads only its quarter of each chunk's record, into registers, one chunk
-// ahead.  The waves exchange the state as bf16 MFMA operand packs through LDS
-// (pack (dw, ks) = rows 4g..4g+3 of feature blocks 2ks and 2ks+1 at value
-// column 16dw + l%16, written by wave ks).  The Lyapunov scale of chunk c is
-// applied inside chunk c+1 (the packs hold the unscaled state), so one barrier
-// per chunk suffices:
+// Sequential scan over a window's chunks.  One workgroup of 8 waves per
+// (sequence, head), two waves per SIMD so that one wave's VALU work overlaps
+// the other's MFMAs.  Wave w owns the state rows of feature block w (S^T tiles
+// for every value block dv: 16 MFMAs per chunk) and two y tiles (token block
+// w/2, value blocks 2(w&1) and 2(w&1)+1: 8 MFMAs).  It loads only its share of
+// each chunk's record, into registers, one chunk ahead, through a buffer
+// descriptor (a fixed per-lane offset and scalar offsets: no per-load address
+// arithmetic).  The waves exchange the state as bf16 MFMA operand packs
+// through LDS: pack (dv, ks) = rows 4g..4g+3 of feature blocks 2ks and 2ks+1
+// at value column 16dv + l%16; wave w writes the half of pack (dv, w/2) that
+// holds its feature block.  The Lyapunov scale of chunk c is applied inside
+// chunk c+1 (the packs hold the unscaled state), so one barrier per chunk
+// suffices:
 //   y_c      = Y0 + sc_c (S~_c Z^T)
 //   S~_{c+1} = sc_c (e^cum_63 S~_c - M^T S~_c) + R0,  sc_{c+1} from |S~_{c+1}|_F.
 // ---------------------------------------------------------------------------
 namespace {
 
-// one wave's quarter of a chunk record, in registers
-struct RecQ {
-    bf16x8 mt[2][4];  // -M^T A operands: feature block 2w + hf, k-step ks
-    bf16x8 zb[4];     // Z^T B operands: token block w, k-step ks
-    uint2 r0[2][4];   // R0^T tiles: feature block 2w + hf, value block dw
-    uint2 y0[4];      // Y0^T tiles: value block dw, token block w
+constexpr int kScanWaves = 8;
+constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor, word 3 (gfx9 family)
+
+// one wave's share of a chunk record, in registers
+struct RecW {
+    bf16x8 mt[4];  // -M^T A operands: feature block w, k-step ks
+    bf16x8 zb[4];  // Z^T B operands: token block w/2, k-step ks
+    uint2 r0[4];   // R0^T tiles: feature block w, value block dv
+    uint2 y0[2];   // Y0^T tiles: value blocks 2(w&1) + j, token block w/2
     float e63;
 };
 
-__device__ __forceinline__ void load_recq(RecQ &R, const uint8_t *rec, int w, int lane) {
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-            R.mt[hf][ks] = *reinterpret_cast<const bf16x8 *>(rec + kRecMT + (((2 * w + hf) * 4 + ks) * 64 + lane) * 16);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-        R.zb[ks] = *reinterpret_cast<const bf16x8 *>(rec + kRecZB + ((w * 4 + ks) * 64 + lane) * 16);
-#pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int dw = 0; dw < 4; ++dw)
-            R.r0[hf][dw] = *reinterpret_cast<const uint2 *>(rec + kRecR0 + (((2 * w + hf) * 4 + dw) * 64 + lane) * 8);
-#pragma unroll
-    for (int dw = 0; dw < 4; ++dw)
-        R.y0[dw] = *reinterpret_cast<const uint2 *>(rec + kRecY0 + ((w * 4 + dw) * 64 + lane) * 8);
-    R.e63 = *reinterpret_cast<const float *>(rec + kRecSC);
+__device__ __forceinline__ bf16x8 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return as_bf16x8(__builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0)));
 }
 
-}  // namespace
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+}
 
-// One chunk of the scan (see above).  `cur` holds this chunk's record quarter;
-// `nxt` receives the next chunk's.  Called with the two register sets swapped
-// on alternate chunks, so that no copy (and no wait for the loads) is needed.
-__device__ __forceinline__ void scan_chunk(const DeltaArgs &a, int cw, int b, int h, int w, int lane, int g, int c16,
-                                           const uint8_t *rbase, f32x4 (&st)[2][4], float &sc, const RecQ &cur,
-                                           RecQ &nxt, bf16x8 (*sPk)[4][4][64], float (*sRed)[4]) {
-    const int buf = cw & 1;
-    const int c = a.c0 + cw;
-    // next chunk's quarter (clamped to the window: the duplicate is unused)
-    load_recq(nxt, rbase + static_cast<size_t>(min(cw + 1, a.nw - 1)) * kDeltaRecBytes, w, lane);
-    bf16x8 pk[4][4];
+// `ro`: byte offset of the chunk's record inside the window (uniform)
+__device__ __forceinline__ void load_recw(RecW &R, __amdgpu_buffer_rsrc_t rs, int ro, int w, int lane) {
+    const int v16 = lane * 16, v8 = lane * 8, tb = w >> 1, dvy = 2 * (w & 1);
 #pragma unroll
-    for (int dw = 0; dw < 4; ++dw)
+    for (int ks = 0; ks < 4; ++ks) R.mt[ks] = bload16(rs, v16, ro + kRecMT + (w * 4 + ks) * 1024);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) pk[dw][ks] = sPk[buf][dw][ks][lane];
-    // ---- y^T (value block dw, token block w) = Y0^T + sc S~ Z^T
-    const int t = c * kC + 16 * w + c16;
+    for (int ks = 0; ks < 4; ++ks) R.zb[ks] = bload16(rs, v16, ro + kRecZB + (tb * 4 + ks) * 1024);
 #pragma unroll
-    for (int dw = 0; dw < 4; ++dw) {
+    for (int dv = 0; dv < 4; ++dv) R.r0[dv] = bload8(rs, v8, ro + kRecR0 + (w * 4 + dv) * 512);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) R.y0[j] = bload8(rs, v8, ro + kRecY0 + (tb * 4 + dvy + j) * 512);
+    R.e63 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, ro + kRecSC, 0));
+}
+
+template <int DTY>
+__device__ __forceinline__ void store_y4(uint8_t *p, f32x4 v) {
+    if constexpr (DTY == PRIME_BF16) {
+        *reinterpret_cast<uint2 *>(p) = pack4(v);
+    } else if constexpr (DTY == PRIME_F32) {
+        *reinterpret_cast<f32x4 *>(p) = v;
+    } else {
+        uint16_t *h = reinterpret_cast<uint16_t *>(p);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) h[r] = f32_to_h16_bits(v[r]);
+    }
+}
+
+// y^T tiles (value blocks DV0, DV0+1; this wave's token block) = Y0^T + sc S~ Z^T
+// (DV0 a template constant: a runtime index would put the packs in scratch memory)
+template <int DTY, int DV0>
+__device__ __forceinline__ void y_tiles(const bf16x8 (&pk)[4][4], const RecW &cur, float sc, bool tok_ok,
+                                        uint8_t *yrow, int g) {
+    constexpr int es = DTY == PRIME_F32 ? 4 : 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
         f32x4 p = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) p = mfma(pk[dw][ks], cur.zb[ks], p);
-        const f32x4 y0 = unpack4(cur.y0[dw]);
+        for (int ks = 0; ks < 4; ++ks) p = mfma(pk[DV0 + j][ks], cur.zb[ks], p);
+        const f32x4 y0 = unpack4(cur.y0[j]);
         f32x4 yv;
 #pragma unroll
         for (int r = 0; r < 4; ++r) yv[r] = y0[r] + sc * p[r];
-        if (t < a.L) {
-            const int64_t o = b * a.y_sb + h * a.y_sh + t * a.y_sl + 16 * dw + 4 * g;
-            if (a.dt_y == PRIME_BF16) {
-                *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + o) = pack4(yv);
-            } else if (a.dt_y == PRIME_F32) {
-                *reinterpret_cast<f32x4 *>(static_cast<float *>(a.y) + o) = yv;
-            } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) store_elem(a.y, o + r, a.dt_y, yv[r]);
-            }
-        }
+        if (tok_ok) store_y4<DTY>(yrow + (16 * (DV0 + j) + 4 * g) * es, yv);
     }
-    // ---- S~'^T = sc (e^cum_63 S~^T - M^T S~^T) + R0^T on this wave's feature blocks
+}
+
+// One chunk of the scan.  `cur` holds this chunk's record share; `nxt`
+// receives the next chunk's.  Called with the two register sets swapped on
+// alternate chunks, so that no copy (and no wait for the loads) is needed.
+// `yrow`: this lane's y row (token 16 (w/2) + l%16 of the chunk).
+template <int DTY>
+__device__ __forceinline__ void scan_chunk(const DeltaArgs &a, int cw, int w, int lane, int g, int c16,
+                                           __amdgpu_buffer_rsrc_t rs, f32x4 (&st)[4], float &sc, const RecW &cur,
+                                           RecW &nxt, bf16x8 (*sPk)[4][4][64], float (*sRed)[kScanWaves],
+                                           uint8_t *yrow) {
+    const int buf = cw & 1;
+    const int tb = w >> 1;
+    // next chunk's share (clamped to the window: the duplicate is unused)
+    load_recw(nxt, rs, min(cw + 1, a.nw - 1) * static_cast<int>(kDeltaRecBytes), w, lane);
+    bf16x8 pk[4][4];
+#pragma unroll
+    for (int dv = 0; dv < 4; ++dv)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) pk[dv][ks] = sPk[buf][dv][ks][lane];
+    // ---- y^T (value blocks 2(w&1), 2(w&1)+1; token block tb)
+    const bool tok_ok = (a.c0 + cw) * kC + 16 * tb + c16 < a.L;
+    if (w & 1) y_tiles<DTY, 2>(pk, cur, sc, tok_ok, yrow, g);
+    else y_tiles<DTY, 0>(pk, cur, sc, tok_ok, yrow, g);
+    // ---- S~'^T = sc (e^cum_63 S~^T - M^T S~^T) + R0^T on feature block w
     float ss = 0.f;
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
+    for (int dv = 0; dv < 4; ++dv) {
+        f32x4 x;
 #pragma unroll
-        for (int dw = 0; dw < 4; ++dw) {
-            f32x4 x;
+        for (int r = 0; r < 4; ++r) x[r] = cur.e63 * st[dv][r];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) x[r] = cur.e63 * st[hf][dw][r];
+        for (int ks = 0; ks < 4; ++ks) x = mfma(cur.mt[ks], pk[dv][ks], x);
+        const f32x4 r0 = unpack4(cur.r0[dv]);
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) x = mfma(cur.mt[hf][ks], pk[dw][ks], x);
-            const f32x4 r0 = unpack4(cur.r0[hf][dw]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                x[r] = sc * x[r] + r0[r];
-                ss += x[r] * x[r];
-            }
-            st[hf][dw] = x;
+        for (int r = 0; r < 4; ++r) {
+            x[r] = sc * x[r] + r0[r];
+            ss += x[r] * x[r];
         }
+        st[dv] = x;
+    }
 #pragma unroll
-    for (int dw = 0; dw < 4; ++dw) sPk[buf ^ 1][dw][w][lane] = pack8x(st[0][dw], st[1][dw]);
+    for (int dv = 0; dv < 4; ++dv)
+        *reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(&sPk[buf ^ 1][dv][tb][lane]) + 8 * (w & 1)) =
+            pack4(st[dv]);
     ss = wave_sum(ss);
     if (lane == 0) sRed[buf][w] = ss;
     __syncthreads();
     // ---- Lyapunov clamp (:266-270), kept as the pending scale of the state
     sc = 1.0f;
     if (a.bound > 0.f) {
-        const float nrm = sqrtf(sRed[buf][0] + sRed[buf][1] + sRed[buf][2] + sRed[buf][3]);
-        sc = fminf(1.0f, a.bound / (nrm + 1e-6f));
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < kScanWaves; ++i) t += sRed[buf][i];
+        sc = fminf(1.0f, a.bound / (sqrtf(t) + 1e-6f));
     }
 }
 
-__global__ __launch_bounds__(256, 1) void delta_scan_kernel(const DeltaArgs a) {
-    __shared__ __attribute__((aligned(16))) bf16x8 sPk[2][4][4][64];  // [buf][dw][ks][lane]
-    __shared__ float sRed[2][4];
+}  // namespace
+
+template <int DTY>
+__global__ __launch_bounds__(kScanWaves * kWave, 1) void delta_scan_kernel(const DeltaArgs a) {
+    __shared__ __attribute__((aligned(16))) bf16x8 sPk[2][4][4][64];  // [buf][dv][ks][lane]
+    __shared__ float sRed[2][kScanWaves];
 
     const int tid = threadIdx.x;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
     const int seq = blockIdx.x;
     if (seq >= a.B * a.H) return;
     const int b = seq / a.H, h = seq - b * a.H;
-    const int w = wave;
     const size_t sofs = static_cast<size_t>(seq) * kD * kP;
-    const uint8_t *rbase = a.ws_rec + static_cast<size_t>(seq) * a.nw * kDeltaRecBytes;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        a.ws_rec + static_cast<size_t>(seq) * a.nw * kDeltaRecBytes, 0,
+        static_cast<int>(static_cast<size_t>(a.nw) * kDeltaRecBytes), kBufWord3);
 
-    // ---- state entering the window: st[hf][dw][r] = S[d = 16dw + c16][e = 16(2w + hf) + 4g + r]
+    // ---- state entering the window: st[dv][r] = S[d = 16dv + c16][e = 16w + 4g + r]
     const float *src = a.first ? a.state_in : a.ws_state;
-    f32x4 st[2][4];
+    f32x4 st[4];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
+    for (int dv = 0; dv < 4; ++dv)
+        st[dv] = src ? *reinterpret_cast<const f32x4 *>(src + sofs + (16 * dv + c16) * kP + 16 * w + 4 * g)
+                     : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int dw = 0; dw < 4; ++dw)
-            st[hf][dw] = src ? *reinterpret_cast<const f32x4 *>(src + sofs + (16 * dw + c16) * kP + 16 * (2 * w + hf) + 4 * g)
-                             : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int dw = 0; dw < 4; ++dw) sPk[0][dw][w][lane] = pack8x(st[0][dw], st[1][dw]);
+    for (int dv = 0; dv < 4; ++dv)
+        *reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(&sPk[0][dv][w >> 1][lane]) + 8 * (w & 1)) =
+            pack4(st[dv]);
     float sc = 1.0f;  // pending Lyapunov scale of the state in st / the packs
-    RecQ ra, rb;
-    load_recq(ra, rbase, w, lane);
+    RecW ra, rb;
+    load_recw(ra, rs, 0, w, lane);
     __syncthreads();
 
+    // this lane's y row in the window's first chunk, advanced by one chunk per step
+    constexpr int es = DTY == PRIME_F32 ? 4 : 2;
+    uint8_t *yrow = static_cast<uint8_t *>(a.y) +
+                    (b * a.y_sb + h * a.y_sh + static_cast<int64_t>(a.c0 * kC + 16 * (w >> 1) + c16) * a.y_sl) * es;
+    const int64_t ystep = static_cast<int64_t>(kC) * a.y_sl * es;
     int cw = 0;
     for (; cw + 1 < a.nw; cw += 2) {
-        scan_chunk(a, cw, b, h, w, lane, g, c16, rbase, st, sc, ra, rb, sPk, sRed);
-        scan_chunk(a, cw + 1, b, h, w, lane, g, c16, rbase, st, sc, rb, ra, sPk, sRed);
+        scan_chunk<DTY>(a, cw, w, lane, g, c16, rs, st, sc, ra, rb, sPk, sRed, yrow);
+        scan_chunk<DTY>(a, cw + 1, w, lane, g, c16, rs, st, sc, rb, ra, sPk, sRed, yrow + ystep);
+        yrow += 2 * ystep;
     }
-    if (cw < a.nw) scan_chunk(a, cw, b, h, w, lane, g, c16, rbase, st, sc, ra, rb, sPk, sRed);
+    if (cw < a.nw) scan_chunk<DTY>(a, cw, w, lane, g, c16, rs, st, sc, ra, rb, sPk, sRed, yrow);
 
     // ---- state leaving the window (the pending scale applied)
     float *dst = a.last ? a.state_out : a.ws_state;
     if (dst) {
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
+        for (int dv = 0; dv < 4; ++dv) {
+            f32x4 x = st[dv];
 #pragma unroll
-            for (int dw = 0; dw < 4; ++dw) {
-                f32x4 x = st[hf][dw];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) x[r] *= sc;
-                *reinterpret_cast<f32x4 *>(dst + sofs + (16 * dw + c16) * kP + 16 * (2 * w + hf) + 4 * g) = x;
-            }
+            for (int r = 0; r < 4; ++r) x[r] *= sc;
+            *reinterpret_cast<f32x4 *>(dst + sofs + (16 * dv + c16) * kP + 16 * w + 4 * g) = x;
+        }
     }
 }
 
@@ -560,34 +593,46 @@ __global__ __launch_bounds__(kStepWaves * 64) void delta_step_kernel(const Delta
 
 namespace {
 
-// Per-device side stream and events for overlapping the prep of window w+1 with
-// the scan of window w (the scan occupies one CU per (sequence, head); the
-// prep fills the rest).  Created once per device, default priority, kept for
-// the life of the process.
+// Side stream and events for overlapping the prep of window w+1 with the scan
+// of window w (the scan occupies one CU per (sequence, head); the prep fills
+// the rest).  One set per (device, caller stream), created on first use
+// outside any graph capture, default priority, kept for the life of the
+// process.  A call holds its set's lock for its whole enqueue sequence, so
+// that calls on different streams never share events and calls from several
+// host threads on one stream do not interleave their records and waits.
 struct SideStream {
+    int dev = -1;
+    hipStream_t caller = nullptr;
     hipStream_t s = nullptr;
     hipEvent_t start = nullptr, prep[2] = {nullptr, nullptr}, scan[2] = {nullptr, nullptr};
-    bool ok = false;
+    std::mutex mu;
 };
 
+constexpr int kMaxSideStreams = 64;
 std::mutex g_side_mu;
-SideStream g_side[64];
+SideStream g_side[kMaxSideStreams];
+int g_side_n = 0;
 
-SideStream *side_stream() {
+// The set of (current device, caller); null when it does not exist and may
+// not be created now (capture in progress, or the table is full): the caller
+// then runs the windows on its own stream alone.
+SideStream *side_stream(hipStream_t caller, bool may_create) {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lk(g_side_mu);
-    SideStream &x = g_side[dev];
-    if (!x.ok) {
-        const unsigned f = hipEventDisableTiming;
-        if (hipStreamCreateWithFlags(&x.s, hipStreamNonBlocking) != hipSuccess) return nullptr;
-        if (hipEventCreateWithFlags(&x.start, f) != hipSuccess) return nullptr;
-        for (int i = 0; i < 2; ++i)
-            if (hipEventCreateWithFlags(&x.prep[i], f) != hipSuccess ||
-                hipEventCreateWithFlags(&x.scan[i], f) != hipSuccess)
-                return nullptr;
-        x.ok = true;
-    }
+    for (int i = 0; i < g_side_n; ++i)
+        if (g_side[i].dev == dev && g_side[i].caller == caller) return &g_side[i];
+    if (!may_create || g_side_n >= kMaxSideStreams) return nullptr;
+    SideStream &x = g_side[g_side_n];
+    const unsigned f = hipEventDisableTiming;
+    if (hipStreamCreateWithFlags(&x.s, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&x.start, f) != hipSuccess) return nullptr;
+    for (int i = 0; i < 2; ++i)
+        if (hipEventCreateWithFlags(&x.prep[i], f) != hipSuccess || hipEventCreateWithFlags(&x.scan[i], f) != hipSuccess)
+            return nullptr;
+    x.dev = dev;
+    x.caller = caller;
+    ++g_side_n;  // published last: a half-built set is never found
     return &x;
 }
 
@@ -599,7 +644,13 @@ void launch_prep(const DeltaArgs &a, hipStream_t s) {
 
 void launch_scan(const DeltaArgs &a, hipStream_t s) {
     const TimerEvents t = timer_events(PRIME_KERNEL_DELTA_SCAN);
-    hipExtLaunchKernelGGL(delta_scan_kernel, dim3(a.B * a.H), dim3(256), 0, s, t.start, t.stop, 0, a);
+    const dim3 grid(a.B * a.H), block(kScanWaves * kWave);
+    if (a.dt_y == PRIME_BF16)
+        hipExtLaunchKernelGGL(delta_scan_kernel<PRIME_BF16>, grid, block, 0, s, t.start, t.stop, 0, a);
+    else if (a.dt_y == PRIME_F32)
+        hipExtLaunchKernelGGL(delta_scan_kernel<PRIME_F32>, grid, block, 0, s, t.start, t.stop, 0, a);
+    else
+        hipExtLaunchKernelGGL(delta_scan_kernel<PRIME_F16>, grid, block, 0, s, t.start, t.stop, 0, a);
     if (hipPeekAtLastError() != hipSuccess) timer_drop(t);
 }
 
@@ -620,7 +671,14 @@ DeltaArgs window_args(DeltaArgs a, int c0, int window, int NC, uint8_t *rec) {
 // (caller's stream) reads the other.
 hipError_t launch_delta_prefill(DeltaArgs a, int NC, int cap, hipStream_t stream) {
     uint8_t *rec0 = a.ws_rec;
-    if (NC <= cap || cap < 2) {
+    SideStream *ss = nullptr;
+    if (NC > cap && cap >= 2) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) != hipSuccess) cs = hipStreamCaptureStatusActive;
+        ss = side_stream(stream, cs == hipStreamCaptureStatusNone);
+    }
+    if (ss == nullptr) {
+        // one window at a time on the caller's stream
         const int window = NC <= cap ? NC : cap;
         for (int c0 = 0; c0 < NC; c0 += window) {
             const DeltaArgs w = window_args(a, c0, window, NC, rec0);
@@ -629,8 +687,7 @@ hipError_t launch_delta_prefill(DeltaArgs a, int NC, int cap, hipStream_t stream
         }
         return hipGetLastError();
     }
-    SideStream *ss = side_stream();
-    if (!ss) return hipErrorOutOfMemory;
+    std::lock_guard<std::mutex> lk(ss->mu);
     const int half = cap / 2;
     const size_t half_bytes = static_cast<size_t>(a.B) * a.H * half * kDeltaRecBytes;
     const int nwin = (NC + half - 1) / half;

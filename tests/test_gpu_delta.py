@@ -124,6 +124,53 @@ def test_delta_prefill_long_sequence_subset():
     assert_close(s, so, TOL_BF16, "S")
 
 
+def test_delta_prefill_concurrent_calls_on_two_streams():
+    """Two prime_delta_prefill calls enqueued at the same time from two host
+    threads, each on its own stream with a four-chunk workspace (so both run
+    the double-buffered path, prep on a side stream overlapped with the scan),
+    three times each: every result equals the one-window result of the same
+    inputs.  The calls share no side stream or event (one set per caller
+    stream, its lock held across the whole enqueue sequence)."""
+    import threading
+    B, H, L = 1, 2, 64 * 21 + 9
+    cases = [_inputs(B, H, L, seed=95 + i) for i in range(2)]
+    refs = [_run(*c, 0.995, 25.0) for c in cases]
+    results = [[], []]
+    errors = []
+    start = threading.Barrier(2)
+
+    def worker(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                q, k, v, beta, alpha = cases[i]
+                ins = (to_dev(q, torch.bfloat16), to_dev(k, torch.bfloat16), to_dev(v, torch.bfloat16), to_dev(beta),
+                       to_dev(alpha))
+                ws = torch.empty(_lib.delta_workspace_size(B, H, 64 * 4), dtype=torch.uint8, device=dev())
+                outs = [(torch.empty(B, H, L, D, device=dev()), torch.empty(B, H, D, 2 * D, device=dev()))
+                        for _ in range(3)]
+                s.synchronize()
+                start.wait()
+                for y, st in outs:
+                    _lib.delta_prefill(*ins, 0.995, FEAT_EPS, 25.0, None, y, st, workspace=ws)
+                s.synchronize()
+            results[i] = [(to_np(y).reshape(B * H, L, D), to_np(st).reshape(B * H, D, 2 * D)) for y, st in outs]
+        except Exception as exc:  # reported by the main thread
+            errors.append(exc)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors, errors
+    for i in range(2):
+        assert len(results[i]) == 3
+        for y, st in results[i]:
+            assert_close(y, refs[i][0], 1e-5, f"call {i} y")
+            assert_close(st, refs[i][1], 1e-5, f"call {i} S")
+
+
 @pytest.mark.parametrize("bound", [25.0, 0.3])
 def test_delta_decode_step_matches_oracle(bound):
     B, H = 3, 4
