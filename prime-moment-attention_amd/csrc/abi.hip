@@ -692,8 +692,8 @@ int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const 
     if (q->dtype != k->dtype || q->dtype != v->dtype || (q->dtype != PRIME_BF16 && q->dtype != PRIME_F32))
         return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "q/k/v must share dtype BF16 or F32");
     if (!valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported y dtype");
-    if (!rows_aligned(y, true))
-        return fail(PRIME_ERR_MISALIGNED, "y rows must start on 16-byte boundaries");
+    if (!rows_aligned(q, true) || !rows_aligned(k, true) || !rows_aligned(v, true) || !rows_aligned(y, true))
+        return fail(PRIME_ERR_MISALIGNED, "q/k/v/y rows must start on 16-byte boundaries");
     if (!aligned16(workspace)) return fail(PRIME_ERR_MISALIGNED, "workspace must be 16-byte aligned");
     if ((state_in && !aligned16(state_in)) || (state_out && !aligned16(state_out)))
         return fail(PRIME_ERR_MISALIGNED, "state buffers must be 16-byte aligned");

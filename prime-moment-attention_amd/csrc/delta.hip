@@ -36,9 +36,7 @@ namespace {
 
 constexpr int kP = 2 * kD;        // features
 constexpr int kP136 = kP + 8;     // 128-wide rows, 16-byte row reads
-constexpr int kP144 = kP + 16;    // 128-wide rows, transposed reads
 constexpr int kP72 = kD + 8;      // 64-wide rows, 16 / 8-byte row reads
-constexpr int kP80 = kD + 16;     // 64-wide rows, transposed reads
 constexpr int kRecMT = 0;         // -M^T A operands   [8 eb'][4 ks][64 lanes] x 16 B
 constexpr int kRecZB = 32768;     // Z^T B operands    [4 tb][4 ks][64 lanes] x 16 B
 constexpr int kRecR0 = 49152;     // R0^T acc tiles    [8 eb][4 dw][64 lanes] x 8 B (bf16x4)
@@ -49,7 +47,33 @@ static_assert(kRecSC + 16 <= static_cast<int>(kDeltaRecBytes), "record layout");
 
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
 
-__device__ __forceinline__ float ld_in(const void *p, int64_t i, int dt) { return load_elem(p, i, dt); }
+// 16 consecutive inputs of one row (bf16 or fp32; 32- or 64-byte aligned), zero when !valid
+__device__ __forceinline__ void load16(const void *p, int64_t off, int dt, bool valid, float (&o)[16]) {
+    if (!valid) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[e] = 0.f;
+        return;
+    }
+    if (dt == PRIME_BF16) {
+        const u32x4 *s = reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(p) + off);
+        const u32x4 a = s[0], b = s[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o[2 * i] = __uint_as_float(a[i] << 16);
+            o[2 * i + 1] = __uint_as_float(a[i] & 0xFFFF0000u);
+            o[8 + 2 * i] = __uint_as_float(b[i] << 16);
+            o[8 + 2 * i + 1] = __uint_as_float(b[i] & 0xFFFF0000u);
+        }
+    } else {
+        const f32x4 *s = reinterpret_cast<const f32x4 *>(static_cast<const float *>(p) + off);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 v = s[i];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[4 * i + r] = v[r];
+        }
+    }
+}
 
 __device__ __forceinline__ uint2 pack4(f32x4 x) { return uint2{pack2(x[0], x[1]), pack2(x[2], x[3])}; }
 
@@ -86,11 +110,12 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t sV[kC][kP72];     // v rows
     __shared__ __attribute__((aligned(16))) float sN[kC][kC + 4];      // N (strictly lower), fp32
     __shared__ __attribute__((aligned(16))) uint16_t sA[kC][kP72];     // A (lower), bf16
-    __shared__ __attribute__((aligned(16))) uint16_t sU[kC][kP80];     // U = T^-1 V
-    __shared__ __attribute__((aligned(16))) uint16_t sUw[kC][kP80];    // diag(omega) U
-    __shared__ __attribute__((aligned(16))) uint16_t sW[kC][kP144];    // W = T^-1 diag(e^cum) Phi
-    __shared__ __attribute__((aligned(16))) uint16_t sWw[kC][kP144];   // diag(omega) W
-    __shared__ float sCum[kC], sBeta[kC], sEc[kC], sOm[kC];  // cum, beta, e^cum, omega
+    // the solve's results, transposed (one row per column of X = [U | W]):
+    __shared__ __attribute__((aligned(16))) uint16_t sUt[kD][kP72];    // U^T, U = T^-1 V
+    __shared__ __attribute__((aligned(16))) uint16_t sUwt[kD][kP72];   // (diag(omega) U)^T
+    __shared__ __attribute__((aligned(16))) uint16_t sWt[kP][kP72];    // W^T, W = T^-1 diag(e^cum) Phi
+    __shared__ __attribute__((aligned(16))) uint16_t sWwt[kP][kP72];   // (diag(omega) W)^T
+    __shared__ __attribute__((aligned(16))) float sCum[kC], sBeta[kC], sEc[kC], sOm[kC];  // cum, beta, e^cum, omega
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -113,20 +138,20 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
         const int64_t ko = b * a.k_sb + hk * a.k_sh + tc * a.k_sl + d0;
         const int64_t vo = b * a.v_sb + hk * a.v_sh + tc * a.v_sl + d0;
         float qv[16], kv[16], vv[16];
+        load16(a.q, qo, a.dt_in, valid, qv);
+        load16(a.k, ko, a.dt_in, valid, kv);
+        load16(a.v, vo, a.dt_in, valid, vv);
         float s1 = 0.f, s2 = 0.f;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            qv[e] = valid ? ld_in(a.q, qo + e, a.dt_in) : 0.f;
-            kv[e] = valid ? ld_in(a.k, ko + e, a.dt_in) : 0.f;
-            vv[e] = valid ? ld_in(a.v, vo + e, a.dt_in) : 0.f;
             const float k2 = kv[e] * kv[e];
             s1 += k2;
             s2 += k2 * k2;
         }
-        s1 += __shfl_xor(s1, 1, kWave);
-        s1 += __shfl_xor(s1, 2, kWave);
-        s2 += __shfl_xor(s2, 1, kWave);
-        s2 += __shfl_xor(s2, 2, kWave);
+        s1 += xor_lane<1>(s1);
+        s1 += xor_lane<2>(s1);
+        s2 += xor_lane<1>(s2);
+        s2 += xor_lane<2>(s2);
         const float r1 = 1.0f / fmaxf(sqrtf(s1), a.feat_eps);
         const float r2 = 0.70710678118654752f / fmaxf(sqrtf(s2), a.feat_eps);
         float ph[16], ph2[16], ps2[16];
@@ -208,10 +233,13 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
     __syncthreads();
 
     // ---- solve T X = [V | diag(e^cum) Phi] (:242-245): thread = one of 192 columns,
-    // forward substitution in fp32 registers.  Row i of N is read as broadcast
-    // 16-byte LDS reads; its offset and the row's result pass through empty asm
-    // statements so that the compiler neither hoists all 504 reads to the top
-    // nor sinks the rows' arithmetic to their last use (either spills).
+    // forward substitution in fp32 registers, each row's sum in four partial
+    // sums (four short dependent chains instead of one long one).  Row i of N
+    // is read as broadcast 16-byte LDS reads; its offset and the row's result
+    // pass through empty asm statements so that the compiler neither hoists
+    // all 504 reads to the top nor sinks the rows' arithmetic to their last
+    // use (either spills).  The column is then stored transposed, 16 bytes at
+    // a time.
     if (tid < kD + kP) {
         const int col = tid;
         const float *nbase = &sN[0][0];
@@ -223,27 +251,29 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
         for (int i = 1; i < kC; ++i) {
             int ro = i * (kC + 4);
             asm volatile("" : "+v"(ro));
-            float acc = x[i];
+            float acc[4] = {x[i], 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < i; j += 4) {
                 const f32x4 n4 = *reinterpret_cast<const f32x4 *>(nbase + ro + j);
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (j + e < i) acc -= n4[e] * x[j + e];
+                    if (j + e < i) acc[e] -= n4[e] * x[j + e];
             }
-            asm volatile("" : "+v"(acc));  // x[i] is final here (no sinking into later rows)
-            x[i] = acc;
+            float r = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            asm volatile("" : "+v"(r));  // x[i] is final here (no sinking into later rows)
+            x[i] = r;
         }
+        uint16_t *dx = col < kD ? &sUt[col][0] : &sWt[col - kD][0];
+        uint16_t *dw = col < kD ? &sUwt[col][0] : &sWwt[col - kD][0];
 #pragma unroll
-        for (int i = 0; i < kC; ++i) {
-            const float om = sOm[i];
-            if (col < kD) {
-                sU[i][col] = f32_to_bf16_bits(x[i]);
-                sUw[i][col] = f32_to_bf16_bits(om * x[i]);
-            } else {
-                sW[i][col - kD] = f32_to_bf16_bits(x[i]);
-                sWw[i][col - kD] = f32_to_bf16_bits(om * x[i]);
-            }
+        for (int i0 = 0; i0 < kC; i0 += 8) {
+            const f32x4 o0 = *reinterpret_cast<const f32x4 *>(&sOm[i0]);
+            const f32x4 o1 = *reinterpret_cast<const f32x4 *>(&sOm[i0 + 4]);
+            *reinterpret_cast<u32x4 *>(dx + i0) = u32x4{pack2(x[i0], x[i0 + 1]), pack2(x[i0 + 2], x[i0 + 3]),
+                                                        pack2(x[i0 + 4], x[i0 + 5]), pack2(x[i0 + 6], x[i0 + 7])};
+            *reinterpret_cast<u32x4 *>(dw + i0) =
+                u32x4{pack2(o0[0] * x[i0], o0[1] * x[i0 + 1]), pack2(o0[2] * x[i0 + 2], o0[3] * x[i0 + 3]),
+                      pack2(o1[0] * x[i0 + 4], o1[1] * x[i0 + 5]), pack2(o1[2] * x[i0 + 6], o1[3] * x[i0 + 7])};
         }
     }
     __syncthreads();
@@ -258,7 +288,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             if (kt == 1 && tb < 2) continue;  // A is lower triangular
-            const bf16x8 ua = tr8(&sU[32 * kt + 4 * g + tr_r][16 * w + tr_c], kP80);
+            const bf16x8 ua = row8p(&sUt[16 * w + c16][0], 32 * kt + 4 * g);
             const bf16x8 ab = row8p(&sA[16 * tb + c16][0], 32 * kt + 4 * g);
             acc = mfma(ua, ab, acc);
         }
@@ -277,7 +307,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
                 if (kt == 1 && tb < 2) continue;
-                const bf16x8 wa = tr8(&sW[32 * kt + 4 * g + tr_r][16 * eb + tr_c], kP144);
+                const bf16x8 wa = row8p(&sWt[16 * eb + c16][0], 32 * kt + 4 * g);
                 const bf16x8 ab = row8p(&sA[i][0], 32 * kt + 4 * g);
                 acc = mfma(wa, ab, acc);
             }
@@ -297,7 +327,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
                 const bf16x8 pa = tr8(&sPhi[32 * kt + 4 * g + tr_r][16 * eb + tr_c], kP136);
-                const bf16x8 ub = tr8(&sUw[32 * kt + 4 * g + tr_r][16 * dw + tr_c], kP80);
+                const bf16x8 ub = row8p(&sUwt[16 * dw + c16][0], 32 * kt + 4 * g);
                 acc = mfma(pa, ub, acc);
             }
             *reinterpret_cast<uint2 *>(rec + kRecR0 + ((eb * 4 + dw) * 64 + lane) * 8) = pack4(acc);
@@ -314,7 +344,7 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
-                const bf16x8 wa = tr8(&sWw[32 * kt + 4 * g + tr_r][16 * eb + tr_c], kP144);
+                const bf16x8 wa = row8p(&sWwt[16 * eb + c16][0], 32 * kt + 4 * g);
                 const bf16x8 pb = tr8(&sPhi[32 * kt + 4 * g + tr_r][16 * ebp + tr_c], kP136);
                 acc = mfma(wa, pb, acc);
             }

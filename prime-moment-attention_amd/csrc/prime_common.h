@@ -46,9 +46,53 @@ __device__ __forceinline__ void store_elem(void *p, int64_t idx, int dt, float x
     else static_cast<float *>(p)[idx] = x;
 }
 
+// x of lane (lane ^ M), M = 8, 4, 2 or 1 (the partner within the lane's row of
+// 16), by DPP moves on the VALU instead of a shuffle through the LDS unit.
+// M = 8 and 4 combine row_shl:M (lanes whose partner is above) and row_shr:M
+// (below) through bank masks (banks are groups of 4 lanes); M = 2 and 1 are
+// quad permutations.
+template <int M>
+__device__ __forceinline__ float xor_lane(float x) {
+    const int v = __float_as_int(x);
+    if constexpr (M == 8) {
+        int t = __builtin_amdgcn_update_dpp(0, v, 0x108, 0xF, 0x3, false);  // row_shl:8, lanes 0-7
+        t = __builtin_amdgcn_update_dpp(t, v, 0x118, 0xF, 0xC, false);      // row_shr:8, lanes 8-15
+        return __int_as_float(t);
+    } else if constexpr (M == 4) {
+        int t = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0x5, false);  // row_shl:4, lanes 0-3 / 8-11
+        t = __builtin_amdgcn_update_dpp(t, v, 0x114, 0xF, 0xA, false);      // row_shr:4, lanes 4-7 / 12-15
+        return __int_as_float(t);
+    } else if constexpr (M == 2) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+    } else {
+        static_assert(M == 1, "partners at 8, 4, 2, 1");
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+    }
+}
+
+// x + x of lane (lane ^ 16), or (lane ^ 32), on the VALU: a v_permlane16_swap /
+// v_permlane32_swap of x with itself leaves, in every lane, its own x in one
+// result and its partner's in the other, so their sum is the pair's sum.
+__device__ __forceinline__ float sum_lane16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_lane32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over the 64 lanes, in every lane: the butterfly x + x(lane ^ o) for
+// o = 32, 16, 8, 4, 2, 1 (the order of a shuffle-based butterfly, so the
+// result is the same), all on the VALU (permlane swaps and DPP) rather than
+// through the LDS unit.
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o, kWave);
+    x = sum_lane32(x);
+    x = sum_lane16(x);
+    x += xor_lane<8>(x);
+    x += xor_lane<4>(x);
+    x += xor_lane<2>(x);
+    x += xor_lane<1>(x);
     return x;
 }
 
