@@ -422,22 +422,59 @@ __device__ __forceinline__ void store_y4(uint8_t *p, f32x4 v) {
     }
 }
 
-// y^T tiles (value blocks DV0, DV0+1; this wave's token block) = Y0^T + sc S~ Z^T
-// (DV0 a template constant: a runtime index would put the packs in scratch memory)
+// y of one chunk is staged in LDS, [64 tokens][64 values] of the output dtype
+// with rows padded by 16 bytes (16-byte aligned rows whose starts move four
+// banks per row, so the tile writes of 16 rows meet no bank twice), and
+// written to global memory in the next chunk as whole 16-byte row segments.
+// Direct stores of the accumulator tiles (8 bytes per lane over 16 rows)
+// were the scan's largest cost.
+template <int DTY>
+struct YStage {
+    static constexpr int es = DTY == PRIME_F32 ? 4 : 2;
+    static constexpr int pitch = kD * es + 16;  // bytes per token row
+    static constexpr int bytes = kC * pitch;    // one chunk
+};
+
+// y^T tiles (value blocks DV0, DV0+1; this wave's token block) = Y0^T + sc S~ Z^T,
+// into the chunk's LDS stage (DV0 a template constant: a runtime index would
+// put the packs in scratch memory)
 template <int DTY, int DV0>
-__device__ __forceinline__ void y_tiles(const bf16x8 (&pk)[4][4], const RecW &cur, float sc, bool tok_ok,
-                                        uint8_t *yrow, int g) {
-    constexpr int es = DTY == PRIME_F32 ? 4 : 2;
+__device__ __forceinline__ void y_tiles(const bf16x8 (&pk)[4][4], const RecW &cur, float sc, uint8_t *ystage,
+                                        int tb, int g, int c16) {
+    using YS = YStage<DTY>;
+    f32x4 p[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) p[j] = mfma(pk[DV0 + j][ks], cur.zb[ks], p[j]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        f32x4 p = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) p = mfma(pk[DV0 + j][ks], cur.zb[ks], p);
         const f32x4 y0 = unpack4(cur.y0[j]);
         f32x4 yv;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) yv[r] = y0[r] + sc * p[r];
-        if (tok_ok) store_y4<DTY>(yrow + (16 * (DV0 + j) + 4 * g) * es, yv);
+        for (int r = 0; r < 4; ++r) yv[r] = y0[r] + sc * p[j][r];
+        store_y4<DTY>(ystage + (16 * tb + c16) * YS::pitch + (16 * (DV0 + j) + 4 * g) * YS::es, yv);
+    }
+}
+
+// Write a staged chunk of y (LDS) to global memory: thread t takes 16-byte
+// segments t, t + 512, ... of the chunk's rows.  GUARD skips tokens at or past
+// L; only the call's last chunk can hold such tokens, and only the write after
+// the loop can reach it, so the writes inside the loop carry no condition (a
+// conditional store would leave the compiler to count outstanding memory
+// operations for both paths, and its conservative count would then wait for
+// the store at the next record wait).
+template <int DTY, bool GUARD>
+__device__ __forceinline__ void y_write(const DeltaArgs &a, int c, const uint8_t *ystage, uint8_t *ychunk,
+                                        int64_t yrow_bytes, int tid) {
+    using YS = YStage<DTY>;
+    constexpr int segs = kD * YS::es / 16;  // 16-byte segments per row
+#pragma unroll
+    for (int i = tid; i < kC * segs; i += kScanWaves * kWave) {
+        const int row = i / segs, sg = i - row * segs;
+        if (!GUARD || c * kC + row < a.L)
+            *reinterpret_cast<u32x4 *>(ychunk + row * yrow_bytes + 16 * sg) =
+                *reinterpret_cast<const u32x4 *>(ystage + row * YS::pitch + 16 * sg);
     }
 }
 
@@ -445,24 +482,29 @@ __device__ __forceinline__ void y_tiles(const bf16x8 (&pk)[4][4], const RecW &cu
 // receives the next chunk's.  Called with the two register sets swapped on
 // alternate chunks, so that no copy (and no wait for the loads) is needed.
 // `yrow`: this lane's y row (token 16 (w/2) + l%16 of the chunk).
-template <int DTY>
+template <int DTY, bool WRITE_PREV>
 __device__ __forceinline__ void scan_chunk(const DeltaArgs &a, int cw, int w, int lane, int g, int c16,
                                            __amdgpu_buffer_rsrc_t rs, f32x4 (&st)[4], float &sc, const RecW &cur,
                                            RecW &nxt, bf16x8 (*sPk)[4][4][64], float (*sRed)[kScanWaves],
-                                           uint8_t *yrow) {
+                                           uint8_t *sY, uint8_t *ychunk, int64_t yrow_bytes) {
     const int buf = cw & 1;
     const int tb = w >> 1;
     // next chunk's share (clamped to the window: the duplicate is unused)
     load_recw(nxt, rs, min(cw + 1, a.nw - 1) * static_cast<int>(kDeltaRecBytes), w, lane);
+    // the previous chunk's y, staged before the last barrier (stores issued
+    // after the loads above, so that waiting for those never waits for them)
+    if constexpr (WRITE_PREV)
+        y_write<DTY, false>(a, a.c0 + cw - 1, sY + (buf ^ 1) * YStage<DTY>::bytes, ychunk - kC * yrow_bytes,
+                            yrow_bytes, threadIdx.x);
     bf16x8 pk[4][4];
 #pragma unroll
     for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) pk[dv][ks] = sPk[buf][dv][ks][lane];
-    // ---- y^T (value blocks 2(w&1), 2(w&1)+1; token block tb)
-    const bool tok_ok = (a.c0 + cw) * kC + 16 * tb + c16 < a.L;
-    if (w & 1) y_tiles<DTY, 2>(pk, cur, sc, tok_ok, yrow, g);
-    else y_tiles<DTY, 0>(pk, cur, sc, tok_ok, yrow, g);
+    // ---- y^T (value blocks 2(w&1), 2(w&1)+1; token block tb), into this chunk's stage
+    uint8_t *ys = sY + buf * YStage<DTY>::bytes;
+    if (w & 1) y_tiles<DTY, 2>(pk, cur, sc, ys, tb, g, c16);
+    else y_tiles<DTY, 0>(pk, cur, sc, ys, tb, g, c16);
     // ---- S~'^T = sc (e^cum_63 S~^T - M^T S~^T) + R0^T on feature block w
     float ss = 0.f;
 #pragma unroll
@@ -502,6 +544,7 @@ __device__ __forceinline__ void scan_chunk(const DeltaArgs &a, int cw, int w, in
 template <int DTY>
 __global__ __launch_bounds__(kScanWaves * kWave, 1) void delta_scan_kernel(const DeltaArgs a) {
     __shared__ __attribute__((aligned(16))) bf16x8 sPk[2][4][4][64];  // [buf][dv][ks][lane]
+    __shared__ __attribute__((aligned(16))) uint8_t sY[2 * YStage<DTY>::bytes];  // y of two chunks
     __shared__ float sRed[2][kScanWaves];
 
     const int tid = threadIdx.x;
@@ -531,18 +574,30 @@ __global__ __launch_bounds__(kScanWaves * kWave, 1) void delta_scan_kernel(const
     load_recw(ra, rs, 0, w, lane);
     __syncthreads();
 
-    // this lane's y row in the window's first chunk, advanced by one chunk per step
-    constexpr int es = DTY == PRIME_F32 ? 4 : 2;
-    uint8_t *yrow = static_cast<uint8_t *>(a.y) +
-                    (b * a.y_sb + h * a.y_sh + static_cast<int64_t>(a.c0 * kC + 16 * (w >> 1) + c16) * a.y_sl) * es;
-    const int64_t ystep = static_cast<int64_t>(kC) * a.y_sl * es;
-    int cw = 0;
+    // the y rows of the window's first chunk, advanced by one chunk per step
+    constexpr int es = YStage<DTY>::es;
+    const int64_t yrow_bytes = a.y_sl * es;
+    uint8_t *ychunk = static_cast<uint8_t *>(a.y) +
+                      (b * a.y_sb + h * a.y_sh + static_cast<int64_t>(a.c0) * kC * a.y_sl) * es;
+    const int64_t ystep = kC * yrow_bytes;
+    // chunk 0 (no earlier y to write), then pairs of chunks writing the y of
+    // the chunk before each
+    scan_chunk<DTY, false>(a, 0, w, lane, g, c16, rs, st, sc, ra, rb, sPk, sRed, sY, ychunk, yrow_bytes);
+    ychunk += ystep;
+    int cw = 1;
     for (; cw + 1 < a.nw; cw += 2) {
-        scan_chunk<DTY>(a, cw, w, lane, g, c16, rs, st, sc, ra, rb, sPk, sRed, yrow);
-        scan_chunk<DTY>(a, cw + 1, w, lane, g, c16, rs, st, sc, rb, ra, sPk, sRed, yrow + ystep);
-        yrow += 2 * ystep;
+        scan_chunk<DTY, true>(a, cw, w, lane, g, c16, rs, st, sc, rb, ra, sPk, sRed, sY, ychunk, yrow_bytes);
+        scan_chunk<DTY, true>(a, cw + 1, w, lane, g, c16, rs, st, sc, ra, rb, sPk, sRed, sY, ychunk + ystep,
+                              yrow_bytes);
+        ychunk += 2 * ystep;
     }
-    if (cw < a.nw) scan_chunk<DTY>(a, cw, w, lane, g, c16, rs, st, sc, ra, rb, sPk, sRed, yrow);
+    if (cw < a.nw) {
+        scan_chunk<DTY, true>(a, cw, w, lane, g, c16, rs, st, sc, rb, ra, sPk, sRed, sY, ychunk, yrow_bytes);
+        ychunk += ystep;
+    }
+    // the last chunk's y (staged before the last barrier)
+    y_write<DTY, true>(a, a.c0 + a.nw - 1, sY + ((a.nw - 1) & 1) * YStage<DTY>::bytes, ychunk - ystep, yrow_bytes,
+                       tid);
 
     // ---- state leaving the window (the pending scale applied)
     float *dst = a.last ? a.state_out : a.ws_state;
