@@ -404,8 +404,26 @@ def bench_model_selective(args, torch, dev):
 
 def read_gpu_clock():
     """The graphics clock(s) of the visible GPU in MHz, from amd-smi (or
-    rocm-smi); an error string when neither answers."""
+    rocm-smi); an error string when neither answers.  Under a profiler no tool
+    is spawned (their launch scripts re-exec an interpreter, which the
+    profiler's preloaded library sees as a program replacing itself): the
+    starred levels of the driver's sysfs ``pp_dpm_sclk`` tables are read
+    instead, for every card the host shows."""
+    import glob
     import subprocess
+    if "rocprof" in os.environ.get("LD_PRELOAD", "") or any(k.startswith("ROCPROF") for k in os.environ):
+        levels = {}
+        for f in sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")):
+            try:
+                lines = [ln for ln in open(f).read().splitlines() if ":" in ln]
+            except OSError:
+                continue
+            mhz = [int("".join(ch for ch in ln.split(":")[1] if ch.isdigit()) or 0) for ln in lines]
+            cur = [m for m, ln in zip(mhz, lines) if ln.rstrip().endswith("*")]
+            if mhz:
+                levels[f.split("/")[4]] = {"cur_mhz": cur[0] if cur else None, "max_mhz": max(mhz)}
+        return {"tool": "sysfs pp_dpm_sclk", "cards": levels} if levels else {"error": "not read under a profiler"}
+    err = "no clock source"
     for cmd in (["amd-smi", "metric", "--clock", "--json"], ["rocm-smi", "--showclocks", "--json"]):
         try:
             r = subprocess.run(cmd, capture_output=True, text=True, timeout=20)
