@@ -51,6 +51,10 @@ extern "C" {
                                      (attention.py:177,185) instead of the
                                      recurrence's max(den, eps) */
 
+/* flag for prime_delta_prefill_workspace_size: size the workspace for F32
+   q/k/v (the fp32 path's per-chunk records are twice the bf16 path's) */
+#define PRIME_FLAG_F32_INPUTS 2u
+
 /* A strided [B, H, L, D] view (decode calls ignore stride_l). */
 typedef struct prime_tensor {
     void   *data;
@@ -174,7 +178,10 @@ size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags)
  *   q, k, v   : [B, H(q) / H_kv, L, D] after the module's projections, QK-norm
  *               and q * 1/sqrt(D) (:107-126); the kernels form psi = [q, q*q/sqrt2]
  *               and phi = [k/max(|k|,feat_eps), (k*k)/max(|k*k|,feat_eps)/sqrt2]
- *               (:73-87).  BF16 or F32 (all three alike).
+ *               (:73-87).  BF16 or F32 (all three alike).  BF16 inputs run
+ *               on bf16 MFMA operands (fp32 accumulation, fp32 state); F32
+ *               inputs take an fp32 path (fp32 MFMA operands and records), as
+ *               the reference computes in fp32 (:123-127).
  *   beta      : fp32 [B, H, L] contiguous, 0.5 mean sigmoid(write) (:134)
  *   alpha     : fp32 [B, H, L] contiguous, decay (1 - 0.5 mean sigmoid(erase)) (:137)
  *   decay_pad : alpha of the zero tokens padding the last chunk (:189, the
@@ -185,9 +192,10 @@ size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags)
  *   state_in  : fp32 [B, H, D, 2D] or NULL (zero); state_out likewise or NULL;
  *               they may be the same buffer
  *   y         : [B, H, L, D], F32 / BF16 / F16
- *   workspace : at least prime_delta_prefill_workspace_size(B, H, L, 0) bytes
- *               (16-byte aligned).  A smaller workspace (at least
- *               prime_delta_prefill_workspace_size(B, H, 64, 0)) makes the call
+ *   workspace : at least prime_delta_prefill_workspace_size(B, H, L, f) bytes
+ *               (16-byte aligned; f = PRIME_FLAG_F32_INPUTS for F32 inputs,
+ *               else 0).  A smaller workspace (at least
+ *               prime_delta_prefill_workspace_size(B, H, 64, f)) makes the call
  *               process the sequence in more, shorter windows; results agree.
  * When the workspace holds fewer chunks than the sequence, the per-chunk
  * solve of the next window runs on a side stream while the current window is
@@ -205,7 +213,8 @@ int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k,
                         const prime_tensor_t *y, float *state_out, void *workspace,
                         size_t workspace_bytes, void *stream);
 
-/* Workspace bytes of prime_delta_prefill for this shape (flags: 0). */
+/* Workspace bytes of prime_delta_prefill for this shape (flags: 0 for BF16
+   inputs, PRIME_FLAG_F32_INPUTS for F32 inputs). */
 size_t prime_delta_prefill_workspace_size(int B, int H, int L, unsigned flags);
 
 /*

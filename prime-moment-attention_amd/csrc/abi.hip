@@ -668,12 +668,12 @@ int prime_selective_decode_step(const prime_tensor_t *q, const prime_tensor_t *k
 }
 
 size_t prime_delta_prefill_workspace_size(int B, int H, int L, unsigned flags) {
-    (void)flags;
     if (B <= 0 || H <= 0 || L <= 0) return 0;
     const int NC = (L + prime::kDeltaChunk - 1) / prime::kDeltaChunk;
     const int win = NC < prime::kDeltaDefaultWindow ? NC : prime::kDeltaDefaultWindow;
     const size_t S = static_cast<size_t>(B) * H;
-    return S * prime::kDeltaStateBytes + S * static_cast<size_t>(win) * prime::kDeltaRecBytes;
+    const size_t rec = prime::delta_rec_bytes((flags & PRIME_FLAG_F32_INPUTS) ? PRIME_F32 : PRIME_BF16);
+    return S * prime::kDeltaStateBytes + S * static_cast<size_t>(win) * rec;
 }
 
 int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
@@ -701,11 +701,13 @@ int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const 
     const size_t sbytes = S * prime::kDeltaStateBytes;
     if (state_in && state_out && state_in != state_out && overlap(state_in, sbytes, state_out, sbytes))
         return fail(PRIME_ERR_ALIAS, "state_out overlaps state_in (only a fully in-place state is allowed)");
-    if (workspace_bytes < sbytes + S * prime::kDeltaRecBytes)
-        return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes is below the minimum %zu", workspace_bytes,
-                    sbytes + S * prime::kDeltaRecBytes);
+    const size_t rec = prime::delta_rec_bytes(q->dtype);
+    if (workspace_bytes < sbytes + S * rec)
+        return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes is below the minimum %zu for %s inputs%s",
+                    workspace_bytes, sbytes + S * rec, q->dtype == PRIME_F32 ? "F32" : "BF16",
+                    q->dtype == PRIME_F32 ? " (size it with PRIME_FLAG_F32_INPUTS)" : "");
     const int NC = (L + prime::kDeltaChunk - 1) / prime::kDeltaChunk;
-    const size_t cap_sz = (workspace_bytes - sbytes) / (S * prime::kDeltaRecBytes);
+    const size_t cap_sz = (workspace_bytes - sbytes) / (S * rec);
     const int cap = static_cast<int>(cap_sz < static_cast<size_t>(NC) ? cap_sz : static_cast<size_t>(NC) + 1);
 
     prime::DeltaArgs a{};

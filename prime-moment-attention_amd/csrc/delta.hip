@@ -722,12 +722,14 @@ SideStream *side_stream(hipStream_t caller, bool may_create) {
 }
 
 void launch_prep(const DeltaArgs &a, hipStream_t s) {
+    if (a.dt_in == PRIME_F32) return launch_delta_prep_f32(a, s);
     const TimerEvents t = timer_events(PRIME_KERNEL_DELTA_PREP);
     hipExtLaunchKernelGGL(delta_prep_kernel, dim3(a.B * a.H * a.nw), dim3(256), 0, s, t.start, t.stop, 0, a);
     if (hipPeekAtLastError() != hipSuccess) timer_drop(t);
 }
 
 void launch_scan(const DeltaArgs &a, hipStream_t s) {
+    if (a.dt_in == PRIME_F32) return launch_delta_scan_f32(a, s);
     const TimerEvents t = timer_events(PRIME_KERNEL_DELTA_SCAN);
     const dim3 grid(a.B * a.H), block(kScanWaves * kWave);
     if (a.dt_y == PRIME_BF16)
@@ -774,7 +776,7 @@ hipError_t launch_delta_prefill(DeltaArgs a, int NC, int cap, hipStream_t stream
     }
     std::lock_guard<std::mutex> lk(ss->mu);
     const int half = cap / 2;
-    const size_t half_bytes = static_cast<size_t>(a.B) * a.H * half * kDeltaRecBytes;
+    const size_t half_bytes = static_cast<size_t>(a.B) * a.H * half * delta_rec_bytes(a.dt_in);
     const int nwin = (NC + half - 1) / half;
     hipError_t e;
     if ((e = hipEventRecord(ss->start, stream)) != hipSuccess) return e;

@@ -195,13 +195,20 @@ struct DeltaStepArgs {
 
 constexpr int kDeltaChunk = 64;
 constexpr size_t kDeltaStateBytes = static_cast<size_t>(kD) * 2 * kD * sizeof(float);  // one (b,h) state
-constexpr size_t kDeltaRecBytes = 73984;         // per-chunk transfer record (multiple of 256)
+constexpr size_t kDeltaRecBytes = 73984;         // per-chunk transfer record, bf16 inputs (multiple of 256)
+constexpr size_t kDeltaRecBytesF32 = 147712;     // per-chunk transfer record, fp32 inputs (fp32 operands)
 constexpr int kDeltaDefaultWindow = 128;         // record chunks of the recommended workspace
+
+// Record bytes per chunk for inputs of dtype `dt_in`.
+inline size_t delta_rec_bytes(int dt_in) { return dt_in == PRIME_F32 ? kDeltaRecBytesF32 : kDeltaRecBytes; }
 
 // Launch the delta prefill over every window (prep + scan per window); cap =
 // chunks of record space per (sequence, head) in the workspace.
 hipError_t launch_delta_prefill(DeltaArgs a, int NC, int cap, hipStream_t stream);
 hipError_t launch_delta_step(const DeltaStepArgs &a, hipStream_t stream);
+// fp32-input prep and scan kernels of one window (delta_f32.hip)
+void launch_delta_prep_f32(const DeltaArgs &a, hipStream_t s);
+void launch_delta_scan_f32(const DeltaArgs &a, hipStream_t s);
 
 // Launch timer (the C-ABI prime_timer_* calls).  timer_events(kernel) hands
 // out the event pair for one launch of `kernel` while that kernel is being

@@ -646,8 +646,14 @@ def _gate(t, B, H, L, name):
     _dev_check(t)
 
 
-def delta_workspace_size(B: int, H: int, L: int) -> int:
-    return int(load().prime_delta_prefill_workspace_size(B, H, L, 0))
+PRIME_FLAG_F32_INPUTS = 2
+
+
+def delta_workspace_size(B: int, H: int, L: int, dtype=None) -> int:
+    """Workspace bytes of prime_delta_prefill; fp32 inputs (``dtype`` torch.float32)
+    need records twice the size of bf16 inputs'."""
+    flags = PRIME_FLAG_F32_INPUTS if dtype == torch.float32 else 0
+    return int(load().prime_delta_prefill_workspace_size(B, H, L, flags))
 
 
 def delta_prefill(q, k, v, beta, alpha, decay_pad: float, feat_eps: float, bound: float, state_in, y,
@@ -667,7 +673,7 @@ def delta_prefill(q, k, v, beta, alpha, decay_pad: float, feat_eps: float, bound
     _check_delta_state(state_in, B, H, D, "state_in")
     _check_delta_state(state_out, B, H, D, "state_out")
     if workspace is None:
-        workspace = torch.empty(delta_workspace_size(B, H, Lq), dtype=torch.uint8, device=q.device)
+        workspace = torch.empty(delta_workspace_size(B, H, Lq, q.dtype), dtype=torch.uint8, device=q.device)
     _dev_check(workspace)
     qd, kd, vd, yd = tensor_desc(q, True), tensor_desc(k, True), tensor_desc(v, True), tensor_desc(y, True)
     ptr = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None

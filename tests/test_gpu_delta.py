@@ -9,7 +9,7 @@ import torch
 from oracle import oracle as O
 from prime_moment_attention import _lib
 
-from gpu_util import TOL_BF16, assert_close, dev, to_dev, to_np
+from gpu_util import TOL_BF16, TOL_F32, assert_close, dev, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -103,13 +103,68 @@ def test_delta_prefill_windows_agree(with_state, ws_chunks):
     assert_close(s2, s1, 1e-5, "S")
 
 
-def test_delta_prefill_f32_inputs():
-    B, H, L = 1, 2, 130
-    q, k, v, beta, alpha = _inputs(B, H, L, seed=64, bf16=False)
+@pytest.mark.parametrize("L", [1, 64, 130, 700])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_delta_prefill_f32_inputs(L, with_state):
+    """fp32 inputs take the fp32 path (fp32 MFMA operands and records): the
+    fp32 tolerance applies."""
+    B, H = 2, 3
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=64 + L, bf16=False)
+    st = np.random.default_rng(65).standard_normal((B * H, D, 2 * D)) * 0.05 if with_state else None
+    yo, so = _oracle(q, k, v, beta, alpha, 0.995, 25.0, st)
+    y, s = _run(q, k, v, beta, alpha, 0.995, 25.0, st, dt=torch.float32)
+    assert_close(y, yo, TOL_F32, "y")
+    assert_close(s, so, TOL_F32, "S")
+
+
+def test_delta_prefill_f32_clamp_active_and_gqa():
+    B, H, L = 1, 4, 300
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=66, Hkv=2, beta_scale=1.0, bf16=False)
+    yo, so = _oracle(q, k, v, beta, alpha, 0.99, 0.5)
+    nrm = np.sqrt((so ** 2).sum(axis=(1, 2)))
+    assert np.all(nrm <= 0.5 + 1e-6) and np.all(nrm > 0.49)
+    y, s = _run(q, k, v, beta, alpha, 0.99, 0.5, dt=torch.float32)
+    assert_close(y, yo, TOL_F32, "y")
+    assert_close(s, so, TOL_F32, "S")
+
+
+def test_delta_prefill_f32_long_sequence_and_bf16_output():
+    """64 chunks of fp32 inputs, y written as bf16 (the state stays fp32)."""
+    B, H, L = 1, 2, 4096
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=67, beta_scale=1.0, bf16=False)
     yo, so = _oracle(q, k, v, beta, alpha, 0.995, 25.0)
-    y, s = _run(q, k, v, beta, alpha, 0.995, 25.0, dt=torch.float32)
-    assert_close(y, yo, TOL_BF16, "y")  # bf16 MFMA inside: the bf16 tolerance applies
-    assert_close(s, so, TOL_BF16, "S")
+    y = torch.empty(B, H, L, D, device=dev(), dtype=torch.bfloat16)
+    s = torch.empty(B, H, D, 2 * D, device=dev())
+    _lib.delta_prefill(to_dev(q), to_dev(k), to_dev(v), to_dev(beta), to_dev(alpha), 0.995, FEAT_EPS, 25.0,
+                       None, y, s)
+    torch.cuda.synchronize()
+    assert_close(to_np(s).reshape(B * H, D, 2 * D), so, TOL_F32, "S")
+    assert_close(to_np(y).reshape(B * H, L, D), yo, 4e-3, "y (bf16 output)")
+
+
+@pytest.mark.parametrize("ws_chunks", [1, 4])
+def test_delta_prefill_f32_windows_agree(ws_chunks):
+    """fp32 records in workspaces of one and four chunks (the latter double
+    buffered on the side stream) give the one-window result."""
+    B, H, L = 1, 2, 64 * 5 + 17
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=68, bf16=False)
+    st = np.random.default_rng(69).standard_normal((B * H, D, 2 * D)) * 0.05
+    y1, s1 = _run(q, k, v, beta, alpha, 0.995, 25.0, st, dt=torch.float32)
+    small = torch.empty(_lib.delta_workspace_size(B, H, 64 * ws_chunks, torch.float32), dtype=torch.uint8,
+                        device=dev())
+    y2, s2 = _run(q, k, v, beta, alpha, 0.995, 25.0, st, dt=torch.float32, workspace=small, inplace=True)
+    assert_close(y2, y1, 1e-6, "y")
+    assert_close(s2, s1, 1e-6, "S")
+
+
+def test_delta_prefill_f32_rejects_bf16_sized_workspace():
+    """A workspace sized for one bf16 chunk holds no fp32 record: the call fails
+    with an error naming the flag, before any launch."""
+    B, H, L = 1, 2, 64
+    q, k, v, beta, alpha = _inputs(B, H, L, seed=70, bf16=False)
+    ws = torch.empty(_lib.delta_workspace_size(B, H, 64), dtype=torch.uint8, device=dev())
+    with pytest.raises(RuntimeError, match="PRIME_FLAG_F32_INPUTS"):
+        _run(q, k, v, beta, alpha, 0.995, 25.0, dt=torch.float32, workspace=ws)
 
 
 def test_delta_prefill_long_sequence_subset():
