@@ -272,8 +272,11 @@ int prime_linear(const void *x, const void *w, void *y, int M, int N, int K, int
  * unlike the base form's.  q arrives pre-scaled by 1/sqrt(D) as for the base
  * form (selective.py:362).
  *
- * prime_selective_prefill: L tokens of BF16 q/k/v [B, H(kv), L, 64] (strided
- * as prime_chunked_prefill), log_decay fp32 [B, H, L] contiguous = log l_t
+ * prime_selective_prefill: L tokens of q/k/v [B, H(kv), L, 64] (strided as
+ * prime_chunked_prefill), BF16 (bf16 MFMA operands, fp32 accumulation and
+ * state) or F32 (an fp32 kernel: fp32 MFMA operands throughout, one workgroup
+ * per sequence; the reference computes in fp32, selective.py:363-365);
+ * prime_selective_prefill_qknorm takes BF16 only.  log_decay fp32 [B, H, L] contiguous = log l_t
  * (natural log, <= 0), k_scale fp32 [H] = beta_h; state_in may be NULL (zero);
  * same y, state_out, workspace rules as prime_chunked_prefill (whose
  * workspace size applies).  Replaces the parallel branch (selective.py:

@@ -277,8 +277,6 @@ static int prefill_impl(const prime_tensor_t *q, const prime_tensor_t *k, const 
     if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !(decay || selective) ||
         (selective && !k_scale))
         return fail(PRIME_ERR_INVALID_ARG, "prefill: null argument");
-    if (selective && q->dtype != PRIME_BF16)
-        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "the selective prefill takes BF16 q/k/v");
     if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0 || chunk <= 0)
         return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d chunk=%d", B, H, H_kv, L, chunk);

@@ -749,6 +749,8 @@ static hipError_t launch_variant(PrefillArgs a, hipStream_t stream) {
 }
 
 hipError_t launch_prefill(PrefillArgs a, hipStream_t stream) {
+    if (a.log_decay != nullptr && a.dt_in == PRIME_F32 && !a.accumulate && !a.states_only)
+        return launch_selective_f32(a, stream);
     return a.dt_in == PRIME_F32 ? launch_variant<true>(a, stream) : launch_variant<false>(a, stream);
 }
 

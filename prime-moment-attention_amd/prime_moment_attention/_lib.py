@@ -458,10 +458,11 @@ def _sel_vec(t: torch.Tensor, n: int, name: str) -> None:
 def selective_prefill(q, k, v, log_decay: torch.Tensor, k_scale: torch.Tensor, eps: float, state_in, y,
                       state_out, workspace: Optional[torch.Tensor] = None,
                       qk_norm: Optional[PrimeQkNorm] = None) -> None:
-    """Selective PRIME prefill (prime_selective_prefill): bf16 q [B,H,L,D],
-    k/v [B,Hkv,L,D]; log_decay fp32 [B,H,L] (log lambda_t, contiguous);
-    k_scale fp32 [H] (beta); states in the selective convention.  qk_norm: as
-    for chunked_prefill (prime_selective_prefill_qknorm)."""
+    """Selective PRIME prefill (prime_selective_prefill): q [B,H,L,D], k/v
+    [B,Hkv,L,D], bf16 (bf16 MFMA operands) or fp32 (an fp32 kernel); log_decay
+    fp32 [B,H,L] (log lambda_t, contiguous); k_scale fp32 [H] (beta); states in
+    the selective convention.  qk_norm (bf16 only): as for chunked_prefill
+    (prime_selective_prefill_qknorm)."""
     B, H, Lq, D = q.shape
     _sel_vec(log_decay, B * H * Lq, "log_decay")
     _sel_vec(k_scale, H, "k_scale")

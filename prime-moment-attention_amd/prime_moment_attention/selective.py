@@ -17,8 +17,9 @@ LayerNorm and 1/sqrt(D) inside the kernel); L > 1 runs prime_selective_prefill
 in place of the parallel branch's [L, L] decay matrix (selective.py:414-440).
 As in the reference, the parallel branch starts from a zero state: an incoming
 ``state`` is used by the L == 1 step only, and the returned state of an L > 1
-call covers that call's tokens.  The prefill kernel takes bf16 q/k/v; fp32
-activations are rounded to bf16 for it (results within the bf16 tolerance).
+call covers that call's tokens.  bf16 projections run the bf16-MFMA prefill;
+fp32 projections (fp16 ones are widened to fp32) run the fp32 prefill kernel,
+as the reference computes this branch in fp32 (selective.py:363-365).
 """
 from __future__ import annotations
 
@@ -111,8 +112,8 @@ class PrimeSelectiveMomentAttention(nn.Module):
             y = y.unsqueeze(2)
             next_state = st_out
         else:
-            if q.dtype != torch.bfloat16:
-                q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
+            if q.dtype not in (torch.bfloat16, torch.float32):
+                q, k, v = q.float(), k.float(), v.float()
             # the QK LayerNorm and scale as the kernels load q and k (or first,
             # in place, where the parameters do not allow that)
             norm = _lib.qk_norm_on_load(self.q_norm if self.use_qk_norm else None,

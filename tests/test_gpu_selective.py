@@ -11,17 +11,17 @@ from oracle import oracle as O
 from prime_moment_attention import (GreedyDecoder, PrimeConfig, PrimeForCausalLM,
                                     PrimeSelectiveMomentAttention, _lib)
 
-from gpu_util import TOL_BF16, assert_close, dev, state_to_dev, state_to_np, to_dev, to_np
+from gpu_util import TOL_BF16, TOL_F32, assert_close, dev, state_to_dev, state_to_np, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
 D = 64
 
 
-def _inputs(B, H, L, seed, Hkv=None):
+def _inputs(B, H, L, seed, Hkv=None, bf16=True):
     Hkv = Hkv or H
-    q, _, _ = O.make_inputs((B, H, L, D), seed=seed)
-    _, k, v = O.make_inputs((B, Hkv, L, D), seed=seed + 1)
+    q, _, _ = O.make_inputs((B, H, L, D), seed=seed, bf16=bf16)
+    _, k, v = O.make_inputs((B, Hkv, L, D), seed=seed + 1, bf16=bf16)
     rng = np.random.default_rng(seed)
     delta = np.log1p(np.exp(rng.standard_normal((B, H, L)) - 1.0))  # softplus step sizes
     tau = rng.uniform(8.0, 400.0, H)
@@ -47,12 +47,12 @@ def _rand_state(BH, seed):
             rng.standard_normal((BH, D)) * 0.1, np.abs(rng.standard_normal((BH, D))) * 0.1)
 
 
-def _run_prefill(q, k, v, log_decay, beta, eps, state=None, workspace=None):
+def _run_prefill(q, k, v, log_decay, beta, eps, state=None, workspace=None, dt=torch.bfloat16):
     B, H, L, _ = q.shape
     y = torch.empty(B, H, L, D, device=dev())
     st_in = state_to_dev(state, B, H, D) if state is not None else None
     st_out = _lib.new_state(B, H, D, dev())
-    _lib.selective_prefill(to_dev(q, torch.bfloat16), to_dev(k, torch.bfloat16), to_dev(v, torch.bfloat16),
+    _lib.selective_prefill(to_dev(q, dt), to_dev(k, dt), to_dev(v, dt),
                            to_dev(log_decay), to_dev(beta), eps, st_in, y, st_out, workspace=workspace)
     torch.cuda.synchronize()
     return to_np(y).reshape(B * H, L, D), state_to_np(st_out, B * H, D)
@@ -71,6 +71,39 @@ def test_selective_prefill_matches_oracle(L, with_state):
     assert_close(y, yo, TOL_BF16, "y")
     for i, (a, b) in enumerate(zip(s, so)):
         assert_close(a, b.reshape(a.shape), TOL_BF16, f"state[{i}]")
+
+
+@pytest.mark.parametrize("L", [1, 13, 64, 100, 300, 1000])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_selective_prefill_f32_matches_oracle(L, with_state):
+    """fp32 inputs run the fp32 prefill kernel: the fp32 tolerance applies."""
+    B, H = 2, 3
+    q, k, v, ld, beta = _inputs(B, H, L, seed=130 + L, bf16=False)
+    st = _rand_state(B * H, 131) if with_state else None
+    yo, so = _oracle(q, k, v, ld, beta, 1.0, st)
+    y, s = _run_prefill(q, k, v, ld, beta, 1.0, st, dt=torch.float32)
+    assert_close(y, yo, TOL_F32, "y")
+    for i, (a, b) in enumerate(zip(s, so)):
+        assert_close(a, b.reshape(a.shape), TOL_F32, f"state[{i}]")
+
+
+def test_selective_prefill_f32_parallel_branch_gqa_and_eps():
+    """fp32 against the reference's own parallel form (the [L, L] decay matrix
+    from the softplus step sizes, selective.py:414-440), with GQA and an eps
+    small enough for the denominator clamp to be reachable."""
+    B, H, Hkv, L = 1, 4, 2, 1500
+    q, k, v, _, beta = _inputs(B, H, L, seed=140, Hkv=Hkv, bf16=False)
+    rng = np.random.default_rng(141)
+    delta = np.log1p(np.exp(rng.standard_normal((B * H, L)) - 1.0))
+    tau = rng.uniform(8.0, 400.0, H)
+    ld = (-delta / np.tile(tau, B)[:, None]).astype(np.float32).reshape(B, H, L)
+    ke, ve = np.repeat(k, H // Hkv, axis=1), np.repeat(v, H // Hkv, axis=1)
+    yo, so = O.selective_parallel(q.reshape(B * H, L, D), ke.reshape(B * H, L, D), ve.reshape(B * H, L, D),
+                                  delta, np.tile(tau, B), np.tile(beta.astype(np.float64), B), eps=1e-3)
+    y, s = _run_prefill(q, k, v, ld, beta, 1e-3, dt=torch.float32)
+    assert_close(y, yo, TOL_F32, "y")
+    for i, (a, b) in enumerate(zip(s, so)):
+        assert_close(a, b.reshape(a.shape), TOL_F32, f"state[{i}]")
 
 
 def test_selective_prefill_segments_gqa_and_eps():
@@ -143,14 +176,14 @@ def test_selective_decode_step_matches_oracle(qk_norm):
         assert_close(a, b.reshape(a.shape), tol, f"state[{i}]")
 
 
-def _module(seed=0, H=2):
+def _module(seed=0, H=2, dtype=torch.bfloat16):
     torch.manual_seed(seed)
     m = PrimeSelectiveMomentAttention(128, H, D, decay=0.99).to(dev())
     with torch.no_grad():  # move off the identity initialisation
         m.delta_proj.weight.normal_(0.0, 0.05)
         m.log_tau.add_(torch.randn(H, device=dev()) * 0.5)
         m.log_beta.add_(torch.randn(H, device=dev()) * 0.3)
-    return m.bfloat16()
+    return m.to(dtype)
 
 
 def _module_ref(m, x, state=None):
@@ -196,6 +229,22 @@ def test_selective_module_prefill_then_step():
     assert_close(to_np(out1.float()), ref1, TOL_BF16, "step out")
     for i, (a, b) in enumerate(zip(state_to_np(st1, 4, D), S1)):
         assert_close(a, b.reshape(a.shape), TOL_BF16, f"step state[{i}]")
+
+
+def test_selective_module_f32_prefill_then_step():
+    """An fp32 module: the prefill runs the fp32 kernel, the step the decode
+    kernel in fp32; both within the fp32 tolerance of the fp64 composition."""
+    m = _module(seed=3, dtype=torch.float32)
+    x = torch.randn(2, 301, 128, device=dev())
+    with torch.no_grad():
+        out, st = m(x[:, :300], return_state=True)
+        out1, st1 = m(x[:, 300:], state=st, return_state=True)
+    ref, S = _module_ref(m, x[:, :300])
+    assert_close(to_np(out), ref, TOL_F32, "prefill out")
+    for i, (a, b) in enumerate(zip(state_to_np(st, 4, D), S)):
+        assert_close(a, b.reshape(a.shape), TOL_F32, f"prefill state[{i}]")
+    ref1, _ = _module_ref(m, x[:, 300:], state=S)
+    assert_close(to_np(out1), ref1, TOL_F32, "step out")
 
 
 def _sel_model(seed=0):
