@@ -7,13 +7,16 @@
 // read out with the UPDATED state.
 //
 // Design: the step is HBM-bound (67.6 KB of state traffic per tile against
-// ~33 kflop).  One wavefront owns one tile.  Lane l owns value columns
-// 4*(l&15)..+3 and key rows {4r + (l>>4)}, r = 0..15, so each wave-wide
-// 128-bit load/store instruction touches four consecutive 256-byte rows: one
-// contiguous 1 KB segment.  All 32 loads of S1/S2 are issued before any math
-// (registers hold the whole 32 KB tile across the wave), the update and readout
-// are fused per row, and the 64-term key contraction ends with two cross-lane
-// butterflies.  The S1/S2 loads and stores are nontemporal: each state byte is
+// ~33 kflop).  Two wavefronts own one tile, wave w the key rows 32w..32w+31.
+// Lane l owns value columns 4*(l&15)..+3 and key rows {32w + 4r + (l>>4)},
+// r = 0..7, so each wave-wide 128-bit load/store instruction touches four
+// consecutive 256-byte rows: one contiguous 1 KB segment.  All 16 loads of a
+// wave's S1/S2 rows are issued before any math (registers hold its 16 KB half
+// tile), the update and readout are fused per row, and the key contraction
+// ends with two cross-lane butterflies and one sum of the two waves' halves
+// through LDS.  Half tiles keep a wave's registers low enough for five waves
+// per SIMD: with whole tiles per wave (three waves at most), the last rounds
+// of a launch left the memory system idle.  The S1/S2 loads and stores are nontemporal: each state byte is
 // touched once per step, and with the streaming hint the stores leave the caches
 // as the loads arrive (42 against 51 us per launch at B = 256 x 12 heads).  The denominator is a wavefront reduction.  state_in may alias
 // state_out: every element is read and written by the same lane.
@@ -23,7 +26,7 @@
 namespace prime {
 
 
-constexpr int kDecodeWaves = 1;  // one wavefront per workgroup: the scheduler places waves one at a time
+constexpr int kDecodeWaves = 2;  // the two row halves of one tile
 
 // x rounded to dtype dt (to nearest even), returned as fp32
 __device__ __forceinline__ float round_to(float x, int dt) {
@@ -34,10 +37,11 @@ __device__ __forceinline__ float round_to(float x, int dt) {
 
 __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const DecodeArgs a) {
     __shared__ float sh[kDecodeWaves][4][kD];  // per wave: q, k, v, updated S0
-    const int wave = threadIdx.x >> 6;
+    __shared__ f32x4 sacc[16];                 // wave 1's readout numerators (row group 0 lanes)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int BH = a.B * a.H;
-    const int tile = blockIdx.x * kDecodeWaves + wave;
+    const int tile = blockIdx.x;
     const bool active = tile < BH;
     const int t = active ? tile : 0;
     const int b = t / a.H, h = t - (t / a.H) * a.H, hk = h / a.group;
@@ -89,12 +93,13 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
     const size_t tb = static_cast<size_t>(t) * (kD * kD);
     const size_t tv = static_cast<size_t>(t) * kD;
 
-    f32x4 r1[16], r2[16];
+    const int rb = 32 * wave;  // this wave's first key row
+    f32x4 r1[8], r2[8];
     float s0v = 0.f, k1v = 0.f, k2v = 0.f, k0v = 0.f;
     if (active && has_in) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const size_t o = tb + (4 * r + rg) * kD + 4 * cg;
+        for (int r = 0; r < 8; ++r) {
+            const size_t o = tb + (rb + 4 * r + rg) * kD + 4 * cg;
             r1[r] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.s1i + o));
             r2[r] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.s2i + o));
         }
@@ -104,7 +109,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
         k0v = a.k0i[t];
     } else {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
+        for (int r = 0; r < 8; ++r) {
             r1[r] = f32x4{0.f, 0.f, 0.f, 0.f};
             r2[r] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
@@ -127,8 +132,8 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
     const f32x4 v4 = *reinterpret_cast<const f32x4 *>(&sh[wave][2][4 * cg]);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = 4 * r + rg;
+    for (int r = 0; r < 8; ++r) {
+        const int row = rb + 4 * r + rg;
         const float kr = sh[wave][1][row];
         const float qr = sh[wave][0][row];
         const float kr2 = h2k * kr * kr;
@@ -146,12 +151,18 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
             __builtin_nontemporal_store(n2, reinterpret_cast<f32x4 *>(a.s2o + o));
         }
     }
-    // sum the four row groups (lanes cg, cg+16, cg+32, cg+48)
+    // sum the four row groups (lanes cg, cg+16, cg+32, cg+48), then the two halves
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         acc[c] += __shfl_xor(acc[c], 16, kWave);
         acc[c] += __shfl_xor(acc[c], 32, kWave);
     }
+    if (wave == 1 && rg == 0) sacc[cg] = acc;
+    __syncthreads();
+    if (wave == 1) return;
+    const f32x4 acc1 = sacc[cg];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] += acc1[c];
     const float den = k0n + wave_sum(qv * k1n + h2q * qv * qv * k2n);
     const float inv = 1.0f / fmaxf(den, a.eps);
 
@@ -173,7 +184,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_step_kernel(const
 
 hipError_t launch_decode_step(const DecodeArgs &a, hipStream_t stream) {
     const int BH = a.B * a.H;
-    const int blocks = (BH + kDecodeWaves - 1) / kDecodeWaves;
+    const int blocks = BH;
     const TimerEvents t = timer_events(PRIME_KERNEL_DECODE);
     hipExtLaunchKernelGGL(decode_step_kernel, dim3(blocks), dim3(kDecodeWaves * kWave), 0, stream, t.start, t.stop, 0,
                           a);
