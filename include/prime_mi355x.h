@@ -381,8 +381,10 @@ int prime_accumulate_noalloc(const prime_tensor_t *k, const prime_tensor_t *v, i
  * k/v must have one head per query head (H_kv == H: the reference module
  * expands grouped k/v before the recurrence, attention.py:92-94).  With
  * PRIME_FLAG_DENSE_CLAMP an incoming state is rejected; without one the two
- * clamps are the same.  MFMA operands are bf16 (fp32 accumulation) for bf16
- * and fp32 inputs alike.  workspace (16-byte aligned): at least B*H*L*8 bytes
+ * clamps are the same.  BF16 inputs run on bf16 MFMA operands (fp32
+ * accumulation); F32 inputs run fp32 passes (fp32 MFMA operands throughout,
+ * one workgroup per sequence, as the reference differentiates in fp32).
+ * workspace (16-byte aligned): at least B*H*L*8 bytes
  * (per-token denominators); with prime_chunked_prefill_backward_workspace_size()
  * bytes, few long sequences are split into segments that run in parallel
  * (segment-entry states by the forward's state-only pass, dual states by a

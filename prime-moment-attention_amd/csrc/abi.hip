@@ -562,7 +562,8 @@ int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t
     a.inv_den = static_cast<float *>(workspace);
     a.g_den = a.inv_den + static_cast<size_t>(B) * H * L;
     prime::plan_backward_segments(B * H, L, &a.G, &a.cps);
-    if (a.G > 1 && workspace_bytes < prime_chunked_prefill_backward_workspace_size(B, H, L)) {
+    if (q->dtype == PRIME_F32 || (a.G > 1 && workspace_bytes < prime_chunked_prefill_backward_workspace_size(B, H, L))) {
+        // (fp32 inputs: the fp32 passes run one workgroup per sequence)
         a.G = 1;  // one segment per sequence in the workspace given
         a.cps = (L + 63) / 64;
     }

@@ -954,6 +954,7 @@ void plan_backward_segments(int S, int L, int *G, int *cps) {
 }
 
 hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream) {
+    if (a.dt_in == PRIME_F32) return launch_prefill_backward_f32(a, stream);
     const int S = a.B * a.H;
     hipError_t e;
     if (a.G > 1) {

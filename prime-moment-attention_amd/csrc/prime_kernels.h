@@ -149,6 +149,8 @@ struct BwdArgs {
 };
 
 hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream);
+// fp32 inputs: the fp32 dq and dk/dv passes, one workgroup per sequence (prefill_bwd_f32.hip)
+hipError_t launch_prefill_backward_f32(const BwdArgs &a, hipStream_t stream);
 // segments per sequence for the backward: enough (sequence, segment) units to
 // fill two workgroups per CU, at least 8 chunks per segment
 void plan_backward_segments(int S, int L, int *G, int *cps);
