@@ -2,6 +2,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "prime_kernels.h"
@@ -9,6 +10,16 @@
 namespace {
 
 thread_local char g_err[512] = "";
+
+// hand-off value of a paired prefill: distinct per call (never 0, the value a
+// consumed flag is reset to)
+std::atomic<unsigned long long> g_epoch{0};
+unsigned long long next_epoch() {
+    unsigned long long e;
+    while ((e = ++g_epoch) == 0) {
+    }
+    return e;
+}
 
 int fail(int code, const char *fmt, ...) {
     va_list ap;
@@ -329,6 +340,18 @@ static int prefill_impl(const prime_tensor_t *q, const prime_tensor_t *k, const 
     const int S = B * H;
     prime::plan_segments(S, L, a.dense_clamp != 0, workspace ? workspace_bytes : 0, &a.G, &a.cps);
     a.ws = a.G > 1 ? static_cast<float *>(workspace) : nullptr;
+    if (a.G == 1 && workspace && q->dtype == PRIME_BF16 && !a.dense_clamp) {
+        // more sequences than CUs: the paired split, when the workspace holds it
+        int K, pcs;
+        prime::plan_pairs(S, L, &K, &pcs);
+        if (K > 0 && workspace_bytes >= prime::pair_ws_bytes(K)) {
+            a.npair = K;
+            a.pcs = pcs;
+            a.ws = static_cast<float *>(workspace);
+            a.pflag = reinterpret_cast<unsigned long long *>(a.ws + static_cast<size_t>(K) * prime::kWsStride);
+            a.epoch = next_epoch();
+        }
+    }
     (void)inplace;  // in place is safe: each workgroup reads its own state before writing it
     return check_hip(prime::launch_prefill(a, static_cast<hipStream_t>(stream)), "prefill launch");
 }
@@ -769,7 +792,11 @@ size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags)
     if (B <= 0 || H <= 0 || L <= 0) return 0;
     int G, cps;
     prime::plan_segments(B * H, L, (flags & PRIME_FLAG_DENSE_CLAMP) != 0, static_cast<size_t>(-1), &G, &cps);
-    return G > 1 ? static_cast<size_t>(B) * H * G * prime::kWsStride * sizeof(float) : 0;
+    if (G > 1) return static_cast<size_t>(B) * H * G * prime::kWsStride * sizeof(float);
+    if (flags & PRIME_FLAG_DENSE_CLAMP) return 0;
+    int K, pcs;
+    prime::plan_pairs(B * H, L, &K, &pcs);
+    return K > 0 ? prime::pair_ws_bytes(K) : 0;
 }
 
 }  // extern "C"

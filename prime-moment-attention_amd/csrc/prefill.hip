@@ -38,6 +38,11 @@
 // (F32IN) keep every LDS array as a bf16 hi plane plus a lo residual plane and
 // accumulate hi*hi + hi*lo + lo*hi (three MFMAs per product, ~2^-16 relative).
 
+#include <algorithm>
+#include <functional>
+#include <mutex>
+#include <vector>
+
 #include "prefill_common.h"
 
 namespace prime {
@@ -231,6 +236,80 @@ void plan_segments(int S, int L, bool dense_clamp, size_t ws_bytes, int *G, int 
     }
     *G = best_g;
     *cps = best_c;
+}
+
+// Paired split.  With more sequences S than CUs the fused kernel (one
+// workgroup per CU) runs ceil(S / CUs) rounds of whole sequences, the last one
+// partly empty (384 sequences on 256 CUs: two rounds of work for 1.5).  Cutting
+// K sequences into a first part of pcs chunks and a second part, launched
+// [K first parts][S - K whole][K second parts], lets the in-order dispatch
+// pack them (at 1.5 x CUs: half the CUs run a first part and then a whole
+// sequence, the other half a whole sequence and then a second part, whose
+// first part ended long before).  The plan comes from simulating that
+// dispatch (each unit to the CU that frees first; a second part starts no
+// earlier than its first part's end) in chunk-steps, with half a chunk-step
+// per workgroup for its prologue and state I/O; a plan must beat whole
+// sequences by 3 %.  Plans are cached per (S, chunks, CUs).
+namespace {
+
+double simulate_pairs(int S, int NC, int cu, int K, int pcs) {
+    constexpr double kUnit = 0.5;
+    std::vector<double> cpu(static_cast<size_t>(cu), 0.0);  // min-heap of CU free times
+    std::vector<double> first_end(static_cast<size_t>(K), 0.0);
+    auto run = [&](double len, double ready) {
+        std::pop_heap(cpu.begin(), cpu.end(), std::greater<double>());
+        const double end = std::max(cpu.back(), ready) + len + kUnit;
+        cpu.back() = end;
+        std::push_heap(cpu.begin(), cpu.end(), std::greater<double>());
+        return end;
+    };
+    double span = 0.0;
+    for (int i = 0; i < K; ++i) span = std::max(span, first_end[static_cast<size_t>(i)] = run(pcs, 0.0));
+    for (int i = K; i < S; ++i) span = std::max(span, run(NC, 0.0));
+    for (int i = 0; i < K; ++i) span = std::max(span, run(NC - pcs, first_end[static_cast<size_t>(i)]));
+    return span;
+}
+
+struct PairPlan {
+    int S, NC, cu, K, pcs;
+};
+std::mutex g_pair_mu;
+std::vector<PairPlan> g_pair_cache;
+
+}  // namespace
+
+void plan_pairs(int S, int L, int *K, int *pcs) {
+    const int NC = (L + kC - 1) / kC;
+    const int cu = device_cus();
+    *K = 0;
+    *pcs = NC;
+    if (S <= cu || NC < 2) return;
+    std::lock_guard<std::mutex> lock(g_pair_mu);
+    for (const PairPlan &p : g_pair_cache)
+        if (p.S == S && p.NC == NC && p.cu == cu) {
+            *K = p.K;
+            *pcs = p.pcs;
+            return;
+        }
+    const double whole = simulate_pairs(S, NC, cu, 0, NC);
+    double best = 0.97 * whole;
+    int best_k = 0, best_p = NC;
+    const int kmax = std::min(S, cu), step = std::max(1, cu / 64);
+    const int cand[5] = {NC / 2, NC / 3, (2 * NC) / 3, NC / 4, (3 * NC) / 4};
+    for (int k = step; k <= kmax; k += step)
+        for (int p : cand) {
+            if (p < 1 || p >= NC) continue;
+            const double t = simulate_pairs(S, NC, cu, k, p);
+            if (t < best - 1e-9) {
+                best = t;
+                best_k = k;
+                best_p = p;
+            }
+        }
+    if (g_pair_cache.size() >= 64) g_pair_cache.clear();
+    g_pair_cache.push_back(PairPlan{S, NC, cu, best_k, best_p});
+    *K = best_k;
+    *pcs = best_p;
 }
 
 // One workgroup = (sequence, segment); see the header comment.  STATE_ONLY
@@ -743,7 +822,7 @@ static hipError_t launch_variant(PrefillArgs a, hipStream_t stream) {
     if constexpr (F32IN)
         hipExtLaunchKernelGGL((prefill_kernel<true, false>), dim3(Sq * a.G), dim3(512), 0, stream, tc.start, tc.stop, 0,
                               a);
-    else launch_prefill_bf16(a, false, Sq * a.G, stream, tc);
+    else launch_prefill_bf16(a, false, Sq * a.G + a.npair, stream, tc);
     if ((e = hipGetLastError()) != hipSuccess) timer_drop(tc);
     return e;
 }

@@ -199,20 +199,60 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
 
     const int Sq = a.B * a.H;
     const int unit = blockIdx.x;
-    if (unit >= Sq * a.nseg_launch) return;  // whole workgroup leaves before any barrier
-    const int seq = unit / a.nseg_launch, seg = unit - seq * a.nseg_launch;
+    const int NC = (a.L + kC - 1) / kC;
+    // part: -1 a whole segment; 0 / 1 the first / second part of a paired sequence
+    int seq, seg, c_begin, c_end, part = -1;
+    if (!STATE_ONLY && a.npair > 0) {
+        if (unit >= Sq + a.npair) return;  // whole workgroup leaves before any barrier
+        seg = 0;
+        if (unit < Sq) {
+            seq = unit;
+            if (unit < a.npair) part = 0;
+        } else {
+            seq = unit - Sq;
+            part = 1;
+        }
+        c_begin = part == 1 ? a.pcs : 0;
+        c_end = part == 0 ? a.pcs : NC;
+    } else {
+        if (unit >= Sq * a.nseg_launch) return;  // whole workgroup leaves before any barrier
+        seq = unit / a.nseg_launch;
+        seg = unit - seq * a.nseg_launch;
+        c_begin = seg * a.cps;
+        c_end = min(c_begin + a.cps, NC);
+    }
     const int b = seq / a.H, h = seq - b * a.H, hk = h / a.group;
     const float lam = SEL ? 1.0f : a.decay[h];
     const float kscale = SEL ? a.k_scale[h] : 1.0f;
     // selective: per-token natural-log decays, read as log2 (exp2 on the VALU)
     const float *ldp = SEL ? a.log_decay + static_cast<size_t>(b * a.H + h) * a.L : nullptr;
-    const int NC = (a.L + kC - 1) / kC;
-    const int c_begin = seg * a.cps;
-    const int c_end = min(c_begin + a.cps, NC);
-    const bool from_ws = !STATE_ONLY && a.G > 1;
+    const bool from_ws = !STATE_ONLY && (a.G > 1 || part == 1);
     const bool has_in = !STATE_ONLY && !from_ws && a.s1i != nullptr;
     const bool dense = !STATE_ONLY && a.dense_clamp;
     float *wslot = a.ws ? a.ws + (static_cast<size_t>(seq) * a.G + seg) * kWsStride : nullptr;
+
+    // second part of a paired sequence: wait for the first part's end state.
+    // The first part has the lower workgroup index, so it was dispatched
+    // earlier and finishes without waiting; the bound only guards against a
+    // broken launch (the state then reads as NaN, so the outputs show it).
+    __shared__ int sPairBad;
+    if (part == 1 && tid == 0) {
+        unsigned long long *f = a.pflag + seq;
+        int n = 0, bad = 0;
+        while (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != a.epoch) {
+            if (++n > kPairSpin) {
+                bad = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(8);
+        }
+        // one acquire for the workgroup: it invalidates this CU's and this
+        // XCD's caches, so the other waves' slot reads after the barrier miss
+        // any line of the slot cached before the first part wrote it
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        __hip_atomic_store(f, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sPairBad = bad;
+    }
 
     if (tid < kC + 2) {
         const double ld = static_cast<double>(lam);
@@ -234,6 +274,9 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
         }
     }
     __syncthreads();  // the power tables (and QKN's parameters) are read by the first tile stores below
+    // second part: every wave's slot reads below come after the first part's release
+    const bool pair_bad = part == 1 && sPairBad != 0;
+    auto ws_at = [&](int i) { return pair_bad ? __builtin_nanf("") : wslot[i]; };
 
     // ---- update role: state registers, tile pointers, first tiles
     const size_t so1 = static_cast<size_t>(seq) * kD * kD;
@@ -327,21 +370,21 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
                     const int n = 16 * nb + c16;
                     float x = 0.f;
                     if (n < kD) {
-                        if (from_ws) x = wslot[(f < kD ? kWsS1 : kWsS2) + fr * kD + n];
+                        if (from_ws) x = ws_at((f < kD ? kWsS1 : kWsS2) + fr * kD + n);
                         else if (has_in) x = (f < kD ? a.s1i : a.s2i)[so1 + fr * kD + n];
                     } else if (n == kD && !dense) {  // dense: K of the call only, incoming in sKi
-                        if (from_ws) x = wslot[(f < kD ? kWsK1 : kWsK2) + fr];
+                        if (from_ws) x = ws_at((f < kD ? kWsK1 : kWsK2) + fr);
                         else if (has_in) x = (f < kD ? a.k1i : a.k2i)[so0 + fr];
                     }
                     st[fi][nb][r] = (f < kD || SEL) ? x : 0.5f * x;  // selective states carry the 1/2
                 }
         {
             float x = 0.f;
-            if (g == 0 && u < 4) x = from_ws ? wslot[kWsS0 + 16 * u + c16] : (has_in ? a.s0i[so0 + 16 * u + c16] : 0.f);
+            if (g == 0 && u < 4) x = from_ws ? ws_at(kWsS0 + 16 * u + c16) : (has_in ? a.s0i[so0 + 16 * u + c16] : 0.f);
             s0t = f32x4{x, 0.f, 0.f, 0.f};
         }
         {
-            const float x = from_ws ? wslot[kWsK0] : (has_in ? a.k0i[seq] : 0.f);
+            const float x = from_ws ? ws_at(kWsK0) : (has_in ? a.k0i[seq] : 0.f);
             k0 = dense ? 0.f : x;
             if (!STATE_ONLY && ut == 0) sKi0 = dense ? x : 0.f;
         }
@@ -541,6 +584,7 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
             }
             __syncthreads();
         }
+        if (part == 0) __syncthreads();  // the update waves' hand-off barrier below
         return;
     }
     // row 0 of the ones operand: lanes of A-row 0 hold eight 1.0s
@@ -600,7 +644,7 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
     // ---- segment / final state (decays used the valid counts: no pad correction)
     float *o_s1, *o_s2, *o_s0, *o_k1, *o_k2, *o_k0;
     size_t off1, off0, offk0;
-    if (STATE_ONLY) {
+    if (STATE_ONLY || part == 0) {  // a segment's contribution / a first part's end state
         o_s1 = wslot + kWsS1; o_s2 = wslot + kWsS2; o_s0 = wslot + kWsS0;
         o_k1 = wslot + kWsK1; o_k2 = wslot + kWsK2; o_k0 = wslot + kWsK0;
         off1 = 0; off0 = 0; offk0 = 0;
@@ -633,6 +677,16 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
     if (u == 0 && lane == 0) o_k0[offk0] = k0 + (STATE_ONLY ? 0.f : linit * sKi0);
     // selective: the segment's own log2 decay, for the scan over segments
     if (SEL && STATE_ONLY && u == 0 && lane == 0) wslot[kWsDecay] = seg_ld;
+    if (!STATE_ONLY && part == 0) {
+        // hand-off: every update thread waits until its slot stores have
+        // reached this XCD's L2; after the barrier (which the readout waves also
+        // meet) one release writes the L2 back and publishes the flag.  (A
+        // device-scope fence in every thread would write the L2 back once per
+        // wave, and those write-backs stall the whole XCD.)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (ut == 0) __hip_atomic_store(a.pflag + seq, a.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 template <bool QKN>

@@ -118,6 +118,16 @@ struct PrefillArgs {
     const void *qn_w, *qn_b, *kn_w, *kn_b;
     int dt_norm;
     float ln_eps, q_scale;
+    // paired split (bf16 fused kernel, G == 1, more sequences than CUs): the
+    // first npair sequences run as two workgroups, chunks [0, pcs) and
+    // [pcs, NC).  Grid order: the npair first parts, the other sequences
+    // whole, then the npair second parts.  A first part writes its end state
+    // to ws slot `seq` and then pflag[seq] = epoch (release); the second part
+    // waits for that value (acquire, bounded), resets the flag to 0 and
+    // starts from the slot.
+    int npair, pcs;
+    unsigned long long *pflag;
+    unsigned long long epoch;
 };
 
 // packed fp32 state slot in the workspace: S1 | S2 | S0 | K1 | K2 | K0
@@ -162,6 +172,14 @@ hipError_t launch_prefill(PrefillArgs a, hipStream_t stream);
 hipError_t launch_selective_f32(const PrefillArgs &a, hipStream_t stream);
 // segments per sequence for the launch plan, given the workspace the caller has
 void plan_segments(int S, int L, bool dense_clamp, size_t ws_bytes, int *G, int *cps);
+// paired split for the bf16 fused kernel when S exceeds the CU count (K = 0:
+// none pays); its workspace: K slots, then K 8-byte flags
+void plan_pairs(int S, int L, int *K, int *pcs);
+inline size_t pair_ws_bytes(int K) {
+    return static_cast<size_t>(K) * (kWsStride * sizeof(float) + sizeof(unsigned long long));
+}
+// spin bound of a second part's wait (iterations of a ~0.2 us sleep plus a load)
+constexpr int kPairSpin = 1 << 22;
 
 // Chunked gated delta-rule prefill (delta.hip).
 struct DeltaArgs {
