@@ -257,8 +257,20 @@ int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int
  */
 #define PRIME_EPILOGUE_NONE 0
 #define PRIME_EPILOGUE_GELU 1
+#define PRIME_EPILOGUE_RESIDUAL 2 /* prime_linear_residual only */
 int prime_linear(const void *x, const void *w, void *y, int M, int N, int K, int64_t ldx, int64_t ldw,
                  int64_t ldy, int dtype, int epilogue, void *stream);
+
+/*
+ * y = r + x . w^T: a projection and the residual add after it in one pass (the
+ * blocks' x + o_proj(...) and x + down_proj(...), model.py:107-118).  The
+ * product is rounded to bf16 first, then added to r and rounded again, as the
+ * separate GEMM and add store it.  r [M, N] with row stride ldr may be y (in
+ * place: the residual stream updated where it lies), otherwise disjoint from
+ * it; the other arguments as prime_linear.  BF16 only.
+ */
+int prime_linear_residual(const void *x, const void *w, const void *r, void *y, int M, int N, int K,
+                          int64_t ldx, int64_t ldw, int64_t ldr, int64_t ldy, int dtype, void *stream);
 
 /*
  * Selective PRIME (PrimeSelectiveMomentAttention, selective.py:264-444): the

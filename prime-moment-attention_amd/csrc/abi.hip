@@ -238,16 +238,15 @@ int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int
     return check_hip(prime::launch_head_layernorm(a, static_cast<hipStream_t>(stream)), "head_layernorm launch");
 }
 
-int prime_linear(const void *x, const void *w, void *y, int M, int N, int K, int64_t ldx, int64_t ldw,
-                 int64_t ldy, int dtype, int epilogue, void *stream) {
-    g_err[0] = 0;
-    if (!x || !w || !y) return fail(PRIME_ERR_INVALID_ARG, "prime_linear: null argument");
+namespace {
+
+int linear_checks(const char *who, const void *x, const void *w, const void *y, int M, int N, int K, int64_t ldx,
+                  int64_t ldw, int64_t ldy, int dtype) {
+    if (!x || !w || !y) return fail(PRIME_ERR_INVALID_ARG, "%s: null argument", who);
     if (M <= 0 || N <= 0 || K <= 0 || K % 64 || N % 4)
         return fail(PRIME_ERR_INVALID_ARG, "bad sizes M=%d N=%d K=%d (K a multiple of 64, N of 4)", M, N, K);
     if (ldx < K || ldw < K || ldy < N) return fail(PRIME_ERR_INVALID_ARG, "row strides below the row lengths");
-    if (dtype != PRIME_BF16) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "prime_linear: BF16 only");
-    if (epilogue != PRIME_EPILOGUE_NONE && epilogue != PRIME_EPILOGUE_GELU)
-        return fail(PRIME_ERR_INVALID_ARG, "unknown epilogue %d", epilogue);
+    if (dtype != PRIME_BF16) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "%s: BF16 only", who);
     if (!aligned16(x) || !aligned16(w) || (ldx % 8) || (ldw % 8))
         return fail(PRIME_ERR_MISALIGNED, "x and w rows must start on 16-byte boundaries");
     if ((reinterpret_cast<uintptr_t>(y) & 7) || (ldy % 4))
@@ -255,9 +254,39 @@ int prime_linear(const void *x, const void *w, void *y, int M, int N, int K, int
     const size_t nx = static_cast<size_t>((M - 1) * ldx + K) * 2, nw = static_cast<size_t>((N - 1) * ldw + K) * 2,
                  ny = static_cast<size_t>((M - 1) * ldy + N) * 2;
     if (overlap(y, ny, x, nx) || overlap(y, ny, w, nw)) return fail(PRIME_ERR_ALIAS, "y overlaps x or w");
+    return PRIME_OK;
+}
+
+}  // namespace
+
+int prime_linear(const void *x, const void *w, void *y, int M, int N, int K, int64_t ldx, int64_t ldw,
+                 int64_t ldy, int dtype, int epilogue, void *stream) {
+    g_err[0] = 0;
+    if (epilogue != PRIME_EPILOGUE_NONE && epilogue != PRIME_EPILOGUE_GELU)
+        return fail(PRIME_ERR_INVALID_ARG, "unknown epilogue %d", epilogue);
+    int rc;
+    if ((rc = linear_checks("prime_linear", x, w, y, M, N, K, ldx, ldw, ldy, dtype))) return rc;
     prime::LinearArgs a{};
     a.x = x; a.w = w; a.y = y; a.ldx = ldx; a.ldw = ldw; a.ldy = ldy;
     a.M = M; a.N = N; a.K = K; a.epilogue = epilogue;
+    return check_hip(prime::launch_linear(a, static_cast<hipStream_t>(stream)), "linear launch");
+}
+
+int prime_linear_residual(const void *x, const void *w, const void *r, void *y, int M, int N, int K,
+                          int64_t ldx, int64_t ldw, int64_t ldr, int64_t ldy, int dtype, void *stream) {
+    g_err[0] = 0;
+    int rc;
+    if ((rc = linear_checks("prime_linear_residual", x, w, y, M, N, K, ldx, ldw, ldy, dtype))) return rc;
+    if (!r) return fail(PRIME_ERR_INVALID_ARG, "prime_linear_residual: null r");
+    if (ldr < N) return fail(PRIME_ERR_INVALID_ARG, "r row stride below the row length");
+    if ((reinterpret_cast<uintptr_t>(r) & 7) || (ldr % 4))
+        return fail(PRIME_ERR_MISALIGNED, "r rows must start on 8-byte boundaries");
+    const size_t nr = static_cast<size_t>((M - 1) * ldr + N) * 2, ny = static_cast<size_t>((M - 1) * ldy + N) * 2;
+    if (!(r == y && ldr == ldy) && overlap(r, nr, y, ny))
+        return fail(PRIME_ERR_ALIAS, "r overlaps y (only r == y with the same row stride is allowed)");
+    prime::LinearArgs a{};
+    a.x = x; a.w = w; a.y = y; a.r = r; a.ldx = ldx; a.ldw = ldw; a.ldy = ldy; a.ldr = ldr;
+    a.M = M; a.N = N; a.K = K; a.epilogue = PRIME_EPILOGUE_RESIDUAL;
     return check_hip(prime::launch_linear(a, static_cast<hipStream_t>(stream)), "linear launch");
 }
 

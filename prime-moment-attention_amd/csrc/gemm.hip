@@ -135,6 +135,14 @@ __global__ __launch_bounds__(TM * TN * KS * kWave) void linear_skinny_kernel(con
                 for (int v = 0; v < KS; ++v) s += red[v][row][c4 + e];
                 o[e] = a.epilogue == PRIME_EPILOGUE_GELU ? gelu_erf(s) : s;
             }
+            if (a.epilogue == PRIME_EPILOGUE_RESIDUAL) {  // the product rounded, then the residual add
+                const uint2 rv = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(a.r) +
+                                                                  static_cast<int64_t>(m) * a.ldr + n);
+                o[0] = bf16_bits_to_f32(f32_to_bf16_bits(o[0])) + __uint_as_float(rv.x << 16);
+                o[1] = bf16_bits_to_f32(f32_to_bf16_bits(o[1])) + __uint_as_float(rv.x & 0xFFFF0000u);
+                o[2] = bf16_bits_to_f32(f32_to_bf16_bits(o[2])) + __uint_as_float(rv.y << 16);
+                o[3] = bf16_bits_to_f32(f32_to_bf16_bits(o[3])) + __uint_as_float(rv.y & 0xFFFF0000u);
+            }
             uint16_t *yp = static_cast<uint16_t *>(a.y) + static_cast<int64_t>(m) * a.ldy + n;
             *reinterpret_cast<uint2 *>(yp) = uint2{pack2(o[0], o[1]), pack2(o[2], o[3])};
         }
@@ -150,6 +158,7 @@ static void launch_cfg(const LinearArgs &a, hipStream_t stream) {
 // 64 x 64 tiles (half the operand traffic of 32 x 32) when they still give
 // enough workgroups; otherwise 32 x 32 tiles with K split over 4 or 16 waves.
 hipError_t launch_linear(const LinearArgs &a, hipStream_t stream) {
+    if (a.M >= 2048 && linear_tile_fits(a)) return launch_linear_tile(a, stream);
     const int64_t tiles64 = static_cast<int64_t>((a.M + 63) / 64) * ((a.N + 63) / 64);
     const int nblk = a.K / kGK;
     if (tiles64 >= 96) launch_cfg<2, 2, 2>(a, stream);

@@ -75,8 +75,13 @@ struct LinearArgs {
     void *y;
     int64_t ldx, ldw, ldy;  // row strides in elements
     int M, N, K, epilogue;
+    const void *r;          // PRIME_EPILOGUE_RESIDUAL: y = r + x w^T (r may be y)
+    int64_t ldr;
 };
 hipError_t launch_linear(const LinearArgs &a, hipStream_t stream);
+// 256 x 256-tile kernel for many rows (gemm_tile.hip): M >= 256, N % 256 == 0, K % 64 == 0
+bool linear_tile_fits(const LinearArgs &a);
+hipError_t launch_linear_tile(const LinearArgs &a, hipStream_t stream);
 
 constexpr int kNormMaxGroups = 16;  // 4-element groups per lane: hidden <= 4 * 64 * 16 = 4096
 hipError_t launch_add_rmsnorm(const RmsNormArgs &a, hipStream_t stream);

@@ -26,7 +26,7 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
            "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
            "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_argmax",
-           "prime_head_layernorm", "prime_linear", "prime_selective_prefill",
+           "prime_head_layernorm", "prime_linear", "prime_linear_residual", "prime_selective_prefill",
            "prime_selective_decode_step", "prime_accumulate", "prime_accumulate_workspace_size",
            "prime_decode_readout", "prime_decode_update", "prime_chunked_prefill_backward",
            "prime_chunked_prefill_backward_workspace_size", "prime_chunked_prefill_qknorm",
@@ -114,6 +114,8 @@ def load() -> ctypes.CDLL:
     L.prime_head_layernorm.restype = ctypes.c_int
     L.prime_linear.argtypes = [fp, fp, fp] + [ctypes.c_int] * 3 + [ctypes.c_int64] * 3 + [ctypes.c_int] * 2 + [fp]
     L.prime_linear.restype = ctypes.c_int
+    L.prime_linear_residual.argtypes = [fp] * 4 + [ctypes.c_int] * 3 + [ctypes.c_int64] * 4 + [ctypes.c_int, fp]
+    L.prime_linear_residual.restype = ctypes.c_int
     L.prime_selective_prefill.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 5 + [
         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, P(PrimeState), P(PrimeTensor), P(PrimeState),
         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
@@ -361,9 +363,7 @@ def head_layernorm(x: torch.Tensor, out: torch.Tensor, norm: Optional[torch.nn.L
 EPILOGUE_NONE, EPILOGUE_GELU = 0, 1
 
 
-def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, epilogue: int = EPILOGUE_NONE) -> torch.Tensor:
-    """prime_linear: out = epilogue(x @ w.T) for bf16 x [M, K], w [N, K],
-    out [M, N] (rows with a contiguous last dimension); returns out."""
+def _linear_checks(x, w, out, who):
     _dev_check(x, w, out)
     if x.dim() != 2 or w.dim() != 2 or out.dim() != 2:
         raise ValueError("x, w and out must be 2-D")
@@ -372,13 +372,35 @@ def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, epilogue: int = 
     if w.shape[1] != K or out.shape != (M, N):
         raise ValueError(f"shape mismatch: x {tuple(x.shape)}, w {tuple(w.shape)}, out {tuple(out.shape)}")
     if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
-        raise RuntimeError("prime_linear takes bf16 tensors")
+        raise RuntimeError(f"{who} takes bf16 tensors")
     if x.stride(1) != 1 or w.stride(1) != 1 or out.stride(1) != 1:
         raise ValueError("the last dimension must be contiguous")
+    return M, N, K
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, epilogue: int = EPILOGUE_NONE) -> torch.Tensor:
+    """prime_linear: out = epilogue(x @ w.T) for bf16 x [M, K], w [N, K],
+    out [M, N] (rows with a contiguous last dimension); returns out."""
+    M, N, K = _linear_checks(x, w, out, "prime_linear")
     rc = load().prime_linear(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(w.data_ptr()),
                              ctypes.c_void_p(out.data_ptr()), M, N, K, x.stride(0), w.stride(0), out.stride(0),
                              _DTYPES[torch.bfloat16], int(epilogue), _stream(x.device))
     _check(rc, "prime_linear")
+    return out
+
+
+def linear_residual(x: torch.Tensor, w: torch.Tensor, r: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """prime_linear_residual: out = r + x @ w.T (the product rounded to bf16,
+    then the add rounded), bf16; r [M, N] may be out itself (in place)."""
+    M, N, K = _linear_checks(x, w, out, "prime_linear_residual")
+    _dev_check(r)
+    if r.shape != (M, N) or r.dtype != torch.bfloat16 or r.stride(1) != 1:
+        raise ValueError("r must be a bf16 [M, N] tensor with a contiguous last dimension")
+    rc = load().prime_linear_residual(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(w.data_ptr()),
+                                      ctypes.c_void_p(r.data_ptr()), ctypes.c_void_p(out.data_ptr()), M, N, K,
+                                      x.stride(0), w.stride(0), r.stride(0), out.stride(0),
+                                      _DTYPES[torch.bfloat16], _stream(x.device))
+    _check(rc, "prime_linear_residual")
     return out
 
 

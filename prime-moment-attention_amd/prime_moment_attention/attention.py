@@ -109,8 +109,6 @@ class PrimeMomentAttention(nn.Module):
         B, L, _ = hidden_states.shape
         orig_dtype = hidden_states.dtype
         H, D = self.num_heads, self.head_dim
-        dev = hidden_states.device
-        y_dtype = orig_dtype if orig_dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
 
         if torch.is_grad_enabled() and (hidden_states.requires_grad or any(p.requires_grad for p in self.parameters())):
             # training: QK-norm and scale as torch ops, the recurrence through the
@@ -127,7 +125,20 @@ class PrimeMomentAttention(nn.Module):
                                           dense_clamp=dense)
             y = y.to(orig_dtype).transpose(1, 2).reshape(B, L, H * D)
             return self.o_proj(y), (next_state if return_state else None)
+        y, next_state = self.mix(hidden_states, state, return_state)
+        return self.o_proj(y), (next_state if return_state else None)
 
+    def mix(self, hidden_states: torch.Tensor, state: Optional[Tuple[torch.Tensor, ...]] = None,
+            return_state: bool = False):
+        """The attention up to its output projection, without autograd:
+        (y [B, L, H*D] in the input dtype, next state or None), so that
+        ``forward`` is ``o_proj`` of it (attention.py:83-208) and a caller can
+        fold o_proj into its residual add (PrimeForCausalLM)."""
+        B, L, _ = hidden_states.shape
+        orig_dtype = hidden_states.dtype
+        H, D = self.num_heads, self.head_dim
+        dev = hidden_states.device
+        y_dtype = orig_dtype if orig_dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
         if L == 1:
             # the QK LayerNorm and the 1/sqrt(D) scale run inside the decode kernel
             q, k, v = self.project(hidden_states, normalize=False)
@@ -162,5 +173,4 @@ class PrimeMomentAttention(nn.Module):
                                           y=y_bl.transpose(1, 2), qk_norm=norm)
 
         y = y.to(orig_dtype).transpose(1, 2).reshape(B, L, H * D)
-        output = self.o_proj(y)
-        return output, (next_state if return_state else None)
+        return y, (next_state if return_state else None)

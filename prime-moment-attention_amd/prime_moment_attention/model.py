@@ -123,6 +123,13 @@ class PrimeGeluMLP(nn.Module):
         return self.down_proj(F.gelu(self.up_proj(x)))
 
 
+def _mlp_inner(mlp: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """The MLP up to its down projection: gelu(up x) or silu(gate x) * up x."""
+    if isinstance(mlp, PrimeGeluMLP):
+        return F.gelu(mlp.up_proj(x))
+    return F.silu(mlp.gate_proj(x)) * mlp.up_proj(x)
+
+
 class PrimeBlock(nn.Module):
     """Pre-norm block, model.py:71-118: x + Attn(RMSNorm x); x + MLP(RMSNorm x)."""
 
@@ -201,30 +208,29 @@ class PrimeForCausalLM(nn.Module):
                 loss = F.cross_entropy(shift_logits.view(-1, self.config.vocab_size),
                                        labels[..., 1:].contiguous().view(-1), ignore_index=-100)
             return {"loss": loss, "logits": logits, "states": ns if return_states else None}
-        # The blocks' residual adds are folded into the following RMSNorm
-        # (prime_add_rmsnorm stores the rounded sum, as the separate add does):
-        # x is this call's own residual stream, updated in place; `pending` is
-        # the MLP output still to be added.
+        # x is this call's own residual stream, updated in place: each block's
+        # output projection and its residual add are one GEMM with beta = 1
+        # (x += y W^T, the sum rounded once), followed by the RMSNorm
+        # (prime_add_rmsnorm without a delta).
         x = self.embed_tokens(input_ids)
         hidden = x.shape[-1]
+        x2 = x.view(-1, hidden)
         next_states = [] if return_states else None
-        pending = None
         for i, layer in enumerate(self.layers):
             at = layer.self_attn
             n1 = torch.empty_like(x)
-            _lib.add_rmsnorm(x, pending, layer.input_layernorm.weight, n1, layer.input_layernorm.eps)
-            h, ns = at(n1, state=states[i] if states is not None else None, return_state=return_states)
+            _lib.add_rmsnorm(x, None, layer.input_layernorm.weight, n1, layer.input_layernorm.eps)
+            y, ns = at.mix(n1, state=states[i] if states is not None else None, return_state=return_states)
+            x2.addmm_(y.reshape(x2.shape[0], -1), at.o_proj.weight.t())
             n2 = torch.empty_like(x)
-            _lib.add_rmsnorm(x, h, layer.post_attention_layernorm.weight, n2, layer.post_attention_layernorm.eps)
-            pending = layer.mlp(n2)
+            _lib.add_rmsnorm(x, None, layer.post_attention_layernorm.weight, n2, layer.post_attention_layernorm.eps)
+            x2.addmm_(_mlp_inner(layer.mlp, n2).reshape(x2.shape[0], -1), layer.mlp.down_proj.weight.t())
             if return_states:
                 next_states.append(ns)
         if logits_to_keep:
             x = x[:, -logits_to_keep:].contiguous()
-            pending = pending[:, -logits_to_keep:].contiguous() if pending is not None else None
         nf = torch.empty_like(x)
-        _lib.add_rmsnorm(x.view(-1, hidden), pending.view(-1, hidden) if pending is not None else None,
-                         self.norm.weight, nf.view(-1, hidden), self.norm.eps)
+        _lib.add_rmsnorm(x.view(-1, hidden), None, self.norm.weight, nf.view(-1, hidden), self.norm.eps)
         logits = self.lm_head(nf)
         loss = None
         if labels is not None:

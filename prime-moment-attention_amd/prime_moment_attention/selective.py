@@ -85,6 +85,13 @@ class PrimeSelectiveMomentAttention(nn.Module):
 
     def forward(self, hidden_states: torch.Tensor, state: Optional[Tuple[torch.Tensor, ...]] = None,
                 return_state: bool = False):
+        y, next_state = self.mix(hidden_states, state, return_state)
+        return self.o_proj(y), next_state
+
+    def mix(self, hidden_states: torch.Tensor, state: Optional[Tuple[torch.Tensor, ...]] = None,
+            return_state: bool = False):
+        """The attention up to its output projection: (y [B, L, H*D] in the
+        input dtype, next state or None); ``forward`` is ``o_proj`` of it."""
         B, L, _ = hidden_states.shape
         H, D = self.num_heads, self.head_dim
         orig_dtype, dev = hidden_states.dtype, hidden_states.device
@@ -133,4 +140,4 @@ class PrimeSelectiveMomentAttention(nn.Module):
         y = no_backward("selective PRIME", y, q, k, v, tau, beta, hidden_states,
                         *(state if state is not None else ()))
         y = y.to(orig_dtype).transpose(1, 2).reshape(B, L, H * D)
-        return self.o_proj(y), (next_state if return_state else None)
+        return y, (next_state if return_state else None)
