@@ -79,36 +79,53 @@ __device__ __forceinline__ bf16x8 frag(const uint16_t *stage, int row, int seg) 
     return as_bf16x8(*reinterpret_cast<const u32x4 *>(stage + row * kTK + 8 * swz(row, seg)));
 }
 
+__device__ __forceinline__ int nk_of(const LinearArgs &a) { return a.K / kTK; }
+
+
+// The operand fragments of one K block for one wave: x rows of its four
+// 32-row blocks and w rows of its four 32-column blocks, two 16-wide k-steps.
+struct Frags {
+    bf16x8 x[2][4], w[2][4];
+};
+
+__device__ __forceinline__ void read_frags(Frags &f, const uint16_t *sx, const uint16_t *sw, int wm, int wn, int r32,
+                                           int h) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) f.x[s][i] = frag(sx, 128 * wm + 32 * i + r32, 2 * s + h);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f.w[s][j] = frag(sw, 128 * wn + 32 * j + r32, 2 * s + h);
+    }
+}
+
+__device__ __forceinline__ void mma_frags(f32x16 (&acc)[4][4], const Frags &f) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(f.w[s][j], f.x[s][i], acc[i][j]);
+}
+
+// epilogue staging: a wave's 128 x 128 bf16 quadrant, rows of 16 16-byte
+// granules stored at granule g ^ (row & 15)
+__device__ __forceinline__ int ep_off(int row, int col) {
+    return row * 128 + 8 * ((col >> 3) ^ (row & 15)) + (col & 7);
+}
+
 }  // namespace
 
-// One K block: wait until this thread's loads of block kt have landed (the
-// loads of the two later blocks, 2 x 8, may still be in flight), barrier (every
-// thread's have landed, and every wave is done with the stage of block kt - 1),
-// issue block kt + 3 into that stage (cX / cW: the stage block kt - 1 used),
-// then the MFMAs of block kt.  The barrier is written as an asm statement (a
-// compiler memory barrier), not __syncthreads(), whose fence would make the
-// compiler wait for every load into LDS, the ones just issued included; the
-// stages are separate arrays so that it can tell the loads into one stage from
-// the operand reads of another.
-#define PRIME_TILE_STEP(kt, rX, rW, cX, cW)                                                       \
-    if ((kt) < nk) {                                                                              \
-        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");                            \
-        const int kb = min((kt) + kNS - 1, nk - 1) * kTK;                                         \
-        load_operand(cX, x, a.ldx, m0, a.M - 1, kb, wave, lane);                                  \
-        load_operand(cW, w, a.ldw, n0, a.N - 1, kb, wave, lane);                                  \
-        bf16x8 fx[2][4], fw[2][4];                                                                \
-        _Pragma("unroll") for (int s = 0; s < 2; ++s) {                                           \
-            _Pragma("unroll") for (int i = 0; i < 4; ++i) fx[s][i] = frag(rX, 128 * wm + 32 * i + r32, 2 * s + h); \
-            _Pragma("unroll") for (int j = 0; j < 4; ++j) fw[s][j] = frag(rW, 128 * wn + 32 * j + r32, 2 * s + h); \
-        }                                                                                         \
-        _Pragma("unroll") for (int s = 0; s < 2; ++s)                                             \
-            _Pragma("unroll") for (int i = 0; i < 4; ++i)                                         \
-                _Pragma("unroll") for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(fw[s][j], fx[s][i], acc[i][j]); \
-    }
-
+// K loop.  Four LDS stages hold K blocks kt+1 .. kt+3 while block kt is
+// multiplied from registers: the step of block kt waits for its own loads of
+// block kt+1, meets the barrier (after which every thread's loads of kt+1
+// have landed and every wave has read block kt's fragments, so kt's stage is
+// free), issues block kt+4 into that stage, reads block kt+1's fragments into
+// the other register set and runs block kt's MFMAs.  The barriers are asm
+// statements (compiler memory barriers), not __syncthreads(), whose fence
+// would make the compiler wait for loads it does not know about anyway.
 __global__ __launch_bounds__(256, 1) void linear_tile_kernel(const LinearArgs a) {
-    __shared__ __attribute__((aligned(1024))) uint16_t sX0[kStage], sX1[kStage], sX2[kStage], sX3[kStage];
-    __shared__ __attribute__((aligned(1024))) uint16_t sW0[kStage], sW1[kStage], sW2[kStage], sW3[kStage];
+    __shared__ __attribute__((aligned(1024))) uint16_t sbuf[kNS * 2 * kStage];  // stage s: x at 2s, w at 2s+1
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int wm = wave >> 1, wn = wave & 1;
@@ -118,6 +135,15 @@ __global__ __launch_bounds__(256, 1) void linear_tile_kernel(const LinearArgs a)
     if ((tiles & 7) == 0) t = (t & 7) * (tiles >> 3) + (t >> 3);  // XCD-contiguous tile ranges
     const int m0 = (t / NB) * kTM, n0 = (t % NB) * kTN;
     const uint16_t *x = static_cast<const uint16_t *>(a.x), *w = static_cast<const uint16_t *>(a.w);
+    auto sx = [&](int st) { return sbuf + (2 * st) * kStage; };
+    auto sw = [&](int st) { return sbuf + (2 * st + 1) * kStage; };
+    // block kb into stage st (kb clamped to the last block: such copies land in
+    // a stage that is never read again, and keep the count of loads per step)
+    auto issue = [&](int kb, int st) {
+        const int k0 = min(kb, nk_of(a) - 1) * kTK;
+        load_operand(sx(st), x, a.ldx, m0, a.M - 1, k0, wave, lane);
+        load_operand(sw(st), w, a.ldw, n0, a.N - 1, k0, wave, lane);
+    };
 
     f32x16 acc[4][4];
 #pragma unroll
@@ -127,60 +153,77 @@ __global__ __launch_bounds__(256, 1) void linear_tile_kernel(const LinearArgs a)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    const int nk = a.K / kTK;
-    // blocks 0, 1, 2 in flight before the loop; each step then issues block
-    // kt + 3 (clamped to the last block: a copy into a stage that is never
-    // read again, so that every step issues the same 8 loads per thread and
-    // one wait count fits all)
-    load_operand(sX0, x, a.ldx, m0, a.M - 1, 0, wave, lane);
-    load_operand(sW0, w, a.ldw, n0, a.N - 1, 0, wave, lane);
-    load_operand(sX1, x, a.ldx, m0, a.M - 1, min(1, nk - 1) * kTK, wave, lane);
-    load_operand(sW1, w, a.ldw, n0, a.N - 1, min(1, nk - 1) * kTK, wave, lane);
-    load_operand(sX2, x, a.ldx, m0, a.M - 1, min(2, nk - 1) * kTK, wave, lane);
-    load_operand(sW2, w, a.ldw, n0, a.N - 1, min(2, nk - 1) * kTK, wave, lane);
+    const int nk = nk_of(a);
     const int r32 = lane & 31, h = lane >> 5;
-    for (int kt = 0; kt < nk; kt += kNS) {
-        PRIME_TILE_STEP(kt, sX0, sW0, sX3, sW3)
-        PRIME_TILE_STEP(kt + 1, sX1, sW1, sX0, sW0)
-        PRIME_TILE_STEP(kt + 2, sX2, sW2, sX1, sW1)
-        PRIME_TILE_STEP(kt + 3, sX3, sW3, sX2, sW2)
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
-#undef PRIME_TILE_STEP
-
-    // ---- epilogue: lane holds y[m][n .. n+3] per register quad
-    uint16_t *y = static_cast<uint16_t *>(a.y);
-    const uint16_t *r = static_cast<const uint16_t *>(a.r);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 128 * wm + 32 * i + r32;
-        if (m >= a.M) continue;
+    for (int b = 0; b < kNS; ++b) issue(b, b);
+    asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
+    Frags fa, fb;
+    read_frags(fa, sx(0), sw(0), wm, wn, r32, h);
+    for (int kt = 0; kt < nk; kt += 2) {
+        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+        issue(kt + kNS, kt & (kNS - 1));
+        read_frags(fb, sx((kt + 1) & (kNS - 1)), sw((kt + 1) & (kNS - 1)), wm, wn, r32, h);
+        // (the scheduler would otherwise sink the reads next to their MFMAs)
+        __builtin_amdgcn_sched_barrier(0);
+        mma_frags(acc, fa);
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+        issue(kt + 1 + kNS, (kt + 1) & (kNS - 1));
+        read_frags(fa, sx((kt + 2) & (kNS - 1)), sw((kt + 2) & (kNS - 1)), wm, wn, r32, h);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_frags(acc, fb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // every load into LDS has landed and every wave is done with the stages
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // ---- epilogue: the products, rounded to bf16, through LDS (the wave's
+    // quadrant in 32 KB of the stages), then row segments of 8 columns per
+    // lane: 4 rows x 256 contiguous bytes per store instruction
+    uint16_t *ep = sbuf + wave * (128 * 128);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int tq = 0; tq < 4; ++tq) {
-                const int n = n0 + 128 * wn + 32 * j + 8 * tq + 4 * h;
-                float o[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = round_bf16(acc[i][j][4 * tq + e]);
-                if (a.epilogue == PRIME_EPILOGUE_GELU) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = gelu_exact(o[e]);
-                } else if (a.epilogue == PRIME_EPILOGUE_RESIDUAL) {
-                    const uint2 rv = *reinterpret_cast<const uint2 *>(r + static_cast<int64_t>(m) * a.ldr + n);
-                    o[0] += __uint_as_float(rv.x << 16);
-                    o[1] += __uint_as_float(rv.x & 0xFFFF0000u);
-                    o[2] += __uint_as_float(rv.y << 16);
-                    o[3] += __uint_as_float(rv.y & 0xFFFF0000u);
-                }
-                *reinterpret_cast<uint2 *>(y + static_cast<int64_t>(m) * a.ldy + n) =
-                    uint2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+                const int row = 32 * i + r32, col = 32 * j + 8 * tq + 4 * h;
+                *reinterpret_cast<uint2 *>(ep + ep_off(row, col)) =
+                    uint2{pack2(acc[i][j][4 * tq], acc[i][j][4 * tq + 1]),
+                          pack2(acc[i][j][4 * tq + 2], acc[i][j][4 * tq + 3])};
             }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave reads back only its own rows
+    uint16_t *y = static_cast<uint16_t *>(a.y);
+    const uint16_t *r = static_cast<const uint16_t *>(a.r);
+    const int gcol = 8 * (lane & 15);
+#pragma unroll 4
+    for (int it = 0; it < 32; ++it) {
+        const int row = 4 * it + (lane >> 4);
+        const int m = m0 + 128 * wm + row, n = n0 + 128 * wn + gcol;
+        if (m >= a.M) continue;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(ep + ep_off(row, gcol));
+        u32x4 o = v;
+        if (a.epilogue == PRIME_EPILOGUE_GELU) {
+            float f[8];
+            unpack8(v, f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = gelu_exact(f[e]);
+            o = pack8(f);
+        } else if (a.epilogue == PRIME_EPILOGUE_RESIDUAL) {
+            float f[8], g[8];
+            unpack8(v, f);
+            unpack8(*reinterpret_cast<const u32x4 *>(r + static_cast<int64_t>(m) * a.ldr + n), g);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] += g[e];
+            o = pack8(f);
+        }
+        *reinterpret_cast<u32x4 *>(y + static_cast<int64_t>(m) * a.ldy + n) = o;
     }
 }
 
 bool linear_tile_fits(const LinearArgs &a) {
-    return a.M >= kTM && a.N % kTN == 0 && a.K % kTK == 0;
+    return a.M >= kTM && a.N % kTN == 0 && a.K % (2 * kTK) == 0;  // K blocks in pairs
 }
 
 hipError_t launch_linear_tile(const LinearArgs &a, hipStream_t stream) {
