@@ -8,11 +8,13 @@
 //   readout waves 0..7 only compute, each for one query block and half of the
 //     value columns: score block, AV, state readout, y;
 //   update waves 8..15 own the state M = [S1; S2/2 | K] in MFMA accumulators,
-//     one feature block each, and, in the step of chunk c, (a) add chunk c's
-//     contribution, (b) convert and store chunk c+1's tiles (loaded from HBM one
-//     chunk earlier) into the other tile buffer, (c) issue the HBM loads of chunk
-//     c+2 and (d) publish the bf16 state copy entering chunk c+1 into the other
-//     state buffer.
+//     one feature block each, and, in the step of chunk c, (a) convert and
+//     store chunk c+1's tiles (loaded from HBM one chunk earlier) into the other
+//     tile buffer, (b) issue the HBM loads of chunk c+2, (c) add chunk c's
+//     contribution and (d) publish the bf16 state copy entering chunk c+1 into
+//     the other state buffer.  (Timestamps per phase show the update waves as
+//     the critical path -- the readout waves wait at the barrier -- and (a)
+//     first lets the conversion overlap the readout waves' first phase.)
 // Chunk c reads tile buffer c&1 and state buffer c&1 while chunk c+1's are
 // written, so one barrier per chunk orders every hazard.  S0 also accumulates
 // on MFMA: update wave u multiplies value block u of [w v] by an A operand whose
@@ -596,6 +598,16 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
         {
             // ---- state update: st = l^n st + [k; k*k/2]^T [w v | w];  S0 on the ones row
             const float ln = SEL ? sel_ln : sPw[nvalid];  // selective: set when chunk c was stored
+            const float sw = SEL ? sel_sw : sPs[nvalid];
+            const bool more = c + 1 < c_end;
+            if constexpr (!STATE_ONLY) {
+                // chunk c+1's tiles first (into the other buffer, which no wave
+                // reads in this step): this conversion and its LDS stores then
+                // overlap the readout waves' first phase instead of following
+                // the update's MFMAs, and the HBM loads of chunk c+2 go out early
+                if (more) store_tiles(c + 1, xq);
+                load_tiles<STATE_ONLY, SEL, UW8>(T, a, qp, kp, vp, ldp, c + 2, ra, lane);
+            }
 #pragma unroll
             for (int fi = 0; fi < FI; ++fi)
 #pragma unroll
@@ -603,7 +615,7 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
 #pragma unroll
                     for (int r = 0; r < 4; ++r) st[fi][nb][r] *= ln;
             s0t[0] *= ln;
-            k0 = ln * k0 + (SEL ? sel_sw : sPs[nvalid]);
+            k0 = ln * k0 + sw;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 // register t of both operands <-> token 32ks + 16(t/4) + 4g + t%4
@@ -632,10 +644,11 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
                     default: s0t = mfma(ones, vop[3].h, s0t); break;
                 }
             }
-            const bool more = c + 1 < c_end;
-            if constexpr (STATE_ONLY) __syncthreads();  // every wave has read the single tile buffer
-            if (more) store_tiles(c + 1, xq);
-            load_tiles<STATE_ONLY, SEL, UW8>(T, a, qp, kp, vp, ldp, c + 2, ra, lane);
+            if constexpr (STATE_ONLY) {
+                __syncthreads();  // every wave has read the single tile buffer
+                if (more) store_tiles(c + 1, xq);
+                load_tiles<STATE_ONLY, SEL, UW8>(T, a, qp, kp, vp, ldp, c + 2, ra, lane);
+            }
             if (more) publish_state(xq);
         }
         __syncthreads();
