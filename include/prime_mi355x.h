@@ -140,8 +140,12 @@ int prime_add_rmsnorm(void *x, const void *delta, const void *weight, void *out,
  *   workspace: optional device scratch of workspace_bytes (16-byte aligned).
  *              With at least prime_chunked_prefill_workspace_size() bytes the
  *              sequences are split into segments that run in parallel (a
- *              carried-state scan between them); with less (or NULL) each
- *              sequence runs as one segment.  Results agree either way.
+ *              carried-state scan between them) when there are fewer of them
+ *              than CUs, or, with more, some run as two halves, the second
+ *              starting from the first's end state handed over through the
+ *              workspace (bit-identical); with less (or NULL) each sequence
+ *              runs as one segment.  Results agree either way.  Calls that
+ *              overlap in time must not share a workspace.
  */
 int prime_chunked_prefill(const prime_tensor_t *q, const prime_tensor_t *k,
                           const prime_tensor_t *v, int B, int H, int H_kv, int L, int D,
@@ -246,14 +250,14 @@ int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int
                          void *stream);
 
 /*
- * Linear layer of the decode step, y = epilogue(x w^T) (F.linear without bias;
- * model.py:59-68, 101-118, 160 at one token per sequence): x [M, K], w [N, K],
- * y [M, N], all BF16, row strides ldx, ldw, ldy in elements; fp32
- * accumulation, one rounding to bf16.  Epilogues: PRIME_EPILOGUE_NONE, or
- * PRIME_EPILOGUE_GELU = the exact GELU 0.5 t (1 + erf(t / sqrt 2)) of
- * F.gelu.  Built for few rows (M up to a few hundred: decode batches), where
- * library GEMMs are latency-bound.  K a multiple of 64; N a multiple of 4;
- * x, w rows 16-byte aligned, y rows 8-byte aligned; y may not overlap x or w.
+ * Linear layer of the PRIME blocks, y = epilogue(x w^T) (F.linear without
+ * bias; model.py:59-68, 101-118, 160): x [M, K], w [N, K], y [M, N], all
+ * BF16, row strides ldx, ldw, ldy in elements; fp32 accumulation, one
+ * rounding to bf16.  Epilogues: PRIME_EPILOGUE_NONE, or PRIME_EPILOGUE_GELU =
+ * the exact GELU 0.5 t (1 + erf(t / sqrt 2)) of F.gelu.  Few rows (decode
+ * batches) run a skinny kernel; M >= 2048 with N a multiple of 256 a
+ * 256 x 256-tile kernel.  K a multiple of 64; N a multiple of 4; x, w rows
+ * 16-byte aligned, y rows 8-byte aligned; y may not overlap x or w.
  */
 #define PRIME_EPILOGUE_NONE 0
 #define PRIME_EPILOGUE_GELU 1
