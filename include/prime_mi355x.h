@@ -277,6 +277,24 @@ int prime_linear_residual(const void *x, const void *w, const void *r, void *y, 
                           int64_t ldx, int64_t ldw, int64_t ldr, int64_t ldy, int dtype, void *stream);
 
 /*
+ * A decode-step projection with the passes around it folded in (model.py:
+ * 47-56, 59-68, 107-118 at one token per sequence): y = epilogue(s_m x w^T),
+ * where s_m = rsqrt(mean_k x[m,k]^2 + rms_eps) when rms_eps > 0 (the RMSNorm
+ * before the projection; pass w with the norm's weight already multiplied
+ * into its columns, w' = w diag(g)) and 1 otherwise; the product (times s_m)
+ * is rounded to bf16, then the epilogue: PRIME_EPILOGUE_NONE, _GELU (exact)
+ * or _RESIDUAL (y = r + product; r may be y, with the same row stride).
+ * BF16; M up to 1024 rows (decode batches); N a multiple of 32, K of 128;
+ * x, w rows 16-byte aligned, y and r rows 8-byte aligned.  With the RMS
+ * prologue K is the normalised width (the hidden size).  The norm's output
+ * is not rounded on its own, unlike RMSNorm followed by F.linear; the
+ * difference is within a bf16 rounding of each product.
+ */
+int prime_linear_fused(const void *x, const void *w, const void *r, void *y, int M, int N, int K, int64_t ldx,
+                       int64_t ldw, int64_t ldr, int64_t ldy, int dtype, int epilogue, float rms_eps,
+                       void *stream);
+
+/*
  * Selective PRIME (PrimeSelectiveMomentAttention, selective.py:264-444): the
  * same moment recurrence with a decay per token and per head,
  *   l_t = exp(-Delta_t / tau_h)  (Delta_t = softplus(W_delta x_t + b), clamped),

@@ -290,6 +290,36 @@ int prime_linear_residual(const void *x, const void *w, const void *r, void *y, 
     return check_hip(prime::launch_linear(a, static_cast<hipStream_t>(stream)), "linear launch");
 }
 
+int prime_linear_fused(const void *x, const void *w, const void *r, void *y, int M, int N, int K, int64_t ldx,
+                       int64_t ldw, int64_t ldr, int64_t ldy, int dtype, int epilogue, float rms_eps,
+                       void *stream) {
+    g_err[0] = 0;
+    int rc;
+    if ((rc = linear_checks("prime_linear_fused", x, w, y, M, N, K, ldx, ldw, ldy, dtype))) return rc;
+    if (epilogue != PRIME_EPILOGUE_NONE && epilogue != PRIME_EPILOGUE_GELU && epilogue != PRIME_EPILOGUE_RESIDUAL)
+        return fail(PRIME_ERR_INVALID_ARG, "unknown epilogue %d", epilogue);
+    if (M > 1024 || N % 32 || K % 128)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_linear_fused: M <= 1024, N a multiple of 32, K of 128 (M=%d N=%d K=%d)",
+                    M, N, K);
+    if (!(rms_eps >= 0.f)) return fail(PRIME_ERR_INVALID_ARG, "prime_linear_fused: rms_eps must be >= 0");
+    if (epilogue == PRIME_EPILOGUE_RESIDUAL) {
+        if (!r) return fail(PRIME_ERR_INVALID_ARG, "prime_linear_fused: null r");
+        if (ldr < N) return fail(PRIME_ERR_INVALID_ARG, "r row stride below the row length");
+        if ((reinterpret_cast<uintptr_t>(r) & 7) || (ldr % 4))
+            return fail(PRIME_ERR_MISALIGNED, "r rows must start on 8-byte boundaries");
+        const size_t nr = static_cast<size_t>((M - 1) * ldr + N) * 2, ny = static_cast<size_t>((M - 1) * ldy + N) * 2;
+        if (!(r == y && ldr == ldy) && overlap(r, nr, y, ny))
+            return fail(PRIME_ERR_ALIAS, "r overlaps y (only r == y with the same row stride is allowed)");
+        const size_t nx = static_cast<size_t>((M - 1) * ldx + K) * 2;
+        if (overlap(r, nr, x, nx) && r != y) return fail(PRIME_ERR_ALIAS, "r overlaps x");
+    }
+    prime::LinearArgs a{};
+    a.x = x; a.w = w; a.y = y; a.r = r; a.ldx = ldx; a.ldw = ldw; a.ldy = ldy; a.ldr = ldr;
+    a.M = M; a.N = N; a.K = K; a.epilogue = epilogue;
+    a.rms = rms_eps > 0.f ? 1 : 0; a.rms_eps = rms_eps;
+    return check_hip(prime::launch_linear_rows(a, static_cast<hipStream_t>(stream)), "linear launch");
+}
+
 int prime_argmax(const void *logits, int dtype, int n, int vocab, int64_t stride_n, int64_t *out, void *stream) {
     g_err[0] = 0;
     if (!logits || !out) return fail(PRIME_ERR_INVALID_ARG, "prime_argmax: null argument");

@@ -1,0 +1,206 @@
+// Projections of the decode step on gfx950 (model.py:59-68, 101-118, 160 at one
+// token per sequence): y[M, N] = epilogue(rowscale * x[M, K] . w[N, K]^T) for a
+// few hundred rows, bf16 in and out, fp32 accumulation.  The element-wise
+// passes around each projection of the block fold into it:
+//   RMS (rms_eps > 0):       y = (x . w'^T) * rsqrt(mean_k x^2 + eps) per row --
+//     the RMSNorm before the projection, with its weight pre-multiplied into
+//     the columns of w (w' = w diag(g)); the norm's output is then never
+//     rounded on its own;
+//   PRIME_EPILOGUE_GELU:     the exact GELU of the rounded product;
+//   PRIME_EPILOGUE_RESIDUAL: y = r + rounded product (r may be y).
+//
+// With M a few hundred the weights are the only large stream, read once per
+// call from HBM, and the kernel is bound by memory latency.  One workgroup of
+// 4 waves owns 64 rows x BN columns (BN = 64 or 32) over the whole of K;
+// wave w owns rows 16w .. 16w+15 and all BN columns as BN / 16
+// v_mfma_f32_16x16x32_bf16 tiles, with w as the A operand so that a lane's
+// register quad holds four consecutive columns of one row (one 8-byte store).
+// K runs in blocks of 64 through four LDS stages, three blocks ahead, filled
+// by global_load_lds_dwordx4 (one wave instruction moves 8 rows x 128 bytes;
+// 16-byte segments XOR-swizzled by row & 7 on the global side, so the
+// ds_read_b128 operand reads of 8 consecutive rows are conflict-free).  The
+// row sums of squares of the RMS prologue come from the x operands the wave
+// reads anyway (lane group g holds k-slots 8g..8g+7 of every 32-wide step;
+// the four groups are summed at the end).
+
+#include "prefill_common.h"
+
+namespace prime {
+namespace {
+
+constexpr int kRM = 64, kRK = 64, kRNS = 4;  // rows per workgroup, K block, LDS stages
+
+// Direct-to-LDS load of `rows` tile rows (a multiple of 8) starting at tile row
+// t0: instruction i covers tile rows t0 + 8 i .. +7; lane l lands at LDS segment
+// l % 8 of row l / 8 and loads the global segment that belongs there.
+// Source rows past rmax re-read row rmax (never stored).
+__device__ __forceinline__ void rows_dma(uint16_t *stage, const uint16_t *src, int64_t ld, int r0, int rmax, int t0,
+                                         int n, int k0, int lane) {
+    for (int i = 0; i < n; ++i) {
+        const int rr = t0 + 8 * i + (lane >> 3);
+        const int seg = (lane & 7) ^ (rr & 7);
+        const int row = min(r0 + rr, rmax);
+        const uint16_t *g = src + static_cast<int64_t>(row) * ld + k0 + 8 * seg;
+        const uint32_t l = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(stage + (t0 + 8 * i) * kRK));
+        // asm: the compiler does not track these loads; the K loop's explicit
+        // vmcnt waits are the only ones (see gemm_tile.hip).  M0 is set here
+        // for each instruction; no compiler-generated code in this kernel uses it.
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(l) : "memory", "m0");
+    }
+}
+
+__device__ __forceinline__ bf16x8 rfrag(const uint16_t *stage, int row, int seg) {
+    return as_bf16x8(*reinterpret_cast<const u32x4 *>(stage + row * kRK + 8 * (seg ^ (row & 7))));
+}
+
+__device__ __forceinline__ float sumsq8(bf16x8 v) {
+    const u32x4 u = __builtin_bit_cast(u32x4, v);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float lo = __uint_as_float(u[i] << 16), hi = __uint_as_float(u[i] & 0xFFFF0000u);
+        s = fmaf(lo, lo, s);
+        s = fmaf(hi, hi, s);
+    }
+    return s;
+}
+
+__device__ __forceinline__ float gelu_erf_r(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+
+__device__ __forceinline__ float bf16r(float x) { return bf16_bits_to_f32(f32_to_bf16_bits(x)); }
+
+}  // namespace
+
+// One K block per step: wait for this thread's loads of block kt+1 (the two
+// later blocks' may still be in flight) and for its LDS reads (block kt's
+// fragments, read one step earlier, must have returned before another wave
+// overwrites their stage), barrier, issue block kt+4 into kt's stage, read
+// kt+1's fragments, run kt's MFMAs.
+template <int BN, bool RMS, int EPI>
+__global__ __launch_bounds__(256) void linear_rows_kernel(const LinearArgs a) {
+    constexpr int NT = BN / 16;                         // n tiles per wave
+    constexpr int XS = kRM * kRK, WS = BN * kRK;        // stage sizes (elements)
+    constexpr int LPS = 2 + BN / 32;                    // loads per thread per stage
+    __shared__ __attribute__((aligned(1024))) uint16_t sbuf[kRNS * (XS + WS)];
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * kRM;
+    const uint16_t *x = static_cast<const uint16_t *>(a.x), *w = static_cast<const uint16_t *>(a.w);
+    const int nk = a.K / kRK;
+    auto sx = [&](int st) { return sbuf + st * (XS + WS); };
+    auto sw = [&](int st) { return sbuf + st * (XS + WS) + XS; };
+    auto issue = [&](int kb, int st) {
+        const int k0 = min(kb, nk - 1) * kRK;
+        rows_dma(sx(st), x, a.ldx, m0, a.M - 1, 16 * wave, 2, k0, lane);
+        rows_dma(sw(st), w, a.ldw, n0, a.N - 1, (BN / 4) * wave, BN / 32, k0, lane);
+    };
+    struct Fr {
+        bf16x8 x[2], w[2][NT];
+    };
+    auto read = [&](Fr &f, int st) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            f.x[s] = rfrag(sx(st), 16 * wave + l16, g + 4 * s);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) f.w[s][j] = rfrag(sw(st), 16 * j + l16, g + 4 * s);
+        }
+    };
+    f32x4 acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ss = 0.f;
+    auto mma = [&](const Fr &f) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j) acc[j] = mfma(f.w[s][j], f.x[s], acc[j]);
+            if constexpr (RMS) ss += sumsq8(f.x[s]);
+        }
+    };
+
+#pragma unroll
+    for (int b = 0; b < kRNS; ++b) issue(b, b);
+    if constexpr (LPS == 4) asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(9) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    Fr fa, fb;
+    read(fa, 0);
+    for (int kt = 0; kt < nk; kt += 2) {
+        // (nk is even: K a multiple of 128)
+        if constexpr (LPS == 4) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        issue(kt + kRNS, kt & (kRNS - 1));
+        read(fb, (kt + 1) & (kRNS - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fa);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (LPS == 4) asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        issue(kt + 1 + kRNS, (kt + 1) & (kRNS - 1));
+        read(fa, (kt + 2) & (kRNS - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no load into LDS outlives the workgroup
+
+    // ---- epilogue: lane holds y[m][n .. n+3], m = m0 + 16 wave + l16, n = n0 + 16 j + 4 g
+    const int m = m0 + 16 * wave + l16;
+    float rs = 1.0f;
+    if constexpr (RMS) {
+        ss += __shfl_xor(ss, 16, kWave);
+        ss += __shfl_xor(ss, 32, kWave);
+        rs = rsqrtf(ss / static_cast<float>(a.K) + a.rms_eps);
+    }
+    if (m >= a.M) return;
+    uint16_t *y = static_cast<uint16_t *>(a.y);
+    const uint16_t *r = static_cast<const uint16_t *>(a.r);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int n = n0 + 16 * j + 4 * g;
+        if (n >= a.N) continue;
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = bf16r(acc[j][e] * rs);
+        if constexpr (EPI == PRIME_EPILOGUE_GELU) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = gelu_erf_r(o[e]);
+        } else if constexpr (EPI == PRIME_EPILOGUE_RESIDUAL) {
+            const uint2 rv = *reinterpret_cast<const uint2 *>(r + static_cast<int64_t>(m) * a.ldr + n);
+            o[0] += __uint_as_float(rv.x << 16);
+            o[1] += __uint_as_float(rv.x & 0xFFFF0000u);
+            o[2] += __uint_as_float(rv.y << 16);
+            o[3] += __uint_as_float(rv.y & 0xFFFF0000u);
+        }
+        *reinterpret_cast<uint2 *>(y + static_cast<int64_t>(m) * a.ldy + n) = uint2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+    }
+}
+
+bool linear_rows_fits(const LinearArgs &a) { return a.N % 32 == 0 && a.K % (2 * kRK) == 0; }
+
+template <int BN, bool RMS>
+static void launch_rows_epi(const LinearArgs &a, hipStream_t stream) {
+    const dim3 grid(a.N / BN, (a.M + kRM - 1) / kRM), block(256);
+    if (a.epilogue == PRIME_EPILOGUE_GELU)
+        hipLaunchKernelGGL((linear_rows_kernel<BN, RMS, PRIME_EPILOGUE_GELU>), grid, block, 0, stream, a);
+    else if (a.epilogue == PRIME_EPILOGUE_RESIDUAL)
+        hipLaunchKernelGGL((linear_rows_kernel<BN, RMS, PRIME_EPILOGUE_RESIDUAL>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((linear_rows_kernel<BN, RMS, PRIME_EPILOGUE_NONE>), grid, block, 0, stream, a);
+}
+
+// 64-column tiles when they give at least one workgroup per CU, else 32.
+hipError_t launch_linear_rows(const LinearArgs &a, hipStream_t stream) {
+    const int64_t wg64 = static_cast<int64_t>((a.M + kRM - 1) / kRM) * (a.N / 64);
+    const bool wide = a.N % 64 == 0 && wg64 >= 128;
+    if (a.rms) {
+        if (wide) launch_rows_epi<64, true>(a, stream);
+        else launch_rows_epi<32, true>(a, stream);
+    } else {
+        if (wide) launch_rows_epi<64, false>(a, stream);
+        else launch_rows_epi<32, false>(a, stream);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace prime

@@ -118,10 +118,12 @@ __device__ __forceinline__ int ep_off(int row, int col) {
 
 // K loop.  Four LDS stages hold K blocks kt+1 .. kt+3 while block kt is
 // multiplied from registers: the step of block kt waits for its own loads of
-// block kt+1, meets the barrier (after which every thread's loads of kt+1
-// have landed and every wave has read block kt's fragments, so kt's stage is
-// free), issues block kt+4 into that stage, reads block kt+1's fragments into
-// the other register set and runs block kt's MFMAs.  The barriers are asm
+// block kt+1 and for its own LDS reads (block kt's fragments, issued one step
+// earlier: they must have returned before another wave overwrites their
+// stage), meets the barrier (after which every thread's loads of kt+1 have
+// landed and kt's stage is free), issues block kt+4 into that stage, reads
+// block kt+1's fragments into the other register set and runs block kt's
+// MFMAs.  The barriers are asm
 // statements (compiler memory barriers), not __syncthreads(), whose fence
 // would make the compiler wait for loads it does not know about anyway.
 __global__ __launch_bounds__(256, 1) void linear_tile_kernel(const LinearArgs a) {
@@ -157,18 +159,18 @@ __global__ __launch_bounds__(256, 1) void linear_tile_kernel(const LinearArgs a)
     const int r32 = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int b = 0; b < kNS; ++b) issue(b, b);
-    asm volatile("s_waitcnt vmcnt(24)\n\ts_barrier" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     Frags fa, fb;
     read_frags(fa, sx(0), sw(0), wm, wn, r32, h);
     for (int kt = 0; kt < nk; kt += 2) {
-        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         issue(kt + kNS, kt & (kNS - 1));
         read_frags(fb, sx((kt + 1) & (kNS - 1)), sw((kt + 1) & (kNS - 1)), wm, wn, r32, h);
         // (the scheduler would otherwise sink the reads next to their MFMAs)
         __builtin_amdgcn_sched_barrier(0);
         mma_frags(acc, fa);
         __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         issue(kt + 1 + kNS, (kt + 1) & (kNS - 1));
         read_frags(fa, sx((kt + 2) & (kNS - 1)), sw((kt + 2) & (kNS - 1)), wm, wn, r32, h);
         __builtin_amdgcn_sched_barrier(0);

@@ -77,8 +77,13 @@ struct LinearArgs {
     int M, N, K, epilogue;
     const void *r;          // PRIME_EPILOGUE_RESIDUAL: y = r + x w^T (r may be y)
     int64_t ldr;
+    int rms;                // rows scaled by rsqrt(mean_k x^2 + rms_eps) before the epilogue
+    float rms_eps;
 };
 hipError_t launch_linear(const LinearArgs &a, hipStream_t stream);
+// few-row kernel with the RMS prologue (gemm_rows.hip): N % 32 == 0, K % 128 == 0
+bool linear_rows_fits(const LinearArgs &a);
+hipError_t launch_linear_rows(const LinearArgs &a, hipStream_t stream);
 // 256 x 256-tile kernel for many rows (gemm_tile.hip): M >= 256, N % 256 == 0, K % 64 == 0
 bool linear_tile_fits(const LinearArgs &a);
 hipError_t launch_linear_tile(const LinearArgs &a, hipStream_t stream);

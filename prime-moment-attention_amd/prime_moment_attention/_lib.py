@@ -26,7 +26,7 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
            "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
            "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_argmax",
-           "prime_head_layernorm", "prime_linear", "prime_linear_residual", "prime_selective_prefill",
+           "prime_head_layernorm", "prime_linear", "prime_linear_residual", "prime_linear_fused", "prime_selective_prefill",
            "prime_selective_decode_step", "prime_accumulate", "prime_accumulate_workspace_size",
            "prime_decode_readout", "prime_decode_update", "prime_chunked_prefill_backward",
            "prime_chunked_prefill_backward_workspace_size", "prime_chunked_prefill_qknorm",
@@ -116,6 +116,9 @@ def load() -> ctypes.CDLL:
     L.prime_linear.restype = ctypes.c_int
     L.prime_linear_residual.argtypes = [fp] * 4 + [ctypes.c_int] * 3 + [ctypes.c_int64] * 4 + [ctypes.c_int, fp]
     L.prime_linear_residual.restype = ctypes.c_int
+    L.prime_linear_fused.argtypes = [fp] * 4 + [ctypes.c_int] * 3 + [ctypes.c_int64] * 4 + [ctypes.c_int] * 2 + [
+        ctypes.c_float, fp]
+    L.prime_linear_fused.restype = ctypes.c_int
     L.prime_selective_prefill.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 5 + [
         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, P(PrimeState), P(PrimeTensor), P(PrimeState),
         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
@@ -360,7 +363,7 @@ def head_layernorm(x: torch.Tensor, out: torch.Tensor, norm: Optional[torch.nn.L
     _check(rc, "prime_head_layernorm")
 
 
-EPILOGUE_NONE, EPILOGUE_GELU = 0, 1
+EPILOGUE_NONE, EPILOGUE_GELU, EPILOGUE_RESIDUAL = 0, 1, 2
 
 
 def _linear_checks(x, w, out, who):
@@ -401,6 +404,28 @@ def linear_residual(x: torch.Tensor, w: torch.Tensor, r: torch.Tensor, out: torc
                                       x.stride(0), w.stride(0), r.stride(0), out.stride(0),
                                       _DTYPES[torch.bfloat16], _stream(x.device))
     _check(rc, "prime_linear_residual")
+    return out
+
+
+def linear_fused(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor, epilogue: int = EPILOGUE_NONE,
+                 rms_eps: float = 0.0, r: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """prime_linear_fused: out = epilogue(s * x @ w.T) for a few hundred bf16
+    rows, s = rsqrt(mean(x^2) + rms_eps) per row when rms_eps > 0 (w carrying
+    the RMSNorm weight in its columns), epilogue NONE, GELU or RESIDUAL
+    (out = r + product; r may be out)."""
+    M, N, K = _linear_checks(x, w, out, "prime_linear_fused")
+    if epilogue == EPILOGUE_RESIDUAL:
+        if r is None:
+            raise ValueError("the residual epilogue needs r")
+        _dev_check(r)
+        if r.shape != (M, N) or r.dtype != torch.bfloat16 or r.stride(1) != 1:
+            raise ValueError("r must be a bf16 [M, N] tensor with a contiguous last dimension")
+    rp = r.data_ptr() if r is not None else None
+    rc = load().prime_linear_fused(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(rp),
+                                   ctypes.c_void_p(out.data_ptr()), M, N, K, x.stride(0), w.stride(0),
+                                   r.stride(0) if r is not None else N, out.stride(0), _DTYPES[torch.bfloat16],
+                                   int(epilogue), float(rms_eps), _stream(x.device))
+    _check(rc, "prime_linear_fused")
     return out
 
 

@@ -320,6 +320,17 @@ class _LayerStep:
         else:
             self.decay = _lib.decay_tensor(at.decay, at.num_heads, device)
             self.sel = None
+        # the folded form (base attention, GELU MLP, bf16): each RMSNorm's weight
+        # multiplied into the columns of the projection after it, so that the
+        # projection kernel applies the norm as a per-row scale (prime_linear_fused)
+        self.qkv_g = self.up_g = None
+        if (self.sel is None and isinstance(layer.mlp, PrimeGeluMLP) and dtype == torch.bfloat16
+                and self.qkv.shape[1] % 128 == 0 and self.qkv.shape[0] % 32 == 0
+                and layer.mlp.up_proj.weight.shape[0] % 128 == 0):
+            g1 = layer.input_layernorm.weight.to(torch.float32)
+            g2 = layer.post_attention_layernorm.weight.to(torch.float32)
+            self.qkv_g = (self.qkv.to(torch.float32) * g1).to(dtype)
+            self.up_g = (layer.mlp.up_proj.weight.to(torch.float32) * g2).to(dtype)
 
 
 def _step_constants(model: "PrimeForCausalLM") -> List[_LayerStep]:
@@ -350,7 +361,14 @@ def _fused_step(model: "PrimeForCausalLM", tokens: torch.Tensor, states, consts:
     add_rmsnorm -> one stacked q/k/v GEMM -> the decode kernel with the QK-norm
     and 1/sqrt(D) inside (attention.py:96-143, or selective.py:384-409) -> o_proj
     -> add_rmsnorm -> MLP; each residual add is fused into the following RMSNorm
-    with the block's rounding.  Returns (logits [B, V], next states).
+    with the block's rounding.  For base attention with the GELU MLP in bf16
+    the folded form runs instead: per layer RMSNorm + stacked q/k/v as one
+    kernel (the norm's weight in the stacked weight's columns, its row scale
+    applied to the products), the decode kernel, o_proj + residual add as one
+    kernel, RMSNorm + up projection + GELU as one kernel, and down_proj with
+    its residual add in the library GEMM (beta = 1); the norms' outputs are
+    then not rounded on their own (prime_linear_fused).  Returns (logits
+    [B, V], next states).
 
     inplace: the kernels update `states` in place (every layer's state must be
     given).  Otherwise the states are functional, as in the reference: new
@@ -361,14 +379,22 @@ def _fused_step(model: "PrimeForCausalLM", tokens: torch.Tensor, states, consts:
     x = model.embed_tokens(tokens).reshape(-1, cfg.hidden_size)  # the residual stream, updated in place
     B = x.shape[0]
     dev = x.device
+    # folded form: RMSNorm -> projection and projection -> residual add /
+    # GELU as one kernel each (prime_linear_fused), the down projection's
+    # residual add in the library GEMM (beta = 1)
+    folded = B <= 1024 and all(c.qkv_g is not None for c in consts)
     pending = None
     next_states = []
     for i, (layer, c) in enumerate(zip(model.layers, consts)):
         at = layer.self_attn
         H, Hk, D = at.num_heads, at.num_kv_heads, at.head_dim
-        n1 = torch.empty_like(x)
-        _lib.add_rmsnorm(x, pending, layer.input_layernorm.weight, n1, layer.input_layernorm.eps)
-        qkv = _decode_linear(n1, c.qkv)
+        if folded:
+            qkv = _lib.linear_fused(x, c.qkv_g, torch.empty(B, c.qkv_g.shape[0], device=dev, dtype=x.dtype),
+                                    _lib.EPILOGUE_NONE, layer.input_layernorm.eps)
+        else:
+            n1 = torch.empty_like(x)
+            _lib.add_rmsnorm(x, pending, layer.input_layernorm.weight, n1, layer.input_layernorm.eps)
+            qkv = _decode_linear(n1, c.qkv)
         q = qkv[:, :H * D].view(B, H, D)
         k = qkv[:, H * D:(H + Hk) * D].view(B, Hk, D)
         v = qkv[:, (H + Hk) * D:].view(B, Hk, D)
@@ -391,6 +417,12 @@ def _fused_step(model: "PrimeForCausalLM", tokens: torch.Tensor, states, consts:
         else:
             _lib.decode_step_qknorm(q, k, v, c.decay, at.eps, c.norm, st_in, st_out, y)
         next_states.append(st_out)
+        if folded:
+            _lib.linear_fused(y.view(B, -1), at.o_proj.weight, x, _lib.EPILOGUE_RESIDUAL, 0.0, x)
+            t = _lib.linear_fused(x, c.up_g, torch.empty(B, c.up_g.shape[0], device=dev, dtype=x.dtype),
+                                  _lib.EPILOGUE_GELU, layer.post_attention_layernorm.eps)
+            x.addmm_(t, layer.mlp.down_proj.weight.t())
+            continue
         a = _decode_linear(y.view(B, -1), at.o_proj.weight)
         n2 = torch.empty_like(x)
         _lib.add_rmsnorm(x, a, layer.post_attention_layernorm.weight, n2, layer.post_attention_layernorm.eps)

@@ -75,3 +75,57 @@ def test_linear_residual_rejects_partial_overlap():
     buf = torch.empty(513, 768, device=dev(), dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="overlap"):
         _lib.linear_residual(x, w, buf[1:], buf[:512])
+
+
+# prime_linear_fused: the decode step's projections with the RMSNorm folded in
+# (model.py:47-56 then 59-68) and the GELU / residual epilogues
+FUSED = [(256, 2304, 768), (256, 768, 768), (256, 3072, 768), (256, 768, 3072), (37, 768, 768), (1000, 1536, 768),
+         (32, 50304, 768)]
+
+
+@pytest.mark.parametrize("M,N,K", FUSED)
+@pytest.mark.parametrize("epi", ["none", "gelu", "residual"])
+@pytest.mark.parametrize("rms", [True, False])
+def test_linear_fused_matches_fp32(M, N, K, epi, rms):
+    x, w = _operands(M, N, K, seed=M + N + K + (1 if rms else 0))
+    x = x * 3 + 0.5  # rows with their own scale, as the residual stream has
+    g = torch.Generator().manual_seed(N)
+    gamma = (1 + 0.2 * torch.randn(K, generator=g)).to(dev(), torch.bfloat16)
+    eps = 1e-6
+    wg = (w.float() * gamma.float()).to(torch.bfloat16) if rms else w  # the norm's weight in w's columns
+    ref = x.float() @ wg.float().T
+    if rms:
+        ref = ref * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + eps)
+    r = (torch.randn(M, N, generator=g) * 2).to(dev(), torch.bfloat16)
+    out = torch.empty(M, N, device=dev(), dtype=torch.bfloat16)
+    code = {"none": _lib.EPILOGUE_NONE, "gelu": _lib.EPILOGUE_GELU, "residual": _lib.EPILOGUE_RESIDUAL}[epi]
+    _lib.linear_fused(x, wg, out, code, eps if rms else 0.0, r if epi == "residual" else None)
+    if epi == "gelu":
+        ref = F.gelu(ref)
+    elif epi == "residual":
+        ref = r.float() + ref
+    torch.cuda.synchronize()
+    assert _rel(out, ref) < 8e-3, _rel(out, ref)
+    if rms and epi == "none":
+        # against the block's own two steps: RMSNorm (rounded) then the projection
+        n = torch.empty_like(x)
+        _lib.add_rmsnorm(x.contiguous(), None, gamma, n, eps)
+        assert _rel(out, F.linear(n, w)) < 1.5e-2
+
+
+def test_linear_fused_residual_in_place():
+    x, w = _operands(256, 768, 3072, seed=5)
+    r = torch.randn(256, 768, device=dev()).to(torch.bfloat16)
+    want = (r.float() + F.linear(x, w).float()).to(torch.bfloat16)
+    _lib.linear_fused(x, w, r, _lib.EPILOGUE_RESIDUAL, 0.0, r)
+    torch.cuda.synchronize()
+    assert _rel(r, want) < 8e-3
+
+
+def test_linear_fused_rejects_bad_shapes():
+    x, w = _operands(256, 768, 768, seed=1)
+    with pytest.raises(RuntimeError, match="multiple"):
+        _lib.linear_fused(x[:, :704], w[:, :704], torch.empty(256, 768, device=dev(), dtype=torch.bfloat16))
+    big = torch.empty(1025, 768, device=dev(), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="1024"):
+        _lib.linear_fused(big, w, torch.empty(1025, 768, device=dev(), dtype=torch.bfloat16))
