@@ -414,12 +414,15 @@ int prime_accumulate_noalloc(const prime_tensor_t *k, const prime_tensor_t *v, i
  * q (pre-scaled), k, v, decay, eps and state_in are the forward's arguments.
  * k/v must have one head per query head (H_kv == H: the reference module
  * expands grouped k/v before the recurrence, attention.py:92-94).  With
- * PRIME_FLAG_DENSE_CLAMP an incoming state is rejected; without one the two
- * clamps are the same.  BF16 inputs run on bf16 MFMA operands (fp32
+ * PRIME_FLAG_DENSE_CLAMP and an incoming state the derivative is that of the
+ * dense branch's double clamp (attention.py:177-185): the inner clamp gates
+ * the call's own tokens, the outer one the incoming state's term (without a
+ * state the two clamps are the same).  BF16 inputs run on bf16 MFMA operands (fp32
  * accumulation); F32 inputs run fp32 passes (fp32 MFMA operands throughout,
  * one workgroup per sequence, as the reference differentiates in fp32).
- * workspace (16-byte aligned): at least B*H*L*8 bytes
- * (per-token denominators); with prime_chunked_prefill_backward_workspace_size()
+ * workspace (16-byte aligned): at least B*H*L*8 bytes (per-token
+ * denominators; rounded up to 256), plus B*H*528 bytes for
+ * PRIME_FLAG_DENSE_CLAMP with a state; with prime_chunked_prefill_backward_workspace_size()
  * bytes, few long sequences are split into segments that run in parallel
  * (segment-entry states by the forward's state-only pass, dual states by a
  * reverse scan).  Results agree either way.

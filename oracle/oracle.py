@@ -62,6 +62,7 @@ def lib() -> ctypes.CDLL:
         L.oracle_selective_parallel.argtypes = [i, i, i, _dp, _dp, _dp, _dp, _dp, _dp, d] + [_dp] * 7
         L.oracle_recurrent_vjp.argtypes = [i, i, i, _dp, _dp, _dp, _dp, d] + [_dp] * 6 + [_dp] + [_dp] * 6 + [
             _dp] * 3 + [_dp] * 6
+        L.oracle_dense_vjp.argtypes = L.oracle_recurrent_vjp.argtypes
         f = ctypes.c_float
         L.baseline_decode_step.argtypes = [i, i, i, _fp, _fp, _fp, _fp, f] + [_fp] * 7 + [i]
         L.baseline_prefill.argtypes = [i, i, i, i, _fp, _fp, _fp, _fp, f] + [_fp] * 7 + [i]
@@ -173,6 +174,23 @@ def recurrent_vjp(q, k, v, lam, dy, eps=1.0, state=None, dstate=None):
                                *([_p(x) for x in si] if si else null), _p(dy),
                                *([_p(x) for x in so] if so else null), _p(dq), _p(dk), _p(dv),
                                *[_p(x) for x in ds])
+    return dq, dk, dv, ds
+
+
+def dense_vjp(q, k, v, lam, dy, eps=1.0, state=None, dstate=None):
+    """Reverse mode of the dense prefill branch with its double clamp
+    (attention.py:160-202); same arguments and results as recurrent_vjp."""
+    q, k, v, dy = _c64(q), _c64(k), _c64(v), _c64(dy)
+    BH, L, D = q.shape
+    si = None if state is None else _state_copy(state, BH, D)[0]
+    so = None if dstate is None else _state_copy(dstate, BH, D)[0]
+    dq, dk, dv = np.zeros_like(q), np.zeros_like(q), np.zeros_like(q)
+    ds = zero_state(BH, D)
+    null = [None] * 6
+    lib().oracle_dense_vjp(BH, L, D, _p(q), _p(k), _p(v), _p(_lam(lam, BH)), eps,
+                           *([_p(x) for x in si] if si else null), _p(dy),
+                           *([_p(x) for x in so] if so else null), _p(dq), _p(dk), _p(dv),
+                           *[_p(x) for x in ds])
     return dq, dk, dv, ds
 
 

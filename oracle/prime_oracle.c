@@ -757,3 +757,168 @@ void oracle_recurrent_vjp(int BH, int L, int D, const double *q, const double *k
     free(cur);
     free(dnum);
 }
+
+/* ------------------------------------------------------------------------- */
+/* Reverse mode of the dense prefill branch (attention.py:160-202) with its   */
+/* double clamp.  Per token t the call's own tokens give (readout of the      */
+/* call's state C_t, run from zero) num_c, den_c = sum_{j<=t} l^(t-j)         */
+/* (1 + q.k_j + 1/2 q^2.k_j^2); an incoming state S adds l^(t+1) times its    */
+/* readout (num_s, den_s):                                                    */
+/*   D1 = max(den_c, eps) (:177),  D = max(D1 + l^(t+1) den_s, eps) (:185),   */
+/*   y = (num_c + l^(t+1) num_s) / D   (without a state: D = D1).             */
+/* torch's clamps pass the gradient where their argument >= eps: the outer    */
+/* one gates dD, the inner one additionally gates what reaches den_c.  The    */
+/* terminal state (:189-202) is l^L S + C_(L-1), as for the recurrence.       */
+/* Same arguments and outputs as oracle_recurrent_vjp.                        */
+/* ------------------------------------------------------------------------- */
+void oracle_dense_vjp(int BH, int L, int D, const double *q, const double *k,
+                      const double *v, const double *lam, double eps,
+                      const double *S0i, const double *S1i, const double *S2i,
+                      const double *K0i, const double *K1i, const double *K2i,
+                      const double *dy, const double *dS0o, const double *dS1o,
+                      const double *dS2o, const double *dK0o, const double *dK1o,
+                      const double *dK2o, double *dq, double *dk, double *dv,
+                      double *dS0, double *dS1, double *dS2, double *dK0, double *dK1,
+                      double *dK2)
+{
+    const size_t DD = (size_t)D * D, NS = 2 * DD + 3 * (size_t)D + 1;
+    double *hist = (double *)malloc(sizeof(double) * NS * (size_t)(L > 0 ? L : 1));
+    double *cs = (double *)calloc(NS, sizeof(double));  /* the call's state */
+    double *ac = (double *)malloc(sizeof(double) * NS);  /* its adjoint */
+    double *nc = (double *)malloc(sizeof(double) * D), *ns = (double *)malloc(sizeof(double) * D);
+    double *gn = (double *)malloc(sizeof(double) * D);
+    for (int bh = 0; bh < BH; ++bh) {
+        const double l = lam[bh];
+        const int has = S0i != NULL;
+        const double *i0 = has ? S0i + (size_t)bh * D : NULL, *i1 = has ? S1i + (size_t)bh * DD : NULL;
+        const double *i2 = has ? S2i + (size_t)bh * DD : NULL, *ik1 = has ? K1i + (size_t)bh * D : NULL;
+        const double *ik2 = has ? K2i + (size_t)bh * D : NULL;
+        const double ik0 = has ? K0i[bh] : 0.0;
+        /* forward: the call's state after each token (layout s0 | s1 | s2 | k0 | k1 | k2) */
+        memset(cs, 0, sizeof(double) * NS);
+        double *c0 = cs, *c1 = cs + D, *c2 = c1 + DD, *ck0 = c2 + DD, *ck1 = ck0 + 1, *ck2 = ck1 + D;
+        for (int t = 0; t < L; ++t) {
+            const double *kt = k + ((size_t)bh * L + t) * D, *vt = v + ((size_t)bh * L + t) * D;
+            for (int j = 0; j < D; ++j) c0[j] = l * c0[j] + vt[j];
+            for (int i = 0; i < D; ++i)
+                for (int j = 0; j < D; ++j) {
+                    c1[IDX2(i, j, D)] = l * c1[IDX2(i, j, D)] + kt[i] * vt[j];
+                    c2[IDX2(i, j, D)] = l * c2[IDX2(i, j, D)] + kt[i] * kt[i] * vt[j];
+                }
+            *ck0 = l * (*ck0) + 1.0;
+            for (int i = 0; i < D; ++i) {
+                ck1[i] = l * ck1[i] + kt[i];
+                ck2[i] = l * ck2[i] + kt[i] * kt[i];
+            }
+            memcpy(hist + (size_t)t * NS, cs, sizeof(double) * NS);
+        }
+        /* adjoints: ac of the call's state after the current token (from dstate_out),
+           the incoming state's in the outputs (its readout terms, then l^L dstate_out) */
+        double *a0 = ac, *a1 = ac + D, *a2 = a1 + DD, *ak0 = a2 + DD, *ak1 = ak0 + 1, *ak2 = ak1 + D;
+        double *b0 = dS0 + (size_t)bh * D, *b1 = dS1 + (size_t)bh * DD, *b2 = dS2 + (size_t)bh * DD;
+        double *bk0 = dK0 + bh, *bk1 = dK1 + (size_t)bh * D, *bk2 = dK2 + (size_t)bh * D;
+        memset(ac, 0, sizeof(double) * NS);
+        memset(b0, 0, sizeof(double) * D); memset(b1, 0, sizeof(double) * DD);
+        memset(b2, 0, sizeof(double) * DD); *bk0 = 0.0;
+        memset(bk1, 0, sizeof(double) * D); memset(bk2, 0, sizeof(double) * D);
+        if (dS0o) {
+            memcpy(a0, dS0o + (size_t)bh * D, sizeof(double) * D);
+            memcpy(a1, dS1o + (size_t)bh * DD, sizeof(double) * DD);
+            memcpy(a2, dS2o + (size_t)bh * DD, sizeof(double) * DD);
+            *ak0 = dK0o[bh];
+            memcpy(ak1, dK1o + (size_t)bh * D, sizeof(double) * D);
+            memcpy(ak2, dK2o + (size_t)bh * D, sizeof(double) * D);
+        }
+        for (int t = L - 1; t >= 0; --t) {
+            const double *h = hist + (size_t)t * NS;
+            const double *h0 = h, *h1 = h + D, *h2 = h1 + DD, *hk0 = h2 + DD, *hk1 = hk0 + 1, *hk2 = hk1 + D;
+            const double *qt = q + ((size_t)bh * L + t) * D, *kt = k + ((size_t)bh * L + t) * D;
+            const double *vt = v + ((size_t)bh * L + t) * D, *gy = dy + ((size_t)bh * L + t) * D;
+            double *gq = dq + ((size_t)bh * L + t) * D, *gk = dk + ((size_t)bh * L + t) * D;
+            double *gv = dv + ((size_t)bh * L + t) * D;
+            const double w = has ? pow(l, t + 1) : 0.0;
+            double den_c, den_s = 0.0;
+            state_readout(D, qt, h0, h1, h2, *hk0, hk1, hk2, nc, &den_c);
+            if (has) state_readout(D, qt, i0, i1, i2, ik0, ik1, ik2, ns, &den_s);
+            const double d1 = den_c < eps ? eps : den_c;
+            const double dsum = has ? d1 + w * den_s : den_c;
+            const double Dt = dsum < eps ? eps : dsum;
+            double dot = 0.0;
+            for (int j = 0; j < D; ++j) {
+                const double num = nc[j] + (has ? w * ns[j] : 0.0);
+                dot += gy[j] * num / Dt;
+                gn[j] = gy[j] / Dt;
+            }
+            const double gD = dsum >= eps ? -dot / Dt : 0.0;  /* outer clamp */
+            const double gc = den_c >= eps ? gD : 0.0;        /* inner clamp: the call's share */
+            for (int i = 0; i < D; ++i) {
+                double g = gc * (hk1[i] + qt[i] * hk2[i]);
+                for (int j = 0; j < D; ++j) g += gn[j] * (h1[IDX2(i, j, D)] + qt[i] * h2[IDX2(i, j, D)]);
+                if (has) {
+                    double gs = gD * (ik1[i] + qt[i] * ik2[i]);
+                    for (int j = 0; j < D; ++j) gs += gn[j] * (i1[IDX2(i, j, D)] + qt[i] * i2[IDX2(i, j, D)]);
+                    g += w * gs;
+                }
+                gq[i] = g;
+            }
+            if (has) {
+                for (int j = 0; j < D; ++j) b0[j] += w * gn[j];
+                for (int i = 0; i < D; ++i)
+                    for (int j = 0; j < D; ++j) {
+                        b1[IDX2(i, j, D)] += w * qt[i] * gn[j];
+                        b2[IDX2(i, j, D)] += w * 0.5 * qt[i] * qt[i] * gn[j];
+                    }
+                *bk0 += w * gD;
+                for (int i = 0; i < D; ++i) {
+                    bk1[i] += w * qt[i] * gD;
+                    bk2[i] += w * 0.5 * qt[i] * qt[i] * gD;
+                }
+            }
+            for (int j = 0; j < D; ++j) a0[j] += gn[j];
+            for (int i = 0; i < D; ++i)
+                for (int j = 0; j < D; ++j) {
+                    a1[IDX2(i, j, D)] += qt[i] * gn[j];
+                    a2[IDX2(i, j, D)] += 0.5 * qt[i] * qt[i] * gn[j];
+                }
+            *ak0 += gc;
+            for (int i = 0; i < D; ++i) {
+                ak1[i] += qt[i] * gc;
+                ak2[i] += 0.5 * qt[i] * qt[i] * gc;
+            }
+            /* token t's update of the call's state: C_t = l C_(t-1) + f(k_t, v_t) */
+            for (int j = 0; j < D; ++j) {
+                double g = a0[j];
+                for (int i = 0; i < D; ++i) g += a1[IDX2(i, j, D)] * kt[i] + a2[IDX2(i, j, D)] * kt[i] * kt[i];
+                gv[j] = g;
+            }
+            for (int i = 0; i < D; ++i) {
+                double g1 = 0.0, g2 = 0.0;
+                for (int j = 0; j < D; ++j) {
+                    g1 += a1[IDX2(i, j, D)] * vt[j];
+                    g2 += a2[IDX2(i, j, D)] * vt[j];
+                }
+                gk[i] = g1 + 2.0 * kt[i] * g2 + ak1[i] + 2.0 * kt[i] * ak2[i];
+            }
+            for (size_t x = 0; x < NS; ++x) ac[x] *= l;
+        }
+        if (has && dS0o) {  /* the terminal state carries l^L S */
+            const double lL = pow(l, L);
+            for (int j = 0; j < D; ++j) b0[j] += lL * dS0o[(size_t)bh * D + j];
+            for (size_t x = 0; x < DD; ++x) {
+                b1[x] += lL * dS1o[(size_t)bh * DD + x];
+                b2[x] += lL * dS2o[(size_t)bh * DD + x];
+            }
+            *bk0 += lL * dK0o[bh];
+            for (int i = 0; i < D; ++i) {
+                bk1[i] += lL * dK1o[(size_t)bh * D + i];
+                bk2[i] += lL * dK2o[(size_t)bh * D + i];
+            }
+        }
+    }
+    free(hist);
+    free(cs);
+    free(ac);
+    free(nc);
+    free(ns);
+    free(gn);
+}

@@ -2,6 +2,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -573,6 +574,8 @@ namespace {
 size_t bwd_token_bytes(int B, int H, int L) {
     return (static_cast<size_t>(B) * H * L * 2 * sizeof(float) + 255) & ~static_cast<size_t>(255);
 }
+// the dense double clamp with an incoming state: kBwdCorr floats per sequence
+size_t bwd_corr_bytes(int B, int H) { return static_cast<size_t>(B) * H * prime::kBwdCorr * sizeof(float); }
 }  // namespace
 
 size_t prime_chunked_prefill_backward_workspace_size(int B, int H, int L) {
@@ -580,7 +583,7 @@ size_t prime_chunked_prefill_backward_workspace_size(int B, int H, int L) {
     int G, cps;
     prime::plan_backward_segments(B * H, L, &G, &cps);
     const size_t slots = G > 1 ? static_cast<size_t>(B) * H * G * prime::kWsStride * sizeof(float) : 0;
-    return bwd_token_bytes(B, H, L) + slots;
+    return bwd_token_bytes(B, H, L) + std::max(slots, bwd_corr_bytes(B, H));
 }
 
 int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
@@ -599,8 +602,8 @@ int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t
     if (H_kv != H)
         return fail(PRIME_ERR_INVALID_ARG, "backward takes k/v with one head per query head (H_kv=%d, H=%d): "
                     "expand grouped k/v first, as the reference module does", H_kv, H);
-    if ((flags & PRIME_FLAG_DENSE_CLAMP) && state_in)
-        return fail(PRIME_ERR_INVALID_ARG, "the double clamp with an incoming state has no backward here");
+    if (flags & ~PRIME_FLAG_DENSE_CLAMP) return fail(PRIME_ERR_INVALID_ARG, "unknown flags 0x%x", flags);
+    const bool dense_in = (flags & PRIME_FLAG_DENSE_CLAMP) && state_in;
     if (q->dtype != k->dtype || q->dtype != v->dtype || (q->dtype != PRIME_BF16 && q->dtype != PRIME_F32))
         return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "q/k/v must share dtype BF16 or F32");
     if (!valid_dtype(dy->dtype) || !valid_dtype(dq->dtype))
@@ -612,9 +615,10 @@ int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t
     if (!rows_aligned(q, true) || !rows_aligned(k, true) || !rows_aligned(v, true) || !rows_aligned(dy, true))
         return fail(PRIME_ERR_MISALIGNED, "q/k/v/dy rows must start on 16-byte boundaries");
     const size_t need = bwd_token_bytes(B, H, L);
-    if (workspace_bytes < need || !aligned16(workspace))
+    const size_t need_all = need + (dense_in ? bwd_corr_bytes(B, H) : 0);
+    if (workspace_bytes < need_all || !aligned16(workspace))
         return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes (16-byte aligned) is below the %zu needed",
-                    workspace_bytes, need);
+                    workspace_bytes, need_all);
     int rc;
     if ((rc = check_state(state_in, "state_in")) || (rc = check_state(dstate_out, "dstate_out")) ||
         (rc = check_state(dstate_in, "dstate_in")))
@@ -644,12 +648,18 @@ int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t
     a.inv_den = static_cast<float *>(workspace);
     a.g_den = a.inv_den + static_cast<size_t>(B) * H * L;
     prime::plan_backward_segments(B * H, L, &a.G, &a.cps);
-    if (q->dtype == PRIME_F32 || (a.G > 1 && workspace_bytes < prime_chunked_prefill_backward_workspace_size(B, H, L))) {
-        // (fp32 inputs: the fp32 passes run one workgroup per sequence)
+    if (q->dtype == PRIME_F32 || dense_in ||
+        (a.G > 1 && workspace_bytes < prime_chunked_prefill_backward_workspace_size(B, H, L))) {
+        // (fp32 inputs: the fp32 passes run one workgroup per sequence; the dense
+        // double clamp carries the call's K apart from the incoming one from token 0)
         a.G = 1;  // one segment per sequence in the workspace given
         a.cps = (L + 63) / 64;
     }
     a.ws = a.G > 1 ? reinterpret_cast<float *>(static_cast<char *>(workspace) + need) : nullptr;
+    if (dense_in) {
+        a.dense_in = 1;
+        a.kcorr = reinterpret_cast<float *>(static_cast<char *>(workspace) + need);
+    }
     return check_hip(prime::launch_prefill_backward(a, static_cast<hipStream_t>(stream)), "backward launch");
 }
 

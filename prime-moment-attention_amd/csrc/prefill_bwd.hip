@@ -174,6 +174,8 @@ __device__ __forceinline__ void load_rows(Rows &R, const BwdArgs &a, int b, int 
 }  // namespace
 
 // ---------------------------------------------------------------- dq pass
+// DIN: the dense double clamp with an incoming state (BwdArgs::dense_in)
+template <bool DIN>
 __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t sQf[kC][kPW];   // [q | q*q]
     __shared__ __attribute__((aligned(16))) uint16_t sKf[kC][kPW];   // [k | k*k/2]
@@ -183,6 +185,11 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
     // fp32: the K column of M (the denominator's moments) entering the chunk, S0, K0
     __shared__ float sKv[kF], sS0[kD], sK0[1], sGd[kC], sPg[kC], sPw[kC + 2], sPs[kC + 2];
     __shared__ float sRedK[kF], sRedS[kD];  // the chunk's K and S0 increments
+    // dense double clamp with an incoming state: the incoming [K1; K2/2] and K0
+    // (the carried K above is then the call's own), and per token of the chunk
+    // l^(t+1) times the outer-clamp denominator adjoint (sPc) and times the part
+    // of it the inner clamp withholds from the call's tokens (sDh)
+    __shared__ float sKin[kF], sK0in[1], sPc[kC], sDh[kC];
     // the state-update weights l^(n-1-j) of a full chunk (0) and of the
     // sequence's last chunk (1, n = its valid tokens), and the same weights split
     // into three bf16 parts (hi, mid, lo: about fp32 precision in sum), row 3
@@ -222,11 +229,20 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
         for (int m = 0; m < tid; ++m, pm *= ld) ps += pm;
         sPs[tid] = static_cast<float>(ps);
     }
+    constexpr bool din = DIN;  // (then G == 1: the S*p are state_in)
     if (tid < kD) sS0[tid] = S0p ? S0p[tid] : 0.f;
-    if (tid == 0) sK0[0] = K0p ? K0p[0] : 0.f;
+    if (tid == 0) {
+        sK0[0] = K0p && !din ? K0p[0] : 0.f;
+        sK0in[0] = K0p && din ? K0p[0] : 0.f;
+    }
     // the denominator's moments [K1; K2/2] in fp32, one feature per thread (tid < 128)
     float kv = 0.f;
     if (tid < kF && K1p) kv = tid < kD ? K1p[tid] : 0.5f * K2p[tid - kD];
+    if (din) {
+        if (tid < kF) sKin[tid] = kv;
+        kv = 0.f;
+    }
+    float corr = 0.f;  // (din) this thread's feature (tid < 128) or K0 (tid == 128) of the correction
     // constant columns of the 80-wide tiles
     for (int idx = tid; idx < kC * 16; idx += 256) {
         const int row = idx >> 4, cc = kD + (idx & 15);
@@ -313,6 +329,8 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
 
     for (int c = c_begin; c < c_end; ++c) {
         const int nvalid = min(kC, a.L - c * kC);
+        // (din) l^(64 c): the incoming state's decay to the chunk's start
+        const float lc = din ? static_cast<float>(pow(static_cast<double>(lam), 64.0 * c)) : 0.f;
         __syncthreads();  // tiles of chunk c and M_c in LDS
         const int wsel = nvalid == kC ? 0 : 1;  // weights of a full chunk or of the last one
         // ---- scores S^T[j][iw] (blocks jb <= w), masked: A = l^(i-j) (1 + phi_q . phi_k)
@@ -357,7 +375,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
         }
         // ---- denominator of row iw in fp32 (whether the clamp is active decides
         // the gradient): row sum of the masked scores + pin (phi_q . K + K0)
-        float dsum = 0.f, dcar = 0.f;
+        float dsum = 0.f, dcar = 0.f, dcin = 0.f;
 #pragma unroll
         for (int jb = 0; jb < 4; ++jb)
 #pragma unroll
@@ -367,11 +385,17 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             float qf[8];
             unpack8(lds128(&sQf[iw][((32 * g) & (kD - 1)) + 8 * t]), qf);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) dcar += (g < 2 ? qf[e] : qf[e] * qf[e]) * sKv[32 * g + 8 * t + e];
+            for (int e = 0; e < 8; ++e) {
+                const float ph = g < 2 ? qf[e] : qf[e] * qf[e];
+                dcar += ph * sKv[32 * g + 8 * t + e];
+                if (din) dcin += ph * sKin[32 * g + 8 * t + e];
+            }
         }
         dsum = sum_lane32(sum_lane16(dsum));
         dcar = sum_lane32(sum_lane16(dcar));
         const float den_iw = dsum + pinc * (dcar + sK0[0]);
+        // (din) the incoming state's denominator term l^(t+1) (K0 + phi_q . K), outside the inner clamp
+        const float cr_iw = din ? lc * pinc * (sum_lane32(sum_lane16(dcin)) + sK0in[0]) : 0.f;
         // ---- G of rows i = 16w + 4g + r; dy of those rows at column 16nb + c16
         // from transposed reads (dyt[nb] element r: row 16w + 4g + r)
         uint2 dyt[4];
@@ -382,7 +406,9 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             const int i = 16 * w + 4 * g + r;
             const bool valid = i < nvalid;
             const float den = __shfl(den_iw, 4 * g + r, kWave);  // row i's denominator sits in lane c16 = 4g + r
-            const float d = fmaxf(den, a.eps);
+            // single clamp max(den, eps), or the double clamp max(max(den, eps) + cr, eps)
+            const float d1 = din ? fmaxf(den, a.eps) + __shfl(cr_iw, 4 * g + r, kWave) : den;
+            const float d = fmaxf(d1, a.eps);
             const float inv = 1.0f / d;
             float part = 0.f, gn[4];
 #pragma unroll
@@ -396,12 +422,18 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             part += xor_lane<2>(part);
             part += xor_lane<4>(part);
             part += xor_lane<8>(part);
-            const float gden = (valid && den >= a.eps) ? -part * inv : 0.f;
+            // the outer clamp's adjoint, and the call's share of it (inner clamp)
+            const float gout = (valid && d1 >= a.eps) ? -part * inv : 0.f;
+            const float gden = den >= a.eps ? gout : 0.f;
 #pragma unroll
             for (int nb = 0; nb < 4; ++nb) sG[i][16 * nb + c16] = f32_to_bf16_bits(gn[nb]);
             if (c16 == 0) {
                 sGd[i] = gden;
                 sPg[i] = pinr[r] * gden;
+                if (din) {
+                    sPc[i] = lc * pinr[r] * gout;
+                    sDh[i] = lc * pinr[r] * (gout - gden);
+                }
                 if (valid) {
                     const size_t o = static_cast<size_t>(seq) * a.L + c * kC + i;
                     a.inv_den[o] = inv;
@@ -456,6 +488,14 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             const float kf = sKv[16 * fb + c16];  // K column of M
 #pragma unroll
             for (int r = 0; r < 4; ++r) dphi[fb][r] += sPg[16 * w + 4 * g + r] * kf;
+        }
+        if (din) {  // the incoming K's denominator term, under the outer clamp only
+#pragma unroll
+            for (int fb = 0; fb < 8; ++fb) {
+                const float kf = sKin[16 * fb + c16];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dphi[fb][r] += sPc[16 * w + 4 * g + r] * kf;
+            }
         }
         // ---- dq = dphi[q] + 2 q dphi[q*q]
         {
@@ -545,6 +585,17 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             if (g == 0) sRedS[16 * w + c16] = (ds0[0] + ds0[1]) + ds0[2];
         }
         __syncthreads();  // every read of chunk c's tiles and of M_c is done; partial sums in LDS
+        if (din) {  // correction: sum over the chunk of sDh_t phi_q(t) (chunk c's tiles are still in LDS)
+            if (tid < kF) {
+                float sacc = 0.f;
+                for (int i = 0; i < nvalid; ++i) sacc += sDh[i] * bf16_bits_to_f32(sQf[i][tid]);
+                corr += sacc;
+            } else if (tid == kF) {
+                float sacc = 0.f;
+                for (int i = 0; i < nvalid; ++i) sacc += sDh[i];
+                corr += sacc;
+            }
+        }
         if (c + 1 < c_end) {
             if (tid < kF) kv = ln * kv + sRedK[tid];
             if (tid < kD) sS0[tid] = ln * sS0[tid] + sRedS[tid];
@@ -554,6 +605,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
             if (c + 2 < c_end) load_rows(R, a, b, h, c + 2, ra, col, true, true, false);
         }
     }
+    if (din && tid <= kF) a.kcorr[static_cast<size_t>(seq) * kBwdCorr + tid] = corr;
 }
 
 // ---------------------------------------------------------------- dk, dv pass
@@ -894,12 +946,14 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int f = 16 * (2 * w + fi) + 4 * g + r, fr = f & (kD - 1), n = 16 * nb + c16;
-                    const float x = f < kD ? st[fi][nb][r] : 0.5f * st[fi][nb][r];
+                    float x = st[fi][nb][r];
+                    if (n == kD && a.dense_in) x += a.kcorr[static_cast<size_t>(seq) * kBwdCorr + f];
+                    if (f >= kD) x *= 0.5f;
                     if (n < kD) (f < kD ? a.ds1i : a.ds2i)[so1 + fr * kD + n] = x;
                     else if (n == kD) (f < kD ? a.dk1i : a.dk2i)[so0 + fr] = x;
                 }
         if (tid < kD) a.ds0i[so0 + tid] = w1;
-        else if (tid == kD) a.dk0i[seq] = w1;
+        else if (tid == kD) a.dk0i[seq] = w1 + (a.dense_in ? a.kcorr[static_cast<size_t>(seq) * kBwdCorr + kF] : 0.f);
     }
 }
 
@@ -972,7 +1026,11 @@ hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream) {
     }
     const int units = S * a.G;
     const TimerEvents t1 = timer_events(PRIME_KERNEL_BWD_DQ);
-    hipExtLaunchKernelGGL(prefill_bwd_dq_kernel, dim3(units), dim3(256), 0, stream, t1.start, t1.stop, 0, a);
+    if (a.dense_in)
+        hipExtLaunchKernelGGL(prefill_bwd_dq_kernel<true>, dim3(units), dim3(256), 0, stream, t1.start, t1.stop, 0, a);
+    else
+        hipExtLaunchKernelGGL(prefill_bwd_dq_kernel<false>, dim3(units), dim3(256), 0, stream, t1.start, t1.stop, 0,
+                              a);
     if ((e = hipGetLastError()) != hipSuccess) return timer_drop(t1), e;
     if (a.G > 1) {
         // each segment's dual contribution, then the reverse scan (slots now hold dual states)

@@ -158,6 +158,8 @@ __device__ __forceinline__ void dscores(const BwdArgs &a, int c, int w, int g, i
 // dq pass: chunks in order, the forward state carried (M tiles of feature
 // block w in wave w's accumulators, Kf / S0 / K0 by threads 0..192).
 // ---------------------------------------------------------------------------
+// DIN: the dense double clamp with an incoming state (BwdArgs::dense_in)
+template <bool DIN>
 __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) float sFq[kC][kPQ];
     __shared__ __attribute__((aligned(16))) float sFk[kC][kPQ];
@@ -167,6 +169,11 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
     __shared__ __attribute__((aligned(16))) float sM[kFP][kPR];
     __shared__ float sKf[kFP], sS0[kD], sCum[kC], sEc[kC], sW[kC], sD[kC], sH[kC], sDen[kC], sK0[1];
     __shared__ float sPart[kBW][16];
+    // dense double clamp with an incoming state: the incoming Kf and K0 (sKf, sK0
+    // then carry the call's own), per token max(den, eps) + the incoming term
+    // (sD1), l^(64c) times the outer clamp's adjoint (sHc), and l^(t+1) times the
+    // part of it the inner clamp withholds from the call's tokens (sDh)
+    __shared__ float sKin[kFP], sK0in[1], sD1[kC], sHc[kC], sDh[kC];
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -196,13 +203,23 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
         else if (tid < kFP + kD) kreg = a.s0i[so0 + tid - kFP];
         else if (tid == kFP + kD) kreg = a.k0i[seq];
     }
+    constexpr bool din = DIN;
+    const bool kthr = tid < kFP || tid == kFP + kD;  // threads that carry Kf or K0
+    if (din && kthr) {
+        if (tid < kFP) sKin[tid] = kreg;
+        else sK0in[0] = kreg;
+        kreg = 0.f;  // the call's own K moments from zero
+    }
     if (tid < kFP) sKf[tid] = kreg;
     else if (tid < kFP + kD) sS0[tid - kFP] = kreg;
     else if (tid == kFP + kD) sK0[0] = kreg;
+    float corr = 0.f;  // (din) this thread's feature (tid < 128) or K0 (tid == 192) of the correction
 
     const int NC = (a.L + kC - 1) / kC;
     const int64_t gbase = b * a.g_sb + h * a.g_sh;
     for (int c = 0; c < NC; ++c) {
+        // (din) l^(64 c): the incoming state's decay to the chunk's start
+        const float lc = din ? static_cast<float>(pow(static_cast<double>(a.decay[h]), 64.0 * c)) : 0.f;
         load_chunk(a, b, h, c, tid, w, lane, sFq, sFk, sV, sG, sCum, sEc, sW, logl);
         __syncthreads();
         scores(a, c, w, g, c16, sFq, sFk, sCum, sA);
@@ -215,15 +232,25 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
 #pragma unroll
                 for (int e = 0; e < 16; ++e) part += sA[i][16 * qt + e];
             }
-            float rd = qt == 0 ? sK0[0] : 0.f;
+            float rd = qt == 0 ? sK0[0] : 0.f, ri = qt == 0 && din ? sK0in[0] : 0.f;
 #pragma unroll
-            for (int e = 0; e < 32; ++e) rd += sFq[i][32 * qt + e] * sKf[32 * qt + e];
+            for (int e = 0; e < 32; ++e) {
+                rd += sFq[i][32 * qt + e] * sKf[32 * qt + e];
+                if (din) ri += sFq[i][32 * qt + e] * sKin[32 * qt + e];
+            }
             part += sEc[i] * rd;
             part += xor_lane<1>(part);
             part += xor_lane<2>(part);
+            if (din) {
+                ri += xor_lane<1>(ri);
+                ri += xor_lane<2>(ri);
+            }
             if (qt == 0) {
+                // single clamp max(den, eps), or the double clamp max(max(den, eps) + cr, eps)
+                const float d1 = din ? fmaxf(part, a.eps) + lc * sEc[i] * ri : part;
                 sDen[i] = part;
-                sD[i] = fmaxf(part, a.eps);
+                sD1[i] = d1;
+                sD[i] = fmaxf(d1, a.eps);
             }
         }
         __syncthreads();
@@ -255,8 +282,14 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
             const int i = tid, ib = i >> 4, cc = i & 15;
             const float dot = sPart[2 * ib][cc] + sPart[2 * ib + 1][cc];
             const float D = sD[i];
-            const float hh = sDen[i] >= a.eps ? -dot / (D * D) : 0.f;
+            // the outer clamp's adjoint, and the call's share of it (inner clamp)
+            const float hout = sD1[i] >= a.eps ? -dot / (D * D) : 0.f;
+            const float hh = sDen[i] >= a.eps ? hout : 0.f;
             sH[i] = hh;
+            if (din) {
+                sHc[i] = lc * hout;
+                sDh[i] = lc * sEc[i] * (hout - hh);
+            }
             const int64_t t = static_cast<int64_t>(c) * kC + i;
             if (t < a.L) {
                 a.inv_den[static_cast<size_t>(seq) * a.L + t] = 1.0f / D;
@@ -292,6 +325,11 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
                     const float hh = ec * sH[tok];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc[r] += hh * sKf[16 * fb + 4 * g + r];
+                    if (din) {  // the incoming K's denominator term, under the outer clamp only
+                        const float hc = ec * sHc[tok];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[r] += hc * sKin[16 * fb + 4 * g + r];
+                    }
                     d2[hf] = acc;
                 }
                 // lane: features 16 db + 4g + r of token tok; dq = dFq1 + 2 q dFq2
@@ -323,6 +361,11 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
                 float acc = e63 * kreg;
                 for (int j = 0; j < kC; ++j) acc += sW[j] * sFk[j][tid];
                 kreg = acc;
+                if (din) {  // correction: sum over the chunk of sDh_t Fq(t)
+                    float sacc = 0.f;
+                    for (int i = 0; i < kC; ++i) sacc += sDh[i] * sFq[i][tid];
+                    corr += sacc;
+                }
             } else if (tid < kFP + kD) {
                 float acc = e63 * kreg;
                 for (int j = 0; j < kC; ++j) acc += sW[j] * sV[j][tid - kFP];
@@ -331,6 +374,11 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
                 float acc = e63 * kreg;
                 for (int j = 0; j < kC; ++j) acc += sW[j];
                 kreg = acc;
+                if (din) {
+                    float sacc = 0.f;
+                    for (int i = 0; i < kC; ++i) sacc += sDh[i];
+                    corr += sacc;
+                }
             }
         }
         __syncthreads();
@@ -342,6 +390,7 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
         else if (tid < kFP + kD) sS0[tid - kFP] = kreg;
         else if (tid == kFP + kD) sK0[0] = kreg;
     }
+    if (din && kthr) a.kcorr[static_cast<size_t>(seq) * kBwdCorr + (tid < kFP ? tid : kFP)] = corr;
 }
 
 // ---------------------------------------------------------------------------
@@ -512,17 +561,22 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
                 if (f < kD) a.ds1i[so1 + f * kD + col] = mt[dv][r];
                 else a.ds2i[so1 + (f - kD) * kD + col] = 0.5f * mt[dv][r];
             }
-        if (tid < kD) a.dk1i[so0 + tid] = kreg;
-        else if (tid < kFP) a.dk2i[so0 + tid - kD] = 0.5f * kreg;
+        // (dense double clamp with a state: plus the dq pass's correction)
+        const float* kc = a.dense_in ? a.kcorr + static_cast<size_t>(seq) * kBwdCorr : nullptr;
+        if (tid < kD) a.dk1i[so0 + tid] = kreg + (kc ? kc[tid] : 0.f);
+        else if (tid < kFP) a.dk2i[so0 + tid - kD] = 0.5f * (kreg + (kc ? kc[tid] : 0.f));
         else if (tid < kFP + kD) a.ds0i[so0 + tid - kFP] = kreg;
-        else if (tid == kFP + kD) a.dk0i[seq] = kreg;
+        else if (tid == kFP + kD) a.dk0i[seq] = kreg + (kc ? kc[kFP] : 0.f);
     }
 }
 
 hipError_t launch_prefill_backward_f32(const BwdArgs &a, hipStream_t stream) {
     const dim3 grid(a.B * a.H), block(kBW * kWave);
     const TimerEvents t1 = timer_events(PRIME_KERNEL_BWD_DQ);
-    hipExtLaunchKernelGGL(prefill_bwd_dq_f32_kernel, grid, block, 0, stream, t1.start, t1.stop, 0, a);
+    if (a.dense_in)
+        hipExtLaunchKernelGGL(prefill_bwd_dq_f32_kernel<true>, grid, block, 0, stream, t1.start, t1.stop, 0, a);
+    else
+        hipExtLaunchKernelGGL(prefill_bwd_dq_f32_kernel<false>, grid, block, 0, stream, t1.start, t1.stop, 0, a);
     hipError_t e;
     if ((e = hipGetLastError()) != hipSuccess) return timer_drop(t1), e;
     const TimerEvents t2 = timer_events(PRIME_KERNEL_BWD_DKV);

@@ -166,7 +166,15 @@ struct BwdArgs {
     int64_t g_sb, g_sh, g_sl;                               // strides of dq, dk, dv
     float *ds0i, *ds1i, *ds2i, *dk0i, *dk1i, *dk2i;         // adjoint of the incoming state (null => none)
     float *inv_den, *g_den;                                 // [B*H, L] fp32, written by the dq pass
+    // the dense branch's double clamp with an incoming state (G == 1): the dq
+    // pass carries the call's own K moments apart from the incoming ones and
+    // writes, per sequence, kBwdCorr floats to kcorr (the incoming K adjoint's
+    // share that the inner clamp withholds from the call's tokens: features
+    // [K1; K2/2], then K0), which the dk/dv pass adds to that adjoint
+    int dense_in;
+    float *kcorr;
 };
+constexpr int kBwdCorr = 132;  // floats per sequence in BwdArgs::kcorr (128 features, K0, padding)
 
 hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream);
 // fp32 inputs: the fp32 dq and dk/dv passes, one workgroup per sequence (prefill_bwd_f32.hip)

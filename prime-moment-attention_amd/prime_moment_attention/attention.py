@@ -113,8 +113,8 @@ class PrimeMomentAttention(nn.Module):
         if torch.is_grad_enabled() and (hidden_states.requires_grad or any(p.requires_grad for p in self.parameters())):
             # training: QK-norm and scale as torch ops, the recurrence through the
             # differentiable prefill (for L == 1 its chunked form is the step,
-            # attention.py:119-143; for L <= chunk_threshold without a state the
-            # dense branch's clamps are one clamp)
+            # attention.py:119-143; for 1 < L <= chunk_threshold the dense
+            # branch's double clamp, attention.py:177-185, with or without a state)
             q, k, v = self.project(hidden_states, normalize=False)
             if self.use_qk_norm:
                 q, k = self.q_norm(q), self.k_norm(k)

@@ -130,9 +130,6 @@ def prime_prefill(q, k, v, state=None, decay=0.9995, eps=1.0, chunk_size=64, ret
     if needs_grad(q, k, v, *(st_in or ())):
         if qk_norm is not None:
             raise NotImplementedError("the QK-norm on load has no backward; normalise q and k with torch ops")
-        if dense_clamp and st_in is not None:
-            raise NotImplementedError("the dense branch's double clamp with an incoming state has no backward "
-                                      "here; call under torch.no_grad() or without a state")
         flags = _lib.PRIME_FLAG_DENSE_CLAMP if dense_clamp else 0
         outs = _PrefillFn.apply(q, k, v, dec, float(eps), flags, bool(return_state), out_dtype, *(st_in or ()))
         if return_state:

@@ -124,14 +124,84 @@ def test_backward_dense_flag_without_state_and_bf16_grads():
     _check(ref, got, dsi)
 
 
+def _dense_case(B, H, L, dtype, seed, eps, k0=None):
+    """Inputs for the dense branch's double clamp with an incoming state, and
+    oracle_dense_vjp's result (dq, dk, dv, dstate_in) and the single clamp's."""
+    BH = B * H
+    bf = dtype == torch.bfloat16
+    q, k, v = O.make_inputs((B, H, L, D), seed=seed, bf16=bf)
+    rng = np.random.default_rng(seed + 1)
+    lam = rng.uniform(0.99, 0.9999, H).astype(np.float32)
+    dy = rng.standard_normal((B, H, L, D)).astype(np.float32)
+    if bf:
+        dy = O.bf16_round(dy)
+    st0 = random_state(BH, D, seed + 2)
+    if k0 is not None:  # a negative K0: the outer clamp active on the first tokens
+        st0 = tuple(np.full_like(x, k0) if i == 3 else x for i, x in enumerate(st0))
+    ds = tuple(0.1 * rng.standard_normal(x.shape) for x in O.zero_state(BH, D))
+    args = (q.reshape(BH, L, D), k.reshape(BH, L, D), v.reshape(BH, L, D), np.tile(lam.astype(np.float64), B),
+            dy.reshape(BH, L, D))
+    ref = O.dense_vjp(*args, eps=eps, state=st0, dstate=ds)
+    single = O.recurrent_vjp(*args, eps=eps, state=st0, dstate=ds)
+    return (q, k, v, lam, dy, st0, ds), ref, single
+
+
+@pytest.mark.parametrize("dtype,B,H,L,k0", [(torch.float32, 1, 2, 13, None), (torch.float32, 2, 2, 200, None),
+                                            (torch.float32, 1, 2, 150, -1.5), (torch.bfloat16, 2, 2, 200, None),
+                                            (torch.bfloat16, 1, 3, 70, -1.5)])
+def test_backward_dense_clamp_with_state(dtype, B, H, L, k0):
+    """The dense branch's double clamp with an incoming state
+    (attention.py:177-185; eps = 2.5 puts the inner clamp on the first
+    tokens) against oracle_dense_vjp; without a negative K0 the case is one
+    whose derivative differs from the single clamp's by more than the
+    tolerance."""
+    eps = 2.5
+    tol = TOL_BF16 if dtype == torch.bfloat16 else TOL_F32
+    (q, k, v, lam, dy, st0, ds), ref, single = _dense_case(B, H, L, dtype, 700 + L, eps, k0)
+    if k0 is None:
+        assert max(np.abs(a - b).max() / np.abs(a).max() for a, b in zip(ref[:3], single[:3])) > 2 * tol
+    g = [torch.empty(B, H, L, D, device=dev(), dtype=torch.float32) for _ in range(3)]
+    dsi = _lib.new_state(B, H, D, dev())
+    _lib.chunked_prefill_backward(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype), to_dev(lam), eps,
+                                  state_to_dev(st0, B, H, D), to_dev(dy, dtype), state_to_dev(ds, B, H, D), *g, dsi,
+                                  flags=1)
+    torch.cuda.synchronize()
+    BH = B * H
+    _check(ref, [to_np(t).reshape(BH, L, D) for t in g], state_to_np(dsi, BH, D), tol)
+
+
+def test_core_autograd_dense_clamp_with_state():
+    """prime_prefill's dense branch (the module's path for L <= chunk_threshold)
+    with an incoming state, trained through: q, k, v and the state's gradients
+    against oracle_dense_vjp."""
+    from prime_moment_attention.chunked_ssd import prime_prefill
+    B, H, L, eps = 2, 2, 90, 2.5
+    BH = B * H
+    (q, k, v, lam, dy, st0, ds), ref, _ = _dense_case(B, H, L, torch.float32, 720, eps)
+    tq, tk, tv = (to_dev(x).requires_grad_(True) for x in (q, k, v))
+    ts = [t.requires_grad_(True) for t in state_to_dev(st0, B, H, D)]
+    y, st = prime_prefill(tq, tk, tv, state=tuple(ts), decay=to_dev(lam), eps=eps, return_state=True,
+                          dense_clamp=True)
+    loss = (y * to_dev(dy)).sum() + sum((a * to_dev(b).reshape(a.shape)).sum() for a, b in zip(st, ds))
+    loss.backward()
+    torch.cuda.synchronize()
+    for name, t, r in (("dq", tq, ref[0]), ("dk", tk, ref[1]), ("dv", tv, ref[2])):
+        assert_close(to_np(t.grad).reshape(BH, L, D), r, TOL_F32, name)
+    assert_state_close(tuple(to_np(t.grad) for t in ts), ref[3], TOL_F32, "dstate_in")
+
+
 def test_backward_rejects_bad_arguments():
     B, H, L = 1, 2, 70
     x = torch.zeros(B, H, L, D, device=dev(), dtype=torch.bfloat16)
     g = [torch.empty(B, H, L, D, device=dev()) for _ in range(3)]
     lam = to_dev(np.full(H, 0.99, np.float32))
     st = _lib.new_state(B, H, D, dev(), zero=True)
-    with pytest.raises(RuntimeError, match="double clamp"):
-        _lib.chunked_prefill_backward(x, x, x, lam, 1.0, st, x, None, *g, None, flags=1)
+    token_bytes = (B * H * L * 8 + 255) // 256 * 256
+    with pytest.raises(RuntimeError, match="workspace"):  # the double clamp with a state needs its correction too
+        _lib.chunked_prefill_backward(x, x, x, lam, 1.0, st, x, None, *g, None, flags=1,
+                                      workspace=torch.empty(token_bytes, dtype=torch.uint8, device=dev()))
+    with pytest.raises(RuntimeError, match="unknown flags"):
+        _lib.chunked_prefill_backward(x, x, x, lam, 1.0, None, x, None, *g, None, flags=4)
     with pytest.raises(RuntimeError, match="workspace"):
         _lib.chunked_prefill_backward(x, x, x, lam, 1.0, None, x, None, *g, None,
                                       workspace=torch.empty(64, dtype=torch.uint8, device=dev()))

@@ -537,3 +537,102 @@ def test_recurrent_vjp_matches_torch_autograd_of_dense_branch(with_state):
         for got, ref in zip(dst, ts):
             r = ref.grad.numpy().reshape(got.shape)
             assert np.abs(got - r).max() <= 1e-10 * max(1.0, np.abs(r).max())
+
+
+# ---------------------------------------------------------------- reverse mode of the dense branch
+def _dense_objective(q, k, v, lam, st, dy, ds, eps):
+    y, so = O.dense(q, k, v, lam, eps=eps, state=st)
+    return float((y * dy).sum() + sum((a * b).sum() for a, b in zip(so, ds)))
+
+
+def _dense_gates(q, k, v, lam, st, eps):
+    """Per token: the call's own denominator den_c and max(den_c, eps) + the
+    incoming state's term (the arguments of the two clamps, attention.py:177, 185)."""
+    BH, L, D = q.shape
+    lam = np.broadcast_to(np.asarray(lam, np.float64), (BH,))
+    dc, d1 = np.zeros((BH, L)), np.zeros((BH, L))
+    for t in range(L):
+        _, c = O.recurrent(q[:, :t + 1], k[:, :t + 1], v[:, :t + 1], lam, eps=eps)
+        qt = q[:, t]
+        dc[:, t] = c[3].reshape(BH) + (qt * c[4]).sum(-1) + 0.5 * (qt * qt * c[5]).sum(-1)
+        ds = st[3].reshape(BH) + (qt * st[4]).sum(-1) + 0.5 * (qt * qt * st[5]).sum(-1)
+        d1[:, t] = np.maximum(dc[:, t], eps) + lam ** (t + 1) * ds
+    return dc, d1
+
+
+@pytest.mark.parametrize("k0", [None, -1.5])
+def test_dense_vjp_matches_finite_differences(k0):
+    """Directional derivatives of <dy, y> + <dstate, state_out> through the
+    dense branch's double clamp with an incoming state (central differences of
+    oracle_dense), with the inner clamp active on some tokens and, for a state
+    with a negative K0, the outer clamp on others."""
+    BH, L, eps = 2, 6, 2.5
+    q, k, v, lam, st, dy, ds = _vjp_case(BH, L, 330, True)
+    if k0 is not None:
+        st = tuple(np.full_like(x, k0) if i == 3 else x for i, x in enumerate(st))
+    dc, d1 = _dense_gates(q, k, v, lam, st, eps)
+    assert (dc < eps).any() and (dc >= eps).any()
+    if k0 is not None:
+        assert (d1 < eps).any() and (d1 >= eps).any()
+    assert np.abs(dc - eps).min() > 1e-4 and np.abs(d1 - eps).min() > 1e-4  # no kink within the steps
+    dq, dk, dv, dst = O.dense_vjp(q, k, v, lam, dy, eps=eps, state=st, dstate=ds)
+    rng = np.random.default_rng(331)
+    h = 1e-7
+    for _ in range(4):
+        tq, tk, tv = (rng.standard_normal(q.shape) for _ in range(3))
+        ts = tuple(rng.standard_normal(x.shape) for x in O.zero_state(BH, 64))
+        move = lambda s: (q + s * tq, k + s * tk, v + s * tv, tuple(a + s * b for a, b in zip(st, ts)))
+        fp = _dense_objective(*move(h)[:3], lam, move(h)[3], dy, ds, eps)
+        fm = _dense_objective(*move(-h)[:3], lam, move(-h)[3], dy, ds, eps)
+        fd = (fp - fm) / (2 * h)
+        an = float((dq * tq).sum() + (dk * tk).sum() + (dv * tv).sum() + sum((a * b).sum() for a, b in zip(dst, ts)))
+        assert abs(fd - an) <= 1e-6 * max(1.0, abs(an)), (fd, an)
+
+
+def test_dense_vjp_equals_recurrent_vjp_where_the_clamps_coincide():
+    """Without a state the dense branch has one clamp; with a state and the
+    inner clamp nowhere active the two clamps act as one.  Either way the
+    reverse mode is the recurrence's."""
+    BH, L = 3, 40
+    q, k, v, lam, st, dy, ds = _vjp_case(BH, L, 340, True)
+    for eps, state in ((1.0, None), (1e-3, st)):
+        a = O.dense_vjp(q, k, v, lam, dy, eps=eps, state=state, dstate=ds)
+        b = O.recurrent_vjp(q, k, v, lam, dy, eps=eps, state=state, dstate=ds)
+        for x, y in zip(a[:3], b[:3]):
+            np.testing.assert_allclose(x, y, rtol=1e-10, atol=1e-12)
+        if state is not None:
+            for x, y in zip(a[3], b[3]):
+                np.testing.assert_allclose(x, y, rtol=1e-10, atol=1e-12)
+
+
+def test_dense_vjp_matches_torch_autograd_of_the_double_clamp():
+    """torch's float64 autograd through the dense branch as the reference
+    writes it (attention.py:160-185: den clamped, the carry added, clamped
+    again) gives the same dq, dk, dv and incoming-state adjoint."""
+    import torch
+    BH, L, D, eps = 3, 9, 64, 2.5
+    q, k, v, lam, st, dy, _ = _vjp_case(BH, L, 350, True)
+    dc, _ = _dense_gates(q, k, v, lam, st, eps)
+    assert (dc < eps).any()
+    dq, dk, dv, dst = O.dense_vjp(q, k, v, lam, dy, eps=eps, state=st)
+    T = lambda x: torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    tq, tk, tv = T(q), T(k), T(v)
+    ts = [T(x) for x in st]
+    lam_t = torch.tensor(lam, dtype=torch.float64).view(BH, 1, 1)
+    idx = torch.arange(L, dtype=torch.float64)
+    diff = idx.view(L, 1) - idx.view(1, L)
+    dm = torch.where(diff >= 0, lam_t ** diff.clamp(min=0), torch.zeros(()))
+    A = dm * (1.0 + tq @ tk.transpose(1, 2) + 0.5 * (tq * tq) @ (tk * tk).transpose(1, 2))
+    num = A @ tv
+    den = A.sum(-1, keepdim=True).clamp(min=eps)
+    S0, S1, S2, K0, K1, K2 = ts
+    into = lam_t ** (idx + 1).view(1, L, 1)
+    num = num + into * (S0.unsqueeze(1) + tq @ S1 + 0.5 * (tq * tq) @ S2)
+    den = (den + into * (K0.view(BH, 1, 1) + (tq * K1.unsqueeze(1)).sum(-1, keepdim=True)
+                         + 0.5 * (tq * tq * K2.unsqueeze(1)).sum(-1, keepdim=True))).clamp(min=eps)
+    ((num / den) * torch.tensor(dy)).sum().backward()
+    for got, ref in ((dq, tq.grad), (dk, tk.grad), (dv, tv.grad)):
+        assert np.abs(got - ref.numpy()).max() <= 1e-10 * max(1.0, np.abs(ref.numpy()).max())
+    for got, ref in zip(dst, ts):
+        r = ref.grad.numpy().reshape(got.shape)
+        assert np.abs(got - r).max() <= 1e-10 * max(1.0, np.abs(r).max())
