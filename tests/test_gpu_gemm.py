@@ -80,7 +80,7 @@ def test_linear_residual_rejects_partial_overlap():
 # prime_linear_fused: the decode step's projections with the RMSNorm folded in
 # (model.py:47-56 then 59-68) and the GELU / residual epilogues
 FUSED = [(256, 2304, 768), (256, 768, 768), (256, 3072, 768), (256, 768, 3072), (37, 768, 768), (1000, 1536, 768),
-         (32, 50304, 768)]
+         (32, 50304, 768), (130, 640, 384), (64, 352, 512)]
 
 
 @pytest.mark.parametrize("M,N,K", FUSED)
