@@ -117,11 +117,15 @@ __global__ __launch_bounds__(256) void head_layernorm_kernel(const HeadNormArgs 
     const int lane = threadIdx.x & 63, sub = lane % LPR;
     const uint32_t wave = blockIdx.x * 4u + (threadIdx.x >> 6);
     float w[VE], bb[VE];
+    // a power-of-two scale folds into the weight and bias (pow2_scale): one
+    // rounding, the same bits (fp16 keeps both: its exponent range is narrower)
+    const bool fold = a.weight && DT != PRIME_F16 && pow2_scale(a.scale);
+    const float scale = fold ? 1.0f : a.scale;
     if (a.weight) {
 #pragma unroll
         for (int e = 0; e < VE; ++e) {
-            w[e] = load_elem(a.weight, VE * sub + e, a.dt_norm);
-            bb[e] = load_elem(a.bias, VE * sub + e, a.dt_norm);
+            w[e] = (fold ? a.scale : 1.0f) * load_elem(a.weight, VE * sub + e, a.dt_norm);
+            bb[e] = (fold ? a.scale : 1.0f) * load_elem(a.bias, VE * sub + e, a.dt_norm);
         }
     }
     uint4 raw[kHeadNormBatch];
@@ -161,11 +165,11 @@ __global__ __launch_bounds__(256) void head_layernorm_kernel(const HeadNormArgs 
             for (int o = LPR / 2; o >= 1; o >>= 1) q += __shfl_xor(q, o, kWave);
             const float rs = rsqrtf(q * (1.0f / kD) + a.ln_eps);
 #pragma unroll
-            for (int e = 0; e < VE; ++e) v[e] = Group<DT>::round(v[e] * rs * w[e] + bb[e]);
+            for (int e = 0; e < VE; ++e) v[e] = Group<DT>::round(fmaf(v[e] * rs, w[e], bb[e]));
         }
-        if (a.scale != 1.0f) {
+        if (scale != 1.0f) {
 #pragma unroll
-            for (int e = 0; e < VE; ++e) v[e] = Group<DT>::round(v[e] * a.scale);
+            for (int e = 0; e < VE; ++e) v[e] = Group<DT>::round(v[e] * scale);
         }
         uint4 o;
         if constexpr (DT == PRIME_F32) {

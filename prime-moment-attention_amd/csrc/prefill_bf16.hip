@@ -62,6 +62,8 @@ __device__ __forceinline__ u32x4 scale8(u32x4 x, float w) {
 // lanes (this lane: columns col..col+7): the same arithmetic, summation order
 // and roundings as head_layernorm_kernel, so the result is bit-identical to
 // normalising the projections first.  affine false: no LayerNorm, the scale only.
+// With the LayerNorm and scale == 1 the FMA results are packed (rounded) once;
+// a power-of-two scale reaches here folded into w and b (pow2_scale).
 // Every lane of the wave takes part (the sums are lane shuffles).
 // (w, b: LDS rows of the parameters, read at columns col..col+7)
 __device__ __forceinline__ u32x4 norm_row8(u32x4 x, bool affine, const float *w, const float *b, int col, float eps,
@@ -91,7 +93,10 @@ __device__ __forceinline__ u32x4 norm_row8(u32x4 x, bool affine, const float *w,
         sq += xor_lane<1>(sq);
         const float rs = rsqrtf(sq * (1.0f / kD) + eps);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e] * rs * w[col + e] + b[col + e]));
+        for (int e = 0; e < 8; ++e) v[e] = fmaf(v[e] * rs, w[col + e], b[col + e]);
+        if (scale == 1.0f) return pack8(v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e]));
     }
     if (scale != 1.0f) {
 #pragma unroll
@@ -272,7 +277,9 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
         if (tid < 4 * kD) {
             const int t = tid >> 6, e = tid & (kD - 1);
             const void *src = t == 0 ? a.qn_w : t == 1 ? a.qn_b : t == 2 ? a.kn_w : a.kn_b;
-            sLn[t][e] = src ? load_elem(src, e, a.dt_norm) : 0.f;
+            // a power-of-two q scale folds into q's weight and bias (pow2_scale)
+            const float fold = t < 2 && a.qn_w && pow2_scale(a.q_scale) ? a.q_scale : 1.0f;
+            sLn[t][e] = src ? fold * load_elem(src, e, a.dt_norm) : 0.f;
         }
     }
     __syncthreads();  // the power tables (and QKN's parameters) are read by the first tile stores below
@@ -327,8 +334,9 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
             // the module's QK LayerNorm (and q's scale) on the raw projections
             const bool qa = a.qn_w != nullptr, ka = a.kn_w != nullptr;
             if constexpr (!STATE_ONLY) {
-                T.q0 = norm_row8(T.q0, qa, sLn[0], sLn[1], col, a.ln_eps, a.q_scale);
-                if constexpr (!UW8) T.q1 = norm_row8(T.q1, qa, sLn[0], sLn[1], col, a.ln_eps, a.q_scale);
+                const float qs = qa && pow2_scale(a.q_scale) ? 1.0f : a.q_scale;  // (folded into sLn)
+                T.q0 = norm_row8(T.q0, qa, sLn[0], sLn[1], col, a.ln_eps, qs);
+                if constexpr (!UW8) T.q1 = norm_row8(T.q1, qa, sLn[0], sLn[1], col, a.ln_eps, qs);
             }
             __builtin_amdgcn_sched_barrier(0);  // one row's temporaries at a time
             T.k0 = norm_row8(T.k0, ka, sLn[2], sLn[3], col, a.ln_eps, 1.0f);

@@ -25,6 +25,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
+// s = 2^e for a normal exponent: then round(round(x) * s) == round(x * s) for
+// the fp32 and bf16 roundings (scaling by s is exact in both, whose exponent
+// ranges are the same), so a scale can be folded into the operands before the
+// one rounding
+__device__ __forceinline__ bool pow2_scale(float s) {
+    const uint32_t u = __float_as_uint(s) & 0x7FFFFFFFu;
+    return (u & 0x007FFFFFu) == 0u && u >= 0x00800000u && u < 0x7F800000u;
+}
+
 __device__ __forceinline__ float h16_bits_to_f32(uint16_t b) {
     return static_cast<float>(__builtin_bit_cast(_Float16, b));
 }
