@@ -15,20 +15,6 @@ namespace prime {
 
 constexpr int kArgmaxThreads = 1024;
 
-__device__ __forceinline__ uint64_t argmax_key(float f, uint32_t idx) {
-    uint32_t k;
-    if (f != f) {
-        k = 0xffffffffu;
-    } else {
-        if (f == 0.f) f = 0.f;  // -0 and +0 compare equal
-        const uint32_t b = __float_as_uint(f);
-        k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    }
-    return (static_cast<uint64_t>(k) << 32) | static_cast<uint64_t>(~idx);
-}
-
-__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
 template <int DT>
 __device__ __forceinline__ void scan_vector(const uint4 &r, uint32_t j0, uint64_t &best) {
     if constexpr (DT == PRIME_F32) {

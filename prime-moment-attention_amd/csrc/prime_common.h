@@ -105,4 +105,22 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// Argmax candidate as one 64-bit key: an order-preserving image of the value in
+// the high word (NaN -> all ones, -0 folded onto +0) and ~index in the low
+// word, so the larger key is the larger value and, among equal values, the
+// smaller index (torch.argmax's first maximal index, NaN counting as largest).
+__device__ __forceinline__ uint64_t argmax_key(float f, uint32_t idx) {
+    uint32_t k;
+    if (f != f) {
+        k = 0xffffffffu;
+    } else {
+        if (f == 0.f) f = 0.f;  // -0 and +0 compare equal
+        const uint32_t b = __float_as_uint(f);
+        k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    }
+    return (static_cast<uint64_t>(k) << 32) | static_cast<uint64_t>(~idx);
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
 }  // namespace prime
