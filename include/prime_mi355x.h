@@ -437,6 +437,33 @@ int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t
 size_t prime_chunked_prefill_backward_workspace_size(int B, int H, int L);
 
 /*
+ * prime_selective_prefill_backward: the adjoint of prime_selective_prefill
+ * (torch autograd through selective.py:414-440, and through the step branch
+ * :384-409 for a call with an incoming state), F32 q/k/v (convert bf16 inputs
+ * first; the passes are the fp32 backward's, one workgroup per sequence).
+ * Inputs as for prime_selective_prefill: log_decay fp32 [B,H,L] (log lambda_t,
+ * contiguous), k_scale fp32 [H] (beta; the key enters as beta k), state_in in
+ * the selective convention (S2, K2 carry the 1/2), or NULL; dy; dstate_out
+ * (the final state's adjoint, selective convention) or NULL.  Outputs: dq, dk,
+ * dv (one dtype and stride set), dstate_in (or NULL), d_log_decay fp32
+ * [B,H,L] (the adjoint of log_decay: every later token's decay factor
+ * e^(c_i - c_j) contains log lambda_t, so d_log_decay[t] sums, over the
+ * tokens i >= t, phi_q'(i).dphi_q'(i) - phi_k'(i).dphi_k'(i) with the
+ * features [1, q, q*q] and [1, beta k, beta^2 k*k/2], plus
+ * <dstate_out, state_out>), d_k_scale fp32 [B,H] (the adjoint of k_scale per
+ * sequence: sum over the batch for the [H] parameter).  H_kv == H.
+ * workspace (16-byte aligned): prime_selective_prefill_backward_workspace_size.
+ */
+int prime_selective_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                                     int B, int H, int H_kv, int L, int D, const float *log_decay,
+                                     const float *k_scale, float eps, const prime_state_t *state_in,
+                                     const prime_tensor_t *dy, const prime_state_t *dstate_out,
+                                     const prime_tensor_t *dq, const prime_tensor_t *dk, const prime_tensor_t *dv,
+                                     const prime_state_t *dstate_in, float *d_log_decay, float *d_k_scale,
+                                     void *workspace, size_t workspace_bytes, void *stream);
+size_t prime_selective_prefill_backward_workspace_size(int B, int H, int L);
+
+/*
  * prime_decode_readout replaces prime_query_step_cpp (prime_cpp_kernel.cpp:85-100):
  * y = (S0 + S1^T q + 1/2 S2^T q^2) / max(K0 + q.K1 + 1/2 q^2.K2, eps) against
  * `state` as it is (the reference's eps is 1e-3); the state is not written.

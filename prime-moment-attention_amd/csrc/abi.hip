@@ -663,6 +663,81 @@ int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t
     return check_hip(prime::launch_prefill_backward(a, static_cast<hipStream_t>(stream)), "backward launch");
 }
 
+size_t prime_selective_prefill_backward_workspace_size(int B, int H, int L) {
+    if (B <= 0 || H <= 0 || L <= 0) return 0;
+    // the per-token denominators (8 bytes), the query-side decay terms (4), one float per sequence
+    return bwd_token_bytes(B, H, L) + static_cast<size_t>(B) * H * L * sizeof(float) +
+           static_cast<size_t>(B) * H * sizeof(float);
+}
+
+int prime_selective_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                                     int B, int H, int H_kv, int L, int D, const float *log_decay,
+                                     const float *k_scale, float eps, const prime_state_t *state_in,
+                                     const prime_tensor_t *dy, const prime_state_t *dstate_out,
+                                     const prime_tensor_t *dq, const prime_tensor_t *dk, const prime_tensor_t *dv,
+                                     const prime_state_t *dstate_in, float *d_log_decay, float *d_k_scale,
+                                     void *workspace, size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    if (!q || !k || !v || !dy || !dq || !dk || !dv || !q->data || !k->data || !v->data || !dy->data || !dq->data ||
+        !dk->data || !dv->data || !log_decay || !k_scale || !d_log_decay || !d_k_scale || !workspace)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_selective_prefill_backward: null argument");
+    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (B <= 0 || H <= 0 || L <= 0) return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d L=%d", B, H, L);
+    if (H_kv != H)
+        return fail(PRIME_ERR_INVALID_ARG, "backward takes k/v with one head per query head (H_kv=%d, H=%d): "
+                    "expand grouped k/v first, as the reference module does", H_kv, H);
+    if (q->dtype != PRIME_F32 || k->dtype != PRIME_F32 || v->dtype != PRIME_F32)
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "selective backward: F32 q/k/v (the reference differentiates "
+                    "the selective branch in fp32; convert bf16 inputs first)");
+    if (!valid_dtype(dy->dtype) || !valid_dtype(dq->dtype))
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dy / gradient dtype");
+    if (dk->dtype != dq->dtype || dv->dtype != dq->dtype || dk->stride_b != dq->stride_b ||
+        dv->stride_b != dq->stride_b || dk->stride_h != dq->stride_h || dv->stride_h != dq->stride_h ||
+        dk->stride_l != dq->stride_l || dv->stride_l != dq->stride_l)
+        return fail(PRIME_ERR_INVALID_ARG, "dq, dk and dv must share dtype and strides");
+    if (!rows_aligned(q, true) || !rows_aligned(k, true) || !rows_aligned(v, true) || !rows_aligned(dy, true))
+        return fail(PRIME_ERR_MISALIGNED, "q/k/v/dy rows must start on 16-byte boundaries");
+    const size_t need = prime_selective_prefill_backward_workspace_size(B, H, L);
+    if (workspace_bytes < need || !aligned16(workspace))
+        return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes (16-byte aligned) is below the %zu needed",
+                    workspace_bytes, need);
+    int rc;
+    if ((rc = check_state(state_in, "state_in")) || (rc = check_state(dstate_out, "dstate_out")) ||
+        (rc = check_state(dstate_in, "dstate_in")))
+        return rc;
+    prime::BwdArgs a{};
+    a.q = q->data; a.k = k->data; a.v = v->data; a.dy = dy->data;
+    a.q_sb = q->stride_b; a.q_sh = q->stride_h; a.q_sl = q->stride_l;
+    a.k_sb = k->stride_b; a.k_sh = k->stride_h; a.k_sl = k->stride_l;
+    a.v_sb = v->stride_b; a.v_sh = v->stride_h; a.v_sl = v->stride_l;
+    a.dy_sb = dy->stride_b; a.dy_sh = dy->stride_h; a.dy_sl = dy->stride_l;
+    a.dt_in = q->dtype; a.dt_dy = dy->dtype;
+    a.B = B; a.H = H; a.L = L; a.decay = k_scale; a.eps = eps;  // (decay: not read in the selective form)
+    if (state_in) {
+        a.s0i = state_in->s0; a.s1i = state_in->s1; a.s2i = state_in->s2;
+        a.k0i = state_in->k0; a.k1i = state_in->k1; a.k2i = state_in->k2;
+    }
+    if (dstate_out) {
+        a.ds0o = dstate_out->s0; a.ds1o = dstate_out->s1; a.ds2o = dstate_out->s2;
+        a.dk0o = dstate_out->k0; a.dk1o = dstate_out->k1; a.dk2o = dstate_out->k2;
+    }
+    a.dq = dq->data; a.dk = dk->data; a.dv = dv->data; a.dt_g = dq->dtype;
+    a.g_sb = dq->stride_b; a.g_sh = dq->stride_h; a.g_sl = dq->stride_l;
+    if (dstate_in) {
+        a.ds0i = dstate_in->s0; a.ds1i = dstate_in->s1; a.ds2i = dstate_in->s2;
+        a.dk0i = dstate_in->k0; a.dk1i = dstate_in->k1; a.dk2i = dstate_in->k2;
+    }
+    const size_t ntok = static_cast<size_t>(B) * H * L;
+    a.inv_den = static_cast<float *>(workspace);
+    a.g_den = a.inv_den + ntok;
+    a.pq = reinterpret_cast<float *>(static_cast<char *>(workspace) + bwd_token_bytes(B, H, L));
+    a.fin = a.pq + ntok;
+    a.G = 1;
+    a.cps = (L + 63) / 64;
+    a.logd = log_decay; a.kscale = k_scale; a.dlogd = d_log_decay; a.dkscale = d_k_scale;
+    return check_hip(prime::launch_prefill_backward_f32(a, static_cast<hipStream_t>(stream)), "backward launch");
+}
+
 int prime_decode_readout(const prime_tensor_t *q, int B, int H, int D, float eps, const prime_state_t *state,
                          const prime_tensor_t *y, void *stream) {
     g_err[0] = 0;

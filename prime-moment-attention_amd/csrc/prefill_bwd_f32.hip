@@ -60,6 +60,8 @@ __device__ __forceinline__ void lower_tile(int t, int &ib, int &jb) {
 
 // The chunk's tiles: Fq, Fk (fp32 inputs), v, dy (dtype dt_dy), one token per
 // 8 threads; tokens past L are zero.  Wave 0 forms cum, e^cum and w.
+// SEL: per-token log decays (logd) and k scaled by kscale[h] as it is loaded.
+template <bool SEL>
 __device__ __forceinline__ void load_chunk(const BwdArgs &a, int b, int h, int c, int tid, int w, int lane,
                                            float (*sFq)[kPQ], float (*sFk)[kPQ], float (*sV)[kPR],
                                            float (*sDY)[kPR], float *sCum, float *sEc, float *sW, float logl) {
@@ -74,7 +76,9 @@ __device__ __forceinline__ void load_chunk(const BwdArgs &a, int b, int h, int c
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-        const f32x4 q = valid ? ld4(qp + 4 * j) : z, k = valid ? ld4(kp + 4 * j) : z, v = valid ? ld4(vp + 4 * j) : z;
+        const f32x4 q = valid ? ld4(qp + 4 * j) : z, v = valid ? ld4(vp + 4 * j) : z;
+        f32x4 k = valid ? ld4(kp + 4 * j) : z;
+        if constexpr (SEL) k *= a.kscale[h];
         f32x4 q2, k2, dy;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -91,7 +95,8 @@ __device__ __forceinline__ void load_chunk(const BwdArgs &a, int b, int h, int c
     }
     if (w == 0) {
         const bool vl = c * kC + lane < a.L;
-        float cum = vl ? logl : 0.f;
+        float cum = 0.f;
+        if (vl) cum = SEL ? a.logd[static_cast<size_t>(b * a.H + h) * a.L + c * kC + lane] : logl;
 #pragma unroll
         for (int s = 1; s < 64; s <<= 1) {
             const float x = __shfl_up(cum, s, kWave);
@@ -158,8 +163,11 @@ __device__ __forceinline__ void dscores(const BwdArgs &a, int c, int w, int g, i
 // dq pass: chunks in order, the forward state carried (M tiles of feature
 // block w in wave w's accumulators, Kf / S0 / K0 by threads 0..192).
 // ---------------------------------------------------------------------------
-// DIN: the dense double clamp with an incoming state (BwdArgs::dense_in)
-template <bool DIN>
+// DIN: the dense double clamp with an incoming state (BwdArgs::dense_in);
+// SEL: the selective form (BwdArgs::logd), which also leaves per token
+// phi_q'(i) . dphi_q'(i) (the query side of the log decays' adjoint, phi_q'
+// = [1, q, q*q]) and per sequence <dstate_out, state_out>
+template <bool DIN, bool SEL>
 __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) float sFq[kC][kPQ];
     __shared__ __attribute__((aligned(16))) float sFk[kC][kPQ];
@@ -174,6 +182,7 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
     // (sD1), l^(64c) times the outer clamp's adjoint (sHc), and l^(t+1) times the
     // part of it the inner clamp withholds from the call's tokens (sDh)
     __shared__ float sKin[kFP], sK0in[1], sD1[kC], sHc[kC], sDh[kC];
+    __shared__ float sFin[kBW];  // SEL: the waves' shares of <dstate_out, state_out>
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -192,14 +201,15 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
         for (int r = 0; r < 4; ++r) {
             const int f = 16 * w + 4 * g + r, col = 16 * dv + c16;
             float x = 0.f;
-            if (a.s1i) x = f < kD ? a.s1i[so1 + f * kD + col] : 0.5f * a.s2i[so1 + (f - kD) * kD + col];
+            // rows 64.. of M: S2/2 (S2 in the selective convention, whose S2 carries the 1/2)
+            if (a.s1i) x = f < kD ? a.s1i[so1 + f * kD + col] : (SEL ? 1.0f : 0.5f) * a.s2i[so1 + (f - kD) * kD + col];
             mt[dv][r] = x;
             sM[f][col] = x;
         }
     float kreg = 0.f;
     if (a.s1i) {
         if (tid < kD) kreg = a.k1i[so0 + tid];
-        else if (tid < kFP) kreg = 0.5f * a.k2i[so0 + tid - kD];
+        else if (tid < kFP) kreg = (SEL ? 1.0f : 0.5f) * a.k2i[so0 + tid - kD];
         else if (tid < kFP + kD) kreg = a.s0i[so0 + tid - kFP];
         else if (tid == kFP + kD) kreg = a.k0i[seq];
     }
@@ -220,7 +230,7 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
     for (int c = 0; c < NC; ++c) {
         // (din) l^(64 c): the incoming state's decay to the chunk's start
         const float lc = din ? static_cast<float>(pow(static_cast<double>(a.decay[h]), 64.0 * c)) : 0.f;
-        load_chunk(a, b, h, c, tid, w, lane, sFq, sFk, sV, sG, sCum, sEc, sW, logl);
+        load_chunk<SEL>(a, b, h, c, tid, w, lane, sFq, sFk, sV, sG, sCum, sEc, sW, logl);
         __syncthreads();
         scores(a, c, w, g, c16, sFq, sFk, sCum, sA);
         __syncthreads();
@@ -294,6 +304,11 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
             if (t < a.L) {
                 a.inv_den[static_cast<size_t>(seq) * a.L + t] = 1.0f / D;
                 a.g_den[static_cast<size_t>(seq) * a.L + t] = hh;
+                // SEL: phi_q'(i) . dphi_q'(i) = (num . dy) / D + den h.  e^cum_i scales num and
+                // den alike, so this is exactly 0 while den >= eps (h = -(num . dy) / den^2)
+                // and (num . dy) / eps where the clamp holds (h = 0): formed here without
+                // the cancellation of summing it over the features
+                if constexpr (SEL) a.pq[static_cast<size_t>(seq) * a.L + t] = sDen[i] >= a.eps ? 0.f : dot / D;
             }
         }
         for (int e = tid; e < kC * kD; e += kBW * kWave) {
@@ -391,6 +406,32 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
         else if (tid == kFP + kD) sK0[0] = kreg;
     }
     if (din && kthr) a.kcorr[static_cast<size_t>(seq) * kBwdCorr + (tid < kFP ? tid : kFP)] = corr;
+    if constexpr (SEL) {
+        // <dstate_out, state_out> in the selective convention (M rows 64.. hold S2
+        // itself, Kf rows 64.. K2): the final state's share of the log decays' adjoint
+        float fp = 0.f;
+        if (a.ds1o) {
+#pragma unroll
+            for (int dv = 0; dv < 4; ++dv)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int f = 16 * w + 4 * g + r, col = 16 * dv + c16;
+                    fp += mt[dv][r] * (f < kD ? a.ds1o[so1 + f * kD + col] : a.ds2o[so1 + (f - kD) * kD + col]);
+                }
+            if (tid < kD) fp += kreg * a.dk1o[so0 + tid];
+            else if (tid < kFP) fp += kreg * a.dk2o[so0 + tid - kD];
+            else if (tid < kFP + kD) fp += kreg * a.ds0o[so0 + tid - kFP];
+            else if (tid == kFP + kD) fp += kreg * a.dk0o[seq];
+        }
+        fp = wave_sum(fp);
+        if (lane == 0) sFin[w] = fp;
+        __syncthreads();
+        if (tid == 0) {
+            float tot = 0.f;
+            for (int i = 0; i < kBW; ++i) tot += sFin[i];
+            a.fin[seq] = tot;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -398,6 +439,11 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
 // carried (dM tiles of feature block w in wave w's accumulators, dKf / dS0 /
 // dK0 by threads 0..192); it ends as the adjoint of the incoming state.
 // ---------------------------------------------------------------------------
+// SEL: the selective form; also forms per token phi_k'(j) . dphi_k'(j), turns
+// the dq pass's query-side terms into the log decays' adjoint (a suffix sum
+// over the tokens, carried from the last chunk back) and the key scale's
+// adjoint per sequence
+template <bool SEL>
 __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) float sFq[kC][kPQ];
     __shared__ __attribute__((aligned(16))) float sFk[kC][kPQ];
@@ -406,6 +452,7 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
     __shared__ __attribute__((aligned(16))) float sA[kC][kPR];   // a, then da
     __shared__ __attribute__((aligned(16))) float sM[kFP][kPR];  // dM
     __shared__ float sKf[kFP], sS0[kD], sCum[kC], sEc[kC], sW[kC], sH[kC], sK0[1];
+    __shared__ float sPp[2][kC], sPc[kC];  // SEL: the two waves' feature parts, the constant feature's part
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -425,13 +472,13 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
             const int f = 16 * w + 4 * g + r, col = 16 * dv + c16;
             float x = 0.f;
             if (f < kD) x = a.ds1o ? a.ds1o[so1 + f * kD + col] : 0.f;
-            else x = a.ds2o ? 2.0f * a.ds2o[so1 + (f - kD) * kD + col] : 0.f;
+            else x = a.ds2o ? (SEL ? 1.0f : 2.0f) * a.ds2o[so1 + (f - kD) * kD + col] : 0.f;
             mt[dv][r] = x;
             sM[f][col] = x;
         }
     float kreg = 0.f;
     if (tid < kD) kreg = a.dk1o ? a.dk1o[so0 + tid] : 0.f;
-    else if (tid < kFP) kreg = a.dk2o ? 2.0f * a.dk2o[so0 + tid - kD] : 0.f;
+    else if (tid < kFP) kreg = a.dk2o ? (SEL ? 1.0f : 2.0f) * a.dk2o[so0 + tid - kD] : 0.f;
     else if (tid < kFP + kD) kreg = a.ds0o ? a.ds0o[so0 + tid - kFP] : 0.f;
     else if (tid == kFP + kD) kreg = a.dk0o ? a.dk0o[seq] : 0.f;
     if (tid < kFP) sKf[tid] = kreg;
@@ -440,8 +487,12 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
 
     const int NC = (a.L + kC - 1) / kC;
     const int64_t gbase = b * a.g_sb + h * a.g_sh;
+    // SEL: the suffix sum of the log decays' adjoint, carried from the last
+    // chunk back (every lane of wave 0 holds it), starting with the final
+    // state's share; and this thread's part of the key scale's adjoint
+    float dl_carry = SEL ? a.fin[seq] : 0.f, dks = 0.f;
     for (int c = NC - 1; c >= 0; --c) {
-        load_chunk(a, b, h, c, tid, w, lane, sFq, sFk, sV, sG, sCum, sEc, sW, logl);
+        load_chunk<SEL>(a, b, h, c, tid, w, lane, sFq, sFk, sV, sG, sCum, sEc, sW, logl);
         __syncthreads();
         scores(a, c, w, g, c16, sFq, sFk, sCum, sA);
         if (tid < kC) {
@@ -486,6 +537,7 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
         {
             const int tok = 16 * jb + c16;
             const float wj = sW[tok];
+            float pkp = 0.f;  // SEL: sum over this lane's features of Fk . dFk
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
                 const int db = 2 * (w & 1) + jj;
@@ -508,7 +560,38 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
                     f32x4 dk;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) dk[r] = d2[0][r] + k[r] * d2[1][r];
+                    if constexpr (SEL) {
+                        // Fk holds kscale k: dk above is the adjoint of the scaled key; the
+                        // key's is kscale times it, the scale's the sum of k times it
+                        const f32x4 kraw = ld4(static_cast<const float *>(a.k) + b * a.k_sb + h * a.k_sh +
+                                               (t0 + tok) * a.k_sl + 16 * db + 4 * g);
+                        const float ks = a.kscale[h];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            dks += kraw[r] * dk[r];
+                            dk[r] *= ks;
+                        }
+                    }
                     store4(a.dk, a.dt_g, gbase + (t0 + tok) * a.g_sl + 16 * db + 4 * g, dk);
+                }
+                if constexpr (SEL) {
+                    const f32x4 k = ld4(&sFk[tok][16 * db + 4 * g]), k2 = ld4(&sFk[tok][kD + 16 * db + 4 * g]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) pkp += k[r] * d2[0][r] + k2[r] * d2[1][r];
+                }
+            }
+            if constexpr (SEL) {
+                // the token's four lane groups, then (after the barrier) the two waves of its token block
+                pkp += __shfl_xor(pkp, 16, kWave);
+                pkp += __shfl_xor(pkp, 32, kWave);
+                if (g == 0) sPp[w & 1][tok] = pkp;
+                // the constant feature: sum_i da_ij + w_j (dS0 . v_j + dK0), dS0 and dK0 the
+                // adjoint of the state leaving the chunk
+                if (tid < kC) {
+                    float cs = 0.f, vs = 0.f;
+                    for (int i = 16 * (tid >> 4); i < kC; ++i) cs += sA[i][tid];  // (da's lower tiles)
+                    for (int d = 0; d < kD; ++d) vs += sS0[d] * sV[tid][d];
+                    sPc[tid] = cs + sW[tid] * (vs + sK0[0]);
                 }
             }
         }
@@ -542,6 +625,22 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
             }
         }
         __syncthreads();
+        if constexpr (SEL) {
+            // the log decays' adjoint: per token dc = phi_q' . dphi_q' - phi_k' . dphi_k',
+            // summed over every later token (a suffix sum over the chunk, plus the carry)
+            if (w == 0) {
+                const int64_t t = t0 + lane;
+                float x = 0.f;
+                if (t < a.L) x = a.pq[static_cast<size_t>(seq) * a.L + t] - (sPc[lane] + sPp[0][lane] + sPp[1][lane]);
+#pragma unroll
+                for (int o = 1; o < kWave; o <<= 1) {
+                    const float y = __shfl_down(x, o, kWave);
+                    if (lane + o < kWave) x += y;
+                }
+                if (t < a.L) a.dlogd[static_cast<size_t>(seq) * a.L + t] = x + dl_carry;
+                dl_carry += __shfl(x, 0, kWave);
+            }
+        }
 #pragma unroll
         for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
@@ -549,6 +648,17 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
         if (tid < kFP) sKf[tid] = kreg;
         else if (tid < kFP + kD) sS0[tid - kFP] = kreg;
         else if (tid == kFP + kD) sK0[0] = kreg;
+    }
+    if constexpr (SEL) {  // the key scale's adjoint, this sequence's share
+        const float v = wave_sum(dks);
+        __syncthreads();  // (sPp: its last readers passed the loop's barriers)
+        if (lane == 0) sPp[0][w] = v;
+        __syncthreads();
+        if (tid == 0) {
+            float tot = 0.f;
+            for (int i = 0; i < kBW; ++i) tot += sPp[0][i];
+            a.dkscale[seq] = tot;
+        }
     }
 
     // ---- adjoint of the incoming state: dS1 = dM[:64], dS2 = dM[64:] / 2, dK1, dK2 = dKf[64:] / 2
@@ -559,12 +669,12 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
             for (int r = 0; r < 4; ++r) {
                 const int f = 16 * w + 4 * g + r, col = 16 * dv + c16;
                 if (f < kD) a.ds1i[so1 + f * kD + col] = mt[dv][r];
-                else a.ds2i[so1 + (f - kD) * kD + col] = 0.5f * mt[dv][r];
+                else a.ds2i[so1 + (f - kD) * kD + col] = (SEL ? 1.0f : 0.5f) * mt[dv][r];
             }
         // (dense double clamp with a state: plus the dq pass's correction)
         const float* kc = a.dense_in ? a.kcorr + static_cast<size_t>(seq) * kBwdCorr : nullptr;
         if (tid < kD) a.dk1i[so0 + tid] = kreg + (kc ? kc[tid] : 0.f);
-        else if (tid < kFP) a.dk2i[so0 + tid - kD] = 0.5f * (kreg + (kc ? kc[tid] : 0.f));
+        else if (tid < kFP) a.dk2i[so0 + tid - kD] = (SEL ? 1.0f : 0.5f) * (kreg + (kc ? kc[tid] : 0.f));
         else if (tid < kFP + kD) a.ds0i[so0 + tid - kFP] = kreg;
         else if (tid == kFP + kD) a.dk0i[seq] = kreg + (kc ? kc[kFP] : 0.f);
     }
@@ -573,14 +683,20 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
 hipError_t launch_prefill_backward_f32(const BwdArgs &a, hipStream_t stream) {
     const dim3 grid(a.B * a.H), block(kBW * kWave);
     const TimerEvents t1 = timer_events(PRIME_KERNEL_BWD_DQ);
-    if (a.dense_in)
-        hipExtLaunchKernelGGL(prefill_bwd_dq_f32_kernel<true>, grid, block, 0, stream, t1.start, t1.stop, 0, a);
+    const bool sel = a.logd != nullptr;  // (the selective form has no dense clamp)
+    if (sel)
+        hipExtLaunchKernelGGL((prefill_bwd_dq_f32_kernel<false, true>), grid, block, 0, stream, t1.start, t1.stop, 0, a);
+    else if (a.dense_in)
+        hipExtLaunchKernelGGL((prefill_bwd_dq_f32_kernel<true, false>), grid, block, 0, stream, t1.start, t1.stop, 0, a);
     else
-        hipExtLaunchKernelGGL(prefill_bwd_dq_f32_kernel<false>, grid, block, 0, stream, t1.start, t1.stop, 0, a);
+        hipExtLaunchKernelGGL((prefill_bwd_dq_f32_kernel<false, false>), grid, block, 0, stream, t1.start, t1.stop, 0, a);
     hipError_t e;
     if ((e = hipGetLastError()) != hipSuccess) return timer_drop(t1), e;
     const TimerEvents t2 = timer_events(PRIME_KERNEL_BWD_DKV);
-    hipExtLaunchKernelGGL(prefill_bwd_dkv_f32_kernel, grid, block, 0, stream, t2.start, t2.stop, 0, a);
+    if (sel)
+        hipExtLaunchKernelGGL(prefill_bwd_dkv_f32_kernel<true>, grid, block, 0, stream, t2.start, t2.stop, 0, a);
+    else
+        hipExtLaunchKernelGGL(prefill_bwd_dkv_f32_kernel<false>, grid, block, 0, stream, t2.start, t2.stop, 0, a);
     if ((e = hipGetLastError()) != hipSuccess) timer_drop(t2);
     return e;
 }

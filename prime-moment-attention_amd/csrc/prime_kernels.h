@@ -173,6 +173,13 @@ struct BwdArgs {
     // [K1; K2/2], then K0), which the dk/dv pass adds to that adjoint
     int dense_in;
     float *kcorr;
+    // selective form (fp32 passes only): per-token natural-log decays logd
+    // [B*H, L] and the key scale kscale [H] (k enters as kscale[h] k); the
+    // states in the selective convention (S2, K2 carry the 1/2).  Outputs:
+    // dlogd [B*H, L] (the log decays' adjoint) and dkscale [B*H] (the key
+    // scale's adjoint per sequence).  Scratch: pq [B*H, L], fin [B*H].
+    const float *logd, *kscale;
+    float *dlogd, *dkscale, *pq, *fin;
 };
 constexpr int kBwdCorr = 132;  // floats per sequence in BwdArgs::kcorr (128 features, K0, padding)
 

@@ -30,7 +30,8 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_selective_decode_step", "prime_accumulate", "prime_accumulate_workspace_size",
            "prime_decode_readout", "prime_decode_update", "prime_chunked_prefill_backward",
            "prime_chunked_prefill_backward_workspace_size", "prime_chunked_prefill_qknorm",
-           "prime_selective_prefill_qknorm", "prime_accumulate_noalloc")
+           "prime_selective_prefill_qknorm", "prime_accumulate_noalloc", "prime_selective_prefill_backward",
+           "prime_selective_prefill_backward_workspace_size")
 
 # bytes of the fixed device scratch behind prime_accumulate_noalloc
 NOALLOC_SCRATCH_BYTES = 32 << 20
@@ -155,6 +156,12 @@ def load() -> ctypes.CDLL:
     L.prime_chunked_prefill_backward.restype = ctypes.c_int
     L.prime_chunked_prefill_backward_workspace_size.argtypes = [ctypes.c_int] * 3
     L.prime_chunked_prefill_backward_workspace_size.restype = ctypes.c_size_t
+    L.prime_selective_prefill_backward.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 5 + [
+        fp, fp, ctypes.c_float, P(PrimeState), P(PrimeTensor), P(PrimeState)] + [P(PrimeTensor)] * 3 + [
+        P(PrimeState), fp, fp, fp, ctypes.c_size_t, fp]
+    L.prime_selective_prefill_backward.restype = ctypes.c_int
+    L.prime_selective_prefill_backward_workspace_size.argtypes = [ctypes.c_int] * 3
+    L.prime_selective_prefill_backward_workspace_size.restype = ctypes.c_size_t
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     v = L.prime_abi_version()
     if v != ABI_VERSION:
@@ -590,6 +597,43 @@ def chunked_prefill_backward(q, k, v, decay: torch.Tensor, eps: float, state_in,
         r(descs[3]), r(so), r(descs[4]), r(descs[5]), r(descs[6]), r(sd), workspace.data_ptr(),
         workspace.numel() * workspace.element_size(), _stream(q.device))
     _check(rc, "prime_chunked_prefill_backward")
+
+
+def selective_backward_workspace_size(B: int, H: int, L: int) -> int:
+    return int(load().prime_selective_prefill_backward_workspace_size(B, H, L))
+
+
+def selective_prefill_backward(q, k, v, log_decay: torch.Tensor, k_scale: torch.Tensor, eps: float, state_in, dy,
+                               dstate_out, dq, dk, dv, dstate_in, d_log_decay: torch.Tensor,
+                               d_k_scale: torch.Tensor, workspace: Optional[torch.Tensor] = None) -> None:
+    """Backward of the selective prefill (prime_selective_prefill_backward).
+    q, k, v [B,H,L,D] fp32 (k/v with H heads), dy [B,H,L,D]; log_decay fp32
+    [B,H,L]; k_scale fp32 [H]; states (selective convention) 6-tuples or
+    None; outputs dq/dk/dv (one dtype and stride set), dstate_in,
+    d_log_decay fp32 [B,H,L] and d_k_scale fp32 [B,H] (per sequence)."""
+    _dev_check(q, k, v, dy, dq, dk, dv, log_decay, k_scale, d_log_decay, d_k_scale)
+    B, H, Lq, D = q.shape
+    for t, n in ((k, "k"), (v, "v"), (dy, "dy"), (dq, "dq"), (dk, "dk"), (dv, "dv")):
+        _shape(t, (B, H, Lq, D), n)
+    _sel_vec(log_decay, B * H * Lq, "log_decay")
+    _sel_vec(k_scale, H, "k_scale")
+    _sel_vec(d_log_decay, B * H * Lq, "d_log_decay")
+    _sel_vec(d_k_scale, B * H, "d_k_scale")
+    _check_state(state_in, B, H, D, "state_in")
+    _check_state(dstate_out, B, H, D, "dstate_out")
+    _check_state(dstate_in, B, H, D, "dstate_in")
+    if workspace is None:
+        workspace = torch.empty(max(selective_backward_workspace_size(B, H, Lq), 4), dtype=torch.uint8,
+                                device=q.device)
+    descs = [tensor_desc(t, True) for t in (q, k, v, dy, dq, dk, dv)]
+    si, so, sd = state_desc(state_in), state_desc(dstate_out), state_desc(dstate_in)
+    r = lambda x: ctypes.byref(x) if x is not None else None
+    rc = load().prime_selective_prefill_backward(
+        r(descs[0]), r(descs[1]), r(descs[2]), B, H, H, Lq, D, log_decay.data_ptr(), k_scale.data_ptr(),
+        float(eps), r(si), r(descs[3]), r(so), r(descs[4]), r(descs[5]), r(descs[6]), r(sd),
+        d_log_decay.data_ptr(), d_k_scale.data_ptr(), workspace.data_ptr(),
+        workspace.numel() * workspace.element_size(), _stream(q.device))
+    _check(rc, "prime_selective_prefill_backward")
 
 
 def accumulate_workspace_size(B: int, H: int, L: int) -> int:

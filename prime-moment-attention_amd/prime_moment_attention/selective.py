@@ -20,6 +20,16 @@ As in the reference, the parallel branch starts from a zero state: an incoming
 call covers that call's tokens.  bf16 projections run the bf16-MFMA prefill;
 fp32 projections (fp16 ones are widened to fp32) run the fp32 prefill kernel,
 as the reference computes this branch in fp32 (selective.py:363-365).
+
+When autograd records (a parameter or the input requires grad), the module
+differentiates as torch autograd does through the reference: the QK
+LayerNorm, the q scale, the grouped-head expansion, softplus/clamp of the
+step sizes and the tau and beta clamps run as torch ops, and the recurrence
+runs through ``_SelectivePrefillFn`` (the fp32 prefill forward, the HIP
+backward prime_selective_prefill_backward), which gives the gradients in q,
+k, v, the per-token log decays, beta and the incoming state.  L == 1 with a
+state then runs as a one-token prefill from that state: the reference's step
+branch (selective.py:384-409) computes the same function.
 """
 from __future__ import annotations
 
@@ -31,7 +41,44 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
-from .chunked_ssd import no_backward
+from .chunked_ssd import _prep, needs_grad
+
+
+class _SelectivePrefillFn(torch.autograd.Function):
+    """prime_selective_prefill (fp32 q/k/v with H heads) with its backward
+    (prime_selective_prefill_backward): differentiable in q, k, v, log_decay
+    [B, H, L], beta [H] and the incoming state (selective convention)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, log_decay, beta, eps, return_state, *state):
+        B, H, L, D = q.shape
+        st_in = tuple(state) if state else None
+        y = torch.empty(B, H, L, D, device=q.device, dtype=torch.float32)
+        st_out = _lib.new_state(B, H, D, q.device) if return_state else None
+        _lib.selective_prefill(q, k, v, log_decay, beta, eps, st_in, y, st_out)
+        ctx.save_for_backward(q, k, v, log_decay, beta, *(st_in or ()))
+        ctx.eps, ctx.has_state = eps, st_in is not None
+        ctx.set_materialize_grads(False)
+        return (y, *st_out) if return_state else y
+
+    @staticmethod
+    def backward(ctx, dy, *dstate):
+        q, k, v, log_decay, beta, *st = ctx.saved_tensors
+        B, H, L, D = q.shape
+        dev = q.device
+        dy = torch.zeros(B, H, L, D, device=dev, dtype=torch.float32) if dy is None else _prep(dy)
+        dso = None
+        if any(t is not None for t in dstate):
+            zs = _lib.new_state(B, H, D, dev, zero=True)
+            dso = tuple(z if t is None else t.to(torch.float32).reshape(z.shape).contiguous()
+                        for z, t in zip(zs, dstate))
+        dq, dk, dv = (torch.empty(B, H, L, D, device=dev, dtype=torch.float32) for _ in range(3))
+        dld = torch.empty(B, H, L, device=dev, dtype=torch.float32)
+        dbeta = torch.empty(B, H, device=dev, dtype=torch.float32)
+        dsi = _lib.new_state(B, H, D, dev) if ctx.has_state else None
+        _lib.selective_prefill_backward(q, k, v, log_decay, beta, ctx.eps, tuple(st) if st else None, dy, dso,
+                                        dq, dk, dv, dsi, dld, dbeta)
+        return (dq, dk, dv, dld, dbeta.sum(0), None, None, *(dsi or ()))
 
 
 class PrimeSelectiveMomentAttention(nn.Module):
@@ -101,6 +148,8 @@ class PrimeSelectiveMomentAttention(nn.Module):
         v = self.v_proj(hidden_states).view(B, L, self.num_kv_heads, D).transpose(1, 2)
         tau = self.get_tau(dev).float().contiguous()
         beta = self.get_beta(dev).float().contiguous()
+        if needs_grad(hidden_states, *self.parameters(), *(state or ())):
+            return self._mix_autograd(hidden_states, q, k, v, tau, beta, state, return_state)
         if L == 1:
             norm = _lib.qk_norm(self.q_norm if self.use_qk_norm else None,
                                 self.k_norm if self.use_qk_norm else None, self.scaling, q.dtype)
@@ -137,7 +186,24 @@ class PrimeSelectiveMomentAttention(nn.Module):
             _lib.selective_prefill(q, k, v, log_decay, beta, self.eps, None, y_bl.transpose(1, 2), next_state,
                                    qk_norm=norm)
             y = y_bl.transpose(1, 2)
-        y = no_backward("selective PRIME", y, q, k, v, tau, beta, hidden_states,
-                        *(state if state is not None else ()))
         y = y.to(orig_dtype).transpose(1, 2).reshape(B, L, H * D)
         return y, (next_state if return_state else None)
+
+    def _mix_autograd(self, hidden_states, q, k, v, tau, beta, state, return_state):
+        """``mix`` under autograd (selective.py:354-440 as torch differentiates
+        it): torch ops up to the recurrence, _SelectivePrefillFn for it."""
+        B, L, _ = hidden_states.shape
+        H, D = self.num_heads, self.head_dim
+        if self.num_kv_groups > 1:
+            k = k.repeat_interleave(self.num_kv_groups, dim=1)
+            v = v.repeat_interleave(self.num_kv_groups, dim=1)
+        if self.use_qk_norm:
+            q, k = self.q_norm(q), self.k_norm(k)
+        q = q * self.scaling
+        q, k, v = (t.to(torch.float32).contiguous() for t in (q, k, v))
+        log_decay = (-self.step_size(hidden_states).float() / tau.view(1, 1, H)).transpose(1, 2).contiguous()
+        # the parallel branch (L > 1) starts from a zero state, the step branch from `state`
+        st = _lib.as_state(state, B, H, D, q.device) if (state is not None and L == 1) else ()
+        outs = _SelectivePrefillFn.apply(q, k, v, log_decay, beta, float(self.eps), bool(return_state), *st)
+        y, next_state = (outs[0], tuple(outs[1:])) if return_state else (outs, None)
+        return y.to(hidden_states.dtype).transpose(1, 2).reshape(B, L, H * D), next_state

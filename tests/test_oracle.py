@@ -18,6 +18,9 @@ Each oracle routine is checked against something it was not written from:
                     O(L^2) routine) against the step branch applied token by
                     token; beta = 1 with a constant step reduces to the base
                     recurrence with S2, K2 halved; one token gives y = v.
+  selective_ref  <- (the float64 torch composition the selective backward
+                    tests differentiate) the step branch token by token, with
+                    and without an incoming state, the eps clamp active.
 A planted-mistake check (oracle_plant_check) shows the pins detect a wrong
 index/sign in a modified copy of the formula.
 """
@@ -427,6 +430,39 @@ def test_selective_single_token_is_v():
     np.testing.assert_allclose(y, v, rtol=1e-12)
     np.testing.assert_allclose(s[4], beta[:, None] * k[:, 0], rtol=1e-12)
     np.testing.assert_allclose(s[5], 0.5 * beta[:, None] ** 2 * k[:, 0] ** 2, rtol=1e-12)
+
+
+@pytest.mark.parametrize("with_state", [False, True])
+@pytest.mark.parametrize("eps", [1.0, 6.0])
+def test_selective_torch_composition_matches_token_steps(with_state, eps):
+    """tests/selective_ref.py (the parallel form with the incoming state
+    decayed by e^(c_i)) against oracle_selective_recurrent; eps = 6 makes the
+    denominator clamp active for some tokens."""
+    import torch
+    from selective_ref import selective_forward
+    B, H, L, D = 2, 2, 37, 8
+    BH = B * H
+    q, k, v, delta, tau, beta = _sel_inputs(BH, L, D, 98)
+    lam = np.exp(-delta / tau[:, None])
+    st = None
+    if with_state:
+        rng = np.random.default_rng(99)
+        st = (rng.standard_normal((BH, D)), 0.1 * rng.standard_normal((BH, D, D)),
+              0.1 * rng.standard_normal((BH, D, D)), 3.0 + rng.random(BH), 0.1 * rng.standard_normal((BH, D)),
+              0.1 * np.abs(rng.standard_normal((BH, D))))
+    yr, sr = O.selective_recurrent(q, k, v, lam, beta, eps=eps, state=st)
+    t = lambda x, *sh: torch.from_numpy(np.ascontiguousarray(x, dtype=np.float64)).reshape(*sh)
+    shapes = [(B, H, D), (B, H, D, D), (B, H, D, D), (B, H, 1), (B, H, D), (B, H, D)]
+    ts = tuple(t(x, *sh) for x, sh in zip(st, shapes)) if st is not None else None
+    y, so = selective_forward(t(q, B, H, L, D), t(k, B, H, L, D), t(v, B, H, L, D), t(np.log(lam), B, H, L),
+                              t(beta, B, H), eps, ts)
+    if eps > 1.0:  # the clamp changes some outputs
+        y_free, _ = selective_forward(t(q, B, H, L, D), t(k, B, H, L, D), t(v, B, H, L, D),
+                                      t(np.log(lam), B, H, L), t(beta, B, H), -1e30, ts)
+        assert not torch.allclose(y, y_free)
+    np.testing.assert_allclose(y.reshape(BH, L, D).numpy(), yr, rtol=1e-9, atol=1e-11)
+    for a, b in zip(so, sr):
+        np.testing.assert_allclose(a.reshape(-1).numpy(), np.asarray(b).reshape(-1), rtol=1e-9, atol=1e-11)
 
 
 # ---------------------------------------------------------------- reverse mode
