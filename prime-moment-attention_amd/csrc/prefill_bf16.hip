@@ -32,6 +32,14 @@ namespace {
 
 constexpr int kPV8 = kD + 16;  // sV / sVw pitch in bf16 (40 dwords, conflict-free transposed reads)
 constexpr int kSR = kD + 2;    // state copy rows: 64 value columns, the K column, a zero row
+// Pitch of the feature tiles and the state copy: 72 dwords.  On gfx950 a
+// ds_read_b128 serves 16 lanes a cycle, lane octets {0,3}, {1,2}, {4,7}, {5,6}
+// together (measured with SQ_LDS_BANK_CONFLICT), so a row read (lane = row
+// c16, 16-byte granule g) meets rows r and r+8 at granules g and g+1 in one
+// cycle: a pitch of 68 dwords puts them on the same banks (2-way conflicts on
+// every readout row read), 72 dwords on disjoint ones; ds_read_b64_tr_b16 (32
+// consecutive lanes, 8 rows) and the tile stores are conflict-free at 72 too.
+constexpr int kPS = kPT;
 
 __device__ __forceinline__ u32x4 ld16(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
 
@@ -146,14 +154,14 @@ __device__ __forceinline__ void store_row(u32x4 q, u32x4 k, u32x4 v, int row, in
         if constexpr (!STATE_ONLY) q = and4(q, m);
     }
     if constexpr (!STATE_ONLY) {
-        st16(sQf + row * kPW + col, q);
-        st16(sQf + row * kPW + kD + col, sq8(q, 1.0f));
+        st16(sQf + row * kPS + col, q);
+        st16(sQf + row * kPS + kD + col, sq8(q, 1.0f));
         st16(sV + row * kPV8 + col, v);
     }
     // selective: k enters as beta k, its square feature as beta^2 k^2 / 2 (from the
     // unrounded product), i.e. the module's beta and beta^2 / 2 weights
-    st16(sKf + row * kPW + col, SEL ? scale8(k, ks) : k);
-    st16(sKf + row * kPW + kD + col, sq8(k, SEL ? 0.5f * ks * ks : 0.5f));
+    st16(sKf + row * kPS + col, SEL ? scale8(k, ks) : k);
+    st16(sKf + row * kPS + kD + col, sq8(k, SEL ? 0.5f * ks * ks : 0.5f));
     st16(sVw + row * kPV8 + col, scale8(v, w));
     if (col == 0) sVw[row * kPV8 + kD] = f32_to_bf16_bits(w);
 }
@@ -178,11 +186,11 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
     constexpr int KI = STATE_ONLY ? 1 : kF;
     constexpr int XB = STATE_ONLY ? 1 : 2;   // tile buffers
 
-    __shared__ __attribute__((aligned(16))) uint16_t sQf[QB][QR][kPW];   // [q | q*q]
-    __shared__ __attribute__((aligned(16))) uint16_t sKf[XB][kC][kPW];   // [k | k*k/2]
+    __shared__ __attribute__((aligned(16))) uint16_t sQf[QB][QR][kPS];   // [q | q*q]
+    __shared__ __attribute__((aligned(16))) uint16_t sKf[XB][kC][kPS];   // [k | k*k/2]
     __shared__ __attribute__((aligned(16))) uint16_t sV[QB][QR][kPV8];   // [v | 1 0..0]
     __shared__ __attribute__((aligned(16))) uint16_t sVw[XB][kC][kPV8];  // [w v | w 0..0]
-    __shared__ __attribute__((aligned(16))) uint16_t sSt[QB][SR][kPW];   // bf16 [S1; S2/2 | K]^T entering the chunk
+    __shared__ __attribute__((aligned(16))) uint16_t sSt[QB][SR][kPS];   // bf16 [S1; S2/2 | K]^T entering the chunk
     __shared__ __attribute__((aligned(16))) float sS0[QB][kD];           // S0 entering the chunk
     __shared__ float sK0[QB];                                             // K0 entering the chunk
     __shared__ float sPw[kC + 2];                                         // l^n, n = 0..65
@@ -632,7 +640,7 @@ __global__ __launch_bounds__(64 * ((STATE_ONLY ? 0 : (RH ? 8 : 4)) + (UW8 ? 8 : 
 #pragma unroll
                 for (int fi = 0; fi < FI; ++fi) {
                     const uint16_t *p0 = &sKf[p][j0][16 * (FI * u + fi) + tr_c];
-                    ak[fi] = tr_op<false>(p0, p0 + 16 * kPW, 0);
+                    ak[fi] = tr_op<false>(p0, p0 + 16 * kPS, 0);
                 }
 #pragma unroll
                 for (int nb = 0; nb < NBX; ++nb) {

@@ -177,11 +177,11 @@ __device__ __forceinline__ void load_rows(Rows &R, const BwdArgs &a, int b, int 
 // DIN: the dense double clamp with an incoming state (BwdArgs::dense_in)
 template <bool DIN>
 __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t sQf[kC][kPW];   // [q | q*q]
-    __shared__ __attribute__((aligned(16))) uint16_t sKf[kC][kPW];   // [k | k*k/2]
+    __shared__ __attribute__((aligned(16))) uint16_t sQf[kC][kPT];   // [q | q*q]
+    __shared__ __attribute__((aligned(16))) uint16_t sKf[kC][kPT];   // [k | k*k/2]
     __shared__ __attribute__((aligned(16))) uint16_t sV[kC][kPV];    // [v | 0..]
     __shared__ __attribute__((aligned(16))) uint16_t sG[kC][kPV];    // dy, overwritten by the value part of G (dy / d)
-    __shared__ __attribute__((aligned(16))) uint16_t sSt[kD][kPW];   // bf16 value columns of M^T entering the chunk
+    __shared__ __attribute__((aligned(16))) uint16_t sSt[kD][kPT];   // bf16 value columns of M^T entering the chunk
     // fp32: the K column of M (the denominator's moments) entering the chunk, S0, K0
     __shared__ float sKv[kF], sS0[kD], sK0[1], sGd[kC], sPg[kC], sPw[kC + 2], sPs[kC + 2];
     __shared__ float sRedK[kF], sRedS[kD];  // the chunk's K and S0 increments
@@ -471,7 +471,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
 #pragma unroll
             for (int fb = 0; fb < 8; ++fb) {
                 const uint16_t *p0 = &sKf[32 * ks + 4 * g + tr_r][16 * fb + tr_c];
-                dphi[fb] = mfma(A, tr_op<false>(p0, p0 + 16 * kPW, 0).h, dphi[fb]);
+                dphi[fb] = mfma(A, tr_op<false>(p0, p0 + 16 * kPT, 0).h, dphi[fb]);
             }
         }
 #pragma unroll
@@ -480,7 +480,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
 #pragma unroll
             for (int fb = 0; fb < 8; ++fb) {
                 const uint16_t *p0 = &sSt[32 * ks + 4 * g + tr_r][16 * fb + tr_c];
-                dphi[fb] = mfma(A, tr_op<false>(p0, p0 + 16 * kPW, 0).h, dphi[fb]);
+                dphi[fb] = mfma(A, tr_op<false>(p0, p0 + 16 * kPT, 0).h, dphi[fb]);
             }
         }
 #pragma unroll
@@ -557,7 +557,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
 #pragma unroll
             for (int fi = 0; fi < 2; ++fi) {
                 const uint16_t *pk = &sKf[32 * ks + 4 * g + tr_r][16 * (2 * w + fi) + tr_c];
-                const bf16x8 raw = tr_op<false>(pk, pk + 16 * kPW, 0).h;
+                const bf16x8 raw = tr_op<false>(pk, pk + 16 * kPT, 0).h;
                 dk[fi] = mfma(raw, wpart, dk[fi]);
                 ak[fi] = scale_op(raw, wt);
             }
@@ -613,11 +613,11 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dq_kernel(const BwdArgs a)
 // segment's contribution sum_t l^(t-s0+1) phi_q(t) G_t^T written to its slot.
 template <bool DUAL>
 __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t sQf[kC][kPW];   // [q | q*q]
-    __shared__ __attribute__((aligned(16))) uint16_t sKf[kC][kPW];   // [k | k*k/2]
+    __shared__ __attribute__((aligned(16))) uint16_t sQf[kC][kPT];   // [q | q*q]
+    __shared__ __attribute__((aligned(16))) uint16_t sKf[kC][kPT];   // [k | k*k/2]
     __shared__ __attribute__((aligned(16))) uint16_t sV[kC][kPV];    // [v | 0..]
     __shared__ __attribute__((aligned(16))) uint16_t sG[kC][kPV];    // [dy / d | gden | 0..]
-    __shared__ __attribute__((aligned(16))) uint16_t sW[kSR][kPW];   // bf16 W^T at the chunk end
+    __shared__ __attribute__((aligned(16))) uint16_t sW[kSR][kPT];   // bf16 W^T at the chunk end
     __shared__ float sW1[kSR], sGd[kC], sPw[kC + 2];
     __shared__ __attribute__((aligned(16))) float sOm[kC];  // om_t = l^(t+1) (= sPw[t + 1]), 16-byte aligned
     __shared__ float sRed[kD], sRedG[1];  // the chunk's W1 increment (value columns, gden column)
@@ -824,7 +824,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
 #pragma unroll
             for (int fb = 0; fb < 8; ++fb) {
                 const uint16_t *p0 = &sQf[32 * ks + 4 * g + tr_r][16 * fb + tr_c];
-                dphi[fb] = mfma(A, tr_op<false>(p0, p0 + 16 * kPW, 0).h, dphi[fb]);
+                dphi[fb] = mfma(A, tr_op<false>(p0, p0 + 16 * kPT, 0).h, dphi[fb]);
             }
         }
 #pragma unroll
@@ -833,7 +833,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
 #pragma unroll
             for (int fb = 0; fb < 8; ++fb) {
                 const uint16_t *p0 = &sW[32 * ks + 4 * g + tr_r][16 * fb + tr_c];
-                dphi[fb] = mfma(A, tr_op<false>(p0, p0 + 16 * kPW, 0).h, dphi[fb]);
+                dphi[fb] = mfma(A, tr_op<false>(p0, p0 + 16 * kPT, 0).h, dphi[fb]);
             }
         }
 #pragma unroll
@@ -889,7 +889,7 @@ __global__ __launch_bounds__(256, 2) void prefill_bwd_dkv_kernel(const BwdArgs a
 #pragma unroll
             for (int fi = 0; fi < 2; ++fi) {
                 const uint16_t *p0 = &sQf[32 * ks + 4 * g + tr_r][16 * (2 * w + fi) + tr_c];
-                aq[fi] = scale_op(tr_op<false>(p0, p0 + 16 * kPW, 0).h, om);
+                aq[fi] = scale_op(tr_op<false>(p0, p0 + 16 * kPT, 0).h, om);
             }
 #pragma unroll
             for (int nb = 0; nb < 5; ++nb) {
