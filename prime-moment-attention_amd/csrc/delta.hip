@@ -358,33 +358,42 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
 
 // ---------------------------------------------------------------------------
 // Sequential scan over a window's chunks.  One workgroup of 8 waves per
-// (sequence, head), two waves per SIMD so that one wave's VALU work overlaps
-// the other's MFMAs.  Wave w owns the state rows of feature block w (S^T tiles
-// for every value block dv: 16 MFMAs per chunk) and two y tiles (token block
-// w/2, value blocks 2(w&1) and 2(w&1)+1: 8 MFMAs).  It loads only its share of
-// each chunk's record, into registers, one chunk ahead, through a buffer
-// descriptor (a fixed per-lane offset and scalar offsets: no per-load address
-// arithmetic).  The waves exchange the state as bf16 MFMA operand packs
-// through LDS: pack (dv, ks) = rows 4g..4g+3 of feature blocks 2ks and 2ks+1
-// at value column 16dv + l%16; wave w writes the half of pack (dv, w/2) that
-// holds its feature block.  The Lyapunov scale of chunk c is applied inside
-// chunk c+1 (the packs hold the unscaled state), so one barrier per chunk
-// suffices:
+// (sequence, head) in two roles, one wave of each per SIMD:
+//   state waves 0..3 carry the recurrence: wave s owns the state rows of
+//     feature blocks 2s and 2s+1 (S^T tiles for every value block dv: 32
+//     MFMAs per chunk) and publishes them as bf16 MFMA operand packs;
+//   y waves 4..7 compute the output off that chain: wave 4+v the y tiles of
+//     value block v for all four token blocks (16 MFMAs per chunk) from the
+//     same packs, and write the previous chunk's y out.
+// Only the state update carries into the next chunk, so the y work overlaps
+// the state waves' chain instead of lengthening it.  Each wave loads only its
+// role's share of each chunk's record, into registers, one chunk ahead,
+// through a buffer descriptor (a fixed per-lane offset and scalar offsets: no
+// per-load address arithmetic).  Pack (dv, ks) = rows 4g..4g+3 of feature
+// blocks 2ks and 2ks+1 at value column 16dv + l%16, written whole by state
+// wave ks.  The Lyapunov scale of chunk c is applied inside chunk c+1 (the
+// packs hold the unscaled state), so one barrier per chunk suffices:
 //   y_c      = Y0 + sc_c (S~_c Z^T)
 //   S~_{c+1} = sc_c (e^cum_63 S~_c - M^T S~_c) + R0,  sc_{c+1} from |S~_{c+1}|_F.
 // ---------------------------------------------------------------------------
 namespace {
 
 constexpr int kScanWaves = 8;
+constexpr int kStateWaves = 4;             // waves 0..3: the state; 4..7: y
+constexpr int kYThreads = (kScanWaves - kStateWaves) * kWave;
 constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor, word 3 (gfx9 family)
 
-// one wave's share of a chunk record, in registers
-struct RecW {
-    bf16x8 mt[4];  // -M^T A operands: feature block w, k-step ks
-    bf16x8 zb[4];  // Z^T B operands: token block w/2, k-step ks
-    uint2 r0[4];   // R0^T tiles: feature block w, value block dv
-    uint2 y0[2];   // Y0^T tiles: value blocks 2(w&1) + j, token block w/2
+// a state wave's share of a chunk record, in registers
+struct RecS {
+    bf16x8 mt[2][4];  // -M^T A operands: feature blocks 2s + fi, k-step ks
+    uint2 r0[2][4];   // R0^T tiles: feature blocks 2s + fi, value block dv
     float e63;
+};
+
+// a y wave's share: Z^T B operands of every token block and the Y0^T tiles of its value block
+struct RecY {
+    bf16x8 zb[4][4];  // token block tb, k-step ks
+    uint2 y0[4];      // token block tb, value block v
 };
 
 __device__ __forceinline__ bf16x8 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
@@ -396,17 +405,27 @@ __device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, int voff, int 
 }
 
 // `ro`: byte offset of the chunk's record inside the window (uniform)
-__device__ __forceinline__ void load_recw(RecW &R, __amdgpu_buffer_rsrc_t rs, int ro, int w, int lane) {
-    const int v16 = lane * 16, v8 = lane * 8, tb = w >> 1, dvy = 2 * (w & 1);
+__device__ __forceinline__ void load_recs(RecS &R, __amdgpu_buffer_rsrc_t rs, int ro, int sw, int lane) {
+    const int v16 = lane * 16, v8 = lane * 8;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) R.mt[ks] = bload16(rs, v16, ro + kRecMT + (w * 4 + ks) * 1024);
+    for (int fi = 0; fi < 2; ++fi)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) R.zb[ks] = bload16(rs, v16, ro + kRecZB + (tb * 4 + ks) * 1024);
+        for (int ks = 0; ks < 4; ++ks) R.mt[fi][ks] = bload16(rs, v16, ro + kRecMT + ((2 * sw + fi) * 4 + ks) * 1024);
 #pragma unroll
-    for (int dv = 0; dv < 4; ++dv) R.r0[dv] = bload8(rs, v8, ro + kRecR0 + (w * 4 + dv) * 512);
+    for (int fi = 0; fi < 2; ++fi)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) R.y0[j] = bload8(rs, v8, ro + kRecY0 + (tb * 4 + dvy + j) * 512);
+        for (int dv = 0; dv < 4; ++dv) R.r0[fi][dv] = bload8(rs, v8, ro + kRecR0 + ((2 * sw + fi) * 4 + dv) * 512);
     R.e63 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, ro + kRecSC, 0));
+}
+
+__device__ __forceinline__ void load_recy(RecY &R, __amdgpu_buffer_rsrc_t rs, int ro, int v, int lane) {
+    const int v16 = lane * 16, v8 = lane * 8;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) R.zb[tb][ks] = bload16(rs, v16, ro + kRecZB + (tb * 4 + ks) * 1024);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) R.y0[tb] = bload8(rs, v8, ro + kRecY0 + (tb * 4 + v) * 512);
 }
 
 template <int DTY>
@@ -435,42 +454,23 @@ struct YStage {
     static constexpr int bytes = kC * pitch;    // one chunk
 };
 
-// y^T tiles (value blocks DV0, DV0+1; this wave's token block) = Y0^T + sc S~ Z^T,
-// into the chunk's LDS stage (DV0 a template constant: a runtime index would
-// put the packs in scratch memory)
-template <int DTY, int DV0>
-__device__ __forceinline__ void y_tiles(const bf16x8 (&pk)[4][4], const RecW &cur, float sc, uint8_t *ystage,
-                                        int tb, int g, int c16) {
-    using YS = YStage<DTY>;
-    f32x4 p[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) p[j] = mfma(pk[DV0 + j][ks], cur.zb[ks], p[j]);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const f32x4 y0 = unpack4(cur.y0[j]);
-        f32x4 yv;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) yv[r] = y0[r] + sc * p[j][r];
-        store_y4<DTY>(ystage + (16 * tb + c16) * YS::pitch + (16 * (DV0 + j) + 4 * g) * YS::es, yv);
-    }
-}
-
-// Write a staged chunk of y (LDS) to global memory: thread t takes 16-byte
-// segments t, t + 512, ... of the chunk's rows.  GUARD skips tokens at or past
-// L; only the call's last chunk can hold such tokens, and only the write after
-// the loop can reach it, so the writes inside the loop carry no condition (a
-// conditional store would leave the compiler to count outstanding memory
-// operations for both paths, and its conservative count would then wait for
-// the store at the next record wait).
-template <int DTY, bool GUARD>
+// Write a staged chunk of y (LDS) to global memory: thread t of `nt` takes
+// 16-byte segments t, t + nt, ... of the chunk's rows.  GUARD skips tokens at
+// or past L; only the call's last chunk can hold such tokens, and only the
+// write after the loop can reach it, so the writes inside the loop carry no
+// condition (a conditional store would leave the compiler to count
+// outstanding memory operations for both paths, and its conservative count
+// would then wait for the store at the next record wait).
+template <int DTY, bool GUARD, int NT = kYThreads>
 __device__ __forceinline__ void y_write(const DeltaArgs &a, int c, const uint8_t *ystage, uint8_t *ychunk,
-                                        int64_t yrow_bytes, int tid) {
+                                        int64_t yrow_bytes, int t) {
     using YS = YStage<DTY>;
     constexpr int segs = kD * YS::es / 16;  // 16-byte segments per row
+    static_assert((kC * segs) % NT == 0, "whole segments per thread");
+    // a fixed trip count, so that the compiler counts this thread's stores exactly
 #pragma unroll
-    for (int i = tid; i < kC * segs; i += kScanWaves * kWave) {
+    for (int j = 0; j < kC * segs / NT; ++j) {
+        const int i = t + j * NT;
         const int row = i / segs, sg = i - row * segs;
         if (!GUARD || c * kC + row < a.L)
             *reinterpret_cast<u32x4 *>(ychunk + row * yrow_bytes + 16 * sg) =
@@ -478,65 +478,100 @@ __device__ __forceinline__ void y_write(const DeltaArgs &a, int c, const uint8_t
     }
 }
 
-// One chunk of the scan.  `cur` holds this chunk's record share; `nxt`
-// receives the next chunk's.  Called with the two register sets swapped on
-// alternate chunks, so that no copy (and no wait for the loads) is needed.
-// `yrow`: this lane's y row (token 16 (w/2) + l%16 of the chunk).
-template <int DTY, bool WRITE_PREV>
-__device__ __forceinline__ void scan_chunk(const DeltaArgs &a, int cw, int w, int lane, int g, int c16,
-                                           __amdgpu_buffer_rsrc_t rs, f32x4 (&st)[4], float &sc, const RecW &cur,
-                                           RecW &nxt, bf16x8 (*sPk)[4][4][64], float (*sRed)[kScanWaves],
-                                           uint8_t *sY, uint8_t *ychunk, int64_t yrow_bytes) {
+// the pending Lyapunov scale of the state entering the next chunk (every wave)
+__device__ __forceinline__ float clamp_scale(const DeltaArgs &a, const float *red) {
+    if (!(a.bound > 0.f)) return 1.0f;
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < kStateWaves; ++i) t += red[i];
+    return fminf(1.0f, a.bound / (sqrtf(t) + 1e-6f));
+}
+
+// One chunk of a state wave.  `cur` holds this chunk's record share; `nxt2`
+// receives the share of the chunk after the next one: the state waves keep
+// three register sets in rotation, so each share is loaded two chunk periods
+// before its use (with one, the chain waited on the memory latency of every
+// chunk's share: 4.38 ms against 3.50 ms at config 5 with no loads at all).
+__device__ __forceinline__ void state_chunk(const DeltaArgs &a, int cw, int sw, int lane, __amdgpu_buffer_rsrc_t rs,
+                                            f32x4 (&st)[2][4], float &sc, const RecS &cur, RecS &nxt2,
+                                            bf16x8 (*sPk)[4][4][64], float (*sRed)[kStateWaves]) {
     const int buf = cw & 1;
-    const int tb = w >> 1;
-    // next chunk's share (clamped to the window: the duplicate is unused)
-    load_recw(nxt, rs, min(cw + 1, a.nw - 1) * static_cast<int>(kDeltaRecBytes), w, lane);
-    // the previous chunk's y, staged before the last barrier (stores issued
-    // after the loads above, so that waiting for those never waits for them)
-    if constexpr (WRITE_PREV)
-        y_write<DTY, false>(a, a.c0 + cw - 1, sY + (buf ^ 1) * YStage<DTY>::bytes, ychunk - kC * yrow_bytes,
-                            yrow_bytes, threadIdx.x);
+    // share of chunk cw + 2 (clamped to the window: the duplicate is unused),
+    // issued as one group ahead of this chunk's work (kept there: interleaved
+    // with the MFMAs, the compiler's counts waited on these fresh loads)
+    load_recs(nxt2, rs, min(cw + 2, a.nw - 1) * static_cast<int>(kDeltaRecBytes), sw, lane);
+    __builtin_amdgcn_sched_barrier(0);
     bf16x8 pk[4][4];
 #pragma unroll
     for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) pk[dv][ks] = sPk[buf][dv][ks][lane];
-    // ---- y^T (value blocks 2(w&1), 2(w&1)+1; token block tb), into this chunk's stage
-    uint8_t *ys = sY + buf * YStage<DTY>::bytes;
-    if (w & 1) y_tiles<DTY, 2>(pk, cur, sc, ys, tb, g, c16);
-    else y_tiles<DTY, 0>(pk, cur, sc, ys, tb, g, c16);
-    // ---- S~'^T = sc (e^cum_63 S~^T - M^T S~^T) + R0^T on feature block w
+    // ---- S~'^T = sc (e^cum_63 S~^T - M^T S~^T) + R0^T on feature blocks 2sw, 2sw + 1
     float ss = 0.f;
 #pragma unroll
     for (int dv = 0; dv < 4; ++dv) {
-        f32x4 x;
+        f32x4 x[2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) x[r] = cur.e63 * st[dv][r];
+        for (int fi = 0; fi < 2; ++fi)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) x = mfma(cur.mt[ks], pk[dv][ks], x);
-        const f32x4 r0 = unpack4(cur.r0[dv]);
+            for (int r = 0; r < 4; ++r) x[fi][r] = cur.e63 * st[fi][dv][r];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            x[r] = sc * x[r] + r0[r];
-            ss += x[r] * x[r];
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int fi = 0; fi < 2; ++fi) x[fi] = mfma(cur.mt[fi][ks], pk[dv][ks], x[fi]);
+#pragma unroll
+        for (int fi = 0; fi < 2; ++fi) {
+            const f32x4 r0 = unpack4(cur.r0[fi][dv]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                x[fi][r] = sc * x[fi][r] + r0[r];
+                ss += x[fi][r] * x[fi][r];
+            }
+            st[fi][dv] = x[fi];
         }
-        st[dv] = x;
+        // pack (dv, sw) of the next chunk: rows 4g..4g+3 of both feature blocks
+        const uint2 lo = pack4(x[0]), hi = pack4(x[1]);
+        sPk[buf ^ 1][dv][sw][lane] = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
     }
-#pragma unroll
-    for (int dv = 0; dv < 4; ++dv)
-        *reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(&sPk[buf ^ 1][dv][tb][lane]) + 8 * (w & 1)) =
-            pack4(st[dv]);
     ss = wave_sum(ss);
-    if (lane == 0) sRed[buf][w] = ss;
+    if (lane == 0) sRed[buf][sw] = ss;
     __syncthreads();
-    // ---- Lyapunov clamp (:266-270), kept as the pending scale of the state
-    sc = 1.0f;
-    if (a.bound > 0.f) {
-        float t = 0.f;
+    sc = clamp_scale(a, sRed[buf]);  // Lyapunov clamp (:266-270), kept as the pending scale
+}
+
+// One chunk of a y wave: y^T tiles of value block v (all token blocks) = Y0^T +
+// sc S~ Z^T into the chunk's LDS stage, after writing the previous chunk's
+// staged y (WRITE_PREV) to global memory.
+template <int DTY, bool WRITE_PREV>
+__device__ __forceinline__ void y_chunk(const DeltaArgs &a, int cw, int v, int lane, int g, int c16,
+                                        __amdgpu_buffer_rsrc_t rs, float &sc, const RecY &cur, RecY &nxt,
+                                        bf16x8 (*sPk)[4][4][64], float (*sRed)[kStateWaves], uint8_t *sY,
+                                        uint8_t *ychunk, int64_t yrow_bytes, int ty) {
+    using YS = YStage<DTY>;
+    const int buf = cw & 1;
+    load_recy(nxt, rs, min(cw + 1, a.nw - 1) * static_cast<int>(kDeltaRecBytes), v, lane);
+    bf16x8 pk[4];
 #pragma unroll
-        for (int i = 0; i < kScanWaves; ++i) t += sRed[buf][i];
-        sc = fminf(1.0f, a.bound / (sqrtf(t) + 1e-6f));
+    for (int ks = 0; ks < 4; ++ks) pk[ks] = sPk[buf][v][ks][lane];
+    uint8_t *ys = sY + buf * YS::bytes;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        f32x4 p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) p = mfma(pk[ks], cur.zb[tb][ks], p);
+        const f32x4 y0 = unpack4(cur.y0[tb]);
+        f32x4 yv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) yv[r] = y0[r] + sc * p[r];
+        store_y4<DTY>(ys + (16 * tb + c16) * YS::pitch + (16 * v + 4 * g) * YS::es, yv);
     }
+    // the previous chunk's y, staged before the last barrier: stored after this
+    // chunk's use of `cur`, so that the wait for `cur` (loaded one chunk ago)
+    // covers only stores issued a chunk ago, never the loads of `nxt` just issued
+    if constexpr (WRITE_PREV)
+        y_write<DTY, false>(a, a.c0 + cw - 1, sY + (buf ^ 1) * YS::bytes, ychunk - kC * yrow_bytes, yrow_bytes, ty);
+    __syncthreads();
+    sc = clamp_scale(a, sRed[buf]);
 }
 
 }  // namespace
@@ -545,7 +580,7 @@ template <int DTY>
 __global__ __launch_bounds__(kScanWaves * kWave, 1) void delta_scan_kernel(const DeltaArgs a) {
     __shared__ __attribute__((aligned(16))) bf16x8 sPk[2][4][4][64];  // [buf][dv][ks][lane]
     __shared__ __attribute__((aligned(16))) uint8_t sY[2 * YStage<DTY>::bytes];  // y of two chunks
-    __shared__ float sRed[2][kScanWaves];
+    __shared__ float sRed[2][kStateWaves];
 
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -557,22 +592,7 @@ __global__ __launch_bounds__(kScanWaves * kWave, 1) void delta_scan_kernel(const
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         a.ws_rec + static_cast<size_t>(seq) * a.nw * kDeltaRecBytes, 0,
         static_cast<int>(static_cast<size_t>(a.nw) * kDeltaRecBytes), kBufWord3);
-
-    // ---- state entering the window: st[dv][r] = S[d = 16dv + c16][e = 16w + 4g + r]
-    const float *src = a.first ? a.state_in : a.ws_state;
-    f32x4 st[4];
-#pragma unroll
-    for (int dv = 0; dv < 4; ++dv)
-        st[dv] = src ? *reinterpret_cast<const f32x4 *>(src + sofs + (16 * dv + c16) * kP + 16 * w + 4 * g)
-                     : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int dv = 0; dv < 4; ++dv)
-        *reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(&sPk[0][dv][w >> 1][lane]) + 8 * (w & 1)) =
-            pack4(st[dv]);
-    float sc = 1.0f;  // pending Lyapunov scale of the state in st / the packs
-    RecW ra, rb;
-    load_recw(ra, rs, 0, w, lane);
-    __syncthreads();
+    float sc = 1.0f;  // pending Lyapunov scale of the state in the packs
 
     // the y rows of the window's first chunk, advanced by one chunk per step
     constexpr int es = YStage<DTY>::es;
@@ -580,35 +600,72 @@ __global__ __launch_bounds__(kScanWaves * kWave, 1) void delta_scan_kernel(const
     uint8_t *ychunk = static_cast<uint8_t *>(a.y) +
                       (b * a.y_sb + h * a.y_sh + static_cast<int64_t>(a.c0) * kC * a.y_sl) * es;
     const int64_t ystep = kC * yrow_bytes;
-    // chunk 0 (no earlier y to write), then pairs of chunks writing the y of
-    // the chunk before each
-    scan_chunk<DTY, false>(a, 0, w, lane, g, c16, rs, st, sc, ra, rb, sPk, sRed, sY, ychunk, yrow_bytes);
-    ychunk += ystep;
-    int cw = 1;
-    for (; cw + 1 < a.nw; cw += 2) {
-        scan_chunk<DTY, true>(a, cw, w, lane, g, c16, rs, st, sc, rb, ra, sPk, sRed, sY, ychunk, yrow_bytes);
-        scan_chunk<DTY, true>(a, cw + 1, w, lane, g, c16, rs, st, sc, ra, rb, sPk, sRed, sY, ychunk + ystep,
-                              yrow_bytes);
-        ychunk += 2 * ystep;
-    }
-    if (cw < a.nw) {
-        scan_chunk<DTY, true>(a, cw, w, lane, g, c16, rs, st, sc, rb, ra, sPk, sRed, sY, ychunk, yrow_bytes);
-        ychunk += ystep;
-    }
-    // the last chunk's y (staged before the last barrier)
-    y_write<DTY, true>(a, a.c0 + a.nw - 1, sY + ((a.nw - 1) & 1) * YStage<DTY>::bytes, ychunk - ystep, yrow_bytes,
-                       tid);
 
-    // ---- state leaving the window (the pending scale applied)
-    float *dst = a.last ? a.state_out : a.ws_state;
-    if (dst) {
+    if (w < kStateWaves) {
+        const int sw = w;
+        // ---- state entering the window: st[fi][dv][r] = S[d = 16dv + c16][e = 16(2sw + fi) + 4g + r]
+        const float *src = a.first ? a.state_in : a.ws_state;
+        f32x4 st[2][4];
+#pragma unroll
+        for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+            for (int dv = 0; dv < 4; ++dv)
+                st[fi][dv] = src ? *reinterpret_cast<const f32x4 *>(src + sofs + (16 * dv + c16) * kP +
+                                                                    16 * (2 * sw + fi) + 4 * g)
+                                 : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dv = 0; dv < 4; ++dv) {
-            f32x4 x = st[dv];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) x[r] *= sc;
-            *reinterpret_cast<f32x4 *>(dst + sofs + (16 * dv + c16) * kP + 16 * w + 4 * g) = x;
+            const uint2 lo = pack4(st[0][dv]), hi = pack4(st[1][dv]);
+            sPk[0][dv][sw][lane] = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
         }
+        RecS ra, rb, rc;
+        load_recs(ra, rs, 0, sw, lane);
+        load_recs(rb, rs, min(1, a.nw - 1) * static_cast<int>(kDeltaRecBytes), sw, lane);
+        __syncthreads();
+        int cw = 0;
+        for (; cw + 2 < a.nw; cw += 3) {
+            state_chunk(a, cw, sw, lane, rs, st, sc, ra, rc, sPk, sRed);
+            state_chunk(a, cw + 1, sw, lane, rs, st, sc, rb, ra, sPk, sRed);
+            state_chunk(a, cw + 2, sw, lane, rs, st, sc, rc, rb, sPk, sRed);
+        }
+        if (cw < a.nw) state_chunk(a, cw, sw, lane, rs, st, sc, ra, rc, sPk, sRed);
+        if (cw + 1 < a.nw) state_chunk(a, cw + 1, sw, lane, rs, st, sc, rb, ra, sPk, sRed);
+        // ---- state leaving the window (the pending scale applied)
+        float *dst = a.last ? a.state_out : a.ws_state;
+        if (dst) {
+#pragma unroll
+            for (int fi = 0; fi < 2; ++fi)
+#pragma unroll
+                for (int dv = 0; dv < 4; ++dv) {
+                    f32x4 x = st[fi][dv];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) x[r] *= sc;
+                    *reinterpret_cast<f32x4 *>(dst + sofs + (16 * dv + c16) * kP + 16 * (2 * sw + fi) + 4 * g) = x;
+                }
+        }
+    } else {
+        const int v = w - kStateWaves, ty = tid - kStateWaves * kWave;
+        RecY ra, rb;
+        load_recy(ra, rs, 0, v, lane);
+        __syncthreads();
+        // chunk 0 (no earlier y to write), then pairs of chunks writing the y of
+        // the chunk before each
+        y_chunk<DTY, false>(a, 0, v, lane, g, c16, rs, sc, ra, rb, sPk, sRed, sY, ychunk, yrow_bytes, ty);
+        ychunk += ystep;
+        int cw = 1;
+        for (; cw + 1 < a.nw; cw += 2) {
+            y_chunk<DTY, true>(a, cw, v, lane, g, c16, rs, sc, rb, ra, sPk, sRed, sY, ychunk, yrow_bytes, ty);
+            y_chunk<DTY, true>(a, cw + 1, v, lane, g, c16, rs, sc, ra, rb, sPk, sRed, sY, ychunk + ystep,
+                               yrow_bytes, ty);
+            ychunk += 2 * ystep;
+        }
+        if (cw < a.nw) {
+            y_chunk<DTY, true>(a, cw, v, lane, g, c16, rs, sc, rb, ra, sPk, sRed, sY, ychunk, yrow_bytes, ty);
+            ychunk += ystep;
+        }
+        // the last chunk's y (staged before the last barrier)
+        y_write<DTY, true>(a, a.c0 + a.nw - 1, sY + ((a.nw - 1) & 1) * YStage<DTY>::bytes, ychunk - ystep,
+                           yrow_bytes, ty);
     }
 }
 
