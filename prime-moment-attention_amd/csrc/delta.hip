@@ -742,11 +742,19 @@ namespace {
 // process.  A call holds its set's lock for its whole enqueue sequence, so
 // that calls on different streams never share events and calls from several
 // host threads on one stream do not interleave their records and waits.
+// The record space is used as up to kRecParts parts of one window each: with
+// three, the prep of window w+2 waits only for the scan of window w-1, so it
+// runs a whole window ahead of the scan that reads it and the scan stream
+// never stalls on a cross-stream event (with two, every window paid the event
+// latency twice: prep waiting for the scan two windows back, then the scan
+// for that prep).
+constexpr int kRecParts = 3;
+
 struct SideStream {
     int dev = -1;
     hipStream_t caller = nullptr;
     hipStream_t s = nullptr;
-    hipEvent_t start = nullptr, prep[2] = {nullptr, nullptr}, scan[2] = {nullptr, nullptr};
+    hipEvent_t start = nullptr, prep[kRecParts] = {nullptr, nullptr, nullptr}, scan[kRecParts] = {nullptr, nullptr, nullptr};
     std::mutex mu;
 };
 
@@ -769,7 +777,7 @@ SideStream *side_stream(hipStream_t caller, bool may_create) {
     const unsigned f = hipEventDisableTiming;
     if (hipStreamCreateWithFlags(&x.s, hipStreamNonBlocking) != hipSuccess) return nullptr;
     if (hipEventCreateWithFlags(&x.start, f) != hipSuccess) return nullptr;
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kRecParts; ++i)
         if (hipEventCreateWithFlags(&x.prep[i], f) != hipSuccess || hipEventCreateWithFlags(&x.scan[i], f) != hipSuccess)
             return nullptr;
     x.dev = dev;
@@ -832,25 +840,31 @@ hipError_t launch_delta_prefill(DeltaArgs a, int NC, int cap, hipStream_t stream
         return hipGetLastError();
     }
     std::lock_guard<std::mutex> lk(ss->mu);
-    const int half = cap / 2;
-    const size_t half_bytes = static_cast<size_t>(a.B) * a.H * half * delta_rec_bytes(a.dt_in);
-    const int nwin = (NC + half - 1) / half;
+    // parts of the record space: three when it holds three windows of 64
+    // chunks or more (the recommended workspace does), else two halves
+    const int nparts = cap >= kRecParts * 64 ? kRecParts : 2;
+    const int part = cap / nparts;
+    const size_t part_bytes = static_cast<size_t>(a.B) * a.H * part * delta_rec_bytes(a.dt_in);
+    const int nwin = (NC + part - 1) / part;
     hipError_t e;
     if ((e = hipEventRecord(ss->start, stream)) != hipSuccess) return e;
     if ((e = hipStreamWaitEvent(ss->s, ss->start, 0)) != hipSuccess) return e;
-    // prep of window 0
-    launch_prep(window_args(a, 0, half, NC, rec0), ss->s);
-    if ((e = hipEventRecord(ss->prep[0], ss->s)) != hipSuccess) return e;
+    // preps of the first nparts - 1 windows: their parts are free
+    for (int w = 0; w + 1 < nparts && w < nwin; ++w) {
+        launch_prep(window_args(a, w * part, part, NC, rec0 + w * part_bytes), ss->s);
+        if ((e = hipEventRecord(ss->prep[w], ss->s)) != hipSuccess) return e;
+    }
     for (int w = 0; w < nwin; ++w) {
-        const int hb = w & 1;
-        if ((e = hipStreamWaitEvent(stream, ss->prep[hb], 0)) != hipSuccess) return e;
-        launch_scan(window_args(a, w * half, half, NC, rec0 + hb * half_bytes), stream);
-        if ((e = hipEventRecord(ss->scan[hb], stream)) != hipSuccess) return e;
-        if (w + 1 < nwin) {
-            const int nb = hb ^ 1;
-            // the half about to be overwritten was read by the scan of window w-1
+        const int pb = w % nparts;
+        if ((e = hipStreamWaitEvent(stream, ss->prep[pb], 0)) != hipSuccess) return e;
+        launch_scan(window_args(a, w * part, part, NC, rec0 + pb * part_bytes), stream);
+        if ((e = hipEventRecord(ss->scan[pb], stream)) != hipSuccess) return e;
+        const int wn = w + nparts - 1;  // the next window to prepare
+        if (wn < nwin) {
+            const int nb = wn % nparts;
+            // its part was last read by the scan of window wn - nparts = w - 1
             if (w >= 1 && (e = hipStreamWaitEvent(ss->s, ss->scan[nb], 0)) != hipSuccess) return e;
-            launch_prep(window_args(a, (w + 1) * half, half, NC, rec0 + nb * half_bytes), ss->s);
+            launch_prep(window_args(a, wn * part, part, NC, rec0 + nb * part_bytes), ss->s);
             if ((e = hipEventRecord(ss->prep[nb], ss->s)) != hipSuccess) return e;
         }
     }

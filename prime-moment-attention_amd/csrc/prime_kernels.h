@@ -244,7 +244,7 @@ constexpr int kDeltaChunk = 64;
 constexpr size_t kDeltaStateBytes = static_cast<size_t>(kD) * 2 * kD * sizeof(float);  // one (b,h) state
 constexpr size_t kDeltaRecBytes = 73984;         // per-chunk transfer record, bf16 inputs (multiple of 256)
 constexpr size_t kDeltaRecBytesF32 = 147712;     // per-chunk transfer record, fp32 inputs (fp32 operands)
-constexpr int kDeltaDefaultWindow = 128;         // record chunks of the recommended workspace
+constexpr int kDeltaDefaultWindow = 192;         // record chunks of the recommended workspace (3 windows of 64)
 
 // Record bytes per chunk for inputs of dtype `dt_in`.
 inline size_t delta_rec_bytes(int dt_in) { return dt_in == PRIME_F32 ? kDeltaRecBytesF32 : kDeltaRecBytes; }
