@@ -163,7 +163,8 @@ __global__ __launch_bounds__(256) void head_layernorm_kernel(const HeadNormArgs 
             for (int e = 0; e < VE; ++e) { v[e] -= mean; q += v[e] * v[e]; }
 #pragma unroll
             for (int o = LPR / 2; o >= 1; o >>= 1) q += __shfl_xor(q, o, kWave);
-            const float rs = rsqrtf(q * (1.0f / kD) + a.ln_eps);
+            // v_rsq_f32 (as the prefill's QK-norm on load, which must give the same bits)
+            const float rs = __builtin_amdgcn_rsqf(q * (1.0f / kD) + a.ln_eps);
 #pragma unroll
             for (int e = 0; e < VE; ++e) v[e] = Group<DT>::round(fmaf(v[e] * rs, w[e], bb[e]));
         }

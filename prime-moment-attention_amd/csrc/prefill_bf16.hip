@@ -99,7 +99,10 @@ __device__ __forceinline__ u32x4 norm_row8(u32x4 x, bool affine, const float *w,
         sq += xor_lane<4>(sq);
         sq += xor_lane<2>(sq);
         sq += xor_lane<1>(sq);
-        const float rs = rsqrtf(sq * (1.0f / kD) + eps);
+        // v_rsq_f32 itself: rsqrtf adds a denormal guard (compare, two scalings,
+        // selects) that an argument of at least eps never takes; head_layernorm
+        // uses the same instruction, so both give the same bits
+        const float rs = __builtin_amdgcn_rsqf(sq * (1.0f / kD) + eps);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = fmaf(v[e] * rs, w[col + e], b[col + e]);
         if (scale == 1.0f) return pack8(v);
