@@ -202,8 +202,10 @@ size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags)
  *               prime_delta_prefill_workspace_size(B, H, 64, f)) makes the call
  *               process the sequence in more, shorter windows; results agree.
  * When the workspace holds fewer chunks than the sequence, the per-chunk
- * solve of the next window runs on a side stream while the current window is
- * scanned on `stream`.  The library keeps one side stream and its events per
+ * solve of later windows runs on a side stream while the current window is
+ * scanned on `stream` (two windows ahead when the workspace holds three
+ * windows of 64 chunks, as the recommended size does; one window ahead with
+ * less).  The library keeps one side stream and its events per
  * (device, caller stream), created on the first such call outside graph
  * capture and held for the life of the process; a call holds them for its
  * whole enqueue sequence, so calls on different streams or threads are
