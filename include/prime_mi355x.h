@@ -55,11 +55,17 @@ extern "C" {
    q/k/v (the fp32 path's per-chunk records are twice the bf16 path's) */
 #define PRIME_FLAG_F32_INPUTS 2u
 
+/* tensor layouts (prime_tensor_t.layout) */
+#define PRIME_LAYOUT_STRIDED 0 /* the strided view below */
+#define PRIME_LAYOUT_FRAG    1 /* y of the decode steps only: the [B, H*D] output
+                                  in the fragment layout of prime_linear_frag
+                                  (bf16; B padded to a multiple of 16 rows) */
+
 /* A strided [B, H, L, D] view (decode calls ignore stride_l). */
 typedef struct prime_tensor {
     void   *data;
     int32_t dtype;      /* PRIME_F32 / PRIME_BF16 / PRIME_F16 */
-    int32_t reserved;
+    int32_t layout;     /* PRIME_LAYOUT_STRIDED (0) unless stated */
     int64_t stride_b;   /* strides in ELEMENTS */
     int64_t stride_h;
     int64_t stride_l;
@@ -357,6 +363,54 @@ int prime_selective_decode_step(const prime_tensor_t *q, const prime_tensor_t *k
                                 const prime_state_t *state_out, const prime_tensor_t *y, void *stream);
 
 /*
+ * Fragment layout and the decode step's projections.  No counterpart in the
+ * reference: they are the MI355X form of the one-token step of
+ * PrimeForCausalLM (model.py:101-118 per block, model.py:160 for the lm_head,
+ * model.py:230-231 for the greedy token), where each projection sees only a
+ * few hundred rows.
+ *
+ * Fragment layout of a bf16 matrix X[R, K] (K a multiple of 32; R padded to
+ * prime_frag_rows(R) = R rounded up to a multiple of 32, padding rows zero or
+ * ignored): 16 x 32 blocks in row-block-major order, each block the 64 lane
+ * slots of 8 elements of one MFMA operand,
+ *   X(r, k) at ((r/16) (K/32) + k/32) * 512 + (r%16 + 16 ((k%32)/8)) * 8 + k%8.
+ *
+ * prime_pack_frag: out (fragment layout, prime_frag_rows(M) x K) <- M rows of
+ * the row-major bf16 matrix src (row stride ld, src_rows rows): row r is src
+ * row rows[r] (an embedding gather; ids outside [0, src_rows) give a zero
+ * row) or row r when rows is NULL.  Weights are packed once; the step packs
+ * its token embeddings per call.
+ *
+ * prime_linear_frag: y = epilogue(s . (x w^T) + bias) for x (fragment layout,
+ * prime_frag_rows(M) x K) and w (fragment layout, N x K), bf16, fp32
+ * accumulation, K = 256 x {1, 2, 3, 4, 6, 12}, N a multiple of 16.
+ *   flags PRIME_LINEAR_RMS: s = rsqrt(mean_k x^2 + rms_eps) per row (the
+ *     RMSNorm before the projection, its weight multiplied into w's columns);
+ *     otherwise s = 1.  bias: fp32 [N] or NULL.  The product is rounded to
+ *     bf16 once, then
+ *   epilogue PRIME_EPILOGUE_GELU: exact-erf GELU, rounded again;
+ *   epilogue PRIME_EPILOGUE_RESIDUAL: y = r + product, rounded (r in y's
+ *     layout; r == y updates in place).
+ *   flags PRIME_LINEAR_OUT_FRAG: y (and r) in the fragment layout
+ *     (prime_frag_rows(M) x N, N a multiple of 32); otherwise y row-major
+ *     [M, ldy], 8-byte aligned rows.
+ *   tokens (row-major output only): the greedy token of every row, argmax of
+ *     the rounded products (first index of the largest, NaN largest), into
+ *     int64 [M]; y may then be NULL (no logits written).  Needs a workspace
+ *     of prime_linear_frag_workspace_size(M, N, K) bytes.
+ * y must not overlap x or w.
+ */
+#define PRIME_LINEAR_RMS      1u
+#define PRIME_LINEAR_OUT_FRAG 2u
+int prime_frag_rows(int M);
+int prime_pack_frag(const void *src, int64_t ld, int64_t src_rows, const int64_t *rows, int M, int K, void *out,
+                    void *stream);
+size_t prime_linear_frag_workspace_size(int M, int N, int K);
+int prime_linear_frag(const void *x, const void *w, const void *r, void *y, int M, int N, int K, int64_t ldy,
+                      int epilogue, unsigned flags, float rms_eps, const float *bias, int64_t *tokens,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Greedy token choice of the generate loop (model.py:230-231, argmax over the
  * vocabulary at temperature 0): out[i] = the first index j of the largest
  * logits[i, j], NaN counting as the largest value (torch.argmax's answer).
@@ -511,6 +565,17 @@ int prime_decode_update(const prime_tensor_t *k, const prime_tensor_t *v, int B,
 int prime_timer_enable(unsigned mask);
 int prime_timer_reset(void);
 int prime_timer_read(int kernel, double *total_ms, int64_t *launches);
+
+/*
+ * HBM bandwidth probe.  No counterpart in the reference: benchmark harnesses
+ * use it for the achievable-bandwidth figure that kernel rooflines are read
+ * against.  copy != 0: dst = src over `bytes` (read + write); copy == 0: a
+ * read-only pass over src, one 16-byte word per workgroup written to dst
+ * (dst must hold `blocks` x 16 bytes).  Nontemporal 16-byte loads and stores,
+ * `blocks` workgroups of 256 threads in a grid-stride loop.  bytes a multiple
+ * of 16, both pointers 16-byte aligned.
+ */
+int prime_hbm_stream(const void *src, void *dst, size_t bytes, int copy, int blocks, void *stream);
 
 #ifdef __cplusplus
 }

@@ -125,54 +125,65 @@ class CausalLMCPU:
     tied lm_head.  ``step`` is one token per sequence through the step formula
     (attention.py:119-143).  The timed CPU baseline of bench.py's model leg."""
 
-    def __init__(self, state_dict, num_layers, num_heads, head_dim, decay, eps=1.0, rms_eps=1e-6, qk_norm=True):
+    def __init__(self, state_dict, num_layers, num_heads, head_dim, decay, eps=1.0, rms_eps=1e-6, qk_norm=True,
+                 round_bf16=False):
         self.W = {k: v.detach().to("cpu", torch.float32) for k, v in state_dict.items()}
         self.nl, self.H, self.D = num_layers, num_heads, head_dim
         self.decay, self.eps, self.rms_eps, self.qk_norm = decay, eps, rms_eps, qk_norm
         self.gelu = "layers.0.mlp.gate_proj.weight" not in self.W
         if "lm_head.weight" not in self.W:
             self.W["lm_head.weight"] = self.W["embed_tokens.weight"]
+        # round_bf16: every activation a bf16 model stores (norm outputs,
+        # projections, the QK-norm, the attention output, the GELU, the
+        # residual stream after each add) is rounded to bf16 there, the
+        # arithmetic in between staying fp32 -- the model in bf16 up to the
+        # summation order of its products
+        self.round_bf16 = round_bf16
+
+    def _r(self, x):
+        return x.to(torch.bfloat16).to(torch.float32) if self.round_bf16 else x
 
     def _rms(self, x, w):
-        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.rms_eps) * w
+        return self._r(x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.rms_eps) * w)
 
     def _mlp(self, p, x):
-        W = self.W
+        W, r = self.W, self._r
         if self.gelu:
-            return F.gelu(x @ W[p + "mlp.up_proj.weight"].T) @ W[p + "mlp.down_proj.weight"].T
-        return (F.silu(x @ W[p + "mlp.gate_proj.weight"].T) * (x @ W[p + "mlp.up_proj.weight"].T)) \
+            return r(F.gelu(r(x @ W[p + "mlp.up_proj.weight"].T))) @ W[p + "mlp.down_proj.weight"].T
+        return r(r(F.silu(r(x @ W[p + "mlp.gate_proj.weight"].T))) * r(x @ W[p + "mlp.up_proj.weight"].T)) \
             @ W[p + "mlp.down_proj.weight"].T
 
     def _qkv(self, p, h, B, L):
-        W, H, D = self.W, self.H, self.D
-        q = (h @ W[p + "self_attn.q_proj.weight"].T).view(B, L, H, D).transpose(1, 2)
-        k = (h @ W[p + "self_attn.k_proj.weight"].T).view(B, L, H, D).transpose(1, 2)
-        v = (h @ W[p + "self_attn.v_proj.weight"].T).view(B, L, H, D).transpose(1, 2)
+        W, H, D, r = self.W, self.H, self.D, self._r
+        q = r(h @ W[p + "self_attn.q_proj.weight"].T).view(B, L, H, D).transpose(1, 2)
+        k = r(h @ W[p + "self_attn.k_proj.weight"].T).view(B, L, H, D).transpose(1, 2)
+        v = r(h @ W[p + "self_attn.v_proj.weight"].T).view(B, L, H, D).transpose(1, 2)
         if self.qk_norm:
-            q = F.layer_norm(q, (D,), W[p + "self_attn.q_norm.weight"], W[p + "self_attn.q_norm.bias"])
-            k = F.layer_norm(k, (D,), W[p + "self_attn.k_norm.weight"], W[p + "self_attn.k_norm.bias"])
-        return q / D ** 0.5, k, v
+            q = r(F.layer_norm(q, (D,), W[p + "self_attn.q_norm.weight"], W[p + "self_attn.q_norm.bias"]))
+            k = r(F.layer_norm(k, (D,), W[p + "self_attn.k_norm.weight"], W[p + "self_attn.k_norm.bias"]))
+        return r(q / D ** 0.5), k, v
 
     @torch.no_grad()
-    def prefill(self, ids):
+    def prefill(self, ids, carry="dense"):
         """ids [B, L] -> (last-position logits [B, V], per-layer states)."""
-        W = self.W
+        W, r = self.W, self._r
         B, L = ids.shape
         x = W["embed_tokens.weight"][ids]
         states = []
         for i in range(self.nl):
             p = f"layers.{i}."
             q, k, v = self._qkv(p, self._rms(x, W[p + "input_layernorm.weight"]), B, L)
-            y, st = chunked_core(q.contiguous(), k.contiguous(), v.contiguous(), self.decay, eps=self.eps)
+            y, st = chunked_core(q.contiguous(), k.contiguous(), v.contiguous(), self.decay, eps=self.eps,
+                                 carry=carry)
             states.append(st)
-            x = x + y.transpose(1, 2).reshape(B, L, -1) @ W[p + "self_attn.o_proj.weight"].T
-            x = x + self._mlp(p, self._rms(x, W[p + "post_attention_layernorm.weight"]))
-        return self._rms(x[:, -1], W["norm.weight"]) @ W["lm_head.weight"].T, states
+            x = r(x + r(y).transpose(1, 2).reshape(B, L, -1) @ W[p + "self_attn.o_proj.weight"].T)
+            x = r(x + self._mlp(p, self._rms(x, W[p + "post_attention_layernorm.weight"])))
+        return r(self._rms(x[:, -1], W["norm.weight"]) @ W["lm_head.weight"].T), states
 
     @torch.no_grad()
     def step(self, tok, states):
         """tok [B] -> (logits [B, V], new states)."""
-        W = self.W
+        W, r = self.W, self._r
         x = W["embed_tokens.weight"][tok]
         B = x.shape[0]
         new = []
@@ -181,6 +192,6 @@ class CausalLMCPU:
             q, k, v = self._qkv(p, self._rms(x, W[p + "input_layernorm.weight"])[:, None], B, 1)
             y, st = decode_step(q[:, :, 0], k[:, :, 0], v[:, :, 0], self.decay, self.eps, states[i])
             new.append(st)
-            x = x + y.reshape(B, -1) @ W[p + "self_attn.o_proj.weight"].T
-            x = x + self._mlp(p, self._rms(x, W[p + "post_attention_layernorm.weight"]))
-        return self._rms(x, W["norm.weight"]) @ W["lm_head.weight"].T, new
+            x = r(x + r(y).reshape(B, -1) @ W[p + "self_attn.o_proj.weight"].T)
+            x = r(x + self._mlp(p, self._rms(x, W[p + "post_attention_layernorm.weight"])))
+        return r(self._rms(x, W["norm.weight"]) @ W["lm_head.weight"].T), new

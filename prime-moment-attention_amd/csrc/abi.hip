@@ -4,7 +4,9 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <mutex>
+#include <random>
 
 #include "prime_kernels.h"
 
@@ -12,15 +14,22 @@ namespace {
 
 thread_local char g_err[512] = "";
 
-// hand-off value of a paired prefill: distinct per call (never 0, the value a
-// consumed flag is reset to)
-std::atomic<unsigned long long> g_epoch{0};
-unsigned long long next_epoch() {
-    unsigned long long e;
-    while ((e = ++g_epoch) == 0) {
-    }
-    return e;
+// hand-off value of a paired prefill: the flag words live in a caller's
+// workspace that nobody clears, so the value must not be one that leftover
+// data holds by accident (small integers, token ids, float patterns, an epoch
+// of another process).  High 32 bits: a per-process random nonce with bit 63
+// set (never 0, the value a consumed flag is reset to); low 32 bits: a call
+// counter, so that calls of one process never share a value within 2^32 calls.
+unsigned long long epoch_nonce() {
+    std::random_device rd;
+    unsigned long long n = (static_cast<unsigned long long>(rd()) << 32) ^ rd();
+    n ^= static_cast<unsigned long long>(std::chrono::steady_clock::now().time_since_epoch().count()) * 0x9E3779B97F4A7C15ull;
+    n ^= reinterpret_cast<uintptr_t>(&n) * 0xC2B2AE3D27D4EB4Full;
+    return (n | 0x8000000000000000ull) & 0xFFFFFFFF00000000ull;
 }
+const unsigned long long g_epoch_nonce = epoch_nonce();
+std::atomic<unsigned int> g_epoch{0};
+unsigned long long next_epoch() { return g_epoch_nonce | static_cast<unsigned long long>(++g_epoch); }
 
 int fail(int code, const char *fmt, ...) {
     va_list ap;
@@ -143,6 +152,14 @@ int decode_impl(const prime_tensor_t *q, const prime_tensor_t *k, const prime_te
     a.s0o = state_out->s0; a.s1o = state_out->s1; a.s2o = state_out->s2;
     a.k0o = state_out->k0; a.k1o = state_out->k1; a.k2o = state_out->k2;
     a.y = y->data; a.dt_y = y->dtype; a.y_sb = y->stride_b; a.y_sh = y->stride_h;
+    if (y->layout == PRIME_LAYOUT_FRAG) {
+        if (y->dtype != PRIME_BF16 || (H * D) % 32 || !aligned16(y->data))
+            return fail(PRIME_ERR_INVALID_ARG, "fragment-layout y: bf16, H*D a multiple of 32, 16-byte aligned");
+        a.y_frag = 1;
+        a.y_ks = H * D / 32;
+    } else if (y->layout != PRIME_LAYOUT_STRIDED) {
+        return fail(PRIME_ERR_INVALID_ARG, "unknown y layout %d", y->layout);
+    }
     a.q_scale = norm ? norm->q_scale : 1.0f;
     a.k_scale = k_scale; a.selective = selective ? 1 : 0;
     if (gate) {
@@ -319,6 +336,93 @@ int prime_linear_fused(const void *x, const void *w, const void *r, void *y, int
     a.M = M; a.N = N; a.K = K; a.epilogue = epilogue;
     a.rms = rms_eps > 0.f ? 1 : 0; a.rms_eps = rms_eps;
     return check_hip(prime::launch_linear_rows(a, static_cast<hipStream_t>(stream)), "linear launch");
+}
+
+int prime_pack_frag(const void *src, int64_t ld, int64_t src_rows, const int64_t *rows, int M, int K, void *out,
+                    void *stream) {
+    g_err[0] = 0;
+    if (!src || !out) return fail(PRIME_ERR_INVALID_ARG, "prime_pack_frag: null argument");
+    if (M <= 0 || K <= 0 || K % 32 || ld < K || src_rows <= 0 || (!rows && src_rows < M))
+        return fail(PRIME_ERR_INVALID_ARG, "prime_pack_frag: bad sizes M=%d K=%d ld=%lld src_rows=%lld", M, K,
+                    static_cast<long long>(ld), static_cast<long long>(src_rows));
+    if (!aligned16(src) || (ld * 2) % 16 || !aligned16(out))
+        return fail(PRIME_ERR_MISALIGNED, "prime_pack_frag: src rows and out must be 16-byte aligned");
+    if (rows && (reinterpret_cast<uintptr_t>(rows) & 7)) return fail(PRIME_ERR_MISALIGNED, "rows must be 8-byte aligned");
+    const int Mp = prime_frag_rows(M);
+    const size_t nout = static_cast<size_t>(Mp) * K * 2;
+    if (overlap(out, nout, src, static_cast<size_t>((src_rows - 1) * ld + K) * 2))
+        return fail(PRIME_ERR_ALIAS, "prime_pack_frag: out overlaps src");
+    return check_hip(prime::launch_pack_frag(static_cast<const uint16_t *>(src), ld, rows, M, Mp, K, src_rows,
+                                             static_cast<uint16_t *>(out), static_cast<hipStream_t>(stream)),
+                     "pack launch");
+}
+
+int prime_frag_rows(int M) { return M <= 0 ? 0 : (M + 31) / 32 * 32; }
+
+size_t prime_linear_frag_workspace_size(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || N % 16 || K <= 0 || K % 32) return 0;
+    prime::FragArgs a{};
+    a.M = M; a.Mp = prime_frag_rows(M); a.N = N; a.K = K;
+    prime::frag_plan(a);
+    return static_cast<size_t>(a.Mp) * a.gn * sizeof(uint64_t);
+}
+
+int prime_linear_frag(const void *x, const void *w, const void *r, void *y, int M, int N, int K, int64_t ldy,
+                      int epilogue, unsigned flags, float rms_eps, const float *bias, int64_t *tokens,
+                      void *workspace, size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    if (!x || !w || (!y && !tokens)) return fail(PRIME_ERR_INVALID_ARG, "prime_linear_frag: null argument");
+    if (flags & ~(PRIME_LINEAR_RMS | PRIME_LINEAR_OUT_FRAG))
+        return fail(PRIME_ERR_INVALID_ARG, "prime_linear_frag: unknown flags 0x%x", flags);
+    const bool out_frag = (flags & PRIME_LINEAR_OUT_FRAG) != 0;
+    if (M <= 0 || N <= 0 || N % 16 || (out_frag && N % 32))
+        return fail(PRIME_ERR_INVALID_ARG, "prime_linear_frag: M > 0, N a multiple of 16 (32 for a fragment-layout "
+                    "output) (M=%d N=%d)", M, N);
+    if (!prime::frag_k_supported(K))
+        return fail(PRIME_ERR_INVALID_ARG, "prime_linear_frag: K must be 256 x {1, 2, 3, 4, 6, 12} (K=%d)", K);
+    if (epilogue != PRIME_EPILOGUE_NONE && epilogue != PRIME_EPILOGUE_GELU && epilogue != PRIME_EPILOGUE_RESIDUAL)
+        return fail(PRIME_ERR_INVALID_ARG, "unknown epilogue %d", epilogue);
+    if (epilogue == PRIME_EPILOGUE_RESIDUAL && !r) return fail(PRIME_ERR_INVALID_ARG, "prime_linear_frag: null r");
+    if ((flags & PRIME_LINEAR_RMS) && !(rms_eps >= 0.f))
+        return fail(PRIME_ERR_INVALID_ARG, "prime_linear_frag: rms_eps must be >= 0");
+    if (!aligned16(x) || !aligned16(w)) return fail(PRIME_ERR_MISALIGNED, "x and w must be 16-byte aligned");
+    const int Mp = prime_frag_rows(M);
+    size_t ny = 0;
+    if (y || r) {
+        if (out_frag) {
+            if ((y && !aligned16(y)) || (r && !aligned16(r)))
+                return fail(PRIME_ERR_MISALIGNED, "fragment-layout y and r must be 16-byte aligned");
+            ny = static_cast<size_t>(Mp) * N * 2;
+        } else {
+            if (ldy < N) return fail(PRIME_ERR_INVALID_ARG, "y row stride below the row length");
+            if (((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(r)) & 7) || ldy % 4)
+                return fail(PRIME_ERR_MISALIGNED, "row-major y and r rows must start on 8-byte boundaries");
+            ny = static_cast<size_t>((M - 1) * ldy + N) * 2;
+        }
+    }
+    const size_t nx = static_cast<size_t>(Mp) * K * 2, nw = static_cast<size_t>(N) * K * 2;
+    if (y && (overlap(y, ny, x, nx) || overlap(y, ny, w, nw)))
+        return fail(PRIME_ERR_ALIAS, "prime_linear_frag: y overlaps x or w");
+    if (r && r != y && y && overlap(r, ny, y, ny))
+        return fail(PRIME_ERR_ALIAS, "r overlaps y (only r == y is allowed)");
+    prime::FragArgs a{};
+    a.x = static_cast<const uint16_t *>(x); a.w = static_cast<const uint16_t *>(w);
+    a.r = static_cast<const uint16_t *>(r); a.y = static_cast<uint16_t *>(y); a.bias = bias;
+    a.M = M; a.Mp = Mp; a.N = N; a.K = K; a.KS = K / 32; a.ldy = ldy;
+    a.epilogue = epilogue; a.rms = (flags & PRIME_LINEAR_RMS) ? 1 : 0; a.out_frag = out_frag ? 1 : 0;
+    a.rms_eps = rms_eps;
+    prime::frag_plan(a);
+    if (tokens) {
+        if (out_frag) return fail(PRIME_ERR_INVALID_ARG, "prime_linear_frag: argmax with a row-major output only");
+        if (reinterpret_cast<uintptr_t>(tokens) & 7) return fail(PRIME_ERR_MISALIGNED, "tokens must be 8-byte aligned");
+        const size_t need = static_cast<size_t>(Mp) * a.gn * sizeof(uint64_t);
+        if (!workspace || workspace_bytes < need)
+            return fail(PRIME_ERR_INVALID_ARG, "prime_linear_frag: argmax needs a workspace of %zu bytes", need);
+        if (reinterpret_cast<uintptr_t>(workspace) & 7) return fail(PRIME_ERR_MISALIGNED, "workspace misaligned");
+        a.keys = static_cast<uint64_t *>(workspace);
+        a.tokens = tokens;
+    }
+    return check_hip(prime::launch_linear_frag(a, static_cast<hipStream_t>(stream)), "linear_frag launch");
 }
 
 int prime_argmax(const void *logits, int dtype, int n, int vocab, int64_t stride_n, int64_t *out, void *stream) {

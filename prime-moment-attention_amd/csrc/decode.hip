@@ -203,7 +203,9 @@ __global__ __launch_bounds__(W * kWave) void decode_step_kernel(const DecodeArgs
     }
     if (rg == 0 && !a.no_readout) {
         const f32x4 s04 = *reinterpret_cast<const f32x4 *>(&sh[wave][3][4 * cg]);
-        const int64_t yo = b * a.y_sb + h * a.y_sh + 4 * cg;
+        // (y in the fragment layout: the four columns of a lane are one lane
+        // slot's consecutive elements)
+        const int64_t yo = a.y_frag ? frag_index(b, h * kD + 4 * cg, a.y_ks) : b * a.y_sb + h * a.y_sh + 4 * cg;
 #pragma unroll
         for (int c = 0; c < 4; ++c) store_elem(a.y, yo + c, a.dt_y, (s04[c] + acc[c]) * inv);
     }

@@ -123,4 +123,12 @@ __device__ __forceinline__ uint64_t argmax_key(float f, uint32_t idx) {
 
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+// Element (r, k) of a bf16 matrix in the fragment layout of the decode step's
+// projections: 16 x 32 blocks in row-block-major order (KS = K / 32 blocks per
+// block row), each block the 64 lane slots of 8 elements of one MFMA operand
+// (slot = r % 16 + 16 * ((k % 32) / 8)).
+__device__ __forceinline__ int64_t frag_index(int r, int k, int KS) {
+    return (static_cast<int64_t>(r >> 4) * KS + (k >> 5)) * 512 + ((r & 15) + 16 * ((k & 31) >> 3)) * 8 + (k & 7);
+}
+
 }  // namespace prime

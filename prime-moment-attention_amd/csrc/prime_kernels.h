@@ -19,6 +19,7 @@ struct DecodeArgs {
     void *y;
     int dt_y;
     int64_t y_sb, y_sh;
+    int y_frag, y_ks;  // y in the fragment layout [B padded / 16][H D / 32][512] (bf16)
     // optional prologue: q <- LN(q) * q_scale, k <- LN(k) (LN over the head dim,
     // affine; qn_w == nullptr: no LN), LN output rounded to dt_q / dt_k
     const void *qn_w, *qn_b, *kn_w, *kn_b;
@@ -87,6 +88,30 @@ hipError_t launch_linear_rows(const LinearArgs &a, hipStream_t stream);
 // 256 x 256-tile kernel for many rows (gemm_tile.hip): M >= 256, N % 256 == 0, K % 64 == 0
 bool linear_tile_fits(const LinearArgs &a);
 hipError_t launch_linear_tile(const LinearArgs &a, hipStream_t stream);
+
+// Fragment-layout projections (gemm_frag.hip): x [Mp/16][K/32][512] and
+// w [N/16][K/32][512] bf16 blocks; y row-major [M, ldy] or fragment layout
+// [Mp/16][N/32][512]; r in y's layout.
+struct FragArgs {
+    const uint16_t *x, *w, *r;
+    uint16_t *y;               // may be null when tokens is set
+    const float *bias;         // fp32 [N] or null
+    uint64_t *keys;            // argmax tile keys [Mp][gn] or null
+    int64_t *tokens;           // argmax per row [M] or null (then keys is null)
+    int M, Mp, N, K, KS;       // KS = K / 32
+    int64_t ldy;
+    int epilogue, rms, out_frag;
+    float rms_eps;
+    int mt, nt, gm, gn;        // tile (16-row blocks) and grid (row tiles, column tiles)
+    int persistent;            // lm_head kernel: mt = m-blocks per row half, nt = row halves,
+                               // gn = column-tile ranges per row tile
+};
+void frag_tile(int Mp, int N, int K, int *MT, int *NT);
+void frag_plan(FragArgs &a);  // fills persistent, mt, nt, gm, gn from M, Mp, N, K
+bool frag_k_supported(int K);
+hipError_t launch_linear_frag(const FragArgs &a, hipStream_t stream);
+hipError_t launch_pack_frag(const uint16_t *src, int64_t ld, const int64_t *idx, int M, int Mp, int K,
+                            int64_t nrows_src, uint16_t *out, hipStream_t stream);
 
 constexpr int kNormMaxGroups = 16;  // 4-element groups per lane: hidden <= 4 * 64 * 16 = 4096
 hipError_t launch_add_rmsnorm(const RmsNormArgs &a, hipStream_t stream);

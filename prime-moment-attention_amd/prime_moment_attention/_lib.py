@@ -31,7 +31,8 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_decode_readout", "prime_decode_update", "prime_chunked_prefill_backward",
            "prime_chunked_prefill_backward_workspace_size", "prime_chunked_prefill_qknorm",
            "prime_selective_prefill_qknorm", "prime_accumulate_noalloc", "prime_selective_prefill_backward",
-           "prime_selective_prefill_backward_workspace_size")
+           "prime_selective_prefill_backward_workspace_size", "prime_hbm_stream",
+           "prime_frag_rows", "prime_pack_frag", "prime_linear_frag_workspace_size", "prime_linear_frag")
 
 # bytes of the fixed device scratch behind prime_accumulate_noalloc
 NOALLOC_SCRATCH_BYTES = 32 << 20
@@ -49,7 +50,7 @@ KERNEL_NAMES = {KERNEL_PREFILL_CHUNKS: "prefill_bf16_kernel (fused chunk loop)",
 
 
 class PrimeTensor(ctypes.Structure):
-    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32),
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int32), ("layout", ctypes.c_int32),
                 ("stride_b", ctypes.c_int64), ("stride_h", ctypes.c_int64), ("stride_l", ctypes.c_int64)]
 
 
@@ -163,6 +164,17 @@ def load() -> ctypes.CDLL:
     L.prime_selective_prefill_backward_workspace_size.argtypes = [ctypes.c_int] * 3
     L.prime_selective_prefill_backward_workspace_size.restype = ctypes.c_size_t
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
+    L.prime_hbm_stream.argtypes = [fp, fp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, fp]
+    L.prime_hbm_stream.restype = ctypes.c_int
+    L.prime_frag_rows.argtypes = [ctypes.c_int]
+    L.prime_frag_rows.restype = ctypes.c_int
+    L.prime_pack_frag.argtypes = [fp, ctypes.c_int64, ctypes.c_int64, fp, ctypes.c_int, ctypes.c_int, fp, fp]
+    L.prime_pack_frag.restype = ctypes.c_int
+    L.prime_linear_frag_workspace_size.argtypes = [ctypes.c_int] * 3
+    L.prime_linear_frag_workspace_size.restype = ctypes.c_size_t
+    L.prime_linear_frag.argtypes = [fp] * 4 + [ctypes.c_int] * 3 + [ctypes.c_int64, ctypes.c_int, ctypes.c_uint,
+                                                                   ctypes.c_float, fp, fp, fp, ctypes.c_size_t, fp]
+    L.prime_linear_frag.restype = ctypes.c_int
     v = L.prime_abi_version()
     if v != ABI_VERSION:
         raise RuntimeError(f"libprime_mi355x ABI {v} != expected {ABI_VERSION}")
@@ -210,6 +222,26 @@ def _check_state(state, B: int, H: int, D: int, name: str) -> None:
         _dev_check(t)
 
 
+PRIME_LAYOUT_STRIDED, PRIME_LAYOUT_FRAG = 0, 1
+
+
+def frag_desc(y: torch.Tensor) -> PrimeTensor:
+    """Descriptor of a decode-step output held in the fragment layout (a flat
+    bf16 buffer of frag_rows(B) x H*D elements)."""
+    if y.dtype != torch.bfloat16 or not y.is_contiguous():
+        raise ValueError("a fragment-layout y is a contiguous bf16 buffer")
+    return PrimeTensor(y.data_ptr(), PRIME_BF16, PRIME_LAYOUT_FRAG, 0, 0, 0)
+
+
+def _y_desc(y, B, H, D, y_frag):
+    if not y_frag:
+        _shape(y, (B, H, D), "y")
+        return tensor_desc(y, False)
+    if y.numel() < frag_rows(B) * H * D:
+        raise ValueError(f"fragment-layout y needs {frag_rows(B) * H * D} elements")
+    return frag_desc(y)
+
+
 def tensor_desc(x: torch.Tensor, has_l: bool) -> PrimeTensor:
     """Descriptor of a [B, H, L, D] (has_l) or [B, H, D] view; D must be contiguous."""
     if x.dtype not in _DTYPES:
@@ -253,13 +285,14 @@ def bind_decode_step(q, k, v, decay: torch.Tensor, eps: float, state_in, state_o
     return launch
 
 
-def _decode_checks(q, k, v, decay, state_in, state_out, y):
+def _decode_checks(q, k, v, decay, state_in, state_out, y, y_frag=False):
     _dev_check(q, k, v, y, decay)
     B, H, D = q.shape
     Hkv = k.shape[1]
     _shape(k, (B, Hkv, D), "k")
     _shape(v, (B, Hkv, D), "v")
-    _shape(y, (B, H, D), "y")
+    if not y_frag:
+        _shape(y, (B, H, D), "y")
     _check_decay(decay, H)
     _check_state(state_in, B, H, D, "state_in")
     _check_state(state_out, B, H, D, "state_out")
@@ -309,13 +342,14 @@ def qk_norm_on_load(q_norm, k_norm, q_scale: float, q: torch.Tensor) -> Optional
 
 
 def decode_step_qknorm(q, k, v, decay: torch.Tensor, eps: float, norm: PrimeQkNorm, state_in, state_out,
-                       y) -> None:
+                       y, y_frag: bool = False) -> None:
     """prime_decode_step_qknorm: q, k the raw projections [B,H,D] / [B,Hkv,D];
-    the QK LayerNorm and q scale (``qk_norm(...)``) are applied in the kernel."""
-    _decode_checks(q, k, v, decay, state_in, state_out, y)
+    the QK LayerNorm and q scale (``qk_norm(...)``) are applied in the kernel.
+    y_frag: y is a flat bf16 buffer receiving the output in the fragment layout."""
+    _decode_checks(q, k, v, decay, state_in, state_out, y, y_frag)
     B, H, D = q.shape
     L = load()
-    qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), tensor_desc(y, False)
+    qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), _y_desc(y, B, H, D, y_frag)
     si, so = state_desc(state_in), state_desc(state_out)
     rc = L.prime_decode_step_qknorm(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), B, H, k.shape[1], D,
                                     decay.data_ptr(), float(eps), ctypes.byref(norm),
@@ -551,15 +585,15 @@ def selective_gate(B: int, H: int, decay_bh: Optional[torch.Tensor] = None, step
 
 
 def selective_decode_step(q, k, v, gate: PrimeSelectiveGate, k_scale: torch.Tensor, eps: float,
-                          norm: Optional[PrimeQkNorm], state_in, state_out, y) -> None:
+                          norm: Optional[PrimeQkNorm], state_in, state_out, y, y_frag: bool = False) -> None:
     """Selective PRIME decode step (prime_selective_decode_step): the decays
     from ``selective_gate(...)``, k_scale fp32 [H]; norm: the QK LayerNorm
     and q scale for raw projections (``qk_norm(...)``) or None.  The tensors
     the gate points to must stay alive until the call returns."""
     B, H, D = q.shape
-    _decode_checks(q, k, v, k_scale, state_in, state_out, y)
+    _decode_checks(q, k, v, k_scale, state_in, state_out, y, y_frag)
     L = load()
-    qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), tensor_desc(y, False)
+    qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), _y_desc(y, B, H, D, y_frag)
     si, so = state_desc(state_in), state_desc(state_out)
     rc = L.prime_selective_decode_step(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), B, H, k.shape[1], D,
                                        ctypes.byref(gate), k_scale.data_ptr(), float(eps),
@@ -818,6 +852,100 @@ def timer_read(kernel: int) -> Tuple[float, int]:
     ms, n = ctypes.c_double(), ctypes.c_int64()
     _check(load().prime_timer_read(kernel, ctypes.byref(ms), ctypes.byref(n)), "prime_timer_read")
     return ms.value, n.value
+
+
+def hbm_stream(src: torch.Tensor, dst: torch.Tensor, copy: bool = True, blocks: int = 0) -> None:
+    """prime_hbm_stream: nontemporal 16-byte copy of src into dst (copy), or a
+    read-only pass over src (dst receives one 16-byte word per workgroup)."""
+    if not (src.is_cuda and dst.is_cuda and src.is_contiguous() and dst.is_contiguous()):
+        raise ValueError("hbm_stream: contiguous device tensors")
+    nbytes = src.numel() * src.element_size()
+    if blocks <= 0:
+        blocks = 8 * torch.cuda.get_device_properties(src.device).multi_processor_count
+    if copy and dst.numel() * dst.element_size() < nbytes:
+        raise ValueError("hbm_stream: dst smaller than src")
+    if not copy and dst.numel() * dst.element_size() < 16 * blocks:
+        raise ValueError("hbm_stream: dst must hold 16 bytes per workgroup")
+    _check(load().prime_hbm_stream(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), nbytes,
+                                   1 if copy else 0, blocks, _stream(src.device)), "prime_hbm_stream")
+
+
+LINEAR_RMS, LINEAR_OUT_FRAG = 1, 2
+
+
+def frag_rows(M: int) -> int:
+    """Rows of the fragment layout of an M-row matrix (M rounded up to 32)."""
+    return (M + 31) // 32 * 32
+
+
+def frag_supported(K: int) -> bool:
+    """prime_linear_frag's contraction sizes: 256 x {1, 2, 3, 4, 6, 12}."""
+    return K % 256 == 0 and K // 256 in (1, 2, 3, 4, 6, 12)
+
+
+def pack_frag(src: torch.Tensor, out: Optional[torch.Tensor] = None, rows: Optional[torch.Tensor] = None,
+              M: Optional[int] = None) -> torch.Tensor:
+    """prime_pack_frag: the bf16 matrix src [R, K] (contiguous rows) in the
+    fragment layout, as a flat tensor of frag_rows(M) * K elements; with rows
+    (int64 [M] on the device) row r is src[rows[r]] (an embedding gather)."""
+    _dev_check(src)
+    if src.dim() != 2 or src.dtype != torch.bfloat16 or src.stride(1) != 1:
+        raise ValueError("src must be a bf16 [R, K] tensor with contiguous rows")
+    R, K = src.shape
+    if rows is not None:
+        _dev_check(rows)
+        if rows.dtype != torch.int64 or not rows.is_contiguous():
+            raise ValueError("rows must be a contiguous int64 tensor")
+        M = rows.numel()
+    M = R if M is None else M
+    n = frag_rows(M) * K
+    if out is None:
+        out = torch.empty(n, device=src.device, dtype=torch.bfloat16)
+    elif out.numel() < n or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous bf16 tensor of at least {n} elements")
+    rc = load().prime_pack_frag(ctypes.c_void_p(src.data_ptr()), src.stride(0), R,
+                                ctypes.c_void_p(rows.data_ptr()) if rows is not None else None, M, K,
+                                ctypes.c_void_p(out.data_ptr()), _stream(src.device))
+    _check(rc, "prime_pack_frag")
+    return out
+
+
+def linear_frag_workspace_size(M: int, N: int, K: int) -> int:
+    return int(load().prime_linear_frag_workspace_size(M, N, K))
+
+
+def linear_frag(x: torch.Tensor, w: torch.Tensor, M: int, N: int, K: int, y: Optional[torch.Tensor],
+                epilogue: int = EPILOGUE_NONE, flags: int = 0, rms_eps: float = 0.0,
+                bias: Optional[torch.Tensor] = None, r: Optional[torch.Tensor] = None, ldy: int = 0,
+                tokens: Optional[torch.Tensor] = None, workspace: Optional[torch.Tensor] = None) -> None:
+    """prime_linear_frag: y = epilogue(s * x w^T + bias) with x, w in the
+    fragment layout (flat bf16 tensors from pack_frag or an earlier
+    linear_frag); y row-major [M, ldy] (ldy 0: N) or, with LINEAR_OUT_FRAG,
+    fragment layout; tokens (int64 [M]): the argmax of each row's rounded
+    products (needs workspace of linear_frag_workspace_size bytes)."""
+    _dev_check(x, w, y, bias, r, tokens, workspace)
+    Mp = frag_rows(M)
+    if x.numel() < Mp * K or w.numel() < N * K or x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise ValueError("x and w must be bf16 fragment-layout buffers of frag_rows(M) x K and N x K")
+    ldy = ldy or N
+    if y is not None:
+        need = Mp * N if flags & LINEAR_OUT_FRAG else (M - 1) * ldy + N
+        if y.dtype != torch.bfloat16 or y.numel() < need or not y.is_contiguous():
+            raise ValueError(f"y must be a contiguous bf16 tensor of at least {need} elements")
+    if r is not None:
+        need = Mp * N if flags & LINEAR_OUT_FRAG else (M - 1) * ldy + N
+        if r.dtype != torch.bfloat16 or not r.is_contiguous() or r.numel() < need:
+            raise ValueError(f"r must be a contiguous bf16 tensor in y's layout ({need} elements)")
+    if bias is not None and (bias.dtype != torch.float32 or bias.numel() != N or not bias.is_contiguous()):
+        raise ValueError(f"bias must be a contiguous fp32 tensor of {N} values")
+    if tokens is not None and (tokens.dtype != torch.int64 or tokens.numel() < M):
+        raise ValueError("tokens must be an int64 tensor of M values")
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    rc = load().prime_linear_frag(p(x), p(w), p(r), p(y), M, N, K, ldy, int(epilogue), int(flags), float(rms_eps),
+                                  p(bias), p(tokens), p(workspace),
+                                  workspace.numel() * workspace.element_size() if workspace is not None else 0,
+                                  _stream(x.device))
+    _check(rc, "prime_linear_frag")
 
 
 _decay_cache = {}

@@ -180,6 +180,40 @@ class PrimeForCausalLM(nn.Module):
             if hasattr(layer.self_attn, "init_selective_weights"):  # model.py:148-149
                 layer.self_attn.init_selective_weights()
 
+    @classmethod
+    def from_pretrained_base_to_selective(cls, checkpoint_path: str,
+                                          device: Any = "cpu") -> "PrimeForCausalLM":
+        """Identity-preserving warm start of a selective model from a base PRIME
+        checkpoint (model.py:269-310): every pretrained tensor (embeddings,
+        projections, norms, MLP, lm_head) is kept; the selective parameters the
+        checkpoint lacks keep their initialisation (init_selective_weights:
+        zero step weights and a step bias that reproduces the base decay, so
+        the warm-started model computes the base model at step 0).
+
+        The checkpoint holds "config" (a PrimeConfig or a dict of its fields)
+        and "model_state_dict".  It is read with torch.load(weights_only=True),
+        PrimeConfig being the only class allowed besides tensors (the
+        reference unpickles the whole file)."""
+        with torch.serialization.safe_globals([PrimeConfig]):
+            ckpt = torch.load(checkpoint_path, map_location=device, weights_only=True)
+        base = ckpt.get("config", None)
+        if base is None:
+            raise ValueError(f"Checkpoint at {checkpoint_path} has no saved config.")
+        get = (lambda k, d=None: base.get(k, d)) if isinstance(base, dict) else (lambda k, d=None: getattr(base, k, d))
+        sel_config = PrimeConfig(
+            vocab_size=get("vocab_size"), hidden_size=get("hidden_size"), num_layers=get("num_layers"),
+            num_heads=get("num_heads"), head_dim=get("head_dim"), num_kv_heads=get("num_kv_heads"),
+            intermediate_size=get("intermediate_size"), decay=get("decay"), use_qk_norm=get("use_qk_norm"),
+            rms_norm_eps=get("rms_norm_eps"), eps=get("eps"), tie_word_embeddings=get("tie_word_embeddings"),
+            initializer_range=get("initializer_range"), use_selective=True, mlp_type=get("mlp_type", "swiglu"))
+        model = cls(sel_config).to(device)
+        sd = ckpt["model_state_dict"]
+        missing_keys, unexpected_keys = model.load_state_dict(sd, strict=False)
+        print(f"[Selective Warm-Start] Loaded {len(sd)} pretrained tensors from {checkpoint_path}")
+        print(f"    Missing keys initialized to identity: {len(missing_keys)}")
+        print(f"    Unexpected keys: {len(unexpected_keys)}")
+        return model
+
     def _init_weights(self, module: nn.Module):
         if isinstance(module, (nn.Linear, nn.Embedding)):
             nn.init.normal_(module.weight, mean=0.0, std=self.config.initializer_range)
@@ -200,7 +234,11 @@ class PrimeForCausalLM(nn.Module):
         if input_ids.shape[-1] == 1 and _fused_step_supported(self):
             # one token per sequence (the generate loop, model.py:238): the fused
             # step GreedyDecoder runs, with functional states
-            logits, ns = _fused_step(self, input_ids, states, _step_constants(self), inplace=False)
+            consts = _step_constants(self)
+            if _frag_step_ready(consts):
+                logits, ns = _frag_step(self, input_ids, states, consts, inplace=False)
+            else:
+                logits, ns = _fused_step(self, input_ids, states, consts, inplace=False)
             logits = logits.unsqueeze(1)
             loss = None
             if labels is not None:
@@ -323,6 +361,8 @@ class _LayerStep:
         # the folded form (base attention, GELU MLP, bf16): each RMSNorm's weight
         # multiplied into the columns of the projection after it, so that the
         # projection kernel applies the norm as a per-row scale (prime_linear_fused)
+        # (the kernels take "apply the norm" as its own flag; a norm eps of 0
+        # is a valid configuration and still normalises)
         self.qkv_g = self.up_g = None
         if (self.sel is None and isinstance(layer.mlp, PrimeGeluMLP) and dtype == torch.bfloat16
                 and self.qkv.shape[1] % 128 == 0 and self.qkv.shape[0] % 32 == 0
@@ -331,11 +371,85 @@ class _LayerStep:
             g2 = layer.post_attention_layernorm.weight.to(torch.float32)
             self.qkv_g = (self.qkv.to(torch.float32) * g1).to(dtype)
             self.up_g = (layer.mlp.up_proj.weight.to(torch.float32) * g2).to(dtype)
+        # the fragment-layout step (prime_linear_frag): the same folded form with
+        # every weight packed once into MFMA-operand blocks
+        self.frag = None
+        at_dims = (at.num_heads * at.head_dim, layer.mlp.up_proj.weight.shape[0] if isinstance(layer.mlp, PrimeGeluMLP)
+                   else 0)
+        if (isinstance(layer.mlp, PrimeGeluMLP) and dtype == torch.bfloat16 and at.head_dim == 64 and self.qkv.is_cuda
+                and _lib.frag_supported(self.qkv.shape[1]) and _lib.frag_supported(at_dims[0])
+                and _lib.frag_supported(at_dims[1]) and self.qkv.shape[1] % 32 == 0 and at_dims[1] % 32 == 0):
+            self.frag = _FragLayer(layer, self, dtype)
+        self.folded = self.qkv_g is not None or self.frag is not None
+
+
+class _FragLayer:
+    """One block's weights for the fragment-layout step: the stacked q/k/v
+    weight (and, for selective attention, the step projection's rows, its bias
+    kept apart) with the input RMSNorm's weight in its columns, padded to a
+    multiple of 64 rows; o_proj; up_proj with the post-attention RMSNorm's
+    weight in its columns; down_proj -- each packed into the fragment layout."""
+
+    def __init__(self, layer: "PrimeBlock", ls: "_LayerStep", dtype: torch.dtype):
+        at = layer.self_attn
+        g1 = layer.input_layernorm.weight.to(torch.float32)
+        g2 = layer.post_attention_layernorm.weight.to(torch.float32)
+        w = ls.qkv.to(torch.float32) * g1
+        self.nq0 = w.shape[0]
+        bias = None
+        if ls.sel is not None:
+            H = at.num_heads
+            w = torch.cat([w, at.delta_proj.weight.to(torch.float32) * g1])
+            bias = torch.zeros(w.shape[0], dtype=torch.float32, device=w.device)
+            bias[self.nq0:self.nq0 + H] = at.delta_proj.bias.to(torch.float32)
+        n = w.shape[0]
+        self.nq = -(-n // 64) * 64
+        if self.nq > n:
+            w = torch.cat([w, w.new_zeros(self.nq - n, w.shape[1])])
+            if bias is not None:
+                bias = torch.cat([bias, bias.new_zeros(self.nq - n)])
+        self.bq = bias.contiguous() if bias is not None else None
+        self.wq = _lib.pack_frag(w.to(dtype).contiguous())
+        self.wo = _lib.pack_frag(at.o_proj.weight.contiguous())
+        self.wu = _lib.pack_frag((layer.mlp.up_proj.weight.to(torch.float32) * g2).to(dtype).contiguous())
+        self.wd = _lib.pack_frag(layer.mlp.down_proj.weight.contiguous())
+        self.inter = layer.mlp.up_proj.weight.shape[0]
+
+
+class _StepConstants(list):
+    """Per-layer step constants, plus the lm_head with the final RMSNorm's
+    weight in its columns in the fragment layout (``head``; None when the
+    fragment step does not apply)."""
+    head = None
+
+
+def _constants_key(model: "PrimeForCausalLM"):
+    """What the step constants are derived from: every parameter's storage and
+    version counter (an in-place update or a new tensor changes it)."""
+    return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in model.parameters())
 
 
 def _step_constants(model: "PrimeForCausalLM") -> List[_LayerStep]:
+    """The per-layer step constants, rebuilt only when a parameter changed
+    since they were last built (the stacked and norm-folded weights are tens
+    of MB at the PRIME-125M shape; the generate loop calls this per token)."""
+    key = _constants_key(model)
+    cached = model.__dict__.get("_step_cache")
+    if cached is not None and cached[0] == key:
+        return cached[1]
     w = model.embed_tokens.weight
-    return [_LayerStep(layer, w.dtype, w.device) for layer in model.layers]
+    consts = _StepConstants(_LayerStep(layer, w.dtype, w.device) for layer in model.layers)
+    V, hidden = model.lm_head.weight.shape
+    if (all(c.frag is not None for c in consts) and w.is_cuda and V % 16 == 0 and hidden % 32 == 0
+            and model.lm_head.weight.dtype == torch.bfloat16):
+        g = model.norm.weight.to(torch.float32)
+        consts.head = _lib.pack_frag((model.lm_head.weight.to(torch.float32) * g).to(w.dtype).contiguous())
+    model.__dict__["_step_cache"] = (key, consts)
+    return consts
+
+
+def _frag_step_ready(consts) -> bool:
+    return getattr(consts, "head", None) is not None
 
 
 def _fused_step_supported(model: "PrimeForCausalLM") -> bool:
@@ -436,6 +550,82 @@ def _fused_step(model: "PrimeForCausalLM", tokens: torch.Tensor, states, consts:
     return model.lm_head(nf), next_states
 
 
+def _step_states(at, st, B, H, D, dev, inplace):
+    """(state_in, state_out) of one layer's decode step: in place, or the
+    reference's functional contract (new tensors unless the module keeps its
+    own layout in place)."""
+    if inplace:
+        return st, st
+    st_in = _lib.as_state(st, B, H, D, dev) if st is not None else None
+    if at.inplace_state and st_in is not None and all(a.data_ptr() == b.data_ptr() for a, b in zip(st_in, st)):
+        return st_in, st_in
+    return st_in, _lib.new_state(B, H, D, dev)
+
+
+@torch.no_grad()
+def _frag_step(model: "PrimeForCausalLM", tokens: torch.Tensor, states, consts: "_StepConstants", inplace: bool,
+               want_logits: bool = True, tokens_out: Optional[torch.Tensor] = None):
+    """One token per sequence through the whole model on the fragment-layout
+    kernels (the blocks of model.py:107-118, the final norm and lm_head of
+    model.py:160, the greedy choice of model.py:230-231).  The residual stream
+    x, the attention output y and the MLP's hidden layer stay in the fragment
+    layout from the embedding gather to the lm_head:
+      x  <- embed_tokens[tokens]                      (prime_pack_frag)
+      per layer:
+        qkv <- RMS(x) . Wqkv'^T (+ step bias)         (prime_linear_frag, row-major)
+        y   <- decode step (QK-norm, 1/sqrt(D) inside; selective gate from qkv)
+        x   <- x + y . Wo^T                           (residual epilogue, in place)
+        t   <- GELU(RMS(x) . Wup'^T)
+        x   <- x + t . Wdown^T
+      logits <- RMS(x) . Wlm'^T, and/or the argmax of each row into tokens_out
+    (W' carries the RMSNorm weight before the projection in its columns, so
+    the norm's output is never rounded on its own).  Returns (logits [B, V] or
+    None, next states); `states` as in _fused_step."""
+    cfg = model.config
+    K = cfg.hidden_size
+    tok = tokens.reshape(-1)
+    if tok.dtype != torch.int64:
+        tok = tok.to(torch.int64)
+    tok = tok.contiguous()
+    B = tok.numel()
+    dev = tok.device
+    Mp = _lib.frag_rows(B)
+    x = _lib.pack_frag(model.embed_tokens.weight, rows=tok)
+    at0 = model.layers[0].self_attn
+    y = torch.empty(Mp * at0.num_heads * at0.head_dim, device=dev, dtype=x.dtype)
+    t = torch.empty(Mp * consts[0].frag.inter, device=dev, dtype=x.dtype)
+    next_states = []
+    for i, (layer, c) in enumerate(zip(model.layers, consts)):
+        f, at = c.frag, layer.self_attn
+        H, Hk, D = at.num_heads, at.num_kv_heads, at.head_dim
+        qkv = torch.empty(B, f.nq, device=dev, dtype=x.dtype)
+        _lib.linear_frag(x, f.wq, B, f.nq, K, qkv, flags=_lib.LINEAR_RMS, rms_eps=layer.input_layernorm.eps,
+                         bias=f.bq)
+        q = qkv[:, :H * D].view(B, H, D)
+        k = qkv[:, H * D:(H + Hk) * D].view(B, Hk, D)
+        v = qkv[:, (H + Hk) * D:(H + 2 * Hk) * D].view(B, Hk, D)
+        st_in, st_out = _step_states(at, states[i] if states is not None else None, B, H, D, dev, inplace)
+        if c.sel is not None:
+            tau, beta = c.sel
+            gate = _lib.selective_gate(B, H, step=qkv[:, f.nq0:f.nq0 + H], tau=tau)
+            _lib.selective_decode_step(q, k, v, gate, beta, at.eps, c.norm, st_in, st_out, y, y_frag=True)
+        else:
+            _lib.decode_step_qknorm(q, k, v, c.decay, at.eps, c.norm, st_in, st_out, y, y_frag=True)
+        next_states.append(st_out)
+        _lib.linear_frag(y, f.wo, B, K, H * D, x, _lib.EPILOGUE_RESIDUAL, _lib.LINEAR_OUT_FRAG, r=x)
+        _lib.linear_frag(x, f.wu, B, f.inter, K, t, _lib.EPILOGUE_GELU, _lib.LINEAR_RMS | _lib.LINEAR_OUT_FRAG,
+                         rms_eps=layer.post_attention_layernorm.eps)
+        _lib.linear_frag(t, f.wd, B, K, f.inter, x, _lib.EPILOGUE_RESIDUAL, _lib.LINEAR_OUT_FRAG, r=x)
+    V = model.lm_head.weight.shape[0]
+    logits = torch.empty(B, V, device=dev, dtype=x.dtype) if want_logits else None
+    ws = None
+    if tokens_out is not None:
+        ws = torch.empty(_lib.linear_frag_workspace_size(B, V, K), device=dev, dtype=torch.uint8)
+    _lib.linear_frag(x, consts.head, B, V, K, logits, flags=_lib.LINEAR_RMS, rms_eps=model.norm.eps,
+                     tokens=tokens_out, workspace=ws)
+    return logits, next_states
+
+
 class GreedyDecoder:
     """Greedy decoding with in-place states and a HIP-graph-captured step.
 
@@ -476,6 +666,12 @@ class GreedyDecoder:
 
     @torch.no_grad()
     def _step_eager(self) -> torch.Tensor:
+        if _frag_step_ready(self.consts):
+            # the lm_head kernel writes the greedy tokens itself (no logits);
+            # the embedding gather at the start of the step has consumed the old ones
+            _frag_step(self.model, self.token, self.states, self.consts, inplace=True, want_logits=False,
+                       tokens_out=self.token.view(-1))
+            return self.token
         logits, _ = _fused_step(self.model, self.token, self.states, self.consts, inplace=True)
         _lib.argmax(logits, self.token)  # the embedding above has consumed the old token
         return self.token

@@ -190,6 +190,89 @@ def test_config4_prime125m_full_shape():
     torch.cuda.synchronize()
 
 
+# Parity of the whole model at the PRIME-125M shape against the fp32
+# PyTorch-CPU restatement of the reference model (oracle/torch_cpu.py
+# CausalLMCPU, model.py:47-200 with the chunked core of chunked_ssd.py:48-184
+# and the step of attention.py:119-143), on the same weights and ids.  Two of
+# the 32 sequences of the B=32 x 2048 prefill (the first and the last, so both
+# halves of the paired split) and 8 teacher-forced decode steps (every side
+# fed the GPU's greedy tokens) are recomputed on the CPU twice: in fp32, and
+# with every activation the bf16 model stores rounded to bf16 where it stores
+# it (the same model in bf16 up to the summation order of its products).
+#   states: all 12 layers' final states within the bf16 input tolerance of
+#     the fp32 restatement;
+#   logits: the bf16 residual stream makes the last logits of this random-init
+#     model move by percents under any change of rounding (single steps of one
+#     sequence swing between 1e-2 and 1e-1 in relative L2 for every bf16 form
+#     of the step, the bf16 emulation included), so the bound is the model's
+#     own bf16 noise floor measured on the same inputs: the root mean square,
+#     over the prefill and the 8 steps of both sequences, of the GPU's
+#     relative L2 distance to the fp32 restatement may be at most
+#     LOGITS_NOISE_FACTOR times that of the bf16 emulation; and no single
+#     logits vector may be farther than LOGITS_MAX_REL_L2;
+#   the greedy-token agreement with the fp32 restatement is printed.
+LOGITS_NOISE_FACTOR = 2.0
+LOGITS_MAX_REL_L2 = 0.25
+
+
+def test_config4_prime125m_parity_against_fp32_restatement():
+    from oracle.torch_cpu import CausalLMCPU
+    from prime_moment_attention import PrimeForCausalLM, prime_125m_config
+    cfg = prime_125m_config("gelu")
+    torch.manual_seed(4)
+    model = PrimeForCausalLM(cfg).to(device=dev(), dtype=torch.bfloat16).eval()
+    gen = torch.Generator(device=dev()).manual_seed(4)
+    B, L, pick, steps = 32, 2048, [0, 31], 8
+    ids = torch.randint(0, cfg.vocab_size, (B, L), device=dev(), generator=gen)
+    print(f"[config 4 parity] PRIME-125M B={B} L={L}, sequences {pick} and {steps} steps on the CPU", flush=True)
+    with torch.no_grad():
+        out = model(ids, return_states=True, logits_to_keep=1)
+    torch.cuda.synchronize()
+    logits = {"gpu": [out["logits"][pick, -1].float().cpu()]}
+    gst = [tuple(t[pick].float().cpu() for t in st) for st in out["states"]]
+    del out
+    rel = lambda a, r: float((a - r).norm() / r.norm())
+    # the GPU's decode steps on its greedy tokens (functional states)
+    st_g = [tuple(t.to(dev()).contiguous() for t in s) for s in gst]
+    toks = [logits["gpu"][0].argmax(-1)]
+    for _ in range(steps):
+        with torch.no_grad():
+            o = model(toks[-1].view(-1, 1).to(dev()), states=st_g, return_states=True)
+        st_g = o["states"]
+        logits["gpu"].append(o["logits"][:, -1].float().cpu())
+        toks.append(logits["gpu"][-1].argmax(-1))
+    ids_c = ids[pick].cpu()
+    for mode in ("fp32", "bf16"):
+        cpu = CausalLMCPU(model.state_dict(), cfg.num_layers, cfg.num_heads, cfg.head_dim, cfg.decay, eps=cfg.eps,
+                          rms_eps=cfg.rms_norm_eps, qk_norm=cfg.use_qk_norm, round_bf16=(mode == "bf16"))
+        cl, cst = cpu.prefill(ids_c, carry="scan")
+        if mode == "fp32":
+            for i in range(cfg.num_layers):
+                for c, (a, r) in enumerate(zip(gst[i], cst[i])):
+                    e = float((a.reshape(r.shape) - r).abs().max() / r.abs().max().clamp_min(1e-30))
+                    assert e < TOL_BF16, f"layer {i} state component {c}: rel err {e:.3e}"
+        logits[mode] = [cl]
+        for t in range(steps):
+            cl, cst = cpu.step(toks[t], cst)
+            logits[mode].append(cl)
+    ref = logits["fp32"]
+    agree = sum(int((g.argmax(-1) == r.argmax(-1)).sum()) for g, r in zip(logits["gpu"], ref))
+    eg_all, eb_all = [], []
+    for t in range(steps + 1):
+        eg = [rel(logits["gpu"][t][i], ref[t][i]) for i in range(len(pick))]
+        eb = [rel(logits["bf16"][t][i], ref[t][i]) for i in range(len(pick))]
+        eg_all += eg
+        eb_all += eb
+        what = "prefill" if t == 0 else f"step {t}"
+        print(f"[config 4 parity] {what}: logits rel L2 to the fp32 restatement per sequence: GPU "
+              f"{' '.join(f'{e:.2e}' for e in eg)}, bf16 emulation {' '.join(f'{e:.2e}' for e in eb)}", flush=True)
+    rms = lambda v: (sum(e * e for e in v) / len(v)) ** 0.5
+    print(f"[config 4 parity] rms rel L2: GPU {rms(eg_all):.3e}, bf16 emulation {rms(eb_all):.3e}; greedy "
+          f"agreement with the fp32 restatement {agree}/{(steps + 1) * len(pick)}", flush=True)
+    assert rms(eg_all) <= LOGITS_NOISE_FACTOR * rms(eb_all), (rms(eg_all), rms(eb_all))
+    assert max(eg_all) <= LOGITS_MAX_REL_L2, max(eg_all)
+
+
 # ------------------------------------------------------------------ config 5
 def test_config5_delta_long_context():
     """B=1, H=12, D=64, L=131072, chunk 64: bf16 q/k/v (N(0,1), QK-normed,

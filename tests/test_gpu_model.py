@@ -96,12 +96,60 @@ def test_prefill_then_steps_equal_longer_prefill():
             assert _rel(step["logits"][:, -1], full[:, t]) < TOL_LOGITS
 
 
-def test_greedy_decoder_graph_equals_eager_generate():
+def _gelu_cfg(hidden):
+    """GELU-MLP configurations whose one-token step is folded: hidden 128 takes
+    the row kernels (prime_linear_fused), hidden 256 the fragment-layout
+    kernels (prime_linear_frag, K = 256 and 768)."""
+    return PrimeConfig(vocab_size=512, hidden_size=hidden, num_layers=2, num_heads=hidden // 64, head_dim=64,
+                       decay=0.995, mlp_type="gelu", intermediate_size=2 * hidden if hidden == 128 else 3 * hidden)
+
+
+@pytest.mark.parametrize("hidden", [128, 256])
+@pytest.mark.parametrize("L0", [40, 600])
+def test_folded_gelu_step_matches_fp32_composition(L0, hidden):
+    """The folded one-token step the headline decode runs (GELU MLP, bf16:
+    each RMSNorm's weight in the next projection's columns, the row scale and
+    the GELU / residual add inside the projection kernels; hidden 256: the
+    fragment-layout step with the lm_head's own kernel) against the fp32 CPU
+    composition of the same weights over the whole sequence, for prompts on the
+    dense (L <= 512) and the chunked branch."""
+    from prime_moment_attention import model as M
+    model = _model(_gelu_cfg(hidden))
+    consts = M._step_constants(model)
+    assert all(c.folded for c in consts), "the folded step must be taken for this configuration"
+    assert M._frag_step_ready(consts) == (hidden == 256)
+    ids = torch.randint(0, 512, (3, L0 + 4), generator=torch.Generator().manual_seed(12))
+    with torch.no_grad():
+        out = model(ids[:, :L0].to(dev()), return_states=True)
+        states = out["states"]
+        for t in range(L0, L0 + 4):
+            step = model(ids[:, t:t + 1].to(dev()), states=states, return_states=True)
+            states = step["states"]
+            ref = _ref_forward(model, ids[:, :t + 1])[:, -1]
+            assert torch.isfinite(step["logits"]).all()
+            assert _rel(step["logits"][:, -1], ref) < TOL_LOGITS, (t, _rel(step["logits"][:, -1], ref))
+
+
+@pytest.mark.parametrize("cfg", ["swiglu", "gelu_frag", "selective_frag"])
+def test_greedy_decoder_graph_equals_eager_generate(cfg):
     """Greedy tokens: HIP-graph decoder == eager decoder == generate(temperature=0);
     graph replays are interleaved with eager work and synchronisations, and the
-    states stay in place."""
-    model = _model(_small(layers=2, heads=2, decay=0.99))
-    ids = torch.randint(0, 384, (3, 30), generator=torch.Generator().manual_seed(3)).to(dev())
+    states stay in place.  For the fragment-layout step the decoder takes the
+    lm_head kernel's own argmax while generate takes torch.argmax of its logits."""
+    if cfg == "swiglu":
+        model = _model(_small(layers=2, heads=2, decay=0.99))
+    else:
+        c = _gelu_cfg(256)
+        c.use_selective = cfg == "selective_frag"
+        model = _model(c)
+        if c.use_selective:
+            with torch.no_grad():
+                g = torch.Generator().manual_seed(5)
+                for layer in model.layers:
+                    layer.self_attn.delta_proj.weight.copy_(torch.randn(layer.self_attn.delta_proj.weight.shape,
+                                                                        generator=g) * 0.02)
+                    layer.self_attn.log_beta.copy_(torch.rand(layer.self_attn.log_beta.shape, generator=g) - 0.5)
+    ids = torch.randint(0, model.config.vocab_size, (3, 30), generator=torch.Generator().manual_seed(3)).to(dev())
     n = 12
     ref = model.generate(ids, max_new_tokens=n, temperature=0.0)
     eager = GreedyDecoder(model, use_graph=False).generate(ids, n)

@@ -146,3 +146,28 @@ def test_paired_split_graph_replays():
         graph.replay()
         torch.cuda.synchronize()
         _same((y, st), ref, f"replay {i}")
+
+
+@pytest.mark.parametrize("pattern", ["small_ints", "bf16_one", "int64_ids"])
+def test_paired_split_leftover_workspace_data(pattern):
+    """The hand-off flags sit in a workspace nobody clears: whatever earlier
+    tensors left there (small integers, a bf16 run [1, 0, 0, 0] = 0x3F80 as a
+    64-bit word, token ids) must not read as the call's hand-off value, so the
+    result stays bit-identical to one workgroup per sequence."""
+    B, H, L = 32, 12, 512 + 64
+    nbytes = _need_pairs(B, H, L)
+    q, k, v = _inputs(B, H, H, L, seed=33)
+    lam = torch.full((H,), 0.9993, device=dev())
+    whole = _run_base(q, k, v, lam, None, torch.empty(0, dtype=torch.uint8, device=dev()))
+    words = (nbytes + 7) // 8
+    if pattern == "small_ints":
+        fill = torch.arange(words, device=dev(), dtype=torch.int64) % 4096
+    elif pattern == "bf16_one":
+        fill = torch.full((words,), 0x3F80, device=dev(), dtype=torch.int64)
+    else:
+        fill = torch.randint(0, 50304, (words,), device=dev(), dtype=torch.int64,
+                             generator=torch.Generator(device=dev()).manual_seed(5))
+    ws8 = torch.empty(words * 8, dtype=torch.uint8, device=dev())
+    for _ in range(2):  # the pattern again before a second call on the same workspace
+        ws8.view(torch.int64).copy_(fill)
+        _same(_run_base(q, k, v, lam, None, ws8[:nbytes]), whole, f"paired over leftover {pattern}")

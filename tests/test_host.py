@@ -62,3 +62,40 @@ def test_learnable_decay_refused_under_autograd():
     decay = torch.nn.Parameter(torch.full((2,), 0.99))
     with pytest.raises(NotImplementedError, match="decay"):
         prime_prefill(q, q, q, decay=decay)
+
+
+@pytest.mark.parametrize("config_as_dict", [False, True])
+def test_base_to_selective_warm_start(tmp_path, config_as_dict):
+    """from_pretrained_base_to_selective (model.py:269-310): a base checkpoint
+    warm-starts a selective model that keeps every pretrained tensor; only
+    the selective parameters are new, at their identity initialisation; the
+    checkpoint is read without unpickling anything but PrimeConfig."""
+    import dataclasses
+    from prime_moment_attention import PrimeConfig, PrimeForCausalLM
+    cfg = PrimeConfig(vocab_size=96, hidden_size=128, num_layers=2, num_heads=2, head_dim=64, decay=0.99)
+    torch.manual_seed(0)
+    base = PrimeForCausalLM(cfg)
+    path = tmp_path / "base.pt"
+    torch.save({"config": dataclasses.asdict(cfg) if config_as_dict else cfg,
+                "model_state_dict": base.state_dict()}, path)
+    sel = PrimeForCausalLM.from_pretrained_base_to_selective(str(path))
+    assert sel.config.use_selective and sel.config.decay == 0.99
+    sd_b, sd_s = base.state_dict(), sel.state_dict()
+    for k, v in sd_b.items():
+        assert torch.equal(sd_s[k], v), k
+    new = set(sd_s) - set(sd_b)
+    assert new and all(k.split(".")[-2] in ("delta_proj",) or k.endswith(("log_tau", "log_beta")) for k in new), new
+    for layer in sel.layers:
+        at = layer.self_attn
+        assert not at.delta_proj.weight.any()
+        lam = torch.exp(-torch.nn.functional.softplus(at.delta_proj.bias) / at.get_tau(at.log_tau.device))
+        assert torch.allclose(lam, torch.full_like(lam, 0.99), rtol=1e-5)
+        assert torch.equal(at.get_beta(at.log_beta.device), torch.ones_like(at.log_beta))
+
+
+def test_base_to_selective_needs_a_config(tmp_path):
+    from prime_moment_attention import PrimeForCausalLM
+    path = tmp_path / "noconf.pt"
+    torch.save({"model_state_dict": {}}, path)
+    with pytest.raises(ValueError, match="no saved config"):
+        PrimeForCausalLM.from_pretrained_base_to_selective(str(path))
