@@ -230,6 +230,31 @@ int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k,
 size_t prime_delta_prefill_workspace_size(int B, int H, int L, unsigned flags);
 
 /*
+ * Backward of prime_delta_prefill: gradients of the chunked delta-rule
+ * prefill (the autograd graph of chunked_delta_prime.py:177-283 -- features
+ * :73-87, the per-chunk triangular solve, the per-chunk Lyapunov clamp) with
+ * respect to q, k, v, beta, alpha and the incoming state, given dy (the
+ * gradient of y) and dstate_out (of the final state; NULL = zero).
+ *   q, k, v, beta, alpha, decay_pad, feat_eps, bound, state_in: as the forward
+ *   dy           : [B, H, L, D], BF16 or F32, strided
+ *   dq, dk, dv   : fp32 contiguous [B, H, L, D] -- dk and dv per QUERY head
+ *                  (the caller sums the H / H_kv heads of a group)
+ *   dbeta, dalpha: fp32 [B, H, L]; dalpha is 0 where alpha is outside the
+ *                  forward's clamp [1e-5, 1]
+ *   dstate_in    : fp32 [B, H, D, 2D] or NULL
+ *   workspace    : prime_delta_prefill_backward_workspace_size(B, H, L) bytes
+ *                  (the state entering every chunk, recomputed in fp32)
+ * fp32 arithmetic throughout.
+ */
+size_t prime_delta_prefill_backward_workspace_size(int B, int H, int L);
+int prime_delta_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                                 const float *beta, const float *alpha, int B, int H, int H_kv, int L, int D,
+                                 int chunk, float decay_pad, float feat_eps, float bound, const float *state_in,
+                                 const prime_tensor_t *dy, const float *dstate_out, float *dq, float *dk, float *dv,
+                                 float *dbeta, float *dalpha, float *dstate_in, void *workspace,
+                                 size_t workspace_bytes, void *stream);
+
+/*
  * One delta-rule PRIME decode step.  Replaces the L == 1 branch of
  * ChunkedGatedDeltaPrimeAttention.forward (chunked_delta_prime.py:140-176),
  * which predicts with the undecayed state: v_hat = S phi, S <- alpha S +

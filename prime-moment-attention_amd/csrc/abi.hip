@@ -998,6 +998,53 @@ int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const 
                      "delta prefill launch");
 }
 
+size_t prime_delta_prefill_backward_workspace_size(int B, int H, int L) {
+    if (B <= 0 || H <= 0 || L <= 0) return 0;
+    const size_t NC = (static_cast<size_t>(L) + prime::kDeltaChunk - 1) / prime::kDeltaChunk;
+    return static_cast<size_t>(B) * H * NC * prime::kDeltaStateBytes;
+}
+
+int prime_delta_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                                 const float *beta, const float *alpha, int B, int H, int H_kv, int L, int D,
+                                 int chunk, float decay_pad, float feat_eps, float bound, const float *state_in,
+                                 const prime_tensor_t *dy, const float *dstate_out, float *dq, float *dk, float *dv,
+                                 float *dbeta, float *dalpha, float *dstate_in, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    if (!q || !k || !v || !dy || !q->data || !k->data || !v->data || !dy->data || !beta || !alpha || !dq || !dk ||
+        !dv || !dbeta || !dalpha || !workspace)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_delta_prefill_backward: null argument");
+    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d", B, H, H_kv, L);
+    if (chunk != prime::kDeltaChunk)
+        return fail(PRIME_ERR_INVALID_ARG, "chunk %d unsupported: the per-chunk clamp fixes chunk = 64", chunk);
+    if (q->dtype != k->dtype || q->dtype != v->dtype || (q->dtype != PRIME_BF16 && q->dtype != PRIME_F32))
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "q/k/v must share dtype BF16 or F32");
+    if (dy->dtype != PRIME_BF16 && dy->dtype != PRIME_F32)
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "dy must be BF16 or F32");
+    if (!rows_aligned(q, true) || !rows_aligned(k, true) || !rows_aligned(v, true) || !rows_aligned(dy, true))
+        return fail(PRIME_ERR_MISALIGNED, "q/k/v/dy rows must start on 16-byte boundaries");
+    if (!aligned16(workspace)) return fail(PRIME_ERR_MISALIGNED, "workspace must be 16-byte aligned");
+    if (workspace_bytes < prime_delta_prefill_backward_workspace_size(B, H, L))
+        return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes is below the %zu this shape needs", workspace_bytes,
+                    prime_delta_prefill_backward_workspace_size(B, H, L));
+    prime::DeltaBwdArgs a{};
+    a.q = q->data; a.k = k->data; a.v = v->data; a.dy = dy->data;
+    a.q_sb = q->stride_b; a.q_sh = q->stride_h; a.q_sl = q->stride_l;
+    a.k_sb = k->stride_b; a.k_sh = k->stride_h; a.k_sl = k->stride_l;
+    a.v_sb = v->stride_b; a.v_sh = v->stride_h; a.v_sl = v->stride_l;
+    a.dy_sb = dy->stride_b; a.dy_sh = dy->stride_h; a.dy_sl = dy->stride_l;
+    a.dt_in = q->dtype; a.dt_dy = dy->dtype;
+    a.B = B; a.H = H; a.group = H / H_kv; a.L = L;
+    a.beta = beta; a.alpha = alpha;
+    a.decay_pad = decay_pad; a.feat_eps = feat_eps; a.bound = bound;
+    a.state_in = state_in; a.dstate_out = dstate_out;
+    a.dq = dq; a.dk = dk; a.dv = dv; a.dbeta = dbeta; a.dalpha = dalpha; a.dstate_in = dstate_in;
+    a.ws = static_cast<float *>(workspace);
+    return check_hip(prime::launch_delta_backward(a, static_cast<hipStream_t>(stream)), "delta backward launch");
+}
+
 int prime_delta_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
                             const float *beta, const float *alpha, int B, int H, int H_kv, int D,
                             float feat_eps, float bound, const float *state_in, float *state_out,

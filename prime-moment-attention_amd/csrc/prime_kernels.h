@@ -250,6 +250,25 @@ struct DeltaArgs {
     int first, last;            // window is the first / last of the call
 };
 
+// Backward of the delta-rule prefill (delta_bwd.hip): q, k, v, dy strided
+// [B, H(kv), L, D]; gradients fp32 contiguous, dk / dv per query head
+// ([B, H, L, D]); ws = [B*H][chunks][D*2D] fp32 (the state entering each chunk).
+struct DeltaBwdArgs {
+    const void *q, *k, *v, *dy;
+    int64_t q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl, dy_sb, dy_sh, dy_sl;
+    int dt_in, dt_dy;
+    int B, H, group, L;
+    const float *beta, *alpha;  // [B, H, L]
+    float decay_pad, feat_eps, bound;
+    const float *state_in;      // [B, H, D, 2D] or null
+    const float *dstate_out;    // [B, H, D, 2D] or null
+    float *dq, *dk, *dv;        // [B, H, L, D]
+    float *dbeta, *dalpha;      // [B, H, L]
+    float *dstate_in;           // [B, H, D, 2D] or null
+    float *ws;
+};
+hipError_t launch_delta_backward(const DeltaBwdArgs &a, hipStream_t stream);
+
 // One delta-rule decode step (delta.hip).
 struct DeltaStepArgs {
     const void *q, *k, *v;

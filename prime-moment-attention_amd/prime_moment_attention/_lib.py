@@ -32,7 +32,8 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_chunked_prefill_backward_workspace_size", "prime_chunked_prefill_qknorm",
            "prime_selective_prefill_qknorm", "prime_accumulate_noalloc", "prime_selective_prefill_backward",
            "prime_selective_prefill_backward_workspace_size", "prime_hbm_stream",
-           "prime_frag_rows", "prime_pack_frag", "prime_linear_frag_workspace_size", "prime_linear_frag")
+           "prime_frag_rows", "prime_pack_frag", "prime_linear_frag_workspace_size", "prime_linear_frag",
+           "prime_delta_prefill_backward", "prime_delta_prefill_backward_workspace_size")
 
 # bytes of the fixed device scratch behind prime_accumulate_noalloc
 NOALLOC_SCRATCH_BYTES = 32 << 20
@@ -166,6 +167,11 @@ def load() -> ctypes.CDLL:
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     L.prime_hbm_stream.argtypes = [fp, fp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, fp]
     L.prime_hbm_stream.restype = ctypes.c_int
+    L.prime_delta_prefill_backward_workspace_size.argtypes = [ctypes.c_int] * 3
+    L.prime_delta_prefill_backward_workspace_size.restype = ctypes.c_size_t
+    L.prime_delta_prefill_backward.argtypes = [P(PrimeTensor)] * 3 + [fp, fp] + [ctypes.c_int] * 6 + [
+        ctypes.c_float] * 3 + [fp, P(PrimeTensor)] + [fp] * 8 + [ctypes.c_size_t, fp]
+    L.prime_delta_prefill_backward.restype = ctypes.c_int
     L.prime_frag_rows.argtypes = [ctypes.c_int]
     L.prime_frag_rows.restype = ctypes.c_int
     L.prime_pack_frag.argtypes = [fp, ctypes.c_int64, ctypes.c_int64, fp, ctypes.c_int, ctypes.c_int, fp, fp]
@@ -808,6 +814,50 @@ def delta_prefill(q, k, v, beta, alpha, decay_pad: float, feat_eps: float, bound
                                     ptr(state_in), ctypes.byref(yd), ptr(state_out), ptr(workspace),
                                     workspace.numel(), _stream(q.device))
     _check(rc, "prime_delta_prefill")
+
+
+def delta_backward_workspace_size(B: int, H: int, L: int) -> int:
+    return int(load().prime_delta_prefill_backward_workspace_size(B, H, L))
+
+
+def delta_prefill_backward(q, k, v, beta, alpha, decay_pad: float, feat_eps: float, bound: float, state_in, dy,
+                           dstate_out, workspace: Optional[torch.Tensor] = None):
+    """Gradients of the chunked delta-rule prefill (prime_delta_prefill_backward)
+    for the forward's inputs: returns (dq [B,H,L,D], dk, dv [B,Hkv,L,D] summed
+    over each group of query heads, dbeta, dalpha [B,H,L], dstate_in [B,H,D,2D]
+    or None when state_in is None), all fp32."""
+    _dev_check(q, k, v, dy)
+    B, H, Lq, D = q.shape
+    Hkv = k.shape[1]
+    _shape(k, (B, Hkv, Lq, D), "k")
+    _shape(v, (B, Hkv, Lq, D), "v")
+    _shape(dy, (B, H, Lq, D), "dy")
+    _gate(beta, B, H, Lq, "beta")
+    _gate(alpha, B, H, Lq, "alpha")
+    _check_delta_state(state_in, B, H, D, "state_in")
+    _check_delta_state(dstate_out, B, H, D, "dstate_out")
+    dev = q.device
+    f32 = dict(device=dev, dtype=torch.float32)
+    dq = torch.empty(B, H, Lq, D, **f32)
+    dk = torch.empty(B, H, Lq, D, **f32)
+    dv = torch.empty(B, H, Lq, D, **f32)
+    dbeta = torch.empty(B, H, Lq, **f32)
+    dalpha = torch.empty(B, H, Lq, **f32)
+    dstate = torch.empty(B, H, D, 2 * D, **f32) if state_in is not None else None
+    if workspace is None:
+        workspace = torch.empty(delta_backward_workspace_size(B, H, Lq), dtype=torch.uint8, device=dev)
+    qd, kd, vd, yd = tensor_desc(q, True), tensor_desc(k, True), tensor_desc(v, True), tensor_desc(dy, True)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    rc = load().prime_delta_prefill_backward(
+        ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ptr(beta), ptr(alpha), B, H, Hkv, Lq, D, 64,
+        float(decay_pad), float(feat_eps), float(bound), ptr(state_in), ctypes.byref(yd), ptr(dstate_out), ptr(dq),
+        ptr(dk), ptr(dv), ptr(dbeta), ptr(dalpha), ptr(dstate), ptr(workspace),
+        workspace.numel() * workspace.element_size(), _stream(dev))
+    _check(rc, "prime_delta_prefill_backward")
+    if Hkv != H:
+        dk = dk.view(B, Hkv, H // Hkv, Lq, D).sum(2)
+        dv = dv.view(B, Hkv, H // Hkv, Lq, D).sum(2)
+    return dq, dk, dv, dbeta, dalpha, dstate
 
 
 def delta_decode_step(q, k, v, beta, alpha, feat_eps: float, bound: float, state_in, state_out, y) -> None:

@@ -15,6 +15,11 @@ The per-token scalars the kernels take are the reference's: beta =
 (:133-137).  The chunked branch clamps once per 64-token chunk, so its result
 depends on the chunk size; only ``chunk_size = 64`` (the reference default) is
 supported.
+
+Training: with autograd recording, the chunked branch runs through
+prime_delta_prefill_backward (gradients in q, k, v, beta, alpha and the
+incoming state), and the projections, QK LayerNorm and gates are the
+reference's differentiable torch ops.  The step branch has no backward.
 """
 from __future__ import annotations
 
@@ -26,6 +31,34 @@ import torch.nn as nn
 
 from . import _lib
 from .chunked_ssd import no_backward
+
+
+class _DeltaPrefillFn(torch.autograd.Function):
+    """The chunked delta-rule prefill with its HIP backward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, alpha, s_in, decay, feat_eps, bound, y_dtype):
+        B, H, L, D = q.shape
+        y = torch.empty(B, H, L, D, device=q.device, dtype=y_dtype)
+        s_out = torch.empty(B, H, D, 2 * D, device=q.device, dtype=torch.float32)
+        _lib.delta_prefill(q, k, v, beta, alpha, decay, feat_eps, bound, s_in, y, s_out)
+        ctx.save_for_backward(q, k, v, beta, alpha, s_in)
+        ctx.consts = (decay, feat_eps, bound)
+        return y, s_out
+
+    @staticmethod
+    def backward(ctx, dy, ds_out):
+        q, k, v, beta, alpha, s_in = ctx.saved_tensors
+        decay, feat_eps, bound = ctx.consts
+        if dy is None:
+            dy = torch.zeros(q.shape, device=q.device, dtype=torch.float32)
+        dy = dy.contiguous()
+        if dy.dtype not in (torch.float32, torch.bfloat16):
+            dy = dy.float()
+        ds = ds_out.contiguous().float() if ds_out is not None else None
+        dq, dk, dv, dbeta, dalpha, dstate = _lib.delta_prefill_backward(q, k, v, beta, alpha, decay, feat_eps,
+                                                                          bound, s_in, dy, ds)
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dbeta, dalpha, dstate, None, None, None, None)
 
 
 class ChunkedGatedDeltaPrimeAttention(nn.Module):
@@ -89,6 +122,10 @@ class ChunkedGatedDeltaPrimeAttention(nn.Module):
         B, L, _ = hidden_states.shape
         H, D = self.num_heads, self.head_dim
         dtype, dev = hidden_states.dtype, hidden_states.device
+        if torch.is_grad_enabled() and L > 1 and (hidden_states.requires_grad or
+                                                  any(p.requires_grad for p in self.parameters()) or
+                                                  (state is not None and state.requires_grad)):
+            return self._forward_train(hidden_states, state, return_state)
         q, k, v = self.project(hidden_states)
         beta, alpha = self.gates(hidden_states)
         if q.dtype not in (torch.bfloat16, torch.float32):
@@ -108,6 +145,33 @@ class ChunkedGatedDeltaPrimeAttention(nn.Module):
                        else t.contiguous() for t in (q, k, v))
             y = torch.empty(B, H, L, D, device=dev, dtype=y_dtype)
             _lib.delta_prefill(q, k, v, beta, alpha, self.decay, self.eps, self.lyapunov_bound, s_in, y, s_out)
-        y = no_backward("the delta-rule PRIME recurrence", y, q, k, v, beta, alpha, s_in)
+        y = no_backward("the delta-rule PRIME decode step", y, q, k, v, beta, alpha, s_in)
+        y = y.to(dtype).transpose(1, 2).reshape(B, L, H * D)
+        return self.o_proj(y), (s_out if return_state else None)
+
+    def _forward_train(self, hidden_states, state, return_state):
+        """The chunked branch under autograd: the reference's torch ops for the
+        projections, QK LayerNorm, scale and gates (chunked_delta_prime.py:
+        105-137), the HIP prefill and its backward for the recurrence."""
+        B, L, _ = hidden_states.shape
+        H, D = self.num_heads, self.head_dim
+        dtype, dev = hidden_states.dtype, hidden_states.device
+        q = self.q_proj(hidden_states).view(B, L, H, D).transpose(1, 2)
+        k = self.k_proj(hidden_states).view(B, L, self.num_kv_heads, D).transpose(1, 2)
+        v = self.v_proj(hidden_states).view(B, L, self.num_kv_heads, D).transpose(1, 2)
+        if self.use_qk_norm:
+            q = self.q_norm(q)
+            k = self.k_norm(k)
+        q = q * self.scaling
+        beta, alpha = self.gates(hidden_states)
+        if q.dtype not in (torch.bfloat16, torch.float32):
+            q, k, v = q.float(), k.float(), v.float()
+        q, k, v = (t.contiguous() for t in (q, k, v))
+        y_dtype = dtype if dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
+        s_in = None
+        if state is not None:
+            s_in = state.to(device=dev, dtype=torch.float32).reshape(B, H, D, 2 * D).contiguous()
+        y, s_out = _DeltaPrefillFn.apply(q, k, v, beta, alpha, s_in, self.decay, self.eps, self.lyapunov_bound,
+                                         y_dtype)
         y = y.to(dtype).transpose(1, 2).reshape(B, L, H * D)
         return self.o_proj(y), (s_out if return_state else None)

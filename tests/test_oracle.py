@@ -672,3 +672,70 @@ def test_dense_vjp_matches_torch_autograd_of_the_double_clamp():
     for got, ref in zip(dst, ts):
         r = ref.grad.numpy().reshape(got.shape)
         assert np.abs(got - r).max() <= 1e-10 * max(1.0, np.abs(r).max())
+
+
+# ---------------------------------------------------------------- delta backward reference
+def _delta_case(B, H, L, D, seed, bound):
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    q = torch.nn.functional.normalize(torch.randn(B, H, L, D, generator=g, dtype=torch.float64), dim=-1) / D ** 0.5
+    k = torch.randn(B, H, L, D, generator=g, dtype=torch.float64)
+    v = torch.randn(B, H, L, D, generator=g, dtype=torch.float64)
+    beta = torch.sigmoid(torch.randn(B, H, L, generator=g, dtype=torch.float64)) * 0.5
+    alpha = 0.999 * (1 - 0.5 * torch.sigmoid(torch.randn(B, H, L, generator=g, dtype=torch.float64) - 2.5))
+    state = torch.randn(B, H, D, 2 * D, generator=g, dtype=torch.float64) * 0.3
+    return q, k, v, beta, alpha, state
+
+
+@pytest.mark.parametrize("L,bound", [(64 * 3 + 17, 25.0), (64 * 2 + 5, 1.5), (40, 0.8)])
+def test_delta_torch_restatement_matches_oracle(L, bound):
+    """tests/delta_ref.py (differentiable torch ops) computes what the fp64 C
+    oracle computes: y and the final state, ragged L, incoming state, the
+    clamp active (bounds 1.5 and 0.8 engage it) or not."""
+    import torch
+    import delta_ref as R
+    B, H, D = 1, 2, 64
+    q, k, v, beta, alpha, state = _delta_case(B, H, L, D, L, bound)
+    y, S = R.delta_chunked(q, k, v, beta, alpha, 0.9995, 1e-5, bound, 64, state)
+    psi, phi = O.delta_features(q.reshape(B * H, L, D).numpy(), k.reshape(B * H, L, D).numpy(), eps=1e-5)
+    yo, So = O.delta_chunked(psi, phi, v.reshape(B * H, L, D).numpy(), beta.reshape(B * H, L).numpy(),
+                             alpha.reshape(B * H, L).numpy(), 0.9995, bound=bound, chunk=64,
+                             state=state.reshape(B * H, D, 2 * D).numpy())
+    assert O.rel_err(y.reshape(B * H, L, D).numpy(), yo) < 1e-12
+    assert O.rel_err(S.reshape(B * H, D, 2 * D).numpy(), So) < 1e-12
+    if bound < 25.0:
+        assert float(S.norm(dim=(-2, -1)).max()) <= bound * (1 + 1e-9)
+
+
+@pytest.mark.parametrize("bound", [25.0, 0.6])
+def test_delta_torch_autograd_matches_central_differences(bound):
+    """fp64 autograd of the restatement against central differences of the
+    loss along random directions, for every input (q, k, v, beta, alpha, the
+    incoming state), with two chunks, a ragged tail and (bound 0.6) the
+    per-chunk clamp active: the reference gradients are the function's."""
+    import torch
+    import delta_ref as R
+    B, H, L, D = 1, 1, 64 + 21, 8
+    xs = list(_delta_case(B, H, L, D, 3, bound))
+    g = torch.Generator().manual_seed(9)
+    ry = torch.randn(B, H, L, D, generator=g, dtype=torch.float64)
+    rs = torch.randn(B, H, D, 2 * D, generator=g, dtype=torch.float64)
+
+    def loss(*a):
+        y, S = R.delta_chunked(*a[:5], 0.9995, 1e-5, bound, 64, a[5])
+        return (y * ry).sum() + (S * rs).sum()
+
+    for t in xs:
+        t.requires_grad_(True)
+    grads = torch.autograd.grad(loss(*xs), xs)
+    with torch.no_grad():
+        for i, (x, gr) in enumerate(zip(xs, grads)):
+            u = torch.randn(x.shape, generator=g, dtype=torch.float64)
+            h = 1e-6
+            xp = [t.detach().clone() for t in xs]
+            xm = [t.detach().clone() for t in xs]
+            xp[i] += h * u
+            xm[i] -= h * u
+            fd = (loss(*xp) - loss(*xm)) / (2 * h)
+            an = (gr * u).sum()
+            assert abs(float(fd - an)) <= 1e-6 * max(1.0, abs(float(an))), (i, float(fd), float(an))
