@@ -17,7 +17,14 @@
  *                to one value per head; pass H copies of the scalar for the
  *                reference behaviour)
  * q is taken PRE-SCALED by 1/sqrt(D), as at the reference's core boundary
- * (chunked_ssd.py:58-61, attention.py:101).  D must be 64.
+ * (chunked_ssd.py:58-61, attention.py:101).
+ *
+ * Head dim: D = 64 runs the MFMA chunk kernels; the base form (prefill,
+ * decode step, backward, QK-norm) also takes 1 <= D <= 63 (the reference's
+ * own tests use 32 and 16), run token by token in one wavefront per
+ * (sequence, head) with no row-alignment requirement and no workspace beyond
+ * the backward's per-token records.  The selective and delta-rule forms,
+ * prime_accumulate and the split decode readout/update take D = 64 only.
  */
 #ifndef PRIME_MI355X_H
 #define PRIME_MI355X_H
@@ -39,7 +46,7 @@ extern "C" {
 /* error codes */
 #define PRIME_OK                   0
 #define PRIME_ERR_INVALID_ARG     -1  /* null pointer, bad size, inconsistent shape */
-#define PRIME_ERR_UNSUPPORTED_DIM -2  /* head dim other than 64 */
+#define PRIME_ERR_UNSUPPORTED_DIM -2  /* head dim not taken by this entry point */
 #define PRIME_ERR_UNSUPPORTED_DTYPE -3
 #define PRIME_ERR_MISALIGNED      -4  /* pointer/stride breaks 16-byte row alignment */
 #define PRIME_ERR_ALIAS           -5  /* output overlaps an input it may not alias */
@@ -275,7 +282,7 @@ int prime_delta_decode_step(const prime_tensor_t *q, const prime_tensor_t *k,
  * param_dtype, epsilon ln_eps) rounded to x's dtype, then multiplied by
  * `scale` and rounded again (pass 1/sqrt(D) for q, 1 for k).  weight = bias =
  * NULL applies the scale only (a module without QK-norm).  x, out: strided
- * [B, H, L, D] views of one dtype, D = 64; out may be x (the same view) but may
+ * [B, H, L, D] views of one dtype, D = 64 (or 1 .. 63); out may be x (the same view) but may
  * not partly overlap it.  The chunked prefill's producer for q and k.
  */
 int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int B, int H, int L, int D,

@@ -102,6 +102,54 @@ int check_hip(hipError_t e, const char *what) {
     return PRIME_OK;
 }
 
+// Head dims below 64 (generic_d.hip): argument descriptor shared by the
+// prefill, the decode step and the backward.
+int generic_args(prime::GenericArgs &a, const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                 int B, int H, int H_kv, int L, int D, const float *decay, float eps, unsigned flags,
+                 const prime_state_t *state_in, const prime_state_t *state_out) {
+    if (D < 1 || D > prime::kGenericMaxD)
+        return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (64, or 1 .. %d)", D, prime::kGenericMaxD);
+    if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d", B, H, H_kv, L);
+    if (flags & ~PRIME_FLAG_DENSE_CLAMP) return fail(PRIME_ERR_INVALID_ARG, "unknown flags 0x%x", flags);
+    if (!valid_dtype(q->dtype) || !valid_dtype(k->dtype) || !valid_dtype(v->dtype))
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported q/k/v dtype");
+    int rc;
+    if ((rc = check_state(state_in, "state_in")) || (rc = check_state(state_out, "state_out"))) return rc;
+    bool inplace;
+    if ((rc = check_state_alias(state_in, state_out, static_cast<size_t>(B) * H, D, &inplace))) return rc;
+    a.q = q->data; a.k = k->data; a.v = v->data;
+    a.q_sb = q->stride_b; a.q_sh = q->stride_h; a.q_sl = q->stride_l;
+    a.k_sb = k->stride_b; a.k_sh = k->stride_h; a.k_sl = k->stride_l;
+    a.v_sb = v->stride_b; a.v_sh = v->stride_h; a.v_sl = v->stride_l;
+    a.dt_q = q->dtype; a.dt_k = k->dtype; a.dt_v = v->dtype;
+    a.B = B; a.H = H; a.group = H / H_kv; a.L = L; a.D = D;
+    a.decay = decay; a.eps = eps;
+    a.dense_clamp = (flags & PRIME_FLAG_DENSE_CLAMP) ? 1 : 0;
+    if (state_in) {
+        a.s0i = state_in->s0; a.s1i = state_in->s1; a.s2i = state_in->s2;
+        a.k0i = state_in->k0; a.k1i = state_in->k1; a.k2i = state_in->k2;
+    }
+    if (state_out) {
+        a.s0o = state_out->s0; a.s1o = state_out->s1; a.s2o = state_out->s2;
+        a.k0o = state_out->k0; a.k1o = state_out->k1; a.k2o = state_out->k2;
+    }
+    return PRIME_OK;
+}
+
+int generic_norm(prime::GenericArgs &a, const prime_qk_norm_t *norm) {
+    if (!norm) return PRIME_OK;
+    if ((norm->q_weight == nullptr) != (norm->q_bias == nullptr) ||
+        (norm->k_weight == nullptr) != (norm->k_bias == nullptr))
+        return fail(PRIME_ERR_INVALID_ARG, "QK-norm: LayerNorm weight without bias or bias without weight");
+    if ((norm->q_weight || norm->k_weight) && !valid_dtype(norm->dtype))
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported norm dtype");
+    a.qk_norm = 1;
+    a.qn_w = norm->q_weight; a.qn_b = norm->q_bias; a.kn_w = norm->k_weight; a.kn_b = norm->k_bias;
+    a.dt_norm = norm->dtype; a.ln_eps = norm->eps; a.q_scale = norm->q_scale;
+    return PRIME_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -123,7 +171,20 @@ int decode_impl(const prime_tensor_t *q, const prime_tensor_t *k, const prime_te
     if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !(decay || selective) || !state_out ||
         (selective && !k_scale))
         return fail(PRIME_ERR_INVALID_ARG, "prime_decode_step: null argument");
-    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (D != prime::kD) {
+        // head dims below 64: the generic recurrence over one token
+        if (selective) return fail(PRIME_ERR_UNSUPPORTED_DIM, "the selective form takes head dim 64 (got %d)", D);
+        if (!valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported y dtype");
+        if (y->layout != PRIME_LAYOUT_STRIDED)
+            return fail(PRIME_ERR_INVALID_ARG, "head dim %d: y must be a strided view", D);
+        prime::GenericArgs g{};
+        int rc;
+        if ((rc = generic_args(g, q, k, v, B, H, H_kv, 1, D, decay, eps, 0u, state_in, state_out)) ||
+            (rc = generic_norm(g, norm)))
+            return rc;
+        g.y = y->data; g.dt_y = y->dtype; g.y_sb = y->stride_b; g.y_sh = y->stride_h; g.y_sl = 0;
+        return check_hip(prime::launch_generic_prefill(g, static_cast<hipStream_t>(stream)), "decode launch");
+    }
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv)
         return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d", B, H, H_kv);
     if (!valid_dtype(q->dtype) || !valid_dtype(k->dtype) || !valid_dtype(v->dtype) || !valid_dtype(y->dtype))
@@ -227,7 +288,8 @@ int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int
                          void *stream) {
     g_err[0] = 0;
     if (!x || !out || !x->data || !out->data) return fail(PRIME_ERR_INVALID_ARG, "prime_head_layernorm: null argument");
-    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (D != prime::kD && (D < 1 || D > prime::kGenericMaxD))
+        return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (64, or 1 .. %d)", D, prime::kGenericMaxD);
     if (B <= 0 || H <= 0 || L <= 0) return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d L=%d", B, H, L);
     if (static_cast<int64_t>(B) * H * L >= (int64_t(1) << 31))
         return fail(PRIME_ERR_INVALID_ARG, "B*H*L = %lld rows exceeds 2^31 - 1",
@@ -237,7 +299,7 @@ int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int
     if ((weight == nullptr) != (bias == nullptr))
         return fail(PRIME_ERR_INVALID_ARG, "LayerNorm weight and bias must both be given or both be null");
     if (weight && !valid_dtype(param_dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported parameter dtype");
-    if (!rows_aligned(x, true) || !rows_aligned(out, true))
+    if (D == prime::kD && (!rows_aligned(x, true) || !rows_aligned(out, true)))
         return fail(PRIME_ERR_MISALIGNED, "x/out rows must start on 16-byte boundaries");
     const int64_t es = elem_size(x->dtype);
     auto span = [&](const prime_tensor_t *t) {
@@ -252,7 +314,10 @@ int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int
     a.x_sb = x->stride_b; a.x_sh = x->stride_h; a.x_sl = x->stride_l;
     a.o_sb = out->stride_b; a.o_sh = out->stride_h; a.o_sl = out->stride_l;
     a.B = B; a.H = H; a.L = L; a.dt = x->dtype; a.dt_norm = param_dtype;
-    a.ln_eps = ln_eps; a.scale = scale;
+    a.ln_eps = ln_eps; a.scale = scale; a.D = D;
+    if (D != prime::kD)
+        return check_hip(prime::launch_generic_head_layernorm(a, static_cast<hipStream_t>(stream)),
+                         "head_layernorm launch");
     return check_hip(prime::launch_head_layernorm(a, static_cast<hipStream_t>(stream)), "head_layernorm launch");
 }
 
@@ -452,7 +517,19 @@ static int prefill_impl(const prime_tensor_t *q, const prime_tensor_t *k, const 
     if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !(decay || selective) ||
         (selective && !k_scale))
         return fail(PRIME_ERR_INVALID_ARG, "prefill: null argument");
-    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (D != prime::kD) {
+        // head dims below 64: one wavefront per (sequence, head), chunk size irrelevant
+        if (selective) return fail(PRIME_ERR_UNSUPPORTED_DIM, "the selective form takes head dim 64 (got %d)", D);
+        if (chunk <= 0) return fail(PRIME_ERR_INVALID_ARG, "bad chunk %d", chunk);
+        if (!valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported y dtype");
+        prime::GenericArgs g{};
+        int rc;
+        if ((rc = generic_args(g, q, k, v, B, H, H_kv, L, D, decay, eps, flags, state_in, state_out)) ||
+            (rc = generic_norm(g, norm)))
+            return rc;
+        g.y = y->data; g.dt_y = y->dtype; g.y_sb = y->stride_b; g.y_sh = y->stride_h; g.y_sl = y->stride_l;
+        return check_hip(prime::launch_generic_prefill(g, static_cast<hipStream_t>(stream)), "prefill launch");
+    }
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0 || chunk <= 0)
         return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d chunk=%d", B, H, H_kv, L, chunk);
     if (flags & ~PRIME_FLAG_DENSE_CLAMP) return fail(PRIME_ERR_INVALID_ARG, "unknown flags 0x%x", flags);
@@ -701,7 +778,40 @@ int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t
     if (!q || !k || !v || !dy || !dq || !dk || !dv || !q->data || !k->data || !v->data || !dy->data || !dq->data ||
         !dk->data || !dv->data || !decay || !workspace)
         return fail(PRIME_ERR_INVALID_ARG, "prime_chunked_prefill_backward: null argument");
-    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (D != prime::kD) {
+        // head dims below 64: the generic reverse pass (workspace: the per-token
+        // denominators, as the 64 path's minimum)
+        if (H_kv != H)
+            return fail(PRIME_ERR_INVALID_ARG, "backward takes k/v with one head per query head (H_kv=%d, H=%d)",
+                        H_kv, H);
+        if (!valid_dtype(dy->dtype) || !valid_dtype(dq->dtype))
+            return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dy / gradient dtype");
+        if (dk->dtype != dq->dtype || dv->dtype != dq->dtype || dk->stride_b != dq->stride_b ||
+            dv->stride_b != dq->stride_b || dk->stride_h != dq->stride_h || dv->stride_h != dq->stride_h ||
+            dk->stride_l != dq->stride_l || dv->stride_l != dq->stride_l)
+            return fail(PRIME_ERR_INVALID_ARG, "dq, dk and dv must share dtype and strides");
+        if (B > 0 && H > 0 && L > 0 && (workspace_bytes < bwd_token_bytes(B, H, L) || !aligned16(workspace)))
+            return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes (16-byte aligned) is below the %zu needed",
+                        workspace_bytes, bwd_token_bytes(B, H, L));
+        prime::GenericArgs g{};
+        int rc;
+        if ((rc = generic_args(g, q, k, v, B, H, H_kv, L, D, decay, eps, flags, state_in, nullptr)) ||
+            (rc = check_state(dstate_out, "dstate_out")) || (rc = check_state(dstate_in, "dstate_in")))
+            return rc;
+        g.dy = dy->data; g.dt_dy = dy->dtype; g.dy_sb = dy->stride_b; g.dy_sh = dy->stride_h; g.dy_sl = dy->stride_l;
+        if (dstate_out) {
+            g.ds0 = dstate_out->s0; g.ds1 = dstate_out->s1; g.ds2 = dstate_out->s2;
+            g.dk0 = dstate_out->k0; g.dk1 = dstate_out->k1; g.dk2 = dstate_out->k2;
+        }
+        g.dq = dq->data; g.dk = dk->data; g.dv = dv->data; g.dt_g = dq->dtype;
+        g.g_sb = dq->stride_b; g.g_sh = dq->stride_h; g.g_sl = dq->stride_l;
+        if (dstate_in) {
+            g.dsi0 = dstate_in->s0; g.dsi1 = dstate_in->s1; g.dsi2 = dstate_in->s2;
+            g.dki0 = dstate_in->k0; g.dki1 = dstate_in->k1; g.dki2 = dstate_in->k2;
+        }
+        g.ws = static_cast<float *>(workspace);
+        return check_hip(prime::launch_generic_backward(g, static_cast<hipStream_t>(stream)), "backward launch");
+    }
     if (B <= 0 || H <= 0 || L <= 0) return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d L=%d", B, H, L);
     if (H_kv != H)
         return fail(PRIME_ERR_INVALID_ARG, "backward takes k/v with one head per query head (H_kv=%d, H=%d): "

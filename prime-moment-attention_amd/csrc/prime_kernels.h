@@ -61,14 +61,16 @@ hipError_t launch_argmax_rows(const ArgmaxArgs &a, hipStream_t stream);
 
 // Per-head LayerNorm (+ scale) of projected q or k rows (norm.hip).
 struct HeadNormArgs {
-    const void *x;        // [B, H, L, 64] view, element strides below
+    const void *x;        // [B, H, L, D] view, element strides below
     void *out;            // same shape, own strides; may be x itself
-    const void *weight, *bias;  // [64] each, or null (no LayerNorm: scale only)
+    const void *weight, *bias;  // [D] each, or null (no LayerNorm: scale only)
     int64_t x_sb, x_sh, x_sl, o_sb, o_sh, o_sl;
     int B, H, L, dt, dt_norm;
     float ln_eps, scale;
+    int D;                // 64 (norm.hip), or below 64 (generic_d.hip)
 };
 hipError_t launch_head_layernorm(const HeadNormArgs &a, hipStream_t stream);
+hipError_t launch_generic_head_layernorm(const HeadNormArgs &a, hipStream_t stream);
 
 // Skinny bf16 linear layer y = epilogue(x w^T) (gemm.hip).
 struct LinearArgs {
@@ -249,6 +251,39 @@ struct DeltaArgs {
     int c0, nw;                 // window: chunks c0 .. c0 + nw - 1
     int first, last;            // window is the first / last of the call
 };
+
+// Head dims below 64 (generic_d.hip): one wavefront per (sequence, head).
+struct GenericArgs {
+    const void *q, *k, *v;
+    int64_t q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;
+    int dt_q, dt_k, dt_v;
+    int B, H, group, L, D;
+    const float *decay;
+    float eps;
+    int dense_clamp;
+    const float *s0i, *s1i, *s2i, *k0i, *k1i, *k2i;  // incoming state or null
+    float *s0o, *s1o, *s2o, *k0o, *k1o, *k2o;        // final state or null
+    void *y;
+    int dt_y;
+    int64_t y_sb, y_sh, y_sl;
+    int qk_norm;  // forward only: LayerNorm weights (may be null) and q scale
+    const void *qn_w, *qn_b, *kn_w, *kn_b;
+    int dt_norm;
+    float ln_eps, q_scale;
+    // backward
+    const void *dy;
+    int dt_dy;
+    int64_t dy_sb, dy_sh, dy_sl;
+    const float *ds0, *ds1, *ds2, *dk0, *dk1, *dk2;  // adjoint of the final state or null
+    void *dq, *dk, *dv;
+    int dt_g;
+    int64_t g_sb, g_sh, g_sl;
+    float *dsi0, *dsi1, *dsi2, *dki0, *dki1, *dki2;  // adjoint of the incoming state or null
+    float *ws;                                        // [B*H][L][2]
+};
+constexpr int kGenericMaxD = 63;
+hipError_t launch_generic_prefill(const GenericArgs &a, hipStream_t stream);
+hipError_t launch_generic_backward(const GenericArgs &a, hipStream_t stream);
 
 // Backward of the delta-rule prefill (delta_bwd.hip): q, k, v, dy strided
 // [B, H(kv), L, D]; gradients fp32 contiguous, dk / dv per query head

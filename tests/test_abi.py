@@ -44,8 +44,11 @@ def test_bad_dims_and_dtypes_rejected():
     t = _lib.PrimeTensor(16, _lib.PRIME_BF16, 0, 0, 0, 0)  # never dereferenced: validation fails first
     st = _lib.PrimeState(16, 16, 16, 16, 16, 16)
     b = ctypes.byref
-    rc = L.prime_decode_step(b(t), b(t), b(t), 1, 1, 1, 32, 16, 1.0, None, b(st), b(t), None)
-    assert rc == -2 and "head dim" in _lib.last_error()
+    for D in (0, 65, 96, 128):  # 64, or 1 .. 63 (the token-sequential kernels)
+        rc = L.prime_decode_step(b(t), b(t), b(t), 1, 1, 1, D, 16, 1.0, None, b(st), b(t), None)
+        assert rc == -2 and "head dim" in _lib.last_error()
+    rc = L.prime_decode_step(b(t), b(t), b(t), 1, 3, 2, 32, 16, 1.0, None, b(st), b(t), None)
+    assert rc == -1  # head dim 32 is taken; H not a multiple of H_kv
     rc = L.prime_decode_step(b(t), b(t), b(t), 1, 3, 2, 64, 16, 1.0, None, b(st), b(t), None)
     assert rc == -1  # H not a multiple of H_kv
     t16 = _lib.PrimeTensor(16, _lib.PRIME_F16, 0, 0, 0, 0)

@@ -125,9 +125,9 @@ def test_decode_rejects_bad_arguments():
     x = torch.zeros(B, H, D, device=dev())
     st = _lib.new_state(B, H, D, dev())
     dec = to_dev(np.ones(H, np.float32))
-    with pytest.raises(RuntimeError, match="head dim"):
-        _lib.decode_step(x[..., :32], x[..., :32], x[..., :32], dec, 1.0, None,
-                         _lib.new_state(B, H, 32, dev()), x[..., :32])
+    xw = torch.zeros(B, H, 96, device=dev())
+    with pytest.raises(RuntimeError, match="head dim"):  # 64, or 1 .. 63
+        _lib.decode_step(xw, xw, xw, dec, 1.0, None, _lib.new_state(B, H, 96, dev()), xw)
     # partially overlapping in/out state
     st_bad = (st[0], st[1], st[2], st[3], st[4], st[4])
     st_in = _lib.new_state(B, H, D, dev())

@@ -3,6 +3,8 @@ reference) on the HIP kernels: logits against an fp32 CPU composition of the
 same weights (textbook layers + the fp32 PyTorch-CPU restatement of the PRIME
 core from oracle/torch_cpu.py), prefill/decode continuity, and the HIP-graph
 greedy decoder against eager generation."""
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -49,7 +51,7 @@ def _ref_forward(model, ids, L_threshold=512):
         if cfg.use_qk_norm:
             q = F.layer_norm(q, (D,), W[p + "self_attn.q_norm.weight"], W[p + "self_attn.q_norm.bias"])
             k = F.layer_norm(k, (D,), W[p + "self_attn.k_norm.weight"], W[p + "self_attn.k_norm.bias"])
-        q = q / 8.0
+        q = q / math.sqrt(D)
         y, _ = TC.chunked_core(q.contiguous(), k.contiguous(), v.contiguous(), cfg.decay, eps=cfg.eps)
         y = y.transpose(1, 2).reshape(B, L, H * D)
         x = x + y @ W[p + "self_attn.o_proj.weight"].T
