@@ -204,8 +204,13 @@ size_t prime_chunked_prefill_workspace_size(int B, int H, int L, unsigned flags)
  *   decay_pad : alpha of the zero tokens padding the last chunk (:189, the
  *               module's decay; the final state keeps that padding's decay)
  *   bound     : Lyapunov bound; <= 0 disables the clamp (:266-270)
- *   chunk     : must be 64 (the clamp is applied per chunk, so the result
- *               depends on the chunk size)
+ *   chunk     : tokens per clamp (the reference's chunk_size; the result
+ *               depends on it).  D = 64 with chunk 64 runs the MFMA kernels
+ *               below; any other D in 1 .. 64 or chunk >= 1 runs the token
+ *               recurrence the chunk form unrolls (one wavefront per
+ *               (sequence, head), the clamp after every `chunk` tokens and
+ *               after the padded last chunk; q/k/v of any supported dtype, no
+ *               alignment or workspace requirement: workspace may be NULL)
  *   state_in  : fp32 [B, H, D, 2D] or NULL (zero); state_out likewise or NULL;
  *               they may be the same buffer
  *   y         : [B, H, L, D], F32 / BF16 / F16
@@ -249,11 +254,14 @@ size_t prime_delta_prefill_workspace_size(int B, int H, int L, unsigned flags);
  *   dbeta, dalpha: fp32 [B, H, L]; dalpha is 0 where alpha is outside the
  *                  forward's clamp [1e-5, 1]
  *   dstate_in    : fp32 [B, H, D, 2D] or NULL
- *   workspace    : prime_delta_prefill_backward_workspace_size(B, H, L) bytes
- *                  (the state entering every chunk, recomputed in fp32)
+ *   workspace    : prime_delta_prefill_backward_workspace_size(B, H, L, D, chunk)
+ *                  bytes (the state entering every chunk, recomputed in fp32;
+ *                  outside D = 64 with chunk 64 also one chunk's token states
+ *                  per (sequence, head), recomputed chunk by chunk for the
+ *                  reverse pass)
  * fp32 arithmetic throughout.
  */
-size_t prime_delta_prefill_backward_workspace_size(int B, int H, int L);
+size_t prime_delta_prefill_backward_workspace_size(int B, int H, int L, int D, int chunk);
 int prime_delta_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
                                  const float *beta, const float *alpha, int B, int H, int H_kv, int L, int D,
                                  int chunk, float decay_pad, float feat_eps, float bound, const float *state_in,
@@ -266,7 +274,8 @@ int prime_delta_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *
  * ChunkedGatedDeltaPrimeAttention.forward (chunked_delta_prime.py:140-176),
  * which predicts with the undecayed state: v_hat = S phi, S <- alpha S +
  * beta (v - v_hat) phi^T, Lyapunov clamp, y = S psi.
- *   q, k, v : [B, H(q) / H_kv, D] (stride_l ignored); beta, alpha: fp32 [B, H]
+ *   q, k, v : [B, H(q) / H_kv, D] (stride_l ignored; D = 64, or 1 .. 63 in
+ *             one wavefront per (sequence, head)); beta, alpha: fp32 [B, H]
  *   state_in: fp32 [B, H, D, 2D] or NULL; state_out may equal state_in
  *   y       : [B, H, D]
  */

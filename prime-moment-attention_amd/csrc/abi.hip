@@ -1047,6 +1047,42 @@ int prime_selective_decode_step(const prime_tensor_t *q, const prime_tensor_t *k
     return decode_impl(q, k, v, B, H, H_kv, D, nullptr, eps, norm, state_in, state_out, y, stream, gate, k_scale);
 }
 
+}  // extern "C"
+
+namespace {
+
+// The delta rule's shapes outside the MFMA kernels (D = 64 with chunk 64):
+// head dims 1 .. 64 with any chunk, token by token (delta_gen.hip).
+bool delta_generic(int D, int chunk) { return D != prime::kD || chunk != prime::kDeltaChunk; }
+
+int delta_gen_args(prime::DeltaGenArgs &a, const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                   const float *beta, const float *alpha, int B, int H, int H_kv, int L, int D, int chunk,
+                   float decay_pad, float feat_eps, float bound, const float *state_in, const float *state_out) {
+    if (D < 1 || D > prime::kDeltaGenMaxD)
+        return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (1 .. %d)", D, prime::kDeltaGenMaxD);
+    if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0 || chunk <= 0)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d chunk=%d", B, H, H_kv, L, chunk);
+    if (!valid_dtype(q->dtype) || !valid_dtype(k->dtype) || !valid_dtype(v->dtype))
+        return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported q/k/v dtype");
+    const size_t sbytes = static_cast<size_t>(B) * H * D * 2 * D * sizeof(float);
+    if (state_in && state_out && state_in != state_out && overlap(state_in, sbytes, state_out, sbytes))
+        return fail(PRIME_ERR_ALIAS, "state_out overlaps state_in (only a fully in-place state is allowed)");
+    a.q = q->data; a.k = k->data; a.v = v->data;
+    a.q_sb = q->stride_b; a.q_sh = q->stride_h; a.q_sl = q->stride_l;
+    a.k_sb = k->stride_b; a.k_sh = k->stride_h; a.k_sl = k->stride_l;
+    a.v_sb = v->stride_b; a.v_sh = v->stride_h; a.v_sl = v->stride_l;
+    a.dt_q = q->dtype; a.dt_k = k->dtype; a.dt_v = v->dtype;
+    a.B = B; a.H = H; a.group = H / H_kv; a.L = L; a.D = D; a.chunk = chunk;
+    a.beta = beta; a.alpha = alpha;
+    a.decay_pad = decay_pad; a.feat_eps = feat_eps; a.bound = bound;
+    a.state_in = state_in;
+    return PRIME_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 size_t prime_delta_prefill_workspace_size(int B, int H, int L, unsigned flags) {
     if (B <= 0 || H <= 0 || L <= 0) return 0;
     const int NC = (L + prime::kDeltaChunk - 1) / prime::kDeltaChunk;
@@ -1062,13 +1098,22 @@ int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const 
                         const prime_tensor_t *y, float *state_out, void *workspace, size_t workspace_bytes,
                         void *stream) {
     g_err[0] = 0;
-    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !beta || !alpha || !workspace)
+    if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !beta || !alpha)
         return fail(PRIME_ERR_INVALID_ARG, "prime_delta_prefill: null argument");
-    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (delta_generic(D, chunk)) {
+        prime::DeltaGenArgs g{};
+        int rc;
+        if ((rc = delta_gen_args(g, q, k, v, beta, alpha, B, H, H_kv, L, D, chunk, decay_pad, feat_eps, bound,
+                                 state_in, state_out)))
+            return rc;
+        if (!valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported y dtype");
+        g.state_out = state_out;
+        g.y = y->data; g.dt_y = y->dtype; g.y_sb = y->stride_b; g.y_sh = y->stride_h; g.y_sl = y->stride_l;
+        return check_hip(prime::launch_delta_gen_forward(g, static_cast<hipStream_t>(stream)), "delta prefill launch");
+    }
+    if (!workspace) return fail(PRIME_ERR_INVALID_ARG, "prime_delta_prefill: null workspace");
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0)
         return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d", B, H, H_kv, L);
-    if (chunk != prime::kDeltaChunk)
-        return fail(PRIME_ERR_INVALID_ARG, "chunk %d unsupported: the per-chunk clamp fixes chunk = 64", chunk);
     if (q->dtype != k->dtype || q->dtype != v->dtype || (q->dtype != PRIME_BF16 && q->dtype != PRIME_F32))
         return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "q/k/v must share dtype BF16 or F32");
     if (!valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported y dtype");
@@ -1108,8 +1153,9 @@ int prime_delta_prefill(const prime_tensor_t *q, const prime_tensor_t *k, const 
                      "delta prefill launch");
 }
 
-size_t prime_delta_prefill_backward_workspace_size(int B, int H, int L) {
-    if (B <= 0 || H <= 0 || L <= 0) return 0;
+size_t prime_delta_prefill_backward_workspace_size(int B, int H, int L, int D, int chunk) {
+    if (B <= 0 || H <= 0 || L <= 0 || D < 1 || D > prime::kDeltaGenMaxD || chunk <= 0) return 0;
+    if (delta_generic(D, chunk)) return prime::delta_gen_backward_ws_bytes(B, H, L, D, chunk);
     const size_t NC = (static_cast<size_t>(L) + prime::kDeltaChunk - 1) / prime::kDeltaChunk;
     return static_cast<size_t>(B) * H * NC * prime::kDeltaStateBytes;
 }
@@ -1124,11 +1170,26 @@ int prime_delta_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *
     if (!q || !k || !v || !dy || !q->data || !k->data || !v->data || !dy->data || !beta || !alpha || !dq || !dk ||
         !dv || !dbeta || !dalpha || !workspace)
         return fail(PRIME_ERR_INVALID_ARG, "prime_delta_prefill_backward: null argument");
-    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (delta_generic(D, chunk)) {
+        prime::DeltaGenArgs g{};
+        int rc;
+        if ((rc = delta_gen_args(g, q, k, v, beta, alpha, B, H, H_kv, L, D, chunk, decay_pad, feat_eps, bound,
+                                 state_in, nullptr)))
+            return rc;
+        if (!valid_dtype(dy->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dy dtype");
+        const size_t need = prime_delta_prefill_backward_workspace_size(B, H, L, D, chunk);
+        if (workspace_bytes < need || !aligned16(workspace))
+            return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes (16-byte aligned) is below the %zu needed",
+                        workspace_bytes, need);
+        g.dy = dy->data; g.dt_dy = dy->dtype; g.dy_sb = dy->stride_b; g.dy_sh = dy->stride_h; g.dy_sl = dy->stride_l;
+        g.dstate_out = dstate_out;
+        g.dq = dq; g.dk = dk; g.dv = dv; g.dbeta = dbeta; g.dalpha = dalpha; g.dstate_in = dstate_in;
+        g.ws = static_cast<float *>(workspace);
+        return check_hip(prime::launch_delta_gen_backward(g, static_cast<hipStream_t>(stream)),
+                         "delta backward launch");
+    }
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0)
         return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d L=%d", B, H, H_kv, L);
-    if (chunk != prime::kDeltaChunk)
-        return fail(PRIME_ERR_INVALID_ARG, "chunk %d unsupported: the per-chunk clamp fixes chunk = 64", chunk);
     if (q->dtype != k->dtype || q->dtype != v->dtype || (q->dtype != PRIME_BF16 && q->dtype != PRIME_F32))
         return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "q/k/v must share dtype BF16 or F32");
     if (dy->dtype != PRIME_BF16 && dy->dtype != PRIME_F32)
@@ -1136,9 +1197,9 @@ int prime_delta_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *
     if (!rows_aligned(q, true) || !rows_aligned(k, true) || !rows_aligned(v, true) || !rows_aligned(dy, true))
         return fail(PRIME_ERR_MISALIGNED, "q/k/v/dy rows must start on 16-byte boundaries");
     if (!aligned16(workspace)) return fail(PRIME_ERR_MISALIGNED, "workspace must be 16-byte aligned");
-    if (workspace_bytes < prime_delta_prefill_backward_workspace_size(B, H, L))
+    if (workspace_bytes < prime_delta_prefill_backward_workspace_size(B, H, L, D, chunk))
         return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes is below the %zu this shape needs", workspace_bytes,
-                    prime_delta_prefill_backward_workspace_size(B, H, L));
+                    prime_delta_prefill_backward_workspace_size(B, H, L, D, chunk));
     prime::DeltaBwdArgs a{};
     a.q = q->data; a.k = k->data; a.v = v->data; a.dy = dy->data;
     a.q_sb = q->stride_b; a.q_sh = q->stride_h; a.q_sl = q->stride_l;
@@ -1162,7 +1223,20 @@ int prime_delta_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, co
     g_err[0] = 0;
     if (!q || !k || !v || !y || !q->data || !k->data || !v->data || !y->data || !beta || !alpha || !state_out)
         return fail(PRIME_ERR_INVALID_ARG, "prime_delta_decode_step: null argument");
-    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (D != prime::kD) {
+        // head dims below 64: the token-sequential kernel in the step's form
+        prime::DeltaGenArgs g{};
+        int rc;
+        if ((rc = delta_gen_args(g, q, k, v, beta, alpha, B, H, H_kv, 1, D, 1, 1.0f, feat_eps, bound, state_in,
+                                 state_out)))
+            return rc;
+        if (!valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported y dtype");
+        g.step = 1;
+        g.q_sl = g.k_sl = g.v_sl = 0;
+        g.state_out = state_out;
+        g.y = y->data; g.dt_y = y->dtype; g.y_sb = y->stride_b; g.y_sh = y->stride_h; g.y_sl = 0;
+        return check_hip(prime::launch_delta_gen_forward(g, static_cast<hipStream_t>(stream)), "delta step launch");
+    }
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv)
         return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d H_kv=%d", B, H, H_kv);
     if (!valid_dtype(q->dtype) || !valid_dtype(k->dtype) || !valid_dtype(v->dtype) || !valid_dtype(y->dtype))

@@ -304,6 +304,32 @@ struct DeltaBwdArgs {
 };
 hipError_t launch_delta_backward(const DeltaBwdArgs &a, hipStream_t stream);
 
+// The delta rule at head dims up to 64 and any chunk size (delta_gen.hip):
+// one wavefront per (sequence, head), the recurrence token by token.
+struct DeltaGenArgs {
+    const void *q, *k, *v, *dy;
+    int64_t q_sb, q_sh, q_sl, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl, dy_sb, dy_sh, dy_sl;
+    int dt_q, dt_k, dt_v, dt_dy;
+    int B, H, group, L, D, chunk;
+    int step;                   // 1: the decode step's form (L == 1)
+    const float *beta, *alpha;  // [B, H, L]
+    float decay_pad, feat_eps, bound;
+    const float *state_in;      // [B, H, D, 2D] or null
+    float *state_out;           // [B, H, D, 2D] or null
+    void *y;
+    int dt_y;
+    int64_t y_sb, y_sh, y_sl;
+    const float *dstate_out;    // backward: [B, H, D, 2D] or null
+    float *dq, *dk, *dv;        // [B, H, L, D] fp32 contiguous
+    float *dbeta, *dalpha;      // [B, H, L]
+    float *dstate_in;           // [B, H, D, 2D] or null
+    float *ws;                  // backward workspace (delta_gen_backward_ws_bytes)
+};
+constexpr int kDeltaGenMaxD = 64;
+hipError_t launch_delta_gen_forward(const DeltaGenArgs &a, hipStream_t stream);
+hipError_t launch_delta_gen_backward(const DeltaGenArgs &a, hipStream_t stream);
+size_t delta_gen_backward_ws_bytes(int B, int H, int L, int D, int chunk);
+
 // One delta-rule decode step (delta.hip).
 struct DeltaStepArgs {
     const void *q, *k, *v;

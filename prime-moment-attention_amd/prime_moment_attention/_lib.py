@@ -167,7 +167,7 @@ def load() -> ctypes.CDLL:
     L.prime_timer_read.argtypes = [ctypes.c_int, P(ctypes.c_double), P(ctypes.c_int64)]
     L.prime_hbm_stream.argtypes = [fp, fp, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, fp]
     L.prime_hbm_stream.restype = ctypes.c_int
-    L.prime_delta_prefill_backward_workspace_size.argtypes = [ctypes.c_int] * 3
+    L.prime_delta_prefill_backward_workspace_size.argtypes = [ctypes.c_int] * 5
     L.prime_delta_prefill_backward_workspace_size.restype = ctypes.c_size_t
     L.prime_delta_prefill_backward.argtypes = [P(PrimeTensor)] * 3 + [fp, fp] + [ctypes.c_int] * 6 + [
         ctypes.c_float] * 3 + [fp, P(PrimeTensor)] + [fp] * 8 + [ctypes.c_size_t, fp]
@@ -788,12 +788,20 @@ def delta_workspace_size(B: int, H: int, L: int, dtype=None) -> int:
     return int(load().prime_delta_prefill_workspace_size(B, H, L, flags))
 
 
+def delta_generic(D: int, chunk: int) -> bool:
+    """True for the shapes the token-sequential delta kernels run (any head dim
+    up to 64 and chunk other than D = 64 with chunk 64)."""
+    return D != 64 or chunk != 64
+
+
 def delta_prefill(q, k, v, beta, alpha, decay_pad: float, feat_eps: float, bound: float, state_in, y,
-                  state_out, workspace: Optional[torch.Tensor] = None) -> None:
+                  state_out, workspace: Optional[torch.Tensor] = None, chunk: int = 64) -> None:
     """Chunked delta-rule prefill (prime_delta_prefill).  q [B,H,L,D], k/v
-    [B,Hkv,L,D] (bf16 or fp32 alike), beta/alpha fp32 [B,H,L], states fp32
-    [B,H,D,2D] or None, y [B,H,L,D].  workspace None allocates the recommended
-    size from torch's caching allocator."""
+    [B,Hkv,L,D] (bf16 or fp32 alike at D = 64, chunk 64; any supported dtypes
+    otherwise), beta/alpha fp32 [B,H,L], states fp32 [B,H,D,2D] or None, y
+    [B,H,L,D]; the Lyapunov clamp per `chunk` tokens.  workspace None
+    allocates the recommended size from torch's caching allocator (none is
+    needed outside D = 64 with chunk 64)."""
     _dev_check(q, k, v, y)
     B, H, Lq, D = q.shape
     Hkv = k.shape[1]
@@ -804,24 +812,25 @@ def delta_prefill(q, k, v, beta, alpha, decay_pad: float, feat_eps: float, bound
     _gate(alpha, B, H, Lq, "alpha")
     _check_delta_state(state_in, B, H, D, "state_in")
     _check_delta_state(state_out, B, H, D, "state_out")
-    if workspace is None:
+    if workspace is None and not delta_generic(D, chunk):
         workspace = torch.empty(delta_workspace_size(B, H, Lq, q.dtype), dtype=torch.uint8, device=q.device)
-    _dev_check(workspace)
+    if workspace is not None:
+        _dev_check(workspace)
     qd, kd, vd, yd = tensor_desc(q, True), tensor_desc(k, True), tensor_desc(v, True), tensor_desc(y, True)
     ptr = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
     rc = load().prime_delta_prefill(ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ptr(beta), ptr(alpha),
-                                    B, H, Hkv, Lq, D, 64, float(decay_pad), float(feat_eps), float(bound),
+                                    B, H, Hkv, Lq, D, int(chunk), float(decay_pad), float(feat_eps), float(bound),
                                     ptr(state_in), ctypes.byref(yd), ptr(state_out), ptr(workspace),
-                                    workspace.numel(), _stream(q.device))
+                                    workspace.numel() if workspace is not None else 0, _stream(q.device))
     _check(rc, "prime_delta_prefill")
 
 
-def delta_backward_workspace_size(B: int, H: int, L: int) -> int:
-    return int(load().prime_delta_prefill_backward_workspace_size(B, H, L))
+def delta_backward_workspace_size(B: int, H: int, L: int, D: int = 64, chunk: int = 64) -> int:
+    return int(load().prime_delta_prefill_backward_workspace_size(B, H, L, D, chunk))
 
 
 def delta_prefill_backward(q, k, v, beta, alpha, decay_pad: float, feat_eps: float, bound: float, state_in, dy,
-                           dstate_out, workspace: Optional[torch.Tensor] = None):
+                           dstate_out, workspace: Optional[torch.Tensor] = None, chunk: int = 64):
     """Gradients of the chunked delta-rule prefill (prime_delta_prefill_backward)
     for the forward's inputs: returns (dq [B,H,L,D], dk, dv [B,Hkv,L,D] summed
     over each group of query heads, dbeta, dalpha [B,H,L], dstate_in [B,H,D,2D]
@@ -845,11 +854,11 @@ def delta_prefill_backward(q, k, v, beta, alpha, decay_pad: float, feat_eps: flo
     dalpha = torch.empty(B, H, Lq, **f32)
     dstate = torch.empty(B, H, D, 2 * D, **f32) if state_in is not None else None
     if workspace is None:
-        workspace = torch.empty(delta_backward_workspace_size(B, H, Lq), dtype=torch.uint8, device=dev)
+        workspace = torch.empty(delta_backward_workspace_size(B, H, Lq, D, chunk), dtype=torch.uint8, device=dev)
     qd, kd, vd, yd = tensor_desc(q, True), tensor_desc(k, True), tensor_desc(v, True), tensor_desc(dy, True)
     ptr = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
     rc = load().prime_delta_prefill_backward(
-        ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ptr(beta), ptr(alpha), B, H, Hkv, Lq, D, 64,
+        ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ptr(beta), ptr(alpha), B, H, Hkv, Lq, D, int(chunk),
         float(decay_pad), float(feat_eps), float(bound), ptr(state_in), ctypes.byref(yd), ptr(dstate_out), ptr(dq),
         ptr(dk), ptr(dv), ptr(dbeta), ptr(dalpha), ptr(dstate), ptr(workspace),
         workspace.numel() * workspace.element_size(), _stream(dev))

@@ -12,9 +12,10 @@ in the HIP kernels through the C ABI:
 
 The per-token scalars the kernels take are the reference's: beta =
 0.5 mean(sigmoid(write)) and alpha = decay (1 - 0.5 mean(sigmoid(erase)))
-(:133-137).  The chunked branch clamps once per 64-token chunk, so its result
-depends on the chunk size; only ``chunk_size = 64`` (the reference default) is
-supported.
+(:133-137).  The chunked branch clamps once per chunk, so its result depends
+on ``chunk_size``: head_dim 64 with chunk_size 64 (the reference default)
+runs the MFMA chunk kernels, any other head_dim up to 64 or chunk size the
+token-sequential kernels.
 
 Training: with autograd recording, the chunked branch runs through
 prime_delta_prefill_backward (gradients in q, k, v, beta, alpha and the
@@ -37,19 +38,19 @@ class _DeltaPrefillFn(torch.autograd.Function):
     """The chunked delta-rule prefill with its HIP backward."""
 
     @staticmethod
-    def forward(ctx, q, k, v, beta, alpha, s_in, decay, feat_eps, bound, y_dtype):
+    def forward(ctx, q, k, v, beta, alpha, s_in, decay, feat_eps, bound, y_dtype, chunk):
         B, H, L, D = q.shape
         y = torch.empty(B, H, L, D, device=q.device, dtype=y_dtype)
         s_out = torch.empty(B, H, D, 2 * D, device=q.device, dtype=torch.float32)
-        _lib.delta_prefill(q, k, v, beta, alpha, decay, feat_eps, bound, s_in, y, s_out)
+        _lib.delta_prefill(q, k, v, beta, alpha, decay, feat_eps, bound, s_in, y, s_out, chunk=chunk)
         ctx.save_for_backward(q, k, v, beta, alpha, s_in)
-        ctx.consts = (decay, feat_eps, bound)
+        ctx.consts = (decay, feat_eps, bound, chunk)
         return y, s_out
 
     @staticmethod
     def backward(ctx, dy, ds_out):
         q, k, v, beta, alpha, s_in = ctx.saved_tensors
-        decay, feat_eps, bound = ctx.consts
+        decay, feat_eps, bound, chunk = ctx.consts
         if dy is None:
             dy = torch.zeros(q.shape, device=q.device, dtype=torch.float32)
         dy = dy.contiguous()
@@ -57,8 +58,8 @@ class _DeltaPrefillFn(torch.autograd.Function):
             dy = dy.float()
         ds = ds_out.contiguous().float() if ds_out is not None else None
         dq, dk, dv, dbeta, dalpha, dstate = _lib.delta_prefill_backward(q, k, v, beta, alpha, decay, feat_eps,
-                                                                          bound, s_in, dy, ds)
-        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dbeta, dalpha, dstate, None, None, None, None)
+                                                                          bound, s_in, dy, ds, chunk=chunk)
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dbeta, dalpha, dstate, None, None, None, None, None)
 
 
 class ChunkedGatedDeltaPrimeAttention(nn.Module):
@@ -66,8 +67,10 @@ class ChunkedGatedDeltaPrimeAttention(nn.Module):
                  chunk_size: int = 64, decay: float = 0.9995, use_qk_norm: bool = True,
                  lyapunov_bound: float = 25.0, eps: float = 1e-5):
         super().__init__()
-        if chunk_size != 64:
-            raise ValueError("chunk_size must be 64 (the Lyapunov clamp is applied per 64-token chunk)")
+        if chunk_size < 1:
+            raise ValueError("chunk_size must be positive")
+        if head_dim > 64:
+            raise ValueError("head_dim above 64 is not supported")
         self.hidden_size = hidden_size
         self.num_heads = num_heads
         self.head_dim = head_dim
@@ -144,7 +147,8 @@ class ChunkedGatedDeltaPrimeAttention(nn.Module):
             q, k, v = (t if (t.stride(-1) == 1 and all((s * t.element_size()) % 16 == 0 for s in t.stride()[:-1]))
                        else t.contiguous() for t in (q, k, v))
             y = torch.empty(B, H, L, D, device=dev, dtype=y_dtype)
-            _lib.delta_prefill(q, k, v, beta, alpha, self.decay, self.eps, self.lyapunov_bound, s_in, y, s_out)
+            _lib.delta_prefill(q, k, v, beta, alpha, self.decay, self.eps, self.lyapunov_bound, s_in, y, s_out,
+                               chunk=self.chunk_size)
         y = no_backward("the delta-rule PRIME decode step", y, q, k, v, beta, alpha, s_in)
         y = y.to(dtype).transpose(1, 2).reshape(B, L, H * D)
         return self.o_proj(y), (s_out if return_state else None)
@@ -172,6 +176,6 @@ class ChunkedGatedDeltaPrimeAttention(nn.Module):
         if state is not None:
             s_in = state.to(device=dev, dtype=torch.float32).reshape(B, H, D, 2 * D).contiguous()
         y, s_out = _DeltaPrefillFn.apply(q, k, v, beta, alpha, s_in, self.decay, self.eps, self.lyapunov_bound,
-                                         y_dtype)
+                                         y_dtype, self.chunk_size)
         y = y.to(dtype).transpose(1, 2).reshape(B, L, H * D)
         return self.o_proj(y), (s_out if return_state else None)

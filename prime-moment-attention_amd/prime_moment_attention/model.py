@@ -360,13 +360,14 @@ class _LayerStep:
             self.sel = None
         # the folded form (base attention, GELU MLP, bf16): each RMSNorm's weight
         # multiplied into the columns of the projection after it, so that the
-        # projection kernel applies the norm as a per-row scale (prime_linear_fused)
-        # (the kernels take "apply the norm" as its own flag; a norm eps of 0
-        # is a valid configuration and still normalises)
+        # projection kernel applies the norm as a per-row scale (prime_linear_fused,
+        # which applies it for rms_eps > 0 only: a norm eps of 0 keeps the unfolded
+        # form; the fragment-layout step below takes "apply the norm" as a flag)
         self.qkv_g = self.up_g = None
         if (self.sel is None and isinstance(layer.mlp, PrimeGeluMLP) and dtype == torch.bfloat16
                 and self.qkv.shape[1] % 128 == 0 and self.qkv.shape[0] % 32 == 0
-                and layer.mlp.up_proj.weight.shape[0] % 128 == 0):
+                and layer.mlp.up_proj.weight.shape[0] % 128 == 0
+                and layer.input_layernorm.eps > 0 and layer.post_attention_layernorm.eps > 0):
             g1 = layer.input_layernorm.weight.to(torch.float32)
             g2 = layer.post_attention_layernorm.weight.to(torch.float32)
             self.qkv_g = (self.qkv.to(torch.float32) * g1).to(dtype)
