@@ -651,12 +651,15 @@ def bench_backward(args, lib, torch, dev):
     config-2 shape (B=8 x H=12 x L=8192) and at a training shape (B=32 x
     H=12 x L=2048).  Algorithmic bytes per token-head: q, k, v, dy read by both
     passes (2 x 512 B), dq, dk, dv written (3 x 256 B fp32), 16 B of per-token
-    denominators; flop per token-head: 196,608 (MFMA blocks of both passes)."""
+    denominators; flop per token-head: 196,608 (MFMA blocks of both passes).
+    The config-2 shape once more with fp32 q/k/v/dy (the fp32 passes; bytes
+    counted as for bf16, so its fraction is a lower bound)."""
     out = {}
-    for (B, H, L) in ((8, 12, 8192), (32, 12, 2048)):
+    for (B, H, L, dt) in ((8, 12, 8192, torch.bfloat16), (32, 12, 2048, torch.bfloat16),
+                          (8, 12, 8192, torch.float32)):
         gen = torch.Generator(device=dev).manual_seed(args.seed + 17 + B)
-        q, k, v = qkv((B, H, L, D), gen, dev, torch.bfloat16)
-        dy = torch.randn(B, H, L, D, device=dev, generator=gen).to(torch.bfloat16)
+        q, k, v = qkv((B, H, L, D), gen, dev, dt)
+        dy = torch.randn(B, H, L, D, device=dev, generator=gen).to(dt)
         lam = torch.empty(H, device=dev).uniform_(0.99, 0.9999, generator=gen)
         g = [torch.empty(B, H, L, D, device=dev) for _ in range(3)]
         ws = torch.empty(lib.backward_workspace_size(B, H, L), dtype=torch.uint8, device=dev)
@@ -678,7 +681,7 @@ def bench_backward(args, lib, torch, dev):
         flops = th * BWD_FLOP_PER_TOKEN_HEAD
         kern = {n: v for n, v in kern.items() if v[1]}  # the segment kernels run only for few long sequences
         kt = sum(t for t, _ in kern.values())
-        out[f"B{B}_H{H}_L{L}"] = {
+        out[f"B{B}_H{H}_L{L}" + ("_f32" if dt == torch.float32 else "")] = {
             "tok_s": B * L / (ms * 1e-3), "ms": ms,
             "finite": all(bool(torch.isfinite(t).all().item()) for t in g),
             "kernels": {n: {"avg_us": None if t is None else t * 1e3, "launches": c} for n, (t, c) in kern.items()},

@@ -759,11 +759,19 @@ size_t bwd_token_bytes(int B, int H, int L) {
 size_t bwd_corr_bytes(int B, int H) { return static_cast<size_t>(B) * H * prime::kBwdCorr * sizeof(float); }
 }  // namespace
 
+namespace {
+// segment slots of the backward's plan for bf16 (per_cu 2) or fp32 (1) inputs
+size_t bwd_slot_bytes(int B, int H, int L, int per_cu, int *G, int *cps) {
+    prime::plan_backward_segments(B * H, L, G, cps, per_cu);
+    return *G > 1 ? static_cast<size_t>(B) * H * *G * prime::kWsStride * sizeof(float) : 0;
+}
+}  // namespace
+
 size_t prime_chunked_prefill_backward_workspace_size(int B, int H, int L) {
     if (B <= 0 || H <= 0 || L <= 0) return 0;
     int G, cps;
-    prime::plan_backward_segments(B * H, L, &G, &cps);
-    const size_t slots = G > 1 ? static_cast<size_t>(B) * H * G * prime::kWsStride * sizeof(float) : 0;
+    // enough for either plan (the inputs' dtype is not an argument)
+    const size_t slots = std::max(bwd_slot_bytes(B, H, L, 2, &G, &cps), bwd_slot_bytes(B, H, L, 1, &G, &cps));
     return bwd_token_bytes(B, H, L) + std::max(slots, bwd_corr_bytes(B, H));
 }
 
@@ -861,11 +869,11 @@ int prime_chunked_prefill_backward(const prime_tensor_t *q, const prime_tensor_t
     }
     a.inv_den = static_cast<float *>(workspace);
     a.g_den = a.inv_den + static_cast<size_t>(B) * H * L;
-    prime::plan_backward_segments(B * H, L, &a.G, &a.cps);
-    if (q->dtype == PRIME_F32 || dense_in ||
-        (a.G > 1 && workspace_bytes < prime_chunked_prefill_backward_workspace_size(B, H, L))) {
-        // (fp32 inputs: the fp32 passes run one workgroup per sequence; the dense
-        // double clamp carries the call's K apart from the incoming one from token 0)
+    // (fp32 inputs: the fp32 passes run one workgroup per CU)
+    const size_t slots = bwd_slot_bytes(B, H, L, q->dtype == PRIME_F32 ? 1 : 2, &a.G, &a.cps);
+    if (dense_in || (a.G > 1 && workspace_bytes < need + slots)) {
+        // (the dense double clamp carries the call's K apart from the incoming
+        // one from token 0)
         a.G = 1;  // one segment per sequence in the workspace given
         a.cps = (L + 63) / 64;
     }

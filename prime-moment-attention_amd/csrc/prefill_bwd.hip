@@ -992,11 +992,36 @@ __global__ __launch_bounds__(256) void bwd_dual_scan_kernel(const BwdArgs a) {
     if (a.ds1i) dst[off] = carry / fac;
 }
 
-void plan_backward_segments(int S, int L, int *G, int *cps) {
+hipError_t launch_bwd_dual_scan(const BwdArgs &a, hipStream_t stream) {
+    const int64_t n = static_cast<int64_t>(a.B) * a.H * kWsElems;
+    const TimerEvents ts = timer_events(PRIME_KERNEL_BWD_DUAL_SCAN);
+    hipExtLaunchKernelGGL(bwd_dual_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                          ts.start, ts.stop, 0, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) timer_drop(ts);
+    return e;
+}
+
+void plan_backward_segments(int S, int L, int *G, int *cps, int per_cu) {
     const int NC = (L + kC - 1) / kC;
     int g = 1;
     const int cu = device_cus();
-    if (S > 0 && S < 2 * cu) g = min(min(2 * cu / S, NC / 8), 64);
+    if (S > 0 && S < per_cu * cu) g = min(min(per_cu * cu / S, NC / 8), 64);
+    if (per_cu == 1 && S > 0 && S < cu) {
+        // one workgroup per CU: the passes take (rounds of units over the CUs) x
+        // (chunks per segment) chunk periods; take the fewest, then the fewest
+        // segments (G = 2 leaves a quarter of the CUs idle at 96 sequences,
+        // G = 8 fills three rounds exactly)
+        long best = static_cast<long>(NC);
+        g = 1;
+        for (int t = 2; t <= min(NC / 8, 64); ++t) {
+            const long c = (NC + t - 1) / t, rounds = (static_cast<long>(S) * t + cu - 1) / cu;
+            if (rounds * c < best) {
+                best = rounds * c;
+                g = t;
+            }
+        }
+    }
     if (g < 2) {
         *G = 1;
         *cps = NC;
@@ -1008,7 +1033,6 @@ void plan_backward_segments(int S, int L, int *G, int *cps) {
 }
 
 hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream) {
-    if (a.dt_in == PRIME_F32) return launch_prefill_backward_f32(a, stream);
     const int S = a.B * a.H;
     hipError_t e;
     if (a.G > 1) {
@@ -1024,6 +1048,7 @@ hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream) {
         f.G = a.G; f.cps = a.cps; f.ws = a.ws; f.states_only = 1;
         if ((e = launch_prefill(f, stream)) != hipSuccess) return e;
     }
+    if (a.dt_in == PRIME_F32) return launch_prefill_backward_f32(a, stream);
     const int units = S * a.G;
     const TimerEvents t1 = timer_events(PRIME_KERNEL_BWD_DQ);
     if (a.dense_in)
@@ -1038,11 +1063,7 @@ hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream) {
         hipExtLaunchKernelGGL(prefill_bwd_dkv_kernel<true>, dim3(units), dim3(256), 0, stream, td.start, td.stop, 0,
                               a);
         if ((e = hipGetLastError()) != hipSuccess) return timer_drop(td), e;
-        const int64_t n = static_cast<int64_t>(S) * kWsElems;
-        const TimerEvents ts = timer_events(PRIME_KERNEL_BWD_DUAL_SCAN);
-        hipExtLaunchKernelGGL(bwd_dual_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0,
-                              stream, ts.start, ts.stop, 0, a);
-        if ((e = hipGetLastError()) != hipSuccess) return timer_drop(ts), e;
+        if ((e = launch_bwd_dual_scan(a, stream)) != hipSuccess) return e;
     }
     const TimerEvents t2 = timer_events(PRIME_KERNEL_BWD_DKV);
     hipExtLaunchKernelGGL(prefill_bwd_dkv_kernel<false>, dim3(units), dim3(256), 0, stream, t2.start, t2.stop, 0,

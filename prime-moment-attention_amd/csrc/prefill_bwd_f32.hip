@@ -187,11 +187,24 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
-    const int seq = blockIdx.x;
-    if (seq >= a.B * a.H) return;
+    // one unit per (sequence, segment of a.cps chunks); G > 1 only for the base
+    // form without the dense clamp's incoming-state split
+    const int unit = blockIdx.x;
+    if (unit >= a.B * a.H * a.G) return;
+    const int seq = unit / a.G, seg = unit - seq * a.G;
     const int b = seq / a.H, h = seq - b * a.H;
     const float logl = logf(a.decay[h]);
     const size_t so1 = static_cast<size_t>(seq) * kD * kD, so0 = static_cast<size_t>(seq) * kD;
+    // the state entering the segment: state_in, or the segment's slot (the
+    // forward's state-only pass; the same components and conventions)
+    const float *S0p = a.s0i ? a.s0i + so0 : nullptr, *S1p = a.s1i ? a.s1i + so1 : nullptr;
+    const float *S2p = a.s2i ? a.s2i + so1 : nullptr, *K0p = a.k0i ? a.k0i + seq : nullptr;
+    const float *K1p = a.k1i ? a.k1i + so0 : nullptr, *K2p = a.k2i ? a.k2i + so0 : nullptr;
+    if (a.G > 1) {
+        const float *slot = a.ws + static_cast<size_t>(unit) * kWsStride;
+        S1p = slot + kWsS1; S2p = slot + kWsS2; S0p = slot + kWsS0;
+        K1p = slot + kWsK1; K2p = slot + kWsK2; K0p = slot + kWsK0;
+    }
 
     // incoming state: M = [S1; S2/2], Kf = [K1; K2/2]
     f32x4 mt[4];
@@ -202,16 +215,16 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
             const int f = 16 * w + 4 * g + r, col = 16 * dv + c16;
             float x = 0.f;
             // rows 64.. of M: S2/2 (S2 in the selective convention, whose S2 carries the 1/2)
-            if (a.s1i) x = f < kD ? a.s1i[so1 + f * kD + col] : (SEL ? 1.0f : 0.5f) * a.s2i[so1 + (f - kD) * kD + col];
+            if (S1p) x = f < kD ? S1p[f * kD + col] : (SEL ? 1.0f : 0.5f) * S2p[(f - kD) * kD + col];
             mt[dv][r] = x;
             sM[f][col] = x;
         }
     float kreg = 0.f;
-    if (a.s1i) {
-        if (tid < kD) kreg = a.k1i[so0 + tid];
-        else if (tid < kFP) kreg = (SEL ? 1.0f : 0.5f) * a.k2i[so0 + tid - kD];
-        else if (tid < kFP + kD) kreg = a.s0i[so0 + tid - kFP];
-        else if (tid == kFP + kD) kreg = a.k0i[seq];
+    if (S1p) {
+        if (tid < kD) kreg = K1p[tid];
+        else if (tid < kFP) kreg = (SEL ? 1.0f : 0.5f) * K2p[tid - kD];
+        else if (tid < kFP + kD) kreg = S0p[tid - kFP];
+        else if (tid == kFP + kD) kreg = K0p[0];
     }
     constexpr bool din = DIN;
     const bool kthr = tid < kFP || tid == kFP + kD;  // threads that carry Kf or K0
@@ -226,8 +239,9 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
     float corr = 0.f;  // (din) this thread's feature (tid < 128) or K0 (tid == 192) of the correction
 
     const int NC = (a.L + kC - 1) / kC;
+    const int c_begin = seg * a.cps, c_end = min(c_begin + a.cps, NC);
     const int64_t gbase = b * a.g_sb + h * a.g_sh;
-    for (int c = 0; c < NC; ++c) {
+    for (int c = c_begin; c < c_end; ++c) {
         // (din) l^(64 c): the incoming state's decay to the chunk's start
         const float lc = din ? static_cast<float>(pow(static_cast<double>(a.decay[h]), 64.0 * c)) : 0.f;
         load_chunk<SEL>(a, b, h, c, tid, w, lane, sFq, sFk, sV, sG, sCum, sEc, sW, logl);
@@ -443,7 +457,10 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dq_f32_kernel(cons
 // the dq pass's query-side terms into the log decays' adjoint (a suffix sum
 // over the tokens, carried from the last chunk back) and the key scale's
 // adjoint per sequence
-template <bool SEL>
+// DUAL: the dual-state pass of a segment (G > 1) -- from a zero adjoint, no dk /
+// dv, the adjoint reached at the segment's start (its contribution) written to
+// its slot for the reverse scan over segments.
+template <bool SEL, bool DUAL>
 __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(const BwdArgs a) {
     __shared__ __attribute__((aligned(16))) float sFq[kC][kPQ];
     __shared__ __attribute__((aligned(16))) float sFk[kC][kPQ];
@@ -457,13 +474,18 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
-    const int seq = blockIdx.x;
-    if (seq >= a.B * a.H) return;
+    const int unit = blockIdx.x;
+    if (unit >= a.B * a.H * a.G) return;
+    const int seq = unit / a.G, seg = unit - seq * a.G;
     const int b = seq / a.H, h = seq - b * a.H;
     const float logl = logf(a.decay[h]);
     const size_t so1 = static_cast<size_t>(seq) * kD * kD, so0 = static_cast<size_t>(seq) * kD;
+    float *slot = a.G > 1 ? a.ws + static_cast<size_t>(unit) * kWsStride : nullptr;
 
-    // adjoint of the final state: dM = [dS1; 2 dS2], dKf = [dK1; 2 dK2]
+    // adjoint of the state leaving the last chunk: dM = [dS1; 2 dS2], dKf = [dK1;
+    // 2 dK2] of the final state; with segments the dual state at the segment's
+    // end, which the reverse scan left in its slot in this convention; zero for
+    // the dual pass
     f32x4 mt[4];
 #pragma unroll
     for (int dv = 0; dv < 4; ++dv)
@@ -471,16 +493,27 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
         for (int r = 0; r < 4; ++r) {
             const int f = 16 * w + 4 * g + r, col = 16 * dv + c16;
             float x = 0.f;
-            if (f < kD) x = a.ds1o ? a.ds1o[so1 + f * kD + col] : 0.f;
+            if (DUAL) x = 0.f;
+            else if (slot) x = f < kD ? slot[kWsS1 + f * kD + col] : slot[kWsS2 + (f - kD) * kD + col];
+            else if (f < kD) x = a.ds1o ? a.ds1o[so1 + f * kD + col] : 0.f;
             else x = a.ds2o ? (SEL ? 1.0f : 2.0f) * a.ds2o[so1 + (f - kD) * kD + col] : 0.f;
             mt[dv][r] = x;
             sM[f][col] = x;
         }
     float kreg = 0.f;
-    if (tid < kD) kreg = a.dk1o ? a.dk1o[so0 + tid] : 0.f;
-    else if (tid < kFP) kreg = a.dk2o ? (SEL ? 1.0f : 2.0f) * a.dk2o[so0 + tid - kD] : 0.f;
-    else if (tid < kFP + kD) kreg = a.ds0o ? a.ds0o[so0 + tid - kFP] : 0.f;
-    else if (tid == kFP + kD) kreg = a.dk0o ? a.dk0o[seq] : 0.f;
+    if (DUAL) {
+        kreg = 0.f;
+    } else if (slot) {
+        if (tid < kD) kreg = slot[kWsK1 + tid];
+        else if (tid < kFP) kreg = slot[kWsK2 + tid - kD];
+        else if (tid < kFP + kD) kreg = slot[kWsS0 + tid - kFP];
+        else if (tid == kFP + kD) kreg = slot[kWsK0];
+    } else {
+        if (tid < kD) kreg = a.dk1o ? a.dk1o[so0 + tid] : 0.f;
+        else if (tid < kFP) kreg = a.dk2o ? (SEL ? 1.0f : 2.0f) * a.dk2o[so0 + tid - kD] : 0.f;
+        else if (tid < kFP + kD) kreg = a.ds0o ? a.ds0o[so0 + tid - kFP] : 0.f;
+        else if (tid == kFP + kD) kreg = a.dk0o ? a.dk0o[seq] : 0.f;
+    }
     if (tid < kFP) sKf[tid] = kreg;
     else if (tid < kFP + kD) sS0[tid - kFP] = kreg;
     else if (tid == kFP + kD) sK0[0] = kreg;
@@ -491,10 +524,11 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
     // chunk back (every lane of wave 0 holds it), starting with the final
     // state's share; and this thread's part of the key scale's adjoint
     float dl_carry = SEL ? a.fin[seq] : 0.f, dks = 0.f;
-    for (int c = NC - 1; c >= 0; --c) {
+    const int c_begin = seg * a.cps, c_end = min(c_begin + a.cps, NC);
+    for (int c = c_end - 1; c >= c_begin; --c) {
         load_chunk<SEL>(a, b, h, c, tid, w, lane, sFq, sFk, sV, sG, sCum, sEc, sW, logl);
         __syncthreads();
-        scores(a, c, w, g, c16, sFq, sFk, sCum, sA);
+        if (!DUAL) scores(a, c, w, g, c16, sFq, sFk, sCum, sA);
         if (tid < kC) {
             const int64_t t = static_cast<int64_t>(c) * kC + tid;
             sH[tid] = t < a.L ? a.g_den[static_cast<size_t>(seq) * a.L + t] : 0.f;
@@ -507,6 +541,7 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
         __syncthreads();
         const int jb = w >> 1;  // this wave's token block (as the column j of a and da)
         const int64_t t0 = static_cast<int64_t>(c) * kC;
+        if constexpr (!DUAL) {
         // ---- dv^T tiles (value blocks 2(w&1)+jj, tokens of block jb):
         //      sum_i a_ij g_i + w_j (Fk_j dM + dS0)
         {
@@ -595,6 +630,7 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
                 }
             }
         }
+        }  // !DUAL
         // ---- adjoint to the chunk's start: dM = e^cum_63 dM + Fq^T diag(e^cum) G, and the vectors
         {
             const float e63 = sEc[kC - 1];
@@ -661,8 +697,25 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
         }
     }
 
+    if constexpr (DUAL) {
+        // the segment's contribution to the dual state at its start, this kernel's convention
+#pragma unroll
+        for (int dv = 0; dv < 4; ++dv)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int f = 16 * w + 4 * g + r, col = 16 * dv + c16;
+                if (f < kD) slot[kWsS1 + f * kD + col] = mt[dv][r];
+                else slot[kWsS2 + (f - kD) * kD + col] = mt[dv][r];
+            }
+        if (tid < kD) slot[kWsK1 + tid] = kreg;
+        else if (tid < kFP) slot[kWsK2 + tid - kD] = kreg;
+        else if (tid < kFP + kD) slot[kWsS0 + tid - kFP] = kreg;
+        else if (tid == kFP + kD) slot[kWsK0] = kreg;
+        return;
+    }
     // ---- adjoint of the incoming state: dS1 = dM[:64], dS2 = dM[64:] / 2, dK1, dK2 = dKf[64:] / 2
-    if (a.ds1i) {
+    // (with segments the reverse scan over them writes it)
+    if (a.ds1i && a.G == 1) {
 #pragma unroll
         for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
@@ -681,9 +734,10 @@ __global__ __launch_bounds__(kBW * kWave, 1) void prefill_bwd_dkv_f32_kernel(con
 }
 
 hipError_t launch_prefill_backward_f32(const BwdArgs &a, hipStream_t stream) {
-    const dim3 grid(a.B * a.H), block(kBW * kWave);
+    // (with segments the forward's state-only pass has filled the slots)
+    const dim3 grid(a.B * a.H * a.G), block(kBW * kWave);
     const TimerEvents t1 = timer_events(PRIME_KERNEL_BWD_DQ);
-    const bool sel = a.logd != nullptr;  // (the selective form has no dense clamp)
+    const bool sel = a.logd != nullptr;  // (the selective form has no dense clamp and one segment)
     if (sel)
         hipExtLaunchKernelGGL((prefill_bwd_dq_f32_kernel<false, true>), grid, block, 0, stream, t1.start, t1.stop, 0, a);
     else if (a.dense_in)
@@ -692,11 +746,21 @@ hipError_t launch_prefill_backward_f32(const BwdArgs &a, hipStream_t stream) {
         hipExtLaunchKernelGGL((prefill_bwd_dq_f32_kernel<false, false>), grid, block, 0, stream, t1.start, t1.stop, 0, a);
     hipError_t e;
     if ((e = hipGetLastError()) != hipSuccess) return timer_drop(t1), e;
+    if (a.G > 1 && !sel) {
+        // each segment's dual contribution, then the reverse scan (slots now hold dual states)
+        const TimerEvents td = timer_events(PRIME_KERNEL_BWD_DUAL);
+        hipExtLaunchKernelGGL((prefill_bwd_dkv_f32_kernel<false, true>), grid, block, 0, stream, td.start, td.stop, 0,
+                              a);
+        if ((e = hipGetLastError()) != hipSuccess) return timer_drop(td), e;
+        if ((e = launch_bwd_dual_scan(a, stream)) != hipSuccess) return e;
+    }
     const TimerEvents t2 = timer_events(PRIME_KERNEL_BWD_DKV);
     if (sel)
-        hipExtLaunchKernelGGL(prefill_bwd_dkv_f32_kernel<true>, grid, block, 0, stream, t2.start, t2.stop, 0, a);
+        hipExtLaunchKernelGGL((prefill_bwd_dkv_f32_kernel<true, false>), grid, block, 0, stream, t2.start, t2.stop, 0,
+                              a);
     else
-        hipExtLaunchKernelGGL(prefill_bwd_dkv_f32_kernel<false>, grid, block, 0, stream, t2.start, t2.stop, 0, a);
+        hipExtLaunchKernelGGL((prefill_bwd_dkv_f32_kernel<false, false>), grid, block, 0, stream, t2.start, t2.stop,
+                              0, a);
     if ((e = hipGetLastError()) != hipSuccess) timer_drop(t2);
     return e;
 }

@@ -214,8 +214,11 @@ hipError_t launch_prefill_backward(const BwdArgs &a, hipStream_t stream);
 // fp32 inputs: the fp32 dq and dk/dv passes, one workgroup per sequence (prefill_bwd_f32.hip)
 hipError_t launch_prefill_backward_f32(const BwdArgs &a, hipStream_t stream);
 // segments per sequence for the backward: enough (sequence, segment) units to
-// fill two workgroups per CU, at least 8 chunks per segment
-void plan_backward_segments(int S, int L, int *G, int *cps);
+// fill per_cu workgroups per CU (2 for the bf16 passes, 1 for the fp32 ones),
+// at least 8 chunks per segment
+void plan_backward_segments(int S, int L, int *G, int *cps, int per_cu = 2);
+// the reverse scan over segments of the backward's dual states (prefill_bwd.hip)
+hipError_t launch_bwd_dual_scan(const BwdArgs &a, hipStream_t stream);
 int device_cus();  // compute units of the current device (cached)
 
 hipError_t launch_decode_step(const DecodeArgs &a, hipStream_t stream);
