@@ -504,7 +504,17 @@ def bench_selective(args, lib, torch, dev):
                                     "bytes_per_launch": algo, "avg_launch_us": main_ms * 1e3,
                                     "achieved": algo / (main_ms * 1e-3) / 1e9, "peak": PEAK_HBM / 1e9,
                                     "unit": "GB/s", "frac": algo / (main_ms * 1e-3) / PEAK_HBM}}}
-    del q, k, v, y, delta, log_decay, ws
+    # the same with fp32 q/k/v and y (the fp32 kernel; segments for few long sequences)
+    q32, k32, v32 = (t.float() for t in (q, k, v))
+    y32 = torch.empty(B, H, L, D, device=dev, dtype=torch.float32)
+    run32 = lambda: lib.selective_prefill(q32, k32, v32, log_decay, beta, 1.0, None, y32, st, workspace=ws)
+    for _ in range(3):
+        run32()
+    torch.cuda.synchronize()
+    ms32 = timed(run32, max(10, args.kernel_steps // 20), 0)
+    out["prefill_f32"] = {"tok_s": B * L / (ms32 * 1e-3), "ms": ms32,
+                          "finite": bool(torch.isfinite(y32).all().item())}
+    del q, k, v, y, delta, log_decay, ws, q32, k32, v32, y32
     # decode B=256 x 12 layers
     Bd, layers = 256, 12
     states = []
@@ -1106,6 +1116,7 @@ def compact(rec):
     if "selective" in rec:
         se = rec["selective"]
         out["selective"] = {"prefill_tok_s": se["prefill"]["tok_s"], "prefill_ms": se["prefill"]["ms"],
+                            "prefill_f32_ms": se["prefill_f32"]["ms"],
                             "prefill_hbm_frac": se["prefill"]["roofline"]["frac"],
                             "decode_B256_tok_s": se["decode_B256"]["tok_s"],
                             "decode_hbm_frac": se["decode_B256"]["roofline"]["frac"]}

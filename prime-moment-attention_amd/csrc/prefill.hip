@@ -780,6 +780,16 @@ __global__ __launch_bounds__(256) void segment_scan_kernel(const PrefillArgs a) 
     else a.k0o[seq] = carry;
 }
 
+hipError_t launch_segment_scan(const PrefillArgs &a, hipStream_t stream) {
+    const int64_t n = static_cast<int64_t>(a.B) * a.H * kWsElems;
+    const TimerEvents tb = timer_events(PRIME_KERNEL_SEGMENT_SCAN);
+    hipExtLaunchKernelGGL(segment_scan_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream,
+                          tb.start, tb.stop, 0, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) timer_drop(tb);
+    return e;
+}
+
 template <bool F32IN>
 static hipError_t launch_variant(PrefillArgs a, hipStream_t stream) {
     const int Sq = a.B * a.H;

@@ -223,6 +223,9 @@ int device_cus();  // compute units of the current device (cached)
 
 hipError_t launch_decode_step(const DecodeArgs &a, hipStream_t stream);
 hipError_t launch_prefill(PrefillArgs a, hipStream_t stream);
+// the scan over a prefill's segments: slot s <- the state entering segment s
+// (prefill.hip)
+hipError_t launch_segment_scan(const PrefillArgs &a, hipStream_t stream);
 // selective form with fp32 inputs: one fp32 kernel over each sequence's chunks (selective_f32.hip)
 hipError_t launch_selective_f32(const PrefillArgs &a, hipStream_t stream);
 // segments per sequence for the launch plan, given the workspace the caller has

@@ -20,6 +20,11 @@
 //   y^T tiles (value block x token block: V^T A^T + M^T (e^cum Fq)^T) and the
 //   state update (wave w owns M's feature rows 16w..16w+15 in accumulators) |
 //   publish the state to LDS for the next chunk's readout.
+// Few long sequences run in segments of a.cps chunks, as the bf16 path does:
+// a state-only pass (STATE_ONLY: no readout) forms every segment's state from
+// zero and its total log decay, the scan over segments turns them into the
+// state entering each segment, and the main pass runs one workgroup per
+// (sequence, segment) from that state.
 
 #include "prefill_common.h"
 
@@ -53,6 +58,7 @@ __device__ __forceinline__ void store_y4(void *y, int dt, int64_t idx, f32x4 v) 
 
 }  // namespace
 
+template <bool STATE_ONLY>
 __global__ __launch_bounds__(kSelWaves * kWave, 1) void selective_prefill_f32_kernel(const PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) float sFq[kC][kPQ];
     __shared__ __attribute__((aligned(16))) float sFk[kC][kPQ];
@@ -64,8 +70,12 @@ __global__ __launch_bounds__(kSelWaves * kWave, 1) void selective_prefill_f32_ke
     const int tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, c16 = lane & 15;
-    const int seq = blockIdx.x;
-    if (seq >= a.B * a.H) return;
+    // units: (sequence, segment); the state-only pass takes segments 0 .. G-2
+    const int nseg = STATE_ONLY ? a.G - 1 : a.G;
+    const int unit = blockIdx.x;
+    if (unit >= a.B * a.H * nseg) return;
+    const int seq = unit / nseg, seg = unit - seq * nseg;
+    float *slot = a.G > 1 ? a.ws + (static_cast<size_t>(seq) * a.G + seg) * kWsStride : nullptr;
     const int b = seq / a.H, h = seq - b * a.H, hk = h / a.group;
     const float beta = a.k_scale[h], hb2 = 0.5f * beta * beta;
     const float *ldp = a.log_decay + static_cast<size_t>(seq) * a.L;
@@ -83,12 +93,21 @@ __global__ __launch_bounds__(kSelWaves * kWave, 1) void selective_prefill_f32_ke
         for (int r = 0; r < 4; ++r) {
             const int f = 16 * w + 4 * g + r, col = 16 * dv + c16;
             float x = 0.f;
-            if (a.s1i) x = f < kD ? a.s1i[so1 + f * kD + col] : a.s2i[so1 + (f - kD) * kD + col];
+            if (STATE_ONLY) x = 0.f;
+            else if (slot) x = f < kD ? slot[kWsS1 + f * kD + col] : slot[kWsS2 + (f - kD) * kD + col];
+            else if (a.s1i) x = f < kD ? a.s1i[so1 + f * kD + col] : a.s2i[so1 + (f - kD) * kD + col];
             mt[dv][r] = x;
             sM[f][col] = x;
         }
     float kreg = 0.f;
-    if (a.s1i) {
+    if (STATE_ONLY) {
+        kreg = 0.f;
+    } else if (slot) {
+        if (tid < kD) kreg = slot[kWsK1 + tid];
+        else if (tid < kFP) kreg = slot[kWsK2 + tid - kD];
+        else if (tid < kFP + kD) kreg = slot[kWsS0 + tid - kFP];
+        else if (tid == kFP + kD) kreg = slot[kWsK0];
+    } else if (a.s1i) {
         if (tid < kD) kreg = a.k1i[so0 + tid];
         else if (tid < kFP) kreg = a.k2i[so0 + tid - kD];
         else if (tid < kFP + kD) kreg = a.s0i[so0 + tid - kFP];
@@ -99,8 +118,10 @@ __global__ __launch_bounds__(kSelWaves * kWave, 1) void selective_prefill_f32_ke
     else if (tid == kFP + kD) sK0[0] = kreg;
 
     const int NC = (a.L + kC - 1) / kC;
+    const int c_begin = seg * a.cps, c_end = min(c_begin + a.cps, NC);
     const int64_t ybase = b * a.y_sb + h * a.y_sh;
-    for (int c = 0; c < NC; ++c) {
+    float seg_ld = 0.f;  // (state-only, wave 0) the segment's total natural-log decay
+    for (int c = c_begin; c < c_end; ++c) {
         // ---- the chunk's features: thread = (token tid/8, 8 dims)
         {
             const int i = tid >> 3, d0 = 8 * (tid & 7);
@@ -139,12 +160,14 @@ __global__ __launch_bounds__(kSelWaves * kWave, 1) void selective_prefill_f32_ke
                 if (lane >= s) cum += x;
             }
             const float cend = __shfl(cum, 63, kWave);
+            seg_ld += cend;
             sCum[lane] = cum;
             sEc[lane] = expf(cum);
             sW[lane] = valid ? expf(cend - cum) : 0.f;
         }
         __syncthreads();
 
+        if constexpr (!STATE_ONLY) {
         // ---- A on the 10 lower 16x16 tiles (feature k-slot g of k-step s: 32g + s)
         for (int ti = w; ti < 10; ti += kSelWaves) {
             const int ib = ti < 1 ? 0 : ti < 3 ? 1 : ti < 6 ? 2 : 3;
@@ -211,6 +234,7 @@ __global__ __launch_bounds__(kSelWaves * kWave, 1) void selective_prefill_f32_ke
                 }
             }
         }
+        }  // !STATE_ONLY
         // ---- state update: M tiles of feature block w; Kf, S0, K0 by their threads
         {
             const float e63 = sEc[kC - 1];
@@ -252,8 +276,25 @@ __global__ __launch_bounds__(kSelWaves * kWave, 1) void selective_prefill_f32_ke
         else if (tid == kFP + kD) sK0[0] = kreg;
     }
 
+    if constexpr (STATE_ONLY) {
+        // the segment's state from zero and its log2 decay, for the scan over segments
+#pragma unroll
+        for (int dv = 0; dv < 4; ++dv)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int f = 16 * w + 4 * g + r, col = 16 * dv + c16;
+                if (f < kD) slot[kWsS1 + f * kD + col] = mt[dv][r];
+                else slot[kWsS2 + (f - kD) * kD + col] = mt[dv][r];
+            }
+        if (tid < kD) slot[kWsK1 + tid] = kreg;
+        else if (tid < kFP) slot[kWsK2 + tid - kD] = kreg;
+        else if (tid < kFP + kD) slot[kWsS0 + tid - kFP] = kreg;
+        else if (tid == kFP + kD) slot[kWsK0] = kreg;
+        if (tid == 0) slot[kWsDecay] = seg_ld * 1.44269504088896341f;  // log2
+        return;
+    }
     // ---- final state, in the selective convention (S2, K2 carry the 1/2)
-    if (a.s1o) {
+    if (a.s1o && seg == a.G - 1) {
 #pragma unroll
         for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
@@ -270,10 +311,19 @@ __global__ __launch_bounds__(kSelWaves * kWave, 1) void selective_prefill_f32_ke
 }
 
 hipError_t launch_selective_f32(const PrefillArgs &a, hipStream_t stream) {
+    const int S = a.B * a.H;
+    hipError_t e;
+    if (a.G > 1) {
+        const TimerEvents ta = timer_events(PRIME_KERNEL_PREFILL_SEGMENTS);
+        hipExtLaunchKernelGGL(selective_prefill_f32_kernel<true>, dim3(S * (a.G - 1)), dim3(kSelWaves * kWave), 0,
+                              stream, ta.start, ta.stop, 0, a);
+        if ((e = hipGetLastError()) != hipSuccess) return timer_drop(ta), e;
+        if ((e = launch_segment_scan(a, stream)) != hipSuccess) return e;
+    }
     const TimerEvents t = timer_events(PRIME_KERNEL_PREFILL_CHUNKS);
-    hipExtLaunchKernelGGL(selective_prefill_f32_kernel, dim3(a.B * a.H), dim3(kSelWaves * kWave), 0, stream, t.start,
-                          t.stop, 0, a);
-    const hipError_t e = hipGetLastError();
+    hipExtLaunchKernelGGL(selective_prefill_f32_kernel<false>, dim3(S * a.G), dim3(kSelWaves * kWave), 0, stream,
+                          t.start, t.stop, 0, a);
+    e = hipGetLastError();
     if (e != hipSuccess) timer_drop(t);
     return e;
 }

@@ -121,6 +121,27 @@ def test_selective_prefill_segments_gqa_and_eps():
     assert_close(y1, y, 2e-3, "y one segment vs segments")
 
 
+@pytest.mark.parametrize("with_state", [False, True])
+def test_selective_prefill_f32_segments(with_state):
+    """fp32 inputs split into segments (the fp32 kernel's state-only pass, the
+    scan with each segment's own decay, one workgroup per segment) against the
+    oracle and against one workgroup per sequence."""
+    B, H, L = 1, 4, 4096 + 37
+    q, k, v, ld, beta = _inputs(B, H, L, seed=42, Hkv=2, bf16=False)
+    st = _rand_state(B * H, 43) if with_state else None
+    assert _lib.workspace_size(B, H, L) > 0  # the segmented path runs
+    yo, so = _oracle(q, k, v, ld, beta, 1.0, st)
+    y, s = _run_prefill(q, k, v, ld, beta, 1.0, st, dt=torch.float32)
+    assert_close(y, yo, TOL_F32, "y")
+    for i, (a, b) in enumerate(zip(s, so)):
+        assert_close(a, b.reshape(a.shape), TOL_F32, f"state[{i}]")
+    y1, s1 = _run_prefill(q, k, v, ld, beta, 1.0, st, dt=torch.float32,
+                          workspace=torch.empty(0, dtype=torch.uint8, device=dev()))
+    assert_close(y1, y, 1e-4, "y one segment vs segments")
+    for i, (a, b) in enumerate(zip(s1, s)):
+        assert_close(a, b, 1e-4, f"state[{i}] one segment vs segments")
+
+
 def test_selective_reduces_to_base_prefill():
     """beta = 1 and log_decay = log(lambda_h) per head: the base chunked
     prefill's y, and its state with S2, K2 halved."""
