@@ -687,19 +687,21 @@ def _delta_case(B, H, L, D, seed, bound):
     return q, k, v, beta, alpha, state
 
 
-@pytest.mark.parametrize("L,bound", [(64 * 3 + 17, 25.0), (64 * 2 + 5, 1.5), (40, 0.8)])
-def test_delta_torch_restatement_matches_oracle(L, bound):
+@pytest.mark.parametrize("L,bound,D,C", [(64 * 3 + 17, 25.0, 64, 64), (64 * 2 + 5, 1.5, 64, 64), (40, 0.8, 64, 64),
+                                         (100, 1.0, 32, 32), (23, 0.7, 8, 5), (130, 25.0, 16, 100)])
+def test_delta_torch_restatement_matches_oracle(L, bound, D, C):
     """tests/delta_ref.py (differentiable torch ops) computes what the fp64 C
     oracle computes: y and the final state, ragged L, incoming state, the
-    clamp active (bounds 1.5 and 0.8 engage it) or not."""
+    clamp active (bounds below 25 engage it) or not, at the head dims and
+    chunk sizes the kernels take."""
     import torch
     import delta_ref as R
-    B, H, D = 1, 2, 64
+    B, H = 1, 2
     q, k, v, beta, alpha, state = _delta_case(B, H, L, D, L, bound)
-    y, S = R.delta_chunked(q, k, v, beta, alpha, 0.9995, 1e-5, bound, 64, state)
+    y, S = R.delta_chunked(q, k, v, beta, alpha, 0.9995, 1e-5, bound, C, state)
     psi, phi = O.delta_features(q.reshape(B * H, L, D).numpy(), k.reshape(B * H, L, D).numpy(), eps=1e-5)
     yo, So = O.delta_chunked(psi, phi, v.reshape(B * H, L, D).numpy(), beta.reshape(B * H, L).numpy(),
-                             alpha.reshape(B * H, L).numpy(), 0.9995, bound=bound, chunk=64,
+                             alpha.reshape(B * H, L).numpy(), 0.9995, bound=bound, chunk=C,
                              state=state.reshape(B * H, D, 2 * D).numpy())
     assert O.rel_err(y.reshape(B * H, L, D).numpy(), yo) < 1e-12
     assert O.rel_err(S.reshape(B * H, D, 2 * D).numpy(), So) < 1e-12
