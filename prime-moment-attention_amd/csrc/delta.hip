@@ -362,8 +362,8 @@ __global__ __launch_bounds__(256, 1) void delta_prep_kernel(const DeltaArgs a) {
 //   state waves 0..3 carry the recurrence: wave s owns the state rows of
 //     feature blocks 2s and 2s+1 (S^T tiles for every value block dv: 32
 //     MFMAs per chunk) and publishes them as bf16 MFMA operand packs;
-//   y waves 4..7 compute the output off that chain: wave 4+v the y tiles of
-//     value block v for all four token blocks (16 MFMAs per chunk) from the
+//   y waves 4..7 compute the output off that chain: wave 4+t the y tiles of
+//     token block t for all four value blocks (16 MFMAs per chunk) from the
 //     same packs, and write the previous chunk's y out.
 // Only the state update carries into the next chunk, so the y work overlaps
 // the state waves' chain instead of lengthening it.  Each wave loads only its
@@ -390,10 +390,15 @@ struct RecS {
     float e63;
 };
 
-// a y wave's share: Z^T B operands of every token block and the Y0^T tiles of its value block
+// a y wave's share: the Z^T B operands and the Y0^T tiles of its token block
+// (a token block per y wave: each wave loads a quarter of Z, where a value
+// block per wave had every y wave load all of it -- 48 KB of the CU's 120 KB
+// of record loads per chunk were such duplicates, and the loads' issue
+// through the CU's memory pipeline was the longest phase of the y waves'
+// chunk, which is the chain's critical path)
 struct RecY {
-    bf16x8 zb[4][4];  // token block tb, k-step ks
-    uint2 y0[4];      // token block tb, value block v
+    bf16x8 zb[4];  // k-step ks
+    uint2 y0[4];   // value block dv
 };
 
 __device__ __forceinline__ bf16x8 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
@@ -418,14 +423,12 @@ __device__ __forceinline__ void load_recs(RecS &R, __amdgpu_buffer_rsrc_t rs, in
     R.e63 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, ro + kRecSC, 0));
 }
 
-__device__ __forceinline__ void load_recy(RecY &R, __amdgpu_buffer_rsrc_t rs, int ro, int v, int lane) {
+__device__ __forceinline__ void load_recy(RecY &R, __amdgpu_buffer_rsrc_t rs, int ro, int tb, int lane) {
     const int v16 = lane * 16, v8 = lane * 8;
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
+    for (int ks = 0; ks < 4; ++ks) R.zb[ks] = bload16(rs, v16, ro + kRecZB + (tb * 4 + ks) * 1024);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) R.zb[tb][ks] = bload16(rs, v16, ro + kRecZB + (tb * 4 + ks) * 1024);
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) R.y0[tb] = bload8(rs, v8, ro + kRecY0 + (tb * 4 + v) * 512);
+    for (int dv = 0; dv < 4; ++dv) R.y0[dv] = bload8(rs, v8, ro + kRecY0 + (tb * 4 + dv) * 512);
 }
 
 template <int DTY>
@@ -506,31 +509,38 @@ __device__ __forceinline__ void state_chunk(const DeltaArgs &a, int cw, int sw, 
     for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) pk[dv][ks] = sPk[buf][dv][ks][lane];
-    // ---- S~'^T = sc (e^cum_63 S~^T - M^T S~^T) + R0^T on feature blocks 2sw, 2sw + 1
+    // ---- S~'^T = sc (e^cum_63 S~^T - M^T S~^T) + R0^T on feature blocks 2sw, 2sw + 1:
+    // the eight accumulator chains (value block x feature block) interleaved
+    // k-step by k-step, so that no MFMA waits for the one before it (two
+    // chains at a time left the matrix unit idle between dependent issues)
     float ss = 0.f;
+    f32x4 x[4][2];
 #pragma unroll
-    for (int dv = 0; dv < 4; ++dv) {
-        f32x4 x[2];
+    for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
         for (int fi = 0; fi < 2; ++fi)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) x[fi][r] = cur.e63 * st[fi][dv][r];
+            for (int r = 0; r < 4; ++r) x[dv][fi][r] = cur.e63 * st[fi][dv][r];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-            for (int fi = 0; fi < 2; ++fi) x[fi] = mfma(cur.mt[fi][ks], pk[dv][ks], x[fi]);
+        for (int dv = 0; dv < 4; ++dv)
+#pragma unroll
+            for (int fi = 0; fi < 2; ++fi) x[dv][fi] = mfma(cur.mt[fi][ks], pk[dv][ks], x[dv][fi]);
+#pragma unroll
+    for (int dv = 0; dv < 4; ++dv) {
 #pragma unroll
         for (int fi = 0; fi < 2; ++fi) {
             const f32x4 r0 = unpack4(cur.r0[fi][dv]);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                x[fi][r] = sc * x[fi][r] + r0[r];
-                ss += x[fi][r] * x[fi][r];
+                x[dv][fi][r] = sc * x[dv][fi][r] + r0[r];
+                ss += x[dv][fi][r] * x[dv][fi][r];
             }
-            st[fi][dv] = x[fi];
+            st[fi][dv] = x[dv][fi];
         }
         // pack (dv, sw) of the next chunk: rows 4g..4g+3 of both feature blocks
-        const uint2 lo = pack4(x[0]), hi = pack4(x[1]);
+        const uint2 lo = pack4(x[dv][0]), hi = pack4(x[dv][1]);
         sPk[buf ^ 1][dv][sw][lane] = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
     }
     ss = wave_sum(ss);
@@ -539,31 +549,37 @@ __device__ __forceinline__ void state_chunk(const DeltaArgs &a, int cw, int sw, 
     sc = clamp_scale(a, sRed[buf]);  // Lyapunov clamp (:266-270), kept as the pending scale
 }
 
-// One chunk of a y wave: y^T tiles of value block v (all token blocks) = Y0^T +
+// One chunk of a y wave: y^T tiles of token block tb (all value blocks) = Y0^T +
 // sc S~ Z^T into the chunk's LDS stage, after writing the previous chunk's
 // staged y (WRITE_PREV) to global memory.
 template <int DTY, bool WRITE_PREV>
-__device__ __forceinline__ void y_chunk(const DeltaArgs &a, int cw, int v, int lane, int g, int c16,
+__device__ __forceinline__ void y_chunk(const DeltaArgs &a, int cw, int tb, int lane, int g, int c16,
                                         __amdgpu_buffer_rsrc_t rs, float &sc, const RecY &cur, RecY &nxt,
                                         bf16x8 (*sPk)[4][4][64], float (*sRed)[kStateWaves], uint8_t *sY,
                                         uint8_t *ychunk, int64_t yrow_bytes, int ty) {
     using YS = YStage<DTY>;
     const int buf = cw & 1;
-    load_recy(nxt, rs, min(cw + 1, a.nw - 1) * static_cast<int>(kDeltaRecBytes), v, lane);
-    bf16x8 pk[4];
+    load_recy(nxt, rs, min(cw + 1, a.nw - 1) * static_cast<int>(kDeltaRecBytes), tb, lane);
+    bf16x8 pk[4][4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) pk[ks] = sPk[buf][v][ks][lane];
+    for (int dv = 0; dv < 4; ++dv)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) pk[dv][ks] = sPk[buf][dv][ks][lane];
     uint8_t *ys = sY + buf * YS::bytes;
+    f32x4 p[4];  // the four value blocks' chains, interleaved k-step by k-step
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-        f32x4 p = {0.f, 0.f, 0.f, 0.f};
+    for (int dv = 0; dv < 4; ++dv) p[dv] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) p = mfma(pk[ks], cur.zb[tb][ks], p);
-        const f32x4 y0 = unpack4(cur.y0[tb]);
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int dv = 0; dv < 4; ++dv) p[dv] = mfma(pk[dv][ks], cur.zb[ks], p[dv]);
+#pragma unroll
+    for (int dv = 0; dv < 4; ++dv) {
+        const f32x4 y0 = unpack4(cur.y0[dv]);
         f32x4 yv;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) yv[r] = y0[r] + sc * p[r];
-        store_y4<DTY>(ys + (16 * tb + c16) * YS::pitch + (16 * v + 4 * g) * YS::es, yv);
+        for (int r = 0; r < 4; ++r) yv[r] = y0[r] + sc * p[dv][r];
+        store_y4<DTY>(ys + (16 * tb + c16) * YS::pitch + (16 * dv + 4 * g) * YS::es, yv);
     }
     // the previous chunk's y, staged before the last barrier: stored after this
     // chunk's use of `cur`, so that the wait for `cur` (loaded one chunk ago)
@@ -644,7 +660,7 @@ __global__ __launch_bounds__(kScanWaves * kWave, 1) void delta_scan_kernel(const
                 }
         }
     } else {
-        const int v = w - kStateWaves, ty = tid - kStateWaves * kWave;
+        const int v = w - kStateWaves, ty = tid - kStateWaves * kWave;  // v: this wave's token block
         RecY ra, rb;
         load_recy(ra, rs, 0, v, lane);
         __syncthreads();
