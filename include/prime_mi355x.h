@@ -19,12 +19,13 @@
  * q is taken PRE-SCALED by 1/sqrt(D), as at the reference's core boundary
  * (chunked_ssd.py:58-61, attention.py:101).
  *
- * Head dim: D = 64 runs the MFMA chunk kernels; the base form (prefill,
- * decode step, backward, QK-norm) also takes 1 <= D <= 63 (the reference's
- * own tests use 32 and 16), run token by token in one wavefront per
- * (sequence, head) with no row-alignment requirement and no workspace beyond
- * the backward's per-token records.  The selective and delta-rule forms,
- * prime_accumulate and the split decode readout/update take D = 64 only.
+ * Head dim: D = 64 runs the MFMA chunk kernels; the base and selective forms
+ * (prefill, decode step, backward, QK-norm) also take 1 <= D <= 63 (the
+ * reference's own tests use 32 and 16), run token by token in one wavefront
+ * per (sequence, head) with no row-alignment requirement and no workspace
+ * beyond the backward's per-token records.  The delta rule takes D <= 64
+ * with any chunk (documented at prime_delta_prefill).  prime_accumulate and
+ * the split decode readout/update take D = 64 only.
  */
 #ifndef PRIME_MI355X_H
 #define PRIME_MI355X_H

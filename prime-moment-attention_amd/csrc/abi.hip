@@ -173,8 +173,9 @@ int decode_impl(const prime_tensor_t *q, const prime_tensor_t *k, const prime_te
         return fail(PRIME_ERR_INVALID_ARG, "prime_decode_step: null argument");
     if (D != prime::kD) {
         // head dims below 64: the generic recurrence over one token
-        if (selective) return fail(PRIME_ERR_UNSUPPORTED_DIM, "the selective form takes head dim 64 (got %d)", D);
         if (!valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported y dtype");
+        if (selective && !gate->decay && (!gate->step || !gate->tau || !valid_dtype(gate->step_dtype)))
+            return fail(PRIME_ERR_INVALID_ARG, "selective gate: give decay_bh, or step (a supported dtype) and tau");
         if (y->layout != PRIME_LAYOUT_STRIDED)
             return fail(PRIME_ERR_INVALID_ARG, "head dim %d: y must be a strided view", D);
         prime::GenericArgs g{};
@@ -183,6 +184,13 @@ int decode_impl(const prime_tensor_t *q, const prime_tensor_t *k, const prime_te
             (rc = generic_norm(g, norm)))
             return rc;
         g.y = y->data; g.dt_y = y->dtype; g.y_sb = y->stride_b; g.y_sh = y->stride_h; g.y_sl = 0;
+        if (selective) {
+            g.selective = 1;
+            g.k_scale = k_scale;
+            g.decay_bh = gate->decay;
+            g.step = gate->step; g.step_sb = gate->step_sb; g.dt_step = gate->step_dtype;
+            g.tau = gate->tau; g.step_min = gate->step_min; g.step_max = gate->step_max;
+        }
         return check_hip(prime::launch_generic_prefill(g, static_cast<hipStream_t>(stream)), "decode launch");
     }
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv)
@@ -519,8 +527,8 @@ static int prefill_impl(const prime_tensor_t *q, const prime_tensor_t *k, const 
         return fail(PRIME_ERR_INVALID_ARG, "prefill: null argument");
     if (D != prime::kD) {
         // head dims below 64: one wavefront per (sequence, head), chunk size irrelevant
-        if (selective) return fail(PRIME_ERR_UNSUPPORTED_DIM, "the selective form takes head dim 64 (got %d)", D);
         if (chunk <= 0) return fail(PRIME_ERR_INVALID_ARG, "bad chunk %d", chunk);
+        if (selective && flags) return fail(PRIME_ERR_INVALID_ARG, "the selective form takes no flags");
         if (!valid_dtype(y->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported y dtype");
         prime::GenericArgs g{};
         int rc;
@@ -528,6 +536,11 @@ static int prefill_impl(const prime_tensor_t *q, const prime_tensor_t *k, const 
             (rc = generic_norm(g, norm)))
             return rc;
         g.y = y->data; g.dt_y = y->dtype; g.y_sb = y->stride_b; g.y_sh = y->stride_h; g.y_sl = y->stride_l;
+        if (selective) {
+            g.selective = 1;
+            g.log_decay = log_decay;
+            g.k_scale = k_scale;
+        }
         return check_hip(prime::launch_generic_prefill(g, static_cast<hipStream_t>(stream)), "prefill launch");
     }
     if (B <= 0 || H <= 0 || H_kv <= 0 || H % H_kv || L <= 0 || chunk <= 0)
@@ -903,7 +916,46 @@ int prime_selective_prefill_backward(const prime_tensor_t *q, const prime_tensor
     if (!q || !k || !v || !dy || !dq || !dk || !dv || !q->data || !k->data || !v->data || !dy->data || !dq->data ||
         !dk->data || !dv->data || !log_decay || !k_scale || !d_log_decay || !d_k_scale || !workspace)
         return fail(PRIME_ERR_INVALID_ARG, "prime_selective_prefill_backward: null argument");
-    if (D != prime::kD) return fail(PRIME_ERR_UNSUPPORTED_DIM, "head dim %d unsupported (only 64)", D);
+    if (D != prime::kD) {
+        // head dims below 64: the generic reverse pass in its selective form
+        if (H_kv != H)
+            return fail(PRIME_ERR_INVALID_ARG, "backward takes k/v with one head per query head (H_kv=%d, H=%d)",
+                        H_kv, H);
+        if (!valid_dtype(dy->dtype) || !valid_dtype(dq->dtype))
+            return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dy / gradient dtype");
+        if (dk->dtype != dq->dtype || dv->dtype != dq->dtype || dk->stride_b != dq->stride_b ||
+            dv->stride_b != dq->stride_b || dk->stride_h != dq->stride_h || dv->stride_h != dq->stride_h ||
+            dk->stride_l != dq->stride_l || dv->stride_l != dq->stride_l)
+            return fail(PRIME_ERR_INVALID_ARG, "dq, dk and dv must share dtype and strides");
+        if (B > 0 && H > 0 && L > 0 &&
+            (workspace_bytes < prime_selective_prefill_backward_workspace_size(B, H, L) || !aligned16(workspace)))
+            return fail(PRIME_ERR_INVALID_ARG, "workspace of %zu bytes (16-byte aligned) is below the %zu needed",
+                        workspace_bytes, prime_selective_prefill_backward_workspace_size(B, H, L));
+        prime::GenericArgs g{};
+        int rc;
+        if ((rc = generic_args(g, q, k, v, B, H, H_kv, L, D, nullptr, eps, 0u, state_in, nullptr)) ||
+            (rc = check_state(dstate_out, "dstate_out")) || (rc = check_state(dstate_in, "dstate_in")))
+            return rc;
+        g.selective = 1;
+        g.log_decay = log_decay;
+        g.k_scale = k_scale;
+        g.dy = dy->data; g.dt_dy = dy->dtype; g.dy_sb = dy->stride_b; g.dy_sh = dy->stride_h; g.dy_sl = dy->stride_l;
+        if (dstate_out) {
+            g.ds0 = dstate_out->s0; g.ds1 = dstate_out->s1; g.ds2 = dstate_out->s2;
+            g.dk0 = dstate_out->k0; g.dk1 = dstate_out->k1; g.dk2 = dstate_out->k2;
+        }
+        g.dq = dq->data; g.dk = dk->data; g.dv = dv->data; g.dt_g = dq->dtype;
+        g.g_sb = dq->stride_b; g.g_sh = dq->stride_h; g.g_sl = dq->stride_l;
+        if (dstate_in) {
+            g.dsi0 = dstate_in->s0; g.dsi1 = dstate_in->s1; g.dsi2 = dstate_in->s2;
+            g.dki0 = dstate_in->k0; g.dki1 = dstate_in->k1; g.dki2 = dstate_in->k2;
+        }
+        g.ws = static_cast<float *>(workspace);
+        g.pq = reinterpret_cast<float *>(static_cast<char *>(workspace) + bwd_token_bytes(B, H, L));
+        g.dlogd = d_log_decay;
+        g.dkscale = d_k_scale;
+        return check_hip(prime::launch_generic_backward(g, static_cast<hipStream_t>(stream)), "backward launch");
+    }
     if (B <= 0 || H <= 0 || L <= 0) return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d L=%d", B, H, L);
     if (H_kv != H)
         return fail(PRIME_ERR_INVALID_ARG, "backward takes k/v with one head per query head (H_kv=%d, H=%d): "

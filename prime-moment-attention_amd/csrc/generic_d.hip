@@ -72,7 +72,7 @@ __device__ __forceinline__ void generic_ln_row(float *row, int D, const void *w,
 // when the args carry a QK LayerNorm; rows past nv are zero.
 __device__ __forceinline__ void generic_stage(const GenericArgs &a, int b, int h, int hk, int t0, int nv,
                                               float (*sq)[kGP], float (*sk)[kGP], float (*sv)[kGP],
-                                              float (*sdy)[kGP], int lane) {
+                                              float (*sdy)[kGP], float *sdec, int lane) {
     const int D = a.D;
     for (int t = 0; t < kGC; ++t) {
         const bool ok = t < nv && lane < D;
@@ -92,15 +92,42 @@ __device__ __forceinline__ void generic_stage(const GenericArgs &a, int b, int h
         }
         __syncthreads();
     }
+    if (a.selective) {
+        // beta k (the kernels then weight k*k by 1/2 and q*q by 1); the token's decay
+        const float beta = a.k_scale[h];
+        for (int t = 0; t < nv; ++t) sk[t][lane] *= beta;
+        if (lane < nv) {
+            const int64_t bh = static_cast<int64_t>(b) * a.H + h;
+            float lam_t;
+            if (a.log_decay) {
+                lam_t = expf(a.log_decay[bh * a.L + t0 + lane]);
+            } else if (a.decay_bh) {
+                lam_t = a.decay_bh[bh];
+            } else {
+                // selective.py:368, 386: Delta = clamp(softplus(s)), each stage
+                // rounded to the step's dtype as the module's tensors are
+                const float sv0 = ld_any(a.step, b * a.step_sb + h, a.dt_step);
+                float d = sv0 > 20.f ? sv0 : log1pf(expf(sv0));
+                d = round_dt(d, a.dt_step);
+                d = round_dt(fminf(fmaxf(d, a.step_min), a.step_max), a.dt_step);
+                lam_t = expf(-d / a.tau[h]);
+            }
+            sdec[lane] = lam_t;
+        }
+        __syncthreads();
+    }
 }
 
 __global__ __launch_bounds__(kGD) void generic_prefill_kernel(const GenericArgs a) {
-    __shared__ float sq[kGC][kGP], sk[kGC][kGP], sv[kGC][kGP];
+    __shared__ float sq[kGC][kGP], sk[kGC][kGP], sv[kGC][kGP], sdec[kGC];
     __shared__ float sKin[3][kGP];  // incoming K1, K2 (dense clamp), K0 at [2][0]
     const int lane = threadIdx.x, bh = blockIdx.x;
     const int b = bh / a.H, h = bh - b * a.H, hk = h / a.group, D = a.D;
     const bool col = lane <= D;
-    const float lam = a.decay[h];
+    const bool sel = a.selective != 0;
+    const float lam = sel ? 1.0f : a.decay[h];
+    // the second-order weights: k*k and q*q/2 (base), (beta k)*(beta k)/2 and q*q (selective)
+    const float ck2 = sel ? 0.5f : 1.0f, cq2 = sel ? 1.0f : 0.5f;
     const size_t o1 = static_cast<size_t>(bh) * D * D, o0 = static_cast<size_t>(bh) * D;
     float S0 = 0.f, S1[kGD - 1], S2[kGD - 1];
 #pragma unroll
@@ -124,20 +151,21 @@ __global__ __launch_bounds__(kGD) void generic_prefill_kernel(const GenericArgs 
     for (int c = 0; c < NC; ++c) {
         const int t0 = c * kGC, nv = min(kGC, a.L - t0);
         __syncthreads();  // the previous chunk's reads are done
-        generic_stage(a, b, h, hk, t0, nv, sq, sk, sv, nullptr, lane);
+        generic_stage(a, b, h, hk, t0, nv, sq, sk, sv, nullptr, sdec, lane);
         float pin = dense ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(t0 + 1))) : 0.f;
         for (int t = 0; t < nv; ++t) {
             const float vj = lane < D ? sv[t][lane] : (lane == D ? 1.0f : 0.0f);
-            S0 = lam * S0 + vj;
+            const float lt = sel ? sdec[t] : lam;
+            S0 = lt * S0 + vj;
             float num = S0;
 #pragma unroll
             for (int i = 0; i < kGD - 1; ++i) {
                 if (i < D) {
                     const float ki = sk[t][i], qi = sq[t][i];
-                    S1[i] = fmaf(lam, S1[i], ki * vj);
-                    S2[i] = fmaf(lam, S2[i], ki * ki * vj);
+                    S1[i] = fmaf(lt, S1[i], ki * vj);
+                    S2[i] = fmaf(lt, S2[i], ck2 * ki * ki * vj);
                     num = fmaf(qi, S1[i], num);
-                    num = fmaf(0.5f * qi * qi, S2[i], num);
+                    num = fmaf(cq2 * qi * qi, S2[i], num);
                 }
             }
             const float den = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(num), D));
@@ -179,15 +207,20 @@ __global__ __launch_bounds__(kGD) void generic_prefill_kernel(const GenericArgs 
 }
 
 __global__ __launch_bounds__(kGD) void generic_backward_kernel(const GenericArgs a) {
-    __shared__ float sq[kGC][kGP], sk[kGC][kGP], sv[kGC][kGP], sdy[kGC][kGP];
+    __shared__ float sq[kGC][kGP], sk[kGC][kGP], sv[kGC][kGP], sdy[kGC][kGP], sdec[kGC];
     __shared__ float sred[kGP][kGP];
     __shared__ float sKin[3][kGP];
     const int lane = threadIdx.x, bh = blockIdx.x;
     const int b = bh / a.H, h = bh - b * a.H, hk = h / a.group, D = a.D;
     const bool col = lane <= D;
-    const float lam = a.decay[h];
+    const bool sel = a.selective != 0;
+    const float lam = sel ? 1.0f : a.decay[h];
+    const float ck2 = sel ? 0.5f : 1.0f, cq2 = sel ? 1.0f : 0.5f;
     const size_t o1 = static_cast<size_t>(bh) * D * D, o0 = static_cast<size_t>(bh) * D;
     float *ws = a.ws + static_cast<size_t>(bh) * a.L * 2;
+    // selective: <dstate_out, state_out> (the final state's share of every log
+    // decay's adjoint), formed at the end of the forward pass
+    float fin = 0.f;
     const int NC = (a.L + kGC - 1) / kGC;
     const bool dense = a.dense_clamp && a.s1i;
     if (dense) {
@@ -215,20 +248,21 @@ __global__ __launch_bounds__(kGD) void generic_backward_kernel(const GenericArgs
         for (int c = 0; c < NC; ++c) {
             const int t0 = c * kGC, nv = min(kGC, a.L - t0);
             __syncthreads();
-            generic_stage(a, b, h, hk, t0, nv, sq, sk, sv, sdy, lane);
+            generic_stage(a, b, h, hk, t0, nv, sq, sk, sv, sdy, sdec, lane);
             float pin = dense ? static_cast<float>(pow(static_cast<double>(lam), static_cast<double>(t0 + 1))) : 0.f;
             for (int t = 0; t < nv; ++t) {
                 const float vj = lane < D ? sv[t][lane] : (lane == D ? 1.0f : 0.0f);
-                S0 = lam * S0 + vj;
+                const float lt = sel ? sdec[t] : lam;
+                S0 = lt * S0 + vj;
                 float num = S0;
 #pragma unroll
                 for (int i = 0; i < kGD - 1; ++i) {
                     if (i < D) {
                         const float ki = sk[t][i], qi = sq[t][i];
-                        S1[i] = fmaf(lam, S1[i], ki * vj);
-                        S2[i] = fmaf(lam, S2[i], ki * ki * vj);
+                        S1[i] = fmaf(lt, S1[i], ki * vj);
+                        S2[i] = fmaf(lt, S2[i], ck2 * ki * ki * vj);
                         num = fmaf(qi, S1[i], num);
-                        num = fmaf(0.5f * qi * qi, S2[i], num);
+                        num = fmaf(cq2 * qi * qi, S2[i], num);
                     }
                 }
                 const float den = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(num), D));
@@ -259,10 +293,15 @@ __global__ __launch_bounds__(kGD) void generic_backward_kernel(const GenericArgs
                     hcol = den >= a.eps ? dD : 0.f;
                 }
                 const float g = lane < D ? dyj / den_c : (lane == D ? hcol : 0.f);
-                // dq_t[i] = sum_j g_j (S1[i][j] + q_i S2[i][j]) (+ the incoming-K term)
+                // selective: phi_q . dphi_q = sum_j g_j num_j (the ones column: hcol den)
+                if (sel) {
+                    const float pqt = wave_sum(col ? g * num : 0.f);
+                    if (lane == 0) a.pq[static_cast<size_t>(bh) * a.L + t0 + t] = pqt;
+                }
+                // dq_t[i] = sum_j g_j (S1[i][j] + 2 cq2 q_i S2[i][j]) (+ the incoming-K term)
 #pragma unroll
                 for (int i = 0; i < kGD - 1; ++i)
-                    if (i < D) sred[lane][i] = g * (S1[i] + sq[t][i] * S2[i]);
+                    if (i < D) sred[lane][i] = g * (S1[i] + (2.0f * cq2) * sq[t][i] * S2[i]);
                 __syncthreads();
                 if (lane < D) {
                     float s = 0.f;
@@ -286,8 +325,19 @@ __global__ __launch_bounds__(kGD) void generic_backward_kernel(const GenericArgs
                 __syncthreads();
             }
         }
+        if (sel && a.ds1 && col) {
+            float f = lane < D ? a.ds0[o0 + lane] * S0 : a.dk0[bh] * S0;
+#pragma unroll
+            for (int i = 0; i < kGD - 1; ++i)
+                if (i < D)
+                    f += lane < D ? a.ds1[o1 + i * D + lane] * S1[i] + a.ds2[o1 + i * D + lane] * S2[i]
+                                  : a.dk1[o0 + i] * S1[i] + a.dk2[o0 + i] * S2[i];
+            fin = f;
+        }
+        if (sel) fin = wave_sum(col ? fin : 0.f);
     }
     // ---------------- pass 2: reverse, dk, dv, the incoming state's adjoint
+    float dl_acc = 0.f, dks = 0.f;  // selective: suffix sum of the log decays' adjoint; beta's
     float dS0 = 0.f, dS1[kGD - 1], dS2[kGD - 1];
 #pragma unroll
     for (int i = 0; i < kGD - 1; ++i) {
@@ -301,11 +351,12 @@ __global__ __launch_bounds__(kGD) void generic_backward_kernel(const GenericArgs
     for (int c = NC - 1; c >= 0; --c) {
         const int t0 = c * kGC, nv = min(kGC, a.L - t0);
         __syncthreads();
-        generic_stage(a, b, h, hk, t0, nv, sq, sk, sv, sdy, lane);
+        generic_stage(a, b, h, hk, t0, nv, sq, sk, sv, sdy, sdec, lane);
         for (int t = nv - 1; t >= 0; --t) {
             const float den_c = ws[2 * (t0 + t)], hcol = ws[2 * (t0 + t) + 1];
             const float g = lane < D ? sdy[t][lane] / den_c : (lane == D ? hcol : 0.f);
             const float vj = lane < D ? sv[t][lane] : (lane == D ? 1.0f : 0.0f);
+            const float lt = sel ? sdec[t] : lam;
             dS0 += g;
             float dvj = dS0;
 #pragma unroll
@@ -313,27 +364,42 @@ __global__ __launch_bounds__(kGD) void generic_backward_kernel(const GenericArgs
                 if (i < D) {
                     const float qi = sq[t][i], ki = sk[t][i];
                     dS1[i] = fmaf(qi, g, dS1[i]);
-                    dS2[i] = fmaf(0.5f * qi * qi, g, dS2[i]);
+                    dS2[i] = fmaf(cq2 * qi * qi, g, dS2[i]);
                     dvj = fmaf(ki, dS1[i], dvj);
-                    dvj = fmaf(ki * ki, dS2[i], dvj);
-                    sred[lane][i] = vj * (dS1[i] + 2.0f * ki * dS2[i]);
+                    dvj = fmaf(ck2 * ki * ki, dS2[i], dvj);
+                    sred[lane][i] = vj * (dS1[i] + (2.0f * ck2) * ki * dS2[i]);
                 }
             }
             if (lane < D) store_elem(a.dv, b * a.g_sb + h * a.g_sh + static_cast<int64_t>(t0 + t) * a.g_sl + lane, a.dt_g, dvj);
+            if (sel) {
+                // the log decays' adjoint: sum over the tokens m >= t of
+                // phi_q(m).dphi_q(m) - phi_k(m).dphi_k(m), plus the final state's share
+                const float pkt = wave_sum(col ? vj * dvj : 0.f);
+                dl_acc += a.pq[static_cast<size_t>(bh) * a.L + t0 + t] - pkt;
+                if (lane == 0) a.dlogd[static_cast<size_t>(bh) * a.L + t0 + t] = dl_acc + fin;
+            }
             __syncthreads();
             if (lane < D) {
                 float s = 0.f;
                 for (int jj = 0; jj <= D; ++jj) s += sred[jj][lane];
-                store_elem(a.dk, b * a.g_sb + h * a.g_sh + static_cast<int64_t>(t0 + t) * a.g_sl + lane, a.dt_g, s);
+                // (selective: s is the scaled key's adjoint; the raw key's is beta s,
+                // beta's the sum of k s = (beta k) s / beta)
+                if (sel) dks = fmaf(sk[t][lane], s, dks);
+                store_elem(a.dk, b * a.g_sb + h * a.g_sh + static_cast<int64_t>(t0 + t) * a.g_sl + lane, a.dt_g,
+                           sel ? a.k_scale[h] * s : s);
             }
             __syncthreads();
-            dS0 *= lam;
+            dS0 *= lt;
 #pragma unroll
             for (int i = 0; i < kGD - 1; ++i) {
-                dS1[i] *= lam;
-                dS2[i] *= lam;
+                dS1[i] *= lt;
+                dS2[i] *= lt;
             }
         }
+    }
+    if (sel) {
+        const float tot = wave_sum(dks);
+        if (lane == 0) a.dkscale[bh] = tot / a.k_scale[h];
     }
     if (a.dsi1) {
         // the ones column's K1 / K2 adjoint collects the dense clamp's direct

@@ -286,6 +286,20 @@ struct GenericArgs {
     int64_t g_sb, g_sh, g_sl;
     float *dsi0, *dsi1, *dsi2, *dki0, *dki1, *dki2;  // adjoint of the incoming state or null
     float *ws;                                        // [B*H][L][2]
+    // selective form: a decay per token, k weighted by k_scale[h] (beta), S2
+    // and K2 carrying the 1/2; decays from log_decay [B*H][L] (natural log), or
+    // for one token (the decode step) from decay_bh [B*H] or the step-size
+    // pre-activations (l = exp(-clamp(softplus(step)) / tau), each stage
+    // rounded to dt_step)
+    int selective;
+    const float *log_decay, *k_scale, *decay_bh, *tau;
+    const void *step;
+    int64_t step_sb;
+    int dt_step;
+    float step_min, step_max;
+    float *dlogd;    // backward: [B*H][L], the log decays' adjoint
+    float *dkscale;  // backward: [B*H], beta's adjoint per sequence
+    float *pq;       // backward scratch: [B*H][L]
 };
 constexpr int kGenericMaxD = 63;
 hipError_t launch_generic_prefill(const GenericArgs &a, hipStream_t stream);

@@ -280,9 +280,9 @@ def test_generic_entry_points_reject_bad_arguments():
     B, H, L, D = 1, 2, 10, 32
     x = torch.zeros(B, H, L, D, device=dev())
     lam = to_dev(np.full(H, 0.99, np.float32))
-    with pytest.raises(RuntimeError, match="selective"):
-        _lib.selective_prefill(x, x, x, torch.zeros(B * H * L, device=dev()), torch.ones(H, device=dev()), 1.0,
-                               None, x.clone(), _lib.new_state(B, H, D, dev()))
+    xw = torch.zeros(B, H, L, 80, device=dev())
+    with pytest.raises(RuntimeError, match="head dim"):  # 64, or 1 .. 63
+        _lib.chunked_prefill(xw, xw, xw, lam, 1.0, 64, None, xw.clone(), _lib.new_state(B, H, 80, dev()))
     g = [torch.empty(B, H, L, D, device=dev()) for _ in range(3)]
     with pytest.raises(RuntimeError, match="workspace"):
         _lib.chunked_prefill_backward(x, x, x, lam, 1.0, None, x, None, *g, None,
@@ -450,3 +450,173 @@ def test_reference_model_generate():
         gen = model.generate(prompt, max_new_tokens=10, temperature=0.7)
     assert gen.shape == (1, 14)
     assert bool((gen >= 0).all() and (gen < 100).all())
+
+
+# ---- selective PRIME at head dims below 64 (selective.py:264-444) ----
+
+def _sel_inputs(B, H, Hkv, L, D, seed, dtype):
+    q, k, v = _inputs(B, H, Hkv, L, D, dtype, seed)
+    rng = np.random.default_rng(seed)
+    delta = np.log1p(np.exp(rng.standard_normal((B, H, L)) - 1.0))  # softplus step sizes
+    tau = rng.uniform(8.0, 400.0, H)
+    beta = rng.uniform(0.6, 2.5, H).astype(np.float32)
+    log_decay = (-delta / tau[None, :, None]).astype(np.float32)
+    return q, k, v, log_decay, beta
+
+
+def _sel_state(BH, D, seed):
+    rng = np.random.default_rng(seed)
+    return (rng.standard_normal((BH, D)), rng.standard_normal((BH, D, D)) * 0.05,
+            rng.standard_normal((BH, D, D)) * 0.05, np.abs(rng.standard_normal(BH)) * 5 + 1,
+            rng.standard_normal((BH, D)) * 0.1, np.abs(rng.standard_normal((BH, D))) * 0.1)
+
+
+@pytest.mark.parametrize("D", [32, 16])
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, TOL_BF16), (torch.float32, TOL_F32)])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_generic_selective_prefill_matches_oracle(D, dtype, tol, with_state):
+    """Per-token decays, beta-weighted keys, the selective state convention
+    (S2, K2 carry the 1/2): against oracle_selective_recurrent, with GQA."""
+    B, H, Hkv, L = 2, 4, 2, 150
+    q, k, v, ld, beta = _sel_inputs(B, H, Hkv, L, D, 200 + D, dtype)
+    st = _sel_state(B * H, D, 7) if with_state else None
+    grp = H // Hkv
+    ke, ve = np.repeat(k, grp, axis=1), np.repeat(v, grp, axis=1)
+    yo, so = O.selective_recurrent(q.reshape(B * H, L, D), ke.reshape(B * H, L, D), ve.reshape(B * H, L, D),
+                                   np.exp(ld.astype(np.float64)).reshape(B * H, L),
+                                   np.tile(beta.astype(np.float64), B), eps=1.0, state=st)
+    y = torch.empty(B, H, L, D, device=dev())
+    s_out = _lib.new_state(B, H, D, dev())
+    _lib.selective_prefill(to_dev(q, dtype), to_dev(k, dtype), to_dev(v, dtype), to_dev(ld), to_dev(beta), 1.0,
+                           state_to_dev(st, B, H, D) if with_state else None, y, s_out)
+    torch.cuda.synchronize()
+    assert_close(to_np(y).reshape(B * H, L, D), yo, tol, "y")
+    assert_state_close(state_to_np(s_out, B * H, D), so, tol)
+
+
+@pytest.mark.parametrize("gate_kind", ["decay_bh", "step"])
+def test_generic_selective_decode_step(gate_kind):
+    """One token through the selective step with the gate formed in the
+    kernel (decays per (sequence, head), or softplus / clamp / exp of the step
+    pre-activations), against the oracle; in place."""
+    B, H, D = 3, 4, 32
+    q, k, v, _, beta = _sel_inputs(B, H, H, 1, D, 300, torch.float32)
+    rng = np.random.default_rng(301)
+    pre = rng.standard_normal((B, H)).astype(np.float32)
+    tau = rng.uniform(8.0, 400.0, H).astype(np.float32)
+    lam = np.exp(-np.clip(np.log1p(np.exp(pre.astype(np.float64))), 1e-4, 50.0) / tau[None, :])
+    st = _sel_state(B * H, D, 302)
+    yo, so = O.selective_recurrent(q.reshape(B * H, 1, D), k.reshape(B * H, 1, D), v.reshape(B * H, 1, D),
+                                   lam.reshape(B * H, 1), np.tile(beta.astype(np.float64), B), eps=1.0, state=st)
+    s = state_to_dev(st, B, H, D)
+    y = torch.empty(B, H, D, device=dev())
+    if gate_kind == "decay_bh":
+        lam_d = to_dev(lam.astype(np.float32))
+        gate = _lib.selective_gate(B, H, decay_bh=lam_d)
+    else:
+        pre_d, tau_d = to_dev(pre), to_dev(tau)
+        gate = _lib.selective_gate(B, H, step=pre_d, tau=tau_d)
+    _lib.selective_decode_step(to_dev(q[:, :, 0]), to_dev(k[:, :, 0]), to_dev(v[:, :, 0]), gate, to_dev(beta), 1.0,
+                               None, s, s, y)
+    torch.cuda.synchronize()
+    assert_close(to_np(y).reshape(B * H, D), yo.reshape(B * H, D), TOL_F32, "y")
+    assert_state_close(state_to_np(s, B * H, D), so, TOL_F32)
+
+
+@pytest.mark.parametrize("D,L", [(32, 100), (16, 70), (8, 1)])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_generic_selective_backward_matches_fp64_autograd(D, L, with_state):
+    """dq, dk, dv, the log decays' adjoint, beta's adjoint per sequence and the
+    incoming state's adjoint against torch float64 autograd of
+    tests/selective_ref.py (the reference's parallel branch with the step
+    branch's incoming state)."""
+    from selective_ref import selective_forward
+    B, H = 2, 2
+    q, k, v, ld, beta = _sel_inputs(B, H, H, L, D, 400 + D + L, torch.float32)
+    rng = np.random.default_rng(401)
+    dy = rng.standard_normal((B, H, L, D)).astype(np.float32)
+    st = None
+    if with_state:
+        st = tuple(x.astype(np.float32) for x in _sel_state(B * H, D, 402))
+        shapes = [(B, H, D), (B, H, D, D), (B, H, D, D), (B, H, 1), (B, H, D), (B, H, D)]
+        st = tuple(x.reshape(sh) for x, sh in zip(st, shapes))
+    ds = tuple((0.1 * rng.standard_normal(x.shape)).astype(np.float32) for x in
+               (np.zeros((B, H, D)), np.zeros((B, H, D, D)), np.zeros((B, H, D, D)), np.zeros((B, H, 1)),
+                np.zeros((B, H, D)), np.zeros((B, H, D))))
+    t = lambda x: torch.from_numpy(np.asarray(x, dtype=np.float64)).requires_grad_(True)
+    tq, tk, tv, tl = t(q), t(k), t(v), t(ld)
+    tb = t(np.broadcast_to(beta, (B, H)).copy())
+    ts = tuple(t(x) for x in st) if st is not None else None
+    yr, so = selective_forward(tq, tk, tv, tl, tb, 1.0, ts)
+    loss = (yr * torch.from_numpy(dy.astype(np.float64))).sum() + \
+        sum((a * torch.from_numpy(b.astype(np.float64))).sum() for a, b in zip(so, ds))
+    loss.backward()
+    print(f"[generic selective bwd] D={D} L={L} state={with_state}", flush=True)
+    g = [torch.empty(B, H, L, D, device=dev()) for _ in range(3)]
+    dld = torch.empty(B, H, L, device=dev())
+    dks = torch.empty(B, H, device=dev())
+    dsi = _lib.new_state(B, H, D, dev()) if with_state else None
+    _lib.selective_prefill_backward(to_dev(q), to_dev(k), to_dev(v), to_dev(ld), to_dev(beta), 1.0,
+                                    tuple(to_dev(x) for x in st) if st is not None else None, to_dev(dy),
+                                    tuple(to_dev(x) for x in ds), *g, dsi, dld, dks)
+    torch.cuda.synchronize()
+    got = {"dq": g[0], "dk": g[1], "dv": g[2], "dlog_decay": dld, "dk_scale": dks}
+    ref = {"dq": tq.grad, "dk": tk.grad, "dv": tv.grad, "dlog_decay": tl.grad, "dk_scale": tb.grad}
+    for n in got:
+        if n == "dlog_decay" and L == 1 and not with_state:
+            # one token from a zero state: its decay multiplies nothing, the
+            # adjoint is exactly zero and the kernel's is the cancellation of
+            # its two terms (the readout's and the final state's) -- held to
+            # the scale of dv instead of its own
+            err = float(got[n].abs().max().cpu()) / float(ref["dv"].abs().max())
+            assert err < TOL_F32, (n, err)
+            continue
+        assert _rel(got[n], ref[n]) < TOL_F32, (n, _rel(got[n], ref[n]))
+    if with_state:
+        for i, (a, r) in enumerate(zip(dsi, ts)):
+            assert _rel(a.reshape(r.grad.shape), r.grad) < TOL_F32, (i, _rel(a.reshape(r.grad.shape), r.grad))
+
+
+def test_generic_selective_module_head_dim_32():
+    """PrimeSelectiveMomentAttention at head_dim 32: the parallel branch and a
+    carried step against an fp32 CPU composition of the module's own weights
+    (selective.py:339-444), and its training gradients through the generic
+    selective backward."""
+    from prime_moment_attention import PrimeSelectiveMomentAttention
+    from selective_ref import selective_forward
+    torch.manual_seed(5)
+    m = PrimeSelectiveMomentAttention(hidden_size=128, num_heads=4, head_dim=32, num_kv_heads=2).to(dev())
+    with torch.no_grad():
+        m.delta_proj.weight.normal_(0.0, 0.05)
+        m.log_beta.uniform_(-0.3, 0.5)
+    B, L = 2, 40
+    x = torch.randn(B, L, 128, device=dev(), requires_grad=True)
+    out, _ = m(x)
+    g = torch.randn(out.shape, generator=torch.Generator().manual_seed(6))
+    (out * g.to(dev())).sum().backward()
+
+    mc = PrimeSelectiveMomentAttention(hidden_size=128, num_heads=4, head_dim=32, num_kv_heads=2).double()
+    mc.load_state_dict({k: v.detach().double().cpu() for k, v in m.state_dict().items()})
+    xc = x.detach().double().cpu().requires_grad_(True)
+    H, Hk, D = 4, 2, 32
+    q = mc.q_proj(xc).view(B, L, H, D).transpose(1, 2)
+    k = mc.k_proj(xc).view(B, L, Hk, D).transpose(1, 2)
+    v = mc.v_proj(xc).view(B, L, Hk, D).transpose(1, 2)
+    q, k = mc.q_norm(q) * mc.scaling, mc.k_norm(k)
+    k, v = k.repeat_interleave(2, 1), v.repeat_interleave(2, 1)
+    delta = torch.nn.functional.softplus(mc.delta_proj(xc)).clamp(min=1e-4, max=50.0)  # [B, L, H]
+    ld = (-delta / mc.get_tau(xc.device)).transpose(1, 2)
+    beta = mc.get_beta(xc.device).view(1, H).expand(B, H)
+    y, _ = selective_forward(q, k, v, ld, beta, mc.eps)
+    oc = mc.o_proj(y.transpose(1, 2).reshape(B, L, H * D))
+    (oc * g.double()).sum().backward()
+    assert _rel(out, oc) < TOL_F32
+    assert _rel(x.grad, xc.grad) < TOL_F32
+    for (name, p), (_, pc) in zip(m.named_parameters(), mc.named_parameters()):
+        assert p.grad is not None, name
+        assert _rel(p.grad, pc.grad) < TOL_F32, (name, _rel(p.grad, pc.grad))
+    # the step branch from the parallel branch's state (no autograd)
+    with torch.no_grad():
+        _, st = m(x.detach(), return_state=True)
+        o1, _ = m(torch.randn(B, 1, 128, device=dev()), state=st)
+    assert torch.isfinite(o1).all()
