@@ -500,10 +500,10 @@ __device__ __forceinline__ void state_chunk(const DeltaArgs &a, int cw, int sw, 
                                             bf16x8 (*sPk)[4][4][64], float (*sRed)[kStateWaves]) {
     const int buf = cw & 1;
     // share of chunk cw + 2 (clamped to the window: the duplicate is unused),
-    // issued as one group ahead of this chunk's work (kept there: interleaved
-    // with the MFMAs, the compiler's counts waited on these fresh loads)
-    load_recs(nxt2, rs, min(cw + 2, a.nw - 1) * static_cast<int>(kDeltaRecBytes), sw, lane);
-    __builtin_amdgcn_sched_barrier(0);
+    // one load instruction after every two MFMAs below: issued as one group,
+    // the 17 loads stalled the wave ~900 cycles before its first MFMA
+    const int ro2 = min(cw + 2, a.nw - 1) * static_cast<int>(kDeltaRecBytes);
+    nxt2.e63 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, 0, ro2 + kRecSC, 0));
     bf16x8 pk[4][4];
 #pragma unroll
     for (int dv = 0; dv < 4; ++dv)
@@ -521,12 +521,29 @@ __device__ __forceinline__ void state_chunk(const DeltaArgs &a, int cw, int sw, 
         for (int fi = 0; fi < 2; ++fi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) x[dv][fi][r] = cur.e63 * st[fi][dv][r];
+    const int v16 = lane * 16, v8 = lane * 8;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int dv = 0; dv < 4; ++dv)
 #pragma unroll
-            for (int fi = 0; fi < 2; ++fi) x[dv][fi] = mfma(cur.mt[fi][ks], pk[dv][ks], x[dv][fi]);
+            for (int fi = 0; fi < 2; ++fi) {
+                x[dv][fi] = mfma(cur.mt[fi][ks], pk[dv][ks], x[dv][fi]);
+                __builtin_amdgcn_sched_barrier(0);
+                const int q = (ks * 4 + dv) * 2 + fi;  // 0..31
+                if (q & 1) {
+                    const int l = q >> 1;  // 0..15: the -M^T operands, then the R0^T tiles
+                    if (l < 8)
+                        nxt2.mt[l >> 2][l & 3] = bload16(rs, v16, ro2 + kRecMT + ((2 * sw + (l >> 2)) * 4 + (l & 3)) * 1024);
+                    else
+                        nxt2.r0[(l - 8) >> 2][(l - 8) & 3] =
+                            bload8(rs, v8, ro2 + kRecR0 + ((2 * sw + ((l - 8) >> 2)) * 4 + ((l - 8) & 3)) * 512);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+    // the pending Lyapunov scale of the state entering this chunk (its norm was
+    // reduced in the previous chunk): read here, under the MFMAs, not before them
+    sc = cw == 0 ? 1.0f : clamp_scale(a, sRed[buf ^ 1]);
 #pragma unroll
     for (int dv = 0; dv < 4; ++dv) {
 #pragma unroll
@@ -544,9 +561,8 @@ __device__ __forceinline__ void state_chunk(const DeltaArgs &a, int cw, int sw, 
         sPk[buf ^ 1][dv][sw][lane] = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
     }
     ss = wave_sum(ss);
-    if (lane == 0) sRed[buf][sw] = ss;
+    if (lane == 0) sRed[buf][sw] = ss;  // Lyapunov clamp (:266-270): applied in the next chunk
     __syncthreads();
-    sc = clamp_scale(a, sRed[buf]);  // Lyapunov clamp (:266-270), kept as the pending scale
 }
 
 // One chunk of a y wave: y^T tiles of token block tb (all value blocks) = Y0^T +
@@ -573,6 +589,7 @@ __device__ __forceinline__ void y_chunk(const DeltaArgs &a, int cw, int tb, int 
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int dv = 0; dv < 4; ++dv) p[dv] = mfma(pk[dv][ks], cur.zb[ks], p[dv]);
+    sc = cw == 0 ? 1.0f : clamp_scale(a, sRed[buf ^ 1]);  // the scale of the state entering this chunk
 #pragma unroll
     for (int dv = 0; dv < 4; ++dv) {
         const f32x4 y0 = unpack4(cur.y0[dv]);
@@ -587,7 +604,6 @@ __device__ __forceinline__ void y_chunk(const DeltaArgs &a, int cw, int tb, int 
     if constexpr (WRITE_PREV)
         y_write<DTY, false>(a, a.c0 + cw - 1, sY + (buf ^ 1) * YS::bytes, ychunk - kC * yrow_bytes, yrow_bytes, ty);
     __syncthreads();
-    sc = clamp_scale(a, sRed[buf]);
 }
 
 }  // namespace
@@ -647,6 +663,7 @@ __global__ __launch_bounds__(kScanWaves * kWave, 1) void delta_scan_kernel(const
         if (cw < a.nw) state_chunk(a, cw, sw, lane, rs, st, sc, ra, rc, sPk, sRed);
         if (cw + 1 < a.nw) state_chunk(a, cw + 1, sw, lane, rs, st, sc, rb, ra, sPk, sRed);
         // ---- state leaving the window (the pending scale applied)
+        sc = clamp_scale(a, sRed[(a.nw - 1) & 1]);
         float *dst = a.last ? a.state_out : a.ws_state;
         if (dst) {
 #pragma unroll
