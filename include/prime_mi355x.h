@@ -143,6 +143,15 @@ int prime_add_rmsnorm(void *x, const void *delta, const void *weight, void *out,
                       int hidden, int dtype, float eps, void *stream);
 
 /*
+ * Exact GELU, y = x * 0.5 * (1 + erf(x / sqrt(2))) computed in fp32 and rounded
+ * once to `dtype` (F32 / BF16 / F16): the MLP activation of the GELU decoder
+ * blocks (nn.GELU(), primelm_50m.py:64; torch.nn.functional.gelu's default
+ * form, the same bits for bf16).  x, y: n contiguous elements, 16-byte
+ * aligned; y may be x (in place), otherwise they must not overlap.
+ */
+int prime_gelu(const void *x, void *y, int64_t n, int dtype, void *stream);
+
+/*
  * Chunked prefill of L tokens for B x H sequences.  Replaces
  * chunked_prime_ssd_core (chunked_ssd.py:48-184) and, with
  * PRIME_FLAG_DENSE_CLAMP, the dense branch of PrimeMomentAttention.forward

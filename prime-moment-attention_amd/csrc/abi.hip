@@ -291,6 +291,19 @@ int prime_add_rmsnorm(void *x, const void *delta, const void *weight, void *out,
     return check_hip(prime::launch_add_rmsnorm(a, static_cast<hipStream_t>(stream)), "add_rmsnorm launch");
 }
 
+int prime_gelu(const void *x, void *y, int64_t n, int dtype, void *stream) {
+    g_err[0] = 0;
+    if (!x || !y) return fail(PRIME_ERR_INVALID_ARG, "prime_gelu: null argument");
+    if (n < 0) return fail(PRIME_ERR_INVALID_ARG, "bad size n=%lld", static_cast<long long>(n));
+    if (!valid_dtype(dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dtype");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15)
+        return fail(PRIME_ERR_MISALIGNED, "x and y must be 16-byte aligned");
+    const size_t bytes = static_cast<size_t>(n) * elem_size(dtype);
+    if (y != x && overlap(x, bytes, y, bytes)) return fail(PRIME_ERR_ALIAS, "y overlaps x without being x");
+    if (n == 0) return PRIME_OK;
+    return check_hip(prime::launch_gelu(x, y, n, dtype, static_cast<hipStream_t>(stream)), "gelu launch");
+}
+
 int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int B, int H, int L, int D,
                          const void *weight, const void *bias, int param_dtype, float ln_eps, float scale,
                          void *stream) {

@@ -185,6 +185,68 @@ __global__ __launch_bounds__(256) void head_layernorm_kernel(const HeadNormArgs 
     }
 }
 
+// Exact (erf) GELU, y = x * 0.5 * (1 + erf(x / sqrt(2))) in fp32, rounded once to
+// the dtype: the MLP activation of primelm_50m.py:64 (nn.GELU()).  16 bytes per
+// lane per access, four accesses in flight per lane; the elements past the last
+// whole 16-byte group go to one lane each.  y may be x.
+template <int DT>
+__global__ __launch_bounds__(256) void gelu_kernel(const void *x, void *y, int64_t n) {
+    constexpr int E = DT == PRIME_F32 ? 4 : 8;  // elements per 16 bytes
+    constexpr int es = DT == PRIME_F32 ? 4 : 2;
+    const int64_t groups = n / E;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    auto act = [](float v) { return v * 0.5f * (1.0f + erff(v * 0.70710678118654752f)); };
+    auto conv = [&](uint4 r) {
+        if constexpr (DT == PRIME_F32) {
+            return make_uint4(__float_as_uint(act(__uint_as_float(r.x))), __float_as_uint(act(__uint_as_float(r.y))),
+                              __float_as_uint(act(__uint_as_float(r.z))), __float_as_uint(act(__uint_as_float(r.w))));
+        } else {
+            uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t lo = Group<DT>::to_b(act(Group<DT>::to_f(w[e] & 0xffffu)));
+                const uint32_t hi = Group<DT>::to_b(act(Group<DT>::to_f(w[e] >> 16)));
+                w[e] = lo | (hi << 16);
+            }
+            return make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    };
+    const uint4 *xs = static_cast<const uint4 *>(x);
+    uint4 *ys = static_cast<uint4 *>(y);
+    int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    for (; g + 3 * stride < groups; g += 4 * stride) {
+        uint4 r[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) r[u] = xs[g + u * stride];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ys[g + u * stride] = conv(r[u]);
+    }
+    for (; g < groups; g += stride) ys[g] = conv(xs[g]);
+    // the tail: fewer than E elements
+    const int64_t t = groups * E + static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t < n) {
+        if constexpr (DT == PRIME_F32) {
+            static_cast<float *>(y)[t] = act(static_cast<const float *>(x)[t]);
+        } else {
+            const uint16_t b = static_cast<const uint16_t *>(x)[t];
+            static_cast<uint16_t *>(y)[t] = static_cast<uint16_t>(Group<DT>::to_b(act(Group<DT>::to_f(b))));
+        }
+    }
+    (void)es;
+}
+
+hipError_t launch_gelu(const void *x, void *y, int64_t n, int dt, hipStream_t stream) {
+    const int E = dt == PRIME_F32 ? 4 : 8;
+    const int64_t groups = n / E;
+    // four 16-byte groups per lane per pass; at least one block for the tail
+    const int64_t want = (groups + 4 * 256 - 1) / (4 * 256);
+    const dim3 grid(static_cast<unsigned>(want < 1 ? 1 : (want > 4096 ? 4096 : want))), block(256);
+    if (dt == PRIME_BF16) hipLaunchKernelGGL(gelu_kernel<PRIME_BF16>, grid, block, 0, stream, x, y, n);
+    else if (dt == PRIME_F16) hipLaunchKernelGGL(gelu_kernel<PRIME_F16>, grid, block, 0, stream, x, y, n);
+    else hipLaunchKernelGGL(gelu_kernel<PRIME_F32>, grid, block, 0, stream, x, y, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_head_layernorm(const HeadNormArgs &a, hipStream_t stream) {
     const uint32_t rows = static_cast<uint32_t>(a.B) * a.L * a.H;
     const uint32_t per_block = 4u * kHeadNormBatch * (a.dt == PRIME_F32 ? 4u : 8u);  // 4 waves

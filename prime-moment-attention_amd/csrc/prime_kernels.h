@@ -117,6 +117,7 @@ hipError_t launch_pack_frag(const uint16_t *src, int64_t ld, const int64_t *idx,
 
 constexpr int kNormMaxGroups = 16;  // 4-element groups per lane: hidden <= 4 * 64 * 16 = 4096
 hipError_t launch_add_rmsnorm(const RmsNormArgs &a, hipStream_t stream);
+hipError_t launch_gelu(const void *x, void *y, int64_t n, int dt, hipStream_t stream);
 
 struct PrefillArgs {
     const void *q, *k, *v;

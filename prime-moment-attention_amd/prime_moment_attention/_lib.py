@@ -25,7 +25,7 @@ _DTYPES = {torch.float32: PRIME_F32, torch.bfloat16: PRIME_BF16, torch.float16: 
 EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_chunked_prefill",
            "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
            "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
-           "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_argmax",
+           "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_gelu", "prime_argmax",
            "prime_head_layernorm", "prime_linear", "prime_linear_residual", "prime_linear_fused", "prime_selective_prefill",
            "prime_selective_decode_step", "prime_accumulate", "prime_accumulate_workspace_size",
            "prime_decode_readout", "prime_decode_update", "prime_chunked_prefill_backward",
@@ -110,6 +110,8 @@ def load() -> ctypes.CDLL:
     L.prime_decode_step_qknorm.restype = ctypes.c_int
     L.prime_add_rmsnorm.argtypes = [fp] * 4 + [ctypes.c_int] * 3 + [ctypes.c_float, fp]
     L.prime_add_rmsnorm.restype = ctypes.c_int
+    L.prime_gelu.argtypes = [fp, fp, ctypes.c_int64, ctypes.c_int, fp]
+    L.prime_gelu.restype = ctypes.c_int
     L.prime_argmax.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, fp, fp]
     L.prime_argmax.restype = ctypes.c_int
     L.prime_head_layernorm.argtypes = [P(PrimeTensor)] * 2 + [ctypes.c_int] * 4 + [fp, fp, ctypes.c_int,
@@ -383,6 +385,22 @@ def add_rmsnorm(x: torch.Tensor, delta: Optional[torch.Tensor], weight: torch.Te
                                   ctypes.c_void_p(weight.data_ptr()), ctypes.c_void_p(out.data_ptr()), rows,
                                   hidden, _DTYPES[x.dtype], float(eps), _stream(x.device))
     _check(rc, "prime_add_rmsnorm")
+
+
+def gelu(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """prime_gelu: out = GELU(x) (exact erf form, fp32 math, one rounding);
+    x contiguous; out defaults to x (in place)."""
+    if out is None:
+        out = x
+    _dev_check(x, out)
+    if not x.is_contiguous() or not out.is_contiguous() or out.dtype != x.dtype or out.numel() != x.numel():
+        raise ValueError("x and out must be contiguous tensors of one size and dtype")
+    if x.dtype not in _DTYPES:
+        raise RuntimeError(f"unsupported dtype {x.dtype}")
+    rc = load().prime_gelu(ctypes.c_void_p(x.data_ptr()), ctypes.c_void_p(out.data_ptr()),
+                           ctypes.c_int64(x.numel()), _DTYPES[x.dtype], _stream(x.device))
+    _check(rc, "prime_gelu")
+    return out
 
 
 def head_layernorm(x: torch.Tensor, out: torch.Tensor, norm: Optional[torch.nn.LayerNorm], scale: float) -> None:

@@ -124,9 +124,11 @@ class PrimeGeluMLP(nn.Module):
 
 
 def _mlp_inner(mlp: nn.Module, x: torch.Tensor) -> torch.Tensor:
-    """The MLP up to its down projection: gelu(up x) or silu(gate x) * up x."""
+    """The MLP up to its down projection (inference path): gelu(up x), the
+    GELU by prime_gelu in place on the projection (the exact form of nn.GELU,
+    the same bits as F.gelu), or silu(gate x) * up x."""
     if isinstance(mlp, PrimeGeluMLP):
-        return F.gelu(mlp.up_proj(x))
+        return _lib.gelu(mlp.up_proj(x))
     return F.silu(mlp.gate_proj(x)) * mlp.up_proj(x)
 
 
@@ -338,7 +340,7 @@ def _decode_linear(x: torch.Tensor, w: torch.Tensor, gelu: bool = False) -> torc
         return _lib.linear(x, w, torch.empty(M, N, device=x.device, dtype=x.dtype),
                            _lib.EPILOGUE_GELU if gelu else _lib.EPILOGUE_NONE)
     y = F.linear(x, w)
-    return F.gelu(y) if gelu else y
+    return _lib.gelu(y) if gelu else y
 
 
 class _LayerStep:

@@ -131,6 +131,60 @@ def test_linear_fused_rejects_bad_shapes():
         _lib.linear_fused(big, w, torch.empty(1025, 768, device=dev(), dtype=torch.bfloat16))
 
 
+# ---------------------------------------------------------------- GELU pass
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 4096 * 3 + 5, 3 * 2**20 + 11])
+def test_gelu_matches_torch(dtype, n):
+    """prime_gelu (the prefill MLP's activation, nn.GELU's exact form) against
+    the float64 GELU of the same values: within one unit in the last place of
+    the dtype plus the fp32 formula's cancellation in 1 + erf for x below
+    about -3 (the fp32 erf of the device library may also differ from another
+    build's by an ulp, which moves a rounding at a halfway point), and equal to
+    torch's F.gelu on the GPU in all but a few elements; the 16-byte body, the
+    per-element tail and the special values (signed zeros, infinities, NaN,
+    large magnitudes) covered; out of place and in place."""
+    g = torch.Generator().manual_seed(n)
+    x = (torch.randn(n, generator=g) * 3).to(dev(), dtype)
+    special = torch.tensor([0.0, -0.0, float("inf"), float("-inf"), float("nan"), 30.0, -30.0, 1e-30, -5.5],
+                           dtype=dtype)[:n]
+    x[:special.numel()] = special.to(dev())
+    torch_gelu = F.gelu(x)
+    x64 = x.double().cpu()
+    want = F.gelu(x64)
+    ulp = {torch.bfloat16: 2.0**-7, torch.float16: 2.0**-10, torch.float32: 2.0**-22}[dtype]
+    tiny = {torch.bfloat16: 1e-38, torch.float16: 6e-8, torch.float32: 1e-44}[dtype]
+
+    def check(y):
+        yc = y.double().cpu()
+        assert torch.equal(yc.isnan(), want.isnan())
+        ok = ~want.isnan()
+        fin = ok & want.isfinite()
+        assert torch.equal(yc[ok & ~fin], want[ok & ~fin])
+        err = (yc[fin] - want[fin]).abs()
+        # one ulp of the result, plus the fp32 formula's own error where 1 + erf
+        # cancels (x below about -3: an ulp or two of erf near -1, times x / 2)
+        bound = ulp * want[fin].abs() + x64[fin].abs() * 2.0**-22 + tiny
+        assert bool((err <= bound).all()), (err - bound).max().item()
+        same = (y == torch_gelu) | (y.isnan() & torch_gelu.isnan())
+        assert (~same).sum().item() <= max(2, n // 1000)
+
+    y = torch.empty_like(x)
+    _lib.gelu(x, y)
+    torch.cuda.synchronize()
+    check(y)
+    _lib.gelu(x)  # in place
+    torch.cuda.synchronize()
+    check(x)
+
+
+def test_gelu_rejects_overlap_and_misalignment():
+    x = torch.randn(64, device=dev(), dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="overlap"):
+        _lib.gelu(x[8:], x[:56])
+    with pytest.raises(RuntimeError, match="aligned"):
+        _lib.gelu(x[1:9], torch.empty(8, device=dev(), dtype=torch.bfloat16))
+
+
 # ---------------------------------------------------------------- fragment layout
 def _frag_index(R, K, device):
     """Flat index of element (r, k) of an R x K matrix in the fragment layout
