@@ -296,6 +296,27 @@ int prime_delta_decode_step(const prime_tensor_t *q, const prime_tensor_t *k,
                             void *stream);
 
 /*
+ * Backward of prime_delta_decode_step: the gradients torch autograd takes
+ * through the L == 1 branch (chunked_delta_prime.py:140-176 -- features
+ * :73-87, the prediction with the undecayed state, the update with alpha
+ * unclamped, the Lyapunov clamp before the readout) with respect to q, k, v,
+ * beta, alpha and the incoming state, given dy and dstate_out (the gradient
+ * of the new state; NULL = zero).
+ *   q, k, v, beta, alpha, feat_eps, bound, state_in: as the forward (D <= 64)
+ *   dy           : [B, H, D], any float dtype, strided (stride_l ignored)
+ *   dq, dk, dv   : fp32 contiguous [B, H, D] -- dk and dv per QUERY head
+ *   dbeta, dalpha: fp32 [B, H]
+ *   dstate_in    : fp32 [B, H, D, 2D] or NULL
+ * One wavefront per (sequence, head), fp32 arithmetic, no workspace.
+ */
+int prime_delta_decode_step_backward(const prime_tensor_t *q, const prime_tensor_t *k,
+                                     const prime_tensor_t *v, const float *beta, const float *alpha,
+                                     int B, int H, int H_kv, int D, float feat_eps, float bound,
+                                     const float *state_in, const prime_tensor_t *dy,
+                                     const float *dstate_out, float *dq, float *dk, float *dv,
+                                     float *dbeta, float *dalpha, float *dstate_in, void *stream);
+
+/*
  * The module's per-head QK-norm on projected rows (attention.py:96-101):
  * out = LayerNorm(x) over D (biased variance, affine weight/bias [D] of
  * param_dtype, epsilon ln_eps) rounded to x's dtype, then multiplied by

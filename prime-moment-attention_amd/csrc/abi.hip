@@ -1289,6 +1289,34 @@ int prime_delta_prefill_backward(const prime_tensor_t *q, const prime_tensor_t *
     return check_hip(prime::launch_delta_backward(a, static_cast<hipStream_t>(stream)), "delta backward launch");
 }
 
+int prime_delta_decode_step_backward(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
+                                     const float *beta, const float *alpha, int B, int H, int H_kv, int D,
+                                     float feat_eps, float bound, const float *state_in, const prime_tensor_t *dy,
+                                     const float *dstate_out, float *dq, float *dk, float *dv, float *dbeta,
+                                     float *dalpha, float *dstate_in, void *stream) {
+    g_err[0] = 0;
+    if (!q || !k || !v || !dy || !q->data || !k->data || !v->data || !dy->data || !beta || !alpha || !dq || !dk ||
+        !dv || !dbeta || !dalpha)
+        return fail(PRIME_ERR_INVALID_ARG, "prime_delta_decode_step_backward: null argument");
+    prime::DeltaGenArgs g{};
+    int rc;
+    if ((rc = delta_gen_args(g, q, k, v, beta, alpha, B, H, H_kv, 1, D, 1, 1.0f, feat_eps, bound, state_in,
+                             nullptr)))
+        return rc;
+    if (!valid_dtype(dy->dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported dy dtype");
+    const size_t sbytes = static_cast<size_t>(B) * H * D * 2 * D * sizeof(float);
+    if (dstate_in && ((state_in && overlap(dstate_in, sbytes, state_in, sbytes)) ||
+                      (dstate_out && overlap(dstate_in, sbytes, dstate_out, sbytes))))
+        return fail(PRIME_ERR_ALIAS, "dstate_in overlaps state_in or dstate_out");
+    g.step = 1;
+    g.q_sl = g.k_sl = g.v_sl = 0;
+    g.dy = dy->data; g.dt_dy = dy->dtype; g.dy_sb = dy->stride_b; g.dy_sh = dy->stride_h; g.dy_sl = 0;
+    g.dstate_out = dstate_out;
+    g.dq = dq; g.dk = dk; g.dv = dv; g.dbeta = dbeta; g.dalpha = dalpha; g.dstate_in = dstate_in;
+    return check_hip(prime::launch_delta_gen_step_backward(g, static_cast<hipStream_t>(stream)),
+                     "delta step backward launch");
+}
+
 int prime_delta_decode_step(const prime_tensor_t *q, const prime_tensor_t *k, const prime_tensor_t *v,
                             const float *beta, const float *alpha, int B, int H, int H_kv, int D,
                             float feat_eps, float bound, const float *state_in, float *state_out,

@@ -367,6 +367,135 @@ __global__ __launch_bounds__(kGW) void delta_gen_backward_kernel(const DeltaGenA
     }
 }
 
+// Backward of the decode step's form (one token, L == 1; chunked_delta_prime.py:
+// 140-176): with E = v - S phi, X = alpha S + beta E phi^T, S' = s X (s the
+// Lyapunov scale min(1, bound / (|X|_F + 1e-6))) and y = S' psi, given dy and
+// dS' (the next state's adjoint):
+//   G = dS' + dy psi^T;  dpsi = S'^T dy;  dX = s G - [s <= 1] bound <G, X> X /
+//   ((|X| + 1e-6)^2 |X|);  g = dX phi;  dv = beta g;  dbeta = g . E;
+//   dalpha = <dX, S> (the step uses alpha unclamped);  dphi = dX^T (beta E) -
+//   S^T (beta g);  dS = alpha dX - (beta g) phi^T;
+// then dq and dk through the feature maps as in the prefill's backward.  One
+// wavefront per (sequence, head), lane j < D owning row j; fp32 throughout.
+template <int MD>
+__global__ __launch_bounds__(kGW) void delta_gen_step_backward_kernel(const DeltaGenArgs a) {
+    __shared__ float ps[1][kFP], pf[1][kFP], sv[1][kVP], sdy[1][kVP];
+    __shared__ float red[kGW][kFP];    // per-lane contributions to a feature-wide sum
+    __shared__ float rdp[2][2 * kGW];  // reduced dpsi, dphi
+    __shared__ float sb[1], sa[1], sn1[1], sn2[1];
+    const int lane = threadIdx.x, bh = blockIdx.x;
+    const int b = bh / a.H, h = bh - b * a.H, hk = h / a.group, D = a.D, P = 2 * D;
+    const bool row = lane < D;
+    const size_t so = static_cast<size_t>(bh) * D * P + static_cast<size_t>(lane) * P;
+    delta_gen_stage(a, b, h, hk, 0, 1, ps, pf, sv, sdy, sb, sa, sn1, sn2, lane);
+    float S[2 * MD], X[2 * MD], G[2 * MD];
+#pragma unroll
+    for (int f = 0; f < 2 * MD; ++f) S[f] = (f < P && row && a.state_in) ? a.state_in[so + f] : 0.f;
+    // the forward: E, X and the scale
+    float pred = 0.f;
+#pragma unroll
+    for (int f = 0; f < 2 * MD; ++f)
+        if (f < P) pred = fmaf(S[f], pf[0][f], pred);
+    const float e = row ? sv[0][lane] - pred : 0.f;
+    const float be = sb[0], al = sa[0], w = be * e;
+    float n2 = 0.f;
+#pragma unroll
+    for (int f = 0; f < 2 * MD; ++f) {
+        X[f] = f < P ? fmaf(w, pf[0][f], al * S[f]) : 0.f;
+        n2 = fmaf(X[f], X[f], n2);
+    }
+    float sc = 1.f, nrm = 0.f, den = 1.f;
+    if (a.bound > 0.f) {
+        nrm = sqrtf(wave_sum(n2));
+        den = nrm + 1e-6f;
+        sc = fminf(a.bound / den, 1.0f);
+    }
+    // the adjoint of S' with the readout's term; dpsi
+    const float dyj = row ? sdy[0][lane] : 0.f;
+    float gx = 0.f;
+#pragma unroll
+    for (int f = 0; f < 2 * MD; ++f)
+        if (f < P) {
+            G[f] = ((a.dstate_out && row) ? a.dstate_out[so + f] : 0.f) + dyj * ps[0][f];
+            red[lane][f] = sc * X[f] * dyj;
+            gx = fmaf(G[f], X[f], gx);
+        } else {
+            G[f] = 0.f;
+        }
+    __syncthreads();
+    for (int f = lane; f < P; f += kGW) {
+        float t = 0.f;
+        for (int j = 0; j < D; ++j) t += red[j][f];
+        rdp[0][f] = t;
+    }
+    __syncthreads();
+    // through the clamp (the identity where bound / (|X| + 1e-6) > 1)
+    if (a.bound > 0.f && a.bound / den <= 1.0f) {
+        const float kx = nrm > 0.f ? a.bound * wave_sum(gx) / (den * den * nrm) : 0.f;
+#pragma unroll
+        for (int f = 0; f < 2 * MD; ++f) G[f] = sc * G[f] - kx * X[f];
+    }
+    // through X = alpha S + (beta E) phi^T and E = v - S phi
+    float gj = 0.f, da = 0.f;
+#pragma unroll
+    for (int f = 0; f < 2 * MD; ++f)
+        if (f < P) {
+            gj = fmaf(G[f], pf[0][f], gj);
+            da = fmaf(G[f], S[f], da);
+        }
+    const float de = row ? be * gj : 0.f;
+#pragma unroll
+    for (int f = 0; f < 2 * MD; ++f)
+        if (f < P) red[lane][f] = G[f] * w - de * S[f];
+    __syncthreads();
+    for (int f = lane; f < P; f += kGW) {
+        float t = 0.f;
+        for (int j = 0; j < D; ++j) t += red[j][f];
+        rdp[1][f] = t;
+    }
+    __syncthreads();
+    const float dbeta = wave_sum(row ? gj * e : 0.f);
+    const float dal = wave_sum(row ? da : 0.f);
+    if (lane == 0) {
+        a.dbeta[bh] = dbeta;
+        a.dalpha[bh] = dal;
+    }
+    const size_t go = static_cast<size_t>(bh) * D;
+    if (row) {
+        a.dv[go + lane] = de;
+        if (a.dstate_in) {
+#pragma unroll
+            for (int f = 0; f < 2 * MD; ++f)
+                if (f < P) a.dstate_in[so + f] = fmaf(-de, pf[0][f], al * G[f]);
+        }
+    }
+    // features: dq from dpsi, dk through the two normalisations
+    float ki = 0.f, u1 = 0.f, u2 = 0.f, f1 = 0.f, f2 = 0.f;
+    const float n1 = sn1[0], nn2 = sn2[0];
+    const float m1 = fmaxf(n1, a.feat_eps), m2 = fmaxf(nn2, a.feat_eps);
+    if (row) {
+        const float qi = ps[0][lane];
+        ki = load_elem(a.k, b * a.k_sb + hk * a.k_sh + lane, a.dt_k);
+        u1 = rdp[1][lane];
+        u2 = rdp[1][D + lane] / kRsqrt2Div;
+        f1 = ki / m1;
+        f2 = ki * ki / m2;
+        a.dq[go + lane] = rdp[0][lane] + kRsqrt2Div * qi * rdp[0][D + lane];
+    }
+    const float dot1 = wave_sum(f1 * u1), dot2 = wave_sum(f2 * u2);
+    if (row) {
+        const float dk1 = n1 >= a.feat_eps ? (u1 - f1 * dot1) / n1 : u1 / a.feat_eps;
+        const float dx2 = nn2 >= a.feat_eps ? (u2 - f2 * dot2) / nn2 : u2 / a.feat_eps;
+        a.dk[go + lane] = dk1 + 2.0f * ki * dx2;
+    }
+}
+
+hipError_t launch_delta_gen_step_backward(const DeltaGenArgs &a, hipStream_t stream) {
+    if (a.D <= 32) hipLaunchKernelGGL(delta_gen_step_backward_kernel<32>, dim3(a.B * a.H), dim3(kGW), 0, stream, a);
+    else hipLaunchKernelGGL(delta_gen_step_backward_kernel<64>, dim3(a.B * a.H), dim3(kGW), 0, stream, a);
+    return hipGetLastError();
+}
+
 size_t delta_gen_backward_ws_bytes(int B, int H, int L, int D, int chunk) {
     const size_t NC = (static_cast<size_t>(L) + chunk - 1) / chunk;
     const size_t DP = static_cast<size_t>(D) * 2 * D;

@@ -349,6 +349,7 @@ struct DeltaGenArgs {
 constexpr int kDeltaGenMaxD = 64;
 hipError_t launch_delta_gen_forward(const DeltaGenArgs &a, hipStream_t stream);
 hipError_t launch_delta_gen_backward(const DeltaGenArgs &a, hipStream_t stream);
+hipError_t launch_delta_gen_step_backward(const DeltaGenArgs &a, hipStream_t stream);
 size_t delta_gen_backward_ws_bytes(int B, int H, int L, int D, int chunk);
 
 // One delta-rule decode step (delta.hip).

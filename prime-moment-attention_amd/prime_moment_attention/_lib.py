@@ -33,7 +33,8 @@ EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_
            "prime_selective_prefill_qknorm", "prime_accumulate_noalloc", "prime_selective_prefill_backward",
            "prime_selective_prefill_backward_workspace_size", "prime_hbm_stream",
            "prime_frag_rows", "prime_pack_frag", "prime_linear_frag_workspace_size", "prime_linear_frag",
-           "prime_delta_prefill_backward", "prime_delta_prefill_backward_workspace_size")
+           "prime_delta_prefill_backward", "prime_delta_prefill_backward_workspace_size",
+           "prime_delta_decode_step_backward")
 
 # bytes of the fixed device scratch behind prime_accumulate_noalloc
 NOALLOC_SCRATCH_BYTES = 32 << 20
@@ -105,6 +106,9 @@ def load() -> ctypes.CDLL:
     L.prime_delta_decode_step.argtypes = [P(PrimeTensor)] * 3 + [fp, fp] + [ctypes.c_int] * 4 + [
         ctypes.c_float] * 2 + [fp, fp, P(PrimeTensor), fp]
     L.prime_delta_decode_step.restype = ctypes.c_int
+    L.prime_delta_decode_step_backward.argtypes = [P(PrimeTensor)] * 3 + [fp, fp] + [ctypes.c_int] * 4 + [
+        ctypes.c_float] * 2 + [fp, P(PrimeTensor)] + [fp] * 7 + [fp]
+    L.prime_delta_decode_step_backward.restype = ctypes.c_int
     L.prime_decode_step_qknorm.argtypes = [P(PrimeTensor)] * 3 + [ctypes.c_int] * 4 + [
         ctypes.c_void_p, ctypes.c_float, P(PrimeQkNorm), P(PrimeState), P(PrimeState), P(PrimeTensor), ctypes.c_void_p]
     L.prime_decode_step_qknorm.restype = ctypes.c_int
@@ -909,6 +913,41 @@ def delta_decode_step(q, k, v, beta, alpha, feat_eps: float, bound: float, state
                                         B, H, Hkv, D, float(feat_eps), float(bound), ptr(state_in), ptr(state_out),
                                         ctypes.byref(yd), _stream(q.device))
     _check(rc, "prime_delta_decode_step")
+
+
+def delta_decode_step_backward(q, k, v, beta, alpha, feat_eps: float, bound: float, state_in, dy, dstate_out):
+    """Gradients of one delta-rule decode step (prime_delta_decode_step_backward)
+    for its inputs: returns (dq [B,H,D], dk, dv [B,Hkv,D] summed over each group
+    of query heads, dbeta, dalpha [B,H], dstate_in [B,H,D,2D] or None when
+    state_in is None), all fp32."""
+    _dev_check(q, k, v, dy)
+    B, H, D = q.shape
+    Hkv = k.shape[1]
+    _shape(k, (B, Hkv, D), "k")
+    _shape(v, (B, Hkv, D), "v")
+    _shape(dy, (B, H, D), "dy")
+    _gate(beta, B, H, 1, "beta")
+    _gate(alpha, B, H, 1, "alpha")
+    _check_delta_state(state_in, B, H, D, "state_in")
+    _check_delta_state(dstate_out, B, H, D, "dstate_out")
+    f32 = dict(device=q.device, dtype=torch.float32)
+    dq = torch.empty(B, H, D, **f32)
+    dk = torch.empty(B, H, D, **f32)
+    dv = torch.empty(B, H, D, **f32)
+    dbeta = torch.empty(B, H, **f32)
+    dalpha = torch.empty(B, H, **f32)
+    dstate = torch.empty(B, H, D, 2 * D, **f32) if state_in is not None else None
+    qd, kd, vd, yd = tensor_desc(q, False), tensor_desc(k, False), tensor_desc(v, False), tensor_desc(dy, False)
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    rc = load().prime_delta_decode_step_backward(
+        ctypes.byref(qd), ctypes.byref(kd), ctypes.byref(vd), ptr(beta), ptr(alpha), B, H, Hkv, D, float(feat_eps),
+        float(bound), ptr(state_in), ctypes.byref(yd), ptr(dstate_out), ptr(dq), ptr(dk), ptr(dv), ptr(dbeta),
+        ptr(dalpha), ptr(dstate), _stream(q.device))
+    _check(rc, "prime_delta_decode_step_backward")
+    if Hkv != H:
+        dk = dk.view(B, Hkv, H // Hkv, D).sum(2)
+        dv = dv.view(B, Hkv, H // Hkv, D).sum(2)
+    return dq, dk, dv, dbeta, dalpha, dstate
 
 
 def timer_enable(*kernels: int) -> None:

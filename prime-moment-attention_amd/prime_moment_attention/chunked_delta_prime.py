@@ -62,6 +62,35 @@ class _DeltaPrefillFn(torch.autograd.Function):
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dbeta, dalpha, dstate, None, None, None, None, None)
 
 
+class _DeltaStepFn(torch.autograd.Function):
+    """The delta-rule decode step (one token) with its HIP backward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, alpha, s_in, feat_eps, bound, y_dtype):
+        B, H, D = q.shape
+        y = torch.empty(B, H, D, device=q.device, dtype=y_dtype)
+        s_out = torch.empty(B, H, D, 2 * D, device=q.device, dtype=torch.float32)
+        _lib.delta_decode_step(q, k, v, beta, alpha, feat_eps, bound, s_in, s_out, y)
+        ctx.save_for_backward(q, k, v, beta, alpha, s_in)
+        ctx.consts = (feat_eps, bound)
+        return y, s_out
+
+    @staticmethod
+    def backward(ctx, dy, ds_out):
+        q, k, v, beta, alpha, s_in = ctx.saved_tensors
+        feat_eps, bound = ctx.consts
+        if dy is None:
+            dy = torch.zeros(q.shape, device=q.device, dtype=torch.float32)
+        dy = dy.contiguous()
+        if dy.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            dy = dy.float()
+        ds = ds_out.contiguous().float() if ds_out is not None else None
+        dq, dk, dv, dbeta, dalpha, dstate = _lib.delta_decode_step_backward(q, k, v, beta, alpha, feat_eps, bound,
+                                                                              s_in, dy, ds)
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dbeta.view_as(beta), dalpha.view_as(alpha), dstate,
+                None, None, None)
+
+
 class ChunkedGatedDeltaPrimeAttention(nn.Module):
     def __init__(self, hidden_size: int, num_heads: int, head_dim: int, num_kv_heads: Optional[int] = None,
                  chunk_size: int = 64, decay: float = 0.9995, use_qk_norm: bool = True,
@@ -125,7 +154,7 @@ class ChunkedGatedDeltaPrimeAttention(nn.Module):
         B, L, _ = hidden_states.shape
         H, D = self.num_heads, self.head_dim
         dtype, dev = hidden_states.dtype, hidden_states.device
-        if torch.is_grad_enabled() and L > 1 and (hidden_states.requires_grad or
+        if torch.is_grad_enabled() and (hidden_states.requires_grad or
                                                   any(p.requires_grad for p in self.parameters()) or
                                                   (state is not None and state.requires_grad)):
             return self._forward_train(hidden_states, state, return_state)
@@ -149,7 +178,7 @@ class ChunkedGatedDeltaPrimeAttention(nn.Module):
             y = torch.empty(B, H, L, D, device=dev, dtype=y_dtype)
             _lib.delta_prefill(q, k, v, beta, alpha, self.decay, self.eps, self.lyapunov_bound, s_in, y, s_out,
                                chunk=self.chunk_size)
-        y = no_backward("the delta-rule PRIME decode step", y, q, k, v, beta, alpha, s_in)
+        y = no_backward("the delta-rule PRIME (inference path)", y, q, k, v, beta, alpha, s_in)
         y = y.to(dtype).transpose(1, 2).reshape(B, L, H * D)
         return self.o_proj(y), (s_out if return_state else None)
 
@@ -175,7 +204,13 @@ class ChunkedGatedDeltaPrimeAttention(nn.Module):
         s_in = None
         if state is not None:
             s_in = state.to(device=dev, dtype=torch.float32).reshape(B, H, D, 2 * D).contiguous()
-        y, s_out = _DeltaPrefillFn.apply(q, k, v, beta, alpha, s_in, self.decay, self.eps, self.lyapunov_bound,
-                                         y_dtype, self.chunk_size)
+        if L == 1:
+            # the step branch (chunked_delta_prime.py:140-176) and its backward
+            y, s_out = _DeltaStepFn.apply(q[:, :, 0], k[:, :, 0], v[:, :, 0], beta.contiguous(),
+                                          alpha.contiguous(), s_in, self.eps, self.lyapunov_bound, y_dtype)
+            y = y.unsqueeze(2)
+        else:
+            y, s_out = _DeltaPrefillFn.apply(q, k, v, beta, alpha, s_in, self.decay, self.eps, self.lyapunov_bound,
+                                             y_dtype, self.chunk_size)
         y = y.to(dtype).transpose(1, 2).reshape(B, L, H * D)
         return self.o_proj(y), (s_out if return_state else None)

@@ -1,11 +1,13 @@
 """TEST INFRASTRUCTURE: a torch restatement of the chunked gated delta-rule
-PRIME forward (chunked_delta_prime.py:73-87 features, :177-283 chunk loop),
+PRIME forward (chunked_delta_prime.py:73-87 features, :177-283 chunk loop,
+and the one-token step branch :140-176),
 written as differentiable torch ops so that torch autograd (in fp64, on the
 CPU) gives the reference gradients the HIP backward is checked against.  It is
 pinned to the fp64 C oracle (oracle_delta_chunked, itself pinned by the
 reference's own vectors in tests/golden/ref_delta.npz) by
-tests/test_oracle.py::test_delta_torch_restatement_matches_oracle, and its
-autograd by central differences there.
+tests/test_oracle.py::test_delta_torch_restatement_matches_oracle (the step:
+test_delta_step_torch_restatement_matches_oracle, against oracle_delta_step),
+and its autograd by central differences there.
 
 q is pre-scaled (the module multiplies by 1/sqrt(D) before the features);
 beta, alpha [B, H, L] per token and head; pad tokens of the last chunk carry
@@ -67,3 +69,19 @@ def delta_chunked(q, k, v, beta, alpha, decay_pad, eps=1e-5, bound=25.0, chunk=6
             S = S * torch.clamp(bound / (nrm + 1e-6), max=1.0)
     y = torch.stack(ys, dim=2).reshape(B, H, n * C, D)[:, :, :L]
     return y, S
+
+
+def delta_step(q, k, v, beta, alpha, eps=1e-5, bound=25.0, state=None):
+    """The L == 1 branch (chunked_delta_prime.py:140-176): q, k, v [B, H, D]
+    (q pre-scaled), beta, alpha [B, H]; predicts with the undecayed state,
+    updates with alpha unclamped, clamps before the readout.  Returns
+    y [B, H, D] and the new state [B, H, D, 2D]."""
+    B, H, D = q.shape
+    psi, phi = features(q, k, eps)
+    S = torch.zeros(B, H, D, 2 * D, dtype=q.dtype) if state is None else state
+    e = v - torch.einsum("bhde,bhe->bhd", S, phi)
+    S = alpha[..., None, None] * S + torch.einsum("bhd,bhe->bhde", beta[..., None] * e, phi)
+    if bound > 0.0:
+        nrm = torch.linalg.norm(S, dim=(-2, -1), keepdim=True)
+        S = S * torch.clamp(bound / (nrm + 1e-6), max=1.0)
+    return torch.einsum("bhde,bhe->bhd", S, psi), S

@@ -709,6 +709,64 @@ def test_delta_torch_restatement_matches_oracle(L, bound, D, C):
         assert float(S.norm(dim=(-2, -1)).max()) <= bound * (1 + 1e-9)
 
 
+@pytest.mark.parametrize("bound,D", [(25.0, 64), (0.7, 64), (1.0, 16), (25.0, 7)])
+def test_delta_step_torch_restatement_matches_oracle(bound, D):
+    """tests/delta_ref.py::delta_step computes what oracle_delta_step computes
+    (the L == 1 branch, chunked_delta_prime.py:140-176): y and the new state,
+    with an incoming state, the clamp engaged (bound below the state's norm)
+    or not."""
+    import torch
+    import delta_ref as R
+    B, H = 2, 3
+    q, k, v, beta, alpha, state = (t[:, :, 0] if t.dim() == 4 and i < 3 else t[..., 0] if i in (3, 4) else t
+                                   for i, t in enumerate(_delta_case(B, H, 1, D, 11 + D, bound)))
+    y, S = R.delta_step(q, k, v, beta, alpha, 1e-5, bound, state)
+    psi, phi = O.delta_features(q.reshape(B * H, 1, D).numpy(), k.reshape(B * H, 1, D).numpy(), eps=1e-5)
+    yo, So = O.delta_step(psi[:, 0], phi[:, 0], v.reshape(B * H, D).numpy(), beta.reshape(-1).numpy(),
+                          alpha.reshape(-1).numpy(), bound=bound, state=state.reshape(B * H, D, 2 * D).numpy())
+    assert O.rel_err(y.reshape(B * H, D).numpy(), yo) < 1e-12
+    assert O.rel_err(S.reshape(B * H, D, 2 * D).numpy(), So) < 1e-12
+    if bound < 25.0:
+        assert float(S.norm(dim=(-2, -1)).max()) <= bound * (1 + 1e-9)
+
+
+@pytest.mark.parametrize("bound", [25.0, 0.6])
+def test_delta_step_torch_autograd_matches_central_differences(bound):
+    """fp64 autograd of the step restatement against central differences of
+    the loss along random directions, for every input (q, k, v, beta, alpha,
+    the incoming state), with (bound 0.6) the clamp active."""
+    import torch
+    import delta_ref as R
+    B, H, D = 2, 1, 8
+    xs = [t[:, :, 0] if i < 3 else t[..., 0] if i in (3, 4) else t
+          for i, t in enumerate(_delta_case(B, H, 1, D, 5, bound))]
+    g = torch.Generator().manual_seed(19)
+    ry = torch.randn(B, H, D, generator=g, dtype=torch.float64)
+    rs = torch.randn(B, H, D, 2 * D, generator=g, dtype=torch.float64)
+
+    def loss(*a):
+        y, S = R.delta_step(*a[:5], 1e-5, bound, a[5])
+        return (y * ry).sum() + (S * rs).sum()
+
+    for t in xs:
+        t.requires_grad_(True)
+    grads = torch.autograd.grad(loss(*xs), xs)
+    with torch.no_grad():
+        if bound < 25.0:
+            _, S = R.delta_step(*xs[:5], 1e-5, 0.0, xs[5])
+            assert float(S.norm(dim=(-2, -1)).min()) > bound  # the clamp is active
+        for i, (x, gr) in enumerate(zip(xs, grads)):
+            u = torch.randn(x.shape, generator=g, dtype=torch.float64)
+            h = 1e-6
+            xp = [t.detach().clone() for t in xs]
+            xm = [t.detach().clone() for t in xs]
+            xp[i] += h * u
+            xm[i] -= h * u
+            fd = (loss(*xp) - loss(*xm)) / (2 * h)
+            an = (gr * u).sum()
+            assert abs(float(fd - an)) <= 1e-6 * max(1.0, abs(float(an))), (i, float(fd), float(an))
+
+
 @pytest.mark.parametrize("bound", [25.0, 0.6])
 def test_delta_torch_autograd_matches_central_differences(bound):
     """fp64 autograd of the restatement against central differences of the
