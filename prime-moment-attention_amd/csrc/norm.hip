@@ -186,15 +186,16 @@ __global__ __launch_bounds__(256) void head_layernorm_kernel(const HeadNormArgs 
 }
 
 // Exact (erf) GELU, y = x * 0.5 * (1 + erf(x / sqrt(2))) in fp32, rounded once to
-// the dtype: the MLP activation of primelm_50m.py:64 (nn.GELU()).  16 bytes per
-// lane per access, four accesses in flight per lane; the elements past the last
-// whole 16-byte group go to one lane each.  y may be x.
+// the dtype: the MLP activation of primelm_50m.py:64 (nn.GELU()).  Workgroup b
+// owns the 16-byte groups [1024 b, 1024 (b + 1)), four per lane at a stride of
+// 256 groups, all four loads issued before the first store (measured faster
+// than a grid-stride loop over a capped grid); the elements past the last whole
+// 16-byte group go to one lane each of workgroup 0.  y may be x.
+constexpr int kGeluGroups = 4;  // 16-byte groups per lane
 template <int DT>
 __global__ __launch_bounds__(256) void gelu_kernel(const void *x, void *y, int64_t n) {
     constexpr int E = DT == PRIME_F32 ? 4 : 8;  // elements per 16 bytes
-    constexpr int es = DT == PRIME_F32 ? 4 : 2;
     const int64_t groups = n / E;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     auto act = [](float v) { return v * 0.5f * (1.0f + erff(v * 0.70710678118654752f)); };
     auto conv = [&](uint4 r) {
         if constexpr (DT == PRIME_F32) {
@@ -213,18 +214,17 @@ __global__ __launch_bounds__(256) void gelu_kernel(const void *x, void *y, int64
     };
     const uint4 *xs = static_cast<const uint4 *>(x);
     uint4 *ys = static_cast<uint4 *>(y);
-    int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    for (; g + 3 * stride < groups; g += 4 * stride) {
-        uint4 r[4];
+    const int64_t g0 = static_cast<int64_t>(blockIdx.x) * 256 * kGeluGroups + threadIdx.x;
+    uint4 r[kGeluGroups];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) r[u] = xs[g + u * stride];
+    for (int u = 0; u < kGeluGroups; ++u)
+        if (g0 + 256 * u < groups) r[u] = xs[g0 + 256 * u];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) ys[g + u * stride] = conv(r[u]);
-    }
-    for (; g < groups; g += stride) ys[g] = conv(xs[g]);
+    for (int u = 0; u < kGeluGroups; ++u)
+        if (g0 + 256 * u < groups) ys[g0 + 256 * u] = conv(r[u]);
     // the tail: fewer than E elements
-    const int64_t t = groups * E + static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (t < n) {
+    const int64_t t = groups * E + threadIdx.x;
+    if (blockIdx.x == 0 && t < n) {
         if constexpr (DT == PRIME_F32) {
             static_cast<float *>(y)[t] = act(static_cast<const float *>(x)[t]);
         } else {
@@ -232,15 +232,14 @@ __global__ __launch_bounds__(256) void gelu_kernel(const void *x, void *y, int64
             static_cast<uint16_t *>(y)[t] = static_cast<uint16_t>(Group<DT>::to_b(act(Group<DT>::to_f(b))));
         }
     }
-    (void)es;
 }
 
 hipError_t launch_gelu(const void *x, void *y, int64_t n, int dt, hipStream_t stream) {
-    const int E = dt == PRIME_F32 ? 4 : 8;
-    const int64_t groups = n / E;
-    // four 16-byte groups per lane per pass; at least one block for the tail
-    const int64_t want = (groups + 4 * 256 - 1) / (4 * 256);
-    const dim3 grid(static_cast<unsigned>(want < 1 ? 1 : (want > 4096 ? 4096 : want))), block(256);
+    const int64_t groups = n / (dt == PRIME_F32 ? 4 : 8);
+    const int64_t per = 256 * kGeluGroups;
+    const int64_t blocks = (groups + per - 1) / per;
+    if (blocks >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<unsigned>(blocks < 1 ? 1 : blocks)), block(256);
     if (dt == PRIME_BF16) hipLaunchKernelGGL(gelu_kernel<PRIME_BF16>, grid, block, 0, stream, x, y, n);
     else if (dt == PRIME_F16) hipLaunchKernelGGL(gelu_kernel<PRIME_F16>, grid, block, 0, stream, x, y, n);
     else hipLaunchKernelGGL(gelu_kernel<PRIME_F32>, grid, block, 0, stream, x, y, n);
