@@ -72,6 +72,36 @@ def test_partial_state_overlap_rejected():
     assert rc == -5 and "overlaps" in _lib.last_error()
 
 
+def test_gelu_and_delta_step_backward_validate_before_device_work():
+    """prime_gelu and prime_delta_decode_step_backward reject null, misaligned,
+    overlapping and out-of-range arguments with their error codes (no launch)."""
+    L = _lib.load()
+    assert L.prime_gelu(None, ctypes.c_void_p(16), 8, _lib.PRIME_BF16, None) == -1
+    assert L.prime_gelu(ctypes.c_void_p(16), ctypes.c_void_p(16), -1, _lib.PRIME_BF16, None) == -1
+    assert L.prime_gelu(ctypes.c_void_p(16), ctypes.c_void_p(16), 8, 9, None) == -3
+    assert L.prime_gelu(ctypes.c_void_p(18), ctypes.c_void_p(48), 8, _lib.PRIME_BF16, None) == -4
+    assert "aligned" in _lib.last_error()
+    assert L.prime_gelu(ctypes.c_void_p(16), ctypes.c_void_p(32), 64, _lib.PRIME_BF16, None) == -5
+    assert "overlaps" in _lib.last_error()
+    assert L.prime_gelu(ctypes.c_void_p(16), ctypes.c_void_p(16), 0, _lib.PRIME_BF16, None) == 0  # nothing to do
+    t = _lib.PrimeTensor(16, _lib.PRIME_BF16, 0, 0, 0, 0)
+    b = ctypes.byref
+    p = ctypes.c_void_p(4096)
+    rc = L.prime_delta_decode_step_backward(b(t), b(t), b(t), p, p, 1, 1, 1, 64, 1e-5, 25.0, None, b(t), None,
+                                            None, p, p, p, p, None, None)
+    assert rc == -1 and "null" in _lib.last_error()
+    rc = L.prime_delta_decode_step_backward(b(t), b(t), b(t), p, p, 1, 1, 1, 65, 1e-5, 25.0, None, b(t), None,
+                                            p, p, p, p, p, None, None)
+    assert rc == -2 and "head dim" in _lib.last_error()
+    rc = L.prime_delta_decode_step_backward(b(t), b(t), b(t), p, p, 1, 3, 2, 64, 1e-5, 25.0, None, b(t), None,
+                                            p, p, p, p, p, None, None)
+    assert rc == -1  # H not a multiple of H_kv
+    s_in = ctypes.c_void_p(1 << 20)
+    rc = L.prime_delta_decode_step_backward(b(t), b(t), b(t), p, p, 1, 1, 1, 64, 1e-5, 25.0, s_in, b(t), None,
+                                            p, p, p, p, p, ctypes.c_void_p((1 << 20) + 64), None)
+    assert rc == -5 and "overlaps" in _lib.last_error()
+
+
 def test_host_wrappers_refuse_cpu_tensors():
     import torch
     x = torch.zeros(1, 1, 64)
