@@ -365,16 +365,20 @@ bool launch_kpw(const FragArgs &a, hipStream_t s) {
 
 // Tile of the workgroup: 32 x 32 outputs where that gives at least half a
 // workgroup per CU (the decode step's projections at 256 rows: 192 to 768
-// workgroups, several resident per CU), 32 x 16 otherwise.  (Measured at 256
-// rows: 64 x 64 tiles, one workgroup per CU, are no faster for the q/k/v
-// projection and slower for the up projection.)
+// workgroups, several resident per CU), 32 x 16 where that does, 16 x 16
+// otherwise (the o and down projections at 32 rows: 96 workgroups instead of
+// 48; the B = 32 step 0.350 -> 0.336 ms).  (Measured at 256 rows: 64 x 64
+// tiles, one workgroup per CU, are no faster for the q/k/v projection and
+// slower for the up projection.)
 void frag_tile(int Mp, int N, int K, int *MT, int *NT) {
     (void)K;
     const int64_t cus = device_cus();
     if (Mp % 32 == 0 && N % 32 == 0 && static_cast<int64_t>(Mp / 32) * (N / 32) >= cus / 2) {
         *MT = 2; *NT = 2;
-    } else {
+    } else if (Mp % 32 == 0 && static_cast<int64_t>(Mp / 32) * (N / 16) >= cus / 2) {
         *MT = 2; *NT = 1;
+    } else {
+        *MT = 1; *NT = 1;
     }
 }
 
@@ -427,6 +431,7 @@ hipError_t launch_linear_frag(const FragArgs &a, hipStream_t s) {
     if (a.persistent) ok = a.mt == 4 ? launch_lm<4, 2>(a, s) : launch_lm<2, 1>(a, s);
     else if (a.mt == 2 && a.nt == 2) ok = launch_kpw<2, 2>(a, s);
     else if (a.mt == 2 && a.nt == 1) ok = launch_kpw<2, 1>(a, s);
+    else if (a.mt == 1 && a.nt == 1) ok = launch_kpw<1, 1>(a, s);
     else ok = false;
     if (!ok) return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();
