@@ -6,9 +6,11 @@ The ChunkedPrimeSSD parity test follows the reference's only numeric test,
 tests/test_chunked_ssd_parity.py:13-42 (weights copied from a
 PrimeMomentAttention into a ChunkedPrimeSSD, B=2, L=256 so the module takes
 its dense branch, H=4, decay 0.9995, LayerNorm QK-norm; outputs within 1e-5,
-states within 2e-3), at head_dim 64 (the only head size these kernels take;
-the reference test uses 32).  Both classes are then checked against a float64
-composition of their own weights through the oracle recurrence."""
+states within 2e-3), at head_dim 64 (the reference test's own head_dim 32
+runs in tests/test_gpu_generic_d.py).  Both classes are then checked against a
+float64 composition of their own weights through the oracle recurrence.  The
+module's inference projection (q, k and v as one GEMM over stacked weights) is
+checked against the three nn.Linear calls autograd records through."""
 import numpy as np
 import pytest
 import torch
@@ -145,3 +147,28 @@ def test_cache_feeds_decode_loop():
     assert len(s0) == 6 and s0[3].shape == (B, H, 1)
     cache.reset()
     assert cache.get_state(0) is None and cache.get_seq_length() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_stacked_qkv_projection_matches_three_linears(dtype):
+    """attention.py:83-85: inference projects q, k and v with one GEMM over the
+    stacked weights; the result is that of the three projections (the same dot
+    products), the stacked copy follows in-place weight updates, and training
+    keeps the three nn.Linear calls."""
+    torch.manual_seed(11)
+    m = PrimeMomentAttention(hidden_size=256, num_heads=4, head_dim=D, num_kv_heads=2, decay=0.999,
+                             use_qk_norm=True).to(dev(), dtype)
+    x = torch.randn(2, 300, 256, device=dev(), dtype=dtype)
+    tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+    for rep in range(2):
+        with torch.no_grad():
+            y_inf, st_inf = m(x, return_state=True)
+        assert m.__dict__.get("_qkv_cache") is not None
+        y_tr, st_tr = m(x, return_state=True)  # autograd records: three projections
+        assert y_tr.requires_grad
+        assert_close(to_np(y_inf), to_np(y_tr.detach()), tol)
+        assert_state_close(state_to_np(st_inf, 8, D), state_to_np(st_tr, 8, D), tol)
+        with torch.no_grad():
+            m.k_proj.weight.mul_(0.5)  # the next inference call restacks
+    y_tr.float().square().mean().backward()
+    assert m.q_proj.weight.grad is not None and m.v_proj.weight.grad is not None
