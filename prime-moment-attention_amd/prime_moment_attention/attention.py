@@ -36,6 +36,49 @@ def _same_storage(a, b) -> bool:
     return all(x.data_ptr() == y.data_ptr() for x, y in zip(a, b))
 
 
+def _stacked_qkv(mod: nn.Module) -> Optional[torch.Tensor]:
+    """The q, k and v weights of an attention module stacked into one
+    [(H + 2 Hk) D, hidden] matrix, so that inference projects with one GEMM
+    instead of three (the same products: each output column is the same dot
+    product).  Cached on the module outside its state dict and rebuilt when a
+    weight's storage or version counter changes; None while autograd records
+    through the weights (training keeps the three nn.Linear calls) or when the
+    three differ in dtype or device or carry a bias."""
+    lins = (mod.q_proj, mod.k_proj, mod.v_proj)
+    ws = tuple(m.weight for m in lins)
+    if torch.is_grad_enabled() and any(w.requires_grad for w in ws):
+        return None
+    if any(m.bias is not None for m in lins) or len({(w.dtype, w.device) for w in ws}) != 1:
+        return None
+    # the cache holds the weight tensors themselves, so their storage
+    # cannot be freed and reused by a new weight at the same address
+    key = tuple((w.data_ptr(), w._version) for w in ws)
+    cached = mod.__dict__.get("_qkv_cache")
+    if cached is not None and all(a is b for a, b in zip(cached[0], ws)) and cached[1] == key:
+        return cached[2]
+    w = torch.cat(ws, 0)
+    mod.__dict__["_qkv_cache"] = (ws, key, w)
+    return w
+
+
+def project_qkv(mod: nn.Module, hidden_states: torch.Tensor):
+    """q, k, v projections of [B, L, hidden] as [B, H(kv), L, D] views
+    (attention.py:83-85): one GEMM into [B, L, (H + 2 Hk) D] over the stacked
+    weights where _stacked_qkv allows it (q, k, v are then column ranges of
+    that result), else the module's three nn.Linear layers."""
+    B, L, _ = hidden_states.shape
+    H, Hk, D = mod.num_heads, mod.num_kv_heads, mod.head_dim
+    w = _stacked_qkv(mod)
+    if w is None:
+        return (mod.q_proj(hidden_states).view(B, L, H, D).transpose(1, 2),
+                mod.k_proj(hidden_states).view(B, L, Hk, D).transpose(1, 2),
+                mod.v_proj(hidden_states).view(B, L, Hk, D).transpose(1, 2))
+    qkv = torch.nn.functional.linear(hidden_states, w)
+    return (qkv[..., :H * D].view(B, L, H, D).transpose(1, 2),
+            qkv[..., H * D:(H + Hk) * D].view(B, L, Hk, D).transpose(1, 2),
+            qkv[..., (H + Hk) * D:].view(B, L, Hk, D).transpose(1, 2))
+
+
 class PrimeMomentAttention(nn.Module):
     def __init__(
         self,
@@ -76,47 +119,11 @@ class PrimeMomentAttention(nn.Module):
         """q (scaled), k, v as [B, H(kv), L, D] views (attention.py:83-101);
         normalize=False returns the raw projections (QK-norm and scale left
         to the decode kernel)."""
-        B, L, _ = hidden_states.shape
-        H, Hk, D = self.num_heads, self.num_kv_heads, self.head_dim
-        w = self._stacked_qkv()
-        if w is not None:
-            # one GEMM into [B, L, (H + 2 Hk) D]; q, k, v are column ranges of it
-            qkv = torch.nn.functional.linear(hidden_states, w)
-            q = qkv[..., :H * D].view(B, L, H, D).transpose(1, 2)
-            k = qkv[..., H * D:(H + Hk) * D].view(B, L, Hk, D).transpose(1, 2)
-            v = qkv[..., (H + Hk) * D:].view(B, L, Hk, D).transpose(1, 2)
-        else:
-            q = self.q_proj(hidden_states).view(B, L, H, D).transpose(1, 2)
-            k = self.k_proj(hidden_states).view(B, L, Hk, D).transpose(1, 2)
-            v = self.v_proj(hidden_states).view(B, L, Hk, D).transpose(1, 2)
+        q, k, v = project_qkv(self, hidden_states)
         if not normalize:
             return q, k, v
         self._normalize(q, k)
         return q, k, v
-
-    def _stacked_qkv(self) -> Optional[torch.Tensor]:
-        """The q, k and v weights stacked into one [(H + 2 Hk) D, hidden] matrix,
-        so that inference projects with one GEMM instead of three (the same
-        products: each output column is the same dot product).  Cached outside
-        the state dict and rebuilt when a weight's storage or version counter
-        changes; None while autograd records through the weights (training
-        keeps the three nn.Linear calls) or when the three differ in dtype or
-        device or carry a bias."""
-        lins = (self.q_proj, self.k_proj, self.v_proj)
-        ws = tuple(m.weight for m in lins)
-        if torch.is_grad_enabled() and any(w.requires_grad for w in ws):
-            return None
-        if any(m.bias is not None for m in lins) or len({(w.dtype, w.device) for w in ws}) != 1:
-            return None
-        # the cache holds the weight tensors themselves, so their storage
-        # cannot be freed and reused by a new weight at the same address
-        key = tuple((w.data_ptr(), w._version) for w in ws)
-        cached = self.__dict__.get("_qkv_cache")
-        if cached is not None and all(a is b for a, b in zip(cached[0], ws)) and cached[1] == key:
-            return cached[2]
-        w = torch.cat(ws, 0)
-        self.__dict__["_qkv_cache"] = (ws, key, w)
-        return w
 
     def _normalize(self, q: torch.Tensor, k: torch.Tensor) -> None:
         """QK-norm and the 1/sqrt(D) scale in place on the fresh projections

@@ -41,6 +41,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
+from .attention import project_qkv
 from .chunked_ssd import _prep, needs_grad
 
 
@@ -143,9 +144,7 @@ class PrimeSelectiveMomentAttention(nn.Module):
         H, D = self.num_heads, self.head_dim
         orig_dtype, dev = hidden_states.dtype, hidden_states.device
         y_dtype = orig_dtype if orig_dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
-        q = self.q_proj(hidden_states).view(B, L, H, D).transpose(1, 2)
-        k = self.k_proj(hidden_states).view(B, L, self.num_kv_heads, D).transpose(1, 2)
-        v = self.v_proj(hidden_states).view(B, L, self.num_kv_heads, D).transpose(1, 2)
+        q, k, v = project_qkv(self, hidden_states)
         tau = self.get_tau(dev).float().contiguous()
         beta = self.get_beta(dev).float().contiguous()
         if needs_grad(hidden_states, *self.parameters(), *(state or ())):

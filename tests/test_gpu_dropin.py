@@ -17,7 +17,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import oracle as O
-from prime_moment_attention import ChunkedPrimeSSD, PrimeMomentAttention, PrimeMomentCache
+from prime_moment_attention import ChunkedPrimeSSD, PrimeMomentAttention, PrimeMomentCache, PrimeSelectiveMomentAttention
 
 from gpu_util import TOL_BF16, TOL_F32, assert_close, assert_state_close, dev, state_to_np, to_np
 
@@ -149,15 +149,22 @@ def test_cache_feeds_decode_loop():
     assert cache.get_state(0) is None and cache.get_seq_length() == 0
 
 
+@pytest.mark.parametrize("selective", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_stacked_qkv_projection_matches_three_linears(dtype):
-    """attention.py:83-85: inference projects q, k and v with one GEMM over the
-    stacked weights; the result is that of the three projections (the same dot
-    products), the stacked copy follows in-place weight updates, and training
-    keeps the three nn.Linear calls."""
+def test_stacked_qkv_projection_matches_three_linears(dtype, selective):
+    """attention.py:83-85 (selective.py:358-360): inference projects q, k and v
+    with one GEMM over the stacked weights; the result is that of the three
+    projections autograd records through, the stacked copy follows in-place
+    weight updates, and training keeps the three nn.Linear calls."""
     torch.manual_seed(11)
-    m = PrimeMomentAttention(hidden_size=256, num_heads=4, head_dim=D, num_kv_heads=2, decay=0.999,
-                             use_qk_norm=True).to(dev(), dtype)
+    if selective:
+        m = PrimeSelectiveMomentAttention(hidden_size=256, num_heads=4, head_dim=D, num_kv_heads=2, decay=0.99)
+        with torch.no_grad():  # per-token decays that vary
+            m.delta_proj.weight.normal_(0.0, 0.05)
+    else:
+        m = PrimeMomentAttention(hidden_size=256, num_heads=4, head_dim=D, num_kv_heads=2, decay=0.999,
+                                 use_qk_norm=True)
+    m = m.to(dev(), dtype)
     x = torch.randn(2, 300, 256, device=dev(), dtype=dtype)
     tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
     for rep in range(2):
