@@ -54,7 +54,10 @@ def _stacked_qkv(mod: nn.Module) -> Optional[torch.Tensor]:
     # cannot be freed and reused by a new weight at the same address
     key = tuple((w.data_ptr(), w._version) for w in ws)
     cached = mod.__dict__.get("_qkv_cache")
-    if cached is not None and all(a is b for a, b in zip(cached[0], ws)) and cached[1] == key:
+    # (a copy made under inference_mode is rebuilt outside it: autograd could
+    # not save an inference tensor for a backward through hidden_states)
+    if (cached is not None and all(a is b for a, b in zip(cached[0], ws)) and cached[1] == key
+            and (not cached[2].is_inference() or torch.is_inference_mode_enabled())):
         return cached[2]
     w = torch.cat(ws, 0)
     mod.__dict__["_qkv_cache"] = (ws, key, w)

@@ -99,3 +99,32 @@ def test_base_to_selective_needs_a_config(tmp_path):
     torch.save({"model_state_dict": {}}, path)
     with pytest.raises(ValueError, match="no saved config"):
         PrimeForCausalLM.from_pretrained_base_to_selective(str(path))
+
+
+def test_stacked_qkv_cache_follows_weights_and_modes():
+    """The attention module's stacked q/k/v copy (one inference GEMM instead
+    of three, attention.py:83-85): rebuilt after an in-place weight update and
+    outside inference_mode when it was made inside it, absent while autograd
+    records through the weights; host logic only (no kernel runs)."""
+    from prime_moment_attention.attention import PrimeMomentAttention, _stacked_qkv
+    m = PrimeMomentAttention(64, 2, 32, num_kv_heads=1)
+    assert _stacked_qkv(m) is None  # weights require grad, grad mode on
+    with torch.no_grad():
+        w = _stacked_qkv(m)
+        assert w.shape == (64 + 2 * 32, 64) and _stacked_qkv(m) is w
+        assert torch.equal(w, torch.cat([m.q_proj.weight, m.k_proj.weight, m.v_proj.weight]))
+        m.v_proj.weight.mul_(2.0)
+        w2 = _stacked_qkv(m)
+        assert w2 is not w and torch.equal(w2[96:], m.v_proj.weight)
+    with torch.inference_mode():
+        assert _stacked_qkv(m) is w2  # an ordinary tensor serves inference_mode too
+        del m.__dict__["_qkv_cache"]
+        wi = _stacked_qkv(m)
+        assert wi.is_inference() and _stacked_qkv(m) is wi
+    for p in m.parameters():
+        p.requires_grad_(False)
+    wo = _stacked_qkv(m)  # grad mode on, frozen weights: usable, not an inference tensor
+    assert wo is not None and not wo.is_inference()
+    m.k_proj.bias = torch.nn.Parameter(torch.zeros(32), requires_grad=False)
+    with torch.no_grad():
+        assert _stacked_qkv(m) is None  # a bias: the three projections run
