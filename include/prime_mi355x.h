@@ -402,6 +402,19 @@ int prime_linear_fused(const void *x, const void *w, const void *r, void *y, int
  * (the module's QK LayerNorm and q scale applied to raw projections).
  * Replaces selective.py:384-409.
  */
+/*
+ * prime_selective_log_decay: the per-token log decays prime_selective_prefill
+ * takes, from the step-size pre-activations s = delta_proj(x): Delta =
+ * clamp(softplus(s), step_min, step_max), each stage rounded to step_dtype
+ * as the module's tensors are (selective.py:368), and
+ * log_decay[b, h, t] = -Delta / tau[h] (the exponent of selective.py:414-416's
+ * decay matrix per token), fp32 [B, H, L] contiguous.  s element (b, t, h)
+ * at step + b * step_sb + t * step_sl + h (elements of step_dtype); tau fp32
+ * [H]; log_decay must not overlap step or tau.
+ */
+int prime_selective_log_decay(const void *step, int step_dtype, int64_t step_sb, int64_t step_sl, const float *tau,
+                              float step_min, float step_max, int B, int H, int L, float *log_decay, void *stream);
+
 typedef struct prime_selective_gate {
     /* either l_t per (sequence, head), fp32 [B, H] contiguous ... */
     const float *decay;

@@ -304,6 +304,29 @@ int prime_gelu(const void *x, void *y, int64_t n, int dtype, void *stream) {
     return check_hip(prime::launch_gelu(x, y, n, dtype, static_cast<hipStream_t>(stream)), "gelu launch");
 }
 
+int prime_selective_log_decay(const void *step, int step_dtype, int64_t step_sb, int64_t step_sl, const float *tau,
+                              float step_min, float step_max, int B, int H, int L, float *log_decay, void *stream) {
+    g_err[0] = 0;
+    if (!step || !tau || !log_decay) return fail(PRIME_ERR_INVALID_ARG, "prime_selective_log_decay: null argument");
+    if (B <= 0 || H <= 0 || L <= 0 || step_sb < 0 || step_sl < 0)
+        return fail(PRIME_ERR_INVALID_ARG, "bad sizes B=%d H=%d L=%d step_sb=%lld step_sl=%lld", B, H, L,
+                    static_cast<long long>(step_sb), static_cast<long long>(step_sl));
+    if (!valid_dtype(step_dtype)) return fail(PRIME_ERR_UNSUPPORTED_DTYPE, "unsupported step dtype");
+    if (!(step_min > 0.f) || !(step_max >= step_min))
+        return fail(PRIME_ERR_INVALID_ARG, "step bounds must satisfy 0 < step_min <= step_max");
+    const int64_t es = elem_size(step_dtype);
+    if (reinterpret_cast<uintptr_t>(step) % es || (reinterpret_cast<uintptr_t>(tau) & 3) ||
+        (reinterpret_cast<uintptr_t>(log_decay) & 3))
+        return fail(PRIME_ERR_MISALIGNED, "step, tau or log_decay misaligned");
+    const size_t nout = static_cast<size_t>(B) * H * L * sizeof(float);
+    const size_t nstep = static_cast<size_t>((B - 1) * step_sb + (L - 1) * step_sl + H) * es;
+    if (overlap(log_decay, nout, step, nstep) || overlap(log_decay, nout, tau, static_cast<size_t>(H) * sizeof(float)))
+        return fail(PRIME_ERR_ALIAS, "log_decay overlaps step or tau");
+    return check_hip(prime::launch_selective_log_decay(step, step_dtype, step_sb, step_sl, tau, step_min, step_max, B,
+                                                       H, L, log_decay, static_cast<hipStream_t>(stream)),
+                     "selective log decay launch");
+}
+
 int prime_head_layernorm(const prime_tensor_t *x, const prime_tensor_t *out, int B, int H, int L, int D,
                          const void *weight, const void *bias, int param_dtype, float ln_eps, float scale,
                          void *stream) {

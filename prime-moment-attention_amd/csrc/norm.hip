@@ -246,6 +246,42 @@ hipError_t launch_gelu(const void *x, void *y, int64_t n, int dt, hipStream_t st
     return hipGetLastError();
 }
 
+// Selective PRIME's per-token log decays from the step-size pre-activations
+// s = delta_proj(x) (selective.py:368, 386): Delta = clamp(softplus(s)), each
+// stage rounded to s's dtype as the module's tensors hold it, then
+// log_decay[b, h, t] = -Delta / tau[h] in fp32.  One thread per (sequence,
+// token): it reads the token's H pre-activations (one short row) and writes
+// one value per head, consecutive threads writing consecutive tokens of a head.
+__global__ __launch_bounds__(256) void selective_log_decay_kernel(const void *step, int dt, int64_t sb, int64_t sl,
+                                                                  const float *tau, float dmin, float dmax, int H,
+                                                                  int L, int64_t rows, float *out) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (r >= rows) return;
+    const int64_t b = r / L, t = r - b * L;
+    auto rnd = [dt](float x) {
+        if (dt == PRIME_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
+        if (dt == PRIME_F16) return h16_bits_to_f32(f32_to_h16_bits(x));
+        return x;
+    };
+    const int64_t src = b * sb + t * sl;
+    for (int h = 0; h < H; ++h) {
+        const float s = load_elem(step, src + h, dt);
+        float d = rnd(s > 20.f ? s : log1pf(expf(s)));  // softplus (threshold 20, as torch)
+        d = rnd(fminf(fmaxf(d, dmin), dmax));
+        out[(b * H + h) * L + t] = -d / tau[h];
+    }
+}
+
+hipError_t launch_selective_log_decay(const void *step, int dt, int64_t sb, int64_t sl, const float *tau, float dmin,
+                                      float dmax, int B, int H, int L, float *out, hipStream_t stream) {
+    const int64_t rows = static_cast<int64_t>(B) * L;
+    const int64_t blocks = (rows + 255) / 256;
+    if (blocks >= (int64_t(1) << 31)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(selective_log_decay_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, step,
+                       dt, sb, sl, tau, dmin, dmax, H, L, rows, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_head_layernorm(const HeadNormArgs &a, hipStream_t stream) {
     const uint32_t rows = static_cast<uint32_t>(a.B) * a.L * a.H;
     const uint32_t per_block = 4u * kHeadNormBatch * (a.dt == PRIME_F32 ? 4u : 8u);  // 4 waves

@@ -118,6 +118,8 @@ hipError_t launch_pack_frag(const uint16_t *src, int64_t ld, const int64_t *idx,
 constexpr int kNormMaxGroups = 16;  // 4-element groups per lane: hidden <= 4 * 64 * 16 = 4096
 hipError_t launch_add_rmsnorm(const RmsNormArgs &a, hipStream_t stream);
 hipError_t launch_gelu(const void *x, void *y, int64_t n, int dt, hipStream_t stream);
+hipError_t launch_selective_log_decay(const void *step, int dt, int64_t sb, int64_t sl, const float *tau, float dmin,
+                                      float dmax, int B, int H, int L, float *out, hipStream_t stream);
 
 struct PrefillArgs {
     const void *q, *k, *v;

@@ -25,7 +25,7 @@ _DTYPES = {torch.float32: PRIME_F32, torch.bfloat16: PRIME_BF16, torch.float16: 
 EXPORTS = ("prime_abi_version", "prime_last_error", "prime_decode_step", "prime_chunked_prefill",
            "prime_chunked_prefill_workspace_size", "prime_timer_enable", "prime_timer_reset",
            "prime_timer_read", "prime_delta_prefill", "prime_delta_prefill_workspace_size",
-           "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_gelu", "prime_argmax",
+           "prime_delta_decode_step", "prime_decode_step_qknorm", "prime_add_rmsnorm", "prime_gelu", "prime_selective_log_decay", "prime_argmax",
            "prime_head_layernorm", "prime_linear", "prime_linear_residual", "prime_linear_fused", "prime_selective_prefill",
            "prime_selective_decode_step", "prime_accumulate", "prime_accumulate_workspace_size",
            "prime_decode_readout", "prime_decode_update", "prime_chunked_prefill_backward",
@@ -116,6 +116,9 @@ def load() -> ctypes.CDLL:
     L.prime_add_rmsnorm.restype = ctypes.c_int
     L.prime_gelu.argtypes = [fp, fp, ctypes.c_int64, ctypes.c_int, fp]
     L.prime_gelu.restype = ctypes.c_int
+    L.prime_selective_log_decay.argtypes = [fp, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, fp, ctypes.c_float,
+                                            ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, fp, fp]
+    L.prime_selective_log_decay.restype = ctypes.c_int
     L.prime_argmax.argtypes = [fp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, fp, fp]
     L.prime_argmax.restype = ctypes.c_int
     L.prime_head_layernorm.argtypes = [P(PrimeTensor)] * 2 + [ctypes.c_int] * 4 + [fp, fp, ctypes.c_int,
@@ -569,6 +572,29 @@ def _sel_vec(t: torch.Tensor, n: int, name: str) -> None:
     _dev_check(t)
     if t.dtype != torch.float32 or t.numel() != n or not t.is_contiguous():
         raise ValueError(f"{name} must be a contiguous fp32 tensor of {n} elements")
+
+
+def selective_log_decay(step: torch.Tensor, tau: torch.Tensor, step_min: float = 1e-4, step_max: float = 50.0,
+                        out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """prime_selective_log_decay: -clamp(softplus(step), step_min, step_max) /
+    tau as fp32 [B, H, L] (each stage rounded to step's dtype, as the module's
+    tensors hold it) from the pre-activations step = delta_proj(x) [B, L, H]
+    (any batch and token strides, contiguous heads); tau fp32 [H]."""
+    _dev_check(step)
+    if step.dim() != 3 or step.stride(2) != 1 or step.dtype not in _DTYPES:
+        raise ValueError("step must be [B, L, H] with contiguous heads")
+    B, Lt, H = step.shape
+    _sel_vec(tau, H, "tau")
+    if out is None:
+        out = torch.empty(B, H, Lt, device=step.device, dtype=torch.float32)
+    elif out.shape != (B, H, Lt) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous fp32 [B, H, L] tensor")
+    rc = load().prime_selective_log_decay(ctypes.c_void_p(step.data_ptr()), _DTYPES[step.dtype], step.stride(0),
+                                          step.stride(1), ctypes.c_void_p(tau.data_ptr()), float(step_min),
+                                          float(step_max), B, H, Lt, ctypes.c_void_p(out.data_ptr()),
+                                          _stream(step.device))
+    _check(rc, "prime_selective_log_decay")
+    return out
 
 
 def selective_prefill(q, k, v, log_decay: torch.Tensor, k_scale: torch.Tensor, eps: float, state_in, y,

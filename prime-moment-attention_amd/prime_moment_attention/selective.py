@@ -127,6 +127,21 @@ class PrimeSelectiveMomentAttention(nn.Module):
     def get_beta(self, device: torch.device) -> torch.Tensor:
         return torch.clamp(torch.exp(self.log_beta.to(device)), min=0.1, max=15.0)
 
+    def _gate_constants(self, device: torch.device):
+        """tau and beta as contiguous fp32 [H] on `device` for the kernels
+        (inference: no autograd through them), cached outside the state dict
+        and rebuilt when log_tau or log_beta changes (storage or version), so
+        that a prefill or a step does not relaunch their elementwise ops."""
+        ps = (self.log_tau, self.log_beta)
+        key = tuple((p.data_ptr(), p._version) for p in ps) + (str(device), self.min_tau, self.max_tau)
+        cached = self.__dict__.get("_gate_cache")
+        if cached is not None and all(a is b for a, b in zip(cached[0], ps)) and cached[1] == key:
+            return cached[2]
+        with torch.no_grad():
+            consts = (self.get_tau(device).float().contiguous(), self.get_beta(device).float().contiguous())
+        self.__dict__["_gate_cache"] = (ps, key, consts)
+        return consts
+
     def step_size(self, hidden_states: torch.Tensor) -> torch.Tensor:
         """Delta [B, L, H] (selective.py:368)."""
         return F.softplus(self.delta_proj(hidden_states)).clamp(min=1e-4, max=50.0)
@@ -145,10 +160,11 @@ class PrimeSelectiveMomentAttention(nn.Module):
         orig_dtype, dev = hidden_states.dtype, hidden_states.device
         y_dtype = orig_dtype if orig_dtype in (torch.float32, torch.bfloat16, torch.float16) else torch.float32
         q, k, v = project_qkv(self, hidden_states)
-        tau = self.get_tau(dev).float().contiguous()
-        beta = self.get_beta(dev).float().contiguous()
         if needs_grad(hidden_states, *self.parameters(), *(state or ())):
+            tau = self.get_tau(dev).float().contiguous()
+            beta = self.get_beta(dev).float().contiguous()
             return self._mix_autograd(hidden_states, q, k, v, tau, beta, state, return_state)
+        tau, beta = self._gate_constants(dev)
         if L == 1:
             norm = _lib.qk_norm(self.q_norm if self.use_qk_norm else None,
                                 self.k_norm if self.use_qk_norm else None, self.scaling, q.dtype)
@@ -177,9 +193,9 @@ class PrimeSelectiveMomentAttention(nn.Module):
                 _lib.head_layernorm(q, q, self.q_norm if self.use_qk_norm else None, self.scaling)
                 if self.use_qk_norm:
                     _lib.head_layernorm(k, k, self.k_norm, 1.0)
-            # per-token log decays -(Delta / tau), [B, H, L]
-            delta = self.step_size(hidden_states)  # [B, L, H]
-            log_decay = (-delta.float() / tau.view(1, 1, H)).transpose(1, 2).contiguous()
+            # per-token log decays -(Delta / tau), [B, H, L], from delta_proj(x)
+            # in one kernel (the stages of step_size, each rounded as there)
+            log_decay = _lib.selective_log_decay(self.delta_proj(hidden_states), tau)
             y_bl = torch.empty(B, L, H, D, device=dev, dtype=y_dtype)
             next_state = _lib.new_state(B, H, D, dev) if return_state else None
             _lib.selective_prefill(q, k, v, log_decay, beta, self.eps, None, y_bl.transpose(1, 2), next_state,

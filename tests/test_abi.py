@@ -102,6 +102,31 @@ def test_gelu_and_delta_step_backward_validate_before_device_work():
     assert rc == -5 and "overlaps" in _lib.last_error()
 
 
+def test_selective_log_decay_validates_before_device_work():
+    """prime_selective_log_decay rejects null, out-of-range, misaligned and
+    overlapping arguments with its error codes (no launch)."""
+    L = _lib.load()
+    st, tau, out = ctypes.c_void_p(1 << 20), ctypes.c_void_p(2 << 20), ctypes.c_void_p(3 << 20)
+    bf = _lib.PRIME_BF16
+    assert L.prime_selective_log_decay(None, bf, 24, 12, tau, 1e-4, 50.0, 2, 12, 8, out, None) == -1
+    assert L.prime_selective_log_decay(st, bf, 96, 12, tau, 1e-4, 50.0, 2, 12, 0, out, None) == -1
+    assert L.prime_selective_log_decay(st, bf, -1, 12, tau, 1e-4, 50.0, 2, 12, 8, out, None) == -1
+    assert L.prime_selective_log_decay(st, 9, 96, 12, tau, 1e-4, 50.0, 2, 12, 8, out, None) == -3
+    assert L.prime_selective_log_decay(st, bf, 96, 12, tau, 0.0, 50.0, 2, 12, 8, out, None) == -1
+    assert "step bounds" in _lib.last_error()
+    assert L.prime_selective_log_decay(st, bf, 96, 12, tau, 1.0, 0.5, 2, 12, 8, out, None) == -1
+    assert L.prime_selective_log_decay(ctypes.c_void_p((1 << 20) + 1), bf, 96, 12, tau, 1e-4, 50.0, 2, 12, 8, out,
+                                       None) == -4
+    assert L.prime_selective_log_decay(st, bf, 96, 12, ctypes.c_void_p((2 << 20) + 2), 1e-4, 50.0, 2, 12, 8, out,
+                                       None) == -4
+    # out overlaps the pre-activations (2 x 8 rows of 12 bf16 from st)
+    assert L.prime_selective_log_decay(st, bf, 96, 12, tau, 1e-4, 50.0, 2, 12, 8, ctypes.c_void_p((1 << 20) + 64),
+                                       None) == -5
+    assert "overlaps" in _lib.last_error()
+    assert L.prime_selective_log_decay(st, bf, 96, 12, tau, 1e-4, 50.0, 2, 12, 8, ctypes.c_void_p((2 << 20) - 16),
+                                       None) == -5  # out runs into tau
+
+
 def test_host_wrappers_refuse_cpu_tensors():
     import torch
     x = torch.zeros(1, 1, 64)

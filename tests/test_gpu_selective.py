@@ -6,6 +6,7 @@ through the greedy decoder."""
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from oracle import oracle as O
 from prime_moment_attention import (GreedyDecoder, PrimeConfig, PrimeForCausalLM,
@@ -324,3 +325,23 @@ def test_selective_gate_from_step_preactivations():
     assert torch.equal(outs[0][0], outs[1][0])
     for a, b in zip(outs[0][1], outs[1][1]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_selective_log_decay_matches_module_ops(dtype):
+    """prime_selective_log_decay equals the module's torch ops bit for bit:
+    -(softplus(s).clamp(1e-4, 50.0)).float() / tau, transposed to [B, H, L]
+    (selective.py:368, 414-416), on pre-activations that cover softplus's
+    linear branch (s > 20), both clamps and ordinary values, read through a
+    strided view (a column range of a wider projection, as the model's)."""
+    torch.manual_seed(5)
+    B, L, H = 3, 777, 12
+    wide = torch.randn(B, L, H + 20, device="cuda") * 6.0
+    wide[0, :40, 20:] = 30.0 + torch.rand(40, H, device="cuda") * 40.0  # linear branch, upper clamp
+    wide[1, :40, 20:] = -20.0 - torch.rand(40, H, device="cuda") * 5.0  # softplus < 1e-4: lower clamp
+    s = wide.to(dtype)[:, :, 20:]
+    tau = torch.linspace(2.0, 2000.0, H, device="cuda")
+    got = _lib.selective_log_decay(s, tau)
+    want = (-(F.softplus(s).clamp(min=1e-4, max=50.0)).float() / tau.view(1, 1, H)).transpose(1, 2).contiguous()
+    assert got.shape == (B, H, L) and got.dtype == torch.float32
+    assert torch.equal(got, want), (got - want).abs().max().item()
