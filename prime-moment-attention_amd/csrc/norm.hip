@@ -250,35 +250,61 @@ hipError_t launch_gelu(const void *x, void *y, int64_t n, int dt, hipStream_t st
 // s = delta_proj(x) (selective.py:368, 386): Delta = clamp(softplus(s)), each
 // stage rounded to s's dtype as the module's tensors hold it, then
 // log_decay[b, h, t] = -Delta / tau[h] in fp32.  One thread per (sequence,
-// token): it reads the token's H pre-activations (one short row) and writes
-// one value per head, consecutive threads writing consecutive tokens of a head.
-__global__ __launch_bounds__(256) void selective_log_decay_kernel(const void *step, int dt, int64_t sb, int64_t sl,
-                                                                  const float *tau, float dmin, float dmax, int H,
-                                                                  int L, int64_t rows, float *out) {
+// group of 4 heads, token), consecutive threads on consecutive tokens, so each
+// head's stores are coalesced; the 4 loads carry no branch (an index past
+// H - 1 re-reads head H - 1) and are all in flight before the first is used.
+constexpr int kDecayHeads = 4;
+template <int DT>
+__global__ __launch_bounds__(256) void selective_log_decay_kernel(const void *__restrict__ step, int64_t sb,
+                                                                  int64_t sl, const float *__restrict__ tau,
+                                                                  float dmin, float dmax, int H, int L, int HG,
+                                                                  int64_t n, float *__restrict__ out) {
     const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-    if (r >= rows) return;
-    const int64_t b = r / L, t = r - b * L;
-    auto rnd = [dt](float x) {
-        if (dt == PRIME_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
-        if (dt == PRIME_F16) return h16_bits_to_f32(f32_to_h16_bits(x));
-        return x;
+    if (r >= n) return;
+    const int64_t bg = r / L, t = r - bg * L;
+    const int64_t b = bg / HG;
+    const int h0 = static_cast<int>(bg - b * HG) * kDecayHeads;
+    auto rnd = [](float x) {
+        if constexpr (DT == PRIME_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
+        else if constexpr (DT == PRIME_F16) return h16_bits_to_f32(f32_to_h16_bits(x));
+        else return x;
+    };
+    auto ld = [&](int64_t i) {
+        if constexpr (DT == PRIME_F32) return static_cast<const float *>(step)[i];
+        else if constexpr (DT == PRIME_BF16) return bf16_bits_to_f32(static_cast<const uint16_t *>(step)[i]);
+        else return h16_bits_to_f32(static_cast<const uint16_t *>(step)[i]);
     };
     const int64_t src = b * sb + t * sl;
-    for (int h = 0; h < H; ++h) {
-        const float s = load_elem(step, src + h, dt);
-        float d = rnd(s > 20.f ? s : log1pf(expf(s)));  // softplus (threshold 20, as torch)
-        d = rnd(fminf(fmaxf(d, dmin), dmax));
-        out[(b * H + h) * L + t] = -d / tau[h];
+    float sv[kDecayHeads];
+#pragma unroll
+    for (int j = 0; j < kDecayHeads; ++j) sv[j] = ld(src + min(h0 + j, H - 1));
+#pragma unroll
+    for (int j = 0; j < kDecayHeads; ++j) {
+        if (h0 + j < H) {
+            const float s = sv[j];
+            float d = rnd(s > 20.f ? s : log1pf(expf(s)));  // softplus (threshold 20, as torch)
+            d = rnd(fminf(fmaxf(d, dmin), dmax));
+            out[(b * H + h0 + j) * L + t] = -d / tau[h0 + j];
+        }
     }
 }
 
 hipError_t launch_selective_log_decay(const void *step, int dt, int64_t sb, int64_t sl, const float *tau, float dmin,
                                       float dmax, int B, int H, int L, float *out, hipStream_t stream) {
-    const int64_t rows = static_cast<int64_t>(B) * L;
-    const int64_t blocks = (rows + 255) / 256;
+    const int HG = (H + kDecayHeads - 1) / kDecayHeads;
+    const int64_t n = static_cast<int64_t>(B) * HG * L;
+    const int64_t blocks = (n + 255) / 256;
     if (blocks >= (int64_t(1) << 31)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(selective_log_decay_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, step,
-                       dt, sb, sl, tau, dmin, dmax, H, L, rows, out);
+    const dim3 g(static_cast<unsigned>(blocks)), blk(256);
+    if (dt == PRIME_BF16)
+        hipLaunchKernelGGL(selective_log_decay_kernel<PRIME_BF16>, g, blk, 0, stream, step, sb, sl, tau, dmin, dmax,
+                           H, L, HG, n, out);
+    else if (dt == PRIME_F16)
+        hipLaunchKernelGGL(selective_log_decay_kernel<PRIME_F16>, g, blk, 0, stream, step, sb, sl, tau, dmin, dmax, H,
+                           L, HG, n, out);
+    else
+        hipLaunchKernelGGL(selective_log_decay_kernel<PRIME_F32>, g, blk, 0, stream, step, sb, sl, tau, dmin, dmax, H,
+                           L, HG, n, out);
     return hipGetLastError();
 }
 
