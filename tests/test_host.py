@@ -128,3 +128,22 @@ def test_stacked_qkv_cache_follows_weights_and_modes():
     m.k_proj.bias = torch.nn.Parameter(torch.zeros(32), requires_grad=False)
     with torch.no_grad():
         assert _stacked_qkv(m) is None  # a bias: the three projections run
+
+
+def test_selective_gate_constants_follow_parameters():
+    """The selective module's cached tau and beta (fp32 [H] for the kernels;
+    selective.py:367-368): the module's own get_tau / get_beta values, rebuilt
+    after an in-place update of log_tau or log_beta; host logic only."""
+    from prime_moment_attention import PrimeSelectiveMomentAttention
+    m = PrimeSelectiveMomentAttention(hidden_size=64, num_heads=4, head_dim=16)
+    tau, beta = m._gate_constants(torch.device("cpu"))
+    assert torch.equal(tau, m.get_tau(torch.device("cpu")).float()) and tau.dtype == torch.float32
+    assert torch.equal(beta, m.get_beta(torch.device("cpu")).float())
+    assert m._gate_constants(torch.device("cpu"))[0] is tau
+    with torch.no_grad():
+        m.log_tau.add_(0.5)
+        m.log_beta.sub_(0.25)
+    tau2, beta2 = m._gate_constants(torch.device("cpu"))
+    assert tau2 is not tau and torch.equal(tau2, m.get_tau(torch.device("cpu")).float())
+    assert torch.equal(beta2, m.get_beta(torch.device("cpu")).float())
+    assert not tau2.requires_grad
